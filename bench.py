@@ -1,0 +1,187 @@
+"""GSPO rollout throughput on one MI355X: 64 prefixes x group 8 = 512 sequences, 2048-frame prefixes,
+1024 sampled tokens each (temperature 1.0, supplied uniforms), 8-layer d512 decoder, vocab 7.
+
+One step = one full rollout: prefill of the 512 prefixes (projector + 8 layers, BOS-only last layer) +
+1023 graph-replayed decode steps, with the frames already resident in HBM. value = 512 * 1024 tokens per
+rollout / seconds per rollout.
+
+Extra objects on the JSON line:
+  roofline      decode attention, the dominant kernel: algorithmic bytes per launch (every K/V byte of
+                the attended positions once, plus q and out) / its average launch duration, measured here
+                with HIP events on the launch stream over launches at the rollout's attended lengths;
+                traffic = measured HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by a copy
+                kernel; read from profiles/decode_attention_traffic.json when present, else null).
+  cpu_baseline  the CPU oracle (the reference's fp32 torch path restated) on this host, on a bounded slice:
+                2 sequences x 2048-frame prefix x 32 sampled tokens; tokens/s of that slice.
+Usage: python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--no-cpu]
+"""
+
+import argparse
+import copy
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GSPO rollout tokens/sec on 1 MI355X (512 seq x 1024 tok); % HBM roofline"
+HBM_PEAK_GBS = 8000.0
+PREFIXES, GROUP, P, NEW = 64, 8, 2048, 1024
+KV_ROW_BYTES = 2 * 2 * 64 * 2  # K + V, 2 KV heads, head_dim 64, bf16: one attended position of one layer
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_model(dev):
+    from viktor_amd.synthetic import make_model
+    m = make_model(1, n_layers=8, seed=0, rope_theta=1e6)
+    g = copy.deepcopy(m).to(dev)
+    g.projector.to(torch.bfloat16)
+    g.decoder.to(torch.bfloat16)
+    return m, g.eval()
+
+
+def decode_attention_timing(eng, n_points=32, reps=5):
+    """Average duration (HIP events on the current stream) and algorithmic bytes of the decode-attention
+    kernel at the attended lengths of a rollout's decode steps j = 0..NEW-2 (len = P + 2 + j), sampled at
+    n_points evenly spaced steps, reps back-to-back launches each."""
+    from viktor_amd import hip_ops as ops
+    B = eng.B
+    cache = eng.cache
+    q = torch.randn(B, 8, 64, device=cache.k.device).to(torch.bfloat16)
+    js = [round(i * (NEW - 2) / (n_points - 1)) for i in range(n_points)]
+    ws = eng.fast.decode_workspace
+    total_ms, total_bytes, launches = 0.0, 0.0, 0
+    stream = torch.cuda.current_stream()
+    for j in js:
+        lens = torch.full((B,), P + 2 + j, dtype=torch.int32, device=cache.k.device)
+        ops.decode_attention(q, cache.k[3], cache.v[3], lens, workspace=ws)  # warm
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            ops.decode_attention(q, cache.k[3], cache.v[3], lens, workspace=ws)
+        e1.record(stream)
+        e1.synchronize()
+        total_ms += e0.elapsed_time(e1)
+        launches += reps
+        total_bytes += reps * (B * (P + 2 + j) * KV_ROW_BYTES + 2 * B * 8 * 64 * 2)
+    avg_s = total_ms / 1e3 / launches
+    return avg_s, total_bytes / launches
+
+
+def cpu_baseline(seconds_budget=30.0):
+    """The CPU oracle (fp32 reference semantics) on a bounded slice of the same workload."""
+    from oracle import reference as R
+    from viktor_amd.synthetic import frames, make_model, uniforms
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    m = make_model(1, n_layers=8, seed=0, rope_theta=1e6)
+    n_seq, steps = 2, 32
+    fr = frames(n_seq, P, 512, seed=0)
+    u = uniforms(n_seq, steps, seed=1)
+    eng = R.RefEngine(R.RefModel(m, "fp32"), steps, temperature=1.0)
+    t0 = time.perf_counter()
+    eng.run([fr[i] for i in range(n_seq)], uniforms=u)
+    dt = time.perf_counter() - t0
+    return {"value": n_seq * steps / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n_seq} sequences x {P}-frame prefix x {steps} sampled tokens (prefill + decode), fp32 "
+                      f"CPU restatement of the reference torch path; {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prefill-batch", type=int, default=128)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the rollout path has no multi-GPU mode here (one process per GPU, "
+              "whole GSPO groups per rank); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    from viktor_amd import DecodeEngine
+    from viktor_amd.synthetic import frames, uniforms
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log("building model / inputs")
+    _, gm = build_model(dev)
+    B = PREFIXES * GROUP
+    fr = frames(PREFIXES, P, 512, seed=0).to(dev).repeat_interleave(GROUP, 0).reshape(-1, 512)
+    u = uniforms(B, NEW, seed=1).to(dev)
+    plens = [P] * B
+    eng = DecodeEngine(gm, B, NEW, P, temperature=1.0, prefill_batch=args.prefill_batch)
+    torch.cuda.synchronize()
+
+    def rollout():
+        eng.set_uniforms(u)
+        eng.generate(fr, plens, steps=NEW)
+
+    log(f"warmup x{args.warmup}")
+    for _ in range(args.warmup):
+        rollout()
+    torch.cuda.synchronize()
+    # prefill / decode split of one rollout (reported, not the metric)
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    eng.set_uniforms(u)
+    e[0].record()
+    eng.prefill(fr, plens)
+    e[1].record()
+    eng.decode(NEW)
+    e[2].record()
+    torch.cuda.synchronize()
+    prefill_ms, decode_ms = e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2])
+
+    log(f"timed x{args.steps}")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        rollout()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_per_step = dt / args.steps * 1e3
+    value = B * NEW * args.steps / dt
+
+    log("decode-attention timing")
+    avg_s, alg_bytes = decode_attention_timing(eng)
+    achieved = alg_bytes / avg_s / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "decode_attention_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+    out = tokens_check = eng.out[:, :NEW].cpu()
+    live = int(((out != 0) & (out != 2)).sum())
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline")
+        cpu = cpu_baseline()
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (N(0,1) frames, seeded random-init weights, "
+                                                      "seeded uniforms)",
+        "config": {"workload": "gspo_rollout", "sequences": B, "prefixes": PREFIXES, "group": GROUP,
+                   "prefix_frames": P, "new_tokens": NEW, "vocab": 7, "layers": 8, "d_model": 512,
+                   "heads": "8q/2kv x 64", "temperature": 1.0, "prefill_batch": args.prefill_batch,
+                   "parallelism": "single GPU"},
+        "prefill_ms": round(prefill_ms, 2), "decode_ms": round(decode_ms, 2),
+        "live_tokens_per_rollout": live,
+        "roofline": {"kernel": "decode_attention", "bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "avg_launch_us": round(avg_s * 1e6, 2),
+                     "alg_bytes_per_launch": int(alg_bytes)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

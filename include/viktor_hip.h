@@ -1,0 +1,180 @@
+/*
+ * viktor_hip.h -- C ABI of libviktor_hip.so, the gfx950 (MI355X) kernels of the decoder's
+ * rollout-and-scoring path.
+ *
+ * Conventions for every entry point:
+ *   - all pointers are device pointers (HIP device memory) unless stated otherwise;
+ *     bf16 tensors are passed as raw 16-bit storage, row-major and contiguous unless a
+ *     stride argument is given;
+ *   - `stream` is a hipStream_t passed as void* (0 = the null stream); every kernel is
+ *     enqueued on it, nothing synchronises the device, nothing allocates device memory,
+ *     so every entry point may be recorded into a HIP graph;
+ *   - the return value is VK_OK (0) or a VK_ERR_* code; vk_last_error() returns the
+ *     message of the last failure on the calling host thread.
+ *   - device-side indices read from memory (token ids, positions, cache rows, lengths)
+ *     are bounds-checked inside the kernels against the sizes passed here: an
+ *     out-of-range write is skipped, an out-of-range read is clamped.
+ *
+ * Each declaration names the reference function it replaces (file:line of GHSSHG/Viktor).
+ */
+#ifndef VIKTOR_HIP_H
+#define VIKTOR_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VK_OK 0
+#define VK_ERR_ARG 1         /* invalid argument: shape, size, alignment or null pointer */
+#define VK_ERR_LAUNCH 2      /* the HIP runtime rejected a kernel launch */
+#define VK_ERR_UNSUPPORTED 3 /* a configuration these kernels are not built for */
+
+#define VK_DTYPE_BF16 0
+#define VK_DTYPE_F32 1
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int vk_version(void);
+
+/* Message of the last non-zero status returned on this host thread ("" if none). */
+const char *vk_last_error(void);
+
+/* Number of compute units of the current device (0 on failure); used to size launch grids. */
+int vk_device_cus(void);
+
+/*
+ * x[n, d] += delta[n, d] (bf16, in place; delta may be NULL), then
+ * h[n, d] = bf16(x * rsqrt(mean(x^2) + eps) * w), fp32 inside.
+ * Replaces add_rmsnorm, viktor/triton_ops.py:17-40.
+ */
+int vk_add_rmsnorm(void *x, const void *delta, const void *w, void *h, int64_t n, int32_t d, float eps,
+                   void *stream);
+
+/*
+ * x[i, :] = emb[tok[i], :] and h = RMSNorm(x) * w (bf16). Token ids outside [0, vocab) give a zero row.
+ * Replaces embed_rmsnorm, viktor/triton_ops.py:149-169.
+ */
+int vk_embed_rmsnorm(const int64_t *tok, const void *emb, int64_t vocab, const void *w, void *x, void *h,
+                     int64_t n, int32_t d, float eps, void *stream);
+
+/*
+ * Per token t of qkv[n, (H + 2 HKV) * D]: heads 0..H-1 are q, then HKV k heads, then HKV v heads.
+ * q and k heads get RMSNorm over D (weights q_norm_w / k_norm_w, result rounded to bf16) and the
+ * half-split RoPE rotation at row rope_pos[t] of cos/sin [table_rows, D/2] (table_dtype bf16 or f32).
+ * q[n, H, D] receives the rotated q heads; k (rotated) and v go to
+ * k_cache/v_cache + seq[t] * stride_cb + pos[t] * stride_cs (+ head * D) when the cache pointers are
+ * non-NULL and seq[t] < cache_rows, pos[t] < cache_len; and to k_out/v_out[n, HKV, D] when non-NULL.
+ * rope_pos may be NULL (then pos is used).
+ * Replaces qkv_rope_cache, viktor/triton_ops.py:43-108.
+ */
+int vk_qkv_rope_cache(const void *qkv, const void *q_norm_w, const void *k_norm_w, const void *cos_t,
+                      const void *sin_t, int32_t table_dtype, int64_t table_rows, const int32_t *pos,
+                      const int32_t *rope_pos, const int32_t *seq, void *q, void *k_cache, void *v_cache,
+                      int64_t stride_cb, int64_t stride_cs, int64_t cache_rows, int64_t cache_len, void *k_out,
+                      void *v_out, int64_t n, float eps, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                      void *stream);
+
+/*
+ * y[M, N] = x[M, K] @ w[N, K]^T on bf16 MFMA with fp32 accumulation; y is bf16 (out_dtype
+ * VK_DTYPE_BF16) or fp32 (VK_DTYPE_F32).
+ * swiglu != 0: w is gate_up [2N, K] and y[M, N] = bf16(bf16(silu(bf16(x w_gate^T))) * bf16(x w_up^T)),
+ * the rounding points of the unfused linear + SwiGLU path.
+ * Requires K % 32 == 0 and 16-byte aligned x, w.
+ * Replaces linear (viktor/triton_ops.py:111-146), swiglu (212-229) and the F.linear / nn.Linear
+ * projections of viktor/fast_decoder.py:39,56-57 and viktor/decoder.py:58-59,114-115,163-164.
+ */
+int vk_linear(const void *x, const void *w, void *y, int64_t M, int32_t N, int32_t K, int32_t swiglu,
+              int32_t out_dtype, void *stream);
+
+/*
+ * out[n, F] = bf16(bf16(silu(gate)) * up) for gu[n, 2F] = [gate | up] (bf16).
+ * Replaces swiglu, viktor/triton_ops.py:212-229.
+ */
+int vk_swiglu(const void *gu, void *out, int64_t n, int32_t f, void *stream);
+
+/*
+ * Single-query GQA attention against one layer of the KV cache:
+ * out[b, h, :] = softmax(q[b, h] . K[b, :len_b, h / (H/HKV)]^T / sqrt(D)) V[b, :len_b, ...]
+ * with len_b = clamp(lengths[b], 1, max_len); k_cache/v_cache element (b, s, hk, d) at
+ * b * stride_b + s * stride_s + hk * D + d. fp32 online softmax, probabilities rounded to bf16
+ * before the PV product (as the reference kernel). Each K/V row is read once for its query-head group.
+ * Built for H = 8, HKV = 2, D = 64. workspace: vk_decode_attention_workspace() bytes (may be 0 bytes
+ * when no split of the key range is needed; then workspace may be NULL).
+ * Replaces decode_attention, viktor/decode_attention.py:11-53 (and the flash_attn_with_kvcache
+ * decode of viktor/fast_decoder.py:86-89).
+ */
+int vk_decode_attention(const void *q, const void *k_cache, const void *v_cache, const int32_t *lengths,
+                        void *out, int64_t B, int32_t H, int32_t HKV, int32_t D, int64_t stride_b,
+                        int64_t stride_s, int64_t max_len, void *workspace, int64_t workspace_bytes,
+                        void *stream);
+
+/* Workspace bytes vk_decode_attention needs for this batch and cache length. */
+int vk_decode_attention_workspace(int64_t B, int32_t H, int64_t max_len, int64_t *bytes);
+
+/*
+ * Variable-length GQA attention over packed queries (flash_attn_varlen_func semantics, scale 1/sqrt(D)).
+ * Sequence i has q_len_i = cu_q[i+1] - cu_q[i] queries (rows cu_q[i].. of q[*, H, D]) and
+ * k_len_i = k_lens[i] keys; key j of sequence i is at k + k_off[i] + j * stride_tok (+ hk * D), same for v.
+ * causal != 0: query r of sequence i sits at position k_len_i - q_len_i + r and sees keys <= it
+ * (bottom-right alignment). out[*, H, D] bf16.
+ * plan: n_blocks entries of (sequence, first query row) built by the host, one per 64-query block.
+ * Built for H = 8, HKV = 2, D = 64.
+ * Replaces flash_attn_varlen_func (viktor/fast_decoder.py:68-73) and flash_attn_func (viktor/decoder.py:82-87).
+ */
+int vk_varlen_attention(const void *q, const void *k, const void *v, const int32_t *cu_q, const int64_t *k_off,
+                        const int32_t *k_lens, const int32_t *plan, int32_t n_blocks, int32_t n_seq,
+                        int64_t stride_tok, void *out, int32_t causal, int32_t H, int32_t HKV, int32_t D,
+                        void *stream);
+
+/*
+ * One decode step's token choice and bookkeeping for B sequences (DecodeEngine._select + state update):
+ *   z = (logits[b] + bias) (fp32 logits, or bf16-rounded when h/w are given with round_bf16) ;
+ *   greedy (temperature <= 0): nxt = first argmax of z;
+ *   sampled: p = softmax(z / temperature) in fp32, nxt = first v with u < sum_{w<=v} p_w, u = uniforms[b * u_stride + col];
+ *   tail rule: EOS after a tail token; homopolymer rule (homo_stop > 0): run = (nxt == prev && is_homo[nxt]) ? run + 1 : 0,
+ *   EOS when run + 1 >= homo_stop; PAD after EOS or PAD.
+ *   out[b * out_stride + col] = nxt with col = pos[b] - plen[b]; tok[b] = nxt; pos[b] += 1;
+ *   pos32 = pos, seqlens = pos + 1, rpos32 = pos + rope_off (each optional, NULL to skip).
+ * Logits come either from `logits` [B, V] fp32 (h and w_head NULL), or are computed here as
+ * h[B, d] @ w_head[V, d]^T (bf16 inputs, fp32 accumulation), the fused LM head.
+ * logp_out (optional): log softmax(z / T or z)[nxt] of the chosen token before the grammar rules.
+ * Replaces greedy_update (viktor/triton_ops.py:172-209), DecodeEngine._select (viktor/engine.py:79-89)
+ * and the head + index_copy bookkeeping of DecodeEngine._step (viktor/engine.py:91-116).
+ */
+int vk_select_update(const float *logits, const void *h, const void *w_head, int32_t d, int32_t round_bf16,
+                     const float *bias, const uint8_t *is_tail, const uint8_t *is_homo, int32_t homo_stop,
+                     float temperature, const float *uniforms, int64_t u_stride, int64_t u_cols, int64_t *tok,
+                     int64_t *run, int64_t *pos, const int64_t *plen, const int64_t *rope_off, int64_t *out,
+                     int64_t out_stride, int64_t out_cols, int32_t *pos32, int32_t *seqlens, int32_t *rpos32,
+                     float *logp_out, int64_t B, int32_t V, int32_t eos, int32_t pad, void *stream);
+
+/*
+ * GSPO scoring of B sequences of T target tokens (scripts/gspo.py:340-353 and 459-477):
+ *   lp[b,t]   = log_softmax(logits[b,t,:])[targets[b,t]]           (fp32; logits bf16 or fp32)
+ *   s[b]      = exp(sum_t mask[b,t] (lp[b,t] - old_lp[b,t]) / n_bases[b])
+ *   pg[b]     = -min(s A, clamp(s, 1 - eps_lo, 1 + eps_hi) A), A = adv[b]
+ *   loss[0]   = inv_n * sum_b pg[b]                                  (fixed summation order)
+ *   dlogits[b,t,v] = inv_n * g_b * s_b * mask[b,t] / n_bases[b] * (1[v = y] - softmax(logits[b,t])_v),
+ *   g_b = d pg_b / d s_b with torch.minimum / clamp subgradients (ties split evenly, clamp passes at its ends).
+ * Targets outside [0, V) are scored as token 0 (the reference clamps PAD targets to 0) and must be masked.
+ * dlogits may be NULL (scoring only); old_lp/adv may be NULL when only lp is wanted (then s, pg, loss untouched).
+ */
+int vk_gspo_score(const void *logits, int32_t logits_dtype, const int64_t *targets, const uint8_t *mask,
+                  const float *old_lp, const float *n_bases, const float *adv, float eps_lo, float eps_hi,
+                  float inv_n, float *lp, float *s, float *pg, float *loss, float *dlogits, int64_t B, int64_t T,
+                  int32_t V, void *stream);
+
+/*
+ * Group-normalised advantages of rewards [G, n] (fp32), population std (ddof 0):
+ *   mode 0 (reference, scripts/gspo.py:447-450): adv = (r - mean) / max(std, param); live[g] = std > 1e-6
+ *   mode 1 (std + eps):                          adv = (r - mean) / (std + param);   live[g] = std > 1e-6
+ */
+int vk_group_advantage(const float *reward, int64_t groups, int32_t n, int32_t mode, float param, float *adv,
+                       uint8_t *live, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VIKTOR_HIP_H */

@@ -1,0 +1,105 @@
+"""The C-ABI boundary on the CPU: the library exists, loads, exports every entry point the header
+declares, and the product path fails loudly without a ROCm device (no compute calls here)."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from viktor_amd import _lib, hip_ops
+from viktor_amd.synthetic import make_model
+
+from .conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "viktor_hip.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(vk_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_binding_table():
+    assert declared_symbols() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    assert os.path.exists(_lib.LIB_PATH), "run python -m viktor_amd.build"
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (vk_\w+)", out))
+    missing = set(declared_symbols()) - exported
+    assert not missing, missing
+
+
+def test_library_loads_and_reports_version():
+    lib = _lib.load()
+    assert lib.vk_version() >= 100
+    assert isinstance(lib.vk_last_error(), bytes)
+
+
+def test_argument_errors_return_status_without_device_work():
+    """Invalid arguments are rejected on the host before any launch (null pointers / bad sizes)."""
+    lib = _lib.load()
+    rc = lib.vk_linear(None, None, None, 4, 8, 32, 0, 0, None)
+    assert rc == 1 and b"null" in lib.vk_last_error()
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    rc = lib.vk_linear(p, p, p, 4, 8, 30, 0, 0, None)  # K % 32 != 0
+    assert rc == 1 and b"K" in lib.vk_last_error()
+    rc = lib.vk_decode_attention(p, p, p, p, p, 4, 8, 2, 128, 128, 128, 16, None, 0, None)  # head_dim 128
+    assert rc == 3
+    with pytest.raises(_lib.HipLibraryError):
+        _lib.check(rc, "decode_attention")
+
+
+def test_ops_refuse_cpu_tensors():
+    x = torch.zeros(4, 512, dtype=torch.bfloat16)
+    w = torch.ones(512, dtype=torch.bfloat16)
+    with pytest.raises(_lib.HipLibraryError):
+        hip_ops.add_rmsnorm(x, w, 1e-6)
+    with pytest.raises(_lib.HipLibraryError):
+        hip_ops.linear(x, torch.zeros(64, 512, dtype=torch.bfloat16))
+
+
+def test_product_has_no_cpu_fallback():
+    from viktor_amd import DecodeEngine
+    m = make_model(1, n_layers=1)
+    with pytest.raises(_lib.HipLibraryError):
+        m.decoder(torch.zeros(1, 4, 512))
+    with pytest.raises(_lib.HipLibraryError):
+        DecodeEngine(m, 2, 4, 8)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(_lib.HipLibraryError):
+        _lib.load.__wrapped__ if hasattr(_lib.load, "__wrapped__") else None
+        saved = _lib._lib
+        try:
+            _lib._lib = None
+            _lib.load(str(tmp_path / "absent.so"))
+        finally:
+            _lib._lib = saved
+
+
+def test_product_never_imports_the_oracle():
+    pkg = os.path.join(ROOT, "viktor_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in re.sub(r"#.*", "", text).split("import") or "import oracle" not in text, f
+                assert "from oracle" not in text and "import oracle" not in text, f
+
+
+def test_attention_plan_orders_longest_first():
+    plan = hip_ops.AttentionPlan([130, 64, 1], [130, 200, 1], [0, 0, 0], "cpu", causal=True)
+    flat = plan.plan.tolist()
+    pairs = list(zip(flat[::2], flat[1::2]))
+    # blocks: seq0 at 0, 64, 128; seq1 at 0; seq2 at 0 -- work = keys visible to the block's last query
+    assert pairs[0] in ((1, 0),) and sorted(pairs) == [(0, 0), (0, 64), (0, 128), (1, 0), (2, 0)]
+    assert plan.total_q == 195 and plan.cu_q.tolist() == [0, 130, 194, 195]
+    with pytest.raises(AssertionError):
+        hip_ops.AttentionPlan([5], [4], [0], "cpu", causal=True)

@@ -1,0 +1,304 @@
+// Single-query GQA decode attention over one layer of the static KV cache [B, S, HKV=2, D=64] (bf16).
+//
+// Semantics: viktor/decode_attention.py:11-53 -- per sequence b and query head h,
+//   out = softmax(q . K[:len]^T * D^-0.5) V[:len], fp32 online softmax in the exp2 domain, the
+//   probabilities rounded to bf16 before the PV product, output rounded to bf16.
+//
+// MI355X design:
+//   * A cache row (one position, both KV heads) is 2 x 64 bf16 = 256 contiguous bytes. Each lane reads
+//     16-byte pieces of it directly into MFMA fragments, so every K/V byte is fetched exactly once for
+//     all 8 query heads (4 per KV head).
+//   * Both KV heads go through one MFMA chain with a block-diagonal query operand: column r (query
+//     head r) of Q^T is non-zero only on the 64 K-values of its own KV head, so
+//     S^T[pos, r] = K_row(pos)[128] . Qbd[r][128] is the score of head r against its own KV head.
+//   * S^T = K Q^T (v_mfma_f32_16x16x32_bf16: A = 16 cache rows, B = Q^T) leaves each lane holding the
+//     scores of one query row (lane % 16) at 4 positions of each 16-position half-tile. The PV product
+//     is computed transposed, O^T = V^T P^T, whose B operand needs exactly those (row, 8 positions)
+//     values: the probabilities never leave the lane that computed them, and the online-softmax
+//     rescale of O^T is lane-local too. The K-order of a 32-position tile is permuted consistently in
+//     both operands ({4g..4g+3, 16+4g..16+4g+3} for lane group g).
+//   * V^T needs position-contiguous fragments, the cache is column-contiguous: each wavefront stages
+//     its 32 x 128 V tile in its own LDS slice (16-byte writes) and gathers the transposed fragments
+//     with 2-byte reads (rows padded so the four lane groups hit disjoint banks).
+//   * Work split: a workgroup of WAVES wavefronts per (sequence, key split); its wavefronts take
+//     interleaved 32-position tiles; per-wave (max, sum, O) partials are merged through LDS. When the
+//     batch alone cannot fill the chip (B < 2 x CUs) the key range is split across workgroups and a
+//     small combine kernel merges the split partials from the workspace.
+#include <math.h>
+
+#include "common.h"
+
+namespace vk {
+
+constexpr int DA_H = 8;        // query heads
+constexpr int DA_HKV = 2;      // KV heads
+constexpr int DA_D = 64;       // head dim
+constexpr int DA_ROW = 128;    // HKV * D elements per cache row
+constexpr int DA_TILE = 32;    // positions per wavefront iteration
+constexpr int DA_PITCH = 136;  // LDS row pitch of the V tile (bf16 elements)
+constexpr int DA_WAVES = 8;
+
+struct DecodeSplit {
+  int nsplit;  // key splits per sequence
+  int tps;     // 32-position tiles per split
+};
+
+static DecodeSplit decode_split(int64_t B, int64_t max_len, int cus) {
+  const int ntiles = static_cast<int>((max_len + DA_TILE - 1) / DA_TILE);
+  const int64_t want = 2 * static_cast<int64_t>(cus > 0 ? cus : 256);
+  int nsplit = 1;
+  if (B < want) nsplit = static_cast<int>((want + B - 1) / B);
+  const int max_split = (ntiles + DA_WAVES - 1) / DA_WAVES;  // at least one tile per wave
+  if (nsplit > max_split) nsplit = max_split;
+  if (nsplit < 1) nsplit = 1;
+  const int tps = (ntiles + nsplit - 1) / nsplit;
+  nsplit = (ntiles + tps - 1) / tps;
+  return {nsplit, tps};
+}
+
+template <bool SPLIT>
+__global__ __launch_bounds__(DA_WAVES * 64) void decode_attn_kernel(
+    const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc, const bf16_t *__restrict__ vc,
+    const int32_t *__restrict__ lengths, bf16_t *__restrict__ out, int64_t stride_b, int64_t stride_s,
+    int64_t max_len, int tps, int nsplit, float *__restrict__ ws_o, float *__restrict__ ws_ml, float scale_log2) {
+  __shared__ __attribute__((aligned(16))) bf16_t Vs[DA_WAVES][DA_TILE * DA_PITCH];
+
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int64_t b = blockIdx.y;
+  const int split = blockIdx.x;
+  int64_t len = lengths[b];
+  len = len < 1 ? 1 : (len > max_len ? max_len : len);
+  const int ntiles = static_cast<int>((len + DA_TILE - 1) / DA_TILE);
+  const int t_begin = split * tps;
+  const int t_end = min(t_begin + tps, ntiles);
+  if (t_begin >= t_end) return;  // whole workgroup: this split lies past the sequence
+
+  const int qrow = lane & 15;  // query head of this lane's S^T / O^T column; also the A-fragment row
+  const int g = lane >> 4;     // lane group: K-values 8g..8g+7 of each 32-wide fragment
+
+  // block-diagonal Q^T fragments: chunk c (32 of the 128 row values) belongs to KV head c / 2
+  bf16x8 bq[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const bool own = qrow < DA_H && (qrow >> 2) == (c >> 1);
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (own) v = *reinterpret_cast<const u32x4 *>(q + (b * DA_H + qrow) * DA_D + (c & 1) * 32 + g * 8);
+    bq[c] = __builtin_bit_cast(bf16x8, v);
+  }
+
+  f32x4 acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const bf16_t *kb = kc + b * stride_b;
+  const bf16_t *vb = vc + b * stride_b;
+  bf16_t *vs = Vs[wid];
+
+  for (int t = t_begin + wid; t < t_end; t += DA_WAVES) {
+    const int64_t p0 = static_cast<int64_t>(t) * DA_TILE;
+    u32x4 kf[2][4], vf[2][4];
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb) {
+      int64_t p = p0 + 16 * pb + qrow;
+      p = p < len ? p : len - 1;  // rows past the length: any valid row, masked below
+      const bf16_t *kr = kb + p * stride_s + g * 8;
+      const bf16_t *vr = vb + p * stride_s + g * 8;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) kf[pb][c] = *reinterpret_cast<const u32x4 *>(kr + 32 * c);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) vf[pb][c] = *reinterpret_cast<const u32x4 *>(vr + 32 * c);
+    }
+    // scores S^T[pos][qrow]
+    f32x4 st[2];
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb) {
+      st[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        st[pb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[pb][c]), bq[c], st[pb], 0, 0, 0);
+    }
+    // online softmax over this tile (lane holds positions p0 + 16 pb + 4 g + i)
+    float sv[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t p = p0 + 16 * pb + 4 * g + i;
+        const float v = p < len ? st[pb][i] * scale_log2 : -INFINITY;
+        sv[pb * 4 + i] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = exp2f(m_run - m_new);
+    float psum = 0.f;
+    bf16x8 pf;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const float p = exp2f(sv[jj] - m_new);
+      psum += p;
+      pf[jj] = __builtin_bit_cast(__bf16, f2bf(p));
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] *= alpha;
+
+    // stage V (row-major) in this wave's LDS slice, gather transposed fragments
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<u32x4 *>(&vs[(16 * pb + qrow) * DA_PITCH + 32 * c + g * 8]) = vf[pb][c];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      bf16x8 va;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const int pl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
+        va[jj] = __builtin_bit_cast(__bf16, vs[pl * DA_PITCH + 16 * j + qrow]);
+      }
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf, acc[j], 0, 0, 0);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+
+  // row sums: add the 4 lane groups of each query row
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+
+  __syncthreads();  // every wave is done with its V slice: reuse the LDS for the merge
+  float *Os = reinterpret_cast<float *>(&Vs[0][0]);  // [WAVES][8][128]
+  float *Ms = Os + DA_WAVES * DA_H * DA_ROW;          // [WAVES][8]
+  float *Ls = Ms + DA_WAVES * DA_H;                   // [WAVES][8]
+  if (qrow < DA_H) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Os[(wid * DA_H + qrow) * DA_ROW + 16 * j + 4 * g + i] = acc[j][i];
+    if (g == 0) {
+      Ms[wid * DA_H + qrow] = m_run;
+      Ls[wid * DA_H + qrow] = l_run;
+    }
+  }
+  __syncthreads();
+  for (int o = threadIdx.x; o < DA_H * DA_D; o += DA_WAVES * 64) {
+    const int h = o / DA_D, d = o % DA_D;
+    const int col = (h / (DA_H / DA_HKV)) * DA_D + d;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < DA_WAVES; ++w) M = fmaxf(M, Ms[w * DA_H + h]);
+    float L = 0.f, N = 0.f;
+#pragma unroll
+    for (int w = 0; w < DA_WAVES; ++w) {
+      const float e = exp2f(Ms[w * DA_H + h] - M);
+      L += e * Ls[w * DA_H + h];
+      N += e * Os[(w * DA_H + h) * DA_ROW + col];
+    }
+    if (!SPLIT) {
+      out[(b * DA_H + h) * DA_D + d] = f2bf(N / L);
+    } else {
+      const int64_t base = (b * nsplit + split) * DA_H + h;
+      ws_o[base * DA_D + d] = N;
+      if (d == 0) {
+        ws_ml[base * 2] = M;
+        ws_ml[base * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+// Merge the key-split partials of each sequence (only the splits its length reaches).
+__global__ __launch_bounds__(DA_H * DA_D) void decode_attn_combine(const float *__restrict__ ws_o,
+                                                                    const float *__restrict__ ws_ml,
+                                                                    const int32_t *__restrict__ lengths,
+                                                                    bf16_t *__restrict__ out, int64_t max_len,
+                                                                    int tps, int nsplit) {
+  const int64_t b = blockIdx.x;
+  const int h = threadIdx.x / DA_D, d = threadIdx.x % DA_D;
+  int64_t len = lengths[b];
+  len = len < 1 ? 1 : (len > max_len ? max_len : len);
+  const int ntiles = static_cast<int>((len + DA_TILE - 1) / DA_TILE);
+  const int nvalid = min(nsplit, (ntiles + tps - 1) / tps);
+  float M = -INFINITY;
+  for (int s = 0; s < nvalid; ++s) M = fmaxf(M, ws_ml[((b * nsplit + s) * DA_H + h) * 2]);
+  float L = 0.f, N = 0.f;
+  for (int s = 0; s < nvalid; ++s) {
+    const int64_t base = (b * nsplit + s) * DA_H + h;
+    const float e = exp2f(ws_ml[base * 2] - M);
+    L += e * ws_ml[base * 2 + 1];
+    N += e * ws_o[base * DA_D + d];
+  }
+  out[(b * DA_H + h) * DA_D + d] = f2bf(N / L);
+}
+
+static int64_t workspace_bytes_for(int64_t B, const DecodeSplit &sp) {
+  if (sp.nsplit <= 1) return 0;
+  return B * sp.nsplit * DA_H * (DA_D + 2) * static_cast<int64_t>(sizeof(float));
+}
+
+static int device_cus_cached() {
+  static int cus = -1;
+  if (cus < 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+
+}  // namespace vk
+
+using namespace vk;
+
+extern "C" int vk_decode_attention_workspace(int64_t B, int32_t H, int64_t max_len, int64_t *bytes) {
+  VK_CHECK_ARG(bytes && B >= 0 && max_len > 0 && H == DA_H, "decode_attention_workspace: bad arguments");
+  *bytes = workspace_bytes_for(B, decode_split(B, max_len, device_cus_cached()));
+  return VK_OK;
+}
+
+extern "C" int vk_decode_attention(const void *q, const void *k_cache, const void *v_cache, const int32_t *lengths,
+                                   void *out, int64_t B, int32_t H, int32_t HKV, int32_t D, int64_t stride_b,
+                                   int64_t stride_s, int64_t max_len, void *workspace, int64_t workspace_bytes,
+                                   void *stream) {
+  VK_CHECK_ARG(q && k_cache && v_cache && lengths && out, "decode_attention: null pointer");
+  if (H != DA_H || HKV != DA_HKV || D != DA_D)
+    return fail(VK_ERR_UNSUPPORTED, "decode_attention: built for H=8 HKV=2 D=64 (got %d/%d/%d)", H, HKV, D);
+  VK_CHECK_ARG(B >= 0 && max_len > 0 && stride_s >= DA_ROW && stride_s % 8 == 0 && stride_b % 8 == 0,
+               "decode_attention: bad strides / sizes");
+  VK_CHECK_ARG(vk_aligned16(q) && vk_aligned16(k_cache) && vk_aligned16(v_cache),
+               "decode_attention: q and the caches must be 16-byte aligned");
+  VK_CHECK_ARG(B < 65536, "decode_attention: B must be < 65536");
+  if (B == 0) return VK_OK;
+  const DecodeSplit sp = decode_split(B, max_len, device_cus_cached());
+  const int64_t need = workspace_bytes_for(B, sp);
+  VK_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+               "decode_attention: workspace of %lld bytes needed", static_cast<long long>(need));
+  const float scale_log2 = static_cast<float>(1.0 / sqrt(static_cast<double>(DA_D)) * 1.4426950408889634);
+  hipStream_t s = VK_STREAM(stream);
+  const dim3 grid(sp.nsplit, static_cast<unsigned>(B));
+  if (sp.nsplit == 1) {
+    decode_attn_kernel<false><<<grid, DA_WAVES * 64, 0, s>>>(
+        static_cast<const bf16_t *>(q), static_cast<const bf16_t *>(k_cache), static_cast<const bf16_t *>(v_cache),
+        lengths, static_cast<bf16_t *>(out), stride_b, stride_s, max_len, sp.tps, 1, nullptr, nullptr, scale_log2);
+    return launch_status("decode_attention");
+  }
+  float *ws_o = static_cast<float *>(workspace);
+  float *ws_ml = ws_o + B * sp.nsplit * DA_H * DA_D;
+  decode_attn_kernel<true><<<grid, DA_WAVES * 64, 0, s>>>(
+      static_cast<const bf16_t *>(q), static_cast<const bf16_t *>(k_cache), static_cast<const bf16_t *>(v_cache),
+      lengths, static_cast<bf16_t *>(out), stride_b, stride_s, max_len, sp.tps, sp.nsplit, ws_o, ws_ml, scale_log2);
+  int st = launch_status("decode_attention");
+  if (st != VK_OK) return st;
+  decode_attn_combine<<<static_cast<unsigned>(B), DA_H * DA_D, 0, s>>>(ws_o, ws_ml, lengths,
+                                                                       static_cast<bf16_t *>(out), max_len, sp.tps,
+                                                                       sp.nsplit);
+  return launch_status("decode_attention_combine");
+}

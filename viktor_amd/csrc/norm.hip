@@ -1,0 +1,140 @@
+// Row-wise kernels of the packed token layout [n, d]: fused residual add + RMSNorm and the
+// embedding lookup + first RMSNorm of a decode step. One wavefront per row, 16-byte accesses.
+//
+// Rounding follows the reference's fused path (viktor/triton_ops.py:17-40, 149-169): the residual
+// sum is stored in bf16 and the norm is taken over that stored value; the normalised output is
+// (x * rsqrt(mean(x^2) + eps)) * w in fp32, rounded once to bf16.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "common.h"
+
+namespace vk {
+
+// Thread-local message of the last failure, returned by vk_last_error().
+static thread_local char g_msg[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_msg, sizeof(g_msg), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int launch_status(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(VK_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return VK_OK;
+}
+
+// CH = number of 8-element chunks each lane owns (d <= 512 * CH).
+template <int CH, bool EMBED>
+__global__ __launch_bounds__(256) void rmsnorm_rows(bf16_t *__restrict__ x, const bf16_t *__restrict__ delta,
+                                                    const int64_t *__restrict__ tok, const bf16_t *__restrict__ emb,
+                                                    int64_t vocab, const bf16_t *__restrict__ w,
+                                                    bf16_t *__restrict__ h, int64_t n, int d, float eps) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (row >= n) return;
+  const int nch = d >> 3;
+  const bf16_t *src = x + row * d;
+  bool zero_row = false;
+  if (EMBED) {
+    const int64_t t = tok[row];
+    zero_row = t < 0 || t >= vocab;
+    src = emb + (zero_row ? 0 : t) * d;
+  }
+  float v[CH][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ci = lane + c * kWave;
+    if (ci < nch) {
+      u32x4 a = *reinterpret_cast<const u32x4 *>(src + ci * 8);
+      if (EMBED && zero_row) a = u32x4{0u, 0u, 0u, 0u};
+      if (!EMBED && delta != nullptr) {
+        const u32x4 b = *reinterpret_cast<const u32x4 *>(delta + row * d + ci * 8);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] = pack_bf(lo_bf(a[j]) + lo_bf(b[j]), hi_bf(a[j]) + hi_bf(b[j]));
+        *reinterpret_cast<u32x4 *>(x + row * d + ci * 8) = a;
+      }
+      if (EMBED) *reinterpret_cast<u32x4 *>(x + row * d + ci * 8) = a;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[c][2 * j] = lo_bf(a[j]);
+        v[c][2 * j + 1] = hi_bf(a[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += v[c][j] * v[c][j];
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / static_cast<float>(d) + eps);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ci = lane + c * kWave;
+    if (ci < nch) {
+      const u32x4 wv = *reinterpret_cast<const u32x4 *>(w + ci * 8);
+      u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = pack_bf(v[c][2 * j] * r * lo_bf(wv[j]), v[c][2 * j + 1] * r * hi_bf(wv[j]));
+      *reinterpret_cast<u32x4 *>(h + row * d + ci * 8) = o;
+    }
+  }
+}
+
+template <bool EMBED>
+static int launch_rows(bf16_t *x, const bf16_t *delta, const int64_t *tok, const bf16_t *emb, int64_t vocab,
+                       const bf16_t *w, bf16_t *h, int64_t n, int d, float eps, hipStream_t s, const char *name) {
+  if (n == 0) return VK_OK;
+  const int rows_per_block = 4;
+  const dim3 grid(static_cast<unsigned>((n + rows_per_block - 1) / rows_per_block));
+  const int ch = (d / 8 + kWave - 1) / kWave;
+  if (ch <= 1)
+    rmsnorm_rows<1, EMBED><<<grid, 256, 0, s>>>(x, delta, tok, emb, vocab, w, h, n, d, eps);
+  else if (ch <= 2)
+    rmsnorm_rows<2, EMBED><<<grid, 256, 0, s>>>(x, delta, tok, emb, vocab, w, h, n, d, eps);
+  else
+    rmsnorm_rows<4, EMBED><<<grid, 256, 0, s>>>(x, delta, tok, emb, vocab, w, h, n, d, eps);
+  return launch_status(name);
+}
+
+}  // namespace vk
+
+using namespace vk;
+
+extern "C" int vk_version(void) { return 100; }
+
+extern "C" const char *vk_last_error(void) { return vk::g_msg; }
+
+extern "C" int vk_device_cus(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return cus;
+}
+
+extern "C" int vk_add_rmsnorm(void *x, const void *delta, const void *w, void *h, int64_t n, int32_t d, float eps,
+                              void *stream) {
+  VK_CHECK_ARG(x && w && h, "add_rmsnorm: null pointer");
+  VK_CHECK_ARG(n >= 0 && d > 0 && d % 8 == 0 && d <= 2048, "add_rmsnorm: need 0 < d <= 2048, d %% 8 == 0 (d=%d)", d);
+  VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w) && vk_aligned16(h) && (!delta || vk_aligned16(delta)),
+               "add_rmsnorm: pointers must be 16-byte aligned");
+  return launch_rows<false>(static_cast<bf16_t *>(x), static_cast<const bf16_t *>(delta), nullptr, nullptr, 0,
+                            static_cast<const bf16_t *>(w), static_cast<bf16_t *>(h), n, d, eps, VK_STREAM(stream),
+                            "add_rmsnorm");
+}
+
+extern "C" int vk_embed_rmsnorm(const int64_t *tok, const void *emb, int64_t vocab, const void *w, void *x, void *h,
+                                int64_t n, int32_t d, float eps, void *stream) {
+  VK_CHECK_ARG(tok && emb && w && x && h, "embed_rmsnorm: null pointer");
+  VK_CHECK_ARG(n >= 0 && d > 0 && d % 8 == 0 && d <= 2048 && vocab > 0, "embed_rmsnorm: bad sizes (d=%d)", d);
+  VK_CHECK_ARG(vk_aligned16(emb) && vk_aligned16(w) && vk_aligned16(x) && vk_aligned16(h),
+               "embed_rmsnorm: pointers must be 16-byte aligned");
+  return launch_rows<true>(static_cast<bf16_t *>(x), nullptr, tok, static_cast<const bf16_t *>(emb), vocab,
+                           static_cast<const bf16_t *>(w), static_cast<bf16_t *>(h), n, d, eps, VK_STREAM(stream),
+                           "embed_rmsnorm");
+}

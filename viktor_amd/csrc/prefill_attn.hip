@@ -1,0 +1,213 @@
+// Variable-length GQA attention of packed queries against per-sequence key ranges, bf16 MFMA with
+// fp32 online softmax (the semantics of flash_attn_varlen_func as called at
+// viktor/fast_decoder.py:68-73, and of flash_attn_func(causal=True) at viktor/decoder.py:82-87).
+//
+// MI355X design:
+//   * Workgroup = one 64-query block of one sequence x one KV head; its 4 wavefronts are the 4 query
+//     heads of that KV head, so every K/V tile staged in LDS serves 4 heads (GQA 4:1).
+//   * Keys advance in 32-row tiles, double buffered in LDS (next tile's global loads in flight during
+//     the MFMAs on the current one; 16-byte pad per row).
+//   * Transposed products as in the decode kernel: S^T = K Q^T (A = key rows from LDS, B = Q^T held in
+//     registers for the whole loop) leaves each lane the scores of one query column; O^T = V^T P^T
+//     consumes those probabilities in place and the online-softmax rescale stays lane-local.
+//   * Keys of sequence i live at base + k_off[i] + j * stride_tok (+ kv head * 64): the same kernel
+//     reads packed k/v rows or a KV-cache layer directly.
+//   * The host orders the query blocks longest-first (causal blocks near the end of a sequence do the
+//     most work) so the tail of the grid is short blocks.
+#include <math.h>
+
+#include "common.h"
+
+namespace vk {
+
+constexpr int PA_H = 8, PA_HKV = 2, PA_D = 64;
+constexpr int PA_Q = 64;      // query rows per workgroup (per wave: one head x 64 queries)
+constexpr int PA_KT = 32;     // keys per LDS tile
+constexpr int PA_PITCH = 72;  // 64 + 8 bf16
+
+__global__ __launch_bounds__(256) void varlen_attn_kernel(
+    const bf16_t *__restrict__ q, const bf16_t *__restrict__ k, const bf16_t *__restrict__ v,
+    const int32_t *__restrict__ cu_q, const int64_t *__restrict__ k_off, const int32_t *__restrict__ k_lens,
+    const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok, bf16_t *__restrict__ out, int causal,
+    float scale_log2) {
+  __shared__ __attribute__((aligned(16))) bf16_t Ks[2][PA_KT * PA_PITCH];
+  __shared__ __attribute__((aligned(16))) bf16_t Vs[2][PA_KT * PA_PITCH];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int col = lane & 15, g = lane >> 4;
+  const int hk = blockIdx.y;
+  const int hq = hk * (PA_H / PA_HKV) + wid;
+  const int seq = plan[2 * blockIdx.x];
+  const int qs = plan[2 * blockIdx.x + 1];
+  if (seq < 0 || seq >= n_seq || qs < 0) return;
+  const int64_t q0 = cu_q[seq];
+  const int q_len = cu_q[seq + 1] - static_cast<int>(q0);
+  const int klen = k_lens[seq];
+  if (q_len <= 0 || klen <= 0 || qs >= q_len) return;
+  const int64_t koff = k_off[seq];
+  const int qshift = klen - q_len;  // query r sits at key position qshift + r
+  const int nq = min(PA_Q, q_len - qs);
+  const int kend = causal ? min(klen, qshift + qs + nq) : klen;
+  if (kend <= 0) return;
+  const int ntiles = (kend + PA_KT - 1) / PA_KT;
+
+  // Q^T fragments for the 4 query blocks of 16 and the two 32-wide halves of D
+  bf16x8 bq[4][2];
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb) {
+    int r = qs + 16 * qb + col;
+    r = r < q_len ? r : q_len - 1;
+    const bf16_t *src = q + ((q0 + r) * PA_H + hq) * PA_D + g * 8;
+#pragma unroll
+    for (int dc = 0; dc < 2; ++dc) bq[qb][dc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(src + 32 * dc));
+  }
+  int qpos[4];
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb) {
+    int r = qs + 16 * qb + col;
+    r = r < q_len ? r : q_len - 1;
+    qpos[qb] = qshift + r;
+  }
+
+  f32x4 acc[4][4];  // [d tile][query block]
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[4], l_run[4];
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb) {
+    m_run[qb] = -INFINITY;
+    l_run[qb] = 0.f;
+  }
+
+  // cooperative tile load: thread -> (key row, 16-byte chunk)
+  const int lrow = tid >> 3, lchunk = tid & 7;
+  u32x4 rk, rv;
+  auto load_tile = [&](int t) {
+    int key = t * PA_KT + lrow;
+    key = key < klen ? key : klen - 1;
+    const int64_t off = koff + static_cast<int64_t>(key) * stride_tok + hk * PA_D + lchunk * 8;
+    rk = *reinterpret_cast<const u32x4 *>(k + off);
+    rv = *reinterpret_cast<const u32x4 *>(v + off);
+  };
+  auto store_tile = [&](int buf) {
+    *reinterpret_cast<u32x4 *>(&Ks[buf][lrow * PA_PITCH + lchunk * 8]) = rk;
+    *reinterpret_cast<u32x4 *>(&Vs[buf][lrow * PA_PITCH + lchunk * 8]) = rv;
+  };
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) load_tile(t + 1);
+    const int kbase = t * PA_KT;
+    // S^T[key][query] for the two 16-key blocks
+    f32x4 st[2][4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      bf16x8 ka[2];
+#pragma unroll
+      for (int dc = 0; dc < 2; ++dc)
+        ka[dc] = *reinterpret_cast<const bf16x8 *>(&Ks[buf][(16 * kb + col) * PA_PITCH + 32 * dc + g * 8]);
+#pragma unroll
+      for (int qb = 0; qb < 4; ++qb) {
+        st[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dc = 0; dc < 2; ++dc)
+          st[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[dc], bq[qb][dc], st[kb][qb], 0, 0, 0);
+      }
+    }
+    bf16x8 pf[4];
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) {
+      float sv[8];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kbase + 16 * kb + 4 * g + i;
+          const bool ok = key < klen && (!causal || key <= qpos[qb]);
+          const float s = ok ? st[kb][qb][i] * scale_log2 : -INFINITY;
+          sv[kb * 4 + i] = s;
+          mx = fmaxf(mx, s);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run[qb], mx);
+      // m_new is finite: tile 0 always holds key 0, visible to every query
+      const float alpha = exp2f(m_run[qb] - m_new);
+      float ps = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const float p = exp2f(sv[jj] - m_new);
+        ps += p;
+        pf[qb][jj] = __builtin_bit_cast(__bf16, f2bf(p));
+      }
+      l_run[qb] = l_run[qb] * alpha + ps;
+      m_run[qb] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) acc[dt][qb] *= alpha;
+    }
+    // O^T += V^T P^T
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      bf16x8 va;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const int kl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
+        va[jj] = __builtin_bit_cast(__bf16, Vs[buf][kl * PA_PITCH + 16 * dt + col]);
+      }
+#pragma unroll
+      for (int qb = 0; qb < 4; ++qb) acc[dt][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[qb], acc[dt][qb], 0, 0, 0);
+    }
+    if (t + 1 < ntiles) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb) {
+    float l = l_run[qb];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const int r = qs + 16 * qb + col;
+    if (r >= q_len) continue;
+    const float inv = 1.0f / l;
+    bf16_t *dst = out + ((q0 + r) * PA_H + hq) * PA_D + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      u32x2 pk;
+      pk[0] = pack_bf(acc[dt][qb][0] * inv, acc[dt][qb][1] * inv);
+      pk[1] = pack_bf(acc[dt][qb][2] * inv, acc[dt][qb][3] * inv);
+      *reinterpret_cast<u32x2 *>(dst + 16 * dt) = pk;
+    }
+  }
+}
+
+}  // namespace vk
+
+using namespace vk;
+
+extern "C" int vk_varlen_attention(const void *q, const void *k, const void *v, const int32_t *cu_q,
+                                   const int64_t *k_off, const int32_t *k_lens, const int32_t *plan, int32_t n_blocks,
+                                   int32_t n_seq, int64_t stride_tok, void *out, int32_t causal, int32_t H,
+                                   int32_t HKV, int32_t D, void *stream) {
+  VK_CHECK_ARG(q && k && v && cu_q && k_off && k_lens && out, "varlen_attention: null pointer");
+  if (H != PA_H || HKV != PA_HKV || D != PA_D)
+    return fail(VK_ERR_UNSUPPORTED, "varlen_attention: built for H=8 HKV=2 D=64 (got %d/%d/%d)", H, HKV, D);
+  VK_CHECK_ARG(n_blocks >= 0 && n_seq >= 0 && stride_tok >= PA_HKV * PA_D && stride_tok % 8 == 0,
+               "varlen_attention: bad sizes");
+  VK_CHECK_ARG(n_blocks == 0 || plan != nullptr, "varlen_attention: missing plan");
+  VK_CHECK_ARG(vk_aligned16(q) && vk_aligned16(k) && vk_aligned16(v) && vk_aligned16(out),
+               "varlen_attention: pointers must be 16-byte aligned");
+  if (n_blocks == 0) return VK_OK;
+  const float scale_log2 = static_cast<float>(1.0 / sqrt(static_cast<double>(PA_D)) * 1.4426950408889634);
+  const dim3 grid(static_cast<unsigned>(n_blocks), PA_HKV);
+  varlen_attn_kernel<<<grid, 256, 0, VK_STREAM(stream)>>>(
+      static_cast<const bf16_t *>(q), static_cast<const bf16_t *>(k), static_cast<const bf16_t *>(v), cu_q, k_off,
+      k_lens, plan, n_seq, stride_tok, static_cast<bf16_t *>(out), causal, scale_log2);
+  return launch_status("varlen_attention");
+}

@@ -1,0 +1,168 @@
+// Fused LM head + token choice + decode-state update (one workgroup of 256 threads per sequence).
+//
+// Semantics (viktor/engine.py:79-116 and viktor/triton_ops.py:172-209):
+//   z = logits + bias (bias = -inf at PAD and BOS);
+//   greedy: first index of max(z); sampled: inverse CDF of softmax(z / T) at the supplied uniform
+//   (the reference draws Gumbel noise from the device RNG instead; the supplied uniform makes the
+//   stream reproducible);
+//   grammar, in the reference's order: EOS after a tail token; homopolymer run counter and EOS when the
+//   run reaches homo_stop tokens; PAD after EOS / PAD;
+//   out[b, pos - plen] = token; tok = token; pos += 1 and the int32 mirrors pos32 = pos,
+//   seqlens = pos + 1, rpos32 = pos + rope_off.
+// The LM head is computed here from the final hidden state (bf16 x bf16 -> fp32, optionally rounded to
+// bf16 as an nn.Linear in bf16 would) or read as fp32 logits.
+#include <math.h>
+
+#include "common.h"
+
+namespace vk {
+
+constexpr int SEL_THREADS = 256;
+constexpr int SEL_MAXV = 512;
+
+__global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
+    const float *__restrict__ logits, const bf16_t *__restrict__ h, const bf16_t *__restrict__ w_head, int d,
+    int round_bf16, const float *__restrict__ bias, const uint8_t *__restrict__ is_tail,
+    const uint8_t *__restrict__ is_homo, int homo_stop, float temperature, const float *__restrict__ uniforms,
+    int64_t u_stride, int64_t u_cols, int64_t *__restrict__ tok, int64_t *__restrict__ run, int64_t *__restrict__ pos,
+    const int64_t *__restrict__ plen, const int64_t *__restrict__ rope_off, int64_t *__restrict__ out,
+    int64_t out_stride, int64_t out_cols, int32_t *__restrict__ pos32, int32_t *__restrict__ seqlens,
+    int32_t *__restrict__ rpos32, float *__restrict__ logp_out, int V, int eos, int pad) {
+  __shared__ float z[SEL_MAXV];
+  __shared__ float red_v[SEL_THREADS / 64];
+  __shared__ int red_i[SEL_THREADS / 64];
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+
+  // 1. logits (+ bias), fp32
+  if (logits != nullptr) {
+    for (int v = tid; v < V; v += SEL_THREADS) z[v] = logits[b * V + v] + bias[v];
+  } else {
+    const bf16_t *hr = h + b * d;
+    for (int v = wid; v < V; v += SEL_THREADS / 64) {
+      const bf16_t *wr = w_head + static_cast<int64_t>(v) * d;
+      float acc = 0.f;
+      for (int c = lane * 8; c < d; c += 64 * 8) {
+        const u32x4 hv = *reinterpret_cast<const u32x4 *>(hr + c);
+        const u32x4 wv = *reinterpret_cast<const u32x4 *>(wr + c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc += lo_bf(hv[j]) * lo_bf(wv[j]) + hi_bf(hv[j]) * hi_bf(wv[j]);
+      }
+      acc = wave_sum(acc);
+      if (lane == 0) z[v] = (round_bf16 ? round_bf(acc) : acc) + bias[v];
+    }
+  }
+  __syncthreads();
+
+  const bool sample = temperature > 0.f;
+  if (sample)
+    for (int v = tid; v < V; v += SEL_THREADS) z[v] = z[v] / temperature;
+  __syncthreads();
+
+  // 2. max with first-index tie-break (greedy choice and softmax shift)
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int v = tid; v < V; v += SEL_THREADS) {
+    const float zv = z[v];
+    if (zv > best || (zv == best && v < bi)) {
+      best = zv;
+      bi = v;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (ov > best || (ov == best && oi < bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    red_v[wid] = best;
+    red_i[wid] = bi;
+  }
+  __syncthreads();
+  if (tid != 0) return;
+  best = red_v[0];
+  bi = red_i[0];
+  for (int w = 1; w < SEL_THREADS / 64; ++w)
+    if (red_v[w] > best || (red_v[w] == best && red_i[w] < bi)) {
+      best = red_v[w];
+      bi = red_i[w];
+    }
+  if (bi >= V) bi = 0;  // all -inf / NaN row: fall back to token 0 (PAD)
+
+  // 3. choice (single thread: the CDF is accumulated in token order)
+  int64_t nxt = bi;
+  float sum = 0.f;
+  const float zmax = best;
+  if (sample || logp_out) {
+    for (int v = 0; v < V; ++v) sum += expf(z[v] - zmax);
+  }
+  const int64_t p = pos[b];
+  const int64_t pl = plen ? plen[b] : 0;
+  const int64_t ocol = p - pl;
+  if (sample) {
+    int64_t uc = ocol < 0 ? 0 : (ocol >= u_cols ? u_cols - 1 : ocol);
+    const float u = uniforms[b * u_stride + uc];
+    const float inv = 1.0f / sum;
+    float cdf = 0.f;
+    int64_t pick = -1, last_pos = bi;
+    for (int v = 0; v < V; ++v) {
+      const float pv = expf(z[v] - zmax) * inv;
+      if (pv > 0.f) last_pos = v;
+      cdf += pv;
+      if (pick < 0 && u < cdf) pick = v;
+    }
+    nxt = pick >= 0 ? pick : last_pos;
+  }
+  if (logp_out) logp_out[b] = z[nxt] - zmax - logf(sum);
+
+  // 4. grammar and bookkeeping
+  const int64_t prev = tok[b];
+  if (prev >= 0 && prev < V && is_tail[prev]) nxt = eos;
+  if (homo_stop > 0) {
+    const bool same = nxt == prev && nxt >= 0 && nxt < V && is_homo[nxt];
+    const int64_t r = same ? run[b] + 1 : 0;
+    run[b] = r;
+    if (r + 1 >= homo_stop) nxt = eos;
+  }
+  if (prev == eos || prev == pad) nxt = pad;
+  if (ocol >= 0 && ocol < out_cols) out[b * out_stride + ocol] = nxt;
+  tok[b] = nxt;
+  const int64_t np = p + 1;
+  pos[b] = np;
+  if (pos32) pos32[b] = static_cast<int32_t>(np);
+  if (seqlens) seqlens[b] = static_cast<int32_t>(np + 1);
+  if (rpos32) rpos32[b] = static_cast<int32_t>(np + (rope_off ? rope_off[b] : 0));
+}
+
+}  // namespace vk
+
+using namespace vk;
+
+extern "C" int vk_select_update(const float *logits, const void *h, const void *w_head, int32_t d, int32_t round_bf16,
+                                const float *bias, const uint8_t *is_tail, const uint8_t *is_homo, int32_t homo_stop,
+                                float temperature, const float *uniforms, int64_t u_stride, int64_t u_cols,
+                                int64_t *tok, int64_t *run, int64_t *pos, const int64_t *plen, const int64_t *rope_off,
+                                int64_t *out, int64_t out_stride, int64_t out_cols, int32_t *pos32, int32_t *seqlens,
+                                int32_t *rpos32, float *logp_out, int64_t B, int32_t V, int32_t eos, int32_t pad,
+                                void *stream) {
+  VK_CHECK_ARG(bias && is_tail && is_homo && tok && pos && out, "select_update: null pointer");
+  VK_CHECK_ARG(V > 0 && V <= SEL_MAXV, "select_update: vocab must be in 1..%d (got %d)", SEL_MAXV, V);
+  VK_CHECK_ARG(B >= 0 && B < (int64_t(1) << 31), "select_update: bad batch");
+  VK_CHECK_ARG((logits != nullptr) != (h != nullptr && w_head != nullptr),
+               "select_update: pass either logits or (h, w_head)");
+  VK_CHECK_ARG(logits != nullptr || (d > 0 && d % 8 == 0 && vk_aligned16(h) && vk_aligned16(w_head)),
+               "select_update: LM head needs d %% 8 == 0 and 16-byte aligned h, w_head");
+  VK_CHECK_ARG(homo_stop <= 0 || run != nullptr, "select_update: homopolymer rule needs run");
+  VK_CHECK_ARG(!(temperature > 0.f) || (uniforms != nullptr && u_cols > 0), "select_update: sampling needs uniforms");
+  VK_CHECK_ARG(out_cols > 0, "select_update: empty output buffer");
+  if (B == 0) return VK_OK;
+  select_update_kernel<<<static_cast<unsigned>(B), SEL_THREADS, 0, VK_STREAM(stream)>>>(
+      logits, static_cast<const bf16_t *>(h), static_cast<const bf16_t *>(w_head), d, round_bf16, bias, is_tail,
+      is_homo, homo_stop, temperature, uniforms, u_stride, u_cols, tok, run, pos, plen, rope_off, out, out_stride,
+      out_cols, pos32, seqlens, rpos32, logp_out, V, eos, pad);
+  return launch_status("select_update");
+}

@@ -1,0 +1,197 @@
+"""Greedy or sampled decoding of variable-length prefixes on the HIP kernels: static KV cache, packed
+prefill with a BOS-only last layer, one captured HIP graph per decode step.
+
+Call surface and state machine of viktor/engine.py:31-220 (DecodeEngine). Each sequence's prefix is its
+projected encoder frames + BOS, so every sequence decodes at its own position; finished sequences keep
+running and emit PAD, which keeps every step shape-static and graph-capturable. A step is
+  embed + RMSNorm -> 8 decoder layers -> fused LM head + token choice + grammar + state update,
+with all state in preallocated device tensors and no host synchronisation inside the step.
+
+Sampling (temperature > 0) draws each token from softmax(logits / T) by the inverse CDF at one uniform
+per (sequence, output column): `uniforms` [B, max_new_tokens]. The reference draws Gumbel noise from the
+device RNG inside its graph (viktor/engine.py:80-83); here the engine fills the uniforms from the torch
+RNG at prefill unless the caller supplied them (set_uniforms), which makes a rollout reproducible.
+"""
+
+import torch
+
+from . import hip_ops as ops
+from ._lib import HipLibraryError
+from .decoder import KVCache
+from .fast_decoder import FastDecoder, PrefillPlan
+from .tokenizer import BOS, EOS, PAD
+
+
+class DecodeEngine:
+    def __init__(self, model, batch_size: int, max_new_tokens: int, max_frames: int, backend: str = "auto",
+                 cuda_graph: bool = True, prefill_batch: int = 128, check_every: int = 32,
+                 attention_backend: str = "auto", temperature: float = 0.0, max_homopolymer=64):
+        self.model, self.dec = model, model.decoder
+        self.temperature = float(temperature)
+        dev = self.dec.lm_head.weight.device
+        self.dtype = self.dec.lm_head.weight.dtype
+        self.pos_scale = getattr(model, "pos_scale", 1)
+        if backend not in ("auto", "hip", "triton"):
+            raise ValueError(f"unknown backend {backend!r}: this engine runs the HIP kernels ('auto' / 'hip')")
+        if dev.type != "cuda" or torch.version.hip is None:
+            raise HipLibraryError("DecodeEngine runs on a ROCm GPU (the model is on %s)" % dev)
+        if self.dtype != torch.bfloat16:
+            raise AssertionError("DecodeEngine needs the bf16 inference copy of the model (see gspo.bf16_copy)")
+        self.backend = "hip"
+        self.fast = FastDecoder(self.dec, attention_backend=attention_backend)
+        self.B, self.max_new = batch_size, max_new_tokens
+        self.prefill_batch, self.check_every = prefill_batch, check_every
+        self._prefill_plans = {}
+        max_len = max_frames + 1 + max_new_tokens
+        assert max_len <= self.dec.cfg.max_seq_len
+        self.max_frames = max_frames
+        self.cache = KVCache(self.dec.cfg, batch_size, max_len, self.dtype, dev)
+
+        self.tok = torch.full((batch_size,), BOS, dtype=torch.long, device=dev)
+        self.pos = torch.zeros(batch_size, dtype=torch.long, device=dev)
+        self.rope_off = torch.zeros(batch_size, dtype=torch.long, device=dev)  # RoPE position - cache position
+        self.pos32 = torch.zeros(batch_size, dtype=torch.int32, device=dev)
+        self.rpos32 = torch.zeros(batch_size, dtype=torch.int32, device=dev)
+        self.seqlens = torch.zeros(batch_size, dtype=torch.int32, device=dev)
+        self.rows = torch.arange(batch_size, dtype=torch.int32, device=dev)
+        self.step_idx = torch.zeros(1, dtype=torch.long, device=dev)
+        self.out = torch.full((batch_size, max_new_tokens), PAD, dtype=torch.long, device=dev)
+        self.bos = torch.tensor([BOS], device=dev)
+        tk = model.tokenizer
+        self.bias = torch.zeros(tk.vocab_size, device=dev)
+        self.bias[[PAD, BOS]] = float("-inf")
+        self.is_tail = tk.tail_mask.to(dev)
+        self.is_homo = torch.tensor([i >= 3 and len(t) == tk.k and len(set(t)) == 1 for i, t in enumerate(tk.strings)],
+                                    device=dev)
+        self.homo_stop = max_homopolymer // tk.k if max_homopolymer else 0  # run length in tokens that ends it
+        self.run = torch.zeros(batch_size, dtype=torch.long, device=dev)
+        self.plen = torch.zeros(batch_size, dtype=torch.long, device=dev)  # output column = pos - plen
+        self.uniforms = torch.zeros(batch_size, max_new_tokens, dtype=torch.float32, device=dev)
+        self._uniforms_set = False
+        self.fast.decode_workspace = ops.decode_attention_workspace(batch_size, self.dec.cfg.n_heads, max_len, dev)
+        self.graph = None
+        if cuda_graph:
+            self._capture()
+
+    # ---- one decode step -----------------------------------------------------------------------
+    def _select_update(self, h):
+        ops.select_update(self.bias, self.is_tail, self.is_homo, self.homo_stop, self.tok, self.run, self.pos,
+                          self.plen, self.rope_off, self.out, self.pos32, self.seqlens, self.rpos32, EOS, PAD,
+                          h=h, w_head=self.dec.lm_head.weight, round_bf16=self.temperature > 0,
+                          temperature=self.temperature, uniforms=self.uniforms)
+
+    def _step(self):
+        # greedy steps choose from fp32 logits, sampled steps from bf16 logits (as the reference's two step kinds)
+        h = self.fast.decode(None, self.pos32, self.rows, self.seqlens, self.cache,
+                             rope_pos=None if self.pos_scale == 1 else self.rpos32, tok=self.tok)
+        self._select_update(h)
+        self.step_idx.add_(1)
+
+    def _reset_state(self):
+        self.pos.fill_(1)
+        self.pos32.fill_(1)
+        self.seqlens.fill_(2)
+        self.rpos32.fill_(1)
+        self.tok.fill_(BOS)
+        self.step_idx.zero_()
+
+    @torch.no_grad()
+    def _capture(self):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                self._reset_state()
+                self._step()
+        torch.cuda.current_stream().wait_stream(s)
+        self._reset_state()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._step()
+        self.out.fill_(PAD)
+
+    # ---- prefill -------------------------------------------------------------------------------
+    def _prefill_hip(self, prefix, lens, row0):
+        """prefix [sum(lens), d] projected frames of sequences row0.. ; returns the final hidden at each BOS."""
+        dev = prefix.device
+        n = len(lens)
+        key = tuple(lens)
+        entry = self._prefill_plans.get(row0)
+        if entry is None or entry[0] != key:
+            seq_lens = [L + 1 for L in lens]
+            plan = PrefillPlan(seq_lens, dev, rows=list(range(row0, row0 + n)), keep=[1] * n, cache=self.cache)
+            L = torch.tensor(lens, device=dev)
+            total, frames = plan.total, sum(lens)
+            cu = torch.tensor(plan.cu, dtype=torch.int32, device=dev)
+            frame_seg = torch.repeat_interleave(torch.arange(n, device=dev), L, output_size=frames)
+            frame_idx = torch.arange(frames, device=dev) + frame_seg
+            last = cu[1:].long() - 1
+            pos = (torch.arange(total, device=dev)
+                   - torch.repeat_interleave(cu[:-1].long(), L + 1, output_size=total)).int()
+            seq = torch.repeat_interleave(torch.arange(row0, row0 + n, device=dev, dtype=torch.int32), L + 1,
+                                          output_size=total)
+            rpos = None if self.pos_scale == 1 else (pos * self.pos_scale).int()
+            entry = key, (plan, frame_idx, last, pos, seq, rpos)
+            self._prefill_plans[row0] = entry
+        plan, frame_idx, last, pos, seq, rpos = entry[1]
+        x = torch.empty(plan.total, prefix.shape[1], dtype=self.dtype, device=dev)
+        x[frame_idx] = prefix
+        x[last] = self.dec.embed.weight[BOS].to(self.dtype)
+        return self.fast.prefill(x, pos, seq, None, plan.max_len, self.cache, rope_pos=rpos, plan=plan)
+
+    def set_uniforms(self, u):
+        """Uniforms [B, max_new_tokens] in [0, 1) driving the sampled tokens (column j -> output token j)."""
+        assert u.shape == self.uniforms.shape
+        self.uniforms.copy_(u)
+        self._uniforms_set = True
+
+    @torch.no_grad()
+    def prefill(self, frames, frame_lens):
+        """frames [sum(frame_lens), d_enc]: encoder frames of B chunks, concatenated; frame_lens [B].
+        Fills the cache and emits the first token of every sequence (chosen from bf16 logits, as the
+        reference does at viktor/engine.py:191)."""
+        frame_lens = [int(n) for n in frame_lens]
+        assert len(frame_lens) == self.B and frames.shape[0] == sum(frame_lens)
+        assert all(0 < n <= self.max_frames for n in frame_lens), "frame count outside 1..max_frames"
+        if self.temperature > 0 and not self._uniforms_set:
+            self.uniforms.uniform_()
+        self._uniforms_set = False
+        offs = [0]
+        for n in frame_lens:
+            offs.append(offs[-1] + n)
+        last = []
+        for lo in range(0, self.B, self.prefill_batch):
+            hi = min(self.B, lo + self.prefill_batch)
+            prefix = self.model.projector(frames[offs[lo]:offs[hi]].to(self.dtype))
+            last.append(self._prefill_hip(prefix, frame_lens[lo:hi], lo))
+        h = torch.cat(last) if len(last) > 1 else last[0]
+        self.tok.fill_(BOS)
+        self.run.zero_()
+        self.out.fill_(PAD)
+        self.plen.copy_(torch.tensor(frame_lens, device=self.pos.device))
+        self.pos.copy_(self.plen)  # the select kernel writes column pos - plen = 0, then advances pos to plen + 1
+        self.rope_off.copy_(self.plen * (self.pos_scale - 1))
+        ops.select_update(self.bias, self.is_tail, self.is_homo, self.homo_stop, self.tok, self.run, self.pos,
+                          self.plen, self.rope_off, self.out, self.pos32, self.seqlens, self.rpos32, EOS, PAD,
+                          h=h.contiguous(), w_head=self.dec.lm_head.weight, round_bf16=True,
+                          temperature=self.temperature, uniforms=self.uniforms)
+        self.step_idx.fill_(1)
+
+    @torch.no_grad()
+    def decode(self, steps=None):
+        """Run decode steps after prefill. steps=None: stop when all sequences ended (checked every
+        check_every steps) or at max_new_tokens. steps=n: run exactly n-1 steps (n output tokens)."""
+        n = self.max_new - 1 if steps is None else steps - 1
+        for i in range(n):
+            if self.graph is not None:
+                self.graph.replay()
+            else:
+                self._step()
+            if steps is None and (i + 1) % self.check_every == 0 and bool(((self.tok == EOS) | (self.tok == PAD)).all()):
+                break
+        return self.out
+
+    def generate(self, frames, frame_lens, steps=None):
+        """Returns token ids [B, max_new_tokens] (PAD after EOS). The buffer is reused by the next call."""
+        self.prefill(frames, frame_lens)
+        return self.decode(steps)

@@ -1,0 +1,244 @@
+"""Inference forward of the Decoder on the gfx950 HIP kernels (same weights as decoder.Decoder).
+
+Tokens are packed [n_tokens, d]: a prefill packs the prefixes of many variable-length sequences, a
+decode step is one token per sequence. Per layer (reference: viktor/fast_decoder.py:33-60):
+  qkv GEMM -> QK-norm + RoPE + KV-cache write -> attention -> o GEMM + residual add + RMSNorm
+  -> gate_up GEMM with SwiGLU epilogue -> down GEMM + residual add + next RMSNorm.
+Every GEMM, norm and attention runs on libviktor_hip.so; there is no other backend.
+Prefill attention reads K/V straight from the KV cache when one is given (packed k/v otherwise); the
+last layer of a prefill can keep only some rows of each sequence (the BOS row for the engine, the
+response rows for teacher-forced scoring), which then attend to their whole sequence.
+"""
+
+import torch
+
+from . import hip_ops as ops
+from ._lib import HipLibraryError, require_device
+
+BF16 = torch.bfloat16
+
+
+def _require(cond, msg):
+    if not cond:
+        raise AssertionError(msg)
+
+
+class PrefillPlan:
+    """Host-side layout of one packed prefill (built from Python ints; no device reads).
+
+    seq_lens[j]: tokens of sequence j (packed back to back); rows[j]: its KV-cache row (None without a
+    cache); keep[j]: rows of sequence j kept by the last layer (its final keep[j] positions), None to keep
+    all. Construction uploads the few small index tensors once; engines cache plans per layout."""
+
+    def __init__(self, seq_lens, device, rows=None, keep=None, cache=None):
+        seq_lens = [int(n) for n in seq_lens]
+        _require(all(n > 0 for n in seq_lens), "PrefillPlan: empty sequence")
+        self.seq_lens = seq_lens
+        self.n_seq = len(seq_lens)
+        cu = [0]
+        for n in seq_lens:
+            cu.append(cu[-1] + n)
+        self.cu = cu
+        self.total = cu[-1]
+        self.max_len = max(seq_lens) if seq_lens else 0
+        self.rows = None if rows is None else [int(r) for r in rows]
+        self.device = device
+        if cache is not None:
+            _require(self.rows is not None and len(self.rows) == self.n_seq, "PrefillPlan: rows for the cache")
+            sb, ss = cache.k.stride(1), cache.k.stride(2)
+            k_off = [r * sb for r in self.rows]
+            self.stride_tok = ss
+        else:
+            hkv_d = None
+            k_off = None
+            self.stride_tok = None
+        self.from_cache = cache is not None
+        self._k_off = k_off
+        self.full = None if cache is None else ops.AttentionPlan(seq_lens, seq_lens, k_off, device, causal=True)
+        self.keep = None if keep is None else [int(k) for k in keep]
+        self.last = None
+        self.last_idx = None
+        self.bos_lengths = None
+        if self.keep is not None:
+            _require(len(self.keep) == self.n_seq and all(0 < k <= n for k, n in zip(self.keep, seq_lens)),
+                     "PrefillPlan: keep counts")
+            idx = [cu[j + 1] - k + i for j, k in enumerate(self.keep) for i in range(k)]
+            self.last_idx = torch.tensor(idx, dtype=torch.long).to(device)
+            if cache is not None:
+                self.last = ops.AttentionPlan(self.keep, seq_lens, k_off, device, causal=True)
+                contiguous_rows = all(r == self.rows[0] + j for j, r in enumerate(self.rows))
+                if all(k == 1 for k in self.keep) and contiguous_rows:
+                    # one query per sequence (its last position): single-query decode kernel on the cache
+                    self.bos_lengths = torch.tensor(seq_lens, dtype=torch.int32).to(device)
+
+    def packed_plans(self, hkv_d):
+        """Attention plans over packed k/v rows [total, HKV, D] (no cache)."""
+        k_off = [c * hkv_d for c in self.cu[:-1]]
+        full = ops.AttentionPlan(self.seq_lens, self.seq_lens, k_off, self.device, causal=True)
+        last = None if self.keep is None else ops.AttentionPlan(self.keep, self.seq_lens, k_off, self.device, causal=True)
+        return full, last
+
+
+class FastDecoder:
+    """Packed-token forward of a Decoder on the HIP kernels (reference: viktor/fast_decoder.py:17-90)."""
+
+    def __init__(self, dec, attention_backend="auto"):
+        cfg = dec.cfg
+        if attention_backend not in ("auto", "hip", "triton"):
+            raise ValueError(f"unknown decode attention backend: {attention_backend}")
+        if (cfg.n_heads, cfg.n_kv_heads, cfg.head_dim) != (8, 2, 64):
+            raise ValueError("the HIP attention kernels are built for 8 query heads, 2 KV heads, head_dim 64 "
+                             f"(got {cfg.n_heads}/{cfg.n_kv_heads}/{cfg.head_dim})")
+        _require(cfg.d_model % 64 == 0 and cfg.ffn_dim % 32 == 0, "FastDecoder: d_model % 64, ffn_dim % 32")
+        self.dec, self.cfg = dec, cfg
+        self.attention_backend = "hip"
+        self._wcache = {}
+        self._plans = {}
+        self.decode_workspace = None
+
+    # weights: bf16 views of the module's parameters (in place when the module is bf16, so weight syncs
+    # into it stay visible to captured graphs; converted copies, refreshed on change, otherwise)
+    def w(self, p):
+        if p.dtype == BF16 and p.is_contiguous():
+            return p
+        key = id(p)
+        ver = (p.data_ptr(), p._version)
+        hit = self._wcache.get(key)
+        if hit is not None and hit[0] == ver:
+            return hit[1]
+        conv = p.detach().to(BF16).contiguous()
+        self._wcache[key] = (ver, conv)
+        return conv
+
+    def _tables(self):
+        return self.dec.cos, self.dec.sin
+
+    def _layers(self, x, pos, seq, cache, attend, return_kv, last_idx=None, rope_pos=None, h=None):
+        """x [n, d] residual stream (updated in place); h: its first attention norm when already computed.
+        Returns the final-normed hidden [n or len(last_idx), d]."""
+        cfg, layers, W = self.cfg, self.dec.layers, self.w
+        eps = cfg.norm_eps
+        cos, sin = self._tables()
+        if h is None:
+            h = ops.add_rmsnorm(x, W(layers[0].attn_norm.weight), eps)
+        n_layers = len(layers)
+        for i, blk in enumerate(layers):
+            a = blk.attn
+            qkv = ops.linear(h, W(a.qkv_proj.weight))
+            kc = cache.k[i] if cache is not None else None
+            vc = cache.v[i] if cache is not None else None
+            r = ops.qkv_rope_cache(qkv, W(a.q_norm.weight), W(a.k_norm.weight), cos, sin, pos, seq, kc, vc, eps,
+                                   cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, return_kv=return_kv, rope_pos=rope_pos)
+            last = last_idx is not None and i == n_layers - 1
+            if last:
+                # rows without a consumer are dropped: all K/V are kept, only the kept rows finish the layer
+                x = x[last_idx]
+                if return_kv:
+                    q, k, v = r
+                    r = (q[last_idx], k, v)
+                else:
+                    r = r[last_idx]
+            o = attend(i, r, last)
+            h = ops.add_rmsnorm(x, W(blk.mlp_norm.weight), eps,
+                                delta=ops.linear(o.reshape(x.shape[0], -1), W(a.o_proj.weight)))
+            g = ops.linear(h, W(blk.gate_up.weight), swiglu=True)
+            m = ops.linear(g, W(blk.down.weight))
+            w_next = layers[i + 1].attn_norm.weight if i + 1 < n_layers else self.dec.norm.weight
+            h = ops.add_rmsnorm(x, W(w_next), eps, delta=m)
+        return h
+
+    def prefill(self, x, pos, seq, cu_seqlens, max_seqlen, cache, last_indices=None, cu_queries=None, rope_pos=None,
+                plan=None):
+        """x [n, d] packed prefix embeddings of several sequences; pos/seq [n] int32 (position, cache row);
+        cu_seqlens [b+1] int32. Fills the cache rows of those sequences. Returns hidden [n, d], or the kept
+        rows when last_indices and cu_queries are given together (e.g. [b, d] at each sequence's last
+        position). plan: a PrefillPlan of this layout (built here from cu_seqlens / seq / cu_queries
+        otherwise, which reads them back to the host). Reference: viktor/fast_decoder.py:62-74."""
+        require_device(x, "FastDecoder.prefill")
+        _require((last_indices is None) == (cu_queries is None), "prefill: last_indices and cu_queries go together")
+        if plan is None:
+            cu = [int(c) for c in cu_seqlens.tolist()]
+            lens = [b - a for a, b in zip(cu[:-1], cu[1:])]
+            keep = None
+            if cu_queries is not None:
+                cq = [int(c) for c in cu_queries.tolist()]
+                keep = [b - a for a, b in zip(cq[:-1], cq[1:])]
+            rows = None
+            if cache is not None:
+                seq_h = seq.tolist()
+                rows = [int(seq_h[c]) for c in cu[:-1]]
+            plan = PrefillPlan(lens, x.device, rows=rows, keep=keep, cache=cache)
+        _require(x.shape[0] == plan.total, "prefill: x rows != plan tokens")
+        x = x.to(BF16).contiguous() if x.dtype != BF16 else x
+        if cache is not None:
+            full, lastp = plan.full, plan.last
+            return_kv = False
+        else:
+            full, lastp = plan.packed_plans(self.cfg.n_kv_heads * self.cfg.head_dim)
+            return_kv = True
+
+        def attend(i, r, last):
+            if return_kv:
+                q, k, v = r
+            else:
+                q = r
+                k, v = cache.k[i], cache.v[i]
+            if last and plan.bos_lengths is not None:
+                r0 = plan.rows[0]
+                return ops.decode_attention(q, k[r0:r0 + plan.n_seq], v[r0:r0 + plan.n_seq], plan.bos_lengths)
+            p = lastp if last else full
+            if return_kv:
+                return ops.varlen_attention(q, k, v, p, stride_tok=k.stride(0))
+            return ops.varlen_attention(q, k, v, p, stride_tok=k.stride(1))
+
+        return self._layers(x, pos, seq, cache, attend, return_kv, last_idx=plan.last_idx, rope_pos=rope_pos)
+
+    def decode(self, x, pos, seq, cache_seqlens, cache, rope_pos=None, tok=None):
+        """One token per sequence: x [B, d] (or tok [B] token ids with x None: the embedding is looked up in
+        the first norm kernel), pos/seq [B] int32, cache_seqlens = pos + 1 (int32).
+        Reference: viktor/fast_decoder.py:76-90."""
+        cfg, W = self.cfg, self.w
+        h = None
+        if tok is not None:
+            require_device(tok, "FastDecoder.decode")
+            x, h = ops.embed_rmsnorm(tok, W(self.dec.embed.weight), W(self.dec.layers[0].attn_norm.weight), cfg.norm_eps)
+        else:
+            require_device(x, "FastDecoder.decode")
+        ws = self.decode_workspace
+
+        def attend(i, q, last):
+            return ops.decode_attention(q, cache.k[i], cache.v[i], cache_seqlens, workspace=ws)
+
+        return self._layers(x, pos, seq, cache, attend, return_kv=False, rope_pos=rope_pos, h=h)
+
+    # ---- Decoder.forward on this path ----------------------------------------------------------
+    def forward(self, x, cache=None, batch_slice=slice(None), pos=None, positions=None):
+        require_device(x, "Decoder.forward")
+        B, T, d = x.shape
+        dev = x.device
+        xb = x.to(BF16).reshape(B * T, d).contiguous()
+        row0 = 0 if batch_slice.start is None else int(batch_slice.start)
+        if pos is not None:
+            _require(T == 1 and cache is not None, "Decoder.forward: decode mode needs T == 1 and a cache")
+            pos32 = pos.to(torch.int32).contiguous()
+            rows = torch.arange(row0, row0 + B, dtype=torch.int32, device=dev)
+            seqlens = (pos32 + 1).contiguous()
+            rp = None if positions is None else positions.reshape(B).to(torch.int32).contiguous()
+            if cache is not None and self.decode_workspace is None:
+                self.decode_workspace = ops.decode_attention_workspace(cache.k.shape[1], self.cfg.n_heads,
+                                                                       cache.k.shape[2], dev)
+            h = self.decode(xb, pos32, rows, seqlens, cache, rope_pos=rp)
+            return h.view(B, 1, d)
+        key = (B, T, row0, cache is not None)
+        plan = self._plans.get(key)
+        if plan is None:
+            rows = list(range(row0, row0 + B)) if cache is not None else None
+            plan = PrefillPlan([T] * B, dev, rows=rows, cache=cache)
+            self._plans[key] = plan
+        pos32 = torch.arange(T, dtype=torch.int32, device=dev).repeat(B)
+        seq = torch.arange(row0, row0 + B, dtype=torch.int32, device=dev).repeat_interleave(T)
+        rp = None
+        if positions is not None:
+            rp = positions.expand(B, T).reshape(B * T).to(torch.int32).contiguous()
+        h = self.prefill(xb, pos32, seq, None, T, cache, rope_pos=rp, plan=plan)
+        return h.view(B, T, d)

@@ -1,0 +1,310 @@
+"""Decoder ops on the gfx950 HIP kernels (libviktor_hip.so), with the call signatures of the reference's
+fused ops so FastDecoder / DecodeEngine code reads the same:
+
+  add_rmsnorm, embed_rmsnorm, qkv_rope_cache, linear, swiglu, greedy_update   (viktor/triton_ops.py)
+  decode_attention                                                              (viktor/decode_attention.py)
+  varlen_attention  (flash_attn_varlen_func as used at viktor/fast_decoder.py:68-73)
+  select_update     (LM head + DecodeEngine._select + step bookkeeping, viktor/engine.py:79-116)
+  gspo_score, group_advantage  (scripts/gspo.py:340-353, 446-477)
+
+Outputs are allocated with torch.empty on the input's device; documented in-place updates: x in
+add_rmsnorm, the KV cache in qkv_rope_cache, the decode state in greedy_update / select_update.
+Every launch goes to torch.cuda.current_stream(), so ops can be captured in a torch.cuda graph.
+Preconditions are checked here and raise AssertionError as the reference's asserts do; a kernel
+status other than OK raises HipLibraryError.
+"""
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import VK_DTYPE_BF16, VK_DTYPE_F32, call, ptr, require_device, stream_handle
+
+BF16 = torch.bfloat16
+
+
+def _require(cond, msg):
+    if not cond:
+        raise AssertionError(msg)
+
+
+def _contig(*ts):
+    return all(t is None or t.is_contiguous() for t in ts)
+
+
+def add_rmsnorm(x, w, eps, delta=None):
+    """x [n, d] bf16 (updated in place by += delta); returns RMSNorm(x) * w [n, d] bf16.
+    Reference: viktor/triton_ops.py:34-40."""
+    require_device(x, "add_rmsnorm")
+    _require(x.dim() == 2 and x.dtype == BF16 and w.dtype == BF16 and w.shape == (x.shape[1],), "add_rmsnorm: shapes")
+    _require(delta is None or (delta.shape == x.shape and delta.dtype == BF16), "add_rmsnorm: delta shape")
+    _require(_contig(x, w, delta), "add_rmsnorm: contiguous tensors")
+    n, d = x.shape
+    h = torch.empty_like(x)
+    call("vk_add_rmsnorm", ptr(x), ptr(delta), ptr(w), ptr(h), n, d, float(eps), stream_handle())
+    return h
+
+
+def embed_rmsnorm(tok, emb, w, eps):
+    """tok [n] int64 -> (x = emb[tok] [n, d], RMSNorm(x) * w). Reference: viktor/triton_ops.py:163-169."""
+    require_device(emb, "embed_rmsnorm")
+    _require(tok.dim() == 1 and tok.dtype == torch.long and emb.dim() == 2 and emb.dtype == BF16, "embed_rmsnorm: shapes")
+    _require(_contig(tok, emb, w), "embed_rmsnorm: contiguous tensors")
+    n, d = tok.shape[0], emb.shape[1]
+    x = torch.empty(n, d, dtype=emb.dtype, device=emb.device)
+    h = torch.empty_like(x)
+    call("vk_embed_rmsnorm", ptr(tok), ptr(emb), emb.shape[0], ptr(w), ptr(x), ptr(h), n, d, float(eps),
+         stream_handle())
+    return x, h
+
+
+def qkv_rope_cache(qkv, q_norm_w, k_norm_w, cos, sin, pos, seq, k_cache, v_cache, eps, n_heads, n_kv_heads,
+                   head_dim, return_kv=False, rope_pos=None):
+    """qkv [n, (H + 2 Hkv) D]; pos/seq [n] int32 cache position and cache row of each token; cos/sin
+    [S, D/2] (fp32 or bf16); k_cache/v_cache [B, S, Hkv, D] (one layer, may be None when return_kv).
+    rope_pos [n]: RoPE positions when they differ from pos. Returns q [n, H, D] (and packed k, v
+    [n, Hkv, D] with return_kv). Reference: viktor/triton_ops.py:94-108."""
+    require_device(qkv, "qkv_rope_cache")
+    n = qkv.shape[0]
+    _require(qkv.dtype == BF16 and qkv.shape[1] == (n_heads + 2 * n_kv_heads) * head_dim, "qkv_rope_cache: qkv shape")
+    _require(pos.dtype == torch.int32 and pos.shape == (n,), "qkv_rope_cache: pos must be int32 [n]")
+    _require(rope_pos is None or (rope_pos.dtype == torch.int32 and rope_pos.shape == (n,)), "qkv_rope_cache: rope_pos")
+    _require(cos.shape == sin.shape and cos.dim() == 2 and cos.shape[1] == head_dim // 2 and cos.dtype == sin.dtype
+             and cos.dtype in (torch.float32, BF16), "qkv_rope_cache: cos/sin tables")
+    _require(_contig(qkv, q_norm_w, k_norm_w, cos, sin, pos, rope_pos), "qkv_rope_cache: contiguous tensors")
+    if k_cache is not None:
+        _require(seq is not None and seq.dtype == torch.int32 and seq.shape == (n,), "qkv_rope_cache: seq")
+        _require(k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride() and k_cache.dim() == 4
+                 and k_cache.shape[2:] == (n_kv_heads, head_dim) and k_cache.stride(3) == 1
+                 and k_cache.stride(2) == head_dim and k_cache.dtype == BF16, "qkv_rope_cache: cache layout")
+    else:
+        _require(return_kv, "qkv_rope_cache: nowhere to write k/v")
+    q = torch.empty(n, n_heads, head_dim, dtype=qkv.dtype, device=qkv.device)
+    k = v = None
+    if return_kv:
+        k = torch.empty(n, n_kv_heads, head_dim, dtype=qkv.dtype, device=qkv.device)
+        v = torch.empty_like(k)
+    tdt = VK_DTYPE_F32 if cos.dtype == torch.float32 else VK_DTYPE_BF16
+    if k_cache is not None:
+        sb, ss, rows, clen = k_cache.stride(0), k_cache.stride(1), k_cache.shape[0], k_cache.shape[1]
+    else:
+        sb = ss = rows = clen = 0
+    call("vk_qkv_rope_cache", ptr(qkv), ptr(q_norm_w), ptr(k_norm_w), ptr(cos), ptr(sin), tdt, cos.shape[0], ptr(pos),
+         ptr(rope_pos), ptr(seq), ptr(q), ptr(k_cache), ptr(v_cache), sb, ss, rows, clen, ptr(k), ptr(v), n,
+         float(eps), n_heads, n_kv_heads, head_dim, stream_handle())
+    return (q, k, v) if return_kv else q
+
+
+def linear(x, w, swiglu=False, out_dtype=None, out=None):
+    """x [M, K] @ w[N, K]^T on bf16 MFMA. swiglu: w is gate_up [2F, K] and the result silu(gate) * up
+    [M, F]. out_dtype: torch.float32 for unrounded logits. Reference: viktor/triton_ops.py:138-146
+    (also serves the F.linear calls of the prefill path)."""
+    require_device(x, "linear")
+    _require(x.dim() == 2 and w.dim() == 2 and x.shape[1] == w.shape[1], "linear: shapes")
+    _require(x.dtype == BF16 and w.dtype == BF16, "linear: bf16 operands")
+    _require(_contig(x, w), "linear: contiguous operands")
+    M, K = x.shape
+    N = w.shape[0] // 2 if swiglu else w.shape[0]
+    _require(not swiglu or w.shape[0] % 2 == 0, "linear: swiglu needs gate_up [2F, K]")
+    odt = out_dtype or x.dtype
+    _require(odt in (BF16, torch.float32), "linear: out dtype")
+    if out is None:
+        out = torch.empty(M, N, dtype=odt, device=x.device)
+    else:
+        _require(out.shape == (M, N) and out.dtype == odt and out.is_contiguous(), "linear: out buffer")
+    call("vk_linear", ptr(x), ptr(w), ptr(out), M, N, K, int(bool(swiglu)),
+         VK_DTYPE_F32 if odt == torch.float32 else VK_DTYPE_BF16, stream_handle())
+    return out
+
+
+def swiglu(gu):
+    """gu [n, 2F] (gate | up) -> silu(gate) * up [n, F]. Reference: viktor/triton_ops.py:223-229."""
+    require_device(gu, "swiglu")
+    _require(gu.dim() == 2 and gu.shape[1] % 2 == 0 and gu.dtype == BF16 and gu.is_contiguous(), "swiglu: gu")
+    n, f2 = gu.shape
+    out = torch.empty(n, f2 // 2, dtype=gu.dtype, device=gu.device)
+    call("vk_swiglu", ptr(gu), ptr(out), n, f2 // 2, stream_handle())
+    return out
+
+
+_ws_cache = {}
+
+
+def decode_attention_workspace(B, H, max_len, device):
+    """Scratch for the key-split partials of decode_attention (None when no split is needed)."""
+    nbytes = ctypes.c_int64(0)
+    _lib.check(_lib.load().vk_decode_attention_workspace(B, H, max_len, ctypes.byref(nbytes)), "decode_attention_workspace")
+    if nbytes.value == 0:
+        return None
+    return torch.empty(nbytes.value, dtype=torch.uint8, device=device)
+
+
+def decode_attention(q, k, v, lengths, block=64, workspace=None):
+    """q [B, H, D]; k/v [B, S, Hkv, D] (one layer of the cache); lengths [B] int32, including the current
+    token, 1 <= lengths <= S. Only the valid prefix of each row is read. Returns [B, H, D] bf16.
+    workspace: preallocated key-split scratch (needed inside graph capture; allocated here otherwise).
+    Reference: viktor/decode_attention.py:41-53 (block is accepted for the signature)."""
+    require_device(q, "decode_attention")
+    B, H, D = q.shape
+    HK = k.shape[2]
+    _require(q.is_contiguous() and H % HK == 0 and H // HK <= 16 and D == 64, "decode_attention: q layout")
+    _require(q.dtype == k.dtype == v.dtype == BF16, "decode_attention: bf16 tensors")
+    _require(k.stride() == v.stride() and k.stride(-1) == 1 and k.stride(-2) == D, "decode_attention: cache layout")
+    _require(lengths.shape == (B,) and lengths.dtype == torch.int32 and lengths.is_contiguous(),
+             "decode_attention: lengths")
+    S = k.shape[1]
+    if workspace is None:
+        key = (B, H, S, q.device)
+        workspace = _ws_cache.get(key)
+        if workspace is None and key not in _ws_cache:
+            workspace = decode_attention_workspace(B, H, S, q.device)
+            _ws_cache[key] = workspace
+    out = torch.empty_like(q)
+    wsz = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    call("vk_decode_attention", ptr(q), ptr(k), ptr(v), ptr(lengths), ptr(out), B, H, HK, D, k.stride(0), k.stride(1),
+         S, ptr(workspace), wsz, stream_handle())
+    return out
+
+
+class AttentionPlan:
+    """Host-built work list of vk_varlen_attention: one (sequence, first query row) entry per 64-query
+    block, ordered by decreasing key count so the longest blocks start first. Device tensors."""
+
+    BLOCK = 64
+
+    def __init__(self, q_lens, k_lens, k_off, device, causal=True):
+        q_lens = [int(a) for a in q_lens]
+        k_lens = [int(a) for a in k_lens]
+        _require(len(q_lens) == len(k_lens) == len(k_off), "AttentionPlan: length mismatch")
+        blocks = []
+        for i, (ql, kl) in enumerate(zip(q_lens, k_lens)):
+            _require(ql >= 0 and kl >= 0 and (not causal or kl >= ql), "AttentionPlan: causal needs k_len >= q_len")
+            for qs in range(0, ql, self.BLOCK):
+                work = min(kl, kl - ql + qs + self.BLOCK) if causal else kl
+                blocks.append((work, i, qs))
+        blocks.sort(key=lambda b: -b[0])
+        cu = [0]
+        for ql in q_lens:
+            cu.append(cu[-1] + ql)
+        self.n_seq = len(q_lens)
+        self.n_blocks = len(blocks)
+        self.total_q = cu[-1]
+        self.causal = causal
+        flat = [v for _, i, qs in blocks for v in (i, qs)] or [0, 0]
+        self.plan = torch.tensor(flat, dtype=torch.int32).to(device)
+        self.cu_q = torch.tensor(cu, dtype=torch.int32).to(device)
+        self.k_lens = torch.tensor(k_lens or [0], dtype=torch.int32).to(device)
+        self.k_off = torch.tensor([int(o) for o in k_off] or [0], dtype=torch.int64).to(device)
+
+
+def varlen_attention(q, k, v, plan: AttentionPlan, stride_tok=None, out=None):
+    """Packed-query GQA attention following `plan`. q [total_q, H, D] bf16; k/v: base tensors (packed
+    [n, Hkv, D] rows or one cache layer [B, S, Hkv, D]) addressed by plan.k_off + key * stride_tok
+    elements. Returns [total_q, H, D] bf16. Reference: flash_attn_varlen_func at viktor/fast_decoder.py:68-73."""
+    require_device(q, "varlen_attention")
+    total, H, D = q.shape
+    HK = k.shape[-2]
+    _require(total == plan.total_q and q.dtype == k.dtype == v.dtype == BF16, "varlen_attention: q shape / dtype")
+    _require(q.is_contiguous() and k.stride(-1) == 1 and k.stride(-2) == D and k.stride() == v.stride(),
+             "varlen_attention: layouts")
+    if stride_tok is None:
+        stride_tok = k.stride(-3)
+    if out is None:
+        out = torch.empty_like(q)
+    call("vk_varlen_attention", ptr(q), ptr(k), ptr(v), ptr(plan.cu_q), ptr(plan.k_off), ptr(plan.k_lens),
+         ptr(plan.plan), plan.n_blocks, plan.n_seq, stride_tok, ptr(out), int(plan.causal), H, HK, D, stream_handle())
+    return out
+
+
+def select_update(bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_off, out, pos32, seqlens, rpos32, eos,
+                  pad, logits=None, h=None, w_head=None, round_bf16=False, temperature=0.0, uniforms=None,
+                  logp_out=None):
+    """One step's token choice + state update for every sequence (fused LM head when h, w_head are given).
+    See vk_select_update in include/viktor_hip.h for the exact rule order."""
+    ref = logits if logits is not None else h
+    require_device(ref, "select_update")
+    B = tok.shape[0]
+    V = bias.shape[0]
+    if logits is not None:
+        _require(logits.shape == (B, V) and logits.dtype == torch.float32 and logits.is_contiguous(), "select_update: logits")
+        d = 0
+    else:
+        _require(h.dim() == 2 and h.shape[0] == B and w_head.shape == (V, h.shape[1]) and h.dtype == BF16
+                 and w_head.dtype == BF16 and _contig(h, w_head), "select_update: h / w_head")
+        d = h.shape[1]
+    for t, dt in ((tok, torch.long), (pos, torch.long), (run, torch.long), (plen, torch.long), (rope_off, torch.long),
+                  (pos32, torch.int32), (seqlens, torch.int32), (rpos32, torch.int32)):
+        _require(t is None or (t.dtype == dt and t.shape == (B,) and t.is_contiguous()), "select_update: state tensors")
+    _require(out.dim() == 2 and out.shape[0] == B and out.dtype == torch.long and out.stride(1) == 1, "select_update: out")
+    _require(is_tail.dtype in (torch.bool, torch.uint8) and is_homo.dtype in (torch.bool, torch.uint8), "select_update: masks")
+    if temperature > 0:
+        _require(uniforms is not None and uniforms.dtype == torch.float32 and uniforms.dim() == 2
+                 and uniforms.shape[0] == B and uniforms.stride(1) == 1, "select_update: uniforms [B, T] fp32")
+    us, uc = (uniforms.stride(0), uniforms.shape[1]) if uniforms is not None else (0, 0)
+    call("vk_select_update", ptr(logits), ptr(h), ptr(w_head), d, int(bool(round_bf16)), ptr(bias), ptr(is_tail),
+         ptr(is_homo), int(homo_stop), float(temperature), ptr(uniforms), us, uc, ptr(tok), ptr(run), ptr(pos), ptr(plen),
+         ptr(rope_off), ptr(out), out.stride(0), out.shape[1], ptr(pos32), ptr(seqlens), ptr(rpos32), ptr(logp_out), B, V,
+         int(eos), int(pad), stream_handle())
+
+
+def greedy_update(logits, bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_off, out, pos32, seqlens,
+                  rpos32, eos, pad):
+    """One greedy step's bookkeeping from fp32 logits [B, V] (reference: viktor/triton_ops.py:200-209)."""
+    select_update(bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_off, out, pos32, seqlens, rpos32, eos,
+                  pad, logits=logits)
+
+
+def gspo_score(logits, targets, mask=None, old_lp=None, n_bases=None, adv=None, eps_lo=4e-4, eps_hi=4e-4, inv_n=None,
+               grad=True):
+    """Per-token log pi of the targets and, with old_lp / n_bases / adv, the GSPO sequence ratio, the
+    clipped objective and dL/dlogits.
+
+    logits [B, T, V] bf16 or fp32; targets [B, T] int64 (PAD-clamped to 0 as the reference gathers);
+    mask [B, T] bool. Returns dict(lp [B, T], and with the ratio inputs: s [B], pg [B], loss [] and
+    dlogits [B, T, V] fp32 when grad). inv_n defaults to 1 / B (loss = mean over the B sequences)."""
+    require_device(logits, "gspo_score")
+    _require(logits.dim() == 3 and logits.dtype in (BF16, torch.float32) and logits.is_contiguous(), "gspo_score: logits")
+    B, T, V = logits.shape
+    _require(targets.shape == (B, T) and targets.dtype == torch.long and targets.is_contiguous(), "gspo_score: targets")
+    dev = logits.device
+    lp = torch.empty(B, T, dtype=torch.float32, device=dev)
+    res = {"lp": lp}
+    ratio = old_lp is not None
+    s = pg = loss = dl = None
+    m8 = None
+    if ratio:
+        _require(mask is not None and adv is not None and n_bases is not None, "gspo_score: ratio needs mask, n_bases, adv")
+        _require(old_lp.shape == (B, T) and old_lp.dtype == torch.float32 and old_lp.is_contiguous(), "gspo_score: old_lp")
+        _require(mask.shape == (B, T), "gspo_score: mask")
+        _require(n_bases.shape == (B,) and adv.shape == (B,), "gspo_score: n_bases / adv")
+        m8 = mask.to(torch.uint8).contiguous()
+        n_bases = n_bases.to(torch.float32).contiguous()
+        adv = adv.to(torch.float32).contiguous()
+        s = torch.empty(B, dtype=torch.float32, device=dev)
+        pg = torch.empty_like(s)
+        loss = torch.empty((), dtype=torch.float32, device=dev)
+        if grad:
+            dl = torch.empty(B, T, V, dtype=torch.float32, device=dev)
+        res.update(s=s, pg=pg, loss=loss)
+        if grad:
+            res["dlogits"] = dl
+    inv = float(1.0 / B if inv_n is None else inv_n) if B else 0.0
+    call("vk_gspo_score", ptr(logits), VK_DTYPE_BF16 if logits.dtype == BF16 else VK_DTYPE_F32, ptr(targets), ptr(m8),
+         ptr(old_lp), ptr(n_bases), ptr(adv), float(eps_lo), float(eps_hi), inv, ptr(lp), ptr(s), ptr(pg), ptr(loss),
+         ptr(dl), B, T, V, stream_handle())
+    return res
+
+
+def group_advantage(reward, std_floor=None, eps=None):
+    """Group-normalised advantages of reward [G, n] fp32: (r - mean) / max(std, std_floor) (the reference's
+    rule, scripts/gspo.py:447-450) or (r - mean) / (std + eps). Returns (adv [G, n], live [G] bool)."""
+    require_device(reward, "group_advantage")
+    _require((std_floor is None) != (eps is None), "group_advantage: give std_floor or eps")
+    r = reward.to(torch.float32).contiguous()
+    G, n = r.shape
+    adv = torch.empty_like(r)
+    live = torch.empty(G, dtype=torch.uint8, device=r.device)
+    mode, param = (0, std_floor) if std_floor is not None else (1, eps)
+    call("vk_group_advantage", ptr(r), G, n, mode, float(param), ptr(adv), ptr(live), stream_handle())
+    return adv, live.bool()

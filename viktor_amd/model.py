@@ -1,0 +1,104 @@
+"""Basecaller subset on the rollout-and-scoring path: per-frame projector + decoder-only LM + tokenizer.
+
+Reference: viktor/model.py:27-131. The encoder (frames producer) is outside this package: a Basecaller
+takes encoder frames [B, P, d_enc] directly; `encoder` may be None (then `d_enc` gives the frame width).
+Teacher-forced logits run on the HIP kernels: every window is packed as [its plens[b] frames | tokens]
+(the causal decoder never reads the padding the reference appends after them), the decoder runs over the
+packed tokens with its last layer kept for the token rows only, and the LM head gives bf16 logits.
+"""
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from ._lib import require_device
+from .decoder import Decoder, DecoderConfig
+from .fast_decoder import PrefillPlan
+from .tokenizer import PAD, KmerTokenizer, get_tokenizer
+
+BF16 = torch.bfloat16
+
+
+class Basecaller(nn.Module):
+    def __init__(self, encoder, tokenizer: KmerTokenizer, cfg: Optional[DecoderConfig] = None, d_enc: int = 512):
+        super().__init__()
+        self.encoder = encoder
+        self.tokenizer = tokenizer
+        self.cfg = cfg or DecoderConfig(vocab_size=tokenizer.vocab_size)
+        d = self.cfg.d_model
+        self.d_enc = getattr(encoder, "d_model", d_enc) if encoder is not None else d_enc
+        # one prefix token per encoder frame (reference: viktor/model.py:34-35)
+        self.projector = nn.Sequential(nn.Linear(self.d_enc, d), nn.GELU(), nn.Linear(d, d))
+        self.decoder = Decoder(self.cfg)
+        # RoPE position of prefix frame j = j * pos_scale; tokens follow at pos_scale * (real frames) + i
+        self.pos_scale = 1
+
+    @classmethod
+    def from_args(cls, encoder, args: dict, d_enc: int = 512):
+        """The model of a training run's args: tokenizer and decoder depth (reference: viktor/model.py:42-48)."""
+        tok = get_tokenizer(args.get("tokenizer", "base"))
+        m = cls(encoder, tok, DecoderConfig(vocab_size=tok.vocab_size, n_layers=args.get("layers", 8)), d_enc=d_enc)
+        m.pos_scale = args.get("prefix_pos_scale", 1)
+        return m
+
+    def project(self, frames):
+        """Projector in bf16 (autocast for fp32 weights, as the reference's training path runs it)."""
+        with torch.autocast("cuda", dtype=BF16, enabled=self.projector[0].weight.dtype != BF16):
+            return self.projector(frames.to(self.projector[0].weight.dtype)).to(BF16)
+
+    def rope_positions(self, x, P, plens=None):
+        """[B, P + T] RoPE positions of a [frames | tokens] window (None at pos_scale 1: the sequence index).
+        Reference: viktor/model.py:62-69."""
+        if self.pos_scale == 1:
+            return None
+        B, L = x.shape[:2]
+        pos = torch.arange(L, device=x.device).expand(B, -1)
+        n = torch.full((B, 1), P, device=x.device) if plens is None else plens[:, None]
+        return torch.where(pos < n, pos * self.pos_scale, pos + (self.pos_scale - 1) * n)
+
+    def logits(self, frames, tokens_in, plens=None):
+        """Teacher forcing from encoder frames [B, P, d_enc]: bf16 logits [B, T, vocab] of every token
+        position. plens [B]: real prefix frames per window (default P). Reference: viktor/model.py:55-60."""
+        require_device(frames, "Basecaller.logits")
+        B, P = frames.shape[:2]
+        T = tokens_in.shape[1]
+        dev = frames.device
+        plens_h = [P] * B if plens is None else [int(p) for p in plens.tolist()]
+        assert all(0 < p <= P for p in plens_h), "plens outside 1..P"
+        prefix = self.project(frames)                                       # [B, P, d] bf16
+        fast = self.decoder.fast()
+        emb = fast.w(self.decoder.embed.weight)[tokens_in.to(dev)]          # [B, T, d] bf16
+        seq_lens = [p + T for p in plens_h]
+        plan = PrefillPlan(seq_lens, dev, keep=[T] * B)
+        # packed rows: window b = [prefix[b, :plens[b]] | emb[b]]
+        pl = torch.tensor(plens_h, device=dev)
+        cu = torch.tensor(plan.cu[:-1], device=dev)
+        frame_rows = torch.repeat_interleave(torch.arange(B, device=dev), pl)
+        frame_pos = torch.arange(int(pl.sum()), device=dev) - torch.repeat_interleave(
+            torch.cumsum(pl, 0) - pl, pl)
+        x = torch.empty(plan.total, prefix.shape[-1], dtype=BF16, device=dev)
+        x[cu[frame_rows] + frame_pos] = prefix[frame_rows, frame_pos]
+        tok_dst = (cu + pl)[:, None] + torch.arange(T, device=dev)[None, :]
+        x[tok_dst.reshape(-1)] = emb.reshape(B * T, -1)
+        pos = torch.cat([torch.arange(n, dtype=torch.int32, device=dev) for n in seq_lens])
+        rpos = None
+        if self.pos_scale != 1:
+            s = self.pos_scale
+            rpos = torch.cat([torch.cat([torch.arange(p, device=dev) * s, s * p + torch.arange(T, device=dev)])
+                              for p in plens_h]).to(torch.int32)
+        h = fast.prefill(x, pos, None, None, plan.max_len, None, rope_pos=rpos, plan=plan)  # [B * T, d]
+        return self.decoder.head(h).view(B, T, -1)
+
+    def batch(self, seqs, weights=None, pad_to=1):
+        """CPU teacher-forcing tensors: tokens_in, targets [B, T] and target weights (targets != PAD), T
+        padded up to a multiple of pad_to. Reference: viktor/model.py:119-131 (per-base weights and
+        alignment centres belong to SFT and are not part of this path)."""
+        if weights is not None:
+            raise NotImplementedError("per-base target weights are an SFT feature outside the rollout/scoring path")
+        tokens_in, targets, _ = self.tokenizer.batch(seqs)
+        T = -(-targets.shape[1] // pad_to) * pad_to
+        tokens_in = F.pad(tokens_in, (0, T - tokens_in.shape[1]), value=PAD)
+        targets = F.pad(targets, (0, T - targets.shape[1]), value=PAD)
+        return tokens_in, targets, (targets != PAD).float()
