@@ -137,17 +137,50 @@ int vk_varlen_attention(const void *q, const void *k, const void *v, const int32
  *   out[b * out_stride + col] = nxt with col = pos[b] - plen[b]; tok[b] = nxt; pos[b] += 1;
  *   pos32 = pos, seqlens = pos + 1, rpos32 = pos + rope_off (each optional, NULL to skip).
  * Logits come either from `logits` [B, V] fp32 (h and w_head NULL), or are computed here as
- * h[B, d] @ w_head[V, d]^T (bf16 inputs, fp32 accumulation), the fused LM head.
+ * h[B, d] @ w_head[V, d]^T (bf16 inputs, fp32 accumulation), the fused LM head; with norm_w non-NULL, h is
+ * the residual stream and the final RMSNorm (weight norm_w, eps) is applied to it first (rounded to bf16).
  * logp_out (optional): log softmax(z / T or z)[nxt] of the chosen token before the grammar rules.
  * Replaces greedy_update (viktor/triton_ops.py:172-209), DecodeEngine._select (viktor/engine.py:79-89)
  * and the head + index_copy bookkeeping of DecodeEngine._step (viktor/engine.py:91-116).
  */
-int vk_select_update(const float *logits, const void *h, const void *w_head, int32_t d, int32_t round_bf16,
+int vk_select_update(const float *logits, const void *h, const void *norm_w, float eps, const void *w_head,
+                     int32_t d, int32_t round_bf16,
                      const float *bias, const uint8_t *is_tail, const uint8_t *is_homo, int32_t homo_stop,
                      float temperature, const float *uniforms, int64_t u_stride, int64_t u_cols, int64_t *tok,
                      int64_t *run, int64_t *pos, const int64_t *plen, const int64_t *rope_off, int64_t *out,
                      int64_t out_stride, int64_t out_cols, int32_t *pos32, int32_t *seqlens, int32_t *rpos32,
                      float *logp_out, int64_t B, int32_t V, int32_t eos, int32_t pad, void *stream);
+
+/*
+ * Decode-step fusions (small M: one row per sequence). Same rounding points as the unfused ops.
+ *
+ * vk_norm_qkv_rope_cache: h = RMSNorm(x) * norm_w (x [M, K] bf16; or, with tok non-NULL, x = emb[tok] with
+ * emb = the `x` argument [vocab, K], and the gathered rows are also stored to x_store), then
+ * qkv = bf16(h @ w_qkv^T) and the vk_qkv_rope_cache transform of qkv: q -> q [M, H, 64], k / v -> caches.
+ * Replaces embed_rmsnorm / add_rmsnorm + linear + qkv_rope_cache (viktor/triton_ops.py:17-108, 149-169;
+ * viktor/fast_decoder.py:41-46, 76-90).
+ */
+int vk_norm_qkv_rope_cache(const void *x, const int64_t *tok, int64_t vocab, void *x_store, const void *norm_w,
+                           float eps, const void *w_qkv, const void *q_norm_w, const void *k_norm_w, const void *cos_t,
+                           const void *sin_t, int32_t table_dtype, int64_t table_rows, const int32_t *pos,
+                           const int32_t *rope_pos, const int32_t *seq, void *q, void *k_cache, void *v_cache,
+                           int64_t stride_cb, int64_t stride_cs, int64_t cache_rows, int64_t cache_len, int64_t M,
+                           int32_t K, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void *stream);
+
+/*
+ * vk_linear_residual: x[M, N] = bf16(x + bf16(a[M, K] @ w[N, K]^T)) in place (the o / down projections
+ * followed by the residual add of add_rmsnorm, viktor/triton_ops.py:24-27, viktor/fast_decoder.py:51-57).
+ */
+int vk_linear_residual(const void *a, const void *w, void *x, int64_t M, int32_t N, int32_t K, void *stream);
+
+/*
+ * vk_norm_linear: y = act(bf16(RMSNorm(x) * norm_w) @ w^T) (norm_w may be NULL: no norm), act = SwiGLU over
+ * w = [gate; up] when swiglu != 0 (bf16 out), else identity (bf16 or fp32 out). The mlp norm + gate_up +
+ * SwiGLU of a decode step (viktor/triton_ops.py:17-40, 111-146).
+ * The three entry points above take K in {256, 512, 1024, 1536} and N % 4 == 0.
+ */
+int vk_norm_linear(const void *x, const void *norm_w, float eps, const void *w, void *y, int64_t M, int32_t N,
+                   int32_t K, int32_t swiglu, int32_t out_dtype, void *stream);
 
 /*
  * GSPO scoring of B sequences of T target tokens (scripts/gspo.py:340-353 and 459-477):

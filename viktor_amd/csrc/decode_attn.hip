@@ -96,20 +96,40 @@ __global__ __launch_bounds__(DA_WAVES * 64) void decode_attn_kernel(
   const bf16_t *vb = vc + b * stride_b;
   bf16_t *vs = Vs[wid];
 
-  for (int t = t_begin + wid; t < t_end; t += DA_WAVES) {
-    const int64_t p0 = static_cast<int64_t>(t) * DA_TILE;
-    u32x4 kf[2][4], vf[2][4];
+  // Software pipeline: the next tile's K loads are issued as soon as the score MFMAs have consumed the
+  // current K fragments, and its V loads as soon as the current V tile sits in LDS, so every wave keeps
+  // 16 KB of loads in flight through the softmax and PV phases without extra registers.
+  u32x4 kf[2][4], vf[2][4];
+  auto row_ptr = [&](const bf16_t *base, int tt, int pb) {
+    int64_t p = static_cast<int64_t>(tt) * DA_TILE + 16 * pb + qrow;
+    p = p < len ? p : len - 1;  // rows past the length: any valid row, masked below
+    return base + p * stride_s + g * 8;
+  };
+  auto load_k = [&](int tt) {
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb) {
-      int64_t p = p0 + 16 * pb + qrow;
-      p = p < len ? p : len - 1;  // rows past the length: any valid row, masked below
-      const bf16_t *kr = kb + p * stride_s + g * 8;
-      const bf16_t *vr = vb + p * stride_s + g * 8;
+      const bf16_t *r = row_ptr(kb, tt, pb);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) kf[pb][c] = *reinterpret_cast<const u32x4 *>(kr + 32 * c);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) vf[pb][c] = *reinterpret_cast<const u32x4 *>(vr + 32 * c);
+      for (int c = 0; c < 4; ++c) kf[pb][c] = *reinterpret_cast<const u32x4 *>(r + 32 * c);
     }
+  };
+  auto load_v = [&](int tt) {
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb) {
+      const bf16_t *r = row_ptr(vb, tt, pb);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) vf[pb][c] = *reinterpret_cast<const u32x4 *>(r + 32 * c);
+    }
+  };
+  // prefetches are unconditional (a wave past its last tile re-reads the current one, an L2 hit) so the
+  // compiler can count the outstanding loads across the loop back edge instead of draining them all
+  const int t_first = min(t_begin + wid, t_end - 1);
+  load_k(t_first);
+  asm volatile("" ::: "memory");  // keep K before V: the loop waits for K with the V loads still in flight
+  load_v(t_first);
+  for (int t = t_begin + wid; t < t_end; t += DA_WAVES) {
+    const int64_t p0 = static_cast<int64_t>(t) * DA_TILE;
+    const int tn = t + DA_WAVES < t_end ? t + DA_WAVES : t;
     // scores S^T[pos][qrow]
     f32x4 st[2];
 #pragma unroll
@@ -119,6 +139,7 @@ __global__ __launch_bounds__(DA_WAVES * 64) void decode_attn_kernel(
       for (int c = 0; c < 4; ++c)
         st[pb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[pb][c]), bq[c], st[pb], 0, 0, 0);
     }
+    load_k(tn);
     // online softmax over this tile (lane holds positions p0 + 16 pb + 4 g + i)
     float sv[8];
     float mx = -INFINITY;
@@ -155,6 +176,7 @@ __global__ __launch_bounds__(DA_WAVES * 64) void decode_attn_kernel(
       for (int c = 0; c < 4; ++c)
         *reinterpret_cast<u32x4 *>(&vs[(16 * pb + qrow) * DA_PITCH + 32 * c + g * 8]) = vf[pb][c];
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    load_v(tn);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       bf16x8 va;

@@ -21,8 +21,8 @@ constexpr int SEL_THREADS = 256;
 constexpr int SEL_MAXV = 512;
 
 __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
-    const float *__restrict__ logits, const bf16_t *__restrict__ h, const bf16_t *__restrict__ w_head, int d,
-    int round_bf16, const float *__restrict__ bias, const uint8_t *__restrict__ is_tail,
+    const float *__restrict__ logits, const bf16_t *__restrict__ h, const bf16_t *__restrict__ norm_w, float eps,
+    const bf16_t *__restrict__ w_head, int d, int round_bf16, const float *__restrict__ bias, const uint8_t *__restrict__ is_tail,
     const uint8_t *__restrict__ is_homo, int homo_stop, float temperature, const float *__restrict__ uniforms,
     int64_t u_stride, int64_t u_cols, int64_t *__restrict__ tok, int64_t *__restrict__ run, int64_t *__restrict__ pos,
     const int64_t *__restrict__ plen, const int64_t *__restrict__ rope_off, int64_t *__restrict__ out,
@@ -38,15 +38,51 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
   if (logits != nullptr) {
     for (int v = tid; v < V; v += SEL_THREADS) z[v] = logits[b * V + v] + bias[v];
   } else {
+    // this lane's slice of the hidden row (chunks of 8 at lane * 8 + 512 c), RMSNorm'ed when norm_w is given
+    constexpr int MAXC = 4;
     const bf16_t *hr = h + b * d;
+    float hv[MAXC][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      const int k = lane * 8 + 512 * c;
+      if (k < d) {
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(hr + k);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          hv[c][2 * j] = lo_bf(v[j]);
+          hv[c][2 * j + 1] = hi_bf(v[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss += hv[c][j] * hv[c][j];
+      }
+    }
+    if (norm_w != nullptr) {
+      const float r = rsqrtf(wave_sum(ss) / static_cast<float>(d) + eps);
+#pragma unroll
+      for (int c = 0; c < MAXC; ++c) {
+        const int k = lane * 8 + 512 * c;
+        if (k < d) {
+          const u32x4 wv = *reinterpret_cast<const u32x4 *>(norm_w + k);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            hv[c][2 * j] = round_bf(hv[c][2 * j] * r * lo_bf(wv[j]));
+            hv[c][2 * j + 1] = round_bf(hv[c][2 * j + 1] * r * hi_bf(wv[j]));
+          }
+        }
+      }
+    }
     for (int v = wid; v < V; v += SEL_THREADS / 64) {
       const bf16_t *wr = w_head + static_cast<int64_t>(v) * d;
       float acc = 0.f;
-      for (int c = lane * 8; c < d; c += 64 * 8) {
-        const u32x4 hv = *reinterpret_cast<const u32x4 *>(hr + c);
-        const u32x4 wv = *reinterpret_cast<const u32x4 *>(wr + c);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc += lo_bf(hv[j]) * lo_bf(wv[j]) + hi_bf(hv[j]) * hi_bf(wv[j]);
+      for (int c = 0; c < MAXC; ++c) {
+        const int k = lane * 8 + 512 * c;
+        if (k < d) {
+          const u32x4 wv = *reinterpret_cast<const u32x4 *>(wr + k);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc += hv[c][2 * j] * lo_bf(wv[j]) + hv[c][2 * j + 1] * hi_bf(wv[j]);
+        }
       }
       acc = wave_sum(acc);
       if (lane == 0) z[v] = (round_bf16 ? round_bf(acc) : acc) + bias[v];
@@ -142,7 +178,8 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
 
 using namespace vk;
 
-extern "C" int vk_select_update(const float *logits, const void *h, const void *w_head, int32_t d, int32_t round_bf16,
+extern "C" int vk_select_update(const float *logits, const void *h, const void *norm_w, float eps, const void *w_head,
+                                int32_t d, int32_t round_bf16,
                                 const float *bias, const uint8_t *is_tail, const uint8_t *is_homo, int32_t homo_stop,
                                 float temperature, const float *uniforms, int64_t u_stride, int64_t u_cols,
                                 int64_t *tok, int64_t *run, int64_t *pos, const int64_t *plen, const int64_t *rope_off,
@@ -154,14 +191,16 @@ extern "C" int vk_select_update(const float *logits, const void *h, const void *
   VK_CHECK_ARG(B >= 0 && B < (int64_t(1) << 31), "select_update: bad batch");
   VK_CHECK_ARG((logits != nullptr) != (h != nullptr && w_head != nullptr),
                "select_update: pass either logits or (h, w_head)");
-  VK_CHECK_ARG(logits != nullptr || (d > 0 && d % 8 == 0 && vk_aligned16(h) && vk_aligned16(w_head)),
-               "select_update: LM head needs d %% 8 == 0 and 16-byte aligned h, w_head");
+  VK_CHECK_ARG(logits != nullptr || (d > 0 && d % 8 == 0 && d <= 2048 && vk_aligned16(h) && vk_aligned16(w_head) &&
+                                      (!norm_w || vk_aligned16(norm_w))),
+               "select_update: LM head needs d %% 8 == 0, d <= 2048 and 16-byte aligned h, w_head, norm_w");
   VK_CHECK_ARG(homo_stop <= 0 || run != nullptr, "select_update: homopolymer rule needs run");
   VK_CHECK_ARG(!(temperature > 0.f) || (uniforms != nullptr && u_cols > 0), "select_update: sampling needs uniforms");
   VK_CHECK_ARG(out_cols > 0, "select_update: empty output buffer");
   if (B == 0) return VK_OK;
   select_update_kernel<<<static_cast<unsigned>(B), SEL_THREADS, 0, VK_STREAM(stream)>>>(
-      logits, static_cast<const bf16_t *>(h), static_cast<const bf16_t *>(w_head), d, round_bf16, bias, is_tail,
+      logits, static_cast<const bf16_t *>(h), static_cast<const bf16_t *>(norm_w), eps,
+      static_cast<const bf16_t *>(w_head), d, round_bf16, bias, is_tail,
       is_homo, homo_stop, temperature, uniforms, u_stride, u_cols, tok, run, pos, plen, rope_off, out, out_stride,
       out_cols, pos32, seqlens, rpos32, logp_out, V, eos, pad);
   return launch_status("select_update");

@@ -1,0 +1,431 @@
+// Small-M GEMMs of a decode step (one row per sequence, M = batch) with the surrounding elementwise
+// work fused in, so a decoder layer is five launches:
+//   norm_qkv_rope   rmsnorm(x) (or embedding gather + rmsnorm) -> x Wqkv^T -> QK-norm + RoPE -> q out,
+//                   k / v written to the KV cache                     (add_rmsnorm + linear + qkv_rope_cache)
+//   linear_residual x += bf16(a W^T)                                  (o / down projection + residual add)
+//   norm_linear     act(rmsnorm(x) W^T), act = SwiGLU / none           (mlp norm + gate_up + SwiGLU)
+// Rounding points are those of the unfused reference path (viktor/triton_ops.py, viktor/fast_decoder.py:
+// 33-60): the normalised activations, the GEMM outputs, the residual sum, and each QK-norm / RoPE step
+// are rounded to bf16 exactly where the unfused ops store bf16.
+//
+// MI355X design: a workgroup owns a 32 x BN output tile and its WAVES wavefronts split K (each a
+// contiguous K slice), so a launch has (N / BN) x (M / 32) workgroups of short dependency chains:
+// every wave issues all its A and B fragment loads (16-byte, straight from global / L2 into MFMA
+// registers) before its first v_mfma_f32_16x16x32_bf16; partial tiles are summed through LDS in a
+// fixed wave order (deterministic), and the epilogue runs on the summed tile with 8 lanes per row.
+#include <math.h>
+
+#include "common.h"
+
+namespace vk {
+
+enum Prologue { PRO_NONE = 0, PRO_NORM = 1, PRO_EMBED_NORM = 2 };
+enum Epilogue { EPI_BF16 = 0, EPI_F32 = 1, EPI_SWIGLU = 2, EPI_RESID = 3, EPI_ROPE = 4 };
+
+struct SkinnyArgs {
+  const bf16_t *a;       // A [M, K]; PRO_EMBED_NORM: the embedding table [vocab, K]
+  const int64_t *tok;    // PRO_EMBED_NORM: token ids [M]
+  int64_t vocab;
+  const bf16_t *norm_w;  // PRO_NORM / PRO_EMBED_NORM: RMSNorm weight [K]
+  float eps;
+  bf16_t *x_store;       // PRO_EMBED_NORM: gathered rows are stored here (the residual stream) [M, K]
+  const bf16_t *w;       // weights [N, K] ([2N, K] gate | up for EPI_SWIGLU)
+  void *y;               // output [M, N] (EPI_RESID: the residual, updated in place)
+  int64_t M;
+  int N, K;
+  // EPI_ROPE: heads of 64 columns: q heads 0..H-1, k heads, v heads
+  const bf16_t *qw, *kw;
+  const void *cos_t, *sin_t;
+  int table_f32;
+  int64_t table_rows;
+  const int32_t *pos, *rope_pos, *seq;
+  bf16_t *kc, *vc;
+  int64_t stride_cb, stride_cs, cache_rows, cache_len;
+  int H, HKV;
+};
+
+constexpr int SK_BM = 32;
+
+template <int BN, int WAVES, int KSTEPS, int PRO, int EPI>
+__global__ __launch_bounds__(WAVES * 64) void skinny_gemm_kernel(const SkinnyArgs p) {
+  constexpr bool SWI = EPI == EPI_SWIGLU;
+  constexpr int NT = BN / 16;          // n tiles of one operand group
+  constexpr int NB = SWI ? 2 * BN : BN;  // output columns accumulated (gate + up for SwiGLU)
+  constexpr int NTT = NB / 16;
+  __shared__ float part[WAVES][SK_BM][NB + 1];
+  __shared__ float ssq[WAVES][SK_BM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * SK_BM;
+  const int n0 = blockIdx.x * BN;
+  const int K = p.K;
+  const int kb = wid * KSTEPS * 32;  // this wave's K slice
+  const int fr = lane & 15, fk = (lane >> 4) * 8;
+
+  // ---- A fragments (2 m-tiles x KSTEPS) ----
+  u32x4 af[KSTEPS][2];
+  const bf16_t *arow[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    int64_t row = m0 + 16 * i + fr;
+    row = row < p.M ? row : p.M - 1;
+    if (PRO == PRO_EMBED_NORM) {
+      int64_t t = p.tok[row];
+      t = (t < 0 || t >= p.vocab) ? 0 : t;
+      arow[i] = p.a + t * K;
+    } else {
+      arow[i] = p.a + row * K;
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) af[s][i] = *reinterpret_cast<const u32x4 *>(arow[i] + kb + 32 * s + fk);
+
+  // ---- B fragments ----
+  u32x4 bfr[KSTEPS][NTT];
+#pragma unroll
+  for (int j = 0; j < NTT; ++j) {
+    int col = n0 + 16 * (j % NT) + fr;
+    col = col < p.N ? col : p.N - 1;
+    const int wrow = (SWI && j >= NT) ? col + p.N : col;
+    const bf16_t *src = p.w + static_cast<int64_t>(wrow) * K + kb + fk;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) bfr[s][j] = *reinterpret_cast<const u32x4 *>(src + 32 * s);
+  }
+
+  // ---- prologue: RMSNorm of the A rows over the full K (sum of squares across lanes and waves) ----
+  if constexpr (PRO != PRO_NONE) {
+    float ss[2] = {0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = lo_bf(af[s][i][e]), hi = hi_bf(af[s][i][e]);
+          ss[i] += lo * lo + hi * hi;
+        }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      ss[i] += __shfl_xor(ss[i], 16, 64);
+      ss[i] += __shfl_xor(ss[i], 32, 64);
+    }
+    if (lane < 16) {
+      ssq[wid][fr] = ss[0];
+      ssq[wid][16 + fr] = ss[1];
+    }
+    if (PRO == PRO_EMBED_NORM && blockIdx.x == 0) {
+      // the gathered rows become the residual stream
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int64_t row = m0 + 16 * i + fr;
+        if (row < p.M) {
+#pragma unroll
+          for (int s = 0; s < KSTEPS; ++s)
+            *reinterpret_cast<u32x4 *>(p.x_store + row * K + kb + 32 * s + fk) = af[s][i];
+        }
+      }
+    }
+    __syncthreads();
+    float r[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) t += ssq[w][16 * i + fr];
+      r[i] = rsqrtf(t / static_cast<float>(K) + p.eps);
+    }
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      const u32x4 wv = *reinterpret_cast<const u32x4 *>(p.norm_w + kb + 32 * s + fk);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          af[s][i][e] = pack_bf(lo_bf(af[s][i][e]) * r[i] * lo_bf(wv[e]), hi_bf(af[s][i][e]) * r[i] * hi_bf(wv[e]));
+    }
+  }
+
+  // ---- MFMA over this wave's K slice ----
+  f32x4 acc[2][NTT];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NTT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < NTT; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[s][i]),
+                                                            __builtin_bit_cast(bf16x8, bfr[s][j]), acc[i][j], 0, 0, 0);
+
+  // ---- split-K reduction through LDS ----
+  {
+    const int oc = lane & 15, orow = (lane >> 4) * 4;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < NTT; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part[wid][16 * i + orow + e][16 * j + oc] = acc[i][j][e];
+  }
+  __syncthreads();
+
+  // ---- epilogue: thread -> (row, 8-lane group); columns {4s..4s+3} (+ {32+4s..} when BN = 64) ----
+  constexpr int TPR = 8;  // threads per row
+  for (int base = 0; base < SK_BM * TPR; base += WAVES * 64) {
+    const int t = base + tid;
+    if (t >= SK_BM * TPR) break;
+    const int rr = t / TPR, sub = t % TPR;
+    const int64_t row = m0 + rr;
+    const bool row_ok = row < p.M;
+    constexpr int HALVES = BN == 64 ? 2 : 1;
+    float v[HALVES][4];
+    float vu[HALVES][4];
+#pragma unroll
+    for (int hf = 0; hf < HALVES; ++hf)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int col = 32 * hf + 4 * sub + c;
+        float sacc = 0.f, uacc = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+          sacc += part[w][rr][col];
+          if (SWI) uacc += part[w][rr][BN + col];
+        }
+        v[hf][c] = sacc;
+        vu[hf][c] = uacc;
+      }
+    if constexpr (EPI == EPI_ROPE) {
+      static_assert(BN == 64, "rope epilogue works on whole 64-column heads");
+      const int hd = n0 / 64;
+      const int H = p.H, HKV = p.HKV;
+      float x1[4], x2[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        x1[c] = round_bf(v[0][c]);
+        x2[c] = round_bf(v[1][c]);
+      }
+      if (hd < H + HKV) {
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ss += x1[c] * x1[c] + x2[c] * x2[c];
+        ss += __shfl_xor(ss, 1, 64);
+        ss += __shfl_xor(ss, 2, 64);
+        ss += __shfl_xor(ss, 4, 64);
+        const float r = rsqrtf(ss / 64.f + p.eps);
+        const bf16_t *wn = hd < H ? p.qw : p.kw;
+        int64_t rp = 0;
+        if (row_ok) rp = p.rope_pos ? p.rope_pos[row] : p.pos[row];
+        rp = rp < 0 ? 0 : (rp >= p.table_rows ? p.table_rows - 1 : rp);
+        uint32_t o1[2], o2[2];
+#pragma unroll
+        for (int c = 0; c < 4; c += 2) {
+          float a1[2], a2[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int j = 4 * sub + c + e;
+            const float y1 = round_bf(x1[c + e] * r * bf2f(wn[j]));
+            const float y2 = round_bf(x2[c + e] * r * bf2f(wn[32 + j]));
+            float cs, sn;
+            if (p.table_f32) {
+              cs = static_cast<const float *>(p.cos_t)[rp * 32 + j];
+              sn = static_cast<const float *>(p.sin_t)[rp * 32 + j];
+            } else {
+              cs = bf2f(static_cast<const bf16_t *>(p.cos_t)[rp * 32 + j]);
+              sn = bf2f(static_cast<const bf16_t *>(p.sin_t)[rp * 32 + j]);
+            }
+            a1[e] = y1 * cs - y2 * sn;
+            a2[e] = y1 * sn + y2 * cs;
+          }
+          o1[c / 2] = pack_bf(a1[0], a1[1]);
+          o2[c / 2] = pack_bf(a2[0], a2[1]);
+        }
+        if (row_ok) {
+          if (hd < H) {
+            bf16_t *dst = static_cast<bf16_t *>(p.y) + (row * H + hd) * 64 + 4 * sub;
+            *reinterpret_cast<u32x2 *>(dst) = u32x2{o1[0], o1[1]};
+            *reinterpret_cast<u32x2 *>(dst + 32) = u32x2{o2[0], o2[1]};
+          } else {
+            const int64_t sq = p.seq[row], ps = p.pos[row];
+            if (sq >= 0 && sq < p.cache_rows && ps >= 0 && ps < p.cache_len) {
+              bf16_t *dst = p.kc + sq * p.stride_cb + ps * p.stride_cs + (hd - H) * 64 + 4 * sub;
+              *reinterpret_cast<u32x2 *>(dst) = u32x2{o1[0], o1[1]};
+              *reinterpret_cast<u32x2 *>(dst + 32) = u32x2{o2[0], o2[1]};
+            }
+          }
+        }
+      } else if (row_ok) {  // v head: the rounded projection goes to the cache unchanged
+        const int64_t sq = p.seq[row], ps = p.pos[row];
+        if (sq >= 0 && sq < p.cache_rows && ps >= 0 && ps < p.cache_len) {
+          bf16_t *dst = p.vc + sq * p.stride_cb + ps * p.stride_cs + (hd - H - HKV) * 64 + 4 * sub;
+          *reinterpret_cast<u32x2 *>(dst) = u32x2{pack_bf(x1[0], x1[1]), pack_bf(x1[2], x1[3])};
+          *reinterpret_cast<u32x2 *>(dst + 32) = u32x2{pack_bf(x2[0], x2[1]), pack_bf(x2[2], x2[3])};
+        }
+      }
+      continue;
+    }
+    if (!row_ok) continue;
+#pragma unroll
+    for (int hf = 0; hf < HALVES; ++hf) {
+      const int col = n0 + 32 * hf + 4 * sub;
+      if (col >= p.N) continue;  // N is a multiple of 4 (checked on the host)
+      const int64_t off = row * p.N + col;
+      if (EPI == EPI_F32) {
+        float *dst = static_cast<float *>(p.y) + off;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) dst[c] = v[hf][c];
+      } else {
+        float o[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          float val = v[hf][c];
+          if (EPI == EPI_SWIGLU) {
+            const float g = round_bf(val);
+            const float u = round_bf(vu[hf][c]);
+            val = round_bf(g / (1.0f + __expf(-g))) * u;
+          }
+          o[c] = val;
+        }
+        bf16_t *dst = static_cast<bf16_t *>(p.y) + off;
+        if (EPI == EPI_RESID) {
+          const u32x2 old = *reinterpret_cast<const u32x2 *>(dst);
+          o[0] = lo_bf(old[0]) + round_bf(o[0]);
+          o[1] = hi_bf(old[0]) + round_bf(o[1]);
+          o[2] = lo_bf(old[1]) + round_bf(o[2]);
+          o[3] = hi_bf(old[1]) + round_bf(o[3]);
+        }
+        *reinterpret_cast<u32x2 *>(dst) = u32x2{pack_bf(o[0], o[1]), pack_bf(o[2], o[3])};
+      }
+    }
+  }
+}
+
+template <int BN, int WAVES, int KSTEPS, int PRO, int EPI>
+static void launch_skinny(const SkinnyArgs &a, hipStream_t s) {
+  const dim3 grid((a.N + BN - 1) / BN, static_cast<unsigned>((a.M + SK_BM - 1) / SK_BM));
+  skinny_gemm_kernel<BN, WAVES, KSTEPS, PRO, EPI><<<grid, WAVES * 64, 0, s>>>(a);
+}
+
+// K = 512 (d_model) with 4 waves of 4 k-steps, K = 1536 (ffn) with 8 waves of 6 k-steps
+template <int BN, int PRO, int EPI>
+static int dispatch_k(const SkinnyArgs &a, hipStream_t s) {
+  if (a.K == 512) {
+    launch_skinny<BN, 4, 4, PRO, EPI>(a, s);
+  } else if (a.K == 1536) {
+    launch_skinny<BN, 8, 6, PRO, EPI>(a, s);
+  } else if (a.K == 256) {
+    launch_skinny<BN, 4, 2, PRO, EPI>(a, s);
+  } else if (a.K == 1024) {
+    launch_skinny<BN, 8, 4, PRO, EPI>(a, s);
+  } else {
+    return fail(VK_ERR_UNSUPPORTED, "skinny linear: K must be 256, 512, 1024 or 1536 (got %d)", a.K);
+  }
+  return VK_OK;
+}
+
+static SkinnyArgs base_args(const void *a, const void *w, void *y, int64_t M, int N, int K) {
+  SkinnyArgs p{};
+  p.a = static_cast<const bf16_t *>(a);
+  p.w = static_cast<const bf16_t *>(w);
+  p.y = y;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  return p;
+}
+
+}  // namespace vk
+
+using namespace vk;
+
+extern "C" int vk_norm_linear(const void *x, const void *norm_w, float eps, const void *w, void *y, int64_t M, int32_t N,
+                              int32_t K, int32_t swiglu, int32_t out_dtype, void *stream) {
+  VK_CHECK_ARG(x && w && y, "norm_linear: null pointer");
+  VK_CHECK_ARG(M >= 0 && N > 0 && N % 4 == 0 && K > 0, "norm_linear: bad sizes");
+  VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w) && (!norm_w || vk_aligned16(norm_w)), "norm_linear: alignment");
+  VK_CHECK_ARG(!(swiglu && out_dtype == VK_DTYPE_F32), "norm_linear: the SwiGLU epilogue stores bf16");
+  if (M == 0) return VK_OK;
+  SkinnyArgs p = base_args(x, w, y, M, N, K);
+  p.norm_w = static_cast<const bf16_t *>(norm_w);
+  p.eps = eps;
+  hipStream_t s = VK_STREAM(stream);
+  int rc;
+  if (norm_w) {
+    if (swiglu)
+      rc = dispatch_k<32, PRO_NORM, EPI_SWIGLU>(p, s);
+    else if (out_dtype == VK_DTYPE_F32)
+      rc = dispatch_k<32, PRO_NORM, EPI_F32>(p, s);
+    else
+      rc = dispatch_k<32, PRO_NORM, EPI_BF16>(p, s);
+  } else {
+    if (swiglu)
+      rc = dispatch_k<32, PRO_NONE, EPI_SWIGLU>(p, s);
+    else if (out_dtype == VK_DTYPE_F32)
+      rc = dispatch_k<32, PRO_NONE, EPI_F32>(p, s);
+    else
+      rc = dispatch_k<32, PRO_NONE, EPI_BF16>(p, s);
+  }
+  if (rc != VK_OK) return rc;
+  return launch_status("norm_linear");
+}
+
+extern "C" int vk_linear_residual(const void *a, const void *w, void *x, int64_t M, int32_t N, int32_t K,
+                                  void *stream) {
+  VK_CHECK_ARG(a && w && x, "linear_residual: null pointer");
+  VK_CHECK_ARG(M >= 0 && N > 0 && N % 4 == 0 && K > 0, "linear_residual: bad sizes");
+  VK_CHECK_ARG(vk_aligned16(a) && vk_aligned16(w) && vk_aligned16(x), "linear_residual: alignment");
+  if (M == 0) return VK_OK;
+  SkinnyArgs p = base_args(a, w, x, M, N, K);
+  const int rc = dispatch_k<32, PRO_NONE, EPI_RESID>(p, VK_STREAM(stream));
+  if (rc != VK_OK) return rc;
+  return launch_status("linear_residual");
+}
+
+extern "C" int vk_norm_qkv_rope_cache(const void *x, const int64_t *tok, int64_t vocab, void *x_store,
+                                      const void *norm_w, float eps, const void *w_qkv, const void *q_norm_w,
+                                      const void *k_norm_w, const void *cos_t, const void *sin_t, int32_t table_dtype,
+                                      int64_t table_rows, const int32_t *pos, const int32_t *rope_pos,
+                                      const int32_t *seq, void *q, void *k_cache, void *v_cache, int64_t stride_cb,
+                                      int64_t stride_cs, int64_t cache_rows, int64_t cache_len, int64_t M, int32_t K,
+                                      int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void *stream) {
+  VK_CHECK_ARG(x && norm_w && w_qkv && q_norm_w && k_norm_w && cos_t && sin_t && pos && seq && q && k_cache &&
+                   v_cache,
+               "norm_qkv_rope_cache: null pointer");
+  VK_CHECK_ARG(head_dim == 64, "norm_qkv_rope_cache: built for head_dim 64");
+  VK_CHECK_ARG(tok == nullptr || (x_store != nullptr && vocab > 0), "norm_qkv_rope_cache: embedding needs x_store");
+  VK_CHECK_ARG(table_dtype == VK_DTYPE_BF16 || table_dtype == VK_DTYPE_F32, "norm_qkv_rope_cache: table dtype");
+  VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w_qkv) && vk_aligned16(norm_w) && vk_aligned16(q),
+               "norm_qkv_rope_cache: alignment");
+  if (M == 0) return VK_OK;
+  SkinnyArgs p = base_args(x, w_qkv, q, M, (n_heads + 2 * n_kv_heads) * 64, K);
+  p.tok = tok;
+  p.vocab = vocab;
+  p.x_store = static_cast<bf16_t *>(x_store);
+  p.norm_w = static_cast<const bf16_t *>(norm_w);
+  p.eps = eps;
+  p.qw = static_cast<const bf16_t *>(q_norm_w);
+  p.kw = static_cast<const bf16_t *>(k_norm_w);
+  p.cos_t = cos_t;
+  p.sin_t = sin_t;
+  p.table_f32 = table_dtype == VK_DTYPE_F32;
+  p.table_rows = table_rows;
+  p.pos = pos;
+  p.rope_pos = rope_pos;
+  p.seq = seq;
+  p.kc = static_cast<bf16_t *>(k_cache);
+  p.vc = static_cast<bf16_t *>(v_cache);
+  p.stride_cb = stride_cb;
+  p.stride_cs = stride_cs;
+  p.cache_rows = cache_rows;
+  p.cache_len = cache_len;
+  p.H = n_heads;
+  p.HKV = n_kv_heads;
+  hipStream_t s = VK_STREAM(stream);
+  const int rc = tok ? dispatch_k<64, PRO_EMBED_NORM, EPI_ROPE>(p, s) : dispatch_k<64, PRO_NORM, EPI_ROPE>(p, s);
+  if (rc != VK_OK) return rc;
+  return launch_status("norm_qkv_rope_cache");
+}

@@ -74,18 +74,16 @@ class DecodeEngine:
             self._capture()
 
     # ---- one decode step -----------------------------------------------------------------------
-    def _select_update(self, h):
+    def _step(self):
+        # layers on the fused small-M kernels; the LM-head kernel applies the final norm, chooses the token
+        # (greedy from fp32 logits, sampled from bf16 logits: the reference's two step kinds) and advances
+        # the state. step_idx is advanced on the host after the replays (it is not read inside a step).
+        x = self.fast.decode_residual(self.pos32, self.rows, self.seqlens, self.cache,
+                                      rope_pos=None if self.pos_scale == 1 else self.rpos32, tok=self.tok)
         ops.select_update(self.bias, self.is_tail, self.is_homo, self.homo_stop, self.tok, self.run, self.pos,
                           self.plen, self.rope_off, self.out, self.pos32, self.seqlens, self.rpos32, EOS, PAD,
-                          h=h, w_head=self.dec.lm_head.weight, round_bf16=self.temperature > 0,
-                          temperature=self.temperature, uniforms=self.uniforms)
-
-    def _step(self):
-        # greedy steps choose from fp32 logits, sampled steps from bf16 logits (as the reference's two step kinds)
-        h = self.fast.decode(None, self.pos32, self.rows, self.seqlens, self.cache,
-                             rope_pos=None if self.pos_scale == 1 else self.rpos32, tok=self.tok)
-        self._select_update(h)
-        self.step_idx.add_(1)
+                          h=x, norm_w=self.dec.norm.weight, eps=self.dec.cfg.norm_eps, w_head=self.dec.lm_head.weight,
+                          round_bf16=self.temperature > 0, temperature=self.temperature, uniforms=self.uniforms)
 
     def _reset_state(self):
         self.pos.fill_(1)
@@ -188,7 +186,9 @@ class DecodeEngine:
             else:
                 self._step()
             if steps is None and (i + 1) % self.check_every == 0 and bool(((self.tok == EOS) | (self.tok == PAD)).all()):
+                n = i + 1
                 break
+        self.step_idx.add_(n)
         return self.out
 
     def generate(self, frames, frame_lens, steps=None):

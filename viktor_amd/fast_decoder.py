@@ -195,21 +195,46 @@ class FastDecoder:
 
     def decode(self, x, pos, seq, cache_seqlens, cache, rope_pos=None, tok=None):
         """One token per sequence: x [B, d] (or tok [B] token ids with x None: the embedding is looked up in
-        the first norm kernel), pos/seq [B] int32, cache_seqlens = pos + 1 (int32).
-        Reference: viktor/fast_decoder.py:76-90."""
-        cfg, W = self.cfg, self.w
-        h = None
+        the first layer's kernel), pos/seq [B] int32, cache_seqlens = pos + 1 (int32). Returns the
+        final-normed hidden [B, d]. Reference: viktor/fast_decoder.py:76-90."""
+        xr = self.decode_residual(pos, seq, cache_seqlens, cache, rope_pos=rope_pos, tok=tok, x=x)
+        return ops.add_rmsnorm(xr, self.w(self.dec.norm.weight), self.cfg.norm_eps)
+
+    def decode_residual(self, pos, seq, cache_seqlens, cache, rope_pos=None, tok=None, x=None):
+        """The decoder layers of one decode step on the fused small-M kernels, five launches per layer:
+          norm_qkv_rope_cache (attn norm + qkv GEMM + QK-norm + RoPE + cache write; layer 0 also gathers the
+          token embeddings), decode_attention, linear_residual (o proj + residual add), norm_linear
+          (mlp norm + gate_up + SwiGLU), linear_residual (down proj + residual add).
+        Returns the residual stream [B, d] after the last layer (x, updated in place, when given); the
+        final RMSNorm is left to the consumer (the LM-head kernel applies it)."""
+        cfg, W, layers = self.cfg, self.w, self.dec.layers
+        eps = cfg.norm_eps
+        H, HKV, D = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+        cos, sin = self._tables()
         if tok is not None:
             require_device(tok, "FastDecoder.decode")
-            x, h = ops.embed_rmsnorm(tok, W(self.dec.embed.weight), W(self.dec.layers[0].attn_norm.weight), cfg.norm_eps)
+            B = tok.shape[0]
+            xr = torch.empty(B, cfg.d_model, dtype=BF16, device=tok.device)
         else:
             require_device(x, "FastDecoder.decode")
+            _require(x.dtype == BF16 and x.is_contiguous(), "decode: x must be contiguous bf16")
+            B, xr = x.shape[0], x
         ws = self.decode_workspace
-
-        def attend(i, q, last):
-            return ops.decode_attention(q, cache.k[i], cache.v[i], cache_seqlens, workspace=ws)
-
-        return self._layers(x, pos, seq, cache, attend, return_kv=False, rope_pos=rope_pos, h=h)
+        for i, blk in enumerate(layers):
+            a = blk.attn
+            kc, vc = cache.k[i], cache.v[i]
+            if i == 0 and tok is not None:
+                q = ops.norm_qkv_rope_cache(W(self.dec.embed.weight), W(blk.attn_norm.weight), eps, W(a.qkv_proj.weight),
+                                            W(a.q_norm.weight), W(a.k_norm.weight), cos, sin, pos, seq, kc, vc, H, HKV,
+                                            D, rope_pos=rope_pos, tok=tok, x_store=xr)
+            else:
+                q = ops.norm_qkv_rope_cache(xr, W(blk.attn_norm.weight), eps, W(a.qkv_proj.weight), W(a.q_norm.weight),
+                                            W(a.k_norm.weight), cos, sin, pos, seq, kc, vc, H, HKV, D, rope_pos=rope_pos)
+            o = ops.decode_attention(q, kc, vc, cache_seqlens, workspace=ws)
+            ops.linear_residual(o.view(B, H * D), W(a.o_proj.weight), xr)
+            g = ops.norm_linear(xr, W(blk.mlp_norm.weight), eps, W(blk.gate_up.weight), swiglu=True)
+            ops.linear_residual(g, W(blk.down.weight), xr)
+        return xr
 
     # ---- Decoder.forward on this path ----------------------------------------------------------
     def forward(self, x, cache=None, batch_slice=slice(None), pos=None, positions=None):

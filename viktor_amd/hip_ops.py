@@ -219,9 +219,10 @@ def varlen_attention(q, k, v, plan: AttentionPlan, stride_tok=None, out=None):
 
 def select_update(bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_off, out, pos32, seqlens, rpos32, eos,
                   pad, logits=None, h=None, w_head=None, round_bf16=False, temperature=0.0, uniforms=None,
-                  logp_out=None):
-    """One step's token choice + state update for every sequence (fused LM head when h, w_head are given).
-    See vk_select_update in include/viktor_hip.h for the exact rule order."""
+                  logp_out=None, norm_w=None, eps=1e-6):
+    """One step's token choice + state update for every sequence (fused LM head when h, w_head are given;
+    with norm_w, h is the residual stream and the final RMSNorm runs first). See vk_select_update in
+    include/viktor_hip.h for the exact rule order."""
     ref = logits if logits is not None else h
     require_device(ref, "select_update")
     B = tok.shape[0]
@@ -242,10 +243,67 @@ def select_update(bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_o
         _require(uniforms is not None and uniforms.dtype == torch.float32 and uniforms.dim() == 2
                  and uniforms.shape[0] == B and uniforms.stride(1) == 1, "select_update: uniforms [B, T] fp32")
     us, uc = (uniforms.stride(0), uniforms.shape[1]) if uniforms is not None else (0, 0)
-    call("vk_select_update", ptr(logits), ptr(h), ptr(w_head), d, int(bool(round_bf16)), ptr(bias), ptr(is_tail),
+    _require(norm_w is None or (norm_w.shape == (d,) and norm_w.dtype == BF16), "select_update: norm_w")
+    call("vk_select_update", ptr(logits), ptr(h), ptr(norm_w), float(eps), ptr(w_head), d, int(bool(round_bf16)),
+         ptr(bias), ptr(is_tail),
          ptr(is_homo), int(homo_stop), float(temperature), ptr(uniforms), us, uc, ptr(tok), ptr(run), ptr(pos), ptr(plen),
          ptr(rope_off), ptr(out), out.stride(0), out.shape[1], ptr(pos32), ptr(seqlens), ptr(rpos32), ptr(logp_out), B, V,
          int(eos), int(pad), stream_handle())
+
+
+def norm_qkv_rope_cache(x, norm_w, eps, w_qkv, q_norm_w, k_norm_w, cos, sin, pos, seq, k_cache, v_cache, n_heads,
+                        n_kv_heads, head_dim, rope_pos=None, tok=None, x_store=None):
+    """Decode-step fusion: h = RMSNorm(x) * norm_w (or, with tok, x = emb[tok] where `x` is the embedding
+    table, stored into x_store), qkv = h @ w_qkv^T, then QK-norm + RoPE + KV-cache write as qkv_rope_cache.
+    Returns q [M, H, D]. Same rounding points as add_rmsnorm + linear + qkv_rope_cache."""
+    require_device(x, "norm_qkv_rope_cache")
+    M = tok.shape[0] if tok is not None else x.shape[0]
+    K = x.shape[1]
+    _require(x.dtype == BF16 and w_qkv.dtype == BF16 and w_qkv.shape == ((n_heads + 2 * n_kv_heads) * head_dim, K),
+             "norm_qkv_rope_cache: shapes")
+    _require(tok is None or (tok.dtype == torch.long and x_store is not None and x_store.shape == (M, K)),
+             "norm_qkv_rope_cache: embedding gather needs tok int64 and x_store [M, K]")
+    _require(pos.dtype == torch.int32 and seq.dtype == torch.int32 and pos.shape == (M,) and seq.shape == (M,),
+             "norm_qkv_rope_cache: pos / seq int32 [M]")
+    _require(rope_pos is None or (rope_pos.dtype == torch.int32 and rope_pos.shape == (M,)), "norm_qkv_rope_cache: rope_pos")
+    _require(cos.dtype == sin.dtype and cos.dtype in (torch.float32, BF16) and cos.shape[1] == head_dim // 2,
+             "norm_qkv_rope_cache: tables")
+    _require(k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride() and k_cache.stride(3) == 1
+             and k_cache.stride(2) == head_dim, "norm_qkv_rope_cache: cache layout")
+    _require(_contig(x, norm_w, w_qkv, q_norm_w, k_norm_w, cos, sin, pos, seq, rope_pos, tok, x_store),
+             "norm_qkv_rope_cache: contiguous tensors")
+    q = torch.empty(M, n_heads, head_dim, dtype=BF16, device=x.device)
+    call("vk_norm_qkv_rope_cache", ptr(x), ptr(tok), x.shape[0] if tok is not None else 0, ptr(x_store), ptr(norm_w),
+         float(eps), ptr(w_qkv), ptr(q_norm_w), ptr(k_norm_w), ptr(cos), ptr(sin),
+         VK_DTYPE_F32 if cos.dtype == torch.float32 else VK_DTYPE_BF16, cos.shape[0], ptr(pos), ptr(rope_pos), ptr(seq),
+         ptr(q), ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1), k_cache.shape[0], k_cache.shape[1], M,
+         K, n_heads, n_kv_heads, head_dim, stream_handle())
+    return q
+
+
+def linear_residual(a, w, x):
+    """x += a @ w^T in place (bf16 GEMM output added to the bf16 residual, rounded as linear + add_rmsnorm)."""
+    require_device(a, "linear_residual")
+    M, K = a.shape
+    _require(a.dtype == w.dtype == x.dtype == BF16 and w.shape[1] == K and x.shape == (M, w.shape[0]),
+             "linear_residual: shapes")
+    _require(_contig(a, w, x), "linear_residual: contiguous tensors")
+    call("vk_linear_residual", ptr(a), ptr(w), ptr(x), M, w.shape[0], K, stream_handle())
+    return x
+
+
+def norm_linear(x, norm_w, eps, w, swiglu=False, out_dtype=None):
+    """act(RMSNorm(x) * norm_w @ w^T) for small M (norm_w None: no norm); act = SwiGLU over [gate; up]."""
+    require_device(x, "norm_linear")
+    M, K = x.shape
+    _require(x.dtype == w.dtype == BF16 and w.shape[1] == K, "norm_linear: shapes")
+    _require(_contig(x, norm_w, w), "norm_linear: contiguous tensors")
+    N = w.shape[0] // 2 if swiglu else w.shape[0]
+    odt = out_dtype or BF16
+    y = torch.empty(M, N, dtype=odt, device=x.device)
+    call("vk_norm_linear", ptr(x), ptr(norm_w), float(eps), ptr(w), ptr(y), M, N, K, int(bool(swiglu)),
+         VK_DTYPE_F32 if odt == torch.float32 else VK_DTYPE_BF16, stream_handle())
+    return y
 
 
 def greedy_update(logits, bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_off, out, pos32, seqlens,
