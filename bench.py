@@ -94,6 +94,31 @@ def cpu_baseline(seconds_budget=30.0):
                       f"CPU restatement of the reference torch path; {dt:.1f} s"}
 
 
+def kernels_mode(reps=5):
+    """Only the dominant kernel at the rollout's mean shape (512 sequences, 2561 attended positions of a
+    3073-position cache layer) plus a plain 256 MiB device copy of known size, for hardware-counter runs
+    (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): the copy's counter readings give the scale factor from
+    counter units to bytes."""
+    from viktor_amd import hip_ops as ops
+    dev = torch.device("cuda", 0)
+    B, S, L = PREFIXES * GROUP, P + 1 + NEW, P + 2 + (NEW - 2) // 2
+    g = torch.Generator(device=dev).manual_seed(0)
+    kc = torch.randn(B, S, 2, 64, device=dev, generator=g).to(torch.bfloat16)
+    vc = torch.randn(B, S, 2, 64, device=dev, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, 8, 64, device=dev, generator=g).to(torch.bfloat16)
+    lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+    ws = ops.decode_attention_workspace(B, 8, S, dev)
+    for _ in range(reps):
+        ops.decode_attention(q, kc, vc, lens, workspace=ws)
+    x = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)  # 256 MiB
+    y = torch.empty_like(x)
+    for _ in range(reps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    alg = B * L * KV_ROW_BYTES + 2 * B * 8 * 64 * 2
+    print(json.dumps({"decode_attention_alg_bytes": alg, "copy_bytes_each_way": x.numel() * 2, "reps": reps}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -101,11 +126,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-batch", type=int, default=128)
+    ap.add_argument("--mode", choices=["rollout", "kernels"], default="rollout")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the rollout path has no multi-GPU mode here (one process per GPU, "
               "whole GSPO groups per rank); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.mode == "kernels":
+        kernels_mode()
+        return
     from viktor_amd import DecodeEngine
     from viktor_amd.synthetic import frames, uniforms
 
