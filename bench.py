@@ -1,14 +1,17 @@
 """GSPO rollout throughput on one MI355X: 64 prefixes x group 8 = 512 sequences, 2048-frame prefixes,
 1024 sampled tokens each (temperature 1.0, supplied uniforms), 8-layer d512 decoder, vocab 7.
 
-One step = one full rollout: prefill of the 512 prefixes (projector + 8 layers, BOS-only last layer) +
-1023 graph-replayed decode steps, with the frames already resident in HBM. value = 512 * 1024 tokens per
-rollout / seconds per rollout.
+One step = one full rollout: prefill of the prefixes (projector + 8 layers, BOS-only last layer) + 1023
+graph-replayed decode steps, with the frames already resident in HBM. value = 512 * 1024 tokens per
+rollout / seconds per rollout. The engine receives all 512 sequences' frames, as the rollout hands them
+over; with --group-size 8 (default) it checks that each group of 8 shares its window, prefills each window
+once and keeps one prefix KV copy per group (--group-size 1: every sequence prefilled and cached on its own).
 
 Extra objects on the JSON line:
-  roofline      decode attention, the dominant kernel: algorithmic bytes per launch (every K/V byte of
-                the attended positions once, plus q and out) / its average launch duration, measured here
-                with HIP events on the launch stream over launches at the rollout's attended lengths;
+  roofline      decode attention, the dominant kernel: algorithmic bytes per call (every K/V byte the call
+                must read once -- the shared prefix once per group, each sequence's own rows -- plus q and
+                out) / its average duration, measured here with HIP events on the launch stream over calls
+                at the rollout's attended lengths;
                 traffic = measured HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by a copy
                 kernel; read from profiles/decode_attention_traffic.json when present, else null).
   cpu_baseline  the CPU oracle (the reference's fp32 torch path restated) on this host, on a bounded slice:
@@ -48,29 +51,40 @@ def build_model(dev):
 
 
 def decode_attention_timing(eng, n_points=32, reps=5):
-    """Average duration (HIP events on the current stream) and algorithmic bytes of the decode-attention
-    kernel at the attended lengths of a rollout's decode steps j = 0..NEW-2 (len = P + 2 + j), sampled at
-    n_points evenly spaced steps, reps back-to-back launches each."""
+    """Average duration (HIP events on the current stream) and algorithmic bytes of one decode-attention
+    call at the attended lengths of a rollout's decode steps j = 0..NEW-2 (P + 1 prefix positions + j + 1
+    own positions), sampled at n_points evenly spaced steps, reps back-to-back calls each."""
     from viktor_amd import hip_ops as ops
-    B = eng.B
+    B, G = eng.B, eng.G
     cache = eng.cache
-    q = torch.randn(B, 8, 64, device=cache.k.device).to(torch.bfloat16)
+    dev = cache.k.device
+    q = torch.randn(B, 8, 64, device=dev).to(torch.bfloat16)
     js = [round(i * (NEW - 2) / (n_points - 1)) for i in range(n_points)]
-    ws = eng.fast.decode_workspace
     total_ms, total_bytes, launches = 0.0, 0.0, 0
     stream = torch.cuda.current_stream()
+    if G > 1:
+        pc, ws = eng.prefix_cache, eng.grouped_workspace
+        plen = torch.full((B // G,), P + 1, dtype=torch.int32, device=dev)
     for j in js:
-        lens = torch.full((B,), P + 2 + j, dtype=torch.int32, device=cache.k.device)
-        ops.decode_attention(q, cache.k[3], cache.v[3], lens, workspace=ws)  # warm
+        if G > 1:
+            lens = torch.full((B,), j + 1, dtype=torch.int32, device=dev)
+            call = lambda: ops.decode_attention_grouped(q, pc.k[3], pc.v[3], plen, cache.k[3], cache.v[3], lens, G,
+                                                        workspace=ws)
+            kv_rows = (B // G) * (P + 1) + B * (j + 1)
+        else:
+            lens = torch.full((B,), P + 2 + j, dtype=torch.int32, device=dev)
+            call = lambda: ops.decode_attention(q, cache.k[3], cache.v[3], lens, workspace=eng.fast.decode_workspace)
+            kv_rows = B * (P + 2 + j)
+        call()  # warm
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(reps):
-            ops.decode_attention(q, cache.k[3], cache.v[3], lens, workspace=ws)
+            call()
         e1.record(stream)
         e1.synchronize()
         total_ms += e0.elapsed_time(e1)
         launches += reps
-        total_bytes += reps * (B * (P + 2 + j) * KV_ROW_BYTES + 2 * B * 8 * 64 * 2)
+        total_bytes += reps * (kv_rows * KV_ROW_BYTES + 2 * B * 8 * 64 * 2)
     avg_s = total_ms / 1e3 / launches
     return avg_s, total_bytes / launches
 
@@ -94,29 +108,42 @@ def cpu_baseline(seconds_budget=30.0):
                       f"CPU restatement of the reference torch path; {dt:.1f} s"}
 
 
-def kernels_mode(reps=5):
-    """Only the dominant kernel at the rollout's mean shape (512 sequences, 2561 attended positions of a
-    3073-position cache layer) plus a plain 256 MiB device copy of known size, for hardware-counter runs
-    (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): the copy's counter readings give the scale factor from
-    counter units to bytes."""
+def kernels_mode(group, reps=5):
+    """Only the dominant kernel at the rollout's mean shape plus a plain 256 MiB device copy of known size,
+    for hardware-counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): the copy's counter readings give
+    the scale factor from counter units to bytes. group 1: 512 sequences x 2561 attended positions of a
+    3073-position cache layer; group G: 512 / G shared 2049-position prefixes + 512 own 512-position rows."""
     from viktor_amd import hip_ops as ops
     dev = torch.device("cuda", 0)
     B, S, L = PREFIXES * GROUP, P + 1 + NEW, P + 2 + (NEW - 2) // 2
     g = torch.Generator(device=dev).manual_seed(0)
-    kc = torch.randn(B, S, 2, 64, device=dev, generator=g).to(torch.bfloat16)
-    vc = torch.randn(B, S, 2, 64, device=dev, generator=g).to(torch.bfloat16)
     q = torch.randn(B, 8, 64, device=dev, generator=g).to(torch.bfloat16)
-    lens = torch.full((B,), L, dtype=torch.int32, device=dev)
-    ws = ops.decode_attention_workspace(B, 8, S, dev)
+    if group == 1:
+        kc = torch.randn(B, S, 2, 64, device=dev, generator=g).to(torch.bfloat16)
+        vc = torch.randn(B, S, 2, 64, device=dev, generator=g).to(torch.bfloat16)
+        lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+        ws = ops.decode_attention_workspace(B, 8, S, dev)
+        call = lambda: ops.decode_attention(q, kc, vc, lens, workspace=ws)
+        alg_rows = B * L
+    else:
+        kp = torch.randn(B // group, P + 1, 2, 64, device=dev, generator=g).to(torch.bfloat16)
+        vp = torch.randn(B // group, P + 1, 2, 64, device=dev, generator=g).to(torch.bfloat16)
+        ks = torch.randn(B, NEW, 2, 64, device=dev, generator=g).to(torch.bfloat16)
+        vs = torch.randn(B, NEW, 2, 64, device=dev, generator=g).to(torch.bfloat16)
+        plen = torch.full((B // group,), P + 1, dtype=torch.int32, device=dev)
+        slen = torch.full((B,), L - P - 1, dtype=torch.int32, device=dev)
+        ws = ops.decode_attention_grouped_workspace(B, group, P + 1, NEW, dev)
+        call = lambda: ops.decode_attention_grouped(q, kp, vp, plen, ks, vs, slen, group, workspace=ws)
+        alg_rows = (B // group) * (P + 1) + B * (L - P - 1)
     for _ in range(reps):
-        ops.decode_attention(q, kc, vc, lens, workspace=ws)
+        call()
     x = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)  # 256 MiB
     y = torch.empty_like(x)
     for _ in range(reps):
         y.copy_(x)
     torch.cuda.synchronize()
-    alg = B * L * KV_ROW_BYTES + 2 * B * 8 * 64 * 2
-    print(json.dumps({"decode_attention_alg_bytes": alg, "copy_bytes_each_way": x.numel() * 2, "reps": reps}))
+    alg = alg_rows * KV_ROW_BYTES + 2 * B * 8 * 64 * 2
+    print(json.dumps({"group": group, "decode_attention_alg_bytes": alg, "copy_bytes_each_way": x.numel() * 2, "reps": reps}))
 
 
 def main():
@@ -127,13 +154,14 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-batch", type=int, default=128)
     ap.add_argument("--mode", choices=["rollout", "kernels"], default="rollout")
+    ap.add_argument("--group-size", type=int, default=GROUP, help="sequences sharing one prefix KV copy (1: none)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the rollout path has no multi-GPU mode here (one process per GPU, "
               "whole GSPO groups per rank); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     if args.mode == "kernels":
-        kernels_mode()
+        kernels_mode(args.group_size)
         return
     from viktor_amd import DecodeEngine
     from viktor_amd.synthetic import frames, uniforms
@@ -146,7 +174,7 @@ def main():
     fr = frames(PREFIXES, P, 512, seed=0).to(dev).repeat_interleave(GROUP, 0).reshape(-1, 512)
     u = uniforms(B, NEW, seed=1).to(dev)
     plens = [P] * B
-    eng = DecodeEngine(gm, B, NEW, P, temperature=1.0, prefill_batch=args.prefill_batch)
+    eng = DecodeEngine(gm, B, NEW, P, temperature=1.0, prefill_batch=args.prefill_batch, group_size=args.group_size)
     torch.cuda.synchronize()
 
     def rollout():
@@ -182,7 +210,8 @@ def main():
     avg_s, alg_bytes = decode_attention_timing(eng)
     achieved = alg_bytes / avg_s / 1e9
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "decode_attention_traffic.json")
+    tname = "decode_attention_traffic.json" if args.group_size == 1 else "decode_attention_grouped_traffic.json"
+    tpath = os.path.join(ROOT, "profiles", tname)
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("bytes_per_launch")
@@ -200,6 +229,7 @@ def main():
         "config": {"workload": "gspo_rollout", "sequences": B, "prefixes": PREFIXES, "group": GROUP,
                    "prefix_frames": P, "new_tokens": NEW, "vocab": 7, "layers": 8, "d_model": 512,
                    "heads": "8q/2kv x 64", "temperature": 1.0, "prefill_batch": args.prefill_batch,
+                   "prefix_kv_shared_by": args.group_size,
                    "parallelism": "single GPU"},
         "prefill_ms": round(prefill_ms, 2), "decode_ms": round(decode_ms, 2),
         "live_tokens_per_rollout": live,

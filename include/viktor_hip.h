@@ -113,6 +113,25 @@ int vk_decode_attention(const void *q, const void *k_cache, const void *v_cache,
 int vk_decode_attention_workspace(int64_t B, int32_t H, int64_t max_len, int64_t *bytes);
 
 /*
+ * Decode attention for groups of G consecutive sequences that share a prefix (GSPO: the G samples of one
+ * window). Sequence b (group p = b / G) attends to prefix rows [0, prefix_len[p]) of k_prefix/v_prefix
+ * (row r of group p at p * stride_pb + r * stride_ps) followed by its own rows [0, suffix_len[b]) of
+ * k_suffix/v_suffix (b * stride_sb + r * stride_ss); softmax over the union, same numerics as
+ * vk_decode_attention. Each prefix row is read once per group (not once per sequence).
+ * G in {2, 4, 8, 16}; H = 8, HKV = 2, D = 64; workspace: vk_decode_attention_grouped_workspace() bytes.
+ * Replaces decode_attention (viktor/decode_attention.py:11-53) for rollouts that repeat each window G
+ * times (scripts/gspo.py:444); no reference counterpart for the sharing itself.
+ */
+int vk_decode_attention_grouped(const void *q, const void *k_prefix, const void *v_prefix,
+                                const int32_t *prefix_len, int64_t stride_pb, int64_t stride_ps, int64_t pre_max,
+                                const void *k_suffix, const void *v_suffix, const int32_t *suffix_len,
+                                int64_t stride_sb, int64_t stride_ss, int64_t suf_max, void *out, int64_t B,
+                                int32_t G, int32_t H, int32_t HKV, int32_t D, void *workspace,
+                                int64_t workspace_bytes, void *stream);
+
+int vk_decode_attention_grouped_workspace(int64_t B, int32_t G, int64_t pre_max, int64_t suf_max, int64_t *bytes);
+
+/*
  * Variable-length GQA attention over packed queries (flash_attn_varlen_func semantics, scale 1/sqrt(D)).
  * Sequence i has q_len_i = cu_q[i+1] - cu_q[i] queries (rows cu_q[i].. of q[*, H, D]) and
  * k_len_i = k_lens[i] keys; key j of sequence i is at k + k_off[i] + j * stride_tok (+ hk * D), same for v.
@@ -135,7 +154,8 @@ int vk_varlen_attention(const void *q, const void *k, const void *v, const int32
  *   tail rule: EOS after a tail token; homopolymer rule (homo_stop > 0): run = (nxt == prev && is_homo[nxt]) ? run + 1 : 0,
  *   EOS when run + 1 >= homo_stop; PAD after EOS or PAD.
  *   out[b * out_stride + col] = nxt with col = pos[b] - plen[b]; tok[b] = nxt; pos[b] += 1;
- *   pos32 = pos, seqlens = pos + 1, rpos32 = pos + rope_off (each optional, NULL to skip).
+ *   pos32 = pos - base, seqlens = pos - base + 1, rpos32 = pos + rope_off (each optional, NULL to skip), with
+ *   base = cache_base[b] (NULL: 0) -- the cache row of position pos when the sequence's cache starts there.
  * Logits come either from `logits` [B, V] fp32 (h and w_head NULL), or are computed here as
  * h[B, d] @ w_head[V, d]^T (bf16 inputs, fp32 accumulation), the fused LM head; with norm_w non-NULL, h is
  * the residual stream and the final RMSNorm (weight norm_w, eps) is applied to it first (rounded to bf16).
@@ -147,7 +167,8 @@ int vk_select_update(const float *logits, const void *h, const void *norm_w, flo
                      int32_t d, int32_t round_bf16,
                      const float *bias, const uint8_t *is_tail, const uint8_t *is_homo, int32_t homo_stop,
                      float temperature, const float *uniforms, int64_t u_stride, int64_t u_cols, int64_t *tok,
-                     int64_t *run, int64_t *pos, const int64_t *plen, const int64_t *rope_off, int64_t *out,
+                     int64_t *run, int64_t *pos, const int64_t *plen, const int64_t *rope_off,
+                     const int64_t *cache_base, int64_t *out,
                      int64_t out_stride, int64_t out_cols, int32_t *pos32, int32_t *seqlens, int32_t *rpos32,
                      float *logp_out, int64_t B, int32_t V, int32_t eos, int32_t pad, void *stream);
 

@@ -43,15 +43,18 @@ def check_stream(gpu_out, oracle_res, steps, thr):
     return float(agree.float().mean()), int((~agree).sum())
 
 
-def run_case(k=1, n_layers=2, lens=(40, 130, 257, 75), steps=24, T=0.0, mh=8, seed=0, ps=1, graph=True):
+def run_case(k=1, n_layers=2, lens=(40, 130, 257, 75), steps=24, T=0.0, mh=8, seed=0, ps=1, graph=True, group=1):
     m = make_model(k, n_layers=n_layers, seed=seed, norm_jitter=0.1, bias_jitter=0.1)
     m.pos_scale = ps
     lens = list(lens)
     fr = synth_frames(1, sum(lens), 512, seed=seed + 1)[0]
+    if group > 1:  # every window repeated `group` times in consecutive rows
+        fr = torch.cat([w for w in fr.split(lens) for _ in range(group)])
+        lens = [n for n in lens for _ in range(group)]
     u = synth_uniforms(len(lens), steps, seed=seed + 2)
     gm = gpu_copy(m)
     eng = DecodeEngine(gm, len(lens), steps, max(lens), cuda_graph=graph, temperature=T, max_homopolymer=mh,
-                       prefill_batch=3)
+                       prefill_batch=3, group_size=group)
     if T > 0:
         eng.set_uniforms(u.to(DEV))
     out = eng.generate(fr.to(DEV), lens).clone()
@@ -75,6 +78,42 @@ def test_greedy_stream_parity_k4():
 def test_sampled_stream_parity():
     out, res, _ = run_case(k=1, T=1.0, steps=32, lens=(50, 300, 120, 9))
     check_stream(out, res, 32, 5e-3)
+
+
+def test_grouped_greedy_stream_parity():
+    """Shared-prefix engine (4 windows x 4 samples): greedy streams of one group are identical and match
+    the oracle."""
+    out, res, eng = run_case(k=1, lens=(40, 130, 257, 75), steps=24, group=4)
+    assert eng.prefix_cache is not None
+    check_stream(out, res, 24, 1e-2)
+    o = out.view(4, 4, -1)
+    assert torch.equal(o, o[:, :1].expand_as(o))
+
+
+def test_grouped_sampled_stream_parity():
+    out, res, _ = run_case(k=1, T=1.0, steps=32, lens=(50, 300, 9), group=8)
+    check_stream(out, res, 32, 5e-3)
+
+
+def test_grouped_matches_ungrouped_engine():
+    """Same inputs through the grouped and the ungrouped engine: identical streams except at near-ties
+    (the attention sums prefix and own rows in another order)."""
+    out_g, res, _ = run_case(k=4, lens=(64, 200, 31), steps=20, mh=16, group=2, seed=3)
+    out_u, _, _ = run_case(k=4, lens=(64, 200, 31), steps=20, mh=16, group=1, seed=3)
+    check_stream(out_g, res, 20, 1e-2)
+    agree = (out_g.view(3, 2, -1)[:, 0] == out_u).float().mean()
+    assert agree > 0.9
+
+
+def test_grouped_rejects_unshared_prefix():
+    m = make_model(1, n_layers=1, seed=0)
+    gm = gpu_copy(m)
+    eng = DecodeEngine(gm, 4, 4, 64, cuda_graph=False, group_size=2)
+    fr = synth_frames(1, 4 * 20, 512, seed=1)[0].to(DEV)
+    with pytest.raises(ValueError, match="share"):
+        eng.generate(fr, [20, 20, 20, 20])
+    with pytest.raises(ValueError, match="prefix lengths"):
+        eng.generate(fr, [20, 21, 20, 19])
 
 
 def test_sampled_stream_parity_k4_temperature():

@@ -200,6 +200,82 @@ def test_decode_attention_cache_view_and_graph():
     assert (eager.float().cpu() - ref).abs().max() < 1e-2
 
 
+@pytest.mark.parametrize("G,pre_max,suf_max", [(8, 2049, 1024), (4, 700, 33), (2, 65, 300), (16, 513, 64)])
+def test_decode_attention_grouped(G, pre_max, suf_max):
+    """Groups of G sequences share prefix rows [0, prefix_len) and own suffix rows [0, suffix_len): equal to
+    attention over the concatenated rows."""
+    torch.manual_seed(G * 1000 + pre_max)
+    P = 6
+    B, H, HKV, D = P * G, 8, 2, 64
+    pre_edge = torch.tensor([1, 31, 32, 33, 512, 513, pre_max])
+    plen = torch.cat([pre_edge, torch.randint(1, pre_max + 1, (P,))])[:P].clamp(max=pre_max).int()
+    suf_edge = torch.tensor([1, 2, 31, 32, 33, suf_max])
+    slen = torch.cat([suf_edge, torch.randint(1, suf_max + 1, (B,))])[:B].clamp(max=suf_max).int()
+    q = torch.randn(B, H, D).to(BF)
+    kp = torch.randn(P, pre_max, HKV, D).to(BF)
+    vp = torch.randn(P, pre_max, HKV, D).to(BF)
+    ks = torch.randn(B, suf_max, HKV, D).to(BF)
+    vs = torch.randn(B, suf_max, HKV, D).to(BF)
+    out = ops.decode_attention_grouped(q.to(DEV), kp.to(DEV), vp.to(DEV), plen.to(DEV), ks.to(DEV), vs.to(DEV),
+                                       slen.to(DEV), G).cpu()
+    for b in range(B):
+        p, lp, ls = b // G, int(plen[b // G]), int(slen[b])
+        k = torch.cat([kp[p, :lp], ks[b, :ls]])[None]
+        v = torch.cat([vp[p, :lp], vs[b, :ls]])[None]
+        ref = _sdpa_ref(q[b:b + 1], k, v, torch.tensor([lp + ls]))
+        err = (out[b:b + 1].float() - ref).abs().max()
+        assert err < 1e-2, (b, lp, ls, float(err))
+
+
+def test_decode_attention_grouped_cache_view_and_graph():
+    """Layer views of [L, P, S, 2, 64] / [L, B, S, 2, 64] caches inside a graph replayed several times; the
+    ungrouped kernel over the concatenated rows agrees to bf16 rounding."""
+    torch.manual_seed(5)
+    L, G, P, Sp, Ss = 2, 8, 4, 300, 40
+    B = G * P
+    kp = torch.randn(L, P, Sp, 2, 64, device=DEV).to(BF)
+    vp = torch.randn(L, P, Sp, 2, 64, device=DEV).to(BF)
+    ks = torch.randn(L, B, Ss, 2, 64, device=DEV).to(BF)
+    vs = torch.randn(L, B, Ss, 2, 64, device=DEV).to(BF)
+    q = torch.randn(B, 8, 64, device=DEV).to(BF)
+    plen = torch.randint(1, Sp + 1, (P,), device=DEV).int()
+    slen = torch.randint(1, Ss + 1, (B,), device=DEV).int()
+    ws = ops.decode_attention_grouped_workspace(B, G, Sp, Ss, DEV)
+    run = lambda: ops.decode_attention_grouped(q, kp[1], vp[1], plen, ks[1], vs[1], slen, G, workspace=ws)
+    eager = run()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = run()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+    # ungrouped: concatenate prefix + suffix rows per sequence
+    kc = torch.zeros(B, Sp + Ss, 2, 64, device=DEV, dtype=BF)
+    vc = torch.zeros_like(kc)
+    for b in range(B):
+        lp, ls = int(plen[b // G]), int(slen[b])
+        kc[b, :lp], vc[b, :lp] = kp[1, b // G, :lp], vp[1, b // G, :lp]
+        kc[b, lp:lp + ls], vc[b, lp:lp + ls] = ks[1, b, :ls], vs[1, b, :ls]
+    flat = ops.decode_attention(q, kc, vc, plen.repeat_interleave(G) + slen)
+    assert (eager.float() - flat.float()).abs().max() < 1e-2
+
+
+def test_decode_attention_grouped_rejects_bad_group():
+    q = torch.zeros(12, 8, 64, device=DEV, dtype=BF)
+    kp = torch.zeros(2, 8, 2, 64, device=DEV, dtype=BF)
+    ks = torch.zeros(12, 8, 2, 64, device=DEV, dtype=BF)
+    with pytest.raises(Exception, match="group size"):
+        ops.decode_attention_grouped(q, kp, kp, torch.ones(2, dtype=torch.int32, device=DEV), ks, ks,
+                                     torch.ones(12, dtype=torch.int32, device=DEV), 6,
+                                     workspace=torch.empty(1 << 20, dtype=torch.uint8, device=DEV))
+
+
 def _varlen_ref(q, k, v, q_lens, k_lens, causal=True):
     outs = []
     qo = ko = 0

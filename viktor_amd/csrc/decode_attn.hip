@@ -276,6 +276,268 @@ static int device_cus_cached() {
   return cus;
 }
 
+
+// ---- groups of sequences that share one prefix (GSPO: G samples of one window) ----------------------
+//
+// A sequence of group p attends to the group's prefix rows (frames + BOS, one copy in the prefix cache
+// [P, S_pre, 2, 64]) followed by its own suffix rows (sampled tokens, suffix cache [B, S_suf, 2, 64]).
+// Prefix: one workgroup per (chunk of prefix rows, group, KV head); its query columns are the 4 heads
+// of that KV head for all G members (4 G columns), so each 128-byte K / V row of the prefix is fetched
+// once for the whole group. Suffix: the single-sequence kernel above, writing partials. Combine: merges
+// prefix-chunk and suffix-split partials of each (sequence, head).
+
+constexpr int GP_WAVES = 8;
+constexpr int GP_TILE = 32;
+constexpr int GP_PITCH = 72;  // one KV head: 64 + 8 pad
+constexpr int GP_CHUNK_TILES = 16;
+
+template <int G>
+__global__ __launch_bounds__(GP_WAVES * 64) void prefix_attn_kernel(
+    const bf16_t *__restrict__ q, const bf16_t *__restrict__ kp, const bf16_t *__restrict__ vp,
+    const int32_t *__restrict__ pre_len, int64_t stride_pb, int64_t stride_ps, int64_t pre_max, int n_chunks,
+    float *__restrict__ ws_o, float *__restrict__ ws_ml, float scale_log2) {
+  constexpr int NC = 4 * G;            // query columns of one KV head (G members x 4 heads)
+  constexpr int NCB = (NC + 15) / 16;  // 16-column MFMA blocks
+  constexpr int LDS_V = GP_WAVES * GP_TILE * GP_PITCH * 2;
+  constexpr int LDS_M = (GP_WAVES * NC * 64 + 2 * GP_WAVES * NC) * 4;
+  __shared__ __attribute__((aligned(16))) char smem[LDS_V > LDS_M ? LDS_V : LDS_M];
+
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int chunk = blockIdx.x, p = blockIdx.y, kvh = blockIdx.z;
+  int64_t len = pre_len[p];
+  len = len < 1 ? 1 : (len > pre_max ? pre_max : len);
+  const int ntiles = static_cast<int>((len + GP_TILE - 1) / GP_TILE);
+  const int t_begin = chunk * GP_CHUNK_TILES;
+  const int t_end = min(t_begin + GP_CHUNK_TILES, ntiles);
+  if (t_begin >= t_end) return;
+  const int col = lane & 15, g = lane >> 4;
+
+  // Q^T fragments: column j = 16 cb + col -> member j / 4, head kvh * 4 + j % 4, the two 32-wide halves of D
+  bf16x8 bq[NCB][2];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    const int j = 16 * cb + col;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      u32x4 v = u32x4{0u, 0u, 0u, 0u};
+      if (j < NC) {
+        const int64_t row = static_cast<int64_t>(p) * G + j / 4;
+        v = *reinterpret_cast<const u32x4 *>(q + (row * DA_H + kvh * 4 + (j & 3)) * DA_D + 32 * c + 8 * g);
+      }
+      bq[cb][c] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+  f32x4 acc[NCB][4];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc[cb][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[NCB], l_run[NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    m_run[cb] = -INFINITY;
+    l_run[cb] = 0.f;
+  }
+  const bf16_t *kb = kp + p * stride_pb + kvh * DA_D;
+  const bf16_t *vb = vp + p * stride_pb + kvh * DA_D;
+  bf16_t *vs = reinterpret_cast<bf16_t *>(smem) + wid * GP_TILE * GP_PITCH;
+
+  u32x4 kf[2][2], vf[2][2];
+  auto row_ptr = [&](const bf16_t *base, int tt, int pb) {
+    int64_t r = static_cast<int64_t>(tt) * GP_TILE + 16 * pb + col;
+    r = r < len ? r : len - 1;
+    return base + r * stride_ps + 8 * g;
+  };
+  auto load_k = [&](int tt) {
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) kf[pb][c] = *reinterpret_cast<const u32x4 *>(row_ptr(kb, tt, pb) + 32 * c);
+  };
+  auto load_v = [&](int tt) {
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) vf[pb][c] = *reinterpret_cast<const u32x4 *>(row_ptr(vb, tt, pb) + 32 * c);
+  };
+  const int t_first = min(t_begin + wid, t_end - 1);
+  load_k(t_first);
+  asm volatile("" ::: "memory");
+  load_v(t_first);
+  for (int t = t_begin + wid; t < t_end; t += GP_WAVES) {
+    const int64_t p0 = static_cast<int64_t>(t) * GP_TILE;
+    const int tn = t + GP_WAVES < t_end ? t + GP_WAVES : t;
+    f32x4 st[2][NCB];
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        st[pb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          st[pb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[pb][c]), bq[cb][c],
+                                                               st[pb][cb], 0, 0, 0);
+      }
+    load_k(tn);
+    bf16x8 pf[NCB];
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      float sv[8];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t r = p0 + 16 * pb + 4 * g + i;
+          const float v = r < len ? st[pb][cb][i] * scale_log2 : -INFINITY;
+          sv[pb * 4 + i] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run[cb], mx);
+      const float alpha = exp2f(m_run[cb] - m_new);
+      float ps = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const float e = exp2f(sv[jj] - m_new);
+        ps += e;
+        pf[cb][jj] = __builtin_bit_cast(__bf16, f2bf(e));
+      }
+      l_run[cb] = l_run[cb] * alpha + ps;
+      m_run[cb] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) acc[cb][dt] *= alpha;
+    }
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        *reinterpret_cast<u32x4 *>(&vs[(16 * pb + col) * GP_PITCH + 32 * c + 8 * g]) = vf[pb][c];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    load_v(tn);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      bf16x8 va;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const int pl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
+        va[jj] = __builtin_bit_cast(__bf16, vs[pl * GP_PITCH + 16 * dt + col]);
+      }
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb)
+        acc[cb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[cb], acc[cb][dt], 0, 0, 0);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    l_run[cb] += __shfl_xor(l_run[cb], 16, 64);
+    l_run[cb] += __shfl_xor(l_run[cb], 32, 64);
+  }
+  __syncthreads();
+  float *Os = reinterpret_cast<float *>(smem);  // [WAVES][NC][64]
+  float *Ms = Os + GP_WAVES * NC * 64;           // [WAVES][NC]
+  float *Ls = Ms + GP_WAVES * NC;
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    const int j = 16 * cb + col;
+    if (j < NC) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Os[(wid * NC + j) * 64 + 16 * dt + 4 * g + i] = acc[cb][dt][i];
+      if (g == 0) {
+        Ms[wid * NC + j] = m_run[cb];
+        Ls[wid * NC + j] = l_run[cb];
+      }
+    }
+  }
+  __syncthreads();
+  for (int o = threadIdx.x; o < NC * 64; o += GP_WAVES * 64) {
+    const int j = o / 64, d = o % 64;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < GP_WAVES; ++w) M = fmaxf(M, Ms[w * NC + j]);
+    float L = 0.f, N = 0.f;
+#pragma unroll
+    for (int w = 0; w < GP_WAVES; ++w) {
+      const float e = exp2f(Ms[w * NC + j] - M);
+      L += e * Ls[w * NC + j];
+      N += e * Os[(w * NC + j) * 64 + d];
+    }
+    // partial of (group p, chunk, member j / 4, head kvh * 4 + j % 4)
+    const int64_t base = ((static_cast<int64_t>(p) * n_chunks + chunk) * G + j / 4) * DA_H + kvh * 4 + (j & 3);
+    ws_o[base * DA_D + d] = N;
+    if (d == 0) {
+      ws_ml[base * 2] = M;
+      ws_ml[base * 2 + 1] = L;
+    }
+  }
+}
+
+// out[b, h] = merge of the prefix-chunk partials of b's group and the suffix-split partials of b
+__global__ __launch_bounds__(DA_H * DA_D) void grouped_combine_kernel(
+    const float *__restrict__ pre_o, const float *__restrict__ pre_ml, const float *__restrict__ suf_o,
+    const float *__restrict__ suf_ml, const int32_t *__restrict__ pre_len, const int32_t *__restrict__ suf_len,
+    bf16_t *__restrict__ out, int G, int64_t pre_max, int n_chunks, int64_t suf_max, int tps, int nsplit) {
+  const int64_t b = blockIdx.x;
+  const int h = threadIdx.x / DA_D, d = threadIdx.x % DA_D;
+  const int64_t p = b / G, member = b % G;
+  int64_t lp = pre_len[p];
+  lp = lp < 1 ? 1 : (lp > pre_max ? pre_max : lp);
+  const int np = min(n_chunks, static_cast<int>((((lp + GP_TILE - 1) / GP_TILE) + GP_CHUNK_TILES - 1) / GP_CHUNK_TILES));
+  int64_t ls = suf_len[b];
+  ls = ls < 1 ? 1 : (ls > suf_max ? suf_max : ls);
+  const int ns = min(nsplit, static_cast<int>((((ls + DA_TILE - 1) / DA_TILE) + tps - 1) / tps));
+  float M = -INFINITY;
+  for (int c = 0; c < np; ++c) M = fmaxf(M, pre_ml[(((p * n_chunks + c) * G + member) * DA_H + h) * 2]);
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, suf_ml[((b * nsplit + s) * DA_H + h) * 2]);
+  float L = 0.f, N = 0.f;
+  for (int c = 0; c < np; ++c) {
+    const int64_t base = ((p * n_chunks + c) * G + member) * DA_H + h;
+    const float e = exp2f(pre_ml[base * 2] - M);
+    L += e * pre_ml[base * 2 + 1];
+    N += e * pre_o[base * DA_D + d];
+  }
+  for (int s = 0; s < ns; ++s) {
+    const int64_t base = (b * nsplit + s) * DA_H + h;
+    const float e = exp2f(suf_ml[base * 2] - M);
+    L += e * suf_ml[base * 2 + 1];
+    N += e * suf_o[base * DA_D + d];
+  }
+  out[(b * DA_H + h) * DA_D + d] = f2bf(N / L);
+}
+
+struct GroupedLayout {
+  int n_chunks;
+  DecodeSplit suf;
+  int64_t pre_o, pre_ml, suf_o, suf_ml, total;  // offsets / size in floats
+};
+
+static GroupedLayout grouped_layout(int64_t B, int G, int64_t pre_max, int64_t suf_max, int cus) {
+  GroupedLayout L{};
+  const int64_t P = B / G;
+  const int ntiles = static_cast<int>((pre_max + GP_TILE - 1) / GP_TILE);
+  L.n_chunks = (ntiles + GP_CHUNK_TILES - 1) / GP_CHUNK_TILES;
+  // suffix partials always go through the workspace (nsplit >= 1)
+  L.suf = decode_split(B, suf_max, cus);
+  L.pre_o = 0;
+  L.pre_ml = L.pre_o + P * L.n_chunks * G * DA_H * DA_D;
+  L.suf_o = L.pre_ml + P * L.n_chunks * G * DA_H * 2;
+  L.suf_ml = L.suf_o + B * L.suf.nsplit * DA_H * DA_D;
+  L.total = L.suf_ml + B * L.suf.nsplit * DA_H * 2;
+  return L;
+}
+
+template <int G>
+static void launch_prefix(const bf16_t *q, const bf16_t *kp, const bf16_t *vp, const int32_t *pre_len, int64_t P,
+                          int64_t stride_pb, int64_t stride_ps, int64_t pre_max, int n_chunks, float *ws_o,
+                          float *ws_ml, float scale_log2, hipStream_t s) {
+  const dim3 grid(n_chunks, static_cast<unsigned>(P), DA_HKV);
+  prefix_attn_kernel<G><<<grid, GP_WAVES * 64, 0, s>>>(q, kp, vp, pre_len, stride_pb, stride_ps, pre_max, n_chunks,
+                                                       ws_o, ws_ml, scale_log2);
+}
 }  // namespace vk
 
 using namespace vk;
@@ -323,4 +585,63 @@ extern "C" int vk_decode_attention(const void *q, const void *k_cache, const voi
                                                                        static_cast<bf16_t *>(out), max_len, sp.tps,
                                                                        sp.nsplit);
   return launch_status("decode_attention_combine");
+}
+
+extern "C" int vk_decode_attention_grouped_workspace(int64_t B, int32_t G, int64_t pre_max, int64_t suf_max,
+                                                     int64_t *bytes) {
+  VK_CHECK_ARG(bytes && B > 0 && G > 0 && B % G == 0 && pre_max > 0 && suf_max > 0,
+               "decode_attention_grouped_workspace: bad arguments");
+  *bytes = grouped_layout(B, G, pre_max, suf_max, device_cus_cached()).total * static_cast<int64_t>(sizeof(float));
+  return VK_OK;
+}
+
+extern "C" int vk_decode_attention_grouped(const void *q, const void *k_prefix, const void *v_prefix,
+                                           const int32_t *prefix_len, int64_t stride_pb, int64_t stride_ps,
+                                           int64_t pre_max, const void *k_suffix, const void *v_suffix,
+                                           const int32_t *suffix_len, int64_t stride_sb, int64_t stride_ss,
+                                           int64_t suf_max, void *out, int64_t B, int32_t G, int32_t H, int32_t HKV,
+                                           int32_t D, void *workspace, int64_t workspace_bytes, void *stream) {
+  VK_CHECK_ARG(q && k_prefix && v_prefix && prefix_len && k_suffix && v_suffix && suffix_len && out && workspace,
+               "decode_attention_grouped: null pointer");
+  if (H != DA_H || HKV != DA_HKV || D != DA_D)
+    return fail(VK_ERR_UNSUPPORTED, "decode_attention_grouped: built for H=8 HKV=2 D=64 (got %d/%d/%d)", H, HKV, D);
+  if (G != 2 && G != 4 && G != 8 && G != 16)
+    return fail(VK_ERR_UNSUPPORTED, "decode_attention_grouped: group size must be 2, 4, 8 or 16 (got %d)", G);
+  VK_CHECK_ARG(B > 0 && B % G == 0 && B < 65536 && pre_max > 0 && suf_max > 0, "decode_attention_grouped: sizes");
+  VK_CHECK_ARG(stride_ps >= DA_ROW && stride_ss >= DA_ROW && stride_ps % 8 == 0 && stride_ss % 8 == 0 &&
+                   stride_pb % 8 == 0 && stride_sb % 8 == 0,
+               "decode_attention_grouped: strides");
+  VK_CHECK_ARG(vk_aligned16(q) && vk_aligned16(k_prefix) && vk_aligned16(v_prefix) && vk_aligned16(k_suffix) &&
+                   vk_aligned16(v_suffix),
+               "decode_attention_grouped: alignment");
+  const GroupedLayout L = grouped_layout(B, G, pre_max, suf_max, device_cus_cached());
+  VK_CHECK_ARG(workspace_bytes >= L.total * static_cast<int64_t>(sizeof(float)),
+               "decode_attention_grouped: workspace of %lld bytes needed",
+               static_cast<long long>(L.total * sizeof(float)));
+  const float scale_log2 = static_cast<float>(1.0 / sqrt(static_cast<double>(DA_D)) * 1.4426950408889634);
+  hipStream_t s = VK_STREAM(stream);
+  float *ws = static_cast<float *>(workspace);
+  const auto qb = static_cast<const bf16_t *>(q);
+  const auto kp = static_cast<const bf16_t *>(k_prefix);
+  const auto vp = static_cast<const bf16_t *>(v_prefix);
+  const int64_t P = B / G;
+  switch (G) {
+    case 2: launch_prefix<2>(qb, kp, vp, prefix_len, P, stride_pb, stride_ps, pre_max, L.n_chunks, ws + L.pre_o, ws + L.pre_ml, scale_log2, s); break;
+    case 4: launch_prefix<4>(qb, kp, vp, prefix_len, P, stride_pb, stride_ps, pre_max, L.n_chunks, ws + L.pre_o, ws + L.pre_ml, scale_log2, s); break;
+    case 8: launch_prefix<8>(qb, kp, vp, prefix_len, P, stride_pb, stride_ps, pre_max, L.n_chunks, ws + L.pre_o, ws + L.pre_ml, scale_log2, s); break;
+    default: launch_prefix<16>(qb, kp, vp, prefix_len, P, stride_pb, stride_ps, pre_max, L.n_chunks, ws + L.pre_o, ws + L.pre_ml, scale_log2, s); break;
+  }
+  int rc = launch_status("decode_attention_grouped prefix");
+  if (rc != VK_OK) return rc;
+  const dim3 sgrid(L.suf.nsplit, static_cast<unsigned>(B));
+  decode_attn_kernel<true><<<sgrid, DA_WAVES * 64, 0, s>>>(
+      qb, static_cast<const bf16_t *>(k_suffix), static_cast<const bf16_t *>(v_suffix), suffix_len,
+      static_cast<bf16_t *>(out), stride_sb, stride_ss, suf_max, L.suf.tps, L.suf.nsplit, ws + L.suf_o, ws + L.suf_ml,
+      scale_log2);
+  rc = launch_status("decode_attention_grouped suffix");
+  if (rc != VK_OK) return rc;
+  grouped_combine_kernel<<<static_cast<unsigned>(B), DA_H * DA_D, 0, s>>>(
+      ws + L.pre_o, ws + L.pre_ml, ws + L.suf_o, ws + L.suf_ml, prefix_len, suffix_len, static_cast<bf16_t *>(out), G,
+      pre_max, L.n_chunks, suf_max, L.suf.tps, L.suf.nsplit);
+  return launch_status("decode_attention_grouped combine");
 }

@@ -3,13 +3,16 @@
 // viktor/fast_decoder.py:68-73, and of flash_attn_func(causal=True) at viktor/decoder.py:82-87).
 //
 // MI355X design:
-//   * Workgroup = one 64-query block of one sequence x one KV head; its 4 wavefronts are the 4 query
-//     heads of that KV head, so every K/V tile staged in LDS serves 4 heads (GQA 4:1).
-//   * Keys advance in 32-row tiles, double buffered in LDS (next tile's global loads in flight during
-//     the MFMAs on the current one; 16-byte pad per row).
+//   * Workgroup = one 64-query block of one sequence x one KV head, 8 wavefronts: the 4 query heads of
+//     that KV head x 2 halves of 32 query rows. Every K/V tile staged in LDS serves 4 heads x 64 rows.
+//   * Keys advance in 64-row tiles, double buffered in LDS (the next tile's global loads are in flight
+//     during the MFMAs on the current one; 16-byte pad per row). Within a tile a wave works in two
+//     32-key halves; halves that lie entirely above the causal diagonal of the wave's rows are skipped.
 //   * Transposed products as in the decode kernel: S^T = K Q^T (A = key rows from LDS, B = Q^T held in
-//     registers for the whole loop) leaves each lane the scores of one query column; O^T = V^T P^T
-//     consumes those probabilities in place and the online-softmax rescale stays lane-local.
+//     registers for the whole loop) leaves each lane the scores of one query row; O^T = V^T P^T consumes
+//     those probabilities in place and the online-softmax rescale stays lane-local.
+//   * Per-wave state is 32 query rows (Q^T 16, O^T 32, scores 16 VGPRs) so the kernel fits 4 waves per
+//     SIMD: two workgroups per CU.
 //   * Keys of sequence i live at base + k_off[i] + j * stride_tok (+ kv head * 64): the same kernel
 //     reads packed k/v rows or a KV-cache layer directly.
 //   * The host orders the query blocks longest-first (causal blocks near the end of a sequence do the
@@ -21,11 +24,12 @@
 namespace vk {
 
 constexpr int PA_H = 8, PA_HKV = 2, PA_D = 64;
-constexpr int PA_Q = 64;      // query rows per workgroup (per wave: one head x 64 queries)
-constexpr int PA_KT = 32;     // keys per LDS tile
+constexpr int PA_Q = 64;      // query rows per workgroup (plan granularity)
+constexpr int PA_WAVES = 8;   // 4 query heads x 2 halves of 32 rows
+constexpr int PA_KT = 64;     // keys per LDS tile
 constexpr int PA_PITCH = 72;  // 64 + 8 bf16
 
-__global__ __launch_bounds__(256) void varlen_attn_kernel(
+__global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ k, const bf16_t *__restrict__ v,
     const int32_t *__restrict__ cu_q, const int64_t *__restrict__ k_off, const int32_t *__restrict__ k_lens,
     const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok, bf16_t *__restrict__ out, int causal,
@@ -37,7 +41,8 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(
   const int lane = tid & 63, wid = tid >> 6;
   const int col = lane & 15, g = lane >> 4;
   const int hk = blockIdx.y;
-  const int hq = hk * (PA_H / PA_HKV) + wid;
+  const int hq = hk * (PA_H / PA_HKV) + (wid & 3);
+  const int half = wid >> 2;
   const int seq = plan[2 * blockIdx.x];
   const int qs = plan[2 * blockIdx.x + 1];
   if (seq < 0 || seq >= n_seq || qs < 0) return;
@@ -52,37 +57,30 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(
   if (kend <= 0) return;
   const int ntiles = (kend + PA_KT - 1) / PA_KT;
 
-  // Q^T fragments for the 4 query blocks of 16 and the two 32-wide halves of D
-  bf16x8 bq[4][2];
+  // this wave's 32 query rows: two blocks of 16 (row = lane % 16 within a block)
+  const int r_first = qs + 32 * half;
+  int qpos[2];
+  bf16x8 bq[2][2];
 #pragma unroll
-  for (int qb = 0; qb < 4; ++qb) {
-    int r = qs + 16 * qb + col;
+  for (int qb = 0; qb < 2; ++qb) {
+    int r = r_first + 16 * qb + col;
     r = r < q_len ? r : q_len - 1;
+    qpos[qb] = qshift + r;
     const bf16_t *src = q + ((q0 + r) * PA_H + hq) * PA_D + g * 8;
 #pragma unroll
     for (int dc = 0; dc < 2; ++dc) bq[qb][dc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(src + 32 * dc));
   }
-  int qpos[4];
-#pragma unroll
-  for (int qb = 0; qb < 4; ++qb) {
-    int r = qs + 16 * qb + col;
-    r = r < q_len ? r : q_len - 1;
-    qpos[qb] = qshift + r;
-  }
+  // highest key any row of this wave may see (rows past q_len are clamped copies of the last row)
+  const int wave_kmax = causal ? qshift + min(r_first + 31, q_len - 1) : klen - 1;
 
-  f32x4 acc[4][4];  // [d tile][query block]
+  f32x4 acc[4][2];  // O^T tiles [d tile][query block]
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[4], l_run[4];
-#pragma unroll
-  for (int qb = 0; qb < 4; ++qb) {
-    m_run[qb] = -INFINITY;
-    l_run[qb] = 0.f;
-  }
+    for (int c = 0; c < 2; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
 
-  // cooperative tile load: thread -> (key row, 16-byte chunk)
+  // cooperative tile load: 512 threads -> (key row 0..63, 16-byte chunk 0..7) of K and of V
   const int lrow = tid >> 3, lchunk = tid & 7;
   u32x4 rk, rv;
   auto load_tile = [&](int t) {
@@ -103,78 +101,85 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     if (t + 1 < ntiles) load_tile(t + 1);
-    const int kbase = t * PA_KT;
-    // S^T[key][query] for the two 16-key blocks
-    f32x4 st[2][4];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      bf16x8 ka[2];
+    for (int ks = 0; ks < 2; ++ks) {
+      const int kbase = t * PA_KT + 32 * ks;
+      if (kbase > wave_kmax) continue;  // wave-uniform: every key of this half is masked for every row
+      const bf16_t *kt = &Ks[buf][32 * ks * PA_PITCH];
+      const bf16_t *vt = &Vs[buf][32 * ks * PA_PITCH];
+      // S^T[key][query] for two 16-key blocks x two 16-query blocks
+      f32x4 st[2][2];
 #pragma unroll
-      for (int dc = 0; dc < 2; ++dc)
-        ka[dc] = *reinterpret_cast<const bf16x8 *>(&Ks[buf][(16 * kb + col) * PA_PITCH + 32 * dc + g * 8]);
-#pragma unroll
-      for (int qb = 0; qb < 4; ++qb) {
-        st[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int kb = 0; kb < 2; ++kb) {
+        bf16x8 ka[2];
 #pragma unroll
         for (int dc = 0; dc < 2; ++dc)
-          st[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[dc], bq[qb][dc], st[kb][qb], 0, 0, 0);
-      }
-    }
-    bf16x8 pf[4];
+          ka[dc] = *reinterpret_cast<const bf16x8 *>(&kt[(16 * kb + col) * PA_PITCH + 32 * dc + g * 8]);
 #pragma unroll
-    for (int qb = 0; qb < 4; ++qb) {
-      float sv[8];
-      float mx = -INFINITY;
+        for (int qb = 0; qb < 2; ++qb) {
+          st[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = kbase + 16 * kb + 4 * g + i;
-          const bool ok = key < klen && (!causal || key <= qpos[qb]);
-          const float s = ok ? st[kb][qb][i] * scale_log2 : -INFINITY;
-          sv[kb * 4 + i] = s;
-          mx = fmaxf(mx, s);
+          for (int dc = 0; dc < 2; ++dc)
+            st[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[dc], bq[qb][dc], st[kb][qb], 0, 0, 0);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run[qb], mx);
-      // m_new is finite: tile 0 always holds key 0, visible to every query
-      const float alpha = exp2f(m_run[qb] - m_new);
-      float ps = 0.f;
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const float p = exp2f(sv[jj] - m_new);
-        ps += p;
-        pf[qb][jj] = __builtin_bit_cast(__bf16, f2bf(p));
       }
-      l_run[qb] = l_run[qb] * alpha + ps;
-      m_run[qb] = m_new;
+      const bool need_mask = kbase + 31 >= klen || (causal && kbase + 31 > qshift + r_first);
+      bf16x8 pf[2];
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) acc[dt][qb] *= alpha;
-    }
-    // O^T += V^T P^T
+      for (int qb = 0; qb < 2; ++qb) {
+        float sv[8];
+        float mx = -INFINITY;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      bf16x8 va;
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const int kl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
-        va[jj] = __builtin_bit_cast(__bf16, Vs[buf][kl * PA_PITCH + 16 * dt + col]);
+          for (int i = 0; i < 4; ++i) {
+            const int key = kbase + 16 * kb + 4 * g + i;
+            const bool ok = !need_mask || (key < klen && (!causal || key <= qpos[qb]));
+            const float s = ok ? st[kb][qb][i] * scale_log2 : -INFINITY;
+            sv[kb * 4 + i] = s;
+            mx = fmaxf(mx, s);
+          }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        // m_new is finite: tile 0 always holds key 0, visible to every query
+        const float m_new = fmaxf(m_run[qb], mx);
+        const float alpha = exp2f(m_run[qb] - m_new);
+        float ps = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const float p = exp2f(sv[jj] - m_new);
+          ps += p;
+          pf[qb][jj] = __builtin_bit_cast(__bf16, f2bf(p));
+        }
+        l_run[qb] = l_run[qb] * alpha + ps;
+        m_run[qb] = m_new;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) acc[dt][qb] *= alpha;
       }
+      // O^T += V^T P^T (key order {4g..4g+3, 16+4g..16+4g+3} in both operands)
 #pragma unroll
-      for (int qb = 0; qb < 4; ++qb) acc[dt][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[qb], acc[dt][qb], 0, 0, 0);
+      for (int dt = 0; dt < 4; ++dt) {
+        bf16x8 va;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const int kl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
+          va[jj] = __builtin_bit_cast(__bf16, vt[kl * PA_PITCH + 16 * dt + col]);
+        }
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) acc[dt][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[qb], acc[dt][qb], 0, 0, 0);
+      }
     }
     if (t + 1 < ntiles) store_tile(buf ^ 1);
     __syncthreads();
   }
 
 #pragma unroll
-  for (int qb = 0; qb < 4; ++qb) {
+  for (int qb = 0; qb < 2; ++qb) {
     float l = l_run[qb];
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
-    const int r = qs + 16 * qb + col;
-    if (r >= q_len) continue;
+    const int r = r_first + 16 * qb + col;
+    if (r >= q_len || r >= qs + nq) continue;
     const float inv = 1.0f / l;
     bf16_t *dst = out + ((q0 + r) * PA_H + hq) * PA_D + 4 * g;
 #pragma unroll
@@ -206,7 +211,7 @@ extern "C" int vk_varlen_attention(const void *q, const void *k, const void *v, 
   if (n_blocks == 0) return VK_OK;
   const float scale_log2 = static_cast<float>(1.0 / sqrt(static_cast<double>(PA_D)) * 1.4426950408889634);
   const dim3 grid(static_cast<unsigned>(n_blocks), PA_HKV);
-  varlen_attn_kernel<<<grid, 256, 0, VK_STREAM(stream)>>>(
+  varlen_attn_kernel<<<grid, PA_WAVES * 64, 0, VK_STREAM(stream)>>>(
       static_cast<const bf16_t *>(q), static_cast<const bf16_t *>(k), static_cast<const bf16_t *>(v), cu_q, k_off,
       k_lens, plan, n_seq, stride_tok, static_cast<bf16_t *>(out), causal, scale_log2);
   return launch_status("varlen_attention");

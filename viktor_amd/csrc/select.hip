@@ -25,9 +25,9 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
     const bf16_t *__restrict__ w_head, int d, int round_bf16, const float *__restrict__ bias, const uint8_t *__restrict__ is_tail,
     const uint8_t *__restrict__ is_homo, int homo_stop, float temperature, const float *__restrict__ uniforms,
     int64_t u_stride, int64_t u_cols, int64_t *__restrict__ tok, int64_t *__restrict__ run, int64_t *__restrict__ pos,
-    const int64_t *__restrict__ plen, const int64_t *__restrict__ rope_off, int64_t *__restrict__ out,
-    int64_t out_stride, int64_t out_cols, int32_t *__restrict__ pos32, int32_t *__restrict__ seqlens,
-    int32_t *__restrict__ rpos32, float *__restrict__ logp_out, int V, int eos, int pad) {
+    const int64_t *__restrict__ plen, const int64_t *__restrict__ rope_off, const int64_t *__restrict__ cache_base,
+    int64_t *__restrict__ out, int64_t out_stride, int64_t out_cols, int32_t *__restrict__ pos32,
+    int32_t *__restrict__ seqlens, int32_t *__restrict__ rpos32, float *__restrict__ logp_out, int V, int eos, int pad) {
   __shared__ float z[SEL_MAXV];
   __shared__ float red_v[SEL_THREADS / 64];
   __shared__ int red_i[SEL_THREADS / 64];
@@ -169,8 +169,10 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
   tok[b] = nxt;
   const int64_t np = p + 1;
   pos[b] = np;
-  if (pos32) pos32[b] = static_cast<int32_t>(np);
-  if (seqlens) seqlens[b] = static_cast<int32_t>(np + 1);
+  // cache_base: the KV-cache row of position p is p - cache_base[b] (a per-sequence suffix cache)
+  const int64_t cp = np - (cache_base ? cache_base[b] : 0);
+  if (pos32) pos32[b] = static_cast<int32_t>(cp);
+  if (seqlens) seqlens[b] = static_cast<int32_t>(cp + 1);
   if (rpos32) rpos32[b] = static_cast<int32_t>(np + (rope_off ? rope_off[b] : 0));
 }
 
@@ -183,7 +185,7 @@ extern "C" int vk_select_update(const float *logits, const void *h, const void *
                                 const float *bias, const uint8_t *is_tail, const uint8_t *is_homo, int32_t homo_stop,
                                 float temperature, const float *uniforms, int64_t u_stride, int64_t u_cols,
                                 int64_t *tok, int64_t *run, int64_t *pos, const int64_t *plen, const int64_t *rope_off,
-                                int64_t *out, int64_t out_stride, int64_t out_cols, int32_t *pos32, int32_t *seqlens,
+                                const int64_t *cache_base, int64_t *out, int64_t out_stride, int64_t out_cols, int32_t *pos32, int32_t *seqlens,
                                 int32_t *rpos32, float *logp_out, int64_t B, int32_t V, int32_t eos, int32_t pad,
                                 void *stream) {
   VK_CHECK_ARG(bias && is_tail && is_homo && tok && pos && out, "select_update: null pointer");
@@ -201,7 +203,8 @@ extern "C" int vk_select_update(const float *logits, const void *h, const void *
   select_update_kernel<<<static_cast<unsigned>(B), SEL_THREADS, 0, VK_STREAM(stream)>>>(
       logits, static_cast<const bf16_t *>(h), static_cast<const bf16_t *>(norm_w), eps,
       static_cast<const bf16_t *>(w_head), d, round_bf16, bias, is_tail,
-      is_homo, homo_stop, temperature, uniforms, u_stride, u_cols, tok, run, pos, plen, rope_off, out, out_stride,
+      is_homo, homo_stop, temperature, uniforms, u_stride, u_cols, tok, run, pos, plen, rope_off, cache_base, out,
+      out_stride,
       out_cols, pos32, seqlens, rpos32, logp_out, V, eos, pad);
   return launch_status("select_update");
 }

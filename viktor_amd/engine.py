@@ -11,6 +11,13 @@ Sampling (temperature > 0) draws each token from softmax(logits / T) by the inve
 per (sequence, output column): `uniforms` [B, max_new_tokens]. The reference draws Gumbel noise from the
 device RNG inside its graph (viktor/engine.py:80-83); here the engine fills the uniforms from the torch
 RNG at prefill unless the caller supplied them (set_uniforms), which makes a rollout reproducible.
+
+group_size = G > 1 (GSPO rollouts: each window repeated G times, scripts/gspo.py:444): consecutive groups
+of G sequences must have identical prefixes (checked at prefill). The engine then prefills each window
+once into a prefix cache [L, B / G, max_frames + 1, Hkv, D] and keeps only the sampled tokens per sequence
+in `cache` [L, B, max_new_tokens, Hkv, D]; decode attention reads each prefix row once per group. Token
+streams are those of the ungrouped engine up to the attention's summation order (prefix and suffix are
+reduced separately, then merged).
 """
 
 import torch
@@ -25,7 +32,7 @@ from .tokenizer import BOS, EOS, PAD
 class DecodeEngine:
     def __init__(self, model, batch_size: int, max_new_tokens: int, max_frames: int, backend: str = "auto",
                  cuda_graph: bool = True, prefill_batch: int = 128, check_every: int = 32,
-                 attention_backend: str = "auto", temperature: float = 0.0, max_homopolymer=64):
+                 attention_backend: str = "auto", temperature: float = 0.0, max_homopolymer=64, group_size: int = 1):
         self.model, self.dec = model, model.decoder
         self.temperature = float(temperature)
         dev = self.dec.lm_head.weight.device
@@ -45,7 +52,18 @@ class DecodeEngine:
         max_len = max_frames + 1 + max_new_tokens
         assert max_len <= self.dec.cfg.max_seq_len
         self.max_frames = max_frames
-        self.cache = KVCache(self.dec.cfg, batch_size, max_len, self.dtype, dev)
+        self.G = int(group_size)
+        assert self.G >= 1 and batch_size % self.G == 0, "batch_size must be a multiple of group_size"
+        if self.G == 1:
+            self.cache = KVCache(self.dec.cfg, batch_size, max_len, self.dtype, dev)
+            self.prefix_cache = None
+        else:
+            self.prefix_cache = KVCache(self.dec.cfg, batch_size // self.G, max_frames + 1, self.dtype, dev)
+            self.cache = KVCache(self.dec.cfg, batch_size, max(max_new_tokens, 2), self.dtype, dev)
+            self.prefix_len32 = torch.ones(batch_size // self.G, dtype=torch.int32, device=dev)
+            self.cache_base = torch.zeros(batch_size, dtype=torch.long, device=dev)  # own-token row = pos - base
+            self.grouped_workspace = ops.decode_attention_grouped_workspace(batch_size, self.G, max_frames + 1,
+                                                                            self.cache.max_len, dev)
 
         self.tok = torch.full((batch_size,), BOS, dtype=torch.long, device=dev)
         self.pos = torch.zeros(batch_size, dtype=torch.long, device=dev)
@@ -68,7 +86,8 @@ class DecodeEngine:
         self.plen = torch.zeros(batch_size, dtype=torch.long, device=dev)  # output column = pos - plen
         self.uniforms = torch.zeros(batch_size, max_new_tokens, dtype=torch.float32, device=dev)
         self._uniforms_set = False
-        self.fast.decode_workspace = ops.decode_attention_workspace(batch_size, self.dec.cfg.n_heads, max_len, dev)
+        self.fast.decode_workspace = ops.decode_attention_workspace(batch_size, self.dec.cfg.n_heads,
+                                                                    self.cache.max_len, dev)
         self.graph = None
         if cuda_graph:
             self._capture()
@@ -78,12 +97,18 @@ class DecodeEngine:
         # layers on the fused small-M kernels; the LM-head kernel applies the final norm, chooses the token
         # (greedy from fp32 logits, sampled from bf16 logits: the reference's two step kinds) and advances
         # the state. step_idx is advanced on the host after the replays (it is not read inside a step).
-        x = self.fast.decode_residual(self.pos32, self.rows, self.seqlens, self.cache,
-                                      rope_pos=None if self.pos_scale == 1 else self.rpos32, tok=self.tok)
+        if self.G == 1:
+            x = self.fast.decode_residual(self.pos32, self.rows, self.seqlens, self.cache,
+                                          rope_pos=None if self.pos_scale == 1 else self.rpos32, tok=self.tok)
+        else:  # pos32 / seqlens index the own-token cache; RoPE runs at the absolute position rpos32
+            x = self.fast.decode_residual(self.pos32, self.rows, self.seqlens, self.cache, rope_pos=self.rpos32,
+                                          tok=self.tok, prefix=(self.prefix_cache, self.prefix_len32, self.G,
+                                                                self.grouped_workspace))
         ops.select_update(self.bias, self.is_tail, self.is_homo, self.homo_stop, self.tok, self.run, self.pos,
                           self.plen, self.rope_off, self.out, self.pos32, self.seqlens, self.rpos32, EOS, PAD,
                           h=x, norm_w=self.dec.norm.weight, eps=self.dec.cfg.norm_eps, w_head=self.dec.lm_head.weight,
-                          round_bf16=self.temperature > 0, temperature=self.temperature, uniforms=self.uniforms)
+                          round_bf16=self.temperature > 0, temperature=self.temperature, uniforms=self.uniforms,
+                          cache_base=None if self.G == 1 else self.cache_base)
 
     def _reset_state(self):
         self.pos.fill_(1)
@@ -109,15 +134,15 @@ class DecodeEngine:
         self.out.fill_(PAD)
 
     # ---- prefill -------------------------------------------------------------------------------
-    def _prefill_hip(self, prefix, lens, row0):
-        """prefix [sum(lens), d] projected frames of sequences row0.. ; returns the final hidden at each BOS."""
+    def _prefill_hip(self, prefix, lens, row0, cache):
+        """prefix [sum(lens), d] projected frames of cache rows row0.. ; returns the final hidden at each BOS."""
         dev = prefix.device
         n = len(lens)
         key = tuple(lens)
         entry = self._prefill_plans.get(row0)
         if entry is None or entry[0] != key:
             seq_lens = [L + 1 for L in lens]
-            plan = PrefillPlan(seq_lens, dev, rows=list(range(row0, row0 + n)), keep=[1] * n, cache=self.cache)
+            plan = PrefillPlan(seq_lens, dev, rows=list(range(row0, row0 + n)), keep=[1] * n, cache=cache)
             L = torch.tensor(lens, device=dev)
             total, frames = plan.total, sum(lens)
             cu = torch.tensor(plan.cu, dtype=torch.int32, device=dev)
@@ -135,7 +160,7 @@ class DecodeEngine:
         x = torch.empty(plan.total, prefix.shape[1], dtype=self.dtype, device=dev)
         x[frame_idx] = prefix
         x[last] = self.dec.embed.weight[BOS].to(self.dtype)
-        return self.fast.prefill(x, pos, seq, None, plan.max_len, self.cache, rope_pos=rpos, plan=plan)
+        return self.fast.prefill(x, pos, seq, None, plan.max_len, cache, rope_pos=rpos, plan=plan)
 
     def set_uniforms(self, u):
         """Uniforms [B, max_new_tokens] in [0, 1) driving the sampled tokens (column j -> output token j)."""
@@ -157,23 +182,64 @@ class DecodeEngine:
         offs = [0]
         for n in frame_lens:
             offs.append(offs[-1] + n)
+        G = self.G
+        if G > 1:  # one prefill per window: the first sequence of every group
+            self._check_groups(frames, frame_lens, offs)
+            lens_p = frame_lens[::G]
+            if len(set(frame_lens)) == 1:
+                n = frame_lens[0]
+                frames_p = frames.view(self.B // G, G, n, -1)[:, 0].reshape(-1, frames.shape[1])
+            else:
+                frames_p = torch.cat([frames[offs[b]:offs[b + 1]] for b in range(0, self.B, G)])
+            offs_p = [0]
+            for n in lens_p:
+                offs_p.append(offs_p[-1] + n)
+            cache, n_rows = self.prefix_cache, len(lens_p)
+        else:
+            frames_p, lens_p, offs_p, cache, n_rows = frames, frame_lens, offs, self.cache, self.B
         last = []
-        for lo in range(0, self.B, self.prefill_batch):
-            hi = min(self.B, lo + self.prefill_batch)
-            prefix = self.model.projector(frames[offs[lo]:offs[hi]].to(self.dtype))
-            last.append(self._prefill_hip(prefix, frame_lens[lo:hi], lo))
+        for lo in range(0, n_rows, self.prefill_batch):
+            hi = min(n_rows, lo + self.prefill_batch)
+            prefix = self.model.projector(frames_p[offs_p[lo]:offs_p[hi]].to(self.dtype))
+            last.append(self._prefill_hip(prefix, lens_p[lo:hi], lo, cache))
         h = torch.cat(last) if len(last) > 1 else last[0]
+        if G > 1:
+            h = h.repeat_interleave(G, 0)
+            self.prefix_len32.copy_(torch.tensor([n + 1 for n in lens_p], dtype=torch.int32, device=h.device))
         self.tok.fill_(BOS)
         self.run.zero_()
         self.out.fill_(PAD)
         self.plen.copy_(torch.tensor(frame_lens, device=self.pos.device))
         self.pos.copy_(self.plen)  # the select kernel writes column pos - plen = 0, then advances pos to plen + 1
+        if G > 1:
+            self.cache_base.copy_(self.plen + 1)  # the first sampled token goes to own-token row 0
         self.rope_off.copy_(self.plen * (self.pos_scale - 1))
         ops.select_update(self.bias, self.is_tail, self.is_homo, self.homo_stop, self.tok, self.run, self.pos,
                           self.plen, self.rope_off, self.out, self.pos32, self.seqlens, self.rpos32, EOS, PAD,
                           h=h.contiguous(), w_head=self.dec.lm_head.weight, round_bf16=True,
-                          temperature=self.temperature, uniforms=self.uniforms)
+                          temperature=self.temperature, uniforms=self.uniforms,
+                          cache_base=None if G == 1 else self.cache_base)
         self.step_idx.fill_(1)
+
+    def _check_groups(self, frames, frame_lens, offs):
+        """Every group of G consecutive sequences must carry the same prefix (lengths and frames)."""
+        G = self.G
+        for b in range(0, self.B, G):
+            if any(frame_lens[b + m] != frame_lens[b] for m in range(G)):
+                raise ValueError(f"group_size={G}: sequences {b}..{b + G - 1} have different prefix lengths")
+        if len(set(frame_lens)) == 1:  # equal lengths: compare each group against its first member in place
+            f = frames.view(self.B // G, G, frame_lens[0], -1)
+            if not torch.equal(f[:, 1:], f[:, :1].expand(-1, G - 1, -1, -1)):
+                raise ValueError(f"group_size={G}: the sequences of a group must share their prefix frames")
+            return
+        dev = frames.device
+        lens = torch.tensor(frame_lens, device=dev)
+        rows = torch.repeat_interleave(torch.arange(self.B, device=dev), lens, output_size=frames.shape[0])
+        start = torch.tensor(offs[:-1], device=dev)
+        lead = torch.div(rows, G, rounding_mode="floor") * G  # first sequence of the row's group
+        src = start[lead] + torch.arange(frames.shape[0], device=dev) - start[rows]
+        if not torch.equal(frames, frames[src]):
+            raise ValueError(f"group_size={G}: the sequences of a group must share their prefix frames")
 
     @torch.no_grad()
     def decode(self, steps=None):

@@ -200,13 +200,16 @@ class FastDecoder:
         xr = self.decode_residual(pos, seq, cache_seqlens, cache, rope_pos=rope_pos, tok=tok, x=x)
         return ops.add_rmsnorm(xr, self.w(self.dec.norm.weight), self.cfg.norm_eps)
 
-    def decode_residual(self, pos, seq, cache_seqlens, cache, rope_pos=None, tok=None, x=None):
+    def decode_residual(self, pos, seq, cache_seqlens, cache, rope_pos=None, tok=None, x=None, prefix=None):
         """The decoder layers of one decode step on the fused small-M kernels, five launches per layer:
           norm_qkv_rope_cache (attn norm + qkv GEMM + QK-norm + RoPE + cache write; layer 0 also gathers the
           token embeddings), decode_attention, linear_residual (o proj + residual add), norm_linear
           (mlp norm + gate_up + SwiGLU), linear_residual (down proj + residual add).
         Returns the residual stream [B, d] after the last layer (x, updated in place, when given); the
-        final RMSNorm is left to the consumer (the LM-head kernel applies it)."""
+        final RMSNorm is left to the consumer (the LM-head kernel applies it).
+        prefix = (prefix_cache, prefix_len32, G, workspace): groups of G consecutive sequences share the
+        prefix rows [0, prefix_len32[b // G]) of prefix_cache; `cache` then holds each sequence's own tokens
+        (pos / cache_seqlens index it) and attention runs over prefix + own rows."""
         cfg, W, layers = self.cfg, self.w, self.dec.layers
         eps = cfg.norm_eps
         H, HKV, D = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
@@ -230,7 +233,11 @@ class FastDecoder:
             else:
                 q = ops.norm_qkv_rope_cache(xr, W(blk.attn_norm.weight), eps, W(a.qkv_proj.weight), W(a.q_norm.weight),
                                             W(a.k_norm.weight), cos, sin, pos, seq, kc, vc, H, HKV, D, rope_pos=rope_pos)
-            o = ops.decode_attention(q, kc, vc, cache_seqlens, workspace=ws)
+            if prefix is None:
+                o = ops.decode_attention(q, kc, vc, cache_seqlens, workspace=ws)
+            else:
+                pc, plen32, G, gws = prefix
+                o = ops.decode_attention_grouped(q, pc.k[i], pc.v[i], plen32, kc, vc, cache_seqlens, G, workspace=gws)
             ops.linear_residual(o.view(B, H * D), W(a.o_proj.weight), xr)
             g = ops.norm_linear(xr, W(blk.mlp_norm.weight), eps, W(blk.gate_up.weight), swiglu=True)
             ops.linear_residual(g, W(blk.down.weight), xr)

@@ -167,6 +167,39 @@ def decode_attention(q, k, v, lengths, block=64, workspace=None):
     return out
 
 
+def decode_attention_grouped_workspace(B, G, pre_max, suf_max, device):
+    nbytes = ctypes.c_int64(0)
+    _lib.check(_lib.load().vk_decode_attention_grouped_workspace(B, G, pre_max, suf_max, ctypes.byref(nbytes)),
+               "decode_attention_grouped_workspace")
+    return torch.empty(nbytes.value, dtype=torch.uint8, device=device)
+
+
+def decode_attention_grouped(q, k_prefix, v_prefix, prefix_len, k_suffix, v_suffix, suffix_len, group_size,
+                             workspace=None):
+    """Decode attention of B = P * G sequences whose groups of G consecutive rows share a prefix: sequence b
+    attends to prefix rows [0, prefix_len[b // G]) of k/v_prefix [P, S_pre, 2, 64] then to its own rows
+    [0, suffix_len[b]) of k/v_suffix [B, S_suf, 2, 64]. Returns [B, 8, 64] bf16 (each prefix row is read once
+    per group)."""
+    require_device(q, "decode_attention_grouped")
+    B, H, D = q.shape
+    G = int(group_size)
+    _require(q.is_contiguous() and q.dtype == BF16 and H == 8 and D == 64, "decode_attention_grouped: q")
+    _require(B % G == 0 and k_prefix.shape[0] == B // G and k_suffix.shape[0] == B, "decode_attention_grouped: batch")
+    for a, b in ((k_prefix, v_prefix), (k_suffix, v_suffix)):
+        _require(a.stride() == b.stride() and a.stride(-1) == 1 and a.stride(-2) == D and a.dtype == b.dtype == BF16,
+                 "decode_attention_grouped: cache layout")
+    _require(prefix_len.dtype == torch.int32 and prefix_len.shape == (B // G,) and suffix_len.dtype == torch.int32
+             and suffix_len.shape == (B,), "decode_attention_grouped: lengths int32")
+    if workspace is None:
+        workspace = decode_attention_grouped_workspace(B, G, k_prefix.shape[1], k_suffix.shape[1], q.device)
+    out = torch.empty_like(q)
+    call("vk_decode_attention_grouped", ptr(q), ptr(k_prefix), ptr(v_prefix), ptr(prefix_len), k_prefix.stride(0),
+         k_prefix.stride(1), k_prefix.shape[1], ptr(k_suffix), ptr(v_suffix), ptr(suffix_len), k_suffix.stride(0),
+         k_suffix.stride(1), k_suffix.shape[1], ptr(out), B, G, H, k_prefix.shape[2], D, ptr(workspace),
+         workspace.numel(), stream_handle())
+    return out
+
+
 class AttentionPlan:
     """Host-built work list of vk_varlen_attention: one (sequence, first query row) entry per 64-query
     block, ordered by decreasing key count so the longest blocks start first. Device tensors."""
@@ -219,7 +252,7 @@ def varlen_attention(q, k, v, plan: AttentionPlan, stride_tok=None, out=None):
 
 def select_update(bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_off, out, pos32, seqlens, rpos32, eos,
                   pad, logits=None, h=None, w_head=None, round_bf16=False, temperature=0.0, uniforms=None,
-                  logp_out=None, norm_w=None, eps=1e-6):
+                  logp_out=None, norm_w=None, eps=1e-6, cache_base=None):
     """One step's token choice + state update for every sequence (fused LM head when h, w_head are given;
     with norm_w, h is the residual stream and the final RMSNorm runs first). See vk_select_update in
     include/viktor_hip.h for the exact rule order."""
@@ -235,6 +268,7 @@ def select_update(bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_o
                  and w_head.dtype == BF16 and _contig(h, w_head), "select_update: h / w_head")
         d = h.shape[1]
     for t, dt in ((tok, torch.long), (pos, torch.long), (run, torch.long), (plen, torch.long), (rope_off, torch.long),
+                  (cache_base, torch.long),
                   (pos32, torch.int32), (seqlens, torch.int32), (rpos32, torch.int32)):
         _require(t is None or (t.dtype == dt and t.shape == (B,) and t.is_contiguous()), "select_update: state tensors")
     _require(out.dim() == 2 and out.shape[0] == B and out.dtype == torch.long and out.stride(1) == 1, "select_update: out")
@@ -247,7 +281,7 @@ def select_update(bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_o
     call("vk_select_update", ptr(logits), ptr(h), ptr(norm_w), float(eps), ptr(w_head), d, int(bool(round_bf16)),
          ptr(bias), ptr(is_tail),
          ptr(is_homo), int(homo_stop), float(temperature), ptr(uniforms), us, uc, ptr(tok), ptr(run), ptr(pos), ptr(plen),
-         ptr(rope_off), ptr(out), out.stride(0), out.shape[1], ptr(pos32), ptr(seqlens), ptr(rpos32), ptr(logp_out), B, V,
+         ptr(rope_off), ptr(cache_base), ptr(out), out.stride(0), out.shape[1], ptr(pos32), ptr(seqlens), ptr(rpos32), ptr(logp_out), B, V,
          int(eos), int(pad), stream_handle())
 
 
