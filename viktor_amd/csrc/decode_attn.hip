@@ -280,37 +280,61 @@ static int device_cus_cached() {
 // ---- groups of sequences that share one prefix (GSPO: G samples of one window) ----------------------
 //
 // A sequence of group p attends to the group's prefix rows (frames + BOS, one copy in the prefix cache
-// [P, S_pre, 2, 64]) followed by its own suffix rows (sampled tokens, suffix cache [B, S_suf, 2, 64]).
-// Prefix: one workgroup per (chunk of prefix rows, group, KV head); its query columns are the 4 heads
-// of that KV head for all G members (4 G columns), so each 128-byte K / V row of the prefix is fetched
-// once for the whole group. Suffix: the single-sequence kernel above, writing partials. Combine: merges
-// prefix-chunk and suffix-split partials of each (sequence, head).
+// [P, S_pre, 2, 64]) followed by its own rows (sampled tokens, own-row cache [B, S_own, 2, 64]).
+// One launch: a workgroup per (part, group p, KV head). Its query columns are the 4 heads of that KV head
+// for all G members (4 G columns), and it walks one tile space: the prefix tiles (every column attends),
+// then the own-row tiles of members 0..G-1 (only that member's 4 columns attend; the others are masked).
+// The tile space is cut into `nparts` equal parts, so every wave runs a long software-pipelined loop and
+// prefix rows are fetched once per group. Each part leaves a partial (max, sum, unnormalised output) per
+// column; a small combine kernel merges the parts of each (sequence, head).
 
-constexpr int GP_WAVES = 8;
-constexpr int GP_TILE = 32;
-constexpr int GP_PITCH = 72;  // one KV head: 64 + 8 pad
-constexpr int GP_CHUNK_TILES = 16;
+constexpr int GU_WAVES = 4;
+#ifndef VK_GU_WG_PER_CU
+#define VK_GU_WG_PER_CU 2  // workgroups per CU the part count aims for (one resident round)
+#endif
+constexpr int GU_TILE = 32;
+constexpr int GU_PITCH = 72;  // one KV head: 64 + 8 pad
 
 template <int G>
-__global__ __launch_bounds__(GP_WAVES * 64) void prefix_attn_kernel(
+__global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ kp, const bf16_t *__restrict__ vp,
-    const int32_t *__restrict__ pre_len, int64_t stride_pb, int64_t stride_ps, int64_t pre_max, int n_chunks,
-    float *__restrict__ ws_o, float *__restrict__ ws_ml, float scale_log2) {
+    const int32_t *__restrict__ pre_len, int64_t stride_pb, int64_t stride_ps, int64_t pre_max,
+    const bf16_t *__restrict__ ks, const bf16_t *__restrict__ vs, const int32_t *__restrict__ own_len,
+    int64_t stride_sb, int64_t stride_ss, int64_t own_max, int nparts, float *__restrict__ ws_o,
+    float *__restrict__ ws_ml, float scale_log2) {
   constexpr int NC = 4 * G;            // query columns of one KV head (G members x 4 heads)
   constexpr int NCB = (NC + 15) / 16;  // 16-column MFMA blocks
-  constexpr int LDS_V = GP_WAVES * GP_TILE * GP_PITCH * 2;
-  constexpr int LDS_M = (GP_WAVES * NC * 64 + 2 * GP_WAVES * NC) * 4;
+  constexpr int LDS_V = GU_WAVES * GU_TILE * GU_PITCH * 2;
+  constexpr int LDS_M = (GU_WAVES * NC * 64 + 2 * GU_WAVES * NC) * 4;
   __shared__ __attribute__((aligned(16))) char smem[LDS_V > LDS_M ? LDS_V : LDS_M];
+  __shared__ int seg_end[G + 1];  // cumulative tile counts: segment 0 = prefix, 1 + m = member m's own rows
+  __shared__ int seg_len[G + 1];
 
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int chunk = blockIdx.x, p = blockIdx.y, kvh = blockIdx.z;
-  int64_t len = pre_len[p];
-  len = len < 1 ? 1 : (len > pre_max ? pre_max : len);
-  const int ntiles = static_cast<int>((len + GP_TILE - 1) / GP_TILE);
-  const int t_begin = chunk * GP_CHUNK_TILES;
-  const int t_end = min(t_begin + GP_CHUNK_TILES, ntiles);
-  if (t_begin >= t_end) return;
+  // wave-uniform values go through readfirstlane so the tile loop and segment search stay scalar
+  const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int part = blockIdx.x, p = blockIdx.y, kvh = blockIdx.z;
   const int col = lane & 15, g = lane >> 4;
+
+  if (wid == 0) {
+    int64_t len = 0;
+    if (lane == 0) {
+      len = pre_len[p];
+      len = len < 1 ? 1 : (len > pre_max ? pre_max : len);
+    } else if (lane <= G) {
+      len = own_len[static_cast<int64_t>(p) * G + lane - 1];
+      len = len < 0 ? 0 : (len > own_max ? own_max : len);
+    }
+    int incl = static_cast<int>((len + GU_TILE - 1) / GU_TILE);
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) {
+      const int v = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += v;
+    }
+    if (lane <= G) {
+      seg_end[lane] = incl;
+      seg_len[lane] = static_cast<int>(len);
+    }
+  }
 
   // Q^T fragments: column j = 16 cb + col -> member j / 4, head kvh * 4 + j % 4, the two 32-wide halves of D
   bf16x8 bq[NCB][2];
@@ -328,107 +352,135 @@ __global__ __launch_bounds__(GP_WAVES * 64) void prefix_attn_kernel(
     }
   }
   f32x4 acc[NCB][4];
-#pragma unroll
-  for (int cb = 0; cb < NCB; ++cb)
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) acc[cb][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run[NCB], l_run[NCB];
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc[cb][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     m_run[cb] = -INFINITY;
     l_run[cb] = 0.f;
   }
-  const bf16_t *kb = kp + p * stride_pb + kvh * DA_D;
-  const bf16_t *vb = vp + p * stride_pb + kvh * DA_D;
-  bf16_t *vs = reinterpret_cast<bf16_t *>(smem) + wid * GP_TILE * GP_PITCH;
+  __syncthreads();
+  const int T = __builtin_amdgcn_readfirstlane(seg_end[G]);
+  const int t_begin = static_cast<int>(static_cast<int64_t>(T) * part / nparts);
+  const int t_end = static_cast<int>(static_cast<int64_t>(T) * (part + 1) / nparts);
+  bf16_t *vsh = reinterpret_cast<bf16_t *>(smem) + wid * GU_TILE * GU_PITCH;
 
+  // tile t -> segment (monotone search from the previous segment), first row, row count, row pointers
+  struct TileRef {
+    const bf16_t *k, *v;
+    int64_t stride;
+    int row0, len, seg;
+  };
+  auto locate = [&](int t, int s) {
+    while (t >= __builtin_amdgcn_readfirstlane(seg_end[s])) ++s;
+    TileRef r;
+    r.seg = s;
+    r.row0 = (t - (s ? __builtin_amdgcn_readfirstlane(seg_end[s - 1]) : 0)) * GU_TILE;
+    r.len = __builtin_amdgcn_readfirstlane(seg_len[s]);
+    if (s == 0) {
+      r.k = kp + p * stride_pb + kvh * DA_D;
+      r.v = vp + p * stride_pb + kvh * DA_D;
+      r.stride = stride_ps;
+    } else {
+      const int64_t b = static_cast<int64_t>(p) * G + s - 1;
+      r.k = ks + b * stride_sb + kvh * DA_D;
+      r.v = vs + b * stride_sb + kvh * DA_D;
+      r.stride = stride_ss;
+    }
+    return r;
+  };
+  auto row_off = [&](const TileRef &r, int pb) {
+    int rr = r.row0 + 16 * pb + col;
+    rr = rr < r.len ? rr : r.len - 1;
+    return static_cast<int64_t>(rr) * r.stride + 8 * g;
+  };
   u32x4 kf[2][2], vf[2][2];
-  auto row_ptr = [&](const bf16_t *base, int tt, int pb) {
-    int64_t r = static_cast<int64_t>(tt) * GP_TILE + 16 * pb + col;
-    r = r < len ? r : len - 1;
-    return base + r * stride_ps + 8 * g;
-  };
-  auto load_k = [&](int tt) {
+  auto load = [&](u32x4 (&f)[2][2], const bf16_t *base, const TileRef &r) {
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) kf[pb][c] = *reinterpret_cast<const u32x4 *>(row_ptr(kb, tt, pb) + 32 * c);
+      for (int c = 0; c < 2; ++c) f[pb][c] = *reinterpret_cast<const u32x4 *>(base + row_off(r, pb) + 32 * c);
   };
-  auto load_v = [&](int tt) {
-#pragma unroll
-    for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-      for (int c = 0; c < 2; ++c) vf[pb][c] = *reinterpret_cast<const u32x4 *>(row_ptr(vb, tt, pb) + 32 * c);
-  };
-  const int t_first = min(t_begin + wid, t_end - 1);
-  load_k(t_first);
-  asm volatile("" ::: "memory");
-  load_v(t_first);
-  for (int t = t_begin + wid; t < t_end; t += GP_WAVES) {
-    const int64_t p0 = static_cast<int64_t>(t) * GP_TILE;
-    const int tn = t + GP_WAVES < t_end ? t + GP_WAVES : t;
-    f32x4 st[2][NCB];
-#pragma unroll
-    for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-      for (int cb = 0; cb < NCB; ++cb) {
-        st[pb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-          st[pb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[pb][c]), bq[cb][c],
-                                                               st[pb][cb], 0, 0, 0);
-      }
-    load_k(tn);
-    bf16x8 pf[NCB];
-#pragma unroll
-    for (int cb = 0; cb < NCB; ++cb) {
-      float sv[8];
-      float mx = -INFINITY;
+
+  // This wave's tiles are t0, t0 + W, ... (< t_end). The next tile's K / V are loaded while the current
+  // one is consumed; at the end the current tile is loaded again, so every load is unconditional.
+  const int t0 = t_begin + wid;
+  if (t0 < t_end) {
+    TileRef cur = locate(t0, 0);
+    load(kf, cur.k, cur);
+    asm volatile("" ::: "memory");
+    load(vf, cur.v, cur);
+    for (int t = t0; t < t_end; t += GU_WAVES) {
+      const int tn = t + GU_WAVES < t_end ? t + GU_WAVES : t;
+      const TileRef nxt = locate(tn, cur.seg);
+      f32x4 st[2][NCB];
 #pragma unroll
       for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int64_t r = p0 + 16 * pb + 4 * g + i;
-          const float v = r < len ? st[pb][cb][i] * scale_log2 : -INFINITY;
-          sv[pb * 4 + i] = v;
-          mx = fmaxf(mx, v);
+        for (int cb = 0; cb < NCB; ++cb) {
+          st[pb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < 2; ++c)
+            st[pb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[pb][c]), bq[cb][c],
+                                                                 st[pb][cb], 0, 0, 0);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run[cb], mx);
-      const float alpha = exp2f(m_run[cb] - m_new);
-      float ps = 0.f;
+      load(kf, nxt.k, nxt);
+      const int member = cur.seg - 1;  // -1: prefix tile, every column attends
+      bf16x8 pf[NCB];
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const float e = exp2f(sv[jj] - m_new);
-        ps += e;
-        pf[cb][jj] = __builtin_bit_cast(__bf16, f2bf(e));
+      for (int cb = 0; cb < NCB; ++cb) {
+        const bool col_ok = member < 0 || ((16 * cb + col) >> 2) == member;
+        float sv[8];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = cur.row0 + 16 * pb + 4 * g + i;
+            const float v = (col_ok && r < cur.len) ? st[pb][cb][i] * scale_log2 : -INFINITY;
+            sv[pb * 4 + i] = v;
+            mx = fmaxf(mx, v);
+          }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run[cb], mx);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a column with no row yet stays empty
+        const float alpha = exp2f(m_run[cb] - m_use);
+        float ps = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const float e = exp2f(sv[jj] - m_use);
+          ps += e;
+          pf[cb][jj] = __builtin_bit_cast(__bf16, f2bf(e));
+        }
+        l_run[cb] = l_run[cb] * alpha + ps;
+        m_run[cb] = m_new;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) acc[cb][dt] *= alpha;
       }
-      l_run[cb] = l_run[cb] * alpha + ps;
-      m_run[cb] = m_new;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) acc[cb][dt] *= alpha;
-    }
+      for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-    for (int pb = 0; pb < 2; ++pb)
+        for (int c = 0; c < 2; ++c)
+          *reinterpret_cast<u32x4 *>(&vsh[(16 * pb + col) * GU_PITCH + 32 * c + 8 * g]) = vf[pb][c];
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      load(vf, nxt.v, nxt);
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-        *reinterpret_cast<u32x4 *>(&vs[(16 * pb + col) * GP_PITCH + 32 * c + 8 * g]) = vf[pb][c];
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    load_v(tn);
+      for (int dt = 0; dt < 4; ++dt) {
+        bf16x8 va;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      bf16x8 va;
+        for (int jj = 0; jj < 8; ++jj) {
+          const int pl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
+          va[jj] = __builtin_bit_cast(__bf16, vsh[pl * GU_PITCH + 16 * dt + col]);
+        }
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const int pl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
-        va[jj] = __builtin_bit_cast(__bf16, vs[pl * GP_PITCH + 16 * dt + col]);
+        for (int cb = 0; cb < NCB; ++cb)
+          acc[cb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[cb], acc[cb][dt], 0, 0, 0);
       }
-#pragma unroll
-      for (int cb = 0; cb < NCB; ++cb)
-        acc[cb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[cb], acc[cb][dt], 0, 0, 0);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      cur = nxt;
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
@@ -437,8 +489,8 @@ __global__ __launch_bounds__(GP_WAVES * 64) void prefix_attn_kernel(
   }
   __syncthreads();
   float *Os = reinterpret_cast<float *>(smem);  // [WAVES][NC][64]
-  float *Ms = Os + GP_WAVES * NC * 64;           // [WAVES][NC]
-  float *Ls = Ms + GP_WAVES * NC;
+  float *Ms = Os + GU_WAVES * NC * 64;           // [WAVES][NC]
+  float *Ls = Ms + GU_WAVES * NC;
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
     const int j = 16 * cb + col;
@@ -454,20 +506,22 @@ __global__ __launch_bounds__(GP_WAVES * 64) void prefix_attn_kernel(
     }
   }
   __syncthreads();
-  for (int o = threadIdx.x; o < NC * 64; o += GP_WAVES * 64) {
+  // partial of (group p, KV head, part, column j); a column no row of this part reaches: (-inf, 0, 0)
+  for (int o = threadIdx.x; o < NC * 64; o += GU_WAVES * 64) {
     const int j = o / 64, d = o % 64;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < GP_WAVES; ++w) M = fmaxf(M, Ms[w * NC + j]);
+    for (int w = 0; w < GU_WAVES; ++w) M = fmaxf(M, Ms[w * NC + j]);
     float L = 0.f, N = 0.f;
+    if (M != -INFINITY) {
 #pragma unroll
-    for (int w = 0; w < GP_WAVES; ++w) {
-      const float e = exp2f(Ms[w * NC + j] - M);
-      L += e * Ls[w * NC + j];
-      N += e * Os[(w * NC + j) * 64 + d];
+      for (int w = 0; w < GU_WAVES; ++w) {
+        const float e = exp2f(Ms[w * NC + j] - M);
+        L += e * Ls[w * NC + j];
+        N += e * Os[(w * NC + j) * 64 + d];
+      }
     }
-    // partial of (group p, chunk, member j / 4, head kvh * 4 + j % 4)
-    const int64_t base = ((static_cast<int64_t>(p) * n_chunks + chunk) * G + j / 4) * DA_H + kvh * 4 + (j & 3);
+    const int64_t base = ((static_cast<int64_t>(p) * DA_HKV + kvh) * nparts + part) * NC + j;
     ws_o[base * DA_D + d] = N;
     if (d == 0) {
       ws_ml[base * 2] = M;
@@ -476,67 +530,66 @@ __global__ __launch_bounds__(GP_WAVES * 64) void prefix_attn_kernel(
   }
 }
 
-// out[b, h] = merge of the prefix-chunk partials of b's group and the suffix-split partials of b
-__global__ __launch_bounds__(DA_H * DA_D) void grouped_combine_kernel(
-    const float *__restrict__ pre_o, const float *__restrict__ pre_ml, const float *__restrict__ suf_o,
-    const float *__restrict__ suf_ml, const int32_t *__restrict__ pre_len, const int32_t *__restrict__ suf_len,
-    bf16_t *__restrict__ out, int G, int64_t pre_max, int n_chunks, int64_t suf_max, int tps, int nsplit) {
+// out[b, h] = merge of the nparts partials of b's column (member b % G, head h) in its group's KV head
+__global__ __launch_bounds__(DA_H * DA_D) void grouped_combine_kernel(const float *__restrict__ ws_o,
+                                                                      const float *__restrict__ ws_ml,
+                                                                      bf16_t *__restrict__ out, int G, int nparts) {
   const int64_t b = blockIdx.x;
   const int h = threadIdx.x / DA_D, d = threadIdx.x % DA_D;
-  const int64_t p = b / G, member = b % G;
-  int64_t lp = pre_len[p];
-  lp = lp < 1 ? 1 : (lp > pre_max ? pre_max : lp);
-  const int np = min(n_chunks, static_cast<int>((((lp + GP_TILE - 1) / GP_TILE) + GP_CHUNK_TILES - 1) / GP_CHUNK_TILES));
-  int64_t ls = suf_len[b];
-  ls = ls < 1 ? 1 : (ls > suf_max ? suf_max : ls);
-  const int ns = min(nsplit, static_cast<int>((((ls + DA_TILE - 1) / DA_TILE) + tps - 1) / tps));
+  const int64_t p = b / G;
+  const int NC = 4 * G;
+  const int j = 4 * static_cast<int>(b % G) + (h & 3);
+  const int64_t base0 = (p * DA_HKV + (h >> 2)) * nparts * NC + j;
   float M = -INFINITY;
-  for (int c = 0; c < np; ++c) M = fmaxf(M, pre_ml[(((p * n_chunks + c) * G + member) * DA_H + h) * 2]);
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, suf_ml[((b * nsplit + s) * DA_H + h) * 2]);
+  for (int k = 0; k < nparts; ++k) M = fmaxf(M, ws_ml[(base0 + static_cast<int64_t>(k) * NC) * 2]);
   float L = 0.f, N = 0.f;
-  for (int c = 0; c < np; ++c) {
-    const int64_t base = ((p * n_chunks + c) * G + member) * DA_H + h;
-    const float e = exp2f(pre_ml[base * 2] - M);
-    L += e * pre_ml[base * 2 + 1];
-    N += e * pre_o[base * DA_D + d];
-  }
-  for (int s = 0; s < ns; ++s) {
-    const int64_t base = (b * nsplit + s) * DA_H + h;
-    const float e = exp2f(suf_ml[base * 2] - M);
-    L += e * suf_ml[base * 2 + 1];
-    N += e * suf_o[base * DA_D + d];
+  for (int k = 0; k < nparts; ++k) {
+    const int64_t base = base0 + static_cast<int64_t>(k) * NC;
+    const float mk = ws_ml[base * 2];
+    const float e = mk == -INFINITY ? 0.f : exp2f(mk - M);
+    L += e * ws_ml[base * 2 + 1];
+    N += e * ws_o[base * DA_D + d];
   }
   out[(b * DA_H + h) * DA_D + d] = f2bf(N / L);
 }
 
 struct GroupedLayout {
-  int n_chunks;
-  DecodeSplit suf;
-  int64_t pre_o, pre_ml, suf_o, suf_ml, total;  // offsets / size in floats
+  int nparts;
+  int64_t o, ml, total;  // offsets / size in floats
 };
 
-static GroupedLayout grouped_layout(int64_t B, int G, int64_t pre_max, int64_t suf_max, int cus) {
+// Parts per (group, KV head): about VK_GU_WG_PER_CU 4-wave workgroups per CU over the launch, and at least
+// one tile per wave at the longest lengths.
+static GroupedLayout grouped_layout(int64_t B, int G, int64_t pre_max, int64_t own_max, int cus) {
   GroupedLayout L{};
-  const int64_t P = B / G;
-  const int ntiles = static_cast<int>((pre_max + GP_TILE - 1) / GP_TILE);
-  L.n_chunks = (ntiles + GP_CHUNK_TILES - 1) / GP_CHUNK_TILES;
-  // suffix partials always go through the workspace (nsplit >= 1)
-  L.suf = decode_split(B, suf_max, cus);
-  L.pre_o = 0;
-  L.pre_ml = L.pre_o + P * L.n_chunks * G * DA_H * DA_D;
-  L.suf_o = L.pre_ml + P * L.n_chunks * G * DA_H * 2;
-  L.suf_ml = L.suf_o + B * L.suf.nsplit * DA_H * DA_D;
-  L.total = L.suf_ml + B * L.suf.nsplit * DA_H * 2;
+  const int64_t pairs = (B / G) * DA_HKV;
+  const int64_t target = static_cast<int64_t>(cus) * VK_GU_WG_PER_CU;
+  int64_t np = (target + pairs - 1) / pairs;
+  const int64_t tmax = (pre_max + GU_TILE - 1) / GU_TILE + G * ((own_max + GU_TILE - 1) / GU_TILE);
+  const int64_t cap = tmax / GU_WAVES;
+  if (np > cap) np = cap;
+  if (np > 64) np = 64;
+  if (np < 1) np = 1;
+#ifdef VK_GU_NPARTS
+  np = VK_GU_NPARTS;
+#endif
+  L.nparts = static_cast<int>(np);
+  const int64_t cols = pairs * L.nparts * 4 * G;
+  L.o = 0;
+  L.ml = cols * DA_D;
+  L.total = L.ml + cols * 2;
   return L;
 }
 
 template <int G>
-static void launch_prefix(const bf16_t *q, const bf16_t *kp, const bf16_t *vp, const int32_t *pre_len, int64_t P,
-                          int64_t stride_pb, int64_t stride_ps, int64_t pre_max, int n_chunks, float *ws_o,
-                          float *ws_ml, float scale_log2, hipStream_t s) {
-  const dim3 grid(n_chunks, static_cast<unsigned>(P), DA_HKV);
-  prefix_attn_kernel<G><<<grid, GP_WAVES * 64, 0, s>>>(q, kp, vp, pre_len, stride_pb, stride_ps, pre_max, n_chunks,
-                                                       ws_o, ws_ml, scale_log2);
+static void launch_grouped(const bf16_t *q, const bf16_t *kp, const bf16_t *vp, const int32_t *pre_len, int64_t P,
+                           int64_t stride_pb, int64_t stride_ps, int64_t pre_max, const bf16_t *ks, const bf16_t *vs,
+                           const int32_t *own_len, int64_t stride_sb, int64_t stride_ss, int64_t own_max, int nparts,
+                           float *ws_o, float *ws_ml, float scale_log2, hipStream_t s) {
+  const dim3 grid(nparts, static_cast<unsigned>(P), DA_HKV);
+  grouped_attn_kernel<G><<<grid, GU_WAVES * 64, 0, s>>>(q, kp, vp, pre_len, stride_pb, stride_ps, pre_max, ks, vs,
+                                                        own_len, stride_sb, stride_ss, own_max, nparts, ws_o, ws_ml,
+                                                        scale_log2);
 }
 }  // namespace vk
 
@@ -624,24 +677,22 @@ extern "C" int vk_decode_attention_grouped(const void *q, const void *k_prefix, 
   const auto qb = static_cast<const bf16_t *>(q);
   const auto kp = static_cast<const bf16_t *>(k_prefix);
   const auto vp = static_cast<const bf16_t *>(v_prefix);
+  const auto ks = static_cast<const bf16_t *>(k_suffix);
+  const auto vs = static_cast<const bf16_t *>(v_suffix);
   const int64_t P = B / G;
+#define VK_GROUPED(GG)                                                                                         \
+  launch_grouped<GG>(qb, kp, vp, prefix_len, P, stride_pb, stride_ps, pre_max, ks, vs, suffix_len, stride_sb,   \
+                     stride_ss, suf_max, L.nparts, ws + L.o, ws + L.ml, scale_log2, s)
   switch (G) {
-    case 2: launch_prefix<2>(qb, kp, vp, prefix_len, P, stride_pb, stride_ps, pre_max, L.n_chunks, ws + L.pre_o, ws + L.pre_ml, scale_log2, s); break;
-    case 4: launch_prefix<4>(qb, kp, vp, prefix_len, P, stride_pb, stride_ps, pre_max, L.n_chunks, ws + L.pre_o, ws + L.pre_ml, scale_log2, s); break;
-    case 8: launch_prefix<8>(qb, kp, vp, prefix_len, P, stride_pb, stride_ps, pre_max, L.n_chunks, ws + L.pre_o, ws + L.pre_ml, scale_log2, s); break;
-    default: launch_prefix<16>(qb, kp, vp, prefix_len, P, stride_pb, stride_ps, pre_max, L.n_chunks, ws + L.pre_o, ws + L.pre_ml, scale_log2, s); break;
+    case 2: VK_GROUPED(2); break;
+    case 4: VK_GROUPED(4); break;
+    case 8: VK_GROUPED(8); break;
+    default: VK_GROUPED(16); break;
   }
-  int rc = launch_status("decode_attention_grouped prefix");
+#undef VK_GROUPED
+  const int rc = launch_status("decode_attention_grouped");
   if (rc != VK_OK) return rc;
-  const dim3 sgrid(L.suf.nsplit, static_cast<unsigned>(B));
-  decode_attn_kernel<true><<<sgrid, DA_WAVES * 64, 0, s>>>(
-      qb, static_cast<const bf16_t *>(k_suffix), static_cast<const bf16_t *>(v_suffix), suffix_len,
-      static_cast<bf16_t *>(out), stride_sb, stride_ss, suf_max, L.suf.tps, L.suf.nsplit, ws + L.suf_o, ws + L.suf_ml,
-      scale_log2);
-  rc = launch_status("decode_attention_grouped suffix");
-  if (rc != VK_OK) return rc;
-  grouped_combine_kernel<<<static_cast<unsigned>(B), DA_H * DA_D, 0, s>>>(
-      ws + L.pre_o, ws + L.pre_ml, ws + L.suf_o, ws + L.suf_ml, prefix_len, suffix_len, static_cast<bf16_t *>(out), G,
-      pre_max, L.n_chunks, suf_max, L.suf.tps, L.suf.nsplit);
+  grouped_combine_kernel<<<static_cast<unsigned>(B), DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml,
+                                                                         static_cast<bf16_t *>(out), G, L.nparts);
   return launch_status("decode_attention_grouped combine");
 }
