@@ -46,12 +46,23 @@ struct SkinnyArgs {
 
 constexpr int SK_BM = 32;
 
+// LDS writes of this wave done, then a plain s_barrier: __syncthreads() would also drain every
+// outstanding global load (its release fence), the prefetched operands and epilogue data included.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <int BN, int WAVES, int KSTEPS, int PRO, int EPI>
 __global__ __launch_bounds__(WAVES * 64) void skinny_gemm_kernel(const SkinnyArgs p) {
+  static_assert(WAVES >= 4, "the epilogue maps 256 threads to 32 rows x 8 column groups");
+  static_assert(BN == 32 || BN == 64, "BN is 32 or 64 columns");
   constexpr bool SWI = EPI == EPI_SWIGLU;
-  constexpr int NT = BN / 16;          // n tiles of one operand group
+  constexpr bool ROPE = EPI == EPI_ROPE;
+  constexpr int NT = BN / 16;            // n tiles of one operand group
   constexpr int NB = SWI ? 2 * BN : BN;  // output columns accumulated (gate + up for SwiGLU)
   constexpr int NTT = NB / 16;
+  constexpr int HALVES = BN / 32;        // 32-column halves of the epilogue
+  static_assert(!ROPE || BN == 64, "the rope epilogue works on whole 64-column heads");
   __shared__ float part[WAVES][SK_BM][NB + 1];
   __shared__ float ssq[WAVES][SK_BM];
 
@@ -62,7 +73,21 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_gemm_kernel(const SkinnyArg
   const int kb = wid * KSTEPS * 32;  // this wave's K slice
   const int fr = lane & 15, fk = (lane >> 4) * 8;
 
-  // ---- A fragments (2 m-tiles x KSTEPS) ----
+  // epilogue mapping: thread tid < 256 -> row m0 + tid / 8 and columns 4 (tid % 8) .. + 3 of each half
+  const int rr = (tid >> 3) & (SK_BM - 1), sub = tid & 7;
+  const int64_t erow = m0 + rr;
+  const bool row_ok = tid < SK_BM * 8 && erow < p.M;
+
+  // ---- every load that does not depend on a result is issued first, in this order: RoPE positions,
+  // A, norm weight, B, epilogue data; the compiler's counted waits then only hold for what is used.
+  int64_t e_pos = 0, e_seq = 0, rp = 0;
+  if constexpr (ROPE) {
+    if (row_ok) {
+      e_pos = p.pos[erow];
+      e_seq = p.seq[erow];
+      rp = p.rope_pos ? p.rope_pos[erow] : e_pos;
+    }
+  }
   u32x4 af[KSTEPS][2];
   const bf16_t *arow[2];
 #pragma unroll
@@ -81,8 +106,11 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_gemm_kernel(const SkinnyArg
   for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
     for (int i = 0; i < 2; ++i) af[s][i] = *reinterpret_cast<const u32x4 *>(arow[i] + kb + 32 * s + fk);
-
-  // ---- B fragments ----
+  u32x4 nwf[PRO != PRO_NONE ? KSTEPS : 1];
+  if constexpr (PRO != PRO_NONE) {
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) nwf[s] = *reinterpret_cast<const u32x4 *>(p.norm_w + kb + 32 * s + fk);
+  }
   u32x4 bfr[KSTEPS][NTT];
 #pragma unroll
   for (int j = 0; j < NTT; ++j) {
@@ -92,6 +120,40 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_gemm_kernel(const SkinnyArg
     const bf16_t *src = p.w + static_cast<int64_t>(wrow) * K + kb + fk;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) bfr[s][j] = *reinterpret_cast<const u32x4 *>(src + 32 * s);
+  }
+  asm volatile("" ::: "memory");
+  // residual values this thread adds to (EPI_RESID) / the QK-norm weights and RoPE table entries of its
+  // columns (EPI_ROPE, addressed by the positions loaded first)
+  u32x2 old[HALVES];
+  u32x2 wnf[2];
+  f32x4 csf, snf;
+  const int hd = n0 / 64;
+  if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+    for (int hf = 0; hf < HALVES; ++hf) {
+      old[hf] = u32x2{0u, 0u};
+      const int col = n0 + 32 * hf + 4 * sub;
+      if (row_ok && col < p.N) old[hf] = *reinterpret_cast<const u32x2 *>(static_cast<bf16_t *>(p.y) + erow * p.N + col);
+    }
+  }
+  if constexpr (ROPE) {
+    wnf[0] = wnf[1] = u32x2{0u, 0u};
+    csf = snf = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (hd < p.H + p.HKV) {
+      const bf16_t *wn = hd < p.H ? p.qw : p.kw;
+      wnf[0] = *reinterpret_cast<const u32x2 *>(wn + 4 * sub);
+      wnf[1] = *reinterpret_cast<const u32x2 *>(wn + 32 + 4 * sub);
+      rp = rp < 0 ? 0 : (rp >= p.table_rows ? p.table_rows - 1 : rp);
+      if (p.table_f32) {
+        csf = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(p.cos_t) + rp * 32 + 4 * sub);
+        snf = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(p.sin_t) + rp * 32 + 4 * sub);
+      } else {
+        const u32x2 c2 = *reinterpret_cast<const u32x2 *>(static_cast<const bf16_t *>(p.cos_t) + rp * 32 + 4 * sub);
+        const u32x2 s2 = *reinterpret_cast<const u32x2 *>(static_cast<const bf16_t *>(p.sin_t) + rp * 32 + 4 * sub);
+        csf = f32x4{lo_bf(c2[0]), hi_bf(c2[0]), lo_bf(c2[1]), hi_bf(c2[1])};
+        snf = f32x4{lo_bf(s2[0]), hi_bf(s2[0]), lo_bf(s2[1]), hi_bf(s2[1])};
+      }
+    }
   }
 
   // ---- prologue: RMSNorm of the A rows over the full K (sum of squares across lanes and waves) ----
@@ -127,7 +189,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_gemm_kernel(const SkinnyArg
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     float r[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -137,14 +199,12 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_gemm_kernel(const SkinnyArg
       r[i] = rsqrtf(t / static_cast<float>(K) + p.eps);
     }
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      const u32x4 wv = *reinterpret_cast<const u32x4 *>(p.norm_w + kb + 32 * s + fk);
+    for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          af[s][i][e] = pack_bf(lo_bf(af[s][i][e]) * r[i] * lo_bf(wv[e]), hi_bf(af[s][i][e]) * r[i] * hi_bf(wv[e]));
-    }
+          af[s][i][e] = pack_bf(lo_bf(af[s][i][e]) * r[i] * lo_bf(nwf[s][e]), hi_bf(af[s][i][e]) * r[i] * hi_bf(nwf[s][e]));
   }
 
   // ---- MFMA over this wave's K slice ----
@@ -172,134 +232,100 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_gemm_kernel(const SkinnyArg
 #pragma unroll
         for (int e = 0; e < 4; ++e) part[wid][16 * i + orow + e][16 * j + oc] = acc[i][j][e];
   }
-  __syncthreads();
+  lds_barrier();
+  if (tid >= SK_BM * 8) return;
 
-  // ---- epilogue: thread -> (row, 8-lane group); columns {4s..4s+3} (+ {32+4s..} when BN = 64) ----
-  constexpr int TPR = 8;  // threads per row
-  for (int base = 0; base < SK_BM * TPR; base += WAVES * 64) {
-    const int t = base + tid;
-    if (t >= SK_BM * TPR) break;
-    const int rr = t / TPR, sub = t % TPR;
-    const int64_t row = m0 + rr;
-    const bool row_ok = row < p.M;
-    constexpr int HALVES = BN == 64 ? 2 : 1;
-    float v[HALVES][4];
-    float vu[HALVES][4];
+  // ---- epilogue: thread -> (row rr, 8-lane group sub); columns {4 sub .. 4 sub + 3} of each half ----
+  float v[HALVES][4];
+  float vu[HALVES][4];
 #pragma unroll
-    for (int hf = 0; hf < HALVES; ++hf)
+  for (int hf = 0; hf < HALVES; ++hf)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int col = 32 * hf + 4 * sub + c;
-        float sacc = 0.f, uacc = 0.f;
+    for (int c = 0; c < 4; ++c) {
+      const int col = 32 * hf + 4 * sub + c;
+      float sacc = 0.f, uacc = 0.f;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) {
-          sacc += part[w][rr][col];
-          if (SWI) uacc += part[w][rr][BN + col];
-        }
-        v[hf][c] = sacc;
-        vu[hf][c] = uacc;
+      for (int w = 0; w < WAVES; ++w) {
+        sacc += part[w][rr][col];
+        if (SWI) uacc += part[w][rr][BN + col];
       }
-    if constexpr (EPI == EPI_ROPE) {
-      static_assert(BN == 64, "rope epilogue works on whole 64-column heads");
-      const int hd = n0 / 64;
-      const int H = p.H, HKV = p.HKV;
-      float x1[4], x2[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        x1[c] = round_bf(v[0][c]);
-        x2[c] = round_bf(v[1][c]);
-      }
-      if (hd < H + HKV) {
-        float ss = 0.f;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) ss += x1[c] * x1[c] + x2[c] * x2[c];
-        ss += __shfl_xor(ss, 1, 64);
-        ss += __shfl_xor(ss, 2, 64);
-        ss += __shfl_xor(ss, 4, 64);
-        const float r = rsqrtf(ss / 64.f + p.eps);
-        const bf16_t *wn = hd < H ? p.qw : p.kw;
-        int64_t rp = 0;
-        if (row_ok) rp = p.rope_pos ? p.rope_pos[row] : p.pos[row];
-        rp = rp < 0 ? 0 : (rp >= p.table_rows ? p.table_rows - 1 : rp);
-        uint32_t o1[2], o2[2];
-#pragma unroll
-        for (int c = 0; c < 4; c += 2) {
-          float a1[2], a2[2];
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            const int j = 4 * sub + c + e;
-            const float y1 = round_bf(x1[c + e] * r * bf2f(wn[j]));
-            const float y2 = round_bf(x2[c + e] * r * bf2f(wn[32 + j]));
-            float cs, sn;
-            if (p.table_f32) {
-              cs = static_cast<const float *>(p.cos_t)[rp * 32 + j];
-              sn = static_cast<const float *>(p.sin_t)[rp * 32 + j];
-            } else {
-              cs = bf2f(static_cast<const bf16_t *>(p.cos_t)[rp * 32 + j]);
-              sn = bf2f(static_cast<const bf16_t *>(p.sin_t)[rp * 32 + j]);
-            }
-            a1[e] = y1 * cs - y2 * sn;
-            a2[e] = y1 * sn + y2 * cs;
-          }
-          o1[c / 2] = pack_bf(a1[0], a1[1]);
-          o2[c / 2] = pack_bf(a2[0], a2[1]);
-        }
-        if (row_ok) {
-          if (hd < H) {
-            bf16_t *dst = static_cast<bf16_t *>(p.y) + (row * H + hd) * 64 + 4 * sub;
-            *reinterpret_cast<u32x2 *>(dst) = u32x2{o1[0], o1[1]};
-            *reinterpret_cast<u32x2 *>(dst + 32) = u32x2{o2[0], o2[1]};
-          } else {
-            const int64_t sq = p.seq[row], ps = p.pos[row];
-            if (sq >= 0 && sq < p.cache_rows && ps >= 0 && ps < p.cache_len) {
-              bf16_t *dst = p.kc + sq * p.stride_cb + ps * p.stride_cs + (hd - H) * 64 + 4 * sub;
-              *reinterpret_cast<u32x2 *>(dst) = u32x2{o1[0], o1[1]};
-              *reinterpret_cast<u32x2 *>(dst + 32) = u32x2{o2[0], o2[1]};
-            }
-          }
-        }
-      } else if (row_ok) {  // v head: the rounded projection goes to the cache unchanged
-        const int64_t sq = p.seq[row], ps = p.pos[row];
-        if (sq >= 0 && sq < p.cache_rows && ps >= 0 && ps < p.cache_len) {
-          bf16_t *dst = p.vc + sq * p.stride_cb + ps * p.stride_cs + (hd - H - HKV) * 64 + 4 * sub;
-          *reinterpret_cast<u32x2 *>(dst) = u32x2{pack_bf(x1[0], x1[1]), pack_bf(x1[2], x1[3])};
-          *reinterpret_cast<u32x2 *>(dst + 32) = u32x2{pack_bf(x2[0], x2[1]), pack_bf(x2[2], x2[3])};
-        }
-      }
-      continue;
+      v[hf][c] = sacc;
+      vu[hf][c] = uacc;
     }
-    if (!row_ok) continue;
+  if constexpr (ROPE) {
+    const int H = p.H, HKV = p.HKV;
+    float x1[4], x2[4];
 #pragma unroll
-    for (int hf = 0; hf < HALVES; ++hf) {
-      const int col = n0 + 32 * hf + 4 * sub;
-      if (col >= p.N) continue;  // N is a multiple of 4 (checked on the host)
-      const int64_t off = row * p.N + col;
-      if (EPI == EPI_F32) {
-        float *dst = static_cast<float *>(p.y) + off;
+    for (int c = 0; c < 4; ++c) {
+      x1[c] = round_bf(v[0][c]);
+      x2[c] = round_bf(v[1][c]);
+    }
+    if (hd < H + HKV) {
+      float ss = 0.f;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) dst[c] = v[hf][c];
-      } else {
-        float o[4];
+      for (int c = 0; c < 4; ++c) ss += x1[c] * x1[c] + x2[c] * x2[c];
+      ss += __shfl_xor(ss, 1, 64);
+      ss += __shfl_xor(ss, 2, 64);
+      ss += __shfl_xor(ss, 4, 64);
+      const float r = rsqrtf(ss / 64.f + p.eps);
+      const float w1[4] = {lo_bf(wnf[0][0]), hi_bf(wnf[0][0]), lo_bf(wnf[0][1]), hi_bf(wnf[0][1])};
+      const float w2[4] = {lo_bf(wnf[1][0]), hi_bf(wnf[1][0]), lo_bf(wnf[1][1]), hi_bf(wnf[1][1])};
+      float a1[4], a2[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          float val = v[hf][c];
-          if (EPI == EPI_SWIGLU) {
-            const float g = round_bf(val);
-            const float u = round_bf(vu[hf][c]);
-            val = round_bf(g / (1.0f + __expf(-g))) * u;
-          }
-          o[c] = val;
-        }
-        bf16_t *dst = static_cast<bf16_t *>(p.y) + off;
-        if (EPI == EPI_RESID) {
-          const u32x2 old = *reinterpret_cast<const u32x2 *>(dst);
-          o[0] = lo_bf(old[0]) + round_bf(o[0]);
-          o[1] = hi_bf(old[0]) + round_bf(o[1]);
-          o[2] = lo_bf(old[1]) + round_bf(o[2]);
-          o[3] = hi_bf(old[1]) + round_bf(o[3]);
-        }
-        *reinterpret_cast<u32x2 *>(dst) = u32x2{pack_bf(o[0], o[1]), pack_bf(o[2], o[3])};
+      for (int c = 0; c < 4; ++c) {
+        const float y1 = round_bf(x1[c] * r * w1[c]);
+        const float y2 = round_bf(x2[c] * r * w2[c]);
+        a1[c] = y1 * csf[c] - y2 * snf[c];
+        a2[c] = y1 * snf[c] + y2 * csf[c];
       }
+      const u32x2 o1 = u32x2{pack_bf(a1[0], a1[1]), pack_bf(a1[2], a1[3])};
+      const u32x2 o2 = u32x2{pack_bf(a2[0], a2[1]), pack_bf(a2[2], a2[3])};
+      if (row_ok) {
+        if (hd < H) {
+          bf16_t *dst = static_cast<bf16_t *>(p.y) + (erow * H + hd) * 64 + 4 * sub;
+          *reinterpret_cast<u32x2 *>(dst) = o1;
+          *reinterpret_cast<u32x2 *>(dst + 32) = o2;
+        } else if (e_seq >= 0 && e_seq < p.cache_rows && e_pos >= 0 && e_pos < p.cache_len) {
+          bf16_t *dst = p.kc + e_seq * p.stride_cb + e_pos * p.stride_cs + (hd - H) * 64 + 4 * sub;
+          *reinterpret_cast<u32x2 *>(dst) = o1;
+          *reinterpret_cast<u32x2 *>(dst + 32) = o2;
+        }
+      }
+    } else if (row_ok && e_seq >= 0 && e_seq < p.cache_rows && e_pos >= 0 && e_pos < p.cache_len) {
+      // v head: the rounded projection goes to the cache unchanged
+      bf16_t *dst = p.vc + e_seq * p.stride_cb + e_pos * p.stride_cs + (hd - H - HKV) * 64 + 4 * sub;
+      *reinterpret_cast<u32x2 *>(dst) = u32x2{pack_bf(x1[0], x1[1]), pack_bf(x1[2], x1[3])};
+      *reinterpret_cast<u32x2 *>(dst + 32) = u32x2{pack_bf(x2[0], x2[1]), pack_bf(x2[2], x2[3])};
+    }
+    return;
+  }
+  if (!row_ok) return;
+#pragma unroll
+  for (int hf = 0; hf < HALVES; ++hf) {
+    const int col = n0 + 32 * hf + 4 * sub;
+    if (col >= p.N) continue;  // N is a multiple of 4 (checked on the host)
+    const int64_t off = erow * p.N + col;
+    if (EPI == EPI_F32) {
+      *reinterpret_cast<f32x4 *>(static_cast<float *>(p.y) + off) = f32x4{v[hf][0], v[hf][1], v[hf][2], v[hf][3]};
+    } else {
+      float o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float val = v[hf][c];
+        if (EPI == EPI_SWIGLU) {
+          const float g = round_bf(val);
+          const float u = round_bf(vu[hf][c]);
+          val = round_bf(g / (1.0f + __expf(-g))) * u;
+        }
+        o[c] = val;
+      }
+      if (EPI == EPI_RESID) {
+        o[0] = lo_bf(old[hf][0]) + round_bf(o[0]);
+        o[1] = hi_bf(old[hf][0]) + round_bf(o[1]);
+        o[2] = lo_bf(old[hf][1]) + round_bf(o[2]);
+        o[3] = hi_bf(old[hf][1]) + round_bf(o[3]);
+      }
+      *reinterpret_cast<u32x2 *>(static_cast<bf16_t *>(p.y) + off) = u32x2{pack_bf(o[0], o[1]), pack_bf(o[2], o[3])};
     }
   }
 }
@@ -310,11 +336,15 @@ static void launch_skinny(const SkinnyArgs &a, hipStream_t s) {
   skinny_gemm_kernel<BN, WAVES, KSTEPS, PRO, EPI><<<grid, WAVES * 64, 0, s>>>(a);
 }
 
-// K = 512 (d_model) with 4 waves of 4 k-steps, K = 1536 (ffn) with 8 waves of 6 k-steps
+#ifndef VK_SK512_WAVES
+#define VK_SK512_WAVES 8  // waves splitting K = 512 (each 512 / 32 / waves k-steps)
+#endif
+
+// K = 512 (d_model) with VK_SK512_WAVES waves, K = 1536 (ffn) with 8 waves of 6 k-steps
 template <int BN, int PRO, int EPI>
 static int dispatch_k(const SkinnyArgs &a, hipStream_t s) {
   if (a.K == 512) {
-    launch_skinny<BN, 4, 4, PRO, EPI>(a, s);
+    launch_skinny<BN, VK_SK512_WAVES, 16 / VK_SK512_WAVES, PRO, EPI>(a, s);
   } else if (a.K == 1536) {
     launch_skinny<BN, 8, 6, PRO, EPI>(a, s);
   } else if (a.K == 256) {
@@ -346,7 +376,8 @@ extern "C" int vk_norm_linear(const void *x, const void *norm_w, float eps, cons
                               int32_t K, int32_t swiglu, int32_t out_dtype, void *stream) {
   VK_CHECK_ARG(x && w && y, "norm_linear: null pointer");
   VK_CHECK_ARG(M >= 0 && N > 0 && N % 4 == 0 && K > 0, "norm_linear: bad sizes");
-  VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w) && (!norm_w || vk_aligned16(norm_w)), "norm_linear: alignment");
+  VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w) && vk_aligned16(y) && (!norm_w || vk_aligned16(norm_w)),
+               "norm_linear: alignment");
   VK_CHECK_ARG(!(swiglu && out_dtype == VK_DTYPE_F32), "norm_linear: the SwiGLU epilogue stores bf16");
   if (M == 0) return VK_OK;
   SkinnyArgs p = base_args(x, w, y, M, N, K);
@@ -398,7 +429,8 @@ extern "C" int vk_norm_qkv_rope_cache(const void *x, const int64_t *tok, int64_t
   VK_CHECK_ARG(head_dim == 64, "norm_qkv_rope_cache: built for head_dim 64");
   VK_CHECK_ARG(tok == nullptr || (x_store != nullptr && vocab > 0), "norm_qkv_rope_cache: embedding needs x_store");
   VK_CHECK_ARG(table_dtype == VK_DTYPE_BF16 || table_dtype == VK_DTYPE_F32, "norm_qkv_rope_cache: table dtype");
-  VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w_qkv) && vk_aligned16(norm_w) && vk_aligned16(q),
+  VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w_qkv) && vk_aligned16(norm_w) && vk_aligned16(q) &&
+                   vk_aligned16(q_norm_w) && vk_aligned16(k_norm_w) && vk_aligned16(cos_t) && vk_aligned16(sin_t),
                "norm_qkv_rope_cache: alignment");
   if (M == 0) return VK_OK;
   SkinnyArgs p = base_args(x, w_qkv, q, M, (n_heads + 2 * n_kv_heads) * 64, K);
