@@ -176,7 +176,8 @@ int vk_select_update(const float *logits, const void *h, const void *norm_w, flo
  * Decode-step fusions (small M: one row per sequence). Same rounding points as the unfused ops.
  *
  * vk_norm_qkv_rope_cache: h = RMSNorm(x) * norm_w (x [M, K] bf16; or, with tok non-NULL, x = emb[tok] with
- * emb = the `x` argument [vocab, K], and the gathered rows are also stored to x_store), then
+ * emb = the `x` argument [vocab, K], and the gathered rows are also stored to x_store; norm_w NULL: h = x,
+ * the activation normalised by vk_add_rmsnorm / vk_embed_rmsnorm beforehand), then
  * qkv = bf16(h @ w_qkv^T) and the vk_qkv_rope_cache transform of qkv: q -> q [M, H, 64], k / v -> caches.
  * Replaces embed_rmsnorm / add_rmsnorm + linear + qkv_rope_cache (viktor/triton_ops.py:17-108, 149-169;
  * viktor/fast_decoder.py:41-46, 76-90).

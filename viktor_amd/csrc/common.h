@@ -22,10 +22,10 @@ __device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float(static_
 
 // fp32 -> bf16, round to nearest even; NaN stays a quiet NaN (the rounding torch and Triton use).
 __device__ __forceinline__ bf16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<bf16_t>(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t nan = (u >> 16) | 0x40u;  // quiet NaN, sign and payload top kept
+  return static_cast<bf16_t>((u & 0x7fffffffu) > 0x7f800000u ? nan : rne);  // a select, no branch
 }
 
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }

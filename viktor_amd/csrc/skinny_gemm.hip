@@ -48,8 +48,13 @@ constexpr int SK_BM = 32;
 
 // LDS writes of this wave done, then a plain s_barrier: __syncthreads() would also drain every
 // outstanding global load (its release fence), the prefetched operands and epilogue data included.
+// Builtins, not inline asm: the compiler's wait analysis treats an asm statement as unknown memory
+// traffic and would then drain all loads before later LDS reads.
 __device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt / expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 template <int BN, int WAVES, int KSTEPS, int PRO, int EPI>
@@ -330,6 +335,378 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_gemm_kernel(const SkinnyArg
   }
 }
 
+// ---- panel kernel: the K dimension streamed through an LDS ring --------------------------------------
+//
+// A workgroup (4 waves) owns 32 rows x 64 output columns (64 gate + 64 up weight rows for SwiGLU) over the
+// whole K. K advances in 64-wide stages through a 3- or 4-slot LDS ring filled by direct global->LDS loads
+// (global_load_lds_dwordx4: lane l of an instruction lands at slot base + 16 l), so two or three stages
+// are in flight while one feeds the MFMAs and the prefetch costs no registers. An LDS row is 128 bytes (64 K
+// values); the 16-byte chunk c of row r sits in slot c ^ ((r >> 1) & 7), which spreads the 16 rows of every
+// fragment read over all 16 bank groups. The product is formed transposed (the weight fragment is the MFMA
+// A operand), the tile is handed to the epilogue through LDS, and the epilogue is the one above with the
+// same rounding points. RMSNorm: the sums of squares come from a pre-pass over the workgroup's rows issued
+// before the ring; each fragment is normalised (bf16(x / rms * w)) as it is read.
+constexpr int PG_BM = 32;
+constexpr int PG_BN = 64;
+constexpr int PG_BK = 64;
+constexpr int PG_ROWB = PG_BK * 2;
+constexpr int PG_NORM_K = 512;  // the RMSNorm prologue is built for K = 512 (d_model)
+
+// s_waitcnt immediate: vmcnt <= n, expcnt / lgkmcnt unconstrained (gfx9 encoding: vmcnt[3:0] bits 3:0,
+// vmcnt[5:4] bits 15:14, expcnt bits 6:4, lgkmcnt bits 11:8)
+constexpr int pg_vmcnt(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | (((n >> 4) & 3) << 14); }
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// one stage of the ring: this wave's LOADS direct-load instructions (instruction q = wid + 4 j -> 1 KB at
+// base + 1024 q). A device function rather than a lambda: with a lambda around the builtin, the host pass
+// drops the kernel's launch stub.
+template <int LOADS>
+__device__ __forceinline__ void pg_issue(char *base, const bf16_t *const *src, int k0, int wid) {
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j)
+    __builtin_amdgcn_global_load_lds(src[j] + k0, (lds_void_t *)(base + (wid + 4 * j) * 1024), 16, 0, 0);
+}
+
+template <int EPI>
+struct PanelShape {
+  static constexpr bool SWI = EPI == EPI_SWIGLU;
+  static constexpr int WR = SWI ? 2 * PG_BN : PG_BN;  // weight rows per tile
+  static constexpr int ROWS = PG_BM + WR;             // LDS rows per stage
+  static constexpr int STAGEB = ROWS * PG_ROWB;
+  static constexpr int LOADS = ROWS / 8 / 4;          // direct-load instructions per wave per stage
+  // the K loop is latency-bound (little MFMA work per stage): as many stages in flight as LDS allows
+  // with 2 workgroups per CU -- 4 slots (3 in flight) for 12 KB stages, 3 for the 20 KB SwiGLU stages
+  static constexpr int STAGES = SWI ? 3 : 4;
+  static constexpr int PARTB = PG_BM * (WR + 1) * 4;
+  static constexpr int BODY = STAGES * STAGEB > PARTB ? STAGES * STAGEB : PARTB;
+  static constexpr int SMEM = BODY + PG_NORM_K * 2 + PG_BM * 4;  // + the RMSNorm weight and row sums
+};
+
+template <int PRO, int EPI>
+__global__ __launch_bounds__(256) void panel_gemm_kernel(const SkinnyArgs p, int m_blocks, int tiles) {
+  using S = PanelShape<EPI>;
+  constexpr bool SWI = S::SWI;
+  constexpr bool ROPE = EPI == EPI_ROPE;
+  constexpr int HALVES = 2;  // 64 output columns = two 32-column halves in the epilogue
+  static_assert(S::ROWS % 32 == 0, "a stage is whole 8-row instructions for 4 waves");
+  __shared__ __attribute__((aligned(16))) char smem[S::SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // XCD-aware tile order: workgroup p runs on XCD p % 8, which owns a contiguous range of tiles; tiles are
+  // numbered n-block-major, so the workgroups of one XCD share weight tiles (a bijection for any count)
+  const int pid = blockIdx.x, xcd = pid & 7, idx = pid >> 3;
+  const int q8 = tiles >> 3, r8 = tiles & 7;
+  const int tile = xcd * q8 + min(xcd, r8) + idx;
+  const int nb = tile / m_blocks, mb = tile % m_blocks;
+  const int64_t m0 = static_cast<int64_t>(mb) * PG_BM;
+  const int n0 = nb * PG_BN;
+  // K stays a run-time value (with the norm it is 512, checked on the host): with a constant trip count
+  // the compiler unrolls the K loop, sees the ring offsets and drains every load before each LDS read
+  const int K = p.K, nk = K / PG_BK;
+  const int fr = lane & 15, fg = lane >> 4;
+
+  // epilogue mapping: thread -> row m0 + tid / 8, columns 4 (tid % 8) .. + 3 of each 32-column half
+  const int rr = tid >> 3, sub = tid & 7;
+  const int64_t erow = m0 + rr;
+  const bool row_ok = erow < p.M;
+
+  // 1. RoPE positions (the table loads depend on them)
+  int64_t e_pos = 0, e_seq = 0, rp = 0;
+  if constexpr (ROPE) {
+    if (row_ok) {
+      e_pos = p.pos[erow];
+      e_seq = p.seq[erow];
+      rp = p.rope_pos ? p.rope_pos[erow] : e_pos;
+    }
+  }
+  // 2. A row pointers (embedding rows through the token ids)
+  auto a_row = [&](int r) {
+    int64_t row = m0 + r;
+    row = row < p.M ? row : p.M - 1;
+    if (PRO == PRO_EMBED_NORM) {
+      int64_t t = p.tok[row];
+      t = (t < 0 || t >= p.vocab) ? 0 : t;
+      return p.a + t * K;
+    }
+    return p.a + row * K;
+  };
+  // 3. the ring: stage 0 and 1 in flight first. Instruction q (= wid + 4 j) of a stage covers LDS rows
+  //    8 q .. 8 q + 7 (A rows first, then weight rows); lane l -> row 8 q + l / 8, slot l % 8, K chunk
+  //    slot ^ ((row >> 1) & 7)
+  const bf16_t *src[S::LOADS];
+#pragma unroll
+  for (int j = 0; j < S::LOADS; ++j) {
+    const int q = wid + 4 * j;
+    const int r = 8 * q + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    if (r < PG_BM) {
+      src[j] = a_row(r) + 8 * c;
+    } else {
+      const int wr = r - PG_BM;
+      int col = n0 + (SWI ? (wr & (PG_BN - 1)) : wr);
+      col = col < p.N ? col : p.N - 1;
+      const int wrow = (SWI && wr >= PG_BN) ? col + p.N : col;
+      src[j] = p.w + static_cast<int64_t>(wrow) * K + 8 * c;
+    }
+  }
+#define PG_ISSUE(stage) pg_issue<S::LOADS>(smem + ((stage) % S::STAGES) * S::STAGEB, src, (stage) * PG_BK, wid)
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int s = 0; s < S::STAGES - 1; ++s)
+    if (s < nk) PG_ISSUE(s);
+  asm volatile("" ::: "memory");
+
+  // 4. RMSNorm (K = 512): wave w reads rows 8 w .. 8 w + 7; lane l owns row 8 w + l / 8 and the 64 K values
+  //    at 64 (l % 8), so a row's sum of squares is a reduction over 8 lanes. These loads, and the norm
+  //    weight staged to LDS, are consumed before the loop: inside it only LDS is read, so the counted waits
+  //    on the ring are the only ones.
+  // the norm weight and the row sums of squares sit in the ring's LDS block, past the ring: LDS accesses
+  // to another object after a direct load make the compiler drain every load before them
+  bf16_t *nws = reinterpret_cast<bf16_t *>(smem + S::BODY);
+  float *rs = reinterpret_cast<float *>(smem + S::BODY + PG_NORM_K * 2);
+  float rinv[1] = {1.f};
+  if constexpr (PRO != PRO_NONE) {
+    const int pre_row = 8 * wid + (lane >> 3);
+    const int pre_k = 64 * (lane & 7);
+    u32x4 xv[8];
+    const bf16_t *xr = a_row(pre_row) + pre_k;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xv[j] = *reinterpret_cast<const u32x4 *>(xr + 8 * j);
+    const u32x4 nwv = *reinterpret_cast<const u32x4 *>(p.norm_w + 8 * lane);
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = lo_bf(xv[j][e]), hi = hi_bf(xv[j][e]);
+        ss += lo * lo + hi * hi;
+      }
+    const int64_t grow = m0 + pre_row;
+    if (PRO == PRO_EMBED_NORM && nb == 0 && grow < p.M) {  // the gathered rows become the residual stream
+#pragma unroll
+      for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4 *>(p.x_store + grow * K + pre_k + 8 * j) = xv[j];
+    }
+    ss += __shfl_xor(ss, 1, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    ss += __shfl_xor(ss, 4, 64);
+    if ((lane & 7) == 0) rs[pre_row] = ss;
+    // every wave stores the (identical) weight: a load left unconsumed on some waves would make the
+    // compiler drain all loads wherever its registers are reused
+    *reinterpret_cast<u32x4 *>(nws + 8 * lane) = nwv;
+    lds_barrier();
+    rinv[0] = rsqrtf(rs[tid >> 3] / static_cast<float>(K) + p.eps);  // the row of this thread's chunk
+  }
+
+  // 5. epilogue data (consumed after the loop)
+  u32x2 old[HALVES];
+  u32x2 wnf[2];
+  f32x4 csf, snf;
+  const int hd = n0 / 64;
+  if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+    for (int hf = 0; hf < HALVES; ++hf) {
+      old[hf] = u32x2{0u, 0u};
+      const int col = n0 + 32 * hf + 4 * sub;
+      if (row_ok && col < p.N) old[hf] = *reinterpret_cast<const u32x2 *>(static_cast<bf16_t *>(p.y) + erow * p.N + col);
+    }
+  }
+  if constexpr (ROPE) {
+    wnf[0] = wnf[1] = u32x2{0u, 0u};
+    csf = snf = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (hd < p.H + p.HKV) {
+      const bf16_t *wn = hd < p.H ? p.qw : p.kw;
+      wnf[0] = *reinterpret_cast<const u32x2 *>(wn + 4 * sub);
+      wnf[1] = *reinterpret_cast<const u32x2 *>(wn + 32 + 4 * sub);
+      rp = rp < 0 ? 0 : (rp >= p.table_rows ? p.table_rows - 1 : rp);
+      if (p.table_f32) {
+        csf = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(p.cos_t) + rp * 32 + 4 * sub);
+        snf = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(p.sin_t) + rp * 32 + 4 * sub);
+      } else {
+        const u32x2 c2 = *reinterpret_cast<const u32x2 *>(static_cast<const bf16_t *>(p.cos_t) + rp * 32 + 4 * sub);
+        const u32x2 s2 = *reinterpret_cast<const u32x2 *>(static_cast<const bf16_t *>(p.sin_t) + rp * 32 + 4 * sub);
+        csf = f32x4{lo_bf(c2[0]), hi_bf(c2[0]), lo_bf(c2[1]), hi_bf(c2[1])};
+        snf = f32x4{lo_bf(s2[0]), hi_bf(s2[0]), lo_bf(s2[1]), hi_bf(s2[1])};
+      }
+    }
+  }
+  // fragment byte offsets inside a stage: LDS row R, K chunk c -> R * 128 + 16 * (c ^ ((R >> 1) & 7))
+  auto frag_off = [](int R, int c) { return R * PG_ROWB + 16 * (c ^ ((R >> 1) & 7)); };
+  constexpr int NW = SWI ? 2 : 1;
+  int woff[NW][2], xoff[2][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int wt = 0; wt < NW; ++wt) woff[wt][ks] = frag_off(PG_BM + wt * PG_BN + 16 * wid + fr, 4 * ks + fg);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) xoff[t][ks] = frag_off(16 * t + fr, 4 * ks + fg);
+  }
+  f32x4 acc[NW][2];
+#pragma unroll
+  for (int wt = 0; wt < NW; ++wt)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[wt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kt = 0; kt < nk; ++kt) {
+    // this wave's loads of stage kt are done once at most (stages issued after it) x LOADS remain
+    const int ahead = min(nk - 1 - kt, S::STAGES - 2);
+    if (ahead >= 2)
+      __builtin_amdgcn_s_waitcnt(pg_vmcnt(2 * S::LOADS));
+    else if (ahead == 1)
+      __builtin_amdgcn_s_waitcnt(pg_vmcnt(S::LOADS));
+    else
+      __builtin_amdgcn_s_waitcnt(pg_vmcnt(0));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kt + S::STAGES - 1 < nk) PG_ISSUE(kt + S::STAGES - 1);
+    char *base = smem + (kt % S::STAGES) * S::STAGEB;
+    if constexpr (PRO != PRO_NONE) {
+      // RMSNorm of the stage's A tile in place, once per workgroup: thread t takes the 16-byte chunk in
+      // slot t % 8 of row t / 8 (K chunk c = slot ^ ((row >> 1) & 7)) -> bf16(x / rms * w)
+      const int row = tid >> 3, c = (tid & 7) ^ ((row >> 1) & 7);
+      u32x4 *xc = reinterpret_cast<u32x4 *>(base + row * PG_ROWB + 16 * (tid & 7));
+      const u32x4 xr = *xc;
+      const u32x4 wv = *reinterpret_cast<const u32x4 *>(nws + kt * PG_BK + 8 * c);
+      u32x4 xn;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        xn[e] = pack_bf(lo_bf(xr[e]) * rinv[0] * lo_bf(wv[e]), hi_bf(xr[e]) * rinv[0] * hi_bf(wv[e]));
+      *xc = xn;
+      lds_barrier();
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      u32x4 xf[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) xf[t] = *reinterpret_cast<const u32x4 *>(base + xoff[t][ks]);
+#pragma unroll
+      for (int wt = 0; wt < NW; ++wt) {
+        const u32x4 wf = *reinterpret_cast<const u32x4 *>(base + woff[wt][ks]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          acc[wt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf),
+                                                               __builtin_bit_cast(bf16x8, xf[t]), acc[wt][t], 0, 0, 0);
+      }
+    }
+  }
+
+#undef PG_ISSUE
+  // tile -> LDS: acc[wt][t] lane holds C^T[weight row 16 wid + 4 g + e (+ 64 for up)][A row 16 t + lane % 16]
+  lds_barrier();
+  float *part = reinterpret_cast<float *>(smem);  // [PG_BM][WR + 1]
+#pragma unroll
+  for (int wt = 0; wt < NW; ++wt)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) part[(16 * t + fr) * (S::WR + 1) + wt * PG_BN + 16 * wid + 4 * fg + e] = acc[wt][t][e];
+  lds_barrier();
+
+  // ---- epilogue: thread -> (row rr, 4-column group sub) of each 32-column half ----
+  float v[HALVES][4], vu[HALVES][4];
+#pragma unroll
+  for (int hf = 0; hf < HALVES; ++hf)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int col = 32 * hf + 4 * sub + c;
+      v[hf][c] = part[rr * (S::WR + 1) + col];
+      vu[hf][c] = SWI ? part[rr * (S::WR + 1) + PG_BN + col] : 0.f;
+    }
+  if constexpr (ROPE) {
+    const int H = p.H, HKV = p.HKV;
+    float x1[4], x2[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      x1[c] = round_bf(v[0][c]);
+      x2[c] = round_bf(v[1][c]);
+    }
+    if (hd < H + HKV) {
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) ss += x1[c] * x1[c] + x2[c] * x2[c];
+      ss += __shfl_xor(ss, 1, 64);
+      ss += __shfl_xor(ss, 2, 64);
+      ss += __shfl_xor(ss, 4, 64);
+      const float r = rsqrtf(ss / 64.f + p.eps);
+      const float w1[4] = {lo_bf(wnf[0][0]), hi_bf(wnf[0][0]), lo_bf(wnf[0][1]), hi_bf(wnf[0][1])};
+      const float w2[4] = {lo_bf(wnf[1][0]), hi_bf(wnf[1][0]), lo_bf(wnf[1][1]), hi_bf(wnf[1][1])};
+      float a1[4], a2[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float y1 = round_bf(x1[c] * r * w1[c]);
+        const float y2 = round_bf(x2[c] * r * w2[c]);
+        a1[c] = y1 * csf[c] - y2 * snf[c];
+        a2[c] = y1 * snf[c] + y2 * csf[c];
+      }
+      const u32x2 o1 = u32x2{pack_bf(a1[0], a1[1]), pack_bf(a1[2], a1[3])};
+      const u32x2 o2 = u32x2{pack_bf(a2[0], a2[1]), pack_bf(a2[2], a2[3])};
+      if (row_ok) {
+        if (hd < H) {
+          bf16_t *dst = static_cast<bf16_t *>(p.y) + (erow * H + hd) * 64 + 4 * sub;
+          *reinterpret_cast<u32x2 *>(dst) = o1;
+          *reinterpret_cast<u32x2 *>(dst + 32) = o2;
+        } else if (e_seq >= 0 && e_seq < p.cache_rows && e_pos >= 0 && e_pos < p.cache_len) {
+          bf16_t *dst = p.kc + e_seq * p.stride_cb + e_pos * p.stride_cs + (hd - H) * 64 + 4 * sub;
+          *reinterpret_cast<u32x2 *>(dst) = o1;
+          *reinterpret_cast<u32x2 *>(dst + 32) = o2;
+        }
+      }
+    } else if (row_ok && e_seq >= 0 && e_seq < p.cache_rows && e_pos >= 0 && e_pos < p.cache_len) {
+      // v head: the rounded projection goes to the cache unchanged
+      bf16_t *dst = p.vc + e_seq * p.stride_cb + e_pos * p.stride_cs + (hd - H - HKV) * 64 + 4 * sub;
+      *reinterpret_cast<u32x2 *>(dst) = u32x2{pack_bf(x1[0], x1[1]), pack_bf(x1[2], x1[3])};
+      *reinterpret_cast<u32x2 *>(dst + 32) = u32x2{pack_bf(x2[0], x2[1]), pack_bf(x2[2], x2[3])};
+    }
+    return;
+  }
+  if (!row_ok) return;
+#pragma unroll
+  for (int hf = 0; hf < HALVES; ++hf) {
+    const int col = n0 + 32 * hf + 4 * sub;
+    if (col >= p.N) continue;  // N is a multiple of 4 (checked on the host)
+    const int64_t off = erow * p.N + col;
+    if (EPI == EPI_F32) {
+      *reinterpret_cast<f32x4 *>(static_cast<float *>(p.y) + off) = f32x4{v[hf][0], v[hf][1], v[hf][2], v[hf][3]};
+    } else {
+      float o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float val = v[hf][c];
+        if (EPI == EPI_SWIGLU) {
+          const float g = round_bf(val);
+          const float u = round_bf(vu[hf][c]);
+          val = round_bf(g / (1.0f + __expf(-g))) * u;
+        }
+        o[c] = val;
+      }
+      if (EPI == EPI_RESID) {
+        o[0] = lo_bf(old[hf][0]) + round_bf(o[0]);
+        o[1] = hi_bf(old[hf][0]) + round_bf(o[1]);
+        o[2] = lo_bf(old[hf][1]) + round_bf(o[2]);
+        o[3] = hi_bf(old[hf][1]) + round_bf(o[3]);
+      }
+      *reinterpret_cast<u32x2 *>(static_cast<bf16_t *>(p.y) + off) = u32x2{pack_bf(o[0], o[1]), pack_bf(o[2], o[3])};
+    }
+  }
+}
+
+template <int PRO, int EPI>
+static int launch_panel(const SkinnyArgs &a, hipStream_t s) {
+  const int64_t m_blocks = (a.M + PG_BM - 1) / PG_BM;
+  const int64_t n_blocks = (a.N + PG_BN - 1) / PG_BN;
+  const int64_t tiles = m_blocks * n_blocks;
+  if (tiles >= (int64_t(1) << 31)) return fail(VK_ERR_ARG, "linear: too many tiles");
+  panel_gemm_kernel<PRO, EPI><<<static_cast<unsigned>(tiles), 256, 0, s>>>(a, static_cast<int>(m_blocks),
+                                                                          static_cast<int>(tiles));
+  return VK_OK;
+}
+
+// The panel kernel takes K % 64 == 0 (with a norm: K = 512); the split-K kernel the rest.
+static bool panel_ok(const SkinnyArgs &a, int pro) {
+  return a.K % PG_BK == 0 && (pro == PRO_NONE || a.K == PG_NORM_K);
+}
+
 template <int BN, int WAVES, int KSTEPS, int PRO, int EPI>
 static void launch_skinny(const SkinnyArgs &a, hipStream_t s) {
   const dim3 grid((a.N + BN - 1) / BN, static_cast<unsigned>((a.M + SK_BM - 1) / SK_BM));
@@ -385,7 +762,16 @@ extern "C" int vk_norm_linear(const void *x, const void *norm_w, float eps, cons
   p.eps = eps;
   hipStream_t s = VK_STREAM(stream);
   int rc;
-  if (norm_w) {
+  if (panel_ok(p, norm_w ? PRO_NORM : PRO_NONE)) {
+    if (norm_w)
+      rc = swiglu ? launch_panel<PRO_NORM, EPI_SWIGLU>(p, s)
+                  : (out_dtype == VK_DTYPE_F32 ? launch_panel<PRO_NORM, EPI_F32>(p, s)
+                                               : launch_panel<PRO_NORM, EPI_BF16>(p, s));
+    else
+      rc = swiglu ? launch_panel<PRO_NONE, EPI_SWIGLU>(p, s)
+                  : (out_dtype == VK_DTYPE_F32 ? launch_panel<PRO_NONE, EPI_F32>(p, s)
+                                               : launch_panel<PRO_NONE, EPI_BF16>(p, s));
+  } else if (norm_w) {
     if (swiglu)
       rc = dispatch_k<32, PRO_NORM, EPI_SWIGLU>(p, s);
     else if (out_dtype == VK_DTYPE_F32)
@@ -411,7 +797,8 @@ extern "C" int vk_linear_residual(const void *a, const void *w, void *x, int64_t
   VK_CHECK_ARG(vk_aligned16(a) && vk_aligned16(w) && vk_aligned16(x), "linear_residual: alignment");
   if (M == 0) return VK_OK;
   SkinnyArgs p = base_args(a, w, x, M, N, K);
-  const int rc = dispatch_k<32, PRO_NONE, EPI_RESID>(p, VK_STREAM(stream));
+  const int rc = panel_ok(p, PRO_NONE) ? launch_panel<PRO_NONE, EPI_RESID>(p, VK_STREAM(stream))
+                                       : dispatch_k<32, PRO_NONE, EPI_RESID>(p, VK_STREAM(stream));
   if (rc != VK_OK) return rc;
   return launch_status("linear_residual");
 }
@@ -423,13 +810,13 @@ extern "C" int vk_norm_qkv_rope_cache(const void *x, const int64_t *tok, int64_t
                                       const int32_t *seq, void *q, void *k_cache, void *v_cache, int64_t stride_cb,
                                       int64_t stride_cs, int64_t cache_rows, int64_t cache_len, int64_t M, int32_t K,
                                       int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void *stream) {
-  VK_CHECK_ARG(x && norm_w && w_qkv && q_norm_w && k_norm_w && cos_t && sin_t && pos && seq && q && k_cache &&
-                   v_cache,
+  VK_CHECK_ARG(x && w_qkv && q_norm_w && k_norm_w && cos_t && sin_t && pos && seq && q && k_cache && v_cache,
                "norm_qkv_rope_cache: null pointer");
+  VK_CHECK_ARG(norm_w || !tok, "norm_qkv_rope_cache: the embedding gather needs norm_w");
   VK_CHECK_ARG(head_dim == 64, "norm_qkv_rope_cache: built for head_dim 64");
   VK_CHECK_ARG(tok == nullptr || (x_store != nullptr && vocab > 0), "norm_qkv_rope_cache: embedding needs x_store");
   VK_CHECK_ARG(table_dtype == VK_DTYPE_BF16 || table_dtype == VK_DTYPE_F32, "norm_qkv_rope_cache: table dtype");
-  VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w_qkv) && vk_aligned16(norm_w) && vk_aligned16(q) &&
+  VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w_qkv) && (!norm_w || vk_aligned16(norm_w)) && vk_aligned16(q) &&
                    vk_aligned16(q_norm_w) && vk_aligned16(k_norm_w) && vk_aligned16(cos_t) && vk_aligned16(sin_t),
                "norm_qkv_rope_cache: alignment");
   if (M == 0) return VK_OK;
@@ -457,7 +844,13 @@ extern "C" int vk_norm_qkv_rope_cache(const void *x, const int64_t *tok, int64_t
   p.H = n_heads;
   p.HKV = n_kv_heads;
   hipStream_t s = VK_STREAM(stream);
-  const int rc = tok ? dispatch_k<64, PRO_EMBED_NORM, EPI_ROPE>(p, s) : dispatch_k<64, PRO_NORM, EPI_ROPE>(p, s);
+  int rc;
+  if (!norm_w)  // x is the normalised activation already
+    rc = panel_ok(p, PRO_NONE) ? launch_panel<PRO_NONE, EPI_ROPE>(p, s) : dispatch_k<64, PRO_NONE, EPI_ROPE>(p, s);
+  else if (panel_ok(p, PRO_NORM))
+    rc = tok ? launch_panel<PRO_EMBED_NORM, EPI_ROPE>(p, s) : launch_panel<PRO_NORM, EPI_ROPE>(p, s);
+  else
+    rc = tok ? dispatch_k<64, PRO_EMBED_NORM, EPI_ROPE>(p, s) : dispatch_k<64, PRO_NORM, EPI_ROPE>(p, s);
   if (rc != VK_OK) return rc;
   return launch_status("norm_qkv_rope_cache");
 }

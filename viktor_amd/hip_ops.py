@@ -288,15 +288,16 @@ def select_update(bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_o
 def norm_qkv_rope_cache(x, norm_w, eps, w_qkv, q_norm_w, k_norm_w, cos, sin, pos, seq, k_cache, v_cache, n_heads,
                         n_kv_heads, head_dim, rope_pos=None, tok=None, x_store=None):
     """Decode-step fusion: h = RMSNorm(x) * norm_w (or, with tok, x = emb[tok] where `x` is the embedding
-    table, stored into x_store), qkv = h @ w_qkv^T, then QK-norm + RoPE + KV-cache write as qkv_rope_cache.
-    Returns q [M, H, D]. Same rounding points as add_rmsnorm + linear + qkv_rope_cache."""
+    table, stored into x_store; norm_w None: h = x), qkv = h @ w_qkv^T, then QK-norm + RoPE + KV-cache write
+    as qkv_rope_cache. Returns q [M, H, D]. Same rounding points as add_rmsnorm + linear + qkv_rope_cache."""
     require_device(x, "norm_qkv_rope_cache")
     M = tok.shape[0] if tok is not None else x.shape[0]
     K = x.shape[1]
     _require(x.dtype == BF16 and w_qkv.dtype == BF16 and w_qkv.shape == ((n_heads + 2 * n_kv_heads) * head_dim, K),
              "norm_qkv_rope_cache: shapes")
-    _require(tok is None or (tok.dtype == torch.long and x_store is not None and x_store.shape == (M, K)),
-             "norm_qkv_rope_cache: embedding gather needs tok int64 and x_store [M, K]")
+    _require(tok is None or (tok.dtype == torch.long and x_store is not None and x_store.shape == (M, K)
+                             and norm_w is not None),
+             "norm_qkv_rope_cache: embedding gather needs tok int64, x_store [M, K] and norm_w")
     _require(pos.dtype == torch.int32 and seq.dtype == torch.int32 and pos.shape == (M,) and seq.shape == (M,),
              "norm_qkv_rope_cache: pos / seq int32 [M]")
     _require(rope_pos is None or (rope_pos.dtype == torch.int32 and rope_pos.shape == (M,)), "norm_qkv_rope_cache: rope_pos")
