@@ -530,25 +530,35 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   }
 }
 
-// out[b, h] = merge of the nparts partials of b's column (member b % G, head h) in its group's KV head
+// out[b, h] = merge of the NP partials of b's column (member b % G, head h) in its group's KV head; all
+// partial loads are issued before the first use (NP is a compile-time count)
+template <int NP>
 __global__ __launch_bounds__(DA_H * DA_D) void grouped_combine_kernel(const float *__restrict__ ws_o,
                                                                       const float *__restrict__ ws_ml,
-                                                                      bf16_t *__restrict__ out, int G, int nparts) {
+                                                                      bf16_t *__restrict__ out, int G) {
   const int64_t b = blockIdx.x;
   const int h = threadIdx.x / DA_D, d = threadIdx.x % DA_D;
   const int64_t p = b / G;
   const int NC = 4 * G;
   const int j = 4 * static_cast<int>(b % G) + (h & 3);
-  const int64_t base0 = (p * DA_HKV + (h >> 2)) * nparts * NC + j;
-  float M = -INFINITY;
-  for (int k = 0; k < nparts; ++k) M = fmaxf(M, ws_ml[(base0 + static_cast<int64_t>(k) * NC) * 2]);
-  float L = 0.f, N = 0.f;
-  for (int k = 0; k < nparts; ++k) {
+  const int64_t base0 = (p * DA_HKV + (h >> 2)) * NP * NC + j;
+  float2 ml[NP];
+  float o[NP];
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
     const int64_t base = base0 + static_cast<int64_t>(k) * NC;
-    const float mk = ws_ml[base * 2];
-    const float e = mk == -INFINITY ? 0.f : exp2f(mk - M);
-    L += e * ws_ml[base * 2 + 1];
-    N += e * ws_o[base * DA_D + d];
+    ml[k] = *reinterpret_cast<const float2 *>(ws_ml + base * 2);
+    o[k] = ws_o[base * DA_D + d];
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < NP; ++k) M = fmaxf(M, ml[k].x);
+  float L = 0.f, N = 0.f;
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
+    const float e = ml[k].x == -INFINITY ? 0.f : exp2f(ml[k].x - M);
+    L += e * ml[k].y;
+    N += e * o[k];
   }
   out[(b * DA_H + h) * DA_D + d] = f2bf(N / L);
 }
@@ -568,11 +578,9 @@ static GroupedLayout grouped_layout(int64_t B, int G, int64_t pre_max, int64_t o
   const int64_t tmax = (pre_max + GU_TILE - 1) / GU_TILE + G * ((own_max + GU_TILE - 1) / GU_TILE);
   const int64_t cap = tmax / GU_WAVES;
   if (np > cap) np = cap;
-  if (np > 64) np = 64;
+  if (np > 16) np = 16;
   if (np < 1) np = 1;
-#ifdef VK_GU_NPARTS
-  np = VK_GU_NPARTS;
-#endif
+  while (np & (np - 1)) np &= np - 1;  // a power of two (the combine kernel is instantiated per count)
   L.nparts = static_cast<int>(np);
   const int64_t cols = pairs * L.nparts * 4 * G;
   L.o = 0;
@@ -692,7 +700,14 @@ extern "C" int vk_decode_attention_grouped(const void *q, const void *k_prefix, 
 #undef VK_GROUPED
   const int rc = launch_status("decode_attention_grouped");
   if (rc != VK_OK) return rc;
-  grouped_combine_kernel<<<static_cast<unsigned>(B), DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml,
-                                                                         static_cast<bf16_t *>(out), G, L.nparts);
+  const dim3 cgrid(static_cast<unsigned>(B));
+  bf16_t *ob = static_cast<bf16_t *>(out);
+  switch (L.nparts) {
+    case 1: grouped_combine_kernel<1><<<cgrid, DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml, ob, G); break;
+    case 2: grouped_combine_kernel<2><<<cgrid, DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml, ob, G); break;
+    case 4: grouped_combine_kernel<4><<<cgrid, DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml, ob, G); break;
+    case 8: grouped_combine_kernel<8><<<cgrid, DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml, ob, G); break;
+    default: grouped_combine_kernel<16><<<cgrid, DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml, ob, G); break;
+  }
   return launch_status("decode_attention_grouped combine");
 }

@@ -28,7 +28,9 @@ int launch_status(const char *what) {
   return VK_OK;
 }
 
-// CH = number of 8-element chunks each lane owns (d <= 512 * CH).
+// CH = number of 8-element chunks each lane owns (d <= 512 * CH). Every load (row, delta, weight) is
+// issued before the reduction, unconditionally (chunk indices clamped, surplus chunks masked), so a row
+// costs one memory round trip.
 template <int CH, bool EMBED>
 __global__ __launch_bounds__(256) void rmsnorm_rows(bf16_t *__restrict__ x, const bf16_t *__restrict__ delta,
                                                     const int64_t *__restrict__ tok, const bf16_t *__restrict__ emb,
@@ -45,29 +47,34 @@ __global__ __launch_bounds__(256) void rmsnorm_rows(bf16_t *__restrict__ x, cons
     zero_row = t < 0 || t >= vocab;
     src = emb + (zero_row ? 0 : t) * d;
   }
+  u32x4 a[CH], b[CH], wv[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    int ci = lane + c * kWave;
+    ci = ci < nch ? ci : nch - 1;
+    a[c] = *reinterpret_cast<const u32x4 *>(src + ci * 8);
+    if (!EMBED && delta != nullptr) b[c] = *reinterpret_cast<const u32x4 *>(delta + row * d + ci * 8);
+    wv[c] = *reinterpret_cast<const u32x4 *>(w + ci * 8);
+  }
   float v[CH][8];
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int ci = lane + c * kWave;
-    if (ci < nch) {
-      u32x4 a = *reinterpret_cast<const u32x4 *>(src + ci * 8);
-      if (EMBED && zero_row) a = u32x4{0u, 0u, 0u, 0u};
-      if (!EMBED && delta != nullptr) {
-        const u32x4 b = *reinterpret_cast<const u32x4 *>(delta + row * d + ci * 8);
+    if (EMBED && zero_row) a[c] = u32x4{0u, 0u, 0u, 0u};
+    if (!EMBED && delta != nullptr) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[j] = pack_bf(lo_bf(a[j]) + lo_bf(b[j]), hi_bf(a[j]) + hi_bf(b[j]));
-        *reinterpret_cast<u32x4 *>(x + row * d + ci * 8) = a;
-      }
-      if (EMBED) *reinterpret_cast<u32x4 *>(x + row * d + ci * 8) = a;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[c][2 * j] = lo_bf(a[j]);
-        v[c][2 * j + 1] = hi_bf(a[j]);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ss += v[c][j] * v[c][j];
+      for (int j = 0; j < 4; ++j) a[c][j] = pack_bf(lo_bf(a[c][j]) + lo_bf(b[c][j]), hi_bf(a[c][j]) + hi_bf(b[c][j]));
     }
+    if ((EMBED || delta != nullptr) && ci < nch) *reinterpret_cast<u32x4 *>(x + row * d + ci * 8) = a[c];
+    const float keep = ci < nch ? 1.f : 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[c][2 * j] = lo_bf(a[c][j]);
+      v[c][2 * j + 1] = hi_bf(a[c][j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += keep * (v[c][j] * v[c][j]);
   }
   ss = wave_sum(ss);
   const float r = rsqrtf(ss / static_cast<float>(d) + eps);
@@ -75,11 +82,10 @@ __global__ __launch_bounds__(256) void rmsnorm_rows(bf16_t *__restrict__ x, cons
   for (int c = 0; c < CH; ++c) {
     const int ci = lane + c * kWave;
     if (ci < nch) {
-      const u32x4 wv = *reinterpret_cast<const u32x4 *>(w + ci * 8);
       u32x4 o;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        o[j] = pack_bf(v[c][2 * j] * r * lo_bf(wv[j]), v[c][2 * j + 1] * r * hi_bf(wv[j]));
+        o[j] = pack_bf(v[c][2 * j] * r * lo_bf(wv[c][j]), v[c][2 * j + 1] * r * hi_bf(wv[c][j]));
       *reinterpret_cast<u32x4 *>(h + row * d + ci * 8) = o;
     }
   }
