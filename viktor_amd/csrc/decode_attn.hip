@@ -307,34 +307,77 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   constexpr int LDS_V = GU_WAVES * GU_TILE * GU_PITCH * 2;
   constexpr int LDS_M = (GU_WAVES * NC * 64 + 2 * GU_WAVES * NC) * 4;
   __shared__ __attribute__((aligned(16))) char smem[LDS_V > LDS_M ? LDS_V : LDS_M];
-  __shared__ int seg_end[G + 1];  // cumulative tile counts: segment 0 = prefix, 1 + m = member m's own rows
-  __shared__ int seg_len[G + 1];
 
-  // wave-uniform values go through readfirstlane so the tile loop and segment search stay scalar
+  // wave-uniform values go through readfirstlane / readlane so the tile loop and segment search stay scalar
   const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int part = blockIdx.x, p = blockIdx.y, kvh = blockIdx.z;
   const int col = lane & 15, g = lane >> 4;
+  // 1-D grid, XCD-aware: workgroup i runs on XCD i % 8, which takes a contiguous range of the logical order
+  // (group, part, KV head) with the KV head fastest, so the two workgroups that read the two halves of the
+  // same 256-byte cache rows run back to back on one XCD (a bijection for any count)
+  const int tiles = gridDim.x, pid = blockIdx.x, xcd = pid & 7, idx = pid >> 3;
+  const int lt_id = xcd * (tiles >> 3) + min(xcd, tiles & 7) + idx;
+  const int kvh = lt_id & 1, part = (lt_id >> 1) % nparts, p = (lt_id >> 1) / nparts;
 
-  if (wid == 0) {
-    int64_t len = 0;
-    if (lane == 0) {
-      len = pre_len[p];
-      len = len < 1 ? 1 : (len > pre_max ? pre_max : len);
-    } else if (lane <= G) {
-      len = own_len[static_cast<int64_t>(p) * G + lane - 1];
-      len = len < 0 ? 0 : (len > own_max ? own_max : len);
-    }
-    int incl = static_cast<int>((len + GU_TILE - 1) / GU_TILE);
+  // The part's tiles: its static share of the prefix tiles (sized by pre_max, so that they are known before
+  // any length is read; tiles past the group's actual prefix length are fully masked), then the own rows of
+  // its members [mb0, mb1). In a rollout every member has the same length, so parts are balanced.
+  const int tp_all = static_cast<int>((pre_max + GU_TILE - 1) / GU_TILE);
+  const int pt0 = tp_all * part / nparts, npre = tp_all * (part + 1) / nparts - pt0;
+  const int mb0 = G * part / nparts, nmem = G * (part + 1) / nparts - mb0;
+  const bf16_t *kpre = kp + p * stride_pb + kvh * DA_D, *vpre = vp + p * stride_pb + kvh * DA_D;
+
+  struct TileRef {
+    const bf16_t *k, *v;
+    int64_t stride;
+    int row0, len, clamp, seg;
+  };
+  auto row_off = [&](const TileRef &r, int pb) {
+    int rr = r.row0 + 16 * pb + col;
+    rr = rr < r.clamp ? rr : r.clamp - 1;
+    return static_cast<int64_t>(rr) * r.stride + 8 * g;
+  };
+  u32x4 kf[2][2], vf[2][2];
+  auto load = [&](u32x4 (&f)[2][2], const bf16_t *base, const TileRef &r) {
 #pragma unroll
-    for (int off = 1; off < 32; off <<= 1) {
-      const int v = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += v;
-    }
-    if (lane <= G) {
-      seg_end[lane] = incl;
-      seg_len[lane] = static_cast<int>(len);
-    }
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) f[pb][c] = *reinterpret_cast<const u32x4 *>(base + row_off(r, pb) + 32 * c);
+  };
+  // the first tile is a prefix tile whenever wid < npre: its loads go out before anything else (rows
+  // clamped to pre_max - 1, always valid; its mask waits for the length)
+  TileRef cur;
+  cur.k = kpre;
+  cur.v = vpre;
+  cur.stride = stride_ps;
+  cur.row0 = (pt0 + wid) * GU_TILE;
+  cur.len = 0;
+  cur.clamp = static_cast<int>(pre_max);
+  cur.seg = 0;
+  const bool spec = wid < npre;
+  if (spec) {
+    load(kf, cur.k, cur);
+    asm volatile("" ::: "memory");
+    load(vf, cur.v, cur);
   }
+
+  // lengths and the segment table, per wave in registers: lane 0 = prefix, lane 1 + i = member mb0 + i
+  int len = 0, cnt = 0;
+  if (lane == 0) {
+    int64_t l = pre_len[p];
+    len = static_cast<int>(l < 1 ? 1 : (l > pre_max ? pre_max : l));
+    cnt = npre;
+  } else if (lane <= nmem) {
+    int64_t l = own_len[static_cast<int64_t>(p) * G + mb0 + lane - 1];
+    len = static_cast<int>(l < 0 ? 0 : (l > own_max ? own_max : l));
+    cnt = (len + GU_TILE - 1) / GU_TILE;
+  }
+  int incl = cnt;
+#pragma unroll
+  for (int off = 1; off < 32; off <<= 1) {
+    const int v = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += v;
+  }
+  const int T = __builtin_amdgcn_readlane(incl, nmem);  // tiles of this part
 
   // Q^T fragments: column j = 16 cb + col -> member j / 4, head kvh * 4 + j % 4, the two 32-wide halves of D
   bf16x8 bq[NCB][2];
@@ -360,57 +403,43 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     m_run[cb] = -INFINITY;
     l_run[cb] = 0.f;
   }
-  __syncthreads();
-  const int T = __builtin_amdgcn_readfirstlane(seg_end[G]);
-  const int t_begin = static_cast<int>(static_cast<int64_t>(T) * part / nparts);
-  const int t_end = static_cast<int>(static_cast<int64_t>(T) * (part + 1) / nparts);
   bf16_t *vsh = reinterpret_cast<bf16_t *>(smem) + wid * GU_TILE * GU_PITCH;
 
-  // tile t -> segment (monotone search from the previous segment), first row, row count, row pointers
-  struct TileRef {
-    const bf16_t *k, *v;
-    int64_t stride;
-    int row0, len, seg;
-  };
+  // local tile t -> segment (monotone search from the previous segment), first row, lengths, row pointers
   auto locate = [&](int t, int s) {
-    while (t >= __builtin_amdgcn_readfirstlane(seg_end[s])) ++s;
+    while (t >= __builtin_amdgcn_readlane(incl, s)) ++s;
     TileRef r;
     r.seg = s;
-    r.row0 = (t - (s ? __builtin_amdgcn_readfirstlane(seg_end[s - 1]) : 0)) * GU_TILE;
-    r.len = __builtin_amdgcn_readfirstlane(seg_len[s]);
+    r.len = __builtin_amdgcn_readlane(len, s);
     if (s == 0) {
-      r.k = kp + p * stride_pb + kvh * DA_D;
-      r.v = vp + p * stride_pb + kvh * DA_D;
+      r.k = kpre;
+      r.v = vpre;
       r.stride = stride_ps;
+      r.row0 = (pt0 + t) * GU_TILE;
+      r.clamp = static_cast<int>(pre_max);
     } else {
-      const int64_t b = static_cast<int64_t>(p) * G + s - 1;
+      const int64_t b = static_cast<int64_t>(p) * G + mb0 + s - 1;
       r.k = ks + b * stride_sb + kvh * DA_D;
       r.v = vs + b * stride_sb + kvh * DA_D;
       r.stride = stride_ss;
+      r.row0 = (t - __builtin_amdgcn_readlane(incl, s - 1)) * GU_TILE;
+      r.clamp = r.len;
     }
     return r;
   };
-  auto row_off = [&](const TileRef &r, int pb) {
-    int rr = r.row0 + 16 * pb + col;
-    rr = rr < r.len ? rr : r.len - 1;
-    return static_cast<int64_t>(rr) * r.stride + 8 * g;
-  };
-  u32x4 kf[2][2], vf[2][2];
-  auto load = [&](u32x4 (&f)[2][2], const bf16_t *base, const TileRef &r) {
-#pragma unroll
-    for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-      for (int c = 0; c < 2; ++c) f[pb][c] = *reinterpret_cast<const u32x4 *>(base + row_off(r, pb) + 32 * c);
-  };
 
-  // This wave's tiles are t0, t0 + W, ... (< t_end). The next tile's K / V are loaded while the current
+  // This wave's tiles are t0 = wid, wid + W, ... (< T). The next tile's K / V are loaded while the current
   // one is consumed; at the end the current tile is loaded again, so every load is unconditional.
-  const int t0 = t_begin + wid;
+  const int t0 = wid, t_end = T;
   if (t0 < t_end) {
-    TileRef cur = locate(t0, 0);
-    load(kf, cur.k, cur);
-    asm volatile("" ::: "memory");
-    load(vf, cur.v, cur);
+    if (spec) {
+      cur.len = __builtin_amdgcn_readlane(len, 0);
+    } else {
+      cur = locate(t0, 0);
+      load(kf, cur.k, cur);
+      asm volatile("" ::: "memory");
+      load(vf, cur.v, cur);
+    }
     for (int t = t0; t < t_end; t += GU_WAVES) {
       const int tn = t + GU_WAVES < t_end ? t + GU_WAVES : t;
       const TileRef nxt = locate(tn, cur.seg);
@@ -426,7 +455,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
                                                                  st[pb][cb], 0, 0, 0);
         }
       load(kf, nxt.k, nxt);
-      const int member = cur.seg - 1;  // -1: prefix tile, every column attends
+      const int member = cur.seg ? mb0 + cur.seg - 1 : -1;  // -1: prefix tile, every column attends
       bf16x8 pf[NCB];
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
@@ -594,7 +623,7 @@ static void launch_grouped(const bf16_t *q, const bf16_t *kp, const bf16_t *vp, 
                            int64_t stride_pb, int64_t stride_ps, int64_t pre_max, const bf16_t *ks, const bf16_t *vs,
                            const int32_t *own_len, int64_t stride_sb, int64_t stride_ss, int64_t own_max, int nparts,
                            float *ws_o, float *ws_ml, float scale_log2, hipStream_t s) {
-  const dim3 grid(nparts, static_cast<unsigned>(P), DA_HKV);
+  const dim3 grid(static_cast<unsigned>(P * nparts * DA_HKV));
   grouped_attn_kernel<G><<<grid, GU_WAVES * 64, 0, s>>>(q, kp, vp, pre_len, stride_pb, stride_ps, pre_max, ks, vs,
                                                         own_len, stride_sb, stride_ss, own_max, nparts, ws_o, ws_ml,
                                                         scale_log2);
