@@ -20,13 +20,12 @@ constexpr int kWave = 64;
 
 __device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float(static_cast<uint32_t>(v) << 16); }
 
-// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN (the rounding torch and Triton use).
-__device__ __forceinline__ bf16_t f2bf(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  const uint32_t nan = (u >> 16) | 0x40u;  // quiet NaN, sign and payload top kept
-  return static_cast<bf16_t>((u & 0x7fffffffu) > 0x7f800000u ? nan : rne);  // a select, no branch
-}
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16 with gfx950's v_cvt_pk_bf16_f32: round to nearest even (the rounding torch and Triton
+// use), NaN -> quiet NaN; one instruction per pair of values.
+__device__ __forceinline__ bf16_t f2bf(float f) { return __builtin_bit_cast(bf16_t, static_cast<__bf16>(f)); }
 
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 
@@ -34,7 +33,8 @@ __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ uint32_t pack_bf(float lo, float hi) {
-  return static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+  const f32x2_v v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v));
 }
 
 // Butterfly reductions over the 64 lanes of a wavefront (every lane gets the result).

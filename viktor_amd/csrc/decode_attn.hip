@@ -289,9 +289,6 @@ static int device_cus_cached() {
 // column; a small combine kernel merges the parts of each (sequence, head).
 
 constexpr int GU_WAVES = 4;
-#ifndef VK_GU_WG_PER_CU
-#define VK_GU_WG_PER_CU 2  // workgroups per CU the part count aims for (one resident round)
-#endif
 constexpr int GU_TILE = 32;
 constexpr int GU_PITCH = 72;  // one KV head: 64 + 8 pad
 
@@ -318,18 +315,18 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   const int lt_id = xcd * (tiles >> 3) + min(xcd, tiles & 7) + idx;
   const int kvh = lt_id & 1, part = (lt_id >> 1) % nparts, p = (lt_id >> 1) / nparts;
 
-  // The part's tiles: its static share of the prefix tiles (sized by pre_max, so that they are known before
-  // any length is read; tiles past the group's actual prefix length are fully masked), then the own rows of
-  // its members [mb0, mb1). In a rollout every member has the same length, so parts are balanced.
+  // The part's tiles: its static share of the prefix tiles (sized by pre_max, so they are known before any
+  // length is read; tiles past the group's actual prefix length are fully masked), then its share of the
+  // own-row tiles of all G members taken as one sequence (member 0's tiles, then member 1's, ...). Both
+  // shares are equal cuts, so parts are balanced for any part count.
   const int tp_all = static_cast<int>((pre_max + GU_TILE - 1) / GU_TILE);
   const int pt0 = tp_all * part / nparts, npre = tp_all * (part + 1) / nparts - pt0;
-  const int mb0 = G * part / nparts, nmem = G * (part + 1) / nparts - mb0;
   const bf16_t *kpre = kp + p * stride_pb + kvh * DA_D, *vpre = vp + p * stride_pb + kvh * DA_D;
 
   struct TileRef {
     const bf16_t *k, *v;
     int64_t stride;
-    int row0, len, clamp, seg;
+    int row0, len, clamp, seg, mc;  // seg: 0 = prefix, 1 + m = member m's own rows; mc: member cursor
   };
   auto row_off = [&](const TileRef &r, int pb) {
     int rr = r.row0 + 16 * pb + col;
@@ -353,6 +350,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   cur.len = 0;
   cur.clamp = static_cast<int>(pre_max);
   cur.seg = 0;
+  cur.mc = 0;
   const bool spec = wid < npre;
   if (spec) {
     load(kf, cur.k, cur);
@@ -360,16 +358,16 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     load(vf, cur.v, cur);
   }
 
-  // lengths and the segment table, per wave in registers: lane 0 = prefix, lane 1 + i = member mb0 + i
+  // lengths, per wave in registers: lane m < G = member m's own rows, lane G = the prefix; incl = inclusive
+  // prefix sum of the members' own-tile counts
   int len = 0, cnt = 0;
-  if (lane == 0) {
-    int64_t l = pre_len[p];
-    len = static_cast<int>(l < 1 ? 1 : (l > pre_max ? pre_max : l));
-    cnt = npre;
-  } else if (lane <= nmem) {
-    int64_t l = own_len[static_cast<int64_t>(p) * G + mb0 + lane - 1];
+  if (lane < G) {
+    const int64_t l = own_len[static_cast<int64_t>(p) * G + lane];
     len = static_cast<int>(l < 0 ? 0 : (l > own_max ? own_max : l));
     cnt = (len + GU_TILE - 1) / GU_TILE;
+  } else if (lane == G) {
+    const int64_t l = pre_len[p];
+    len = static_cast<int>(l < 1 ? 1 : (l > pre_max ? pre_max : l));
   }
   int incl = cnt;
 #pragma unroll
@@ -377,7 +375,9 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     const int v = __shfl_up(incl, off, 64);
     if (lane >= off) incl += v;
   }
-  const int T = __builtin_amdgcn_readlane(incl, nmem);  // tiles of this part
+  const int own_all = __builtin_amdgcn_readlane(incl, G - 1);
+  const int ou0 = static_cast<int>(static_cast<int64_t>(own_all) * part / nparts);
+  const int T = npre + static_cast<int>(static_cast<int64_t>(own_all) * (part + 1) / nparts) - ou0;  // tiles
 
   // Q^T fragments: column j = 16 cb + col -> member j / 4, head kvh * 4 + j % 4, the two 32-wide halves of D
   bf16x8 bq[NCB][2];
@@ -405,24 +405,30 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   }
   bf16_t *vsh = reinterpret_cast<bf16_t *>(smem) + wid * GU_TILE * GU_PITCH;
 
-  // local tile t -> segment (monotone search from the previous segment), first row, lengths, row pointers
-  auto locate = [&](int t, int s) {
-    while (t >= __builtin_amdgcn_readlane(incl, s)) ++s;
+  // local tile t -> prefix tile pt0 + t (t < npre) or own-row tile ou0 + t - npre (member found by a
+  // monotone search from the cursor), first row, lengths, row pointers
+  auto locate = [&](int t, int m) {
     TileRef r;
-    r.seg = s;
-    r.len = __builtin_amdgcn_readlane(len, s);
-    if (s == 0) {
+    if (t < npre) {
+      r.seg = 0;
+      r.mc = m;
+      r.len = __builtin_amdgcn_readlane(len, G);
       r.k = kpre;
       r.v = vpre;
       r.stride = stride_ps;
       r.row0 = (pt0 + t) * GU_TILE;
       r.clamp = static_cast<int>(pre_max);
     } else {
-      const int64_t b = static_cast<int64_t>(p) * G + mb0 + s - 1;
+      const int u = ou0 + t - npre;
+      while (u >= __builtin_amdgcn_readlane(incl, m)) ++m;
+      r.seg = 1 + m;
+      r.mc = m;
+      r.len = __builtin_amdgcn_readlane(len, m);
+      const int64_t b = static_cast<int64_t>(p) * G + m;
       r.k = ks + b * stride_sb + kvh * DA_D;
       r.v = vs + b * stride_sb + kvh * DA_D;
       r.stride = stride_ss;
-      r.row0 = (t - __builtin_amdgcn_readlane(incl, s - 1)) * GU_TILE;
+      r.row0 = (u - (m ? __builtin_amdgcn_readlane(incl, m - 1) : 0)) * GU_TILE;
       r.clamp = r.len;
     }
     return r;
@@ -433,7 +439,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   const int t0 = wid, t_end = T;
   if (t0 < t_end) {
     if (spec) {
-      cur.len = __builtin_amdgcn_readlane(len, 0);
+      cur.len = __builtin_amdgcn_readlane(len, G);
     } else {
       cur = locate(t0, 0);
       load(kf, cur.k, cur);
@@ -442,7 +448,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     }
     for (int t = t0; t < t_end; t += GU_WAVES) {
       const int tn = t + GU_WAVES < t_end ? t + GU_WAVES : t;
-      const TileRef nxt = locate(tn, cur.seg);
+      const TileRef nxt = locate(tn, cur.mc);
       f32x4 st[2][NCB];
 #pragma unroll
       for (int pb = 0; pb < 2; ++pb)
@@ -455,38 +461,53 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
                                                                  st[pb][cb], 0, 0, 0);
         }
       load(kf, nxt.k, nxt);
-      const int member = cur.seg ? mb0 + cur.seg - 1 : -1;  // -1: prefix tile, every column attends
+      const int member = cur.seg - 1;  // -1: prefix tile, every column attends
+      // a prefix tile inside the prefix needs no mask (the common case: a uniform branch)
+      const bool full = member < 0 && cur.row0 + GU_TILE <= cur.len;
       bf16x8 pf[NCB];
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
-        const bool col_ok = member < 0 || ((16 * cb + col) >> 2) == member;
         float sv[8];
-        float mx = -INFINITY;
+        if (full) {
 #pragma unroll
-        for (int pb = 0; pb < 2; ++pb)
+          for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = cur.row0 + 16 * pb + 4 * g + i;
-            const float v = (col_ok && r < cur.len) ? st[pb][cb][i] * scale_log2 : -INFINITY;
-            sv[pb * 4 + i] = v;
-            mx = fmaxf(mx, v);
-          }
+            for (int i = 0; i < 4; ++i) sv[pb * 4 + i] = st[pb][cb][i] * scale_log2;
+        } else {
+          // rows of this lane's group g that exist: 16 pb + i < nv (0 for a column of another member)
+          const bool col_ok = member < 0 || ((16 * cb + col) >> 2) == member;
+          const int nv = col_ok ? cur.len - cur.row0 - 4 * g : 0;
+#pragma unroll
+          for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              sv[pb * 4 + i] = 16 * pb + i < nv ? st[pb][cb][i] * scale_log2 : -INFINITY;
+        }
+        float mx = sv[0];
+#pragma unroll
+        for (int jj = 1; jj < 8; ++jj) mx = fmaxf(mx, sv[jj]);
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float m_new = fmaxf(m_run[cb], mx);
         const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a column with no row yet stays empty
-        const float alpha = exp2f(m_run[cb] - m_use);
-        float ps = 0.f;
+        // exponents are <= 0: the bare v_exp_f32 (no range reduction needed)
+        float e[8], ps = 0.f;
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
-          const float e = exp2f(sv[jj] - m_use);
-          ps += e;
-          pf[cb][jj] = __builtin_bit_cast(__bf16, f2bf(e));
+          e[jj] = __builtin_amdgcn_exp2f(sv[jj] - m_use);
+          ps += e[jj];
         }
-        l_run[cb] = l_run[cb] * alpha + ps;
-        m_run[cb] = m_new;
+        pf[cb] = __builtin_bit_cast(bf16x8, u32x4{pack_bf(e[0], e[1]), pack_bf(e[2], e[3]), pack_bf(e[4], e[5]),
+                                                   pack_bf(e[6], e[7])});
+        // rescale only when some column's running max moved (alpha is exactly 1 otherwise)
+        if (__builtin_amdgcn_ballot_w64(m_new != m_run[cb])) {
+          const float alpha = __builtin_amdgcn_exp2f(m_run[cb] - m_use);
+          l_run[cb] *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) acc[cb][dt] *= alpha;
+          for (int dt = 0; dt < 4; ++dt) acc[cb][dt] *= alpha;
+        }
+        l_run[cb] += ps;
+        m_run[cb] = m_new;
       }
 #pragma unroll
       for (int pb = 0; pb < 2; ++pb)
@@ -597,19 +618,20 @@ struct GroupedLayout {
   int64_t o, ml, total;  // offsets / size in floats
 };
 
-// Parts per (group, KV head): about VK_GU_WG_PER_CU 4-wave workgroups per CU over the launch, and at least
-// one tile per wave at the longest lengths.
+// Parts per (group, KV head): one resident round of 4-wave workgroups over the CUs, and at least one tile
+// per wave at the longest lengths.
 static GroupedLayout grouped_layout(int64_t B, int G, int64_t pre_max, int64_t own_max, int cus) {
   GroupedLayout L{};
   const int64_t pairs = (B / G) * DA_HKV;
-  const int64_t target = static_cast<int64_t>(cus) * VK_GU_WG_PER_CU;
+  // resident 4-wave workgroups per CU at the kernel's register use (G <= 4: 4, G = 8: 3, G = 16: 1)
+  const int per_cu = G <= 4 ? 4 : (G == 8 ? 2 : 1);
+  const int64_t target = static_cast<int64_t>(cus) * per_cu;
   int64_t np = (target + pairs - 1) / pairs;
   const int64_t tmax = (pre_max + GU_TILE - 1) / GU_TILE + G * ((own_max + GU_TILE - 1) / GU_TILE);
   const int64_t cap = tmax / GU_WAVES;
   if (np > cap) np = cap;
-  if (np > 16) np = 16;
+  if (np > 16) np = 16;  // the combine kernel is instantiated for 1 .. 16 parts
   if (np < 1) np = 1;
-  while (np & (np - 1)) np &= np - 1;  // a power of two (the combine kernel is instantiated per count)
   L.nparts = static_cast<int>(np);
   const int64_t cols = pairs * L.nparts * 4 * G;
   L.o = 0;
@@ -732,11 +754,13 @@ extern "C" int vk_decode_attention_grouped(const void *q, const void *k_prefix, 
   const dim3 cgrid(static_cast<unsigned>(B));
   bf16_t *ob = static_cast<bf16_t *>(out);
   switch (L.nparts) {
-    case 1: grouped_combine_kernel<1><<<cgrid, DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml, ob, G); break;
-    case 2: grouped_combine_kernel<2><<<cgrid, DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml, ob, G); break;
-    case 4: grouped_combine_kernel<4><<<cgrid, DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml, ob, G); break;
-    case 8: grouped_combine_kernel<8><<<cgrid, DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml, ob, G); break;
-    default: grouped_combine_kernel<16><<<cgrid, DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml, ob, G); break;
+#define VK_COMBINE(NP) \
+  case NP: grouped_combine_kernel<NP><<<cgrid, DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml, ob, G); break;
+    VK_COMBINE(1) VK_COMBINE(2) VK_COMBINE(3) VK_COMBINE(4) VK_COMBINE(5) VK_COMBINE(6) VK_COMBINE(7)
+    VK_COMBINE(8) VK_COMBINE(9) VK_COMBINE(10) VK_COMBINE(11) VK_COMBINE(12) VK_COMBINE(13) VK_COMBINE(14)
+    VK_COMBINE(15) VK_COMBINE(16)
+#undef VK_COMBINE
+    default: return fail(VK_ERR_ARG, "decode_attention_grouped: part count %d", L.nparts);
   }
   return launch_status("decode_attention_grouped combine");
 }
