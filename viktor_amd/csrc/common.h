@@ -18,6 +18,19 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 
+// CUs of the current device, queried once per process (256 on MI355X; the launch heuristics use it).
+inline int device_cus_cached() {
+  static int cus = -1;
+  if (cus < 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+
 __device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float(static_cast<uint32_t>(v) << 16); }
 
 typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));

@@ -264,18 +264,6 @@ static int64_t workspace_bytes_for(int64_t B, const DecodeSplit &sp) {
   return B * sp.nsplit * DA_H * (DA_D + 2) * static_cast<int64_t>(sizeof(float));
 }
 
-static int device_cus_cached() {
-  static int cus = -1;
-  if (cus < 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-      cus = n;
-    else
-      cus = 256;
-  }
-  return cus;
-}
-
 
 // ---- groups of sequences that share one prefix (GSPO: G samples of one window) ----------------------
 //

@@ -368,7 +368,7 @@ __device__ __forceinline__ void pg_issue(char *base, const bf16_t *const *src, i
     __builtin_amdgcn_global_load_lds(src[j] + k0, (lds_void_t *)(base + (wid + 4 * j) * 1024), 16, 0, 0);
 }
 
-template <int EPI>
+template <int EPI, int KS>
 struct PanelShape {
   static constexpr bool SWI = EPI == EPI_SWIGLU;
   static constexpr int WR = SWI ? 2 * PG_BN : PG_BN;  // weight rows per tile
@@ -379,13 +379,18 @@ struct PanelShape {
   // with 2 workgroups per CU -- 4 slots (3 in flight) for 12 KB stages, 3 for the 20 KB SwiGLU stages
   static constexpr int STAGES = SWI ? 3 : 4;
   static constexpr int PARTB = PG_BM * (WR + 1) * 4;
-  static constexpr int BODY = STAGES * STAGEB > PARTB ? STAGES * STAGEB : PARTB;
+  static constexpr int RING = STAGES * STAGEB;  // one ring per K slice (KS slices)
+  static constexpr int BODY = KS * RING > PARTB ? KS * RING : PARTB;
   static constexpr int SMEM = BODY + PG_NORM_K * 2 + PG_BM * 4;  // + the RMSNorm weight and row sums
 };
 
-template <int PRO, int EPI>
-__global__ __launch_bounds__(256) void panel_gemm_kernel(const SkinnyArgs p, int m_blocks, int tiles) {
-  using S = PanelShape<EPI>;
+// KS = 2: 8 wavefronts, waves 0-3 take the first half of K and waves 4-7 the second, each half through
+// its own ring; the two partial tiles are summed in LDS (fixed order) before the epilogue. This halves the
+// latency chain of the K loop for the shapes with few workgroups (o / down / qkv projections).
+template <int PRO, int EPI, int KS>
+__global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p, int m_blocks, int tiles) {
+  static_assert(KS == 1 || (KS == 2 && PRO == PRO_NONE), "K halves only without the norm prologue");
+  using S = PanelShape<EPI, KS>;
   constexpr bool SWI = S::SWI;
   constexpr bool ROPE = EPI == EPI_ROPE;
   constexpr int HALVES = 2;  // 64 output columns = two 32-column halves in the epilogue
@@ -393,6 +398,7 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(const SkinnyArgs p, int
   __shared__ __attribute__((aligned(16))) char smem[S::SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wq = wid & 3, kh = wid >> 2;  // wave within its K slice, K slice
   // XCD-aware tile order: workgroup p runs on XCD p % 8, which owns a contiguous range of tiles; tiles are
   // numbered n-block-major, so the workgroups of one XCD share weight tiles (a bijection for any count)
   const int pid = blockIdx.x, xcd = pid & 7, idx = pid >> 3;
@@ -403,13 +409,13 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(const SkinnyArgs p, int
   const int n0 = nb * PG_BN;
   // K stays a run-time value (with the norm it is 512, checked on the host): with a constant trip count
   // the compiler unrolls the K loop, sees the ring offsets and drains every load before each LDS read
-  const int K = p.K, nk = K / PG_BK;
+  const int K = p.K, nk = K / (PG_BK * KS), kbase = kh * (K / KS);
   const int fr = lane & 15, fg = lane >> 4;
 
   // epilogue mapping: thread -> row m0 + tid / 8, columns 4 (tid % 8) .. + 3 of each 32-column half
-  const int rr = tid >> 3, sub = tid & 7;
+  const int rr = (tid >> 3) & (PG_BM - 1), sub = tid & 7;
   const int64_t erow = m0 + rr;
-  const bool row_ok = erow < p.M;
+  const bool row_ok = tid < 256 && erow < p.M;
 
   // 1. RoPE positions (the table loads depend on them)
   int64_t e_pos = 0, e_seq = 0, rp = 0;
@@ -437,20 +443,21 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(const SkinnyArgs p, int
   const bf16_t *src[S::LOADS];
 #pragma unroll
   for (int j = 0; j < S::LOADS; ++j) {
-    const int q = wid + 4 * j;
+    const int q = wq + 4 * j;
     const int r = 8 * q + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     if (r < PG_BM) {
-      src[j] = a_row(r) + 8 * c;
+      src[j] = a_row(r) + 8 * c + kbase;
     } else {
       const int wr = r - PG_BM;
       int col = n0 + (SWI ? (wr & (PG_BN - 1)) : wr);
       col = col < p.N ? col : p.N - 1;
       const int wrow = (SWI && wr >= PG_BN) ? col + p.N : col;
-      src[j] = p.w + static_cast<int64_t>(wrow) * K + 8 * c;
+      src[j] = p.w + static_cast<int64_t>(wrow) * K + 8 * c + kbase;
     }
   }
-#define PG_ISSUE(stage) pg_issue<S::LOADS>(smem + ((stage) % S::STAGES) * S::STAGEB, src, (stage) * PG_BK, wid)
+#define PG_ISSUE(stage) \
+  pg_issue<S::LOADS>(smem + kh * S::RING + ((stage) % S::STAGES) * S::STAGEB, src, (stage) * PG_BK, wq)
   asm volatile("" ::: "memory");
 #pragma unroll
   for (int s = 0; s < S::STAGES - 1; ++s)
@@ -537,7 +544,7 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(const SkinnyArgs p, int
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-    for (int wt = 0; wt < NW; ++wt) woff[wt][ks] = frag_off(PG_BM + wt * PG_BN + 16 * wid + fr, 4 * ks + fg);
+    for (int wt = 0; wt < NW; ++wt) woff[wt][ks] = frag_off(PG_BM + wt * PG_BN + 16 * wq + fr, 4 * ks + fg);
 #pragma unroll
     for (int t = 0; t < 2; ++t) xoff[t][ks] = frag_off(16 * t + fr, 4 * ks + fg);
   }
@@ -560,7 +567,7 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(const SkinnyArgs p, int
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (kt + S::STAGES - 1 < nk) PG_ISSUE(kt + S::STAGES - 1);
-    char *base = smem + (kt % S::STAGES) * S::STAGEB;
+    char *base = smem + kh * S::RING + (kt % S::STAGES) * S::STAGEB;
     if constexpr (PRO != PRO_NONE) {
       // RMSNorm of the stage's A tile in place, once per workgroup: thread t takes the 16-byte chunk in
       // slot t % 8 of row t / 8 (K chunk c = slot ^ ((row >> 1) & 7)) -> bf16(x / rms * w)
@@ -592,16 +599,26 @@ __global__ __launch_bounds__(256) void panel_gemm_kernel(const SkinnyArgs p, int
   }
 
 #undef PG_ISSUE
-  // tile -> LDS: acc[wt][t] lane holds C^T[weight row 16 wid + 4 g + e (+ 64 for up)][A row 16 t + lane % 16]
+  // tile -> LDS: acc[wt][t] lane holds C^T[weight row 16 wq + 4 g + e (+ 64 for up)][A row 16 t + lane % 16];
+  // with two K slices the second adds its partial tile to the first
   lds_barrier();
   float *part = reinterpret_cast<float *>(smem);  // [PG_BM][WR + 1]
 #pragma unroll
-  for (int wt = 0; wt < NW; ++wt)
+  for (int h = 0; h < KS; ++h) {
+    if (kh == h) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int wt = 0; wt < NW; ++wt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) part[(16 * t + fr) * (S::WR + 1) + wt * PG_BN + 16 * wid + 4 * fg + e] = acc[wt][t][e];
-  lds_barrier();
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float &dst = part[(16 * t + fr) * (S::WR + 1) + wt * PG_BN + 16 * wq + 4 * fg + e];
+            dst = h == 0 ? acc[wt][t][e] : dst + acc[wt][t][e];
+          }
+    }
+    lds_barrier();
+  }
+  if (tid >= 256) return;
 
   // ---- epilogue: thread -> (row rr, 4-column group sub) of each 32-column half ----
   float v[HALVES][4], vu[HALVES][4];
@@ -697,8 +714,15 @@ static int launch_panel(const SkinnyArgs &a, hipStream_t s) {
   const int64_t n_blocks = (a.N + PG_BN - 1) / PG_BN;
   const int64_t tiles = m_blocks * n_blocks;
   if (tiles >= (int64_t(1) << 31)) return fail(VK_ERR_ARG, "linear: too many tiles");
-  panel_gemm_kernel<PRO, EPI><<<static_cast<unsigned>(tiles), 256, 0, s>>>(a, static_cast<int>(m_blocks),
-                                                                          static_cast<int>(tiles));
+  // two K slices when the 8-wave workgroups (one per CU: two rings of LDS) still fit in one round
+  constexpr bool can_split = PRO == PRO_NONE && EPI != EPI_SWIGLU;
+  if (can_split && a.K % (2 * PG_BK) == 0 && tiles <= device_cus_cached()) {
+    panel_gemm_kernel<PRO, EPI, can_split ? 2 : 1><<<static_cast<unsigned>(tiles), 512, 0, s>>>(
+        a, static_cast<int>(m_blocks), static_cast<int>(tiles));
+  } else {
+    panel_gemm_kernel<PRO, EPI, 1><<<static_cast<unsigned>(tiles), 256, 0, s>>>(a, static_cast<int>(m_blocks),
+                                                                             static_cast<int>(tiles));
+  }
   return VK_OK;
 }
 
