@@ -276,12 +276,15 @@ static int64_t workspace_bytes_for(int64_t B, const DecodeSplit &sp) {
 // prefix rows are fetched once per group. Each part leaves a partial (max, sum, unnormalised output) per
 // column; a small combine kernel merges the parts of each (sequence, head).
 
-constexpr int GU_WAVES = 4;
+// wavefronts per workgroup and resident workgroups per CU the part count aims for, per group size
+// (LDS of the epilogue merge grows with the 4 G columns; registers with the column blocks)
+constexpr int gu_waves(int G) { return G == 8 ? 8 : 4; }
+constexpr int gu_wg_per_cu(int G) { return G >= 8 ? 1 : 4; }
 constexpr int GU_TILE = 32;
 constexpr int GU_PITCH = 72;  // one KV head: 64 + 8 pad
 
 template <int G>
-__global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
+__global__ __launch_bounds__(gu_waves(G) * 64) void grouped_attn_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ kp, const bf16_t *__restrict__ vp,
     const int32_t *__restrict__ pre_len, int64_t stride_pb, int64_t stride_ps, int64_t pre_max,
     const bf16_t *__restrict__ ks, const bf16_t *__restrict__ vs, const int32_t *__restrict__ own_len,
@@ -289,6 +292,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     float *__restrict__ ws_ml, float scale_log2) {
   constexpr int NC = 4 * G;            // query columns of one KV head (G members x 4 heads)
   constexpr int NCB = (NC + 15) / 16;  // 16-column MFMA blocks
+  constexpr int GU_WAVES = gu_waves(G);
   constexpr int LDS_V = GU_WAVES * GU_TILE * GU_PITCH * 2;
   constexpr int LDS_M = (GU_WAVES * NC * 64 + 2 * GU_WAVES * NC) * 4;
   __shared__ __attribute__((aligned(16))) char smem[LDS_V > LDS_M ? LDS_V : LDS_M];
@@ -606,17 +610,17 @@ struct GroupedLayout {
   int64_t o, ml, total;  // offsets / size in floats
 };
 
-// Parts per (group, KV head): one resident round of 4-wave workgroups over the CUs, and at least one tile
-// per wave at the longest lengths.
+// Parts per (group, KV head): one resident round of workgroups over the CUs, and at least one tile per
+// wave at the longest lengths.
 static GroupedLayout grouped_layout(int64_t B, int G, int64_t pre_max, int64_t own_max, int cus) {
   GroupedLayout L{};
   const int64_t pairs = (B / G) * DA_HKV;
-  // resident 4-wave workgroups per CU at the kernel's register use (G <= 4: 4, G = 8: 3, G = 16: 1)
-  const int per_cu = G <= 4 ? 4 : (G == 8 ? 2 : 1);
+  const int waves = G >= 16 ? gu_waves(16) : (G == 8 ? gu_waves(8) : gu_waves(4));
+  const int per_cu = G >= 16 ? gu_wg_per_cu(16) : (G == 8 ? gu_wg_per_cu(8) : gu_wg_per_cu(4));
   const int64_t target = static_cast<int64_t>(cus) * per_cu;
   int64_t np = (target + pairs - 1) / pairs;
   const int64_t tmax = (pre_max + GU_TILE - 1) / GU_TILE + G * ((own_max + GU_TILE - 1) / GU_TILE);
-  const int64_t cap = tmax / GU_WAVES;
+  const int64_t cap = tmax / waves;
   if (np > cap) np = cap;
   if (np > 16) np = 16;  // the combine kernel is instantiated for 1 .. 16 parts
   if (np < 1) np = 1;
@@ -634,7 +638,7 @@ static void launch_grouped(const bf16_t *q, const bf16_t *kp, const bf16_t *vp, 
                            const int32_t *own_len, int64_t stride_sb, int64_t stride_ss, int64_t own_max, int nparts,
                            float *ws_o, float *ws_ml, float scale_log2, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(P * nparts * DA_HKV));
-  grouped_attn_kernel<G><<<grid, GU_WAVES * 64, 0, s>>>(q, kp, vp, pre_len, stride_pb, stride_ps, pre_max, ks, vs,
+  grouped_attn_kernel<G><<<grid, gu_waves(G) * 64, 0, s>>>(q, kp, vp, pre_len, stride_pb, stride_ps, pre_max, ks, vs,
                                                         own_len, stride_sb, stride_ss, own_max, nparts, ws_o, ws_ml,
                                                         scale_log2);
 }
