@@ -179,6 +179,8 @@ int vk_select_update(const float *logits, const void *h, const void *norm_w, flo
  * emb = the `x` argument [vocab, K], and the gathered rows are also stored to x_store; norm_w NULL: h = x,
  * the activation normalised by vk_add_rmsnorm / vk_embed_rmsnorm beforehand), then
  * qkv = bf16(h @ w_qkv^T) and the vk_qkv_rope_cache transform of qkv: q -> q [M, H, 64], k / v -> caches.
+ * ss_in (may be NULL): the row sums of squares of x left by vk_linear_residual ([M, K / 64] fp32, K = 512);
+ * then 1 / rms comes from them instead of a pass over x.
  * Replaces embed_rmsnorm / add_rmsnorm + linear + qkv_rope_cache (viktor/triton_ops.py:17-108, 149-169;
  * viktor/fast_decoder.py:41-46, 76-90).
  */
@@ -187,22 +189,27 @@ int vk_norm_qkv_rope_cache(const void *x, const int64_t *tok, int64_t vocab, voi
                            const void *sin_t, int32_t table_dtype, int64_t table_rows, const int32_t *pos,
                            const int32_t *rope_pos, const int32_t *seq, void *q, void *k_cache, void *v_cache,
                            int64_t stride_cb, int64_t stride_cs, int64_t cache_rows, int64_t cache_len, int64_t M,
-                           int32_t K, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void *stream);
+                           int32_t K, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, const float *ss_in,
+                           void *stream);
 
 /*
  * vk_linear_residual: x[M, N] = bf16(x + bf16(a[M, K] @ w[N, K]^T)) in place (the o / down projections
  * followed by the residual add of add_rmsnorm, viktor/triton_ops.py:24-27, viktor/fast_decoder.py:51-57).
+ * ss_out (may be NULL; N = 512): per-row partial sums of squares of the updated x, one per 64-column
+ * block ([M, N / 64] fp32, each block's sum in a fixed order), for the next norm (the norm half of
+ * add_rmsnorm, viktor/triton_ops.py:28-40).
  */
-int vk_linear_residual(const void *a, const void *w, void *x, int64_t M, int32_t N, int32_t K, void *stream);
+int vk_linear_residual(const void *a, const void *w, void *x, int64_t M, int32_t N, int32_t K, float *ss_out,
+                       void *stream);
 
 /*
  * vk_norm_linear: y = act(bf16(RMSNorm(x) * norm_w) @ w^T) (norm_w may be NULL: no norm), act = SwiGLU over
  * w = [gate; up] when swiglu != 0 (bf16 out), else identity (bf16 or fp32 out). The mlp norm + gate_up +
- * SwiGLU of a decode step (viktor/triton_ops.py:17-40, 111-146).
+ * SwiGLU of a decode step (viktor/triton_ops.py:17-40, 111-146). ss_in as for vk_norm_qkv_rope_cache.
  * The three entry points above take K in {256, 512, 1024, 1536} and N % 4 == 0.
  */
 int vk_norm_linear(const void *x, const void *norm_w, float eps, const void *w, void *y, int64_t M, int32_t N,
-                   int32_t K, int32_t swiglu, int32_t out_dtype, void *stream);
+                   int32_t K, int32_t swiglu, int32_t out_dtype, const float *ss_in, void *stream);
 
 /*
  * GSPO scoring of B sequences of T target tokens (scripts/gspo.py:340-353 and 459-477):

@@ -446,9 +446,17 @@ def test_group_advantage():
 
 
 # ---- decode-step fusions: against the oracle's composition of the unfused ops ------------------------
+def _row_ss(x):
+    """[M, K / 64] fp32 partial sums of squares of the rows of x, one per 64-column block."""
+    M, K = x.shape
+    return (x.double() ** 2).view(M, K // 64, 64).sum(-1).float()
+
+
 @pytest.mark.parametrize("M", [1, 45, 512])
-@pytest.mark.parametrize("embed", [False, True])
+@pytest.mark.parametrize("embed", [False, True, "ss"])
 def test_norm_qkv_rope_cache(M, embed):
+    use_ss = embed == "ss"
+    embed = embed is True
     g = gen(M + int(embed))
     H, HKV, D, K, S, Bc = 8, 2, 64, 512, 300, max(M, 2)
     emb = R.bf(torch.randn(7, K, generator=g))
@@ -471,8 +479,10 @@ def test_norm_qkv_rope_cache(M, embed):
                                     tok=to_dev(tok), x_store=xs)
         assert torch.equal(xs.float().cpu(), x)
     else:
+        # ss: 1 / rms from handed-over row sums of squares instead of the kernel's own pre-pass
         q = ops.norm_qkv_rope_cache(to_dev(x, BF), to_dev(nw, BF), 1e-6, to_dev(wq, BF), to_dev(qw, BF), to_dev(kw, BF),
-                                    to_dev(cos, BF), to_dev(sin, BF), to_dev(pos), to_dev(seq), kc, vc, H, HKV, D)
+                                    to_dev(cos, BF), to_dev(sin, BF), to_dev(pos), to_dev(seq), kc, vc, H, HKV, D,
+                                    ss=to_dev(_row_ss(x)) if use_ss else None)
     h = R.rmsnorm_fused(x, nw, 1e-6)
     qkv = R.linear_fused(h, wq).view(M, H + 2 * HKV, D)
     rp = pos.long()
@@ -505,9 +515,28 @@ def test_linear_residual(M, N, K):
     assert ok, err
 
 
+@pytest.mark.parametrize("M", [1, 77, 512])
+def test_linear_residual_row_sums(M):
+    """ss_out: the per-64-column-block sums of squares of the updated rows, and x unchanged by asking."""
+    g = gen(M * 3 + 1)
+    K = N = 512
+    a = R.bf(torch.randn(M, K, generator=g))
+    w = R.bf(torch.randn(N, K, generator=g) / math.sqrt(K))
+    x = R.bf(torch.randn(M, N, generator=g) * 2)
+    xd, xd2 = to_dev(x, BF), to_dev(x, BF)
+    ss = torch.full((M, N // 64), float("nan"), device=DEV)
+    ops.linear_residual(to_dev(a, BF), to_dev(w, BF), xd, ss_out=ss)
+    ops.linear_residual(to_dev(a, BF), to_dev(w, BF), xd2)
+    assert torch.equal(xd, xd2)
+    want = _row_ss(xd.float().cpu())
+    assert torch.allclose(ss.cpu(), want, rtol=1e-5, atol=0), float((ss.cpu() - want).abs().max())
+
+
 @pytest.mark.parametrize("M", [1, 100, 512])
-@pytest.mark.parametrize("mode", ["swiglu", "bf16", "f32", "nonorm"])
+@pytest.mark.parametrize("mode", ["swiglu", "bf16", "f32", "nonorm", "swiglu_ss", "bf16_ss", "f32_ss"])
 def test_norm_linear(M, mode):
+    use_ss = mode.endswith("_ss")
+    mode = mode.replace("_ss", "")
     g = gen(M + len(mode))
     K, Fd = 512, 1536
     x = R.bf(torch.randn(M, K, generator=g) * 3)
@@ -516,7 +545,8 @@ def test_norm_linear(M, mode):
     w = R.bf(torch.randn(N, K, generator=g) / math.sqrt(K))
     h = x if mode == "nonorm" else R.rmsnorm_fused(x, nw, 1e-6)
     out = ops.norm_linear(to_dev(x, BF), None if mode == "nonorm" else to_dev(nw, BF), 1e-6, to_dev(w, BF),
-                          swiglu=mode == "swiglu", out_dtype=torch.float32 if mode == "f32" else None)
+                          swiglu=mode == "swiglu", out_dtype=torch.float32 if mode == "f32" else None,
+                          ss=to_dev(_row_ss(x)) if use_ss else None)
     y = (h.double() @ w.double().t()).float()
     if mode == "swiglu":
         ref = R.swiglu_fused(R.bf(y[:, :Fd]), R.bf(y[:, Fd:]))

@@ -43,9 +43,9 @@ SIGNATURES = {
                                     _I32, _I32, _I32, _P, _I64, _P],
     "vk_decode_attention_grouped_workspace": [_I64, _I32, _I64, _I64, ctypes.POINTER(_I64)],
     "vk_norm_qkv_rope_cache": [_P, _P, _I64, _P, _P, _F, _P, _P, _P, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _I64,
-                               _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P],
-    "vk_linear_residual": [_P, _P, _P, _I64, _I32, _I32, _P],
-    "vk_norm_linear": [_P, _P, _F, _P, _P, _I64, _I32, _I32, _I32, _I32, _P],
+                               _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P],
+    "vk_linear_residual": [_P, _P, _P, _I64, _I32, _I32, _P, _P],
+    "vk_norm_linear": [_P, _P, _F, _P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P],
     "vk_gspo_score": [_P, _I32, _P, _P, _P, _P, _P, _F, _F, _F, _P, _P, _P, _P, _P, _I64, _I64, _I32, _P],
     "vk_group_advantage": [_P, _I64, _I32, _I32, _F, _P, _P, _P],
 }

@@ -19,7 +19,8 @@
 
 namespace vk {
 
-enum Prologue { PRO_NONE = 0, PRO_NORM = 1, PRO_EMBED_NORM = 2 };
+// PRO_NORM_SS: RMSNorm with the row sums of squares handed over by the residual GEMM that produced x
+enum Prologue { PRO_NONE = 0, PRO_NORM = 1, PRO_EMBED_NORM = 2, PRO_NORM_SS = 3 };
 enum Epilogue { EPI_BF16 = 0, EPI_F32 = 1, EPI_SWIGLU = 2, EPI_RESID = 3, EPI_ROPE = 4 };
 
 struct SkinnyArgs {
@@ -42,6 +43,11 @@ struct SkinnyArgs {
   bf16_t *kc, *vc;
   int64_t stride_cb, stride_cs, cache_rows, cache_len;
   int H, HKV;
+  // EPI_RESID: per-row partial sums of squares of the updated residual, one per 64-column block
+  // ([M, N / 64] fp32; NULL: none). PRO_NORM_SS: those sums for the A rows ([M, ss_blocks]).
+  float *ss_out;
+  const float *ss_in;
+  int ss_blocks;
 };
 
 constexpr int SK_BM = 32;
@@ -368,29 +374,49 @@ __device__ __forceinline__ void pg_issue(char *base, const bf16_t *const *src, i
     __builtin_amdgcn_global_load_lds(src[j] + k0, (lds_void_t *)(base + (wid + 4 * j) * 1024), 16, 0, 0);
 }
 
-template <int EPI, int KS>
+// One 16-byte direct global->LDS load per lane (a whole 1 KB row for a wave); a device function for the
+// same reason as pg_issue: the builtin written in the kernel body also drops the launch stub.
+__device__ __forceinline__ void pg_issue_row(char *dst, const bf16_t *src) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t *)dst, 16, 0, 0);
+}
+// The same with 4 bytes per lane (lane l lands at dst + 4 l).
+__device__ __forceinline__ void pg_issue_dword(char *dst, const int32_t *src) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t *)dst, 4, 0, 0);
+}
+
+template <int PRO, int EPI, int KS>
 struct PanelShape {
   static constexpr bool SWI = EPI == EPI_SWIGLU;
+  static constexpr bool XRES = PRO == PRO_NORM_SS;    // A resident in LDS (K = 512), the ring carries W
   static constexpr int WR = SWI ? 2 * PG_BN : PG_BN;  // weight rows per tile
-  static constexpr int ROWS = PG_BM + WR;             // LDS rows per stage
+  static constexpr int ROWS = (XRES ? 0 : PG_BM) + WR;  // LDS rows per ring stage
   static constexpr int STAGEB = ROWS * PG_ROWB;
   static constexpr int LOADS = ROWS / 8 / 4;          // direct-load instructions per wave per stage
   // the K loop is latency-bound (little MFMA work per stage): as many stages in flight as LDS allows
   // with 2 workgroups per CU -- 4 slots (3 in flight) for 12 KB stages, 3 for the 20 KB SwiGLU stages
+  // (and for the 16 KB SwiGLU weight stages beside a resident A tile)
   static constexpr int STAGES = SWI ? 3 : 4;
+  static constexpr int XB = XRES ? PG_BM * PG_NORM_K * 2 : 0;  // resident A tile: 32 rows x 1 KB
   static constexpr int PARTB = PG_BM * (WR + 1) * 4;
   static constexpr int RING = STAGES * STAGEB;  // one ring per K slice (KS slices)
-  static constexpr int BODY = KS * RING > PARTB ? KS * RING : PARTB;
-  static constexpr int SMEM = BODY + PG_NORM_K * 2 + PG_BM * 4;  // + the RMSNorm weight and row sums
+  static constexpr int BODY = XB + KS * RING > PARTB ? XB + KS * RING : PARTB;
+  // + the RMSNorm weight and row sums of the pre-pass variants
+  static constexpr int SMEM = BODY + ((PRO == PRO_NORM || PRO == PRO_EMBED_NORM) ? PG_NORM_K * 2 + PG_BM * 4 : 0);
 };
 
 // KS = 2: 8 wavefronts, waves 0-3 take the first half of K and waves 4-7 the second, each half through
 // its own ring; the two partial tiles are summed in LDS (fixed order) before the epilogue. This halves the
 // latency chain of the K loop for the shapes with few workgroups (o / down / qkv projections).
+//
+// PRO_NORM_SS: the A tile (32 rows x K = 512) is loaded once into LDS (one direct load per row, chunk c of
+// row r in slot c ^ (r & 15)), normalised in place in one pass -- 1 / rms from the row sums of squares the
+// producing residual GEMM left, bf16(x / rms * w) -- and read from there; the ring carries only W.
 template <int PRO, int EPI, int KS>
 __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p, int m_blocks, int tiles) {
-  static_assert(KS == 1 || (KS == 2 && PRO == PRO_NONE), "K halves only without the norm prologue");
-  using S = PanelShape<EPI, KS>;
+  static_assert(KS == 1 || (KS == 2 && (PRO == PRO_NONE || PRO == PRO_NORM_SS)),
+                "K halves only without the pre-pass norm prologue");
+  using S = PanelShape<PRO, EPI, KS>;
+  constexpr bool XRES = S::XRES;
   constexpr bool SWI = S::SWI;
   constexpr bool ROPE = EPI == EPI_ROPE;
   constexpr int HALVES = 2;  // 64 output columns = two 32-column halves in the epilogue
@@ -417,9 +443,9 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
   const int64_t erow = m0 + rr;
   const bool row_ok = tid < 256 && erow < p.M;
 
-  // 1. RoPE positions (the table loads depend on them)
+  // 1. RoPE positions (the table loads depend on them; XRES: staged in LDS below)
   int64_t e_pos = 0, e_seq = 0, rp = 0;
-  if constexpr (ROPE) {
+  if constexpr (ROPE && !XRES) {
     if (row_ok) {
       e_pos = p.pos[erow];
       e_seq = p.seq[erow];
@@ -446,10 +472,10 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
     const int q = wq + 4 * j;
     const int r = 8 * q + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
-    if (r < PG_BM) {
+    if (!XRES && r < PG_BM) {
       src[j] = a_row(r) + 8 * c + kbase;
     } else {
-      const int wr = r - PG_BM;
+      const int wr = XRES ? r : r - PG_BM;
       int col = n0 + (SWI ? (wr & (PG_BN - 1)) : wr);
       col = col < p.N ? col : p.N - 1;
       const int wrow = (SWI && wr >= PG_BN) ? col + p.N : col;
@@ -457,11 +483,45 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
     }
   }
 #define PG_ISSUE(stage) \
-  pg_issue<S::LOADS>(smem + kh * S::RING + ((stage) % S::STAGES) * S::STAGEB, src, (stage) * PG_BK, wq)
+  pg_issue<S::LOADS>(smem + S::XB + kh * S::RING + ((stage) % S::STAGES) * S::STAGEB, src, (stage) * PG_BK, wq)
+  // PRO_NORM_SS: the norm weight (1 KB) goes to the last slot of the first ring, which the K loop fills only
+  // after the normalisation; every wave loads it (the same bytes) ahead of its tile rows, so the one counted
+  // wait before the normalisation covers it. Register loads are kept out of this stretch: one consumed while
+  // direct loads are in flight makes the compiler wait for all of them.
+  // The tile's row sums of squares (32 rows x 8 fp32 = 1 KB) follow it there the same way: lane l brings
+  // half l % 2 of row l / 2; and for RoPE the rows' int32 positions: [pos x 32 | seq x 32] and
+  // [rope pos x 32 | again], 4 bytes per lane (rows past M read row M - 1; their results are not stored).
+  char *const nwx = smem + S::XB + (S::STAGES - 1) * S::STAGEB;
+  char *const ssx = nwx + PG_NORM_K * 2;
+  char *const psx = ssx + PG_BM * 8 * 4;
+  static_assert(!XRES || PG_NORM_K * 2 + PG_BM * 8 * 4 + 2 * 64 * 4 <= S::STAGEB, "staging fits one ring slot");
+  if constexpr (XRES) {
+    pg_issue_row(nwx, p.norm_w + 8 * lane);
+    int64_t srow = m0 + (lane >> 1);
+    srow = srow < p.M ? srow : p.M - 1;
+    pg_issue_row(ssx, reinterpret_cast<const bf16_t *>(p.ss_in + srow * 8 + 4 * (lane & 1)));
+    if constexpr (ROPE) {
+      int64_t prow = m0 + (lane & 31);
+      prow = prow < p.M ? prow : p.M - 1;
+      pg_issue_dword(psx, (lane < 32 ? p.pos : p.seq) + prow);
+      pg_issue_dword(psx + 256, (p.rope_pos ? p.rope_pos : p.pos) + prow);
+    }
+  }
+  if constexpr (XRES) {
+    // the resident A tile next: row i of the tile is instruction i, issued by wave i % (4 KS)
+#pragma unroll
+    for (int i = 0; i < PG_BM / (4 * KS); ++i) {
+      const int r = wid + 4 * KS * i;
+      const int c = lane ^ (r & 15);
+      pg_issue_row(smem + r * (PG_NORM_K * 2), a_row(r) + 8 * c);
+    }
+  }
   asm volatile("" ::: "memory");
+  // (XRES: K = 512, so every one of these stages exists; issued without a branch, the compiler can count
+  // the loads still in flight at the wait before the normalisation)
 #pragma unroll
   for (int s = 0; s < S::STAGES - 1; ++s)
-    if (s < nk) PG_ISSUE(s);
+    if (XRES || s < nk) PG_ISSUE(s);
   asm volatile("" ::: "memory");
 
   // 4. RMSNorm (K = 512): wave w reads rows 8 w .. 8 w + 7; lane l owns row 8 w + l / 8 and the 64 K values
@@ -473,7 +533,7 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
   bf16_t *nws = reinterpret_cast<bf16_t *>(smem + S::BODY);
   float *rs = reinterpret_cast<float *>(smem + S::BODY + PG_NORM_K * 2);
   float rinv[1] = {1.f};
-  if constexpr (PRO != PRO_NONE) {
+  if constexpr (PRO == PRO_NORM || PRO == PRO_EMBED_NORM) {
     const int pre_row = 8 * wid + (lane >> 3);
     const int pre_k = 64 * (lane & 7);
     u32x4 xv[8];
@@ -505,10 +565,45 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
     rinv[0] = rsqrtf(rs[tid >> 3] / static_cast<float>(K) + p.eps);  // the row of this thread's chunk
   }
 
+  // 4'. PRO_NORM_SS: normalise the resident A tile in place, a whole 1 KB row per wave and step (lane l takes
+  //     slot l, conflict-free). 1 / rms comes from the row's ss_blocks (= K / 64) partial sums, summed in a
+  //     fixed order. K = 512 (checked on the host), so the first STAGES - 1 ring stages were all issued:
+  //     waiting until only their loads are outstanding retires this wave's weight, row sums and tile rows.
+  if constexpr (XRES) {
+    __builtin_amdgcn_s_waitcnt(pg_vmcnt(S::LOADS * (S::STAGES - 1)));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < PG_BM / (4 * KS); ++i) {
+      const int r = wid + 4 * KS * i;
+      const f32x4 sa = *reinterpret_cast<const f32x4 *>(ssx + 32 * r);
+      const f32x4 sb = *reinterpret_cast<const f32x4 *>(ssx + 32 * r + 16);
+      const float ss = ((sa[0] + sa[1]) + (sa[2] + sa[3])) + ((sb[0] + sb[1]) + (sb[2] + sb[3]));
+      const float rn = rsqrtf(ss * (1.0f / PG_NORM_K) + p.eps);  // exactly ss / K (K = 512)
+      u32x4 *xc = reinterpret_cast<u32x4 *>(smem + r * (PG_NORM_K * 2) + 16 * lane);
+      const u32x4 xr = *xc;
+      const u32x4 wr = *reinterpret_cast<const u32x4 *>(nwx + 16 * (lane ^ (r & 15)));
+      u32x4 xn;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        xn[e] = pack_bf(lo_bf(xr[e]) * rn * lo_bf(wr[e]), hi_bf(xr[e]) * rn * hi_bf(wr[e]));
+      *xc = xn;
+    }
+    if constexpr (ROPE) {  // read before the barrier below, which retires them: the loop reuses the slot
+      const int32_t *ps = reinterpret_cast<const int32_t *>(psx);
+      e_pos = ps[rr];
+      e_seq = ps[32 + rr];
+      rp = ps[64 + rr];
+    }
+    lds_barrier();
+  }
+
   // 5. epilogue data (consumed after the loop)
   u32x2 old[HALVES];
   u32x2 wnf[2];
   f32x4 csf, snf;
+  u32x2 ctw[2], stw[2];  // the raw table words, widened in the epilogue (here it would wait for the loads)
   const int hd = n0 / 64;
   if constexpr (EPI == EPI_RESID) {
 #pragma unroll
@@ -519,23 +614,20 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
     }
   }
   if constexpr (ROPE) {
-    wnf[0] = wnf[1] = u32x2{0u, 0u};
-    csf = snf = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (hd < p.H + p.HKV) {
-      const bf16_t *wn = hd < p.H ? p.qw : p.kw;
-      wnf[0] = *reinterpret_cast<const u32x2 *>(wn + 4 * sub);
-      wnf[1] = *reinterpret_cast<const u32x2 *>(wn + 32 + 4 * sub);
-      rp = rp < 0 ? 0 : (rp >= p.table_rows ? p.table_rows - 1 : rp);
-      if (p.table_f32) {
-        csf = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(p.cos_t) + rp * 32 + 4 * sub);
-        snf = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(p.sin_t) + rp * 32 + 4 * sub);
-      } else {
-        const u32x2 c2 = *reinterpret_cast<const u32x2 *>(static_cast<const bf16_t *>(p.cos_t) + rp * 32 + 4 * sub);
-        const u32x2 s2 = *reinterpret_cast<const u32x2 *>(static_cast<const bf16_t *>(p.sin_t) + rp * 32 + 4 * sub);
-        csf = f32x4{lo_bf(c2[0]), hi_bf(c2[0]), lo_bf(c2[1]), hi_bf(c2[1])};
-        snf = f32x4{lo_bf(s2[0]), hi_bf(s2[0]), lo_bf(s2[1]), hi_bf(s2[1])};
-      }
-    }
+    // without branches (loads in branches make the compiler wait for them at the join): v heads load the
+    // q-norm weight and the tables too, unused; an fp32 table row is two 8-byte words, a bf16 row one (read
+    // twice)
+    const bf16_t *wn = hd < p.H ? p.qw : p.kw;
+    wnf[0] = *reinterpret_cast<const u32x2 *>(wn + 4 * sub);
+    wnf[1] = *reinterpret_cast<const u32x2 *>(wn + 32 + 4 * sub);
+    rp = rp < 0 ? 0 : (rp >= p.table_rows ? p.table_rows - 1 : rp);
+    const int64_t esz = p.table_f32 ? 4 : 2;
+    const int64_t toff = (rp * 32 + 4 * sub) * esz, thi = p.table_f32 ? 8 : 0;
+    const char *ct = static_cast<const char *>(p.cos_t) + toff, *st = static_cast<const char *>(p.sin_t) + toff;
+    ctw[0] = *reinterpret_cast<const u32x2 *>(ct);
+    ctw[1] = *reinterpret_cast<const u32x2 *>(ct + thi);
+    stw[0] = *reinterpret_cast<const u32x2 *>(st);
+    stw[1] = *reinterpret_cast<const u32x2 *>(st + thi);
   }
   // fragment byte offsets inside a stage: LDS row R, K chunk c -> R * 128 + 16 * (c ^ ((R >> 1) & 7))
   auto frag_off = [](int R, int c) { return R * PG_ROWB + 16 * (c ^ ((R >> 1) & 7)); };
@@ -544,7 +636,8 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-    for (int wt = 0; wt < NW; ++wt) woff[wt][ks] = frag_off(PG_BM + wt * PG_BN + 16 * wq + fr, 4 * ks + fg);
+    for (int wt = 0; wt < NW; ++wt)
+      woff[wt][ks] = frag_off((XRES ? 0 : PG_BM) + wt * PG_BN + 16 * wq + fr, 4 * ks + fg);
 #pragma unroll
     for (int t = 0; t < 2; ++t) xoff[t][ks] = frag_off(16 * t + fr, 4 * ks + fg);
   }
@@ -567,8 +660,8 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (kt + S::STAGES - 1 < nk) PG_ISSUE(kt + S::STAGES - 1);
-    char *base = smem + kh * S::RING + (kt % S::STAGES) * S::STAGEB;
-    if constexpr (PRO != PRO_NONE) {
+    char *base = smem + S::XB + kh * S::RING + (kt % S::STAGES) * S::STAGEB;
+    if constexpr (PRO == PRO_NORM || PRO == PRO_EMBED_NORM) {
       // RMSNorm of the stage's A tile in place, once per workgroup: thread t takes the 16-byte chunk in
       // slot t % 8 of row t / 8 (K chunk c = slot ^ ((row >> 1) & 7)) -> bf16(x / rms * w)
       const int row = tid >> 3, c = (tid & 7) ^ ((row >> 1) & 7);
@@ -586,7 +679,14 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
     for (int ks = 0; ks < 2; ++ks) {
       u32x4 xf[2];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) xf[t] = *reinterpret_cast<const u32x4 *>(base + xoff[t][ks]);
+      for (int t = 0; t < 2; ++t) {
+        if constexpr (XRES) {  // resident tile: row 16 t + fr, K chunk 8 (global stage) + 4 ks + fg
+          const int c = 8 * (kh * nk + kt) + 4 * ks + fg;
+          xf[t] = *reinterpret_cast<const u32x4 *>(smem + (16 * t + fr) * (PG_NORM_K * 2) + 16 * (c ^ fr));
+        } else {
+          xf[t] = *reinterpret_cast<const u32x4 *>(base + xoff[t][ks]);
+        }
+      }
 #pragma unroll
       for (int wt = 0; wt < NW; ++wt) {
         const u32x4 wf = *reinterpret_cast<const u32x4 *>(base + woff[wt][ks]);
@@ -632,6 +732,15 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
     }
   if constexpr (ROPE) {
     const int H = p.H, HKV = p.HKV;
+    if (p.table_f32) {
+      csf = f32x4{__uint_as_float(ctw[0][0]), __uint_as_float(ctw[0][1]), __uint_as_float(ctw[1][0]),
+                  __uint_as_float(ctw[1][1])};
+      snf = f32x4{__uint_as_float(stw[0][0]), __uint_as_float(stw[0][1]), __uint_as_float(stw[1][0]),
+                  __uint_as_float(stw[1][1])};
+    } else {
+      csf = f32x4{lo_bf(ctw[0][0]), hi_bf(ctw[0][0]), lo_bf(ctw[0][1]), hi_bf(ctw[0][1])};
+      snf = f32x4{lo_bf(stw[0][0]), hi_bf(stw[0][0]), lo_bf(stw[0][1]), hi_bf(stw[0][1])};
+    }
     float x1[4], x2[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -677,11 +786,11 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
     }
     return;
   }
-  if (!row_ok) return;
+  float ssq = 0.f;  // EPI_RESID: this thread's share of the row's sum of squares over the block
 #pragma unroll
   for (int hf = 0; hf < HALVES; ++hf) {
     const int col = n0 + 32 * hf + 4 * sub;
-    if (col >= p.N) continue;  // N is a multiple of 4 (checked on the host)
+    if (!row_ok || col >= p.N) continue;  // N is a multiple of 4 (checked on the host)
     const int64_t off = erow * p.N + col;
     if (EPI == EPI_F32) {
       *reinterpret_cast<f32x4 *>(static_cast<float *>(p.y) + off) = f32x4{v[hf][0], v[hf][1], v[hf][2], v[hf][3]};
@@ -703,7 +812,23 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
         o[2] = lo_bf(old[hf][1]) + round_bf(o[2]);
         o[3] = hi_bf(old[hf][1]) + round_bf(o[3]);
       }
-      *reinterpret_cast<u32x2 *>(static_cast<bf16_t *>(p.y) + off) = u32x2{pack_bf(o[0], o[1]), pack_bf(o[2], o[3])};
+      const u32x2 packed = u32x2{pack_bf(o[0], o[1]), pack_bf(o[2], o[3])};
+      *reinterpret_cast<u32x2 *>(static_cast<bf16_t *>(p.y) + off) = packed;
+      if (EPI == EPI_RESID) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float lo = lo_bf(packed[e]), hi = hi_bf(packed[e]);
+          ssq += lo * lo + hi * hi;
+        }
+      }
+    }
+  }
+  if constexpr (EPI == EPI_RESID) {
+    if (p.ss_out) {  // the 8 lanes of a row (consecutive) reduce their shares in a fixed order
+      ssq += __shfl_xor(ssq, 1, 64);
+      ssq += __shfl_xor(ssq, 2, 64);
+      ssq += __shfl_xor(ssq, 4, 64);
+      if (row_ok && sub == 0) p.ss_out[erow * ((p.N + PG_BN - 1) / PG_BN) + nb] = ssq;
     }
   }
 }
@@ -715,7 +840,7 @@ static int launch_panel(const SkinnyArgs &a, hipStream_t s) {
   const int64_t tiles = m_blocks * n_blocks;
   if (tiles >= (int64_t(1) << 31)) return fail(VK_ERR_ARG, "linear: too many tiles");
   // two K slices when the 8-wave workgroups (one per CU: two rings of LDS) still fit in one round
-  constexpr bool can_split = PRO == PRO_NONE && EPI != EPI_SWIGLU;
+  constexpr bool can_split = (PRO == PRO_NONE || PRO == PRO_NORM_SS) && EPI != EPI_SWIGLU;
   if (can_split && a.K % (2 * PG_BK) == 0 && tiles <= device_cus_cached()) {
     panel_gemm_kernel<PRO, EPI, can_split ? 2 : 1><<<static_cast<unsigned>(tiles), 512, 0, s>>>(
         a, static_cast<int>(m_blocks), static_cast<int>(tiles));
@@ -774,7 +899,7 @@ static SkinnyArgs base_args(const void *a, const void *w, void *y, int64_t M, in
 using namespace vk;
 
 extern "C" int vk_norm_linear(const void *x, const void *norm_w, float eps, const void *w, void *y, int64_t M, int32_t N,
-                              int32_t K, int32_t swiglu, int32_t out_dtype, void *stream) {
+                              int32_t K, int32_t swiglu, int32_t out_dtype, const float *ss_in, void *stream) {
   VK_CHECK_ARG(x && w && y, "norm_linear: null pointer");
   VK_CHECK_ARG(M >= 0 && N > 0 && N % 4 == 0 && K > 0, "norm_linear: bad sizes");
   VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w) && vk_aligned16(y) && (!norm_w || vk_aligned16(norm_w)),
@@ -784,9 +909,16 @@ extern "C" int vk_norm_linear(const void *x, const void *norm_w, float eps, cons
   SkinnyArgs p = base_args(x, w, y, M, N, K);
   p.norm_w = static_cast<const bf16_t *>(norm_w);
   p.eps = eps;
+  p.ss_in = ss_in;
   hipStream_t s = VK_STREAM(stream);
   int rc;
-  if (panel_ok(p, norm_w ? PRO_NORM : PRO_NONE)) {
+  if (ss_in) {  // the norm from the producing GEMM's row sums of squares
+    VK_CHECK_ARG(norm_w && K == PG_NORM_K && vk_aligned16(ss_in), "norm_linear: ss_in needs norm_w and K = %d",
+                 PG_NORM_K);
+    rc = swiglu ? launch_panel<PRO_NORM_SS, EPI_SWIGLU>(p, s)
+                : (out_dtype == VK_DTYPE_F32 ? launch_panel<PRO_NORM_SS, EPI_F32>(p, s)
+                                             : launch_panel<PRO_NORM_SS, EPI_BF16>(p, s));
+  } else if (panel_ok(p, norm_w ? PRO_NORM : PRO_NONE)) {
     if (norm_w)
       rc = swiglu ? launch_panel<PRO_NORM, EPI_SWIGLU>(p, s)
                   : (out_dtype == VK_DTYPE_F32 ? launch_panel<PRO_NORM, EPI_F32>(p, s)
@@ -815,12 +947,15 @@ extern "C" int vk_norm_linear(const void *x, const void *norm_w, float eps, cons
 }
 
 extern "C" int vk_linear_residual(const void *a, const void *w, void *x, int64_t M, int32_t N, int32_t K,
-                                  void *stream) {
+                                  float *ss_out, void *stream) {
   VK_CHECK_ARG(a && w && x, "linear_residual: null pointer");
   VK_CHECK_ARG(M >= 0 && N > 0 && N % 4 == 0 && K > 0, "linear_residual: bad sizes");
   VK_CHECK_ARG(vk_aligned16(a) && vk_aligned16(w) && vk_aligned16(x), "linear_residual: alignment");
   if (M == 0) return VK_OK;
   SkinnyArgs p = base_args(a, w, x, M, N, K);
+  p.ss_out = ss_out;
+  VK_CHECK_ARG(!ss_out || (panel_ok(p, PRO_NONE) && N == PG_NORM_K),
+               "linear_residual: row sums of squares need K %% 64 == 0 and N = %d", PG_NORM_K);
   const int rc = panel_ok(p, PRO_NONE) ? launch_panel<PRO_NONE, EPI_RESID>(p, VK_STREAM(stream))
                                        : dispatch_k<32, PRO_NONE, EPI_RESID>(p, VK_STREAM(stream));
   if (rc != VK_OK) return rc;
@@ -833,7 +968,8 @@ extern "C" int vk_norm_qkv_rope_cache(const void *x, const int64_t *tok, int64_t
                                       int64_t table_rows, const int32_t *pos, const int32_t *rope_pos,
                                       const int32_t *seq, void *q, void *k_cache, void *v_cache, int64_t stride_cb,
                                       int64_t stride_cs, int64_t cache_rows, int64_t cache_len, int64_t M, int32_t K,
-                                      int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void *stream) {
+                                      int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, const float *ss_in,
+                                      void *stream) {
   VK_CHECK_ARG(x && w_qkv && q_norm_w && k_norm_w && cos_t && sin_t && pos && seq && q && k_cache && v_cache,
                "norm_qkv_rope_cache: null pointer");
   VK_CHECK_ARG(norm_w || !tok, "norm_qkv_rope_cache: the embedding gather needs norm_w");
@@ -868,8 +1004,13 @@ extern "C" int vk_norm_qkv_rope_cache(const void *x, const int64_t *tok, int64_t
   p.H = n_heads;
   p.HKV = n_kv_heads;
   hipStream_t s = VK_STREAM(stream);
+  p.ss_in = ss_in;
   int rc;
-  if (!norm_w)  // x is the normalised activation already
+  if (ss_in) {  // the norm from the producing GEMM's row sums of squares
+    VK_CHECK_ARG(norm_w && !tok && K == PG_NORM_K && vk_aligned16(ss_in),
+                 "norm_qkv_rope_cache: ss_in needs norm_w, no tok and K = %d", PG_NORM_K);
+    rc = launch_panel<PRO_NORM_SS, EPI_ROPE>(p, s);
+  } else if (!norm_w)  // x is the normalised activation already
     rc = panel_ok(p, PRO_NONE) ? launch_panel<PRO_NONE, EPI_ROPE>(p, s) : dispatch_k<64, PRO_NONE, EPI_ROPE>(p, s);
   else if (panel_ok(p, PRO_NORM))
     rc = tok ? launch_panel<PRO_EMBED_NORM, EPI_ROPE>(p, s) : launch_panel<PRO_NORM, EPI_ROPE>(p, s);

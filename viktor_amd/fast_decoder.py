@@ -201,13 +201,12 @@ class FastDecoder:
         return ops.add_rmsnorm(xr, self.w(self.dec.norm.weight), self.cfg.norm_eps)
 
     def decode_residual(self, pos, seq, cache_seqlens, cache, rope_pos=None, tok=None, x=None, prefix=None):
-        """The decoder layers of one decode step on the small-M kernels, seven launches per layer:
-          add_rmsnorm (attn norm; layer 0: embed_rmsnorm, the token-embedding gather + norm),
-          norm_qkv_rope_cache (qkv GEMM + QK-norm + RoPE + cache write), decode_attention, linear_residual
-          (o proj + residual add), add_rmsnorm (mlp norm), norm_linear (gate_up + SwiGLU), linear_residual
-          (down proj + residual add). The norms run as their own launches: fused into the GEMM prologues
-          they cost more than a separate pass over the [B, d] rows (every output-column block of a GEMM
-          would redo them).
+        """The decoder layers of one decode step on the small-M kernels, five launches per layer (+1 in
+        layer 0): norm_qkv_rope_cache (attn norm + qkv GEMM + QK-norm + RoPE + cache write; layer 0 runs
+        embed_rmsnorm, the token-embedding gather + norm, before it), decode_attention, linear_residual
+        (o proj + residual add), norm_linear (mlp norm + gate_up + SwiGLU), linear_residual (down proj +
+        residual add). The residual GEMMs leave the row sums of squares of x (per 64-column block), so the
+        norms inside the next GEMMs need no pass of their own over x.
         Returns the residual stream [B, d] after the last layer (x, updated in place, when given); the
         final RMSNorm is left to the consumer (the LM-head kernel applies it).
         prefix = (prefix_cache, prefix_len32, G, workspace): groups of G consecutive sequences share the
@@ -225,24 +224,34 @@ class FastDecoder:
             _require(x.dtype == BF16 and x.is_contiguous(), "decode: x must be contiguous bf16")
             B, xr = x.shape[0], x
         ws = self.decode_workspace
+        # row sums of squares of the residual, left by each residual GEMM for the next norm (one per 64-column
+        # block): the norms run inside the qkv / gate_up GEMMs without a pass of their own over x
+        ss_attn = torch.empty(B, cfg.d_model // 64, dtype=torch.float32, device=(tok if tok is not None else x).device)
+        ss_mlp = torch.empty_like(ss_attn)
         for i, blk in enumerate(layers):
             a = blk.attn
             kc, vc = cache.k[i], cache.v[i]
-            if xr is None:  # layer 0 of a step fed with token ids
+            if xr is None:  # layer 0 of a step fed with token ids: the embedding gather + norm
                 xr, h = ops.embed_rmsnorm(tok, W(self.dec.embed.weight), W(blk.attn_norm.weight), eps)
-            else:
+                q = ops.norm_qkv_rope_cache(h, None, eps, W(a.qkv_proj.weight), W(a.q_norm.weight),
+                                            W(a.k_norm.weight), cos, sin, pos, seq, kc, vc, H, HKV, D, rope_pos=rope_pos)
+            elif i == 0:  # x handed in by the caller: no row sums yet
                 h = ops.add_rmsnorm(xr, W(blk.attn_norm.weight), eps)
-            q = ops.norm_qkv_rope_cache(h, None, eps, W(a.qkv_proj.weight), W(a.q_norm.weight), W(a.k_norm.weight),
-                                        cos, sin, pos, seq, kc, vc, H, HKV, D, rope_pos=rope_pos)
+                q = ops.norm_qkv_rope_cache(h, None, eps, W(a.qkv_proj.weight), W(a.q_norm.weight),
+                                            W(a.k_norm.weight), cos, sin, pos, seq, kc, vc, H, HKV, D, rope_pos=rope_pos)
+            else:
+                q = ops.norm_qkv_rope_cache(xr, W(blk.attn_norm.weight), eps, W(a.qkv_proj.weight), W(a.q_norm.weight),
+                                            W(a.k_norm.weight), cos, sin, pos, seq, kc, vc, H, HKV, D, rope_pos=rope_pos,
+                                            ss=ss_attn)
             if prefix is None:
                 o = ops.decode_attention(q, kc, vc, cache_seqlens, workspace=ws)
             else:
                 pc, plen32, G, gws = prefix
                 o = ops.decode_attention_grouped(q, pc.k[i], pc.v[i], plen32, kc, vc, cache_seqlens, G, workspace=gws)
-            ops.linear_residual(o.view(B, H * D), W(a.o_proj.weight), xr)
-            h = ops.add_rmsnorm(xr, W(blk.mlp_norm.weight), eps)
-            g = ops.norm_linear(h, None, eps, W(blk.gate_up.weight), swiglu=True)
-            ops.linear_residual(g, W(blk.down.weight), xr)
+            ops.linear_residual(o.view(B, H * D), W(a.o_proj.weight), xr, ss_out=ss_mlp)
+            g = ops.norm_linear(xr, W(blk.mlp_norm.weight), eps, W(blk.gate_up.weight), swiglu=True, ss=ss_mlp)
+            last = i == len(layers) - 1
+            ops.linear_residual(g, W(blk.down.weight), xr, ss_out=None if last else ss_attn)
         return xr
 
     # ---- Decoder.forward on this path ----------------------------------------------------------
