@@ -43,7 +43,8 @@ def check_stream(gpu_out, oracle_res, steps, thr):
     return float(agree.float().mean()), int((~agree).sum())
 
 
-def run_case(k=1, n_layers=2, lens=(40, 130, 257, 75), steps=24, T=0.0, mh=8, seed=0, ps=1, graph=True, group=1):
+def run_case(k=1, n_layers=2, lens=(40, 130, 257, 75), steps=24, T=0.0, mh=8, seed=0, ps=1, graph=True, group=1,
+             check_every=32, decode_steps="fixed"):
     m = make_model(k, n_layers=n_layers, seed=seed, norm_jitter=0.1, bias_jitter=0.1)
     m.pos_scale = ps
     lens = list(lens)
@@ -54,10 +55,10 @@ def run_case(k=1, n_layers=2, lens=(40, 130, 257, 75), steps=24, T=0.0, mh=8, se
     u = synth_uniforms(len(lens), steps, seed=seed + 2)
     gm = gpu_copy(m)
     eng = DecodeEngine(gm, len(lens), steps, max(lens), cuda_graph=graph, temperature=T, max_homopolymer=mh,
-                       prefill_batch=3, group_size=group)
+                       prefill_batch=3, group_size=group, check_every=check_every)
     if T > 0:
         eng.set_uniforms(u.to(DEV))
-    out = eng.generate(fr.to(DEV), lens).clone()
+    out = eng.generate(fr.to(DEV), lens, steps=steps if decode_steps == "fixed" else None).clone()
     torch.cuda.synchronize()
     ref = R.RefEngine(R.RefModel(m, "fused"), steps, temperature=T, max_homopolymer=mh)
     res = ref.run(list(fr.split(lens)), uniforms=u if T > 0 else None, forced=out.cpu())
@@ -136,6 +137,18 @@ def test_graph_equals_eager_bitwise():
     a, _, _ = run_case(k=1, graph=True, steps=20)
     b, _, _ = run_case(k=1, graph=False, steps=20)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("group", [1, 4])
+def test_multi_step_graph_equals_eager(group):
+    """check_every = 4: 19 steps run as four 4-step replays and three single-step ones; the streams (and, with
+    early exit, where the run stops) equal step-by-step eager decoding."""
+    for T, mode in ((1.0, "fixed"), (0.0, "early")):
+        a, _, ea = run_case(k=1, graph=True, steps=20, T=T, group=group, check_every=4, decode_steps=mode)
+        b, _, eb = run_case(k=1, graph=False, steps=20, T=T, group=group, check_every=4, decode_steps=mode)
+        assert ea.graph_multi is not None
+        assert torch.equal(a, b), (T, mode)
+        assert int(ea.step_idx) == int(eb.step_idx), (T, mode)
 
 
 def test_rollout_deterministic_and_grammar_invariants():

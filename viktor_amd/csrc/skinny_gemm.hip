@@ -606,11 +606,14 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
   u32x2 ctw[2], stw[2];  // the raw table words, widened in the epilogue (here it would wait for the loads)
   const int hd = n0 / 64;
   if constexpr (EPI == EPI_RESID) {
+    // unconditional (row and column clamped; unused where out of range): a load under a branch makes the
+    // compiler wait for every outstanding load, the ring's included, where its register is merged
+    const int64_t orow = erow < p.M ? erow : p.M - 1;
 #pragma unroll
     for (int hf = 0; hf < HALVES; ++hf) {
-      old[hf] = u32x2{0u, 0u};
-      const int col = n0 + 32 * hf + 4 * sub;
-      if (row_ok && col < p.N) old[hf] = *reinterpret_cast<const u32x2 *>(static_cast<bf16_t *>(p.y) + erow * p.N + col);
+      int col = n0 + 32 * hf + 4 * sub;
+      col = col < p.N ? col : p.N - 4;
+      old[hf] = *reinterpret_cast<const u32x2 *>(static_cast<bf16_t *>(p.y) + orow * p.N + col);
     }
   }
   if constexpr (ROPE) {

@@ -88,7 +88,8 @@ class DecodeEngine:
         self._uniforms_set = False
         self.fast.decode_workspace = ops.decode_attention_workspace(batch_size, self.dec.cfg.n_heads,
                                                                     self.cache.max_len, dev)
-        self.graph = None
+        self.graph = None  # one captured step
+        self.graph_multi = None  # check_every captured steps: one replay, no launch gaps between its steps
         if cuda_graph:
             self._capture()
 
@@ -131,6 +132,11 @@ class DecodeEngine:
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self._step()
+        if self.check_every > 1:  # the steps between two early-exit checks, back to back in one graph
+            self.graph_multi = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph_multi, pool=self.graph.pool()):
+                for _ in range(self.check_every):
+                    self._step()
         self.out.fill_(PAD)
 
     # ---- prefill -------------------------------------------------------------------------------
@@ -246,13 +252,19 @@ class DecodeEngine:
         """Run decode steps after prefill. steps=None: stop when all sequences ended (checked every
         check_every steps) or at max_new_tokens. steps=n: run exactly n-1 steps (n output tokens)."""
         n = self.max_new - 1 if steps is None else steps - 1
-        for i in range(n):
-            if self.graph is not None:
+        done = 0
+        while done < n:
+            if self.graph_multi is not None and done % self.check_every == 0 and n - done >= self.check_every:
+                self.graph_multi.replay()  # check_every steps
+                done += self.check_every
+            elif self.graph is not None:
                 self.graph.replay()
+                done += 1
             else:
                 self._step()
-            if steps is None and (i + 1) % self.check_every == 0 and bool(((self.tok == EOS) | (self.tok == PAD)).all()):
-                n = i + 1
+                done += 1
+            if steps is None and done % self.check_every == 0 and bool(((self.tok == EOS) | (self.tok == PAD)).all()):
+                n = done
                 break
         self.step_idx.add_(n)
         return self.out
