@@ -213,6 +213,13 @@ def main():
 
     log("decode-attention timing")
     avg_s, alg_bytes = decode_attention_timing(eng)
+    if args.group_size == 1:
+        attn_kernels = "decode_attention (decode_attn_kernel)"
+    else:
+        from viktor_amd import hip_ops as ops
+        members, parts = ops.decode_attention_grouped_layout(B, args.group_size, P + 1, eng.cache.k.shape[2])
+        attn_kernels = (f"decode_attention_grouped (grouped_attn_kernel: {members} query members per workgroup, "
+                        f"{parts} part(s)" + (" + grouped_combine_kernel)" if parts > 1 else ", no merge launch)"))
     achieved = alg_bytes / avg_s / 1e9
     traffic = None
     tname = "decode_attention_traffic.json" if args.group_size == 1 else "decode_attention_grouped_traffic.json"
@@ -238,8 +245,7 @@ def main():
                    "parallelism": "single GPU"},
         "prefill_ms": round(prefill_ms, 2), "decode_ms": round(decode_ms, 2),
         "live_tokens_per_rollout": live,
-        "roofline": {"kernel": "decode_attention" if args.group_size == 1 else
-                     "decode_attention_grouped (grouped_attn_kernel + grouped_combine_kernel)",
+        "roofline": {"kernel": attn_kernels,
                      "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "avg_launch_us": round(avg_s * 1e6, 2),

@@ -131,6 +131,11 @@ int vk_decode_attention_grouped(const void *q, const void *k_prefix, const void 
 
 int vk_decode_attention_grouped_workspace(int64_t B, int32_t G, int64_t pre_max, int64_t suf_max, int64_t *bytes);
 
+/* How vk_decode_attention_grouped runs at these sizes: query members per workgroup (G, or G / 2 when the
+ * groups are split by member) and parts per subgroup (1: one launch; > 1: a merge launch follows). */
+int vk_decode_attention_grouped_layout(int64_t B, int32_t G, int64_t pre_max, int64_t suf_max, int32_t *members,
+                                       int32_t *parts);
+
 /*
  * Variable-length GQA attention over packed queries (flash_attn_varlen_func semantics, scale 1/sqrt(D)).
  * Sequence i has q_len_i = cu_q[i+1] - cu_q[i] queries (rows cu_q[i].. of q[*, H, D]) and

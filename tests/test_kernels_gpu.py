@@ -227,6 +227,34 @@ def test_decode_attention_grouped(G, pre_max, suf_max):
         assert err < 1e-2, (b, lp, ls, float(err))
 
 
+@pytest.mark.parametrize("G,P,pre_max,suf_max", [(8, 64, 200, 70), (16, 64, 90, 33)])
+def test_decode_attention_grouped_member_split(G, P, pre_max, suf_max):
+    """Enough groups for each to be split into two halves of G / 2 members (one part each, output written by
+    the attention kernel itself, no merge launch): equal to attention over the concatenated rows, and the
+    same bits on a second call."""
+    g = gen(G * 31 + P)
+    B, H, HKV, D = P * G, 8, 2, 64
+    plen = torch.randint(1, pre_max + 1, (P,), generator=g).int()
+    plen[:4] = torch.tensor([1, 31, 32, pre_max])
+    slen = torch.randint(1, suf_max + 1, (B,), generator=g).int()
+    slen[:5] = torch.tensor([1, 2, 32, 33, suf_max])
+    q = torch.randn(B, H, D, generator=g).to(BF)
+    kp, vp = (torch.randn(P, pre_max, HKV, D, generator=g).to(BF) for _ in range(2))
+    ks, vs = (torch.randn(B, suf_max, HKV, D, generator=g).to(BF) for _ in range(2))
+    args = [t.to(DEV) for t in (q, kp, vp, plen, ks, vs, slen)]
+    out = ops.decode_attention_grouped(*args, G)
+    again = ops.decode_attention_grouped(*args, G)
+    assert torch.equal(out, again)
+    out = out.cpu()
+    for b in list(range(0, B, 5)) + [G // 2 - 1, G // 2, B - 1]:
+        p, lp, ls = b // G, int(plen[b // G]), int(slen[b])
+        k = torch.cat([kp[p, :lp], ks[b, :ls]])[None]
+        v = torch.cat([vp[p, :lp], vs[b, :ls]])[None]
+        ref = _sdpa_ref(q[b:b + 1], k, v, torch.tensor([lp + ls]))
+        err = (out[b:b + 1].float() - ref).abs().max()
+        assert err < 1e-2, (b, lp, ls, float(err))
+
+
 def test_decode_attention_grouped_cache_view_and_graph():
     """Layer views of [L, P, S, 2, 64] / [L, B, S, 2, 64] caches inside a graph replayed several times; the
     ungrouped kernel over the concatenated rows agrees to bf16 rounding."""

@@ -42,6 +42,7 @@ SIGNATURES = {
     "vk_decode_attention_grouped": [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _I32,
                                     _I32, _I32, _I32, _P, _I64, _P],
     "vk_decode_attention_grouped_workspace": [_I64, _I32, _I64, _I64, ctypes.POINTER(_I64)],
+    "vk_decode_attention_grouped_layout": [_I64, _I32, _I64, _I64, ctypes.POINTER(_I32), ctypes.POINTER(_I32)],
     "vk_norm_qkv_rope_cache": [_P, _P, _I64, _P, _P, _F, _P, _P, _P, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _I64,
                                _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P],
     "vk_linear_residual": [_P, _P, _P, _I64, _I32, _I32, _P, _P],

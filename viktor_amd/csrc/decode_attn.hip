@@ -269,30 +269,31 @@ static int64_t workspace_bytes_for(int64_t B, const DecodeSplit &sp) {
 //
 // A sequence of group p attends to the group's prefix rows (frames + BOS, one copy in the prefix cache
 // [P, S_pre, 2, 64]) followed by its own rows (sampled tokens, own-row cache [B, S_own, 2, 64]).
-// One launch: a workgroup per (part, group p, KV head). Its query columns are the 4 heads of that KV head
-// for all G members (4 G columns), and it walks one tile space: the prefix tiles (every column attends),
+// One launch: a workgroup per (part, subgroup, KV head), where a subgroup is G consecutive members of a
+// prefix group (the whole group, or 1 / msplit of it). Its query columns are the 4 heads of that KV head
+// for its G members (4 G columns), and it walks one tile space: the prefix tiles (every column attends),
 // then the own-row tiles of members 0..G-1 (only that member's 4 columns attend; the others are masked).
-// The tile space is cut into `nparts` equal parts, so every wave runs a long software-pipelined loop and
-// prefix rows are fetched once per group. Each part leaves a partial (max, sum, unnormalised output) per
-// column; a small combine kernel merges the parts of each (sequence, head).
+// The tile space is cut into `nparts` equal parts, so every wave runs a long software-pipelined loop.
+// With nparts > 1 each part leaves a partial (max, sum, unnormalised output) per column and a small
+// combine kernel merges the parts of each (sequence, head); with one part the workgroup writes the bf16
+// output itself. With msplit > 1 the subgroups of one prefix group read the same prefix rows, launched
+// next to each other on one XCD, so the second read comes from its L2.
 
-// wavefronts per workgroup and resident workgroups per CU the part count aims for, per group size
-// (LDS of the epilogue merge grows with the 4 G columns; registers with the column blocks)
-constexpr int gu_waves(int G) { return G == 8 ? 8 : 4; }
-constexpr int gu_wg_per_cu(int G) { return G >= 8 ? 1 : 4; }
+// resident workgroups per CU the part count aims for, per wave count (LDS of the epilogue merge grows
+// with the 4 G columns; registers with the column blocks)
+constexpr int gu_wg_per_cu(int waves) { return waves >= 8 ? 1 : 4; }
 constexpr int GU_TILE = 32;
 constexpr int GU_PITCH = 72;  // one KV head: 64 + 8 pad
 
-template <int G>
-__global__ __launch_bounds__(gu_waves(G) * 64) void grouped_attn_kernel(
+template <int G, int GU_WAVES>
+__global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ kp, const bf16_t *__restrict__ vp,
     const int32_t *__restrict__ pre_len, int64_t stride_pb, int64_t stride_ps, int64_t pre_max,
     const bf16_t *__restrict__ ks, const bf16_t *__restrict__ vs, const int32_t *__restrict__ own_len,
-    int64_t stride_sb, int64_t stride_ss, int64_t own_max, int nparts, float *__restrict__ ws_o,
-    float *__restrict__ ws_ml, float scale_log2) {
+    int64_t stride_sb, int64_t stride_ss, int64_t own_max, int nparts, int msplit, float *__restrict__ ws_o,
+    float *__restrict__ ws_ml, bf16_t *__restrict__ out, float scale_log2) {
   constexpr int NC = 4 * G;            // query columns of one KV head (G members x 4 heads)
   constexpr int NCB = (NC + 15) / 16;  // 16-column MFMA blocks
-  constexpr int GU_WAVES = gu_waves(G);
   constexpr int LDS_V = GU_WAVES * GU_TILE * GU_PITCH * 2;
   constexpr int LDS_M = (GU_WAVES * NC * 64 + 2 * GU_WAVES * NC) * 4;
   __shared__ __attribute__((aligned(16))) char smem[LDS_V > LDS_M ? LDS_V : LDS_M];
@@ -301,11 +302,13 @@ __global__ __launch_bounds__(gu_waves(G) * 64) void grouped_attn_kernel(
   const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, g = lane >> 4;
   // 1-D grid, XCD-aware: workgroup i runs on XCD i % 8, which takes a contiguous range of the logical order
-  // (group, part, KV head) with the KV head fastest, so the two workgroups that read the two halves of the
-  // same 256-byte cache rows run back to back on one XCD (a bijection for any count)
+  // (subgroup, part, KV head) with the KV head fastest, so the two workgroups that read the two halves of
+  // the same 256-byte cache rows run back to back on one XCD, and so do the subgroups of one prefix group
+  // (a bijection for any count)
   const int tiles = gridDim.x, pid = blockIdx.x, xcd = pid & 7, idx = pid >> 3;
   const int lt_id = xcd * (tiles >> 3) + min(xcd, tiles & 7) + idx;
-  const int kvh = lt_id & 1, part = (lt_id >> 1) % nparts, p = (lt_id >> 1) / nparts;
+  const int kvh = lt_id & 1, part = (lt_id >> 1) % nparts, p = (lt_id >> 1) / nparts;  // p: subgroup
+  const int pp = p / msplit;                                                            // its prefix group
 
   // The part's tiles: its static share of the prefix tiles (sized by pre_max, so they are known before any
   // length is read; tiles past the group's actual prefix length are fully masked), then its share of the
@@ -313,7 +316,7 @@ __global__ __launch_bounds__(gu_waves(G) * 64) void grouped_attn_kernel(
   // shares are equal cuts, so parts are balanced for any part count.
   const int tp_all = static_cast<int>((pre_max + GU_TILE - 1) / GU_TILE);
   const int pt0 = tp_all * part / nparts, npre = tp_all * (part + 1) / nparts - pt0;
-  const bf16_t *kpre = kp + p * stride_pb + kvh * DA_D, *vpre = vp + p * stride_pb + kvh * DA_D;
+  const bf16_t *kpre = kp + pp * stride_pb + kvh * DA_D, *vpre = vp + pp * stride_pb + kvh * DA_D;
 
   struct TileRef {
     const bf16_t *k, *v;
@@ -358,7 +361,7 @@ __global__ __launch_bounds__(gu_waves(G) * 64) void grouped_attn_kernel(
     len = static_cast<int>(l < 0 ? 0 : (l > own_max ? own_max : l));
     cnt = (len + GU_TILE - 1) / GU_TILE;
   } else if (lane == G) {
-    const int64_t l = pre_len[p];
+    const int64_t l = pre_len[pp];
     len = static_cast<int>(l < 1 ? 1 : (l > pre_max ? pre_max : l));
   }
   int incl = cnt;
@@ -548,7 +551,9 @@ __global__ __launch_bounds__(gu_waves(G) * 64) void grouped_attn_kernel(
     }
   }
   __syncthreads();
-  // partial of (group p, KV head, part, column j); a column no row of this part reaches: (-inf, 0, 0)
+  // partial of (subgroup p, KV head, part, column j); a column no row of this part reaches: (-inf, 0, 0).
+  // One part: the output itself, bf16(N / L) -- what the combine computes from a single partial, bit for
+  // bit (its weight is exp2(0) = 1); every column then has at least the first prefix row.
   for (int o = threadIdx.x; o < NC * 64; o += GU_WAVES * 64) {
     const int j = o / 64, d = o % 64;
     float M = -INFINITY;
@@ -562,6 +567,11 @@ __global__ __launch_bounds__(gu_waves(G) * 64) void grouped_attn_kernel(
         L += e * Ls[w * NC + j];
         N += e * Os[(w * NC + j) * 64 + d];
       }
+    }
+    if (nparts == 1) {
+      const int64_t b = static_cast<int64_t>(p) * G + j / 4;
+      out[(b * DA_H + kvh * 4 + (j & 3)) * DA_D + d] = f2bf(N / L);
+      continue;
     }
     const int64_t base = ((static_cast<int64_t>(p) * DA_HKV + kvh) * nparts + part) * NC + j;
     ws_o[base * DA_D + d] = N;
@@ -606,41 +616,56 @@ __global__ __launch_bounds__(DA_H * DA_D) void grouped_combine_kernel(const floa
 }
 
 struct GroupedLayout {
-  int nparts;
+  int gq;      // query members per workgroup (the kernel's G)
+  int msplit;  // subgroups per prefix group (G / gq)
+  int waves;   // wavefronts per workgroup
+  int nparts;  // parts of each subgroup's tile space (1: no combine launch)
   int64_t o, ml, total;  // offsets / size in floats
 };
 
-// Parts per (group, KV head): one resident round of workgroups over the CUs, and at least one tile per
-// wave at the longest lengths.
+// Groups of G >= 8 whose halves alone fill a resident round of 8-wave workgroups are split by member: each
+// half walks the whole tile space (one part, no combine) with half the query columns, which also halves the
+// masked work of the own-row tiles. Otherwise the whole group is one subgroup and its tile space is cut into
+// parts: one resident round of workgroups over the CUs, and at least one tile per wave at the longest lengths.
 static GroupedLayout grouped_layout(int64_t B, int G, int64_t pre_max, int64_t own_max, int cus) {
   GroupedLayout L{};
-  const int64_t pairs = (B / G) * DA_HKV;
-  const int waves = G >= 16 ? gu_waves(16) : (G == 8 ? gu_waves(8) : gu_waves(4));
-  const int per_cu = G >= 16 ? gu_wg_per_cu(16) : (G == 8 ? gu_wg_per_cu(8) : gu_wg_per_cu(4));
-  const int64_t target = static_cast<int64_t>(cus) * per_cu;
-  int64_t np = (target + pairs - 1) / pairs;
-  const int64_t tmax = (pre_max + GU_TILE - 1) / GU_TILE + G * ((own_max + GU_TILE - 1) / GU_TILE);
-  const int64_t cap = tmax / waves;
-  if (np > cap) np = cap;
-  if (np > 16) np = 16;  // the combine kernel is instantiated for 1 .. 16 parts
-  if (np < 1) np = 1;
-  L.nparts = static_cast<int>(np);
-  const int64_t cols = pairs * L.nparts * 4 * G;
+  if (G >= 8 && (B / G) * 2 * DA_HKV >= cus) {
+    L.gq = G / 2;
+    L.msplit = 2;
+    L.waves = 8;  // (16 waves measured slower)
+    L.nparts = 1;
+  } else {
+    L.gq = G;
+    L.msplit = 1;
+    L.waves = G == 8 ? 8 : 4;
+    const int64_t pairs = (B / G) * DA_HKV;
+    const int64_t target = static_cast<int64_t>(cus) * gu_wg_per_cu(L.waves);
+    int64_t np = (target + pairs - 1) / pairs;
+    const int64_t tmax = (pre_max + GU_TILE - 1) / GU_TILE + G * ((own_max + GU_TILE - 1) / GU_TILE);
+    const int64_t cap = tmax / L.waves;
+    if (np > cap) np = cap;
+    if (np > 16) np = 16;  // the combine kernel is instantiated for 1 .. 16 parts
+    if (np < 1) np = 1;
+    L.nparts = static_cast<int>(np);
+  }
+  const int64_t cols = (B / L.gq) * DA_HKV * L.nparts * 4 * L.gq;
   L.o = 0;
   L.ml = cols * DA_D;
   L.total = L.ml + cols * 2;
   return L;
 }
 
-template <int G>
-static void launch_grouped(const bf16_t *q, const bf16_t *kp, const bf16_t *vp, const int32_t *pre_len, int64_t P,
-                           int64_t stride_pb, int64_t stride_ps, int64_t pre_max, const bf16_t *ks, const bf16_t *vs,
-                           const int32_t *own_len, int64_t stride_sb, int64_t stride_ss, int64_t own_max, int nparts,
-                           float *ws_o, float *ws_ml, float scale_log2, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(P * nparts * DA_HKV));
-  grouped_attn_kernel<G><<<grid, gu_waves(G) * 64, 0, s>>>(q, kp, vp, pre_len, stride_pb, stride_ps, pre_max, ks, vs,
-                                                        own_len, stride_sb, stride_ss, own_max, nparts, ws_o, ws_ml,
-                                                        scale_log2);
+// Psub = subgroups (B / gq)
+template <int G, int W>
+static void launch_grouped(const bf16_t *q, const bf16_t *kp, const bf16_t *vp, const int32_t *pre_len,
+                           int64_t Psub, int64_t stride_pb, int64_t stride_ps, int64_t pre_max, const bf16_t *ks,
+                           const bf16_t *vs, const int32_t *own_len, int64_t stride_sb, int64_t stride_ss,
+                           int64_t own_max, int nparts, int msplit, float *ws_o, float *ws_ml, bf16_t *out,
+                           float scale_log2, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(Psub * nparts * DA_HKV));
+  grouped_attn_kernel<G, W><<<grid, W * 64, 0, s>>>(q, kp, vp, pre_len, stride_pb, stride_ps, pre_max, ks, vs,
+                                                    own_len, stride_sb, stride_ss, own_max, nparts, msplit, ws_o,
+                                                    ws_ml, out, scale_log2);
 }
 }  // namespace vk
 
@@ -699,6 +724,16 @@ extern "C" int vk_decode_attention_grouped_workspace(int64_t B, int32_t G, int64
   return VK_OK;
 }
 
+extern "C" int vk_decode_attention_grouped_layout(int64_t B, int32_t G, int64_t pre_max, int64_t suf_max,
+                                                  int32_t *members, int32_t *parts) {
+  VK_CHECK_ARG(members && parts && B > 0 && G > 0 && B % G == 0 && pre_max > 0 && suf_max > 0,
+               "decode_attention_grouped_layout: bad arguments");
+  const GroupedLayout L = grouped_layout(B, G, pre_max, suf_max, device_cus_cached());
+  *members = L.gq;
+  *parts = L.nparts;
+  return VK_OK;
+}
+
 extern "C" int vk_decode_attention_grouped(const void *q, const void *k_prefix, const void *v_prefix,
                                            const int32_t *prefix_len, int64_t stride_pb, int64_t stride_ps,
                                            int64_t pre_max, const void *k_suffix, const void *v_suffix,
@@ -730,24 +765,22 @@ extern "C" int vk_decode_attention_grouped(const void *q, const void *k_prefix, 
   const auto vp = static_cast<const bf16_t *>(v_prefix);
   const auto ks = static_cast<const bf16_t *>(k_suffix);
   const auto vs = static_cast<const bf16_t *>(v_suffix);
-  const int64_t P = B / G;
-#define VK_GROUPED(GG)                                                                                         \
-  launch_grouped<GG>(qb, kp, vp, prefix_len, P, stride_pb, stride_ps, pre_max, ks, vs, suffix_len, stride_sb,   \
-                     stride_ss, suf_max, L.nparts, ws + L.o, ws + L.ml, scale_log2, s)
-  switch (G) {
-    case 2: VK_GROUPED(2); break;
-    case 4: VK_GROUPED(4); break;
-    case 8: VK_GROUPED(8); break;
-    default: VK_GROUPED(16); break;
-  }
+  bf16_t *ob = static_cast<bf16_t *>(out);
+#define VK_GROUPED(GG, WW)                                                                                     \
+  launch_grouped<GG, WW>(qb, kp, vp, prefix_len, B / L.gq, stride_pb, stride_ps, pre_max, ks, vs, suffix_len,    \
+                         stride_sb, stride_ss, suf_max, L.nparts, L.msplit, ws + L.o, ws + L.ml, ob, scale_log2, s)
+  if (L.gq == 2) VK_GROUPED(2, 4);
+  else if (L.gq == 4 && L.waves == 8) VK_GROUPED(4, 8);
+  else if (L.gq == 4) VK_GROUPED(4, 4);
+  else if (L.gq == 8) VK_GROUPED(8, 8);
+  else VK_GROUPED(16, 4);
 #undef VK_GROUPED
   const int rc = launch_status("decode_attention_grouped");
-  if (rc != VK_OK) return rc;
+  if (rc != VK_OK || L.nparts == 1) return rc;  // one part: the kernel wrote the output
   const dim3 cgrid(static_cast<unsigned>(B));
-  bf16_t *ob = static_cast<bf16_t *>(out);
   switch (L.nparts) {
 #define VK_COMBINE(NP) \
-  case NP: grouped_combine_kernel<NP><<<cgrid, DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml, ob, G); break;
+  case NP: grouped_combine_kernel<NP><<<cgrid, DA_H * DA_D, 0, s>>>(ws + L.o, ws + L.ml, ob, L.gq); break;
     VK_COMBINE(1) VK_COMBINE(2) VK_COMBINE(3) VK_COMBINE(4) VK_COMBINE(5) VK_COMBINE(6) VK_COMBINE(7)
     VK_COMBINE(8) VK_COMBINE(9) VK_COMBINE(10) VK_COMBINE(11) VK_COMBINE(12) VK_COMBINE(13) VK_COMBINE(14)
     VK_COMBINE(15) VK_COMBINE(16)

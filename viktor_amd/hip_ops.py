@@ -174,6 +174,15 @@ def decode_attention_grouped_workspace(B, G, pre_max, suf_max, device):
     return torch.empty(nbytes.value, dtype=torch.uint8, device=device)
 
 
+def decode_attention_grouped_layout(B, G, pre_max, suf_max):
+    """(query members per workgroup, parts per subgroup) of decode_attention_grouped at these sizes: G or G / 2
+    (groups split by member), and 1 part (one launch) or more (a merge launch follows)."""
+    m, n = ctypes.c_int32(0), ctypes.c_int32(0)
+    _lib.check(_lib.load().vk_decode_attention_grouped_layout(B, G, pre_max, suf_max, ctypes.byref(m), ctypes.byref(n)),
+               "decode_attention_grouped_layout")
+    return m.value, n.value
+
+
 def decode_attention_grouped(q, k_prefix, v_prefix, prefix_len, k_suffix, v_suffix, suffix_len, group_size,
                              workspace=None):
     """Decode attention of B = P * G sequences whose groups of G consecutive rows share a prefix: sequence b
