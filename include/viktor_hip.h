@@ -141,7 +141,8 @@ int vk_decode_attention_grouped_layout(int64_t B, int32_t G, int64_t pre_max, in
  * Sequence i has q_len_i = cu_q[i+1] - cu_q[i] queries (rows cu_q[i].. of q[*, H, D]) and
  * k_len_i = k_lens[i] keys; key j of sequence i is at k + k_off[i] + j * stride_tok (+ hk * D), same for v.
  * causal != 0: query r of sequence i sits at position k_len_i - q_len_i + r and sees keys <= it
- * (bottom-right alignment). out[*, H, D] bf16.
+ * (bottom-right alignment). out[*, H, D] bf16. lse (NULL: not written): [*, H] fp32, each row's
+ * log-sum-exp of its scaled scores in log2 units, log2(sum_j 2^(s_j * log2(e) / sqrt(D))), for the backward.
  * plan: n_blocks entries of (sequence, first query row) built by the host, one per 64-query block.
  * Built for H = 8, HKV = 2, D = 64.
  * Replaces flash_attn_varlen_func (viktor/fast_decoder.py:68-73) and flash_attn_func (viktor/decoder.py:82-87).
@@ -149,7 +150,7 @@ int vk_decode_attention_grouped_layout(int64_t B, int32_t G, int64_t pre_max, in
 int vk_varlen_attention(const void *q, const void *k, const void *v, const int32_t *cu_q, const int64_t *k_off,
                         const int32_t *k_lens, const int32_t *plan, int32_t n_blocks, int32_t n_seq,
                         int64_t stride_tok, void *out, int32_t causal, int32_t H, int32_t HKV, int32_t D,
-                        void *stream);
+                        float *lse, void *stream);
 
 /*
  * One decode step's token choice and bookkeeping for B sequences (DecodeEngine._select + state update):
@@ -239,6 +240,69 @@ int vk_gspo_score(const void *logits, int32_t logits_dtype, const int64_t *targe
  */
 int vk_group_advantage(const float *reward, int64_t groups, int32_t n, int32_t mode, float param, float *adv,
                        uint8_t *live, void *stream);
+
+/* ---- the GSPO update's backward and optimizer step (scripts/gspo.py:477-493) ----------------------- */
+
+/*
+ * Backward of causal GQA self-attention over packed sequences (flash_attn_func(causal=True) under autocast,
+ * viktor/decoder.py:82-87, differentiated by the update's backward at scripts/gspo.py:477). Sequence i is
+ * rows cu[i] .. cu[i+1]-1 of q / out / dout [n_rows, 8, 64] bf16 and of k / v (row j at j * stride_tok,
+ * + kv head * 64); query r sees keys <= r. lse [n_rows, 8]: the forward's vk_varlen_attention log-sum-exp
+ * (log2 units). q_plan: (sequence, first row) per 64-query block (as vk_varlen_attention's plan); k_plan:
+ * (sequence, first key) per 64-key block. dd [n_rows, 8] fp32 scratch (written: sum_d dout * out);
+ * dq [n_rows, 8, 64], dk / dv [n_rows, 2, 64] fp32 (written). H = 8, HKV = 2, D = 64.
+ */
+int vk_attention_backward(const void *q, const void *k, const void *v, const void *out, const void *dout,
+                          const float *lse, const int32_t *cu, int32_t n_seq, const int32_t *q_plan, int32_t n_qblocks,
+                          const int32_t *k_plan, int32_t n_kblocks, int64_t n_rows, int64_t stride_tok, float *dd,
+                          float *dq, float *dk, float *dv, int32_t H, int32_t HKV, int32_t D, void *stream);
+
+/* Workgroups (= rows of the weight-gradient partials) vk_rmsnorm_backward uses for n rows. */
+int vk_rmsnorm_backward_blocks(int64_t n, int32_t *blocks);
+
+/*
+ * RMSNorm backward (nn.RMSNorm of the decoder blocks, viktor/decoder.py:110-124), d = 512: given x [n, d]
+ * bf16, weight w [d] bf16 and dy [n, d] (bf16 or fp32 per dy_dtype): dx = r w dy - x r^3 mean(w dy x)
+ * (+ dres when not NULL: the residual stream's incoming gradient; dx may alias dres), fp32;
+ * dw_part [vk_rmsnorm_backward_blocks(n), d] fp32: per-workgroup sums of dy x r (reduce with vk_colsum).
+ */
+int vk_rmsnorm_backward(const void *x, const void *w, const void *dy, int32_t dy_dtype, const float *dres,
+                        float *dx, float *dw_part, int64_t n, int32_t d, float eps, void *stream);
+
+/* out[c] = sum_r part[r, c] (+ out[c] when accumulate), fixed order. */
+int vk_colsum(const float *part, float *out, int32_t rows, int32_t cols, int32_t accumulate, void *stream);
+
+/*
+ * Backward of the QK-norm + RoPE stage (viktor/decoder.py:62-66 with apply_rope, viktor/encoder.py:36-40):
+ * qkv [n, (H + 2 HKV) 64] bf16 (the projection output), dq [n, H, 64] / dk / dv [n, HKV, 64] fp32 (the
+ * attention's input gradients), RoPE rows rope_pos [n] of cos/sin [table_rows, 32]. Writes dqkv [n, (H + 2 HKV) 64]
+ * bf16 (q / k heads through the rotation and the 64-wide norm, v heads copied) and dw_part
+ * [vk_rmsnorm_backward_blocks(n), 128] fp32 (q-norm weight partials 0..63, k-norm 64..127). D = 64.
+ */
+int vk_qknorm_rope_backward(const void *qkv, const void *q_norm_w, const void *k_norm_w, const void *cos_t,
+                            const void *sin_t, int32_t table_dtype, int64_t table_rows, const int32_t *rope_pos,
+                            const float *dq, const float *dk, const float *dv, void *dqkv, float *dw_part, int64_t n,
+                            int32_t H, int32_t HKV, int32_t D, float eps, void *stream);
+
+/* SwiGLU backward (F.silu(gate) * up, viktor/decoder.py:127): gu [n, 2F] (gate | up) bf16, dout [n, F] bf16
+ * -> dgu [n, 2F] bf16. F % 8 == 0. */
+int vk_swiglu_backward(const void *gu, const void *dout, void *dgu, int64_t n, int32_t F, void *stream);
+
+/*
+ * Global gradient norm and clip coefficient of nn.utils.clip_grad_norm_ (scripts/gspo.py:492) over the flat
+ * fp32 gradient g [n]: norm_out[0] = ||g||_2, norm_out[1] = min(1, max_norm / (||g|| + 1e-6)), on the device.
+ * partials: n_partials floats of scratch.
+ */
+int vk_grad_norm_clip(const float *g, int64_t n, float max_norm, float *partials, int32_t n_partials,
+                      float *norm_out, void *stream);
+
+/*
+ * AdamW step (torch.optim.AdamW, scripts/gspo.py:368, 493) over flat fp32 params p, grads g (scaled by
+ * coef[1] when coef is not NULL: the clip coefficient of vk_grad_norm_clip) and moments m, v:
+ * m = b1 m + (1 - b1) g, v = b2 v + (1 - b2) g^2, p = p (1 - lr wd) - lr / (1 - b1^step) m / (sqrt(v / (1 - b2^step)) + eps).
+ */
+int vk_adamw(float *p, const float *g, float *m, float *v, int64_t n, const float *coef, float lr, float b1, float b2,
+             float eps, float wd, int64_t step, void *stream);
 
 #ifdef __cplusplus
 }

@@ -31,8 +31,9 @@ def rope_tables(dim, max_len, theta):
 
 
 def apply_rope(x, cos, sin):
-    """x [..., T, H, D]; cos/sin [..., T, D/2]: rotate the first half against the second half."""
-    x1, x2 = x.float().chunk(2, -1)
+    """x [..., T, H, D]; cos/sin [..., T, D/2]: rotate the first half against the second half (in fp32, or in
+    fp64 for fp64 input)."""
+    x1, x2 = x.to(torch.promote_types(x.dtype, torch.float32)).chunk(2, -1)
     c, s = cos.unsqueeze(-2), sin.unsqueeze(-2)
     return torch.cat([x1 * c - x2 * s, x1 * s + x2 * c], -1)
 
@@ -226,6 +227,9 @@ class RefModel:
     def logits(self, frames, tokens_in, plens=None):
         """Teacher-forced logits [B, T, V] (fp32 mode) or bf16-rounded (fused mode), reference:
         viktor/model.py:55-85 with the window packed as [plens[b] frames | tokens]."""
+        return self._logits(frames, tokens_in, plens)
+
+    def _logits(self, frames, tokens_in, plens=None):
         B, P, _ = frames.shape
         T = tokens_in.shape[1]
         out = []
@@ -419,6 +423,30 @@ def gspo_loss_autograd(logits, targets, mask, old_lp, n_bases, adv, eps_lo, eps_
     loss = pg.sum() * inv_n
     loss.backward()
     return loss.detach(), s.detach(), pg.detach(), lp.detach(), z.grad
+
+
+def gspo_param_grads(ref, frames, tokens_in, plens, targets, mask, old_lp, n_bases, adv, eps_lo, eps_hi, inv_n,
+                     dtype=torch.float32):
+    """Gradients of the GSPO loss (scripts/gspo.py:471-477) w.r.t. every projector / decoder parameter by
+    autograd through the restated teacher-forced forward (viktor/model.py:55-60, viktor/decoder.py:54-144),
+    in `dtype` (fp32 mode weights; fp64 for finite-difference checks). Returns (loss, {name: grad})."""
+    assert ref.mode == "fp32"
+    params = {n: t.detach().to(dtype).clone().requires_grad_(True) for n, t in ref.p.items()}
+    saved, saved_tables = ref.p, (ref.cos, ref.sin)
+    ref.p, ref.cos, ref.sin = params, ref.cos.to(dtype), ref.sin.to(dtype)
+    try:
+        with torch.enable_grad():
+            z = ref._logits(frames.to(dtype), tokens_in, plens)
+            lp = torch.log_softmax(z, -1).gather(-1, targets.clamp(min=0)[..., None])[..., 0]
+            s = torch.stack([((lp[b][mask[b]] - old_lp[b][mask[b]].to(dtype)).sum() / n_bases[b]).exp()
+                             for b in range(z.shape[0])])
+            a = adv.to(dtype)
+            pg = -torch.minimum(s * a, s.clamp(1 - eps_lo, 1 + eps_hi) * a)
+            loss = pg.sum() * inv_n
+            loss.backward()
+    finally:
+        ref.p, (ref.cos, ref.sin) = saved, saved_tables
+    return loss.detach(), {n: p.grad for n, p in params.items() if p.grad is not None}
 
 
 def gspo_grad_closed_form(logits, targets, mask, old_lp, n_bases, adv, eps_lo, eps_hi, inv_n):

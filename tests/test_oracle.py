@@ -318,3 +318,46 @@ def test_sampled_mask_rule():
     assert m[1].tolist() == [True, True, False]
     # "ACG" did not end -> its EOS target is dropped
     assert m[2].tolist() == [True, False, False]
+
+
+def test_gspo_param_grads_match_finite_differences():
+    """The oracle's parameter gradients of the GSPO loss (autograd through the fp32 restatement) against
+    central differences in fp64 on a one-layer model: pins the gradient oracle the update's HIP backward is
+    checked against. The clip range is wide (no clamp), so the objective is smooth."""
+    from viktor_amd.synthetic import frames as synth_frames, make_model
+    m = make_model(1, n_layers=1, seed=21, norm_jitter=0.1, bias_jitter=0.1)
+    ref = R.RefModel(m, "fp32")
+    g = torch.Generator().manual_seed(22)
+    fr = synth_frames(2, 9, 512, seed=23)
+    plens = torch.tensor([9, 5])
+    tok = torch.randint(3, 7, (2, 4), generator=g)
+    targets = torch.randint(3, 7, (2, 4), generator=g)
+    mask = torch.ones(2, 4, dtype=torch.bool)
+    mask[1, 3] = False
+    old = -1.5 + 0.1 * torch.randn(2, 4, generator=g)
+    n_bases = torch.tensor([4.0, 3.0])
+    adv = torch.tensor([0.7, -1.2])
+    args = (fr, tok, plens, targets, mask, old, n_bases, adv, 10.0, 10.0, 0.5)
+    loss, grads = R.gspo_param_grads(ref, *args, dtype=torch.float64)
+    names = ["projector.0.weight", "projector.2.bias", "decoder.embed.weight", "decoder.layers.0.attn_norm.weight",
+             "decoder.layers.0.attn.qkv_proj.weight", "decoder.layers.0.attn.q_norm.weight",
+             "decoder.layers.0.attn.k_norm.weight", "decoder.layers.0.attn.o_proj.weight",
+             "decoder.layers.0.gate_up.weight", "decoder.layers.0.down.weight", "decoder.norm.weight",
+             "decoder.lm_head.weight"]
+    base = ref.p
+    for name in names:
+        gr = grads[name]
+        # the element with the largest gradient, and one more
+        flat = gr.reshape(-1)
+        for idx in (int(flat.abs().argmax()), int(torch.randint(0, flat.numel(), (1,), generator=g))):
+            vals = []
+            for sgn in (1.0, -1.0):
+                p2 = {n: t.double().clone() for n, t in base.items()}
+                p2[name].view(-1)[idx] += sgn * 1e-4
+                ref.p = p2
+                lv, _ = R.gspo_param_grads(ref, *args, dtype=torch.float64)
+                vals.append(float(lv))
+            ref.p = base
+            fd = (vals[0] - vals[1]) / 2e-4
+            an = float(flat[idx])
+            assert abs(fd - an) <= 1e-5 + 1e-3 * abs(an), (name, idx, fd, an)

@@ -1,0 +1,209 @@
+"""The GSPO update's backward and optimizer kernels against fp32 autograd / torch.optim on the CPU, and the
+whole decoder's parameter gradients against the oracle's (pinned to finite differences in test_oracle.py).
+
+Bars: element-wise backward kernels to fp32 rounding (bf16 outputs to one bf16 rounding); the attention
+backward within 2% of the largest gradient entry (its P and dS are bf16 MFMA operands, as in
+flash-attention's backward); AdamW + clip to 1e-5 relative; decoder parameter gradients of the bf16 path
+within 10% relative L2 and cosine > 0.99 of the fp32 oracle's.
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import reference as R
+from viktor_amd import hip_ops as ops
+from viktor_amd import train as TR
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _attn_ref(q, k, v, do):
+    """fp32 autograd of causal GQA attention of one sequence: (o, lse2 [H, T], dq, dk, dv)."""
+    q, k, v = (t.float().clone().requires_grad_(True) for t in (q, k, v))
+    T = q.shape[0]
+    s = torch.einsum("qhd,khd->hqk", q, k.repeat_interleave(4, 1)) / 8.0
+    s = s.masked_fill(torch.ones(T, T, dtype=torch.bool).triu(1)[None], float("-inf"))
+    lse2 = torch.logsumexp(s, -1) / math.log(2.0)
+    o = torch.einsum("hqk,khd->qhd", torch.softmax(s, -1), v.repeat_interleave(4, 1))
+    (o * do.float()).sum().backward()
+    return o.detach(), lse2.detach(), q.grad, k.grad, v.grad
+
+
+@pytest.mark.parametrize("lens", [(1, 37, 64, 65, 130), (300,), (64, 64)])
+def test_attention_backward(lens):
+    g = gen(sum(lens))
+    N = sum(lens)
+    q = torch.randn(N, 8, 64, generator=g).to(BF)
+    k = torch.randn(N, 2, 64, generator=g).to(BF)
+    v = torch.randn(N, 2, 64, generator=g).to(BF)
+    do = torch.randn(N, 8, 64, generator=g).to(BF)
+    plan = TR.TrainPlan(list(lens), DEV)
+    lse = torch.empty(N, 8, device=DEV)
+    qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+    o = ops.varlen_attention(qd, kd, vd, plan.attn, lse=lse)
+    dq, dk, dv = (t.cpu() for t in ops.attention_backward(qd, kd, vd, o, dod, lse, plan.attn, plan.keys))
+    lse, o = lse.cpu(), o.cpu().float()
+    off = 0
+    for n in lens:
+        sl = slice(off, off + n)
+        o_r, lse_r, dq_r, dk_r, dv_r = _attn_ref(q[sl], k[sl], v[sl], do[sl])
+        assert (o[sl] - o_r).abs().max() < 1e-2
+        assert torch.allclose(lse[sl].t(), lse_r, atol=1e-3, rtol=1e-4), float((lse[sl].t() - lse_r).abs().max())
+        for got, ref, name in ((dq[sl], dq_r, "dq"), (dk[sl], dk_r, "dk"), (dv[sl], dv_r, "dv")):
+            # (a one-row sequence has dq = 0 exactly: P = 1, so dS = 0; hence the floor on the scale)
+            err = float((got - ref).abs().max() / max(float(ref.abs().max()), 0.05))
+            assert err < 2e-2, (name, n, err)
+        off += n
+
+
+def test_rmsnorm_backward():
+    g = gen(5)
+    n = 77
+    x = (torch.randn(n, 512, generator=g) * 2).to(BF)
+    w = (torch.rand(512, generator=g) + 0.5).to(BF)
+    dy = torch.randn(n, 512, generator=g)
+    dres = torch.randn(n, 512, generator=g)
+    xx = x.float().requires_grad_(True)
+    ww = w.float().requires_grad_(True)
+    (F.rms_norm(xx, (512,), ww, 1e-6) * dy).sum().backward()
+    for dy_dev in (dy.to(DEV), dy.to(BF).to(DEV)):
+        dx, dw = ops.rmsnorm_backward(x.to(DEV), w.to(DEV), dy_dev, 1e-6, dres=dres.to(DEV).clone())
+        if dy_dev.dtype == BF:  # the reference with the same bf16-rounded dy
+            xx.grad = ww.grad = None
+            (F.rms_norm(xx, (512,), ww, 1e-6) * dy.to(BF).float()).sum().backward()
+        assert torch.allclose(dx.cpu(), xx.grad + dres, rtol=1e-4, atol=1e-4)
+        assert torch.allclose(dw.cpu(), ww.grad, rtol=1e-4, atol=1e-3)
+
+
+def test_qknorm_rope_backward():
+    g = gen(6)
+    n, H, HKV = 50, 8, 2
+    qkv = (torch.randn(n, (H + 2 * HKV) * 64, generator=g) * 2).to(BF)
+    wq = (torch.rand(64, generator=g) + 0.5).to(BF)
+    wk = (torch.rand(64, generator=g) + 0.5).to(BF)
+    cos, sin = R.rope_tables(64, 4096, 1e6)
+    rpos = torch.randint(0, 4096, (n,), generator=g).int()
+    dq = torch.randn(n, H, 64, generator=g)
+    dk = torch.randn(n, HKV, 64, generator=g)
+    dv = torch.randn(n, HKV, 64, generator=g)
+    x = qkv.float().view(n, H + 2 * HKV, 64)
+    q = x[:, :H].clone().requires_grad_(True)
+    k = x[:, H:H + HKV].clone().requires_grad_(True)
+    wqq, wkk = wq.float().requires_grad_(True), wk.float().requires_grad_(True)
+    c, s = cos[rpos.long()], sin[rpos.long()]
+    loss = (R.apply_rope(F.rms_norm(q, (64,), wqq, 1e-6), c, s) * dq).sum() + \
+           (R.apply_rope(F.rms_norm(k, (64,), wkk, 1e-6), c, s) * dk).sum()
+    loss.backward()
+    want = torch.cat([q.grad, k.grad, dv], 1).reshape(n, -1)
+    dqkv, gq, gk = ops.qknorm_rope_backward(qkv.to(DEV), wq.to(DEV), wk.to(DEV), cos.to(DEV), sin.to(DEV),
+                                            rpos.to(DEV), dq.to(DEV), dk.to(DEV), dv.to(DEV), 1e-6, H, HKV, 64)
+    got = dqkv.cpu().float()
+    assert torch.allclose(got, want, rtol=8e-3, atol=1e-4 * want.abs().max()), float((got - want).abs().max())
+    assert torch.allclose(gq.cpu(), wqq.grad, rtol=1e-3, atol=1e-3)
+    assert torch.allclose(gk.cpu(), wkk.grad, rtol=1e-3, atol=1e-3)
+
+
+def test_swiglu_backward():
+    g = gen(7)
+    n, Fd = 40, 1536
+    gu = (torch.randn(n, 2 * Fd, generator=g) * 2).to(BF)
+    dout = torch.randn(n, Fd, generator=g).to(BF)
+    gg = gu.float().requires_grad_(True)
+    gate, up = gg.chunk(2, -1)
+    (F.silu(gate) * up * dout.float()).sum().backward()
+    got = ops.swiglu_backward(gu.to(DEV), dout.to(DEV)).cpu().float()
+    assert torch.allclose(got, gg.grad, rtol=8e-3, atol=1e-3), float((got - gg.grad).abs().max())
+
+
+def test_adamw_with_clip_matches_torch():
+    g = gen(8)
+    n = 10007
+    p0 = torch.randn(n, generator=g)
+    ref = torch.nn.Parameter(p0.clone())
+    opt = torch.optim.AdamW([ref], lr=3e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.01)
+    p, m, v = p0.to(DEV), torch.zeros(n, device=DEV), torch.zeros(n, device=DEV)
+    for step in range(1, 4):
+        grad = torch.randn(n, generator=g) * (3.0 if step == 2 else 0.01)  # step 2 is clipped, the others not
+        ref.grad = grad.clone()
+        nrm = torch.nn.utils.clip_grad_norm_([ref], 1.0)
+        opt.step()
+        gd = grad.to(DEV)
+        coef = ops.grad_norm_clip(gd, 1.0)
+        assert abs(float(coef[0]) - float(nrm)) <= 1e-5 * float(nrm)
+        ops.adamw(p, gd, m, v, 3e-3, (0.9, 0.95), 1e-8, 0.01, step, coef=coef)
+        assert torch.allclose(p.cpu(), ref.detach(), rtol=1e-5, atol=1e-6), step
+
+
+def _param_grads_vs_oracle(n_layers, plens, T, seed, pos_scale=1):
+    from viktor_amd.synthetic import frames as synth_frames, make_model
+    m = make_model(1, n_layers=n_layers, seed=seed, norm_jitter=0.1, bias_jitter=0.1)
+    m.pos_scale = pos_scale
+    ref = R.RefModel(m, "fp32")
+    gm = m.to(DEV)
+    g = gen(seed + 1)
+    B = len(plens)
+    P = max(plens)
+    fr = synth_frames(B, P, 512, seed=seed + 2)
+    pl = torch.tensor(plens)
+    tok = torch.randint(3, 7, (B, T), generator=g)
+    targets = torch.randint(3, 7, (B, T), generator=g)
+    mask = torch.ones(B, T, dtype=torch.bool)
+    mask[0, T - 3:] = False
+    n_bases = mask.sum(1).float()
+    adv = torch.randn(B, generator=g)
+    with torch.no_grad():
+        z0 = TR.train_logits(gm, fr.to(DEV), tok.to(DEV), pl.to(DEV))
+        old = torch.log_softmax(z0.float(), -1).gather(-1, targets.to(DEV)[..., None])[..., 0].cpu()
+    gm.zero_grad(set_to_none=True)
+    z = TR.train_logits(gm, fr.to(DEV), tok.to(DEV), pl.to(DEV))
+    from viktor_amd.gspo import sequence_ratio_loss
+    loss, s, pg, lp = sequence_ratio_loss(z, targets.to(DEV), mask.to(DEV), old.to(DEV), n_bases.to(DEV),
+                                          adv.to(DEV), 0.2, 0.2, 1.0 / B)
+    loss.backward()
+    ref_loss, ref_g = R.gspo_param_grads(ref, fr, tok, pl, targets, mask, old, n_bases, adv, 0.2, 0.2, 1.0 / B)
+    assert abs(float(loss) - float(ref_loss)) < 1e-2 * abs(float(ref_loss)) + 1e-4
+    worst = []
+    for name, p in gm.named_parameters():
+        r = ref_g[name]
+        got = p.grad.detach().float().cpu() if p.grad is not None else torch.zeros_like(r)
+        rel = float((got - r).norm() / (r.norm() + 1e-30))
+        cos = float(F.cosine_similarity(got.reshape(1, -1), r.reshape(1, -1)))
+        worst.append((rel, cos, name))
+        assert rel < 0.1 and cos > 0.99, (name, rel, cos)
+    return sorted(worst)[-3:]
+
+
+def test_decoder_param_grads_match_oracle():
+    """Two layers, three windows of different prefix lengths: every projector / decoder parameter's GSPO
+    gradient through the HIP training path against the oracle's fp32 autograd."""
+    print(_param_grads_vs_oracle(2, [70, 33, 100], 24, seed=31))
+
+
+def test_decoder_param_grads_pos_scale():
+    print(_param_grads_vs_oracle(1, [40, 65], 17, seed=41, pos_scale=2))
+
+
+def test_hip_adamw_update_changes_params_in_place():
+    """HipAdamW: parameters become views of one flat buffer, a step moves them and keeps the module's
+    tensors (the inference copy syncs from them by copy_)."""
+    from viktor_amd.synthetic import make_model
+    m = make_model(1, n_layers=1, seed=51).to(DEV)
+    params = list(m.parameters())
+    before = [p.detach().clone() for p in params]
+    opt = TR.HipAdamW(params, lr=1e-3)
+    for p in params:
+        p.grad = torch.ones_like(p)
+    opt.step()
+    assert float(opt.last_norm[0]) > 1.0 and float(opt.last_norm[1]) < 1.0
+    for p, b in zip(params, before):
+        assert torch.allclose(p.detach(), b - 1e-3, atol=2e-6)  # Adam's first step moves by lr * sign(g)
+        assert p.data.data_ptr() >= opt.flat.data_ptr()

@@ -36,7 +36,7 @@ SIGNATURES = {
     "vk_swiglu": [_P, _P, _I64, _I32, _P],
     "vk_decode_attention": [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I64, _I64, _I64, _P, _I64, _P],
     "vk_decode_attention_workspace": [_I64, _I32, _I64, ctypes.POINTER(_I64)],
-    "vk_varlen_attention": [_P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I64, _P, _I32, _I32, _I32, _I32, _P],
+    "vk_varlen_attention": [_P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I64, _P, _I32, _I32, _I32, _I32, _P, _P],
     "vk_select_update": [_P, _P, _P, _F, _P, _I32, _I32, _P, _P, _P, _I32, _F, _P, _I64, _I64, _P, _P, _P, _P, _P, _P,
                          _P, _I64, _I64, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P],
     "vk_decode_attention_grouped": [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _I32,
@@ -49,6 +49,15 @@ SIGNATURES = {
     "vk_norm_linear": [_P, _P, _F, _P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P],
     "vk_gspo_score": [_P, _I32, _P, _P, _P, _P, _P, _F, _F, _F, _P, _P, _P, _P, _P, _I64, _I64, _I32, _P],
     "vk_group_advantage": [_P, _I64, _I32, _I32, _F, _P, _P, _P],
+    "vk_attention_backward": [_P, _P, _P, _P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _I64, _I64, _P, _P, _P, _P, _I32,
+                              _I32, _I32, _P],
+    "vk_rmsnorm_backward_blocks": [_I64, ctypes.POINTER(_I32)],
+    "vk_rmsnorm_backward": [_P, _P, _P, _I32, _P, _P, _P, _I64, _I32, _F, _P],
+    "vk_colsum": [_P, _P, _I32, _I32, _I32, _P],
+    "vk_qknorm_rope_backward": [_P, _P, _P, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _F, _P],
+    "vk_swiglu_backward": [_P, _P, _P, _I64, _I32, _P],
+    "vk_grad_norm_clip": [_P, _I64, _F, _P, _I32, _P, _P],
+    "vk_adamw": [_P, _P, _P, _P, _I64, _P, _F, _F, _F, _F, _F, _I64, _P],
 }
 
 _lock = threading.Lock()

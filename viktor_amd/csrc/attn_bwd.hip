@@ -1,0 +1,357 @@
+// Backward of causal GQA self-attention over packed sequences (the training-mode attention of the decoder:
+// flash_attn_func(causal=True) under autocast at viktor/decoder.py:82-87, whose backward the GSPO update
+// runs through at scripts/gspo.py:477).
+//
+// Per sequence i (rows cu[i] .. cu[i+1]-1 of the packed q [N, 8, 64], k / v [N, 2, 64] at stride_tok),
+// query head h uses KV head h / 4, query r sees keys j <= r, S = q k^T / sqrt(64), P = softmax(S),
+// o = P v. Given dO, with D_r = sum_d dO_rd o_rd (row dot kernel):
+//   dV_j = sum_r P_rj dO_r          dP_rj = dO_r . v_j          dS_rj = P_rj (dP_rj - D_r)
+//   dQ_r = sum_j dS_rj k_j / 8      dK_j = sum_r dS_rj q_r / 8  (summed over the 4 query heads of a KV head)
+// P is recomputed from the forward's per-row log-sum-exp (log2 units of the scaled scores).
+//
+// MI355X design: the transposed MFMA products of the forward kernels, so the probabilities computed in one
+// product's accumulator layout are consumed in place as the next product's operand:
+//   * dQ kernel = the forward's shape: a workgroup per 64-query block x KV head, 8 wavefronts (4 query
+//     heads x 2 halves of 32 rows), K / V tiles of 64 keys double buffered in LDS. Per key half:
+//     S^T = K Q^T, dP^T = V dO^T (A = key rows from LDS, B = Q^T / dO^T held in registers), dS^T in the
+//     accumulator layout, dQ^T += K^T dS^T (A = K^T read column-wise from LDS).
+//   * dK/dV kernel: a workgroup per 64-key block x KV head, 4 wavefronts of 16 keys (K^T / V^T fragments
+//     in registers), looping over the 32-query tiles at or below the diagonal, Q / dO / lse / D of the 4
+//     query heads staged in LDS: S = Q K^T, dP = dO V^T (A = query rows from LDS), then dV^T += dO^T P and
+//     dK^T += Q^T dS with P / dS consumed in their accumulator layout; the 4 heads accumulate in place.
+// Gradients are written in fp32 (the consumers -- QK-norm / RoPE backward, the qkv weight gradient -- work
+// in fp32 and round once).
+#include <math.h>
+
+#include "common.h"
+
+namespace vk {
+
+constexpr int AB_H = 8, AB_HKV = 2, AB_D = 64;
+constexpr int AB_PITCH = 72;  // 64 + 8 bf16 per LDS row
+
+// D[r, h] = sum_d dO[r, h, d] * o[r, h, d]: one thread per (row, head)
+__global__ __launch_bounds__(256) void attn_bwd_dot_kernel(const bf16_t *__restrict__ dout,
+                                                          const bf16_t *__restrict__ out, float *__restrict__ dd,
+                                                          int64_t n_rows) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // row * 8 + head
+  if (i >= n_rows * AB_H) return;
+  const u32x4 *a = reinterpret_cast<const u32x4 *>(dout + i * AB_D);
+  const u32x4 *b = reinterpret_cast<const u32x4 *>(out + i * AB_D);
+  u32x4 av[8], bv[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    av[c] = a[c];
+    bv[c] = b[c];
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s += lo_bf(av[c][e]) * lo_bf(bv[c][e]) + hi_bf(av[c][e]) * hi_bf(bv[c][e]);
+  dd[i] = s;
+}
+
+// ---- dQ: workgroup = 64 query rows of one sequence x one KV head -----------------------------------------
+__global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
+    const bf16_t *__restrict__ q, const bf16_t *__restrict__ k, const bf16_t *__restrict__ v,
+    const bf16_t *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ dd,
+    const int32_t *__restrict__ cu, const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok,
+    float *__restrict__ dq, float scale_log2, float scale) {
+  __shared__ __attribute__((aligned(16))) bf16_t Ks[2][64 * AB_PITCH];
+  __shared__ __attribute__((aligned(16))) bf16_t Vs[2][64 * AB_PITCH];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int col = lane & 15, g = lane >> 4;
+  const int hk = blockIdx.y, hq = hk * 4 + (wid & 3), half = wid >> 2;
+  const int seq = plan[2 * blockIdx.x], qs = plan[2 * blockIdx.x + 1];
+  if (seq < 0 || seq >= n_seq || qs < 0) return;
+  const int64_t r0 = cu[seq];
+  const int len = cu[seq + 1] - static_cast<int>(r0);
+  if (len <= 0 || qs >= len) return;
+  const int nq = min(64, len - qs);
+  const int kend = qs + nq;  // causal: the block's last row sees keys < kend
+  const int ntiles = (kend + 63) / 64;
+
+  const int r_first = qs + 32 * half;
+  int qpos[2];
+  bf16x8 bq[2][2], bdo[2][2];
+  float lse2[2], dr[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    int r = r_first + 16 * qb + col;
+    r = r < len ? r : len - 1;
+    qpos[qb] = r;
+    const int64_t row = (r0 + r) * AB_H + hq;
+#pragma unroll
+    for (int dc = 0; dc < 2; ++dc) {
+      bq[qb][dc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(q + row * AB_D + 32 * dc + 8 * g));
+      bdo[qb][dc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(dout + row * AB_D + 32 * dc + 8 * g));
+    }
+    lse2[qb] = lse[row];
+    dr[qb] = dd[row];
+  }
+  const int wave_kmax = min(r_first + 31, len - 1);
+
+  f32x4 acc[4][2];  // dQ^T tiles [d tile][query block]
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int lrow = tid >> 3, lchunk = tid & 7;
+  u32x4 rk, rv;
+  auto load_tile = [&](int t) {
+    int key = t * 64 + lrow;
+    key = key < len ? key : len - 1;
+    const int64_t off = (r0 + key) * stride_tok + hk * AB_D + lchunk * 8;
+    rk = *reinterpret_cast<const u32x4 *>(k + off);
+    rv = *reinterpret_cast<const u32x4 *>(v + off);
+  };
+  auto store_tile = [&](int buf) {
+    *reinterpret_cast<u32x4 *>(&Ks[buf][lrow * AB_PITCH + lchunk * 8]) = rk;
+    *reinterpret_cast<u32x4 *>(&Vs[buf][lrow * AB_PITCH + lchunk * 8]) = rv;
+  };
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) load_tile(t + 1);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int kbase = t * 64 + 32 * ks;
+      if (kbase > wave_kmax) continue;  // wave-uniform: every key of this half is above every row's diagonal
+      const bf16_t *kt = &Ks[buf][32 * ks * AB_PITCH];
+      const bf16_t *vt = &Vs[buf][32 * ks * AB_PITCH];
+      f32x4 st[2][2], dpt[2][2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        bf16x8 ka[2], va[2];
+#pragma unroll
+        for (int dc = 0; dc < 2; ++dc) {
+          ka[dc] = *reinterpret_cast<const bf16x8 *>(&kt[(16 * kb + col) * AB_PITCH + 32 * dc + 8 * g]);
+          va[dc] = *reinterpret_cast<const bf16x8 *>(&vt[(16 * kb + col) * AB_PITCH + 32 * dc + 8 * g]);
+        }
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          st[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          dpt[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int dc = 0; dc < 2; ++dc) {
+            st[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[dc], bq[qb][dc], st[kb][qb], 0, 0, 0);
+            dpt[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dc], bdo[qb][dc], dpt[kb][qb], 0, 0, 0);
+          }
+        }
+      }
+      // dS^T in the accumulator layout (key 16 kb + 4 g + i, query col), as the B operand of K^T dS^T
+      bf16x8 dsf[2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = kbase + 16 * kb + 4 * g + i;
+            const bool ok = key < len && key <= qpos[qb];
+            const float p = ok ? exp2f(st[kb][qb][i] * scale_log2 - lse2[qb]) : 0.f;
+            dsf[qb][kb * 4 + i] = static_cast<__bf16>(p * (dpt[kb][qb][i] - dr[qb]));
+          }
+      // dQ^T += K^T dS^T (key order {4g..4g+3, 16+4g..16+4g+3} in both operands)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        bf16x8 ka;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const int kl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
+          ka[jj] = __builtin_bit_cast(__bf16, kt[kl * AB_PITCH + 16 * dt + col]);
+        }
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) acc[dt][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, dsf[qb], acc[dt][qb], 0, 0, 0);
+      }
+    }
+    if (t + 1 < ntiles) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int r = r_first + 16 * qb + col;
+    if (r >= len || r >= qs + nq) continue;
+    float *dst = dq + ((r0 + r) * AB_H + hq) * AB_D + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) *reinterpret_cast<f32x4 *>(dst + 16 * dt) = acc[dt][qb] * scale;
+  }
+}
+
+// ---- dK / dV: workgroup = 64 keys of one sequence x one KV head ------------------------------------------
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(
+    const bf16_t *__restrict__ q, const bf16_t *__restrict__ k, const bf16_t *__restrict__ v,
+    const bf16_t *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ dd,
+    const int32_t *__restrict__ cu, const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok,
+    float *__restrict__ dk, float *__restrict__ dv, float scale_log2, float scale) {
+  __shared__ __attribute__((aligned(16))) bf16_t Qs[4 * 32 * AB_PITCH];
+  __shared__ __attribute__((aligned(16))) bf16_t Os[4 * 32 * AB_PITCH];  // dO
+  __shared__ float Ls[4 * 32], Ds[4 * 32];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int col = lane & 15, g = lane >> 4;
+  const int hk = blockIdx.y;
+  const int seq = plan[2 * blockIdx.x], ks = plan[2 * blockIdx.x + 1];
+  if (seq < 0 || seq >= n_seq || ks < 0) return;
+  const int64_t r0 = cu[seq];
+  const int len = cu[seq + 1] - static_cast<int>(r0);
+  if (len <= 0 || ks >= len) return;
+
+  // this wave's 16 keys (lane col -> key), K^T / V^T fragments of the B operand
+  const int key = ks + 16 * wid + col;
+  const int keyc = key < len ? key : len - 1;
+  bf16x8 bk[2], bv[2];
+#pragma unroll
+  for (int dc = 0; dc < 2; ++dc) {
+    const int64_t off = (r0 + keyc) * stride_tok + hk * AB_D + 32 * dc + 8 * g;
+    bk[dc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(k + off));
+    bv[dc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(v + off));
+  }
+  f32x4 accv[4], acck[4];  // dV^T / dK^T tiles [d tile] (lane col -> key, 4 g + i -> d within the tile)
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) accv[dt] = acck[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int wave_kmin = ks + 16 * wid;  // rows below it see none of this wave's keys
+
+  // staging: thread t loads 16-byte chunks t + 256 c (c < 4) of the Q tile and of the dO tile:
+  // chunk -> (head hh = chunk / 256, row rr = chunk / 8 % 32, d chunk dc8 = chunk % 8)
+  for (int rs = ks; rs < len; rs += 32) {
+    u32x4 qv[4], ov[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int chunk = tid + 256 * c;
+      const int hh = chunk >> 8, rr = (chunk >> 3) & 31, dc8 = chunk & 7;
+      int r = rs + rr;
+      r = r < len ? r : len - 1;
+      const int64_t off = ((r0 + r) * AB_H + hk * 4 + hh) * AB_D + 8 * dc8;
+      qv[c] = *reinterpret_cast<const u32x4 *>(q + off);
+      ov[c] = *reinterpret_cast<const u32x4 *>(dout + off);
+    }
+    float lv = 0.f;
+    if (tid < 128) {
+      const int hh = tid >> 5, rr = tid & 31;
+      int r = rs + rr;
+      r = r < len ? r : len - 1;
+      lv = lse[(r0 + r) * AB_H + hk * 4 + hh];
+    } else {
+      const int hh = (tid - 128) >> 5, rr = tid & 31;
+      int r = rs + rr;
+      r = r < len ? r : len - 1;
+      lv = dd[(r0 + r) * AB_H + hk * 4 + hh];
+    }
+    __syncthreads();  // the previous tile's readers are done
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int chunk = tid + 256 * c;
+      const int hh = chunk >> 8, rr = (chunk >> 3) & 31, dc8 = chunk & 7;
+      *reinterpret_cast<u32x4 *>(&Qs[(hh * 32 + rr) * AB_PITCH + 8 * dc8]) = qv[c];
+      *reinterpret_cast<u32x4 *>(&Os[(hh * 32 + rr) * AB_PITCH + 8 * dc8]) = ov[c];
+    }
+    if (tid < 128)
+      Ls[tid] = lv;
+    else
+      Ds[tid - 128] = lv;
+    __syncthreads();
+    if (rs + 31 < wave_kmin) continue;  // wave-uniform: every row of the tile lies above this wave's keys
+
+#pragma unroll
+    for (int hh = 0; hh < 4; ++hh) {
+      const bf16_t *qt = &Qs[hh * 32 * AB_PITCH];
+      const bf16_t *ot = &Os[hh * 32 * AB_PITCH];
+      // S / dP [row 16 rb + 4 g + i][key col]
+      f32x4 st[2], dpt[2];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        st[rb] = dpt[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dc = 0; dc < 2; ++dc) {
+          const bf16x8 qa = *reinterpret_cast<const bf16x8 *>(&qt[(16 * rb + col) * AB_PITCH + 32 * dc + 8 * g]);
+          const bf16x8 oa = *reinterpret_cast<const bf16x8 *>(&ot[(16 * rb + col) * AB_PITCH + 32 * dc + 8 * g]);
+          st[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa, bk[dc], st[rb], 0, 0, 0);
+          dpt[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(oa, bv[dc], dpt[rb], 0, 0, 0);
+        }
+      }
+      bf16x8 pf, dsf;  // row order {4g..4g+3, 16+4g..16+4g+3}
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rr = 16 * rb + 4 * g + i;
+          const int r = rs + rr;
+          const bool ok = r < len && key <= r && key < len;
+          const float p = ok ? exp2f(st[rb][i] * scale_log2 - Ls[hh * 32 + rr]) : 0.f;
+          pf[rb * 4 + i] = static_cast<__bf16>(p);
+          dsf[rb * 4 + i] = static_cast<__bf16>(p * (dpt[rb][i] - Ds[hh * 32 + rr]));
+        }
+      // dV^T += dO^T P, dK^T += Q^T dS (A = dO^T / Q^T read column-wise: lane col -> d, row order as above)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        bf16x8 oa, qa;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const int rl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
+          oa[jj] = __builtin_bit_cast(__bf16, ot[rl * AB_PITCH + 16 * dt + col]);
+          qa[jj] = __builtin_bit_cast(__bf16, qt[rl * AB_PITCH + 16 * dt + col]);
+        }
+        accv[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(oa, pf, accv[dt], 0, 0, 0);
+        acck[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa, dsf, acck[dt], 0, 0, 0);
+      }
+    }
+  }
+  if (key >= len) return;
+  float *dkp = dk + ((r0 + key) * AB_HKV + hk) * AB_D + 4 * g;
+  float *dvp = dv + ((r0 + key) * AB_HKV + hk) * AB_D + 4 * g;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    *reinterpret_cast<f32x4 *>(dkp + 16 * dt) = acck[dt] * scale;
+    *reinterpret_cast<f32x4 *>(dvp + 16 * dt) = accv[dt];
+  }
+}
+
+}  // namespace vk
+
+using namespace vk;
+
+extern "C" int vk_attention_backward(const void *q, const void *k, const void *v, const void *out, const void *dout,
+                                     const float *lse, const int32_t *cu, int32_t n_seq, const int32_t *q_plan,
+                                     int32_t n_qblocks, const int32_t *k_plan, int32_t n_kblocks, int64_t n_rows,
+                                     int64_t stride_tok, float *dd, float *dq, float *dk, float *dv, int32_t H,
+                                     int32_t HKV, int32_t D, void *stream) {
+  VK_CHECK_ARG(q && k && v && out && dout && lse && cu && dd && dq && dk && dv, "attention_backward: null pointer");
+  if (H != AB_H || HKV != AB_HKV || D != AB_D)
+    return fail(VK_ERR_UNSUPPORTED, "attention_backward: built for H=8 HKV=2 D=64 (got %d/%d/%d)", H, HKV, D);
+  VK_CHECK_ARG(n_seq >= 0 && n_rows >= 0 && n_qblocks >= 0 && n_kblocks >= 0 && stride_tok >= AB_HKV * AB_D &&
+                   stride_tok % 8 == 0,
+               "attention_backward: bad sizes");
+  VK_CHECK_ARG((n_qblocks == 0 || q_plan) && (n_kblocks == 0 || k_plan), "attention_backward: missing plan");
+  VK_CHECK_ARG(vk_aligned16(q) && vk_aligned16(k) && vk_aligned16(v) && vk_aligned16(out) && vk_aligned16(dout) &&
+                   vk_aligned16(dq) && vk_aligned16(dk) && vk_aligned16(dv),
+               "attention_backward: pointers must be 16-byte aligned");
+  if (n_rows == 0) return VK_OK;
+  hipStream_t s = VK_STREAM(stream);
+  const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(AB_D)));
+  const float scale_log2 = static_cast<float>(1.0 / sqrt(static_cast<double>(AB_D)) * 1.4426950408889634);
+  const auto qb = static_cast<const bf16_t *>(q);
+  const auto kb = static_cast<const bf16_t *>(k);
+  const auto vb = static_cast<const bf16_t *>(v);
+  const auto ob = static_cast<const bf16_t *>(out);
+  const auto dob = static_cast<const bf16_t *>(dout);
+  const int64_t nd = n_rows * AB_H;
+  attn_bwd_dot_kernel<<<static_cast<unsigned>((nd + 255) / 256), 256, 0, s>>>(dob, ob, dd, n_rows);
+  int rc = launch_status("attention_backward dot");
+  if (rc != VK_OK) return rc;
+  if (n_qblocks > 0) {
+    attn_bwd_dq_kernel<<<dim3(static_cast<unsigned>(n_qblocks), AB_HKV), 512, 0, s>>>(
+        qb, kb, vb, dob, lse, dd, cu, q_plan, n_seq, stride_tok, dq, scale_log2, scale);
+    rc = launch_status("attention_backward dq");
+    if (rc != VK_OK) return rc;
+  }
+  if (n_kblocks > 0) {
+    attn_bwd_dkdv_kernel<<<dim3(static_cast<unsigned>(n_kblocks), AB_HKV), 256, 0, s>>>(
+        qb, kb, vb, dob, lse, dd, cu, k_plan, n_seq, stride_tok, dk, dv, scale_log2, scale);
+    rc = launch_status("attention_backward dkdv");
+  }
+  return rc;
+}

@@ -33,7 +33,7 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ k, const bf16_t *__restrict__ v,
     const int32_t *__restrict__ cu_q, const int64_t *__restrict__ k_off, const int32_t *__restrict__ k_lens,
     const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok, bf16_t *__restrict__ out, int causal,
-    float scale_log2) {
+    float scale_log2, float *__restrict__ lse) {
   __shared__ __attribute__((aligned(16))) bf16_t Ks[2][PA_KT * PA_PITCH];
   __shared__ __attribute__((aligned(16))) bf16_t Vs[2][PA_KT * PA_PITCH];
 
@@ -181,6 +181,8 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
     const int r = r_first + 16 * qb + col;
     if (r >= q_len || r >= qs + nq) continue;
     const float inv = 1.0f / l;
+    // the row's log-sum-exp in log2 units of the scaled scores (m + log2 l), for the backward pass
+    if (lse != nullptr && g == 0) lse[(q0 + r) * PA_H + hq] = m_run[qb] + log2f(l);
     bf16_t *dst = out + ((q0 + r) * PA_H + hq) * PA_D + 4 * g;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
@@ -199,7 +201,7 @@ using namespace vk;
 extern "C" int vk_varlen_attention(const void *q, const void *k, const void *v, const int32_t *cu_q,
                                    const int64_t *k_off, const int32_t *k_lens, const int32_t *plan, int32_t n_blocks,
                                    int32_t n_seq, int64_t stride_tok, void *out, int32_t causal, int32_t H,
-                                   int32_t HKV, int32_t D, void *stream) {
+                                   int32_t HKV, int32_t D, float *lse, void *stream) {
   VK_CHECK_ARG(q && k && v && cu_q && k_off && k_lens && out, "varlen_attention: null pointer");
   if (H != PA_H || HKV != PA_HKV || D != PA_D)
     return fail(VK_ERR_UNSUPPORTED, "varlen_attention: built for H=8 HKV=2 D=64 (got %d/%d/%d)", H, HKV, D);
@@ -213,6 +215,6 @@ extern "C" int vk_varlen_attention(const void *q, const void *k, const void *v, 
   const dim3 grid(static_cast<unsigned>(n_blocks), PA_HKV);
   varlen_attn_kernel<<<grid, PA_WAVES * 64, 0, VK_STREAM(stream)>>>(
       static_cast<const bf16_t *>(q), static_cast<const bf16_t *>(k), static_cast<const bf16_t *>(v), cu_q, k_off,
-      k_lens, plan, n_seq, stride_tok, static_cast<bf16_t *>(out), causal, scale_log2);
+      k_lens, plan, n_seq, stride_tok, static_cast<bf16_t *>(out), causal, scale_log2, lse);
   return launch_status("varlen_attention");
 }

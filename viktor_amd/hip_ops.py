@@ -240,10 +240,12 @@ class AttentionPlan:
         self.k_off = torch.tensor([int(o) for o in k_off] or [0], dtype=torch.int64).to(device)
 
 
-def varlen_attention(q, k, v, plan: AttentionPlan, stride_tok=None, out=None):
+def varlen_attention(q, k, v, plan: AttentionPlan, stride_tok=None, out=None, lse=None):
     """Packed-query GQA attention following `plan`. q [total_q, H, D] bf16; k/v: base tensors (packed
     [n, Hkv, D] rows or one cache layer [B, S, Hkv, D]) addressed by plan.k_off + key * stride_tok
-    elements. Returns [total_q, H, D] bf16. Reference: flash_attn_varlen_func at viktor/fast_decoder.py:68-73."""
+    elements. Returns [total_q, H, D] bf16. lse [total_q, H] fp32 (optional, written): each row's
+    log-sum-exp of its scaled scores in log2 units, for attention_backward.
+    Reference: flash_attn_varlen_func at viktor/fast_decoder.py:68-73."""
     require_device(q, "varlen_attention")
     total, H, D = q.shape
     HK = k.shape[-2]
@@ -254,8 +256,11 @@ def varlen_attention(q, k, v, plan: AttentionPlan, stride_tok=None, out=None):
         stride_tok = k.stride(-3)
     if out is None:
         out = torch.empty_like(q)
+    _require(lse is None or (lse.dtype == torch.float32 and lse.shape == (total, H) and lse.is_contiguous()),
+             "varlen_attention: lse [total_q, H] fp32")
     call("vk_varlen_attention", ptr(q), ptr(k), ptr(v), ptr(plan.cu_q), ptr(plan.k_off), ptr(plan.k_lens),
-         ptr(plan.plan), plan.n_blocks, plan.n_seq, stride_tok, ptr(out), int(plan.causal), H, HK, D, stream_handle())
+         ptr(plan.plan), plan.n_blocks, plan.n_seq, stride_tok, ptr(out), int(plan.causal), H, HK, D, ptr(lse),
+         stream_handle())
     return out
 
 
@@ -417,3 +422,133 @@ def group_advantage(reward, std_floor=None, eps=None):
     mode, param = (0, std_floor) if std_floor is not None else (1, eps)
     call("vk_group_advantage", ptr(r), G, n, mode, float(param), ptr(adv), ptr(live), stream_handle())
     return adv, live.bool()
+
+
+# ---- the GSPO update's backward and optimizer step -------------------------------------------------------
+class KeyBlockPlan:
+    """(sequence, first key) per 64-key block of causal self-attention over packed sequences, longest work
+    (most query rows at or below the block) first: the dK / dV work list of attention_backward."""
+
+    BLOCK = 64
+
+    def __init__(self, seq_lens, device):
+        lens = [int(n) for n in seq_lens]
+        blocks = sorted(((n - ks, i, ks) for i, n in enumerate(lens) for ks in range(0, n, self.BLOCK)),
+                        key=lambda b: -b[0])
+        flat = [v for _, i, ks in blocks for v in (i, ks)] or [0, 0]
+        self.n_blocks = len(blocks)
+        self.plan = torch.tensor(flat, dtype=torch.int32).to(device)
+
+
+def attention_backward(q, k, v, out, dout, lse, q_plan: AttentionPlan, k_plan: KeyBlockPlan, stride_tok=None):
+    """Gradients of causal GQA self-attention over the packed sequences of q_plan (q_lens == k_lens, keys of
+    sequence i at rows cu[i].. of k / v). q / out / dout [n, 8, 64] bf16, k / v [n, 2, 64] (row stride
+    stride_tok), lse [n, 8] from varlen_attention(..., lse=). Returns dq [n, 8, 64], dk, dv [n, 2, 64] fp32.
+    Reference: the backward of flash_attn_func(causal=True) at viktor/decoder.py:82-87."""
+    require_device(q, "attention_backward")
+    n, H, D = q.shape
+    HK = k.shape[-2]
+    _require(q.dtype == k.dtype == v.dtype == out.dtype == dout.dtype == BF16, "attention_backward: bf16 tensors")
+    _require(_contig(q, out, dout, lse) and k.stride(-1) == 1 and k.stride(-2) == D and k.stride() == v.stride(),
+             "attention_backward: layouts")
+    _require(q_plan.total_q == n and out.shape == q.shape == dout.shape and lse.shape == (n, H)
+             and lse.dtype == torch.float32, "attention_backward: shapes")
+    if stride_tok is None:
+        stride_tok = k.stride(-3)
+    dd = torch.empty(n, H, dtype=torch.float32, device=q.device)
+    dq = torch.empty(n, H, D, dtype=torch.float32, device=q.device)
+    dk = torch.empty(n, HK, D, dtype=torch.float32, device=q.device)
+    dv = torch.empty_like(dk)
+    call("vk_attention_backward", ptr(q), ptr(k), ptr(v), ptr(out), ptr(dout), ptr(lse), ptr(q_plan.cu_q),
+         q_plan.n_seq, ptr(q_plan.plan), q_plan.n_blocks, ptr(k_plan.plan), k_plan.n_blocks, n, stride_tok, ptr(dd),
+         ptr(dq), ptr(dk), ptr(dv), H, HK, D, stream_handle())
+    return dq, dk, dv
+
+
+def _norm_blocks(n):
+    b = ctypes.c_int32(0)
+    _lib.check(_lib.load().vk_rmsnorm_backward_blocks(n, ctypes.byref(b)), "rmsnorm_backward_blocks")
+    return b.value
+
+
+def colsum(part, out=None, accumulate=False):
+    """Column sums of part [rows, cols] fp32 in a fixed order (into out [cols], added when accumulate)."""
+    rows, cols = part.shape
+    if out is None:
+        out = torch.empty(cols, dtype=torch.float32, device=part.device)
+    _require(part.is_contiguous() and part.dtype == torch.float32 and out.shape == (cols,)
+             and out.dtype == torch.float32, "colsum: shapes")
+    call("vk_colsum", ptr(part), ptr(out), rows, cols, int(bool(accumulate)), stream_handle())
+    return out
+
+
+def rmsnorm_backward(x, w, dy, eps, dres=None, dx=None):
+    """Backward of h = rmsnorm(x) * w (x [n, 512] bf16, w [512] bf16, dy [n, 512] bf16 or fp32):
+    returns (dx fp32 [n, 512] = the norm's input gradient + dres, dw fp32 [512]). dx may be dres (in place).
+    Reference: nn.RMSNorm of the decoder blocks, viktor/decoder.py:110-124."""
+    require_device(x, "rmsnorm_backward")
+    n, d = x.shape
+    _require(x.dtype == w.dtype == BF16 and dy.shape == x.shape and dy.dtype in (BF16, torch.float32),
+             "rmsnorm_backward: dtypes")
+    _require(_contig(x, w, dy, dres) and (dres is None or (dres.dtype == torch.float32 and dres.shape == x.shape)),
+             "rmsnorm_backward: layouts")
+    if dx is None:
+        dx = dres if dres is not None else torch.empty(n, d, dtype=torch.float32, device=x.device)
+    part = torch.empty(_norm_blocks(n), d, dtype=torch.float32, device=x.device)
+    call("vk_rmsnorm_backward", ptr(x), ptr(w), ptr(dy), VK_DTYPE_F32 if dy.dtype == torch.float32 else VK_DTYPE_BF16,
+         ptr(dres), ptr(dx), ptr(part), n, d, float(eps), stream_handle())
+    return dx, colsum(part)
+
+
+def qknorm_rope_backward(qkv, q_norm_w, k_norm_w, cos, sin, rope_pos, dq, dk, dv, eps, n_heads, n_kv_heads, head_dim):
+    """Backward of the QK-norm + RoPE stage: qkv [n, (H + 2 Hkv) D] bf16 (projection output), dq / dk / dv fp32
+    attention-input gradients, rope_pos [n] int32 rows of cos/sin [S, D/2]. Returns (dqkv bf16 [n, (H + 2 Hkv) D],
+    d q_norm.weight fp32 [D], d k_norm.weight fp32 [D]). Reference: viktor/decoder.py:62-66."""
+    require_device(qkv, "qknorm_rope_backward")
+    n = qkv.shape[0]
+    _require(qkv.dtype == BF16 and qkv.shape[1] == (n_heads + 2 * n_kv_heads) * head_dim, "qknorm_rope_backward: qkv")
+    _require(dq.shape == (n, n_heads, head_dim) and dk.shape == dv.shape == (n, n_kv_heads, head_dim)
+             and dq.dtype == dk.dtype == dv.dtype == torch.float32, "qknorm_rope_backward: gradients")
+    _require(rope_pos.dtype == torch.int32 and rope_pos.shape == (n,), "qknorm_rope_backward: rope_pos")
+    _require(_contig(qkv, q_norm_w, k_norm_w, cos, sin, rope_pos, dq, dk, dv), "qknorm_rope_backward: layouts")
+    dqkv = torch.empty_like(qkv)
+    part = torch.empty(_norm_blocks(n), 2 * head_dim, dtype=torch.float32, device=qkv.device)
+    tdt = VK_DTYPE_F32 if cos.dtype == torch.float32 else VK_DTYPE_BF16
+    call("vk_qknorm_rope_backward", ptr(qkv), ptr(q_norm_w), ptr(k_norm_w), ptr(cos), ptr(sin), tdt, cos.shape[0],
+         ptr(rope_pos), ptr(dq), ptr(dk), ptr(dv), ptr(dqkv), ptr(part), n, n_heads, n_kv_heads, head_dim, float(eps),
+         stream_handle())
+    dw = colsum(part)
+    return dqkv, dw[:head_dim], dw[head_dim:]
+
+
+def swiglu_backward(gu, dout):
+    """gu [n, 2F] (gate | up) bf16, dout [n, F] bf16 -> d gu [n, 2F] bf16 of silu(gate) * up.
+    Reference: F.silu(gate) * up at viktor/decoder.py:127."""
+    require_device(gu, "swiglu_backward")
+    n, F2 = gu.shape
+    _require(gu.dtype == dout.dtype == BF16 and dout.shape == (n, F2 // 2) and _contig(gu, dout),
+             "swiglu_backward: shapes")
+    dgu = torch.empty_like(gu)
+    call("vk_swiglu_backward", ptr(gu), ptr(dout), ptr(dgu), n, F2 // 2, stream_handle())
+    return dgu
+
+
+def grad_norm_clip(g, max_norm, n_partials=512):
+    """[||g||_2, min(1, max_norm / (||g|| + 1e-6))] of the flat fp32 gradient g, on the device
+    (nn.utils.clip_grad_norm_, scripts/gspo.py:492)."""
+    require_device(g, "grad_norm_clip")
+    _require(g.dtype == torch.float32 and g.is_contiguous() and g.dim() == 1, "grad_norm_clip: flat fp32 gradient")
+    part = torch.empty(n_partials, dtype=torch.float32, device=g.device)
+    out = torch.empty(2, dtype=torch.float32, device=g.device)
+    call("vk_grad_norm_clip", ptr(g), g.numel(), float(max_norm), ptr(part), n_partials, ptr(out), stream_handle())
+    return out
+
+
+def adamw(p, g, m, v, lr, betas, eps, weight_decay, step, coef=None):
+    """One AdamW step over flat fp32 p / g / m / v (torch.optim.AdamW, scripts/gspo.py:368), the gradient
+    scaled by coef[1] when given (grad_norm_clip's clip coefficient)."""
+    require_device(p, "adamw")
+    _require(all(t.dtype == torch.float32 and t.is_contiguous() and t.shape == p.shape for t in (p, g, m, v)),
+             "adamw: flat fp32 buffers of one shape")
+    call("vk_adamw", ptr(p), ptr(g), ptr(m), ptr(v), p.numel(), ptr(coef), float(lr), float(betas[0]), float(betas[1]),
+         float(eps), float(weight_decay), int(step), stream_handle())

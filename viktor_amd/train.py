@@ -1,0 +1,218 @@
+"""The GSPO update on the HIP kernels: the teacher-forced forward with saved activations, its backward, the
+gradient clip and the AdamW step.
+
+Reference: scripts/gspo.py:340-353 (token_logprobs under torch.autocast bf16), 459-493 (the update loop:
+loss.backward() through Basecaller.logits, clip_grad_norm_, AdamW(fused).step()), 113-126 (bf16_copy / sync);
+viktor/model.py:55-60 (Basecaller.logits), viktor/decoder.py:54-144 (the decoder blocks).
+
+The model keeps fp32 master weights, as the reference's trainable model does; every forward casts them to
+bf16 (the autocast the reference trains under) and every weight gradient arrives in fp32 through that cast.
+The decoder stack is one autograd node (`_DecoderStack`): its forward runs the prefill kernels over the
+packed windows and keeps each layer's activations, its backward runs the HIP backward kernels (attention,
+RMSNorm, QK-norm + RoPE, SwiGLU) and the plain weight / input GEMMs (hipBLASLt through torch.matmul).
+The projector, the embedding gather and the LM head (V = 7 columns) stay torch autograd ops, as in the
+reference. The residual stream is bf16, the rounding points of the inference path.
+"""
+
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import hip_ops as ops
+from .gspo import sequence_ratio_loss
+
+BF16 = torch.bfloat16
+_LAYER_PARAMS = ("attn_norm.weight", "attn.qkv_proj.weight", "attn.q_norm.weight", "attn.k_norm.weight",
+                 "attn.o_proj.weight", "mlp_norm.weight", "gate_up.weight", "down.weight")
+
+
+def decoder_params(dec) -> List[torch.Tensor]:
+    """The decoder-stack parameters in _DecoderStack order: 8 per layer (_LAYER_PARAMS), then the final norm."""
+    sd = dict(dec.named_parameters())
+    out = [sd[f"layers.{i}.{n}"] for i in range(dec.cfg.n_layers) for n in _LAYER_PARAMS]
+    return out + [sd["norm.weight"]]
+
+
+def _mm(a, b):
+    """bf16 product a @ b (hipBLASLt, fp32 accumulation); transposed views are made contiguous first."""
+    return torch.matmul(a.contiguous(), b.contiguous())
+
+
+class _DecoderStack(torch.autograd.Function):
+    """x [N, d] bf16 packed rows -> final-normed hidden of the token rows [n_tok, d] bf16."""
+
+    @staticmethod
+    def forward(ctx, x, meta, *params):
+        cfg = meta["cfg"]
+        H, HKV, D, eps = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.norm_eps
+        L = cfg.n_layers
+        N = x.shape[0]
+        w = [p.detach().to(BF16).contiguous() for p in params]
+        plan, rpos, cos, sin = meta["plan"], meta["rpos"], meta["cos"], meta["sin"]
+        x = x.detach().contiguous().clone()
+        h = ops.add_rmsnorm(x, w[0], eps)
+        saved = []
+        for i in range(L):
+            wa, wqkv, wqn, wkn, wo, wm, wgu, wd = w[8 * i:8 * i + 8]
+            x_in = x.clone()
+            qkv = ops.linear(h, wqkv)
+            q, k, v = ops.qkv_rope_cache(qkv, wqn, wkn, cos, sin, rpos, None, None, None, eps, H, HKV, D,
+                                         return_kv=True)
+            lse = torch.empty(N, H, dtype=torch.float32, device=x.device)
+            o = ops.varlen_attention(q, k, v, plan.attn, lse=lse)
+            h2 = ops.add_rmsnorm(x, wm, eps, delta=ops.linear(o.view(N, H * D), wo))
+            x_mid = x.clone()
+            gu = ops.linear(h2, wgu)
+            g = ops.swiglu(gu)
+            w_next = w[8 * (i + 1)] if i + 1 < L else w[8 * L]
+            h_next = ops.add_rmsnorm(x, w_next, eps, delta=ops.linear(g, wd))
+            saved.append((x_in, h, qkv, q, k, v, o, lse, x_mid, h2, gu, g))
+            h = h_next
+        ctx.meta, ctx.saved_acts, ctx.w, ctx.x_final = meta, saved, w, x
+        return h[meta["tok_rows"]]
+
+    @staticmethod
+    def backward(ctx, dh_tok):
+        meta, saved, w = ctx.meta, ctx.saved_acts, ctx.w
+        cfg = meta["cfg"]
+        H, HKV, D, eps = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.norm_eps
+        L = cfg.n_layers
+        plan, rpos, cos, sin = meta["plan"], meta["rpos"], meta["cos"], meta["sin"]
+        x_final = ctx.x_final
+        N, d = x_final.shape
+        grads = [None] * len(w)
+        dh = torch.zeros(N, d, dtype=torch.float32, device=x_final.device)
+        dh[meta["tok_rows"]] = dh_tok.float()
+        dx, grads[8 * L] = ops.rmsnorm_backward(x_final, w[8 * L], dh, eps)  # dx: d loss / d x_L (fp32)
+        for i in reversed(range(L)):
+            x_in, h, qkv, q, k, v, o, lse, x_mid, h2, gu, g = saved[i]
+            wa, wqkv, wqn, wkn, wo, wm, wgu, wd = w[8 * i:8 * i + 8]
+            # x_{i+1} = x_mid + g Wd^T
+            dm = dx.to(BF16)
+            gd = _mm(dm.t(), g)
+            dg = _mm(dm, wd)
+            dgu = ops.swiglu_backward(gu, dg)
+            ggu = _mm(dgu.t(), h2)
+            dh2 = _mm(dgu, wgu)
+            dx, gm = ops.rmsnorm_backward(x_mid, wm, dh2, eps, dres=dx)  # d / d x_mid
+            # x_mid = x_in + o Wo^T
+            da = dx.to(BF16)
+            go = _mm(da.t(), o.view(N, H * D))
+            do = _mm(da, wo).view(N, H, D).contiguous()
+            dq, dk, dv = ops.attention_backward(q, k, v, o, do, lse, plan.attn, plan.keys)
+            dqkv, gqn, gkn = ops.qknorm_rope_backward(qkv, wqn, wkn, cos, sin, rpos, dq, dk, dv, eps, H, HKV, D)
+            gqkv = _mm(dqkv.t(), h)
+            dhh = _mm(dqkv, wqkv)
+            dx, ga = ops.rmsnorm_backward(x_in, wa, dhh, eps, dres=dx)  # d / d x_in
+            grads[8 * i:8 * i + 8] = [ga, gqkv, gqn, gkn, go, gm, ggu, gd]
+        ctx.saved_acts = None
+        return (dx.to(BF16), None, *[gr.float() for gr in grads])
+
+
+class TrainPlan:
+    """Work lists of one packed batch of causal sequences: the attention's 64-query blocks (forward and dQ)
+    and 64-key blocks (dK / dV). Keys of sequence i are the packed k / v rows [n, 2, 64] from cu[i]."""
+
+    def __init__(self, seq_lens, device, kv_row=128):
+        cu = [0]
+        for n in seq_lens:
+            cu.append(cu[-1] + int(n))
+        self.attn = ops.AttentionPlan(seq_lens, seq_lens, [c * kv_row for c in cu[:-1]], device, causal=True)
+        self.keys = ops.KeyBlockPlan(seq_lens, device)
+
+
+def train_logits(model, frames, tokens_in, plens=None):
+    """Differentiable Basecaller.logits: bf16 logits [B, T, V] of every token position, with gradients into the
+    fp32 projector and decoder parameters (reference: viktor/model.py:55-60 under torch.autocast bf16, as
+    token_logprobs calls it at scripts/gspo.py:345-347). frames [B, P, d_enc]; plens [B] real prefix frames."""
+    dec = model.decoder
+    cfg = dec.cfg
+    B, P = frames.shape[:2]
+    T = tokens_in.shape[1]
+    dev = frames.device
+    plens_h = [P] * B if plens is None else [int(p) for p in plens.tolist()]
+    assert all(0 < p <= P for p in plens_h), "plens outside 1..P"
+    with torch.autocast("cuda", dtype=BF16):
+        prefix = model.projector(frames.to(model.projector[0].weight.dtype)).to(BF16)  # [B, P, d]
+    emb = dec.embed.weight.to(BF16)[tokens_in.to(dev)]                                 # [B, T, d]
+    x = torch.cat([torch.cat([prefix[b, :plens_h[b]], emb[b]]) for b in range(B)]).contiguous()
+    seq_lens = [p + T for p in plens_h]
+    s = model.pos_scale
+    rpos = torch.cat([torch.cat([torch.arange(p, device=dev) * s, s * p + torch.arange(T, device=dev)])
+                      for p in plens_h]).to(torch.int32)
+    off = [0]
+    for n in seq_lens:
+        off.append(off[-1] + n)
+    tok_rows = torch.cat([torch.arange(off[b] + plens_h[b], off[b + 1], device=dev) for b in range(B)])
+    plan = TrainPlan(seq_lens, dev)
+    cos, sin = dec.cos.contiguous(), dec.sin.contiguous()
+    meta = {"cfg": cfg, "plan": plan, "rpos": rpos, "cos": cos, "sin": sin, "tok_rows": tok_rows}
+    h = _DecoderStack.apply(x, meta, *decoder_params(dec))
+    logits = torch.matmul(h, dec.lm_head.weight.to(BF16).t())
+    return logits.view(B, T, -1)
+
+
+class HipAdamW:
+    """AdamW over flat fp32 buffers with the global-norm gradient clip folded into the step, all on the device
+    (torch.optim.AdamW(betas=(0.9, 0.95), weight_decay=0, fused=True) + clip_grad_norm_ of scripts/gspo.py:368,
+    492-493). The parameters become views of one flat buffer, so the step is one launch."""
+
+    def __init__(self, params: Sequence[torch.Tensor], lr=1e-5, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.0,
+                 max_grad_norm: Optional[float] = 1.0):
+        self.params = [p for p in params if p.requires_grad]
+        assert self.params and all(p.dtype == torch.float32 and p.is_cuda for p in self.params), \
+            "HipAdamW: fp32 device parameters"
+        n = sum(p.numel() for p in self.params)
+        dev = self.params[0].device
+        self.flat = torch.empty(n, dtype=torch.float32, device=dev)
+        self.grad = torch.zeros(n, dtype=torch.float32, device=dev)
+        self.m = torch.zeros(n, dtype=torch.float32, device=dev)
+        self.v = torch.zeros(n, dtype=torch.float32, device=dev)
+        self.slices = []
+        o = 0
+        for p in self.params:
+            k = p.numel()
+            self.flat[o:o + k].copy_(p.data.reshape(-1))
+            p.data = self.flat[o:o + k].view_as(p)
+            self.slices.append((o, k))
+            o += k
+        self.lr, self.betas, self.eps, self.weight_decay = lr, betas, eps, weight_decay
+        self.max_grad_norm = max_grad_norm
+        self.step_count = 0
+        self.last_norm = None
+
+    def zero_grad(self):
+        for p in self.params:
+            p.grad = None
+
+    def step(self):
+        """Gather the gradients (a missing one counts as zero), clip by the global norm, AdamW-update."""
+        self.grad.zero_()
+        for p, (o, k) in zip(self.params, self.slices):
+            if p.grad is not None:
+                self.grad[o:o + k].copy_(p.grad.reshape(-1))
+        coef = None
+        if self.max_grad_norm is not None:
+            coef = ops.grad_norm_clip(self.grad, self.max_grad_norm)
+            self.last_norm = coef
+        self.step_count += 1
+        ops.adamw(self.flat, self.grad, self.m, self.v, self.lr, self.betas, self.eps, self.weight_decay,
+                  self.step_count, coef=coef)
+
+
+def token_logprobs_train(model, frames, plens, seqs, ended):
+    """Differentiable token_logprobs (scripts/gspo.py:340-353): (logits [B, T, V] bf16, targets, mask)."""
+    from .gspo import sampled_mask
+    tokens_in, targets, _ = model.batch(seqs, pad_to=128)
+    dev = frames.device
+    tokens_in, targets = tokens_in.to(dev), targets.to(dev)
+    logits = train_logits(model, frames, tokens_in, plens)
+    mask = sampled_mask(targets, seqs, ended, model.tokenizer.k)
+    return logits, targets, mask
+
+
+def gspo_loss(model, frames, plens, seqs, ended, old_lp, n_bases, adv, eps_lo=4e-4, eps_hi=4e-4, inv_n=None):
+    """The micro-batch's GSPO loss (scripts/gspo.py:471-477) with its autograd graph into the model:
+    returns (loss, s [B], pg [B], lp [B, T]). old_lp [B, T] fp32 (masked positions ignored), n_bases [B], adv [B]."""
+    logits, targets, mask = token_logprobs_train(model, frames, plens, seqs, ended)
+    return sequence_ratio_loss(logits, targets, mask, old_lp, n_bases, adv, eps_lo, eps_hi, inv_n)
