@@ -16,6 +16,12 @@ Extra objects on the JSON line:
                 kernel; read from profiles/decode_attention_traffic.json when present, else null).
   cpu_baseline  the CPU oracle (the reference's fp32 torch path restated) on this host, on a bounded sample:
                 rounds of 2 sequences x 2048-frame prefix x 64 sampled tokens for about 12 s; tokens/s.
+  gspo_update   one micro-batch of the GSPO update (scripts/gspo.py:471-493 with --micro 32): 32 windows of
+                2048 frames + 768 tokens (the 1024-token rollout's calls padded to a multiple of 128),
+                teacher-forced forward + backward of the sequence-ratio loss into the fp32 projector and
+                decoder weights + clip + AdamW step; ms per micro-batch and the MFMA fraction of its
+                algorithmic flops (GEMMs 3 x 2 x weights per row, causal attention 3.5 x 1024 n (n + 1) per
+                layer and window: forward + the standard 2.5 x backward) against 2.5 PFLOP/s bf16.
 Usage: python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--no-cpu]
 """
 
@@ -33,6 +39,8 @@ sys.path.insert(0, ROOT)
 
 METRIC = "GSPO rollout tokens/sec on 1 MI355X (512 seq x 1024 tok); % HBM roofline"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+UPDATE_MICRO, UPDATE_T = 32, 768
 PREFIXES, GROUP, P, NEW = 64, 8, 2048, 1024
 KV_ROW_BYTES = 2 * 2 * 64 * 2  # K + V, 2 KV heads, head_dim 64, bf16: one attended position of one layer
 
@@ -111,6 +119,56 @@ def cpu_baseline(seconds_budget=12.0, max_rounds=20):
     return {"value": rounds * n_seq * steps / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{rounds} rounds of {n_seq} sequences x {P}-frame prefix x {steps} sampled tokens "
                       f"(prefill + decode), fp32 CPU restatement of the reference torch path; {dt:.1f} s"}
+
+
+def update_timing(steps=3, warmup=2):
+    """One GSPO update micro-batch on the HIP training path (see the module docstring): times and flops."""
+    from viktor_amd import train as TR
+    from viktor_amd.gspo import sequence_ratio_loss
+    from viktor_amd.synthetic import frames, make_model
+    dev = torch.device("cuda", 0)
+    B, T = UPDATE_MICRO, UPDATE_T
+    m = make_model(1, n_layers=8, seed=7).to(dev)
+    opt = TR.HipAdamW(list(m.parameters()), lr=1e-6, betas=(0.9, 0.95), weight_decay=0.0, max_grad_norm=1.0)
+    g = torch.Generator().manual_seed(8)
+    fr = frames(B, P, 512, seed=9).to(dev)
+    pl = torch.full((B,), P, device=dev)
+    tok = torch.randint(3, 7, (B, T), generator=g).to(dev)
+    tgt = torch.randint(3, 7, (B, T), generator=g).to(dev)
+    mask = torch.ones(B, T, dtype=torch.bool, device=dev)
+    nb = torch.full((B,), float(T), device=dev)
+    adv = torch.randn(B, generator=g).to(dev)
+    with torch.no_grad():
+        z0 = TR.train_logits(m, fr, tok, pl)
+        old = torch.log_softmax(z0.float(), -1).gather(-1, tgt[..., None])[..., 0]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    acc = [0.0, 0.0, 0.0]
+    for it in range(warmup + steps):
+        opt.zero_grad()
+        ev[0].record()
+        z = TR.train_logits(m, fr, tok, pl)
+        loss = sequence_ratio_loss(z, tgt, mask, old, nb, adv, 4e-4, 4e-4, 1.0 / B)[0]
+        ev[1].record()
+        loss.backward()
+        ev[2].record()
+        opt.step()
+        ev[3].record()
+        torch.cuda.synchronize()
+        if it >= warmup:
+            for i in range(3):
+                acc[i] += ev[i].elapsed_time(ev[i + 1]) / steps
+    n = P + T
+    rows = B * n
+    weights = 8 * 3014656  # decoder matmul weights
+    gemm = 3 * 2 * weights * rows + 3 * 2 * 2 * 512 * 512 * B * P + 3 * 2 * 512 * 7 * B * T
+    attn = 3.5 * 1024 * n * (n + 1) * 8 * B
+    ms = sum(acc)
+    tflops = (gemm + attn) / (ms / 1e3) / 1e12
+    return {"microbatch": f"{B} windows x ({P} frames + {T} tokens), 8 layers, fwd + bwd + clip + AdamW",
+            "ms_per_microbatch": round(ms, 2), "forward_ms": round(acc[0], 2), "backward_ms": round(acc[1], 2),
+            "optimizer_ms": round(acc[2], 3), "rows_per_s": round(rows / (ms / 1e3), 1),
+            "alg_tflop": round((gemm + attn) / 1e12, 2), "achieved_tflops": round(tflops, 1),
+            "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
 
 
 def kernels_mode(group, reps=5):
@@ -229,6 +287,10 @@ def main():
             traffic = json.load(f).get("bytes_per_launch")
     out = tokens_check = eng.out[:, :NEW].cpu()
     live = int(((out != 0) & (out != 2)).sum())
+    log("gspo update micro-batch")
+    del eng
+    torch.cuda.empty_cache()
+    update = update_timing()
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
@@ -251,6 +313,7 @@ def main():
                      "traffic": traffic, "avg_launch_us": round(avg_s * 1e6, 2),
                      "alg_bytes_per_launch": int(alg_bytes)},
         "cpu_baseline": cpu,
+        "gspo_update": update,
     }
     print(json.dumps(line), flush=True)
 

@@ -34,8 +34,28 @@ def decoder_params(dec) -> List[torch.Tensor]:
 
 
 def _mm(a, b):
-    """bf16 product a @ b (hipBLASLt, fp32 accumulation); transposed views are made contiguous first."""
-    return torch.matmul(a.contiguous(), b.contiguous())
+    """bf16 product a @ b (hipBLASLt, fp32 accumulation). a may be a transposed view (hipBLASLt reads it in
+    place); b is contiguous."""
+    assert b.is_contiguous()
+    return torch.matmul(a, b)
+
+
+class _TokenEmbed(torch.autograd.Function):
+    """emb_bf16[tokens] with the table's gradient as onehot(tokens)^T @ d_rows: with V = 7 (or 343) rows a
+    small deterministic GEMM instead of a sorted scatter-add (the gather of viktor/model.py:78)."""
+
+    @staticmethod
+    def forward(ctx, weight, tokens):
+        ctx.save_for_backward(tokens)
+        ctx.vocab = weight.shape[0]
+        return weight.detach().to(BF16)[tokens]
+
+    @staticmethod
+    def backward(ctx, d_rows):
+        (tokens,) = ctx.saved_tensors
+        d = d_rows.reshape(-1, d_rows.shape[-1]).to(BF16)
+        onehot = torch.nn.functional.one_hot(tokens.reshape(-1), ctx.vocab).to(BF16)
+        return torch.matmul(onehot.t(), d).float(), None
 
 
 class _DecoderStack(torch.autograd.Function):
@@ -134,7 +154,7 @@ def train_logits(model, frames, tokens_in, plens=None):
     assert all(0 < p <= P for p in plens_h), "plens outside 1..P"
     with torch.autocast("cuda", dtype=BF16):
         prefix = model.projector(frames.to(model.projector[0].weight.dtype)).to(BF16)  # [B, P, d]
-    emb = dec.embed.weight.to(BF16)[tokens_in.to(dev)]                                 # [B, T, d]
+    emb = _TokenEmbed.apply(dec.embed.weight, tokens_in.to(dev))                       # [B, T, d] bf16
     x = torch.cat([torch.cat([prefix[b, :plens_h[b]], emb[b]]) for b in range(B)]).contiguous()
     seq_lens = [p + T for p in plens_h]
     s = model.pos_scale
