@@ -103,3 +103,26 @@ def test_attention_plan_orders_longest_first():
     assert plan.total_q == 195 and plan.cu_q.tolist() == [0, 130, 194, 195]
     with pytest.raises(AssertionError):
         hip_ops.AttentionPlan([5], [4], [0], "cpu", causal=True)
+
+
+def test_batch_weights_map_bases_to_tokens():
+    """Basecaller.batch with per-base weights (the GSPO update's SFT term): a k-mer token weighs its lowest
+    base weight, a partial tail token its lowest real base, EOS 1, padding 0 (viktor/model.py:133-145)."""
+    m = make_model(4, n_layers=1)
+    seqs = ["ACGTACGTAC", "ACG"]
+    weights = [[1, 1, 0, 1, 1, 1, 1, 1, 0.5, 1], [1, 0.2, 1]]
+    tokens_in, targets, w = m.batch(seqs, weights)
+    assert w.shape == targets.shape
+    assert w[0, :4].tolist() == [0.0, 1.0, 0.5, 1.0] and float(w[0, 4:].sum()) == 0.0
+    assert abs(float(w[1, 0]) - 0.2) < 1e-7 and float(w[1, 1]) == 1.0
+    _, _, w_none = m.batch(seqs)
+    assert torch.equal(w_none, (targets != 0).float())
+
+
+def test_key_block_plan_covers_every_key_once():
+    plan = hip_ops.KeyBlockPlan([1, 64, 65, 200], "cpu")
+    blocks = plan.plan.view(-1, 2).tolist()
+    assert plan.n_blocks == 1 + 1 + 2 + 4
+    assert sorted(blocks) == sorted([[0, 0], [1, 0], [2, 0], [2, 64], [3, 0], [3, 64], [3, 128], [3, 192]])
+    work = [[1, 64, 65, 200][s] - k for s, k in blocks]
+    assert work == sorted(work, reverse=True)  # longest work (most rows at or below the block) first

@@ -207,3 +207,66 @@ def test_hip_adamw_update_changes_params_in_place():
     for p, b in zip(params, before):
         assert torch.allclose(p.detach(), b - 1e-3, atol=2e-6)  # Adam's first step moves by lr * sign(g)
         assert p.data.data_ptr() >= opt.flat.data_ptr()
+
+
+def _update_inputs(seed):
+    from viktor_amd.synthetic import frames as synth_frames
+    g = gen(seed)
+    Bw, G, P = 3, 2, 40
+    fr = synth_frames(Bw, P, 512, seed=seed + 1).to(DEV)
+    plens = torch.tensor([40, 23, 31], device=DEV)
+    rnd = lambda n: "".join("ACGT"[int(i)] for i in torch.randint(0, 4, (n,), generator=g))
+    calls = [rnd(int(n)) for n in torch.randint(5, 30, (Bw * G,), generator=g)]
+    ended = [bool(e) for e in torch.randint(0, 2, (Bw * G,), generator=g)]
+    reward = [[0.5, 0.9], [0.7, 0.7], [0.2, 0.6]]  # window 1 has no learning signal
+    labels = [rnd(20), rnd(12), rnd(25)]
+    weights = [[1.0] * 20, [1.0] * 5 + [0.0] + [1.0] * 6, [0.5] * 25]
+    return fr, plens, calls, ended, reward, labels, weights, G
+
+
+def test_gspo_update_bookkeeping_matches_direct_gradient():
+    from viktor_amd.synthetic import make_model
+    from viktor_amd.gspo import advantages, sequence_ratio_loss
+    fr, plens, calls, ended, reward, labels, weights, G = _update_inputs(61)
+    m1 = make_model(1, n_layers=2, seed=62, norm_jitter=0.1).to(DEV)
+    m2 = make_model(1, n_layers=2, seed=62, norm_jitter=0.1).to(DEV)
+    opt = TR.HipAdamW(list(m1.parameters()), lr=0.0)
+    st = TR.gspo_update(m1, opt, fr, plens, calls, ended, reward, G, updates=1, micro=2, eps=0.2, labels=labels,
+                        weights=weights, sft_weight=0.5)
+    assert st["n"] == 4 and st["ratio"] == 0.0  # pi_old from the same forward: s = 1 exactly before any step
+    # the same update's gradient in one pass over every live call and every window
+    adv, live = advantages(torch.tensor(reward, dtype=torch.float64).numpy())
+    seqs = [(b, j) for b in live for j in range(G)]
+    ix = torch.tensor([b for b, _ in seqs], device=DEV)
+    cs = [calls[b * G + j] for b, j in seqs]
+    en = [ended[b * G + j] for b, j in seqs]
+    logits, targets, mask = TR.token_logprobs_train(m2, fr[ix], plens[ix], cs, en)
+    old = ops.gspo_score(logits.detach().contiguous(), targets.clamp(min=0).contiguous())["lp"]
+    nb = torch.tensor([float(max(len(c), 1)) for c in cs], device=DEV)
+    a = torch.tensor([adv[b, j] for b, j in seqs], device=DEV, dtype=torch.float32)
+    loss = sequence_ratio_loss(logits, targets, mask, old, nb, a, 0.2, 0.2, 1.0 / len(seqs))[0]
+    loss.backward()
+    # the SFT term as scripts/gspo.py:480-484 forms it: per micro-batch of windows, its weighted-mean CE times
+    # len(micro-batch) / len(windows) (micro = 2: windows [0, 1] and [2])
+    for wb in ([0, 1], [2]):
+        w_ix = torch.tensor(wb, device=DEV)
+        ce = TR.frame_loss(m2, fr[w_ix], [labels[b] for b in wb], [weights[b] for b in wb], plens=plens[w_ix])
+        (0.5 * ce * len(wb) / 3).backward()
+    want = torch.cat([p.grad.reshape(-1) for p in m2.parameters()])
+    rel = float((opt.grad - want).norm() / want.norm())
+    assert rel < 1e-2, rel
+
+
+def test_gspo_update_steps_move_weights():
+    from viktor_amd.synthetic import make_model
+    fr, plens, calls, ended, reward, labels, weights, G = _update_inputs(71)
+    m = make_model(1, n_layers=2, seed=72).to(DEV)
+    before = [p.detach().clone() for p in m.parameters()]
+    opt = TR.HipAdamW(list(m.parameters()), lr=1e-4)
+    st = TR.gspo_update(m, opt, fr, plens, calls, ended, reward, G, updates=2, micro=3)
+    # step 0 takes windows 0 and 2 (both live); step 1 only window 1, whose rewards are equal: no live call,
+    # a zero gradient (Adam still moves the weights on its first-step moments)
+    assert st["n"] == 4 and len(st["grad_norm"]) == 2 and st["grad_norm"][0] > 0 and st["grad_norm"][1] == 0
+    moved = sum(int(not torch.equal(p.detach(), b)) for p, b in zip(m.parameters(), before))
+    assert moved >= len(before) - 1  # (the embedding rows of unused tokens still move: Adam on zero grads
+    #                                     does nothing only at step 1, so allow one untouched tensor)

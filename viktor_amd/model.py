@@ -9,6 +9,7 @@ packed tokens with its last layer kept for the token rows only, and the LM head 
 
 from typing import Optional
 
+import numpy as np
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
@@ -92,13 +93,24 @@ class Basecaller(nn.Module):
         return self.decoder.head(h).view(B, T, -1)
 
     def batch(self, seqs, weights=None, pad_to=1):
-        """CPU teacher-forcing tensors: tokens_in, targets [B, T] and target weights (targets != PAD), T
-        padded up to a multiple of pad_to. Reference: viktor/model.py:119-131 (per-base weights and
-        alignment centres belong to SFT and are not part of this path)."""
-        if weights is not None:
-            raise NotImplementedError("per-base target weights are an SFT feature outside the rollout/scoring path")
+        """CPU teacher-forcing tensors: tokens_in, targets [B, T] and target weights [B, T], T padded up to a
+        multiple of pad_to. weights: one array per sequence, a weight per base; a k-mer token weighs its
+        lowest base weight (a masked base masks its token), EOS 1; without weights every target (EOS
+        included) weighs 1. Reference: viktor/model.py:119-145 (alignment centres, an SFT attention-probe
+        target, are not part of this path)."""
         tokens_in, targets, _ = self.tokenizer.batch(seqs)
         T = -(-targets.shape[1] // pad_to) * pad_to
         tokens_in = F.pad(tokens_in, (0, T - tokens_in.shape[1]), value=PAD)
         targets = F.pad(targets, (0, T - targets.shape[1]), value=PAD)
-        return tokens_in, targets, (targets != PAD).float()
+        if weights is None:
+            return tokens_in, targets, (targets != PAD).float()
+        k = self.tokenizer.k
+        w = torch.zeros(targets.shape)
+        for b, wb in enumerate(weights):
+            wb = np.asarray(wb, dtype=np.float32)
+            pad = np.full(-(-len(wb) // k) * k, np.inf, np.float32)
+            pad[:len(wb)] = wb
+            wt = pad.reshape(-1, k).min(1)
+            w[b, :len(wt)] = torch.from_numpy(wt)
+            w[b, len(wt)] = 1.0  # EOS
+        return tokens_in, targets, w

@@ -236,3 +236,81 @@ def gspo_loss(model, frames, plens, seqs, ended, old_lp, n_bases, adv, eps_lo=4e
     returns (loss, s [B], pg [B], lp [B, T]). old_lp [B, T] fp32 (masked positions ignored), n_bases [B], adv [B]."""
     logits, targets, mask = token_logprobs_train(model, frames, plens, seqs, ended)
     return sequence_ratio_loss(logits, targets, mask, old_lp, n_bases, adv, eps_lo, eps_hi, inv_n)
+
+
+def frame_loss(model, frames, seqs, weights=None, plens=None):
+    """Differentiable weighted-mean token cross-entropy of teacher-forced label sequences, the SFT term of the
+    GSPO update (Basecaller.frame_loss / weighted_loss / token_metrics, viktor/model.py:153-177, 201-203;
+    called at scripts/gspo.py:482-484): sum(ce * w) / sum(w) over the targets (PAD ignored)."""
+    dev = frames.device
+    tokens_in, targets, w = (t.to(dev) for t in model.batch(seqs, weights))
+    logits = train_logits(model, frames, tokens_in, plens)
+    ce = torch.nn.functional.cross_entropy(logits.flatten(0, 1).float(), targets.flatten(), ignore_index=0,
+                                           reduction="none").view_as(targets)
+    return (ce * w).sum() / w.sum()
+
+
+def _old_row(vals, mask_row):
+    """Scatter one sequence's per-token values (its sampled positions, in order) into a row of mask_row's shape."""
+    row = torch.zeros(mask_row.shape, dtype=torch.float32, device=mask_row.device)
+    row[mask_row] = vals
+    return row
+
+
+def gspo_update(model, opt: HipAdamW, frames, plens, calls, ended, reward, G, updates=2, micro=32, eps=4e-4,
+                std_floor=0.003, labels=None, weights=None, sft_weight=0.0):
+    """The GSPO policy update of one rollout (scripts/gspo.py:446-493 on one GPU, without the all-reduce):
+    advantages over each window's G calls (live windows: reward std > 1e-6); pi_old of every live call before
+    any update; then `updates` optimiser steps, step u over the calls of windows b % updates == u: micro-batches
+    of the sequence-ratio loss summed / len(mine), plus sft_weight x the weighted cross-entropy of the windows'
+    labels (when given), backward, clip + AdamW (opt). frames [windows, P, d_enc], plens [windows]; calls /
+    ended: the G calls of window b at b * G .. b * G + G - 1; reward [windows, G]. Returns the step statistics
+    (pg, ce, clip, ratio, n as the reference's, and each step's gradient norm)."""
+    from .gspo import advantages
+    import numpy as np
+    B = frames.shape[0]
+    adv, live = advantages(np.asarray(reward, dtype=np.float64).reshape(B, G), std_floor=std_floor)
+    seqs = [(b, j) for b in live for j in range(G)]
+    n_bases = {bj: max(len(calls[bj[0] * G + bj[1]]), 1) for bj in seqs}
+    dev = frames.device
+
+    def batch_of(mb):
+        ix = torch.tensor([b for b, _ in mb], device=dev)
+        return frames[ix], plens[ix], [calls[b * G + j] for b, j in mb], [ended[b * G + j] for b, j in mb]
+
+    old = {}
+    with torch.no_grad():  # pi_old through the same forward as the update's (scripts/gspo.py:455-462)
+        for i in range(0, len(seqs), micro):
+            mb = seqs[i:i + micro]
+            logits, targets, m = token_logprobs_train(model, *batch_of(mb))
+            lp = ops.gspo_score(logits.contiguous(), targets.clamp(min=0).contiguous())["lp"]
+            for k, bj in enumerate(mb):
+                old[bj] = lp[k][m[k]].clone()
+    stats = {"pg": 0.0, "ce": 0.0, "clip": 0.0, "ratio": 0.0, "n": 0, "grad_norm": []}
+    for u in range(updates):
+        mine = [bj for bj in seqs if bj[0] % updates == u]
+        wins = [b for b in range(B) if b % updates == u]
+        opt.zero_grad()
+        for i in range(0, len(mine), micro):
+            mb = mine[i:i + micro]
+            logits, targets, mask = token_logprobs_train(model, *batch_of(mb))
+            old_lp = torch.stack([_old_row(old[bj], mask[k]) for k, bj in enumerate(mb)])
+            nb = torch.tensor([float(n_bases[bj]) for bj in mb], device=dev)
+            a = torch.tensor([adv[b, j] for b, j in mb], device=dev, dtype=torch.float32)
+            loss, s, pg, _ = sequence_ratio_loss(logits, targets, mask, old_lp, nb, a, eps, eps, 1.0 / len(mine))
+            loss.backward()
+            stats["pg"] += float(pg.sum())
+            stats["n"] += len(mb)
+            stats["clip"] += float(((s - 1).abs() > eps).sum())
+            stats["ratio"] += float((s - 1).abs().sum())
+        if sft_weight and labels is not None:
+            for i in range(0, len(wins), micro):
+                wb = wins[i:i + micro]
+                ix = torch.tensor(wb, device=dev)
+                ce = frame_loss(model, frames[ix], [labels[b] for b in wb],
+                                None if weights is None else [weights[b] for b in wb], plens=plens[ix])
+                (sft_weight * ce * len(wb) / len(wins)).backward()
+                stats["ce"] += float(ce) * len(wb)
+        opt.step()
+        stats["grad_norm"].append(None if opt.last_norm is None else float(opt.last_norm[0]))
+    return stats
