@@ -249,7 +249,7 @@ int vk_group_advantage(const float *reward, int64_t groups, int32_t n, int32_t m
  * rows cu[i] .. cu[i+1]-1 of q / out / dout [n_rows, 8, 64] bf16 and of k / v (row j at j * stride_tok,
  * + kv head * 64); query r sees keys <= r. lse [n_rows, 8]: the forward's vk_varlen_attention log-sum-exp
  * (log2 units). q_plan: (sequence, first row) per 64-query block (as vk_varlen_attention's plan); k_plan:
- * (sequence, first key) per 64-key block. dd [n_rows, 8] fp32 scratch (written: sum_d dout * out);
+ * (sequence, first key) per 128-key block. dd [n_rows, 8] fp32 scratch (written: sum_d dout * out);
  * dq [n_rows, 8, 64], dk / dv [n_rows, 2, 64] fp32 (written). H = 8, HKV = 2, D = 64.
  */
 int vk_attention_backward(const void *q, const void *k, const void *v, const void *out, const void *dout,

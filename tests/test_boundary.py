@@ -120,9 +120,9 @@ def test_batch_weights_map_bases_to_tokens():
 
 
 def test_key_block_plan_covers_every_key_once():
-    plan = hip_ops.KeyBlockPlan([1, 64, 65, 200], "cpu")
+    plan = hip_ops.KeyBlockPlan([1, 128, 129, 300], "cpu")
     blocks = plan.plan.view(-1, 2).tolist()
-    assert plan.n_blocks == 1 + 1 + 2 + 4
-    assert sorted(blocks) == sorted([[0, 0], [1, 0], [2, 0], [2, 64], [3, 0], [3, 64], [3, 128], [3, 192]])
-    work = [[1, 64, 65, 200][s] - k for s, k in blocks]
+    assert plan.n_blocks == 1 + 1 + 2 + 3
+    assert sorted(blocks) == sorted([[0, 0], [1, 0], [2, 0], [2, 128], [3, 0], [3, 128], [3, 256]])
+    work = [[1, 128, 129, 300][s] - k for s, k in blocks]
     assert work == sorted(work, reverse=True)  # longest work (most rows at or below the block) first

@@ -15,10 +15,12 @@
 //     heads x 2 halves of 32 rows), K / V tiles of 64 keys double buffered in LDS. Per key half:
 //     S^T = K Q^T, dP^T = V dO^T (A = key rows from LDS, B = Q^T / dO^T held in registers), dS^T in the
 //     accumulator layout, dQ^T += K^T dS^T (A = K^T read column-wise from LDS).
-//   * dK/dV kernel: a workgroup per 64-key block x KV head, 4 wavefronts of 16 keys (K^T / V^T fragments
+//   * dK/dV kernel: a workgroup per 128-key block x KV head, 8 wavefronts of 16 keys (K^T / V^T fragments
 //     in registers), looping over the 32-query tiles at or below the diagonal, Q / dO / lse / D of the 4
-//     query heads staged in LDS: S = Q K^T, dP = dO V^T (A = query rows from LDS), then dV^T += dO^T P and
-//     dK^T += Q^T dS with P / dS consumed in their accumulator layout; the 4 heads accumulate in place.
+//     query heads staged in LDS (the next tile's loads in flight during the current one), with transposed
+//     copies of Q and dO: S = Q K^T, dP = dO V^T (A = query rows), then dV^T += dO^T P and dK^T += Q^T dS
+//     (A = the transposed copies) with P / dS consumed in their accumulator layout; the 4 heads accumulate
+//     in place. 128 keys per staged tile halve the re-reads of Q / dO against 64.
 // Gradients are written in fp32 (the consumers -- QK-norm / RoPE backward, the qkv weight gradient -- work
 // in fp32 and round once).
 #include <math.h>
@@ -29,6 +31,8 @@ namespace vk {
 
 constexpr int AB_H = 8, AB_HKV = 2, AB_D = 64;
 constexpr int AB_PITCH = 72;  // 64 + 8 bf16 per LDS row
+constexpr int AB_KW = 8;      // wavefronts of a dK/dV workgroup (16 keys each: 128 keys per staged query tile)
+constexpr int AB_KB = 16 * AB_KW;
 
 // D[r, h] = sum_d dO[r, h, d] * o[r, h, d]: one thread per (row, head)
 __global__ __launch_bounds__(256) void attn_bwd_dot_kernel(const bf16_t *__restrict__ dout,
@@ -182,14 +186,21 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
   }
 }
 
-// ---- dK / dV: workgroup = 64 keys of one sequence x one KV head ------------------------------------------
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(
+// ---- dK / dV: workgroup = AB_KB keys of one sequence x one KV head ----------------------------------------
+__global__ __launch_bounds__(AB_KW * 64) void attn_bwd_dkdv_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ k, const bf16_t *__restrict__ v,
     const bf16_t *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ dd,
     const int32_t *__restrict__ cu, const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok,
     float *__restrict__ dk, float *__restrict__ dv, float scale_log2, float scale) {
+  // row-major Q / dO tiles (the A operands of S and dP) and transposed copies [head][d][row] (the A operands of
+  // dK^T and dV^T: a lane's 8 rows of one d are four 32-bit reads instead of eight 16-bit ones)
+  // 32 rows + 6 pad: the staging stores (lanes: 8 d chunks x 8 rows) then fall on 64 distinct banks
+  // (row stride 76 bytes = 19 banks); the rows are 4-byte aligned, read as 32-bit words
+  constexpr int TP = 38;
   __shared__ __attribute__((aligned(16))) bf16_t Qs[4 * 32 * AB_PITCH];
   __shared__ __attribute__((aligned(16))) bf16_t Os[4 * 32 * AB_PITCH];  // dO
+  __shared__ __attribute__((aligned(16))) bf16_t QTs[4 * 64 * TP];
+  __shared__ __attribute__((aligned(16))) bf16_t OTs[4 * 64 * TP];
   __shared__ float Ls[4 * 32], Ds[4 * 32];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int col = lane & 15, g = lane >> 4;
@@ -215,13 +226,16 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(
   for (int dt = 0; dt < 4; ++dt) accv[dt] = acck[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int wave_kmin = ks + 16 * wid;  // rows below it see none of this wave's keys
 
-  // staging: thread t loads 16-byte chunks t + 256 c (c < 4) of the Q tile and of the dO tile:
-  // chunk -> (head hh = chunk / 256, row rr = chunk / 8 % 32, d chunk dc8 = chunk % 8)
-  for (int rs = ks; rs < len; rs += 32) {
-    u32x4 qv[4], ov[4];
+  // staging: thread t loads 16-byte chunks t + NT c (c < 1024 / NT) of the Q tile and of the dO tile:
+  // chunk -> (head hh = chunk / 256, row rr = chunk / 8 % 32, d chunk dc8 = chunk % 8), and threads t < 256
+  // one lse (t < 128) or D value. Software pipelined: tile rs + 32 is loaded while tile rs is computed.
+  constexpr int NT = AB_KW * 64, NC = 1024 / NT;
+  u32x4 qv[NC], ov[NC];
+  float lv = 0.f;
+  auto load_tile = [&](int rs) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int chunk = tid + 256 * c;
+    for (int c = 0; c < NC; ++c) {
+      const int chunk = tid + NT * c;
       const int hh = chunk >> 8, rr = (chunk >> 3) & 31, dc8 = chunk & 7;
       int r = rs + rr;
       r = r < len ? r : len - 1;
@@ -229,31 +243,36 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(
       qv[c] = *reinterpret_cast<const u32x4 *>(q + off);
       ov[c] = *reinterpret_cast<const u32x4 *>(dout + off);
     }
-    float lv = 0.f;
-    if (tid < 128) {
-      const int hh = tid >> 5, rr = tid & 31;
-      int r = rs + rr;
-      r = r < len ? r : len - 1;
-      lv = lse[(r0 + r) * AB_H + hk * 4 + hh];
-    } else {
-      const int hh = (tid - 128) >> 5, rr = tid & 31;
-      int r = rs + rr;
-      r = r < len ? r : len - 1;
-      lv = dd[(r0 + r) * AB_H + hk * 4 + hh];
-    }
+    const int hh = (tid & 127) >> 5, rr = tid & 31;
+    int r = rs + rr;
+    r = r < len ? r : len - 1;
+    const int64_t row = (r0 + r) * AB_H + hk * 4 + hh;
+    lv = tid < 128 ? lse[row] : dd[row];  // (threads >= 256 load a D value they do not store)
+  };
+  load_tile(ks);
+  for (int rs = ks; rs < len; rs += 32) {
     __syncthreads();  // the previous tile's readers are done
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int chunk = tid + 256 * c;
+    for (int c = 0; c < NC; ++c) {
+      const int chunk = tid + NT * c;
       const int hh = chunk >> 8, rr = (chunk >> 3) & 31, dc8 = chunk & 7;
       *reinterpret_cast<u32x4 *>(&Qs[(hh * 32 + rr) * AB_PITCH + 8 * dc8]) = qv[c];
       *reinterpret_cast<u32x4 *>(&Os[(hh * 32 + rr) * AB_PITCH + 8 * dc8]) = ov[c];
+      // (16-bit halves by integer shifts: element extraction from a __bf16 vector with a bit_cast to
+      // uint16_t was lowered to the same register for every element by this compiler)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t qw = qv[c][e >> 1], ow = ov[c][e >> 1];
+        QTs[(hh * 64 + 8 * dc8 + e) * TP + rr] = static_cast<bf16_t>((e & 1) ? (qw >> 16) : (qw & 0xffffu));
+        OTs[(hh * 64 + 8 * dc8 + e) * TP + rr] = static_cast<bf16_t>((e & 1) ? (ow >> 16) : (ow & 0xffffu));
+      }
     }
     if (tid < 128)
       Ls[tid] = lv;
-    else
+    else if (tid < 256)
       Ds[tid - 128] = lv;
     __syncthreads();
+    if (rs + 32 < len) load_tile(rs + 32);
     if (rs + 31 < wave_kmin) continue;  // wave-uniform: every row of the tile lies above this wave's keys
 
 #pragma unroll
@@ -285,16 +304,15 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(
           pf[rb * 4 + i] = static_cast<__bf16>(p);
           dsf[rb * 4 + i] = static_cast<__bf16>(p * (dpt[rb][i] - Ds[hh * 32 + rr]));
         }
-      // dV^T += dO^T P, dK^T += Q^T dS (A = dO^T / Q^T read column-wise: lane col -> d, row order as above)
+      // dV^T += dO^T P, dK^T += Q^T dS (A = dO^T / Q^T from the transposed copies: lane col -> d, rows
+      // {4g..4g+3} and {16+4g..16+4g+3} as four 32-bit reads, the row order of P / dS above)
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        bf16x8 oa, qa;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int rl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
-          oa[jj] = __builtin_bit_cast(__bf16, ot[rl * AB_PITCH + 16 * dt + col]);
-          qa[jj] = __builtin_bit_cast(__bf16, qt[rl * AB_PITCH + 16 * dt + col]);
-        }
+        const bf16_t *qtr = &QTs[(hh * 64 + 16 * dt + col) * TP];
+        const bf16_t *otr = &OTs[(hh * 64 + 16 * dt + col) * TP];
+        const uint32_t *qw = reinterpret_cast<const uint32_t *>(qtr), *ow = reinterpret_cast<const uint32_t *>(otr);
+        const bf16x8 qa = __builtin_bit_cast(bf16x8, u32x4{qw[2 * g], qw[2 * g + 1], qw[8 + 2 * g], qw[9 + 2 * g]});
+        const bf16x8 oa = __builtin_bit_cast(bf16x8, u32x4{ow[2 * g], ow[2 * g + 1], ow[8 + 2 * g], ow[9 + 2 * g]});
         accv[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(oa, pf, accv[dt], 0, 0, 0);
         acck[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa, dsf, acck[dt], 0, 0, 0);
       }
@@ -349,7 +367,7 @@ extern "C" int vk_attention_backward(const void *q, const void *k, const void *v
     if (rc != VK_OK) return rc;
   }
   if (n_kblocks > 0) {
-    attn_bwd_dkdv_kernel<<<dim3(static_cast<unsigned>(n_kblocks), AB_HKV), 256, 0, s>>>(
+    attn_bwd_dkdv_kernel<<<dim3(static_cast<unsigned>(n_kblocks), AB_HKV), AB_KW * 64, 0, s>>>(
         qb, kb, vb, dob, lse, dd, cu, k_plan, n_seq, stride_tok, dk, dv, scale_log2, scale);
     rc = launch_status("attention_backward dkdv");
   }

@@ -426,10 +426,10 @@ def group_advantage(reward, std_floor=None, eps=None):
 
 # ---- the GSPO update's backward and optimizer step -------------------------------------------------------
 class KeyBlockPlan:
-    """(sequence, first key) per 64-key block of causal self-attention over packed sequences, longest work
+    """(sequence, first key) per 128-key block of causal self-attention over packed sequences, longest work
     (most query rows at or below the block) first: the dK / dV work list of attention_backward."""
 
-    BLOCK = 64
+    BLOCK = 128
 
     def __init__(self, seq_lens, device):
         lens = [int(n) for n in seq_lens]
