@@ -16,6 +16,12 @@ Extra objects on the JSON line:
                 kernel; read from profiles/decode_attention_traffic.json when present, else null).
   cpu_baseline  the CPU oracle (the reference's fp32 torch path restated) on this host, on a bounded sample:
                 rounds of 2 sequences x 2048-frame prefix x 64 sampled tokens for about 12 s; tokens/s.
+  gspo_reward   a rollout's 512 rewards on the device (strict identity, scripts/gspo.py:446) straight from the
+                output tokens: 64 synthetic 0.9-1.1 kb labels (5% of bases unscored), each window's 8 calls the
+                label with 5% substitutions / insertions / deletions, as token rows of 1024 (EOS after the
+                call); ms per rollout (device token decode + label packing + the DP kernel) and DP cells per
+                second (label x call bases). (The random-weight model of the rollout ends its calls after a
+                few bases, so its own output would time an almost empty DP.)
   gspo_update   one micro-batch of the GSPO update (scripts/gspo.py:471-493 with --micro 32): 32 windows of
                 2048 frames + 768 tokens (the 1024-token rollout's calls padded to a multiple of 128),
                 teacher-forced forward + backward of the sequence-ratio loss into the fp32 projector and
@@ -119,6 +125,43 @@ def cpu_baseline(seconds_budget=12.0, max_rounds=20):
     return {"value": rounds * n_seq * steps / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{rounds} rounds of {n_seq} sequences x {P}-frame prefix x {steps} sampled tokens "
                       f"(prefill + decode), fp32 CPU restatement of the reference torch path; {dt:.1f} s"}
+
+
+def reward_timing(tokenizer, reps=5):
+    """A rollout's rewards on the device from output tokens (see the module docstring)."""
+    import numpy as np
+    from viktor_amd import reward as RW
+    rng = np.random.default_rng(11)
+    labels = ["".join(rng.choice(list("ACGT"), int(n))) for n in rng.integers(900, 1100, PREFIXES)]
+    weights = [(rng.random(len(l)) > 0.05).astype(np.float32) for l in labels]
+    rows = np.zeros((PREFIXES * GROUP, NEW), dtype=np.int64)  # PAD
+    for i in range(PREFIXES * GROUP):
+        call = []
+        for ch in labels[i // GROUP]:
+            u = rng.random()
+            if u < 0.05 / 3:
+                continue
+            call.append(rng.choice(list("ACGT")) if u < 0.1 / 3 else ch)
+            if rng.random() < 0.05 / 3:
+                call.append(rng.choice(list("ACGT")))
+        call = call[:NEW - 1]
+        rows[i, :len(call)] = [3 + "ACGT".index(b) for b in call]
+        rows[i, len(call)] = 2  # EOS
+    tokens = torch.from_numpy(rows).to("cuda")
+    for _ in range(2):
+        res = RW.gspo_rewards_from_tokens(tokens, tokenizer, labels, weights, GROUP)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        res = RW.gspo_rewards_from_tokens(tokens, tokenizer, labels, weights, GROUP)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / reps * 1e3
+    _, _, lens, _ = RW.calls_from_tokens(tokens, tokenizer)
+    call_len = lens.cpu().numpy()
+    cells = float(sum(len(labels[i // GROUP]) * int(n) for i, n in enumerate(call_len)))
+    return {"rewards": int(tokens.shape[0]), "ms_per_rollout": round(ms, 3), "cells_per_s": round(cells / (ms / 1e3), 1),
+            "mean_call_bases": round(float(call_len.mean()), 1), "mean_reward": round(float(res["reward"].mean()), 4),
+            "includes": "token decode on the device + packing of the labels + the DP kernel"}
 
 
 def update_timing(steps=3, warmup=2):
@@ -287,6 +330,8 @@ def main():
             traffic = json.load(f).get("bytes_per_launch")
     out = tokens_check = eng.out[:, :NEW].cpu()
     live = int(((out != 0) & (out != 2)).sum())
+    log("gspo reward")
+    reward = reward_timing(gm.tokenizer)
     log("gspo update micro-batch")
     del eng
     torch.cuda.empty_cache()
@@ -313,6 +358,7 @@ def main():
                      "traffic": traffic, "avg_launch_us": round(avg_s * 1e6, 2),
                      "alg_bytes_per_launch": int(alg_bytes)},
         "cpu_baseline": cpu,
+        "gspo_reward": reward,
         "gspo_update": update,
     }
     print(json.dumps(line), flush=True)

@@ -304,6 +304,23 @@ int vk_grad_norm_clip(const float *g, int64_t n, float max_norm, float *partials
 int vk_adamw(float *p, const float *g, float *m, float *v, int64_t n, const float *coef, float lr, float b1, float b2,
              float eps, float wd, int64_t step, void *stream);
 
+/*
+ * The GSPO reward on the device: strict identity of call c (bases calls[call_off[c] ..], call_len[c] of them)
+ * against label r = ref_of_call[c] (refs[ref_off[r] ..], ref_len[r] bases, scored[ref_off[r] ..] its mask of
+ * counted bases) -- scripts/gspo.py:86-89 with ref_errors (scripts/train.py:170-188):
+ *   empty label: 1 if len(call) <= empty_max else empty_max / len(call);
+ *   else 1 - (errors of a global alignment path on scored label bases) / max(len(call), len(label)),
+ * a mismatch or deletion counted at its label base, an insertion at the label base before it. The path is the
+ * traceback that prefers diagonal, then deletion, then insertion at each cell (edlib's own order is not
+ * available; the edit distance, and the count when every base is scored, do not depend on it).
+ * Bases are any byte codes compared for equality. Writes reward, edit_distance and scored_errors [n_calls].
+ * max_ref_len / max_call_len: the longest label / call (at most 4096 / 8192).
+ */
+int vk_strict_identity(const uint8_t *calls, const int64_t *call_off, const int32_t *call_len, const uint8_t *refs,
+                       const int64_t *ref_off, const int32_t *ref_len, const uint8_t *scored, const int32_t *ref_of_call,
+                       int32_t n_calls, int32_t n_refs, int32_t max_ref_len, int32_t max_call_len, float empty_max,
+                       float *reward, int32_t *edit_distance, int32_t *scored_errors, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -467,3 +467,63 @@ def gspo_grad_closed_form(logits, targets, mask, old_lp, n_bases, adv, eps_lo, e
     coef = inv_n * g * s / n_bases.double()
     onehot = F.one_hot(y, z.shape[-1]).double()
     return coef[:, None, None] * m[..., None] * (onehot - lp.exp())
+
+
+# ---------------------------------------------------------------------------------------------
+# GSPO reward: strict identity (scripts/gspo.py:86-89, ref_errors at scripts/train.py:170-188, EMPTY_MAX at
+# scripts/evaluate.py:30)
+EMPTY_MAX = 4
+
+
+def edit_distance(a, b):
+    """Levenshtein distance by the textbook row DP (independent of any path choice)."""
+    prev = list(range(len(b) + 1))
+    for i, ca in enumerate(a, 1):
+        cur = [i] + [0] * len(b)
+        for j, cb in enumerate(b, 1):
+            cur[j] = min(prev[j] + 1, cur[j - 1] + 1, prev[j - 1] + (ca != cb))
+        prev = cur
+    return prev[-1]
+
+
+def strict_identity_ref(call, ref, scored, empty_max=EMPTY_MAX):
+    """(reward, edit distance, scored errors) of call against ref with scored [len(ref)] bool. The errors are
+    those of the global alignment path whose every cell takes the first optimal predecessor in the order
+    diagonal, deletion (of a ref base), insertion (of a call base): a mismatch or deletion counts at its ref
+    base, an insertion at the ref base before it (base 0 before any ref base), as ref_errors places them.
+    The count is carried forward along the chosen predecessors (numpy over anti-diagonals)."""
+    n, m = len(call), len(ref)
+    if m == 0:
+        return (1.0 if n <= empty_max else empty_max / n), n, 0
+    r = np.frombuffer(ref.encode(), np.uint8).astype(np.int64)
+    c = np.frombuffer(call.encode(), np.uint8).astype(np.int64)
+    sc = np.asarray(scored, dtype=bool).astype(np.int64)
+    D = [np.zeros(m + 1, np.int64) for _ in range(3)]
+    C = [np.zeros(m + 1, np.int64) for _ in range(3)]
+    for k in range(m + n + 1):
+        d0, c0 = D[k % 3], C[k % 3]
+        d1, c1 = D[(k - 1) % 3], C[(k - 1) % 3]
+        d2, c2 = D[(k - 2) % 3], C[(k - 2) % 3]
+        lo, hi = max(0, k - n), min(m, k)
+        i = np.arange(lo, hi + 1)
+        j = k - i
+        d = np.zeros_like(i)
+        e = np.zeros_like(i)
+        top, left, inner = i == 0, (j == 0) & (i > 0), (i > 0) & (j > 0)
+        d[top] = j[top]
+        e[top] = np.where(j[top] > 0, c1[0] + sc[0], 0)
+        il = i[left]
+        d[left] = il
+        e[left] = c1[il - 1] + sc[il - 1]
+        ii, jj = i[inner], j[inner]
+        mis = (r[ii - 1] != c[jj - 1]).astype(np.int64)
+        dd, du, dl = d2[ii - 1] + mis, d1[ii - 1] + 1, d1[ii] + 1
+        best = np.minimum(np.minimum(dd, du), dl)
+        e_in = np.where(dd == best, c2[ii - 1] + mis * sc[ii - 1],
+                        np.where(du == best, c1[ii - 1] + sc[ii - 1], c1[ii] + sc[ii - 1]))
+        d[inner] = best
+        e[inner] = e_in
+        d0[i] = d
+        c0[i] = e
+    dist, errs = int(D[(m + n) % 3][m]), int(C[(m + n) % 3][m])
+    return 1.0 - errs / max(n, m), dist, errs

@@ -361,3 +361,28 @@ def test_gspo_param_grads_match_finite_differences():
             fd = (vals[0] - vals[1]) / 2e-4
             an = float(flat[idx])
             assert abs(fd - an) <= 1e-5 + 1e-3 * abs(an), (name, idx, fd, an)
+
+
+def test_strict_identity_oracle_pinned():
+    """The reward oracle: its distance is the textbook edit distance; with every base scored the error count
+    is that distance (any optimal path); hand cases with a unique optimal path place the errors as ref_errors
+    does (scripts/train.py:170-188); the empty-label and empty-call rules (scripts/gspo.py:86-89)."""
+    g = np.random.default_rng(3)
+    for _ in range(60):
+        a = "".join(g.choice(list("ACGT"), g.integers(0, 40)))
+        b = "".join(g.choice(list("ACGT"), g.integers(1, 40)))
+        rew, dist, errs = R.strict_identity_ref(a, b, np.ones(len(b), bool))
+        assert dist == R.edit_distance(a, b) == errs
+        assert abs(rew - (1 - dist / max(len(a), len(b)))) < 1e-12
+    # substitution at 2, deletion of base 1, insertion after base 1: each a unique optimal path
+    for call, ref, pos in (("ACTT", "ACGT", 2), ("AGT", "ACGT", 1), ("ACXGT", "ACGT", 1)):
+        for p in range(len(ref)):
+            scored = np.ones(len(ref), bool)
+            scored[p] = False
+            _, _, errs = R.strict_identity_ref(call, ref, scored)
+            assert errs == (0 if p == pos else 1), (call, ref, p)
+    assert R.strict_identity_ref("XACGT", "ACGT", np.array([False, True, True, True]))[2] == 0  # before base 0
+    # an empty call deletes every label base; an empty label scores by length
+    assert R.strict_identity_ref("", "ACGT", np.array([1, 0, 1, 1], bool)) == (0.25, 4, 3)
+    assert R.strict_identity_ref("ACG", "", np.zeros(0, bool)) == (1.0, 3, 0)
+    assert R.strict_identity_ref("ACGTAC", "", np.zeros(0, bool))[0] == 4 / 6

@@ -58,6 +58,7 @@ SIGNATURES = {
     "vk_swiglu_backward": [_P, _P, _P, _I64, _I32, _P],
     "vk_grad_norm_clip": [_P, _I64, _F, _P, _I32, _P, _P],
     "vk_adamw": [_P, _P, _P, _P, _I64, _P, _F, _F, _F, _F, _F, _I64, _P],
+    "vk_strict_identity": [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F, _P, _P, _P, _P],
 }
 
 _lock = threading.Lock()
