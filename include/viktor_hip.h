@@ -321,6 +321,66 @@ int vk_strict_identity(const uint8_t *calls, const int64_t *call_off, const int3
                        int32_t n_calls, int32_t n_refs, int32_t max_ref_len, int32_t max_call_len, float empty_max,
                        float *reward, int32_t *edit_distance, int32_t *scored_errors, void *stream);
 
+/*
+ * The encoder (frames producer): the Dorado SUP conv stack + sliding-window DeepNorm transformer of
+ * viktor/encoder.py:43-192, which the reference runs on koi (viktor/csrc/koi_tx.cpp:253-414: koi_vcs_tx_cnn,
+ * koi_qkv_rotary + koi_vcs_attn, koi_linear, koi_rmsnorm_residual, koi_mm_swiglu).
+ *
+ * Padded chunk layout of a convolution's activations: channels-last [rows, C] bf16, chunk c's data rows at
+ * [start[c], start[c] + len[c]), zero margin rows between chunks; the input row of output row g is
+ * stride * g - pad for every row (margins scale by the strides), so the zero margins are each chunk's
+ * Conv1d padding.
+ *
+ * First convolution (C_in = 1; viktor/encoder.py:43-49 and the first koi_vcs_tx_cnn call, koi_tx.cpp:296-315):
+ * out[g, co] = bf16(silu(bf16(b[co] + sum_k w[co, k] signal[sig_off[c] + stride t - pad + k]))) for data row
+ * g = start[c] + t (samples outside the chunk read as 0), zeros for margin rows; signal, w [C, winlen], b fp32;
+ * out [rows, C] bf16 (C % 8 == 0, winlen <= 32).
+ */
+int vk_encoder_conv_first(const float *signal, const int64_t *sig_off, const int32_t *start, const int32_t *len,
+                          int32_t n_chunks, int64_t rows, const float *w, const float *b, int32_t C, int32_t winlen,
+                          int32_t stride, int32_t pad, void *out, void *stream);
+
+/*
+ * Later convolutions (viktor/encoder.py:43-49; koi_vcs_tx_cnn, koi_tx.cpp:296-315) as one strided GEMM:
+ * out[dst(g), n] = bf16(silu(bf16(sum_k a[g lda + k] w[n, k] + bias[n]))), k = tap * C_in + channel,
+ * K = winlen * C_in (% 32), N = C_out (% 64), lda = stride * C_in; a points at input row -pad of the padded
+ * layout (the buffer holds guard rows around it). compact = 0: dst(g) = g, margin rows written as zeros;
+ * compact = 1: only data rows, dst(g) = dst0[c] + t (the transformer's [frames, C] input).
+ */
+int vk_encoder_conv(const void *a, int64_t lda, const void *w, int32_t K, int32_t N, const float *bias,
+                    const int32_t *start, const int32_t *len, const int32_t *dst0, int32_t n_chunks, int64_t rows,
+                    int32_t compact, void *out, int64_t ldo, void *stream);
+
+/*
+ * Sliding-window self-attention with rotary embedding (viktor/encoder.py:71-84: Wqkv output
+ * .view(N, T, 3, H, D), apply_rope on q and k at positions 0 .. T - 1 of each chunk, flash_attn_func with
+ * window_size = (left, right) or SDPA with the band mask of encoder.py:64-69; koi_qkv_rotary + koi_vcs_attn,
+ * koi_tx.cpp:395-400). qkv [rows, ld] bf16 (q heads, k heads, v heads of 64), chunk c = rows cu[c] ..
+ * cu[c + 1] - 1; plan = n_blocks pairs (chunk, first query row of a 128-row block); cos_t / sin_t fp32
+ * [table_len, 32] (rope_tables); out [rows, ldo] bf16 (heads concatenated). D must be 64.
+ */
+int vk_window_attention(const void *qkv, int64_t ld, const int32_t *cu, const int32_t *plan, int32_t n_blocks,
+                        int32_t n_chunks, int32_t max_len, int32_t H, int32_t D, const float *cos_t,
+                        const float *sin_t, int32_t table_len, int32_t left, int32_t right, void *out, int64_t ldo,
+                        void *stream);
+
+/*
+ * DeepNorm residual + RMSNorm, in place (viktor/encoder.py:106-108: norm(sublayer(x) + alpha x);
+ * koi_rmsnorm_residual, koi_tx.cpp:404-405, 412-413): x = bf16(rmsnorm(bf16(bf16(y + bias) + bf16(alpha x))) * w) with
+ * y fp32 [n, d] (a product before rounding), bias fp32 [d] or NULL, w fp32 [d]; d must be 512.
+ */
+int vk_deepnorm_rmsnorm(const float *y, const float *bias, void *x, float alpha, const float *w, float eps, int64_t n,
+                        int32_t d, void *stream);
+
+/*
+ * Row-deterministic GEMM y = x w^T (x [M, K], w [N, K] bf16; K % 64 == 0): every row is computed by the same
+ * tile code whatever M is, so a chunk's frames do not depend on its batch (the koi VCS property checked at
+ * tests/gpu_check.py:103-105). epilogue 0: bf16 out; 1: fp32 out; 2: SwiGLU, w holds 2N rows and
+ * y[:, n] = bf16(bf16(silu(bf16(x w[n]))) * bf16(x w[N + n])) (koi_linear / koi_mm_swiglu, koi_tx.cpp:401-411).
+ */
+int vk_gemm_rows(const void *x, const void *w, void *y, int64_t M, int32_t N, int32_t K, int32_t epilogue,
+                 void *stream);
+
 #ifdef __cplusplus
 }
 #endif
