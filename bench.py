@@ -28,6 +28,10 @@ Extra objects on the JSON line:
                 decoder weights + clip + AdamW step; ms per micro-batch and the MFMA fraction of its
                 algorithmic flops (GEMMs 3 x 2 x weights per row, causal attention 3.5 x 1024 n (n + 1) per
                 layer and window: forward + the standard 2.5 x backward) against 2.5 PFLOP/s bf16.
+  encoder       the frames producer for one rollout's windows: 128 chunks of 12288 samples (64 windows x 2048
+                frames) through the SUP-shaped encoder (5 convolutions, 18 DeepNorm layers, d_model 512, window
+                (127, 128)) with seeded random weights; ms, chunks/s and the MFMA fraction of its algorithmic
+                flops (convolutions, 4 products per layer, window attention over the keys each frame sees).
 Usage: python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--no-cpu]
 """
 
@@ -47,6 +51,7 @@ METRIC = "GSPO rollout tokens/sec on 1 MI355X (512 seq x 1024 tok); % HBM roofli
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 UPDATE_MICRO, UPDATE_T = 32, 768
+ENC_CHUNKS = 128  # 64 windows x 2048 frames = 128 chunks of 12288 samples at stride 12
 PREFIXES, GROUP, P, NEW = 64, 8, 2048, 1024
 KV_ROW_BYTES = 2 * 2 * 64 * 2  # K + V, 2 KV heads, head_dim 64, bf16: one attended position of one layer
 
@@ -164,6 +169,34 @@ def reward_timing(tokenizer, reps=5):
             "includes": "token decode on the device + packing of the labels + the DP kernel"}
 
 
+def encoder_timing(reps=3):
+    """The encoder for one rollout's windows (see the module docstring): ms and MFMA fraction."""
+    from viktor_amd.encoder import DoradoEncoder
+    from viktor_amd.synthetic import SUP_ENCODER_CFG, encoder_state_dict, signal
+    dev = torch.device("cuda", 0)
+    enc = DoradoEncoder(SUP_ENCODER_CFG, dev).load_state_dict(encoder_state_dict(seed=12))
+    n_chunks, chunk = ENC_CHUNKS, SUP_ENCODER_CFG["basecaller"]["chunksize"]
+    sig = signal(n_chunks * chunk, seed=13).to(dev)
+    lens = [chunk] * n_chunks
+    for _ in range(2):
+        out = enc.forward_varlen(sig, lens)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for _ in range(reps):
+        out = enc.forward_varlen(sig, lens)
+    ev[1].record()
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / reps
+    flops = enc.flops_per_chunk(chunk) * n_chunks
+    tflops = flops / (ms / 1e3) / 1e12
+    assert torch.isfinite(out).all()
+    return {"chunks": n_chunks, "chunk_samples": chunk, "frames": int(out.shape[0]),
+            "layers": enc.depth, "ms": round(ms, 2), "chunks_per_s": round(n_chunks / (ms / 1e3), 1),
+            "samples_per_s": round(n_chunks * chunk / (ms / 1e3), 1), "alg_tflop": round(flops / 1e12, 3),
+            "achieved_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+
 def update_timing(steps=3, warmup=2):
     """One GSPO update micro-batch on the HIP training path (see the module docstring): times and flops."""
     from viktor_amd import train as TR
@@ -259,7 +292,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-batch", type=int, default=128)
-    ap.add_argument("--mode", choices=["rollout", "kernels"], default="rollout")
+    ap.add_argument("--mode", choices=["rollout", "kernels", "encoder"], default="rollout",
+                    help="kernels: decode-attention traffic probe; encoder: the encoder timing object alone")
     ap.add_argument("--group-size", type=int, default=GROUP, help="sequences sharing one prefix KV copy (1: none)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -268,6 +302,9 @@ def main():
         sys.exit(2)
     if args.mode == "kernels":
         kernels_mode(args.group_size)
+        return
+    if args.mode == "encoder":
+        print(json.dumps({"encoder": encoder_timing(reps=max(args.steps, 1))}), flush=True)
         return
     from viktor_amd import DecodeEngine
     from viktor_amd.synthetic import frames, uniforms
@@ -336,6 +373,9 @@ def main():
     del eng
     torch.cuda.empty_cache()
     update = update_timing()
+    log("encoder")
+    torch.cuda.empty_cache()
+    encoder = encoder_timing()
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
@@ -360,6 +400,7 @@ def main():
         "cpu_baseline": cpu,
         "gspo_reward": reward,
         "gspo_update": update,
+        "encoder": encoder,
     }
     print(json.dumps(line), flush=True)
 

@@ -373,7 +373,8 @@ int vk_deepnorm_rmsnorm(const float *y, const float *bias, void *x, float alpha,
                         int32_t d, void *stream);
 
 /*
- * Row-deterministic GEMM y = x w^T (x [M, K], w [N, K] bf16; K % 64 == 0): every row is computed by the same
+ * Row-deterministic GEMM y = x w^T (x [M, K], w [N, K] bf16; K % 64 == 0, N % 8 == 0, 16-byte aligned
+ * pointers): every row is computed by the same
  * tile code whatever M is, so a chunk's frames do not depend on its batch (the koi VCS property checked at
  * tests/gpu_check.py:103-105). epilogue 0: bf16 out; 1: fp32 out; 2: SwiGLU, w holds 2N rows and
  * y[:, n] = bf16(bf16(silu(bf16(x w[n]))) * bf16(x w[N + n])) (koi_linear / koi_mm_swiglu, koi_tx.cpp:401-411).

@@ -539,7 +539,7 @@ extern "C" int vk_deepnorm_rmsnorm(const float *y, const float *bias, void *x, f
 extern "C" int vk_gemm_rows(const void *x, const void *w, void *y, int64_t M, int32_t N, int32_t K, int32_t epilogue,
                             void *stream) {
   VK_CHECK_ARG(x && w && y, "gemm_rows: null pointer");
-  VK_CHECK_ARG(M >= 0 && N > 0 && N % 4 == 0 && K > 0 && K % 64 == 0, "gemm_rows: need N %% 4 == 0, K %% 64 == 0");
+  VK_CHECK_ARG(M >= 0 && N > 0 && N % 8 == 0 && K > 0 && K % 64 == 0, "gemm_rows: need N %% 8 == 0, K %% 64 == 0");
   VK_CHECK_ARG(epilogue >= 0 && epilogue <= 2, "gemm_rows: epilogue 0 (bf16), 1 (fp32) or 2 (SwiGLU)");
   VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w) && vk_aligned16(y), "gemm_rows: pointers must be 16-byte aligned");
   VK_CHECK_ARG(M < (int64_t(1) << 31) / 256 * 256, "gemm_rows: M too large");

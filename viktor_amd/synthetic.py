@@ -96,3 +96,53 @@ def scoring_inputs(B=512, lo=700, hi=1024, k=1, seed=0):
         idx = torch.randint(0, 4, (n_bases,), generator=g)
         seqs.append("".join("ACGT"[i] for i in idx.tolist()))
     return seqs, [True] * B
+
+
+# ---- encoder (frames producer) -----------------------------------------------------------------------
+# The layer shapes of Dorado's SUP v5 transformer encoder (5 convolutions of total stride 12, 18 DeepNorm
+# layers of d_model 512, 8 heads, SwiGLU 2048, attention window (127, 128)) in the config layout of
+# viktor/encoder.py:115-147; 12288-sample chunks.
+SUP_ENCODER_CFG = {
+    "model": {"encoder": {
+        "conv": {"sublayers": [
+            {"type": "convolution", "insize": 1, "size": 64, "winlen": 5, "stride": 1, "padding": 2, "bias": True},
+            {"type": "convolution", "insize": 64, "size": 64, "winlen": 5, "stride": 1, "padding": 2, "bias": True},
+            {"type": "convolution", "insize": 64, "size": 128, "winlen": 9, "stride": 3, "padding": 4, "bias": True},
+            {"type": "convolution", "insize": 128, "size": 128, "winlen": 9, "stride": 2, "padding": 4, "bias": True},
+            {"type": "convolution", "insize": 128, "size": 512, "winlen": 5, "stride": 2, "padding": 2, "bias": True},
+            {"type": "permute", "dims": [0, 2, 1]}]},
+        "transformer_encoder": {"depth": 18, "layer": {
+            "d_model": 512, "nhead": 8, "dim_feedforward": 2048, "deepnorm_alpha": 2.4494897,
+            "attn_window": [127, 128]}}}},
+    "basecaller": {"chunksize": 12288, "overlap": 600},
+    "standardisation": {"mean": 93.6, "stdev": 23.3},
+}
+
+
+def encoder_state_dict(cfg=SUP_ENCODER_CFG, seed=0):
+    """Seeded fp32 encoder weights under the reference module's names: conv / Linear weights
+    N(0, 1) / sqrt(fan_in), biases 0.1 N(0, 1), RMSNorm weights 1 + 0.1 N(0, 1)."""
+    g = _gen(seed)
+    sd = {}
+    convs = [l for l in cfg["model"]["encoder"]["conv"]["sublayers"] if l["type"] == "convolution"]
+    for i, l in enumerate(convs):
+        sd[f"conv.{i}.conv.weight"] = torch.randn(l["size"], l["insize"], l["winlen"], generator=g) / math.sqrt(
+            l["insize"] * l["winlen"])
+        sd[f"conv.{i}.conv.bias"] = 0.1 * torch.randn(l["size"], generator=g)
+    tx = cfg["model"]["encoder"]["transformer_encoder"]
+    C, F = tx["layer"]["d_model"], tx["layer"]["dim_feedforward"]
+    for j in range(tx["depth"]):
+        pre = f"transformer_encoder.{j}."
+        sd[pre + "self_attn.Wqkv.weight"] = torch.randn(3 * C, C, generator=g) / math.sqrt(C)
+        sd[pre + "self_attn.out_proj.weight"] = torch.randn(C, C, generator=g) / math.sqrt(C)
+        sd[pre + "self_attn.out_proj.bias"] = 0.1 * torch.randn(C, generator=g)
+        sd[pre + "ff.fc1.weight"] = torch.randn(2 * F, C, generator=g) / math.sqrt(C)
+        sd[pre + "ff.fc2.weight"] = torch.randn(C, F, generator=g) / math.sqrt(F)
+        sd[pre + "norm1.weight"] = 1 + 0.1 * torch.randn(C, generator=g)
+        sd[pre + "norm2.weight"] = 1 + 0.1 * torch.randn(C, generator=g)
+    return sd
+
+
+def signal(n_samples, seed=0):
+    """Standardised synthetic signal: N(0, 1) fp32 samples."""
+    return torch.randn(int(n_samples), generator=_gen(seed))
