@@ -329,16 +329,17 @@ int vk_strict_identity(const uint8_t *calls, const int64_t *call_off, const int3
  * Padded chunk layout of a convolution's activations: channels-last [rows, C] bf16, chunk c's data rows at
  * [start[c], start[c] + len[c]), zero margin rows between chunks; the input row of output row g is
  * stride * g - pad for every row (margins scale by the strides), so the zero margins are each chunk's
- * Conv1d padding.
+ * Conv1d padding. hint[i] = the chunk of output row 256 i (the last c with start[c] <= 256 i, else 0),
+ * ceil(rows / 256) entries.
  *
  * First convolution (C_in = 1; viktor/encoder.py:43-49 and the first koi_vcs_tx_cnn call, koi_tx.cpp:296-315):
  * out[g, co] = bf16(silu(bf16(b[co] + sum_k w[co, k] signal[sig_off[c] + stride t - pad + k]))) for data row
  * g = start[c] + t (samples outside the chunk read as 0), zeros for margin rows; signal, w [C, winlen], b fp32;
- * out [rows, C] bf16 (C % 8 == 0, winlen <= 32).
+ * out [rows, C] bf16 (C % 8 == 0, C <= 512, winlen <= 32, C * winlen <= 4096).
  */
-int vk_encoder_conv_first(const float *signal, const int64_t *sig_off, const int32_t *start, const int32_t *len,
-                          int32_t n_chunks, int64_t rows, const float *w, const float *b, int32_t C, int32_t winlen,
-                          int32_t stride, int32_t pad, void *out, void *stream);
+int vk_encoder_conv_first(const float *signal, const int64_t *sig_off, const int32_t *start, const int32_t *hint,
+                          const int32_t *len, int32_t n_chunks, int64_t rows, const float *w, const float *b, int32_t C,
+                          int32_t winlen, int32_t stride, int32_t pad, void *out, void *stream);
 
 /*
  * Later convolutions (viktor/encoder.py:43-49; koi_vcs_tx_cnn, koi_tx.cpp:296-315) as one strided GEMM:
@@ -348,8 +349,8 @@ int vk_encoder_conv_first(const float *signal, const int64_t *sig_off, const int
  * compact = 1: only data rows, dst(g) = dst0[c] + t (the transformer's [frames, C] input).
  */
 int vk_encoder_conv(const void *a, int64_t lda, const void *w, int32_t K, int32_t N, const float *bias,
-                    const int32_t *start, const int32_t *len, const int32_t *dst0, int32_t n_chunks, int64_t rows,
-                    int32_t compact, void *out, int64_t ldo, void *stream);
+                    const int32_t *start, const int32_t *hint, const int32_t *len, const int32_t *dst0,
+                    int32_t n_chunks, int64_t rows, int32_t compact, void *out, int64_t ldo, void *stream);
 
 /*
  * Sliding-window self-attention with rotary embedding (viktor/encoder.py:71-84: Wqkv output

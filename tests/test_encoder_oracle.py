@@ -148,8 +148,13 @@ def _emulate_conv_stack(convs, params, sig, lens):
         w = params[f"conv.{i}.conv.weight"].double()
         b = params[f"conv.{i}.conv.bias"].double()
         out = torch.zeros(rows + 2 * _GUARD, l["size"], dtype=torch.float64)
+        hint = lay["hint"].numpy()
         for g in range(rows):
             c = max(int(np.searchsorted(start, g, side="right")) - 1, 0)
+            ch = int(hint[g >> 8])  # the kernels' lookup: walk forward from the 256-row hint
+            while ch + 1 < n and start[ch + 1] <= g:
+                ch += 1
+            assert ch == c
             t = g - start[c]
             if not (0 <= t < ln[c]):
                 continue

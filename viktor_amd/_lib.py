@@ -59,8 +59,8 @@ SIGNATURES = {
     "vk_grad_norm_clip": [_P, _I64, _F, _P, _I32, _P, _P],
     "vk_adamw": [_P, _P, _P, _P, _I64, _P, _F, _F, _F, _F, _F, _I64, _P],
     "vk_strict_identity": [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F, _P, _P, _P, _P],
-    "vk_encoder_conv_first": [_P, _P, _P, _P, _I32, _I64, _P, _P, _I32, _I32, _I32, _I32, _P, _P],
-    "vk_encoder_conv": [_P, _I64, _P, _I32, _I32, _P, _P, _P, _P, _I32, _I64, _I32, _P, _I64, _P],
+    "vk_encoder_conv_first": [_P, _P, _P, _P, _P, _I32, _I64, _P, _P, _I32, _I32, _I32, _I32, _P, _P],
+    "vk_encoder_conv": [_P, _I64, _P, _I32, _I32, _P, _P, _P, _P, _P, _I32, _I64, _I32, _P, _I64, _P],
     "vk_window_attention": [_P, _I64, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _I32, _I32, _I32, _P, _I64, _P],
     "vk_deepnorm_rmsnorm": [_P, _P, _P, _F, _P, _F, _I64, _I32, _P],
     "vk_gemm_rows": [_P, _P, _P, _I64, _I32, _I32, _I32, _P],

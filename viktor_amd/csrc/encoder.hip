@@ -19,17 +19,14 @@
 
 namespace vk {
 
-// Chunk c with start[c] <= g (start ascending; rows before start[0] map to chunk 0).
-__device__ __forceinline__ int find_chunk(const int32_t *__restrict__ start, int n, int64_t g) {
-  int lo = 0, hi = n - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (start[mid] <= g)
-      lo = mid;
-    else
-      hi = mid - 1;
-  }
-  return lo;
+// Chunk c with start[c] <= g (start ascending; rows before start[0] map to chunk 0). hint[g >> 8] is the
+// chunk of row 256 * (g >> 8), so the walk from it is short (a 256-row block spans few chunks).
+constexpr int CHUNK_HINT_SHIFT = 8;
+__device__ __forceinline__ int find_chunk(const int32_t *__restrict__ start, const int32_t *__restrict__ hint, int n,
+                                          int64_t g) {
+  int c = hint[g >> CHUNK_HINT_SHIFT];
+  while (c + 1 < n && start[c + 1] <= g) ++c;
+  return c;
 }
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
@@ -37,19 +34,27 @@ __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)
 // ---- first convolution (C_in = 1): fp32 signal and weights, out = bf16(silu(bf16(conv + b))) ----------
 constexpr int CF_MAX_WIN = 32;
 
+constexpr int CF_MAX_W = 4096;  // C * winlen (weights staged in LDS)
+
 __global__ __launch_bounds__(256) void conv_first_kernel(const float *__restrict__ sig,
                                                          const int64_t *__restrict__ sig_off,
                                                          const int32_t *__restrict__ start,
+                                                         const int32_t *__restrict__ hint,
                                                          const int32_t *__restrict__ len, int n_chunks, int64_t rows,
                                                          const float *__restrict__ w, const float *__restrict__ b,
                                                          int C, int winlen, int stride, int pad,
                                                          bf16_t *__restrict__ out) {
+  __shared__ float ws[CF_MAX_W];
+  __shared__ float bs[512];
+  for (int i = threadIdx.x; i < C * winlen; i += 256) ws[i] = w[i];
+  for (int i = threadIdx.x; i < C; i += 256) bs[i] = b[i];
+  __syncthreads();
   const int groups = C >> 3;  // 8 output channels per thread
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int64_t g = idx / groups;
   const int cg = static_cast<int>(idx - g * groups);
   if (g >= rows) return;
-  const int c = find_chunk(start, n_chunks, g);
+  const int c = find_chunk(start, hint, n_chunks, g);
   const int64_t t = g - start[c];
   u32x4 res = {0u, 0u, 0u, 0u};
   if (t >= 0 && t < len[c]) {
@@ -65,8 +70,8 @@ __global__ __launch_bounds__(256) void conv_first_kernel(const float *__restrict
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int co = cg * 8 + e;
-      float acc = b[co];
-      const float *wr = w + co * winlen;
+      float acc = bs[co];
+      const float *wr = ws + co * winlen;
 #pragma unroll
       for (int k = 0; k < CF_MAX_WIN; ++k)
         if (k < winlen) acc = fmaf(wr[k], x[k], acc);
@@ -89,6 +94,7 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(const bf16_t *__restrict
                                                         const bf16_t *__restrict__ w, int K, int N,
                                                         const float *__restrict__ bias,
                                                         const int32_t *__restrict__ start,
+                                                        const int32_t *__restrict__ hint,
                                                         const int32_t *__restrict__ len,
                                                         const int32_t *__restrict__ dst0, int n_chunks, int64_t rows,
                                                         int compact, bf16_t *__restrict__ out, int64_t ldo) {
@@ -170,7 +176,7 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(const bf16_t *__restrict
   for (int j = 0; j < 2; ++j) {
     const int64_t g = m0 + wid * 32 + 16 * j + fr;
     if (g >= rows) continue;
-    const int c = find_chunk(start, n_chunks, g);
+    const int c = find_chunk(start, hint, n_chunks, g);
     const int64_t t = g - start[c];
     const bool data = t >= 0 && t < len[c];
     if (compact && !data) continue;
@@ -196,17 +202,19 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(const bf16_t *__restrict
 // buffered in LDS; each tile serves the 128 queries. Q and K are rotated in fp32 and rounded to bf16 as
 // apply_rope's output (viktor/encoder.py:36-40, 74-75): Q in registers (both halves of a rotation pair sit
 // in the same lane), K by the thread that stages the key row. Products transposed as in the decoder's
-// varlen kernel: S^T = K Q^T leaves each lane the scores of one query row, O^T = V^T P^T consumes them.
+// varlen kernel: S^T = K Q^T leaves each lane the scores of one query row, O^T = V^T P^T consumes them; V is
+// staged transposed so that operand is two 8-byte LDS reads per lane.
 constexpr int WA_D = 64, WA_Q = 128, WA_KT = 64, WA_PITCH = 72;
+constexpr int WA_VTP = 68;  // keys per row of the transposed V tile (136 B: 8-byte operand reads conflict-free)
 
-__global__ __launch_bounds__(256) void window_attn_kernel(const bf16_t *__restrict__ qkv, int64_t ld,
+__global__ __launch_bounds__(256, 4) void window_attn_kernel(const bf16_t *__restrict__ qkv, int64_t ld,
                                                           const int32_t *__restrict__ cu,
                                                           const int32_t *__restrict__ plan, int n_blocks, int n_chunks,
                                                           int H, const float *__restrict__ cos_t,
                                                           const float *__restrict__ sin_t, int left, int right,
                                                           float scale_log2, bf16_t *__restrict__ out, int64_t ldo) {
   __shared__ __attribute__((aligned(16))) bf16_t Ks[2][WA_KT * WA_PITCH];
-  __shared__ __attribute__((aligned(16))) bf16_t Vs[2][WA_KT * WA_PITCH];
+  __shared__ __attribute__((aligned(16))) bf16_t Vt[2][WA_D * WA_VTP];  // V^T: [d][key]
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int col = lane & 15, g = lane >> 4;
 
@@ -278,7 +286,7 @@ __global__ __launch_bounds__(256) void window_attn_kernel(const bf16_t *__restri
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int c = 0; c < 2; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f}, alpha_q[2];
 
   // tile staging: thread -> key row lrow, d chunks lc and lc + 4 (a rotation pair) of K and of V
   const int lrow = tid >> 2, lc = tid & 3;
@@ -317,8 +325,14 @@ __global__ __launch_bounds__(256) void window_attn_kernel(const bf16_t *__restri
     }
     *reinterpret_cast<u32x4 *>(&Ks[buf][lrow * WA_PITCH + lc * 8]) = k1;
     *reinterpret_cast<u32x4 *>(&Ks[buf][lrow * WA_PITCH + lc * 8 + 32]) = k2;
-    *reinterpret_cast<u32x4 *>(&Vs[buf][lrow * WA_PITCH + lc * 8]) = rv0;
-    *reinterpret_cast<u32x4 *>(&Vs[buf][lrow * WA_PITCH + lc * 8 + 32]) = rv1;
+    // V transposed, so the O^T = V^T P^T operand is two 8-byte reads per lane
+#pragma unroll
+    for (int wv = 0; wv < 4; ++wv) {
+      Vt[buf][(lc * 8 + 2 * wv) * WA_VTP + lrow] = static_cast<bf16_t>(rv0[wv] & 0xffffu);
+      Vt[buf][(lc * 8 + 2 * wv + 1) * WA_VTP + lrow] = static_cast<bf16_t>(rv0[wv] >> 16);
+      Vt[buf][(32 + lc * 8 + 2 * wv) * WA_VTP + lrow] = static_cast<bf16_t>(rv1[wv] & 0xffffu);
+      Vt[buf][(32 + lc * 8 + 2 * wv + 1) * WA_VTP + lrow] = static_cast<bf16_t>(rv1[wv] >> 16);
+    }
   };
 
   load_tile(0);
@@ -332,7 +346,7 @@ __global__ __launch_bounds__(256) void window_attn_kernel(const bf16_t *__restri
       const int kb0 = kt0 + t * WA_KT + 32 * ks;
       if (!active || kb0 > whi || kb0 + 31 < wlo) continue;  // wave-uniform: no row of this wave sees these keys
       const bf16_t *kt = &Ks[buf][32 * ks * WA_PITCH];
-      const bf16_t *vt = &Vs[buf][32 * ks * WA_PITCH];
+      const bf16_t *vt = &Vt[buf][32 * ks];
       f32x4 st[2][2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
@@ -351,47 +365,63 @@ __global__ __launch_bounds__(256) void window_attn_kernel(const bf16_t *__restri
       // no mask needed when every key of the half is inside every row's window and inside the chunk
       const bool need_mask = kb0 < r_last - left || kb0 + 31 > r_first + right || kb0 + 31 >= T;
       bf16x8 pf[2];
+      bool grew = false;
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
+        // branch-free softmax step: the window test uses bitwise ands under one wave-uniform branch (a
+        // short-circuit test per score compiled to a divergent branch per score)
         float sv[8];
-        float mx = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = kb0 + 16 * kb + 4 * g + i;
-            const bool ok = !need_mask || (key < T && key >= qpos[qb] - left && key <= qpos[qb] + right);
-            const float s = ok ? st[kb][qb][i] * scale_log2 : -INFINITY;
-            sv[kb * 4 + i] = s;
-            mx = fmaxf(mx, s);
-          }
+          for (int i = 0; i < 4; ++i) sv[kb * 4 + i] = st[kb][qb][i] * scale_log2;
+        if (need_mask) {
+          const int lo_k = qpos[qb] - left, hi_k = min(qpos[qb] + right, T - 1);
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int key = kb0 + 16 * kb + 4 * g + i;
+              sv[kb * 4 + i] = ((key >= lo_k) & (key <= hi_k)) ? sv[kb * 4 + i] : -INFINITY;
+            }
+        }
+        float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float m_new = fmaxf(m_run[qb], mx);
         // a row may see no key of its first halves (window start): keep exp2 arguments finite
         const float m_sub = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = exp2f(m_run[qb] - m_sub);
-        float ps = 0.f;
+        // exponents are <= 0: the bare v_exp_f32 (no range reduction needed)
+        float e[8], ps = 0.f;
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
-          const float pv = exp2f(sv[jj] - m_sub);
-          ps += pv;
-          pf[qb][jj] = __builtin_bit_cast(__bf16, f2bf(pv));
+          e[jj] = __builtin_amdgcn_exp2f(sv[jj] - m_sub);
+          ps += e[jj];
         }
+        pf[qb] = __builtin_bit_cast(bf16x8, u32x4{pack_bf(e[0], e[1]), pack_bf(e[2], e[3]), pack_bf(e[4], e[5]),
+                                                   pack_bf(e[6], e[7])});
+        // the running max moved: rescale this row's sum (and, below, its output); else alpha is exactly 1
+        const bool moved = m_new != m_run[qb];
+        const float alpha = moved ? __builtin_amdgcn_exp2f(m_run[qb] - m_sub) : 1.0f;
+        alpha_q[qb] = alpha;
+        grew |= moved;
         l_run[qb] = l_run[qb] * alpha + ps;
         m_run[qb] = m_new;
+      }
+      // rescale the outputs only when some row of the wave saw a new maximum (a multiply by 1 otherwise)
+      if (__builtin_amdgcn_ballot_w64(grew) != 0) {
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) acc[dt][qb] *= alpha;
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) acc[dt][qb] *= alpha_q[qb];
       }
       // O^T += V^T P^T (key order {4g..4g+3, 16+4g..16+4g+3} in both operands)
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        bf16x8 va;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int kl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
-          va[jj] = __builtin_bit_cast(__bf16, vt[kl * WA_PITCH + 16 * dt + col]);
-        }
+        const bf16_t *vr = vt + (16 * dt + col) * WA_VTP;
+        const u32x2 lo = *reinterpret_cast<const u32x2 *>(vr + 4 * g);
+        const u32x2 hi = *reinterpret_cast<const u32x2 *>(vr + 16 + 4 * g);
+        const bf16x8 va = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) acc[dt][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[qb], acc[dt][qb], 0, 0, 0);
       }
@@ -468,25 +498,25 @@ int gemm_big(const bf16_t *x, const bf16_t *w, void *y, int64_t M, int N, int K,
 using namespace vk;
 
 extern "C" int vk_encoder_conv_first(const float *signal, const int64_t *sig_off, const int32_t *start,
-                                     const int32_t *len, int32_t n_chunks, int64_t rows, const float *w,
-                                     const float *b, int32_t C, int32_t winlen, int32_t stride, int32_t pad,
-                                     void *out, void *stream) {
-  VK_CHECK_ARG(signal && sig_off && start && len && w && b && out, "encoder_conv_first: null pointer");
-  VK_CHECK_ARG(n_chunks > 0 && rows >= 0 && C > 0 && C % 8 == 0 && winlen > 0 && winlen <= CF_MAX_WIN &&
-                   stride > 0 && pad >= 0,
+                                     const int32_t *hint, const int32_t *len, int32_t n_chunks, int64_t rows,
+                                     const float *w, const float *b, int32_t C, int32_t winlen, int32_t stride,
+                                     int32_t pad, void *out, void *stream) {
+  VK_CHECK_ARG(signal && sig_off && start && hint && len && w && b && out, "encoder_conv_first: null pointer");
+  VK_CHECK_ARG(n_chunks > 0 && rows >= 0 && C > 0 && C % 8 == 0 && C <= 512 && winlen > 0 &&
+                   winlen <= CF_MAX_WIN && C * winlen <= CF_MAX_W && stride > 0 && pad >= 0,
                "encoder_conv_first: bad sizes (C %d winlen %d stride %d pad %d)", C, winlen, stride, pad);
   VK_CHECK_ARG(vk_aligned16(out), "encoder_conv_first: out must be 16-byte aligned");
   if (rows == 0) return VK_OK;
   const int64_t threads = rows * (C / 8);
   conv_first_kernel<<<static_cast<unsigned>((threads + 255) / 256), 256, 0, VK_STREAM(stream)>>>(
-      signal, sig_off, start, len, n_chunks, rows, w, b, C, winlen, stride, pad, static_cast<bf16_t *>(out));
+      signal, sig_off, start, hint, len, n_chunks, rows, w, b, C, winlen, stride, pad, static_cast<bf16_t *>(out));
   return launch_status("encoder_conv_first");
 }
 
 extern "C" int vk_encoder_conv(const void *a, int64_t lda, const void *w, int32_t K, int32_t N, const float *bias,
-                               const int32_t *start, const int32_t *len, const int32_t *dst0, int32_t n_chunks,
-                               int64_t rows, int32_t compact, void *out, int64_t ldo, void *stream) {
-  VK_CHECK_ARG(a && w && bias && start && len && out && (!compact || dst0), "encoder_conv: null pointer");
+                               const int32_t *start, const int32_t *hint, const int32_t *len, const int32_t *dst0,
+                               int32_t n_chunks, int64_t rows, int32_t compact, void *out, int64_t ldo, void *stream) {
+  VK_CHECK_ARG(a && w && bias && start && hint && len && out && (!compact || dst0), "encoder_conv: null pointer");
   VK_CHECK_ARG(n_chunks > 0 && rows >= 0 && K > 0 && K % CG_BK == 0 && N > 0 && N % CG_BN == 0 && lda % 8 == 0 &&
                    ldo >= N && ldo % 4 == 0,
                "encoder_conv: need K %% 32 == 0, N %% 64 == 0, lda %% 8 == 0 (K %d N %d lda %lld)", K, N,
@@ -495,7 +525,7 @@ extern "C" int vk_encoder_conv(const void *a, int64_t lda, const void *w, int32_
   if (rows == 0) return VK_OK;
   const dim3 grid(static_cast<unsigned>((rows + CG_BM - 1) / CG_BM), static_cast<unsigned>(N / CG_BN));
   conv_gemm_kernel<<<grid, 256, 0, VK_STREAM(stream)>>>(static_cast<const bf16_t *>(a), lda,
-                                                         static_cast<const bf16_t *>(w), K, N, bias, start, len, dst0,
+                                                         static_cast<const bf16_t *>(w), K, N, bias, start, hint, len, dst0,
                                                          n_chunks, rows, compact, static_cast<bf16_t *>(out), ldo);
   return launch_status("encoder_conv");
 }

@@ -87,9 +87,12 @@ class _ConvPlan:
             rows = int(ol.sum()) + (n + 1) * M
             if rows >= 2 ** 31:
                 raise HipLibraryError("encoder: batch too large for 32-bit row indices")
+            # chunk of every 256th row (the kernels walk forward from it)
+            hint = np.maximum(np.searchsorted(starts, np.arange(0, rows, 256), side="right") - 1, 0)
             self.layers.append({
                 "rows": rows,
                 "start": torch.from_numpy(starts.astype(np.int32)).to(device),
+                "hint": torch.from_numpy(hint.astype(np.int32)).to(device),
                 "len": torch.from_numpy(ol.astype(np.int32)).to(device),
             })
         frames = out_lens[-1]
@@ -144,8 +147,10 @@ class DoradoEncoder:
     def _check_shapes(self):
         c = self.convs
         msgs = []
-        if not c or c[0]["insize"] != 1 or c[0]["winlen"] > 32 or c[0]["size"] % 8:
-            msgs.append("the first convolution must read 1 channel with winlen <= 32 and a multiple of 8 outputs")
+        if (not c or c[0]["insize"] != 1 or c[0]["winlen"] > 32 or c[0]["size"] % 8 or c[0]["size"] > 512
+                or c[0]["size"] * c[0]["winlen"] > 4096):
+            msgs.append("the first convolution must read 1 channel with winlen <= 32 and a multiple of 8 outputs "
+                        "(at most 512, size * winlen <= 4096)")
         for i, l in enumerate(c):
             if l["winlen"] != 2 * l["padding"] + 1:
                 msgs.append(f"conv {i}: winlen must be 2 * padding + 1")
@@ -277,7 +282,8 @@ class DoradoEncoder:
                 buf[:_GUARD].zero_()
                 buf[_GUARD + lay["rows"]:].zero_()
                 w, b = W[0]
-                call("vk_encoder_conv_first", ptr(sig), ptr(plan.sig_off), ptr(lay["start"]), ptr(lay["len"]), n,
+                call("vk_encoder_conv_first", ptr(sig), ptr(plan.sig_off), ptr(lay["start"]), ptr(lay["hint"]),
+                     ptr(lay["len"]), n,
                      lay["rows"], ptr(w), ptr(b), l["size"], l["winlen"], l["stride"], l["padding"],
                      ptr(buf[_GUARD:]), st)
                 prev = buf
@@ -287,13 +293,15 @@ class DoradoEncoder:
             a = prev[_GUARD - p:]  # row -pad of the input layout
             if last:
                 call("vk_encoder_conv", ptr(a), s * cin, ptr(w), l["winlen"] * cin, l["size"], ptr(b),
-                     ptr(lay["start"]), ptr(lay["len"]), ptr(plan.dst0), n, lay["rows"], 1, ptr(x), l["size"], st)
+                     ptr(lay["start"]), ptr(lay["hint"]), ptr(lay["len"]), ptr(plan.dst0), n, lay["rows"], 1, ptr(x),
+                     l["size"], st)
             else:
                 buf = torch.empty(lay["rows"] + 2 * _GUARD, l["size"], dtype=torch.bfloat16, device=dev)
                 buf[:_GUARD].zero_()
                 buf[_GUARD + lay["rows"]:].zero_()
                 call("vk_encoder_conv", ptr(a), s * cin, ptr(w), l["winlen"] * cin, l["size"], ptr(b),
-                     ptr(lay["start"]), ptr(lay["len"]), ptr(None), n, lay["rows"], 0, ptr(buf[_GUARD:]),
+                     ptr(lay["start"]), ptr(lay["hint"]), ptr(lay["len"]), ptr(None), n, lay["rows"], 0,
+                     ptr(buf[_GUARD:]),
                      l["size"], st)
                 prev = buf
         return x
