@@ -124,37 +124,53 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
         }
       }
       const bool need_mask = kbase + 31 >= klen || (causal && kbase + 31 > qshift + r_first);
+      // branch-free softmax step: the mask is a compare per score under one wave-uniform branch (a
+      // short-circuit test per score compiles to a divergent branch per score)
       bf16x8 pf[2];
+      float alpha_q[2];
+      bool grew = false;
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         float sv[8];
-        float mx = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = kbase + 16 * kb + 4 * g + i;
-            const bool ok = !need_mask || (key < klen && (!causal || key <= qpos[qb]));
-            const float s = ok ? st[kb][qb][i] * scale_log2 : -INFINITY;
-            sv[kb * 4 + i] = s;
-            mx = fmaxf(mx, s);
-          }
+          for (int i = 0; i < 4; ++i) sv[kb * 4 + i] = st[kb][qb][i] * scale_log2;
+        if (need_mask) {
+          const int hi_k = causal ? min(qpos[qb], klen - 1) : klen - 1;  // last key this row sees
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              sv[kb * 4 + i] = kbase + 16 * kb + 4 * g + i <= hi_k ? sv[kb * 4 + i] : -INFINITY;
+        }
+        float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        // m_new is finite: tile 0 always holds key 0, visible to every query
+        // m_new is finite: tile 0 always holds key 0, visible to every query; exponents are <= 0, so the
+        // bare v_exp_f32 (no range reduction) serves
         const float m_new = fmaxf(m_run[qb], mx);
-        const float alpha = exp2f(m_run[qb] - m_new);
-        float ps = 0.f;
+        float e[8], ps = 0.f;
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
-          const float p = exp2f(sv[jj] - m_new);
-          ps += p;
-          pf[qb][jj] = __builtin_bit_cast(__bf16, f2bf(p));
+          e[jj] = __builtin_amdgcn_exp2f(sv[jj] - m_new);
+          ps += e[jj];
         }
+        pf[qb] = __builtin_bit_cast(bf16x8, u32x4{pack_bf(e[0], e[1]), pack_bf(e[2], e[3]), pack_bf(e[4], e[5]),
+                                                   pack_bf(e[6], e[7])});
+        // the running max moved: rescale the row's sum (and, below, its output); else alpha is exactly 1
+        const bool moved = m_new != m_run[qb];
+        const float alpha = moved ? __builtin_amdgcn_exp2f(m_run[qb] - m_new) : 1.0f;
+        alpha_q[qb] = alpha;
+        grew |= moved;
         l_run[qb] = l_run[qb] * alpha + ps;
         m_run[qb] = m_new;
+      }
+      if (__builtin_amdgcn_ballot_w64(grew) != 0) {
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) acc[dt][qb] *= alpha;
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) acc[dt][qb] *= alpha_q[qb];
       }
       // O^T += V^T P^T (key order {4g..4g+3, 16+4g..16+4g+3} in both operands)
 #pragma unroll
