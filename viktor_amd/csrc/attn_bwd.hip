@@ -148,18 +148,24 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
         }
       }
       // dS^T in the accumulator layout (key 16 kb + 4 g + i, query col), as the B operand of K^T dS^T
+      // branch-free: a masked score's exponent is -inf (exp2 -> 0); exponents are <= 0 (the row's
+      // log-sum-exp bounds every score), so the bare v_exp_f32 serves
       bf16x8 dsf[2];
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+      for (int qb = 0; qb < 2; ++qb) {
+        const int hi_k = min(qpos[qb], len - 1);
+        float d[8];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int key = kbase + 16 * kb + 4 * g + i;
-            const bool ok = key < len && key <= qpos[qb];
-            const float p = ok ? exp2f(st[kb][qb][i] * scale_log2 - lse2[qb]) : 0.f;
-            dsf[qb][kb * 4 + i] = static_cast<__bf16>(p * (dpt[kb][qb][i] - dr[qb]));
+            const float x = key <= hi_k ? st[kb][qb][i] * scale_log2 - lse2[qb] : -INFINITY;
+            d[kb * 4 + i] = __builtin_amdgcn_exp2f(x) * (dpt[kb][qb][i] - dr[qb]);
           }
+        dsf[qb] = __builtin_bit_cast(bf16x8, u32x4{pack_bf(d[0], d[1]), pack_bf(d[2], d[3]), pack_bf(d[4], d[5]),
+                                                    pack_bf(d[6], d[7])});
+      }
       // dQ^T += K^T dS^T (key order {4g..4g+3, 16+4g..16+4g+3} in both operands)
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
@@ -292,18 +298,25 @@ __global__ __launch_bounds__(AB_KW * 64) void attn_bwd_dkdv_kernel(
           dpt[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(oa, bv[dc], dpt[rb], 0, 0, 0);
         }
       }
-      bf16x8 pf, dsf;  // row order {4g..4g+3, 16+4g..16+4g+3}
+      // row order {4g..4g+3, 16+4g..16+4g+3}; branch-free: a masked entry's exponent is -inf (exp2 -> 0),
+      // exponents are <= 0 (bare v_exp_f32)
+      float pv[8], dv8[8];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int rr = 16 * rb + 4 * g + i;
           const int r = rs + rr;
-          const bool ok = r < len && key <= r && key < len;
-          const float p = ok ? exp2f(st[rb][i] * scale_log2 - Ls[hh * 32 + rr]) : 0.f;
-          pf[rb * 4 + i] = static_cast<__bf16>(p);
-          dsf[rb * 4 + i] = static_cast<__bf16>(p * (dpt[rb][i] - Ds[hh * 32 + rr]));
+          const bool ok = (r < len) & (key <= r) & (key < len);
+          const float x = ok ? st[rb][i] * scale_log2 - Ls[hh * 32 + rr] : -INFINITY;
+          const float p = __builtin_amdgcn_exp2f(x);
+          pv[rb * 4 + i] = p;
+          dv8[rb * 4 + i] = p * (dpt[rb][i] - Ds[hh * 32 + rr]);
         }
+      const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pack_bf(pv[0], pv[1]), pack_bf(pv[2], pv[3]),
+                                                          pack_bf(pv[4], pv[5]), pack_bf(pv[6], pv[7])});
+      const bf16x8 dsf = __builtin_bit_cast(bf16x8, u32x4{pack_bf(dv8[0], dv8[1]), pack_bf(dv8[2], dv8[3]),
+                                                           pack_bf(dv8[4], dv8[5]), pack_bf(dv8[6], dv8[7])});
       // dV^T += dO^T P, dK^T += Q^T dS (A = dO^T / Q^T from the transposed copies: lane col -> d, rows
       // {4g..4g+3} and {16+4g..16+4g+3} as four 32-bit reads, the row order of P / dS above)
 #pragma unroll
