@@ -140,9 +140,20 @@ def test_linear_swiglu(M):
     # three rounding points (gate, silu, product): a one-ulp flip upstream can reach ~3 ulps of the output
     ok, err = bf_close(y, ref, ulps=4, atol=1e-4)
     assert ok, err
-    # the standalone SwiGLU op on the unfused GEMM output agrees
+    # the standalone SwiGLU op on the unfused GEMM output agrees (8 columns per thread: F % 8 == 0)
     gu = ops.linear(to_dev(x, BF), to_dev(w, BF))
     assert bf_close(ops.swiglu(gu), ref, ulps=4, atol=1e-4)[0]
+
+
+def test_swiglu_op_widths():
+    """The standalone SwiGLU op, vectorised (F % 8 == 0) and per element (other F), equals the formula on
+    the same bf16 inputs bit for bit."""
+    g = gen(7)
+    for Fd in (8, 1536, 12, 5):
+        gu = R.bf(3 * torch.randn(37, 2 * Fd, generator=g))
+        ref = R.swiglu_fused(gu[:, :Fd], gu[:, Fd:])
+        got = ops.swiglu(to_dev(gu, BF)).float().cpu()
+        assert bf_close(got, ref, ulps=1, atol=1e-6)[0], Fd
 
 
 def _sdpa_ref(q, k, v, lens):

@@ -235,10 +235,35 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const bf16_t *__restrict__ 
   out[i] = f2bf(act * u);
 }
 
+// 8 columns per thread (16-byte loads of gate and up, one 16-byte store) when F % 8 == 0
+__global__ __launch_bounds__(256) void swiglu8_kernel(const bf16_t *__restrict__ gu, bf16_t *__restrict__ out,
+                                                      int64_t total8, int F8) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total8) return;
+  const int64_t row = i / F8;
+  const int c8 = static_cast<int>(i - row * F8);
+  const u32x4 g = *reinterpret_cast<const u32x4 *>(gu + (row * 2 * F8 + c8) * 8);
+  const u32x4 u = *reinterpret_cast<const u32x4 *>(gu + (row * 2 * F8 + F8 + c8) * 8);
+  u32x4 o;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float g0 = lo_bf(g[w]), g1 = hi_bf(g[w]);
+    const float a0 = round_bf(g0 / (1.0f + __expf(-g0))), a1 = round_bf(g1 / (1.0f + __expf(-g1)));
+    o[w] = pack_bf(a0 * lo_bf(u[w]), a1 * hi_bf(u[w]));
+  }
+  *reinterpret_cast<u32x4 *>(out + i * 8) = o;
+}
+
 extern "C" int vk_swiglu(const void *gu, void *out, int64_t n, int32_t f, void *stream) {
   VK_CHECK_ARG(gu && out && n >= 0 && f > 0, "swiglu: bad arguments");
   const int64_t total = n * f;
   if (total == 0) return VK_OK;
+  if (f % 8 == 0 && vk_aligned16(gu) && vk_aligned16(out)) {
+    const int64_t total8 = total / 8;
+    swiglu8_kernel<<<static_cast<unsigned>((total8 + 255) / 256), 256, 0, VK_STREAM(stream)>>>(
+        static_cast<const bf16_t *>(gu), static_cast<bf16_t *>(out), total8, f / 8);
+    return launch_status("swiglu");
+  }
   swiglu_kernel<<<static_cast<unsigned>((total + 255) / 256), 256, 0, VK_STREAM(stream)>>>(
       static_cast<const bf16_t *>(gu), static_cast<bf16_t *>(out), total, f);
   return launch_status("swiglu");
