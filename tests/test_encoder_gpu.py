@@ -176,3 +176,23 @@ def test_unsupported_shapes_raise():
     cfg, params, enc = _enc(0)
     with pytest.raises(HipLibraryError):
         enc.forward_varlen(torch.zeros(100, device=DEV), [100])  # not a multiple of the stride
+
+
+def test_basecaller_encode_windows():
+    """Basecaller.encode (viktor/model.py:89-117): full windows whole, short windows at their padded length with
+    ceil(valid / stride) frames kept and the rest zero -- each window equal to encoding it alone."""
+    from viktor_amd.model import Basecaller
+    from viktor_amd.tokenizer import KmerTokenizer
+    cfg, params, enc = _enc(1, seed=11)
+    model = Basecaller(enc, KmerTokenizer(1))
+    S = 3072
+    valid = [3072, 1000, 3072, 20]
+    sig = torch.randn(len(valid), 1, S, generator=torch.Generator().manual_seed(12)).to(DEV)
+    frames, plens = model.encode(sig, torch.tensor(valid))
+    assert frames.shape == (4, S // 12, 512) and plens.tolist() == [256, 84, 256, 2]
+    for b, v in enumerate(valid):
+        n = S if v == S else -(-v // 768) * 768
+        alone = enc.forward_varlen(sig[b, 0, :n].contiguous(), [n])
+        k = int(plens[b])
+        assert torch.equal(frames[b, :k], alone[:k])
+        assert not frames[b, k:].any()

@@ -1,7 +1,8 @@
 """Basecaller subset on the rollout-and-scoring path: per-frame projector + decoder-only LM + tokenizer.
 
-Reference: viktor/model.py:27-131. The encoder (frames producer) is outside this package: a Basecaller
-takes encoder frames [B, P, d_enc] directly; `encoder` may be None (then `d_enc` gives the frame width).
+Reference: viktor/model.py:27-131. A Basecaller takes encoder frames [B, P, d_enc] directly; `encoder` may be
+None (then `d_enc` gives the frame width) or the HIP encoder (viktor_amd.encoder.DoradoEncoder), which
+`encode` runs.
 Teacher-forced logits run on the HIP kernels: every window is packed as [its plens[b] frames | tokens]
 (the causal decoder never reads the padding the reference appends after them), the decoder runs over the
 packed tokens with its last layer kept for the token rows only, and the LM head gives bf16 logits.
@@ -58,6 +59,33 @@ class Basecaller(nn.Module):
         pos = torch.arange(L, device=x.device).expand(B, -1)
         n = torch.full((B, 1), P, device=x.device) if plens is None else plens[:, None]
         return torch.where(pos < n, pos * self.pos_scale, pos + (self.pos_scale - 1) * n)
+
+    @torch.no_grad()
+    def encode(self, sig, valid):
+        """Decoder input as at inference (viktor/model.py:89-117): encoder frames [B, P, d_enc] (P = frames of a
+        full window) and the real frames per window [B]. sig [B, 1, S]; valid: real samples per window. A full
+        window is encoded whole, a short one at its repeat-padded length (a multiple of the granularity, as
+        encoder.encode_chunks) keeping ceil(valid / stride) frames, the rest zero. All windows go through one
+        forward_varlen call (chunks are encoded independently, so this equals encoding them apart)."""
+        enc = self.encoder
+        if enc is None:
+            raise ValueError("Basecaller.encode needs an encoder")
+        B, S = sig.shape[0], sig.shape[-1]
+        st, g = enc.stride, enc.granularity
+        valid = [int(v) for v in (valid.tolist() if torch.is_tensor(valid) else valid)]
+        if not all(0 < v <= S for v in valid):
+            raise ValueError("Basecaller.encode: every window needs 0 < valid <= its length")
+        lens = [S if v == S else min(-(-v // g) * g, S) for v in valid]
+        flat = torch.cat([sig[b, 0, :n] for b, n in enumerate(lens)])
+        out = enc.forward_varlen(flat, lens)
+        P = S // st
+        plens = np.array([-(-v // st) for v in valid], dtype=np.int64)
+        starts = np.concatenate([[0], np.cumsum([n // st for n in lens])[:-1]])
+        src = np.concatenate([np.arange(s0, s0 + k) for s0, k in zip(starts, plens)])
+        dst = np.concatenate([np.arange(b * P, b * P + k) for b, k in enumerate(plens)])
+        frames = out.new_zeros(B * P, out.shape[-1])
+        frames.index_copy_(0, torch.from_numpy(dst).to(out.device), out.index_select(0, torch.from_numpy(src).to(out.device)))
+        return frames.view(B, P, -1), torch.from_numpy(plens).to(out.device)
 
     def logits(self, frames, tokens_in, plens=None):
         """Teacher forcing from encoder frames [B, P, d_enc]: bf16 logits [B, T, vocab] of every token
