@@ -16,6 +16,10 @@ Extra objects on the JSON line:
                 kernel; read from profiles/decode_attention_traffic.json when present, else null).
   cpu_baseline  the CPU oracle (the reference's fp32 torch path restated) on this host, on a bounded sample:
                 rounds of 2 sequences x 2048-frame prefix x 64 sampled tokens for about 12 s; tokens/s.
+  prefill       the rollout's prefill (projector + 8 layers with a BOS-only last layer, once per window
+                when the prefix KV is shared): algorithmic flops (projector, 2 x weights per row less what the
+                BOS-only last layer skips, causal attention 1024 n (n + 1) per layer and window, the LM head of
+                the BOS row) / prefill_ms, against 2.5 PFLOP/s bf16.
   gspo_reward   a rollout's 512 rewards on the device (strict identity, scripts/gspo.py:446) straight from the
                 output tokens: 64 synthetic 0.9-1.1 kb labels (5% of bases unscored), each window's 8 calls the
                 label with 5% substitutions / insertions / deletions, as token rows of 1024 (EOS after the
@@ -67,6 +71,20 @@ def build_model(dev):
     g.projector.to(torch.bfloat16)
     g.decoder.to(torch.bfloat16)
     return m, g.eval()
+
+
+def prefill_flops(windows, frames, layers=8, d=512, weights_per_layer=3014656, vocab=7):
+    """Algorithmic flops of the shared-prefix prefill: per window of n = frames + 1 rows (frames + BOS), the
+    projector (two 512 x 512 products per frame), 2 x weights per row for the decoder products, less the
+    last layer's work the BOS-only last layer skips for the frame rows (o, gate_up, down and the q part of
+    qkv: 5,242,880 flops per row), causal attention 1024 n (n + 1) in each of the first layers-1 layers and
+    the BOS query's 2 x 2 x 8 x 64 x n in the last, and the LM head of the BOS row."""
+    n = frames + 1
+    proj = 2 * 2 * d * d * frames
+    gemm = n * 2 * weights_per_layer * layers - frames * 5242880
+    attn = (layers - 1) * 1024 * n * (n + 1) + 2 * 2 * 8 * 64 * n
+    head = 2 * d * vocab
+    return windows * (proj + gemm + attn + head)
 
 
 def decode_attention_timing(eng, n_points=32, reps=5):
@@ -365,6 +383,11 @@ def main():
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("bytes_per_launch")
+    windows = PREFIXES if args.group_size > 1 else B
+    pf = prefill_flops(windows, P)
+    prefill_obj = {"windows_prefilled": windows, "alg_tflop": round(pf / 1e12, 3),
+                   "achieved_tflops": round(pf / (prefill_ms / 1e3) / 1e12, 1),
+                   "mfma_frac": round(pf / (prefill_ms / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
     out = tokens_check = eng.out[:, :NEW].cpu()
     live = int(((out != 0) & (out != 2)).sum())
     log("gspo reward")
@@ -391,6 +414,7 @@ def main():
                    "prefix_kv_shared_by": args.group_size,
                    "parallelism": "single GPU"},
         "prefill_ms": round(prefill_ms, 2), "decode_ms": round(decode_ms, 2),
+        "prefill": prefill_obj,
         "live_tokens_per_rollout": live,
         "roofline": {"kernel": attn_kernels,
                      "bound": "hbm", "achieved": round(achieved, 1),

@@ -94,6 +94,24 @@ int vk_linear(const void *x, const void *w, void *y, int64_t M, int32_t N, int32
 int vk_swiglu(const void *gu, void *out, int64_t n, int32_t f, void *stream);
 
 /*
+ * The Wqkv product with vk_qkv_rope_cache fused into its epilogue (prefill and the encoder): qkv = x w^T
+ * (x [M, K], w [(H + 2 HKV) 64, K] bf16, K % 64 == 0) rounded to bf16 as the unfused product stores it; the
+ * q and k heads get the per-head RMSNorm (q_norm_w / k_norm_w, both NULL: none) and the half-split RoPE at
+ * rope_pos[t] (NULL: pos[t]) of cos/sin [table_rows, 32] (table_dtype bf16 or f32), with the rounding points
+ * of vk_qkv_rope_cache; q head h of row t goes to q + t q_ld + 64 h; k / v head h to the cache
+ * (k_cache + seq[t] stride_cb + pos[t] stride_cs + 64 h, when seq[t] < cache_rows and pos[t] < cache_len) and /
+ * or to k_out / v_out + t kv_ld + 64 h. head_dim must be 64; 16-byte aligned pointers, strides % 8 == 0.
+ * Replaces linear + qkv_rope_cache (viktor/triton_ops.py:43-108, 138-146; viktor/fast_decoder.py:39-47) and
+ * the Wqkv product + apply_rope of the encoder (viktor/encoder.py:71-75).
+ */
+int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32_t K, const void *q_norm_w, const void *k_norm_w,
+                       float eps, const void *cos_t, const void *sin_t, int32_t table_dtype, int64_t table_rows,
+                       const int32_t *pos, const int32_t *rope_pos, const int32_t *seq, void *q, int64_t q_ld,
+                       void *k_cache, void *v_cache, int64_t stride_cb, int64_t stride_cs, int64_t cache_rows,
+                       int64_t cache_len, void *k_out, void *v_out, int64_t kv_ld, int32_t n_heads, int32_t n_kv_heads,
+                       int32_t head_dim, void *stream);
+
+/*
  * Single-query GQA attention against one layer of the KV cache:
  * out[b, h, :] = softmax(q[b, h] . K[b, :len_b, h / (H/HKV)]^T / sqrt(D)) V[b, :len_b, ...]
  * with len_b = clamp(lengths[b], 1, max_len); k_cache/v_cache element (b, s, hk, d) at
@@ -358,7 +376,8 @@ int vk_encoder_conv(const void *a, int64_t lda, const void *w, int32_t K, int32_
  * window_size = (left, right) or SDPA with the band mask of encoder.py:64-69; koi_qkv_rotary + koi_vcs_attn,
  * koi_tx.cpp:395-400). qkv [rows, ld] bf16 (q heads, k heads, v heads of 64), chunk c = rows cu[c] ..
  * cu[c + 1] - 1; plan = n_blocks pairs (chunk, first query row of a 128-row block); cos_t / sin_t fp32
- * [table_len, 32] (rope_tables); out [rows, ldo] bf16 (heads concatenated). D must be 64.
+ * [table_len, 32] (rope_tables), or both NULL when q and k are already rotated (vk_linear_qkv_rope);
+ * out [rows, ldo] bf16 (heads concatenated). D must be 64.
  */
 int vk_window_attention(const void *qkv, int64_t ld, const int32_t *cu, const int32_t *plan, int32_t n_blocks,
                         int32_t n_chunks, int32_t max_len, int32_t H, int32_t D, const float *cos_t,

@@ -538,6 +538,69 @@ def test_norm_qkv_rope_cache(M, embed):
     assert ok, err
 
 
+@pytest.mark.parametrize("M,tables", [(300, "bf16"), (4500, "f32")])
+def test_linear_qkv_rope(M, tables):
+    """The Wqkv product with QK-norm + RoPE + cache write in its epilogue against the oracle's composition of the
+    fused path's rounding points, and against the unfused pair (linear, then qkv_rope_cache)."""
+    g = gen(M + 5)
+    H, HKV, D, K, S, Bc = 8, 2, 64, 512, 300, M
+    x = R.bf(torch.randn(M, K, generator=g) * 2)
+    wq = R.bf(torch.randn((H + 2 * HKV) * D, K, generator=g) / math.sqrt(K))
+    qw = R.bf(torch.rand(D, generator=g) + 0.5)
+    kw = R.bf(torch.rand(D, generator=g) + 0.5)
+    cos, sin = R.rope_tables(D, 4096, 1e6)
+    if tables == "bf16":
+        cos, sin = R.bf(cos), R.bf(sin)
+    tdt = BF if tables == "bf16" else torch.float32
+    pos = torch.randint(0, S, (M,), generator=g).int()
+    rpos = torch.randint(0, 4096, (M,), generator=g).int()
+    seq = torch.randperm(Bc, generator=g)[:M].int()
+    kc = torch.zeros(Bc, S, HKV, D, dtype=BF, device=DEV)
+    vc = torch.zeros_like(kc)
+    dev = [to_dev(t, BF) for t in (x, wq, qw, kw)] + [to_dev(cos, tdt), to_dev(sin, tdt)]
+    q, k, v = ops.linear_qkv_rope(dev[0], dev[1], dev[2], dev[3], dev[4], dev[5], to_dev(pos), to_dev(seq), kc, vc,
+                                  1e-6, H, HKV, D, return_kv=True, rope_pos=to_dev(rpos))
+    qkv = R.linear_fused(x, wq).view(M, H + 2 * HKV, D)
+    rp = rpos.long()
+    qr = R.qk_norm_rope_fused(qkv[:, :H], qw, cos[rp], sin[rp], 1e-6)
+    kr = R.qk_norm_rope_fused(qkv[:, H:H + HKV], kw, cos[rp], sin[rp], 1e-6)
+    # the GEMM output can sit on a bf16 rounding boundary; the norm's sum of squares runs in another order
+    for got, want in ((q, qr), (k, kr)):
+        ok, err = bf_close(got, want, ulps=4, atol=4e-2)
+        assert ok, err
+    ok, err = bf_close(v, qkv[:, H + HKV:], ulps=1, atol=4e-3)
+    assert ok, err
+    assert torch.equal(kc.cpu()[seq.long(), pos.long()], k.cpu()) and torch.equal(vc.cpu()[seq.long(), pos.long()], v.cpu())
+    # the unfused pair on the same device: the same values up to the norm's summation order
+    qkv_d = ops.linear(dev[0], dev[1])
+    q2, k2, v2 = ops.qkv_rope_cache(qkv_d, dev[2], dev[3], dev[4], dev[5], to_dev(pos), None, None, None, 1e-6, H, HKV,
+                                    D, return_kv=True, rope_pos=to_dev(rpos))
+    assert torch.equal(v2, v)
+    for a, b in ((q, q2), (k, k2)):
+        d = (a.float() - b.float()).abs()
+        assert (d > 0).float().mean() < 1e-3 and bf_close(a, b.float().cpu(), ulps=2, atol=2e-2)[0]
+
+
+def test_linear_qkv_rope_no_norm_in_place():
+    """The encoder's use: no QK-norm, rotary positions per row, q / k / v written back into the packed qkv rows."""
+    g = gen(11)
+    H, D, K, M = 8, 64, 512, 700
+    x = R.bf(torch.randn(M, K, generator=g))
+    wq = R.bf(torch.randn(3 * H * D, K, generator=g) / math.sqrt(K))
+    cos, sin = R.rope_tables(D, 4096, 1e4)
+    pos = (torch.arange(M) % 256).int()
+    qkv = torch.empty(M, 3 * H * D, dtype=BF, device=DEV)
+    ops.linear_qkv_rope(to_dev(x, BF), to_dev(wq, BF), None, None, to_dev(cos), to_dev(sin), to_dev(pos), None, None,
+                        None, 1e-6, H, H, D, return_kv=True, q_out=qkv[:, :H * D],
+                        kv_out=(qkv[:, H * D:2 * H * D], qkv[:, 2 * H * D:]))
+    ref = R.linear_fused(x, wq).view(M, 3, H, D)
+    rp = pos.long()
+    want = torch.cat([R.bf(R.apply_rope(ref[:, 0], cos[rp], sin[rp])), R.bf(R.apply_rope(ref[:, 1], cos[rp], sin[rp])),
+                      ref[:, 2]], 1).reshape(M, -1)
+    ok, err = bf_close(qkv, want, ulps=2, atol=2e-2)
+    assert ok, err
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 512, 512), (512, 512, 512), (77, 512, 1536), (512, 512, 1536)])
 def test_linear_residual(M, N, K):
     g = gen(M * 7 + K)

@@ -207,6 +207,7 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(const bf16_t *__restrict
 constexpr int WA_D = 64, WA_Q = 128, WA_KT = 64, WA_PITCH = 72;
 constexpr int WA_VTP = 68;  // keys per row of the transposed V tile (136 B: 8-byte operand reads conflict-free)
 
+template <bool ROT>
 __global__ __launch_bounds__(256, 4) void window_attn_kernel(const bf16_t *__restrict__ qkv, int64_t ld,
                                                           const int32_t *__restrict__ cu,
                                                           const int32_t *__restrict__ plan, int n_blocks, int n_chunks,
@@ -256,6 +257,11 @@ __global__ __launch_bounds__(256, 4) void window_attn_kernel(const bf16_t *__res
     const bf16_t *src = qbase + (row0 + r) * ld + g * 8;
     const u32x4 lo = *reinterpret_cast<const u32x4 *>(src);
     const u32x4 hi = *reinterpret_cast<const u32x4 *>(src + 32);
+    if (!ROT) {  // q already rotated (by the Wqkv product's epilogue)
+      bq[qb][0] = __builtin_bit_cast(bf16x8, lo);
+      bq[qb][1] = __builtin_bit_cast(bf16x8, hi);
+      continue;
+    }
     const f32x4 c0 = *reinterpret_cast<const f32x4 *>(cos_t + r * 32 + g * 8);
     const f32x4 c1 = *reinterpret_cast<const f32x4 *>(cos_t + r * 32 + g * 8 + 4);
     const f32x4 s0 = *reinterpret_cast<const f32x4 *>(sin_t + r * 32 + g * 8);
@@ -300,15 +306,16 @@ __global__ __launch_bounds__(256, 4) void window_attn_kernel(const bf16_t *__res
     rk1 = *reinterpret_cast<const u32x4 *>(kbase_p + off + 32);
     rv0 = *reinterpret_cast<const u32x4 *>(vbase_p + off);
     rv1 = *reinterpret_cast<const u32x4 *>(vbase_p + off + 32);
+    if (!ROT) return;
     tc0 = *reinterpret_cast<const f32x4 *>(cos_t + key * 32 + lc * 8);
     tc1 = *reinterpret_cast<const f32x4 *>(cos_t + key * 32 + lc * 8 + 4);
     ts0 = *reinterpret_cast<const f32x4 *>(sin_t + key * 32 + lc * 8);
     ts1 = *reinterpret_cast<const f32x4 *>(sin_t + key * 32 + lc * 8 + 4);
   };
   auto store_tile = [&](int buf) {
-    u32x4 k1, k2;
+    u32x4 k1 = rk0, k2 = rk1;
 #pragma unroll
-    for (int wv = 0; wv < 4; ++wv) {
+    for (int wv = 0; wv < 4 && ROT; ++wv) {
       float y1[2], y2[2];
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
@@ -534,22 +541,23 @@ extern "C" int vk_window_attention(const void *qkv, int64_t ld, const int32_t *c
                                    int32_t n_blocks, int32_t n_chunks, int32_t max_len, int32_t H, int32_t D,
                                    const float *cos_t, const float *sin_t, int32_t table_len, int32_t left,
                                    int32_t right, void *out, int64_t ldo, void *stream) {
-  VK_CHECK_ARG(qkv && cu && plan && cos_t && sin_t && out, "window_attention: null pointer");
+  VK_CHECK_ARG(qkv && cu && plan && out && (cos_t == nullptr) == (sin_t == nullptr), "window_attention: null pointer");
   if (D != WA_D) return fail(VK_ERR_UNSUPPORTED, "window_attention: built for head_dim 64 (got %d)", D);
   VK_CHECK_ARG(H > 0 && n_blocks >= 0 && n_chunks > 0 && left >= 0 && right >= 0 && ld >= 3 * H * WA_D &&
                    ld % 8 == 0 && ldo >= H * WA_D && ldo % 4 == 0,
                "window_attention: bad sizes");
-  VK_CHECK_ARG(max_len <= table_len, "window_attention: chunk of %d frames beyond the rotary table (%d)", max_len,
-               table_len);
+  VK_CHECK_ARG(cos_t == nullptr || max_len <= table_len, "window_attention: chunk of %d frames beyond the rotary table (%d)",
+               max_len, table_len);
   VK_CHECK_ARG(vk_aligned16(qkv) && vk_aligned16(out) && vk_aligned16(cos_t) && vk_aligned16(sin_t),
                "window_attention: pointers must be 16-byte aligned");
   if (n_blocks == 0) return VK_OK;
   const int64_t total = static_cast<int64_t>(n_blocks) * H;
   VK_CHECK_ARG(total < (int64_t(1) << 31), "window_attention: too many blocks");
   const float scale_log2 = static_cast<float>(1.0 / sqrt(static_cast<double>(WA_D)) * 1.4426950408889634);
-  window_attn_kernel<<<static_cast<unsigned>(total), 256, 0, VK_STREAM(stream)>>>(
-      static_cast<const bf16_t *>(qkv), ld, cu, plan, n_blocks, n_chunks, H, cos_t, sin_t, left, right, scale_log2,
-      static_cast<bf16_t *>(out), ldo);
+  auto kern = cos_t != nullptr ? window_attn_kernel<true> : window_attn_kernel<false>;
+  kern<<<static_cast<unsigned>(total), 256, 0, VK_STREAM(stream)>>>(static_cast<const bf16_t *>(qkv), ld, cu, plan,
+                                                                     n_blocks, n_chunks, H, cos_t, sin_t, left, right,
+                                                                     scale_log2, static_cast<bf16_t *>(out), ldo);
   return launch_status("window_attention");
 }
 

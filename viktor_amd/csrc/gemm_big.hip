@@ -41,11 +41,36 @@ typedef __attribute__((address_space(3))) void lds_void;
 // vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt in 6:4, lgkmcnt in 11:8)
 constexpr int vmcnt_imm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | (((n >> 4) & 3) << 14); }
 
-template <bool SWIGLU, bool OUT_F32>
+// Epilogues: bf16 out, fp32 out, SwiGLU, or the attention input stage of a Wqkv product (GB_QKV): the
+// product's 64-column heads (H q heads, HKV k heads, HKV v heads) are rounded to bf16 as the unfused product
+// stores them; q and k heads then get the per-head RMSNorm (when qw / kw are given: bf16(x / rms * w)) and
+// the half-split rotary embedding at the row's position (bf16(y1 c - y2 s), bf16(y1 s + y2 c), with the
+// table entries as stored), the rounding points of vk_qkv_rope_cache; then every head goes to its
+// destination -- q rows, the KV cache and / or k / v rows.
+enum GbEpi { GB_BF16 = 0, GB_F32 = 1, GB_SWIGLU = 2, GB_QKV = 3 };
+
+struct GbQkv {
+  const bf16_t *qw, *kw;  // per-head RMSNorm weights [64] (both NULL: no norm)
+  float eps;
+  const void *cos_t, *sin_t;  // [table_rows, 32], fp32 (table_f32) or bf16
+  int table_f32;
+  int64_t table_rows;
+  const int32_t *pos, *rope_pos, *seq;  // per row: cache position, rotary position (NULL: pos), cache row
+  bf16_t *q;                            // q head h of row t at q + t q_ld + 64 h
+  int64_t q_ld;
+  bf16_t *kc, *vc;  // cache row (seq, pos) head h at kc + seq stride_cb + pos stride_cs + 64 h (NULL: none)
+  int64_t stride_cb, stride_cs, cache_rows, cache_len;
+  bf16_t *ko, *vo;  // k / v head h of row t at ko + t kv_ld + 64 h (NULL: none)
+  int64_t kv_ld;
+  int H, HKV;
+};
+
+template <int EPI>
 __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restrict__ x, const bf16_t *__restrict__ w,
                                                           void *__restrict__ y, int64_t M, int N, int K, int tiles_n,
-                                                          int tiles_total) {
+                                                          int tiles_total, const GbQkv qa) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr bool SWIGLU = EPI == GB_SWIGLU, OUT_F32 = EPI == GB_F32, QKV = EPI == GB_QKV;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int wm = wid >> 1, wn = wid & 1;
   constexpr int OUT_COLS = SWIGLU ? 64 : 128;
@@ -170,7 +195,69 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
     for (int jj = 0; jj < PASS_ROWS / 16; ++jj) {
       const int j = pass * (PASS_ROWS / 16) + jj;
       char *rowp = stg + (16 * jj + fr) * PITCH;
-      if (SWIGLU) {
+      if (QKV) {
+        // this wavefront's 64 columns are one head (wave-uniform); lane: row 16 j + fr, columns 16 i + 4 fg + e
+        const int hd = qcol0 >> 6;
+        float v[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[i][e] = round_bf(acc[i][j][e]);
+        if (hd < qa.H + qa.HKV) {  // q or k head: QK-norm, then the rotation
+          int64_t rrow = qrow0 + 16 * j + fr;
+          rrow = rrow < M ? rrow : M - 1;
+          const bf16_t *nw = hd < qa.H ? qa.qw : qa.kw;
+          if (nw != nullptr) {
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) ss += v[i][e] * v[i][e];
+            ss += __shfl_xor(ss, 16, 64);  // the row's other 48 columns: lanes fr + 16, + 32, + 48
+            ss += __shfl_xor(ss, 32, 64);
+            const float r = rsqrtf(ss * (1.0f / 64.0f) + qa.eps);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[i][e] = round_bf(v[i][e] * r * bf2f(nw[16 * i + 4 * fg + e]));
+          }
+          int64_t rp = qa.rope_pos != nullptr ? qa.rope_pos[rrow] : qa.pos[rrow];
+          rp = rp < 0 ? 0 : (rp >= qa.table_rows ? qa.table_rows - 1 : rp);
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            // the lane's 4 consecutive table entries: one 16-byte (fp32) or 8-byte (bf16) load each
+            const int64_t ti = rp * 32 + 16 * i + 4 * fg;
+            float cs[4], sn[4];
+            if (qa.table_f32) {
+              const f32x4 c4 = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(qa.cos_t) + ti);
+              const f32x4 s4 = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(qa.sin_t) + ti);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                cs[e] = c4[e];
+                sn[e] = s4[e];
+              }
+            } else {
+              const u32x2 c2 = *reinterpret_cast<const u32x2 *>(static_cast<const bf16_t *>(qa.cos_t) + ti);
+              const u32x2 s2 = *reinterpret_cast<const u32x2 *>(static_cast<const bf16_t *>(qa.sin_t) + ti);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                cs[e] = (e & 1) ? hi_bf(c2[e >> 1]) : lo_bf(c2[e >> 1]);
+                sn[e] = (e & 1) ? hi_bf(s2[e >> 1]) : lo_bf(s2[e >> 1]);
+              }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float y1 = v[i][e], y2 = v[i + 2][e];
+              v[i][e] = y1 * cs[e] - y2 * sn[e];
+              v[i + 2][e] = y1 * sn[e] + y2 * cs[e];
+            }
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<u32x2 *>(rowp + (16 * i + 4 * fg) * 2) =
+              u32x2{pack_bf(v[i][0], v[i][1]), pack_bf(v[i][2], v[i][3])};
+      } else if (SWIGLU) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           float o[4];
@@ -201,28 +288,48 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
       const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + r * PITCH + c * 16);
       const int64_t row = qrow0 + pass * PASS_ROWS + r;
       const int col = qcol0 + c * (16 / ESZ);
+      if (QKV) {
+        const int hd = qcol0 >> 6;  // c: the 16-byte chunk (8 columns) of the head
+        if (row >= M || hd >= qa.H + 2 * qa.HKV) continue;
+        if (hd < qa.H) {
+          *reinterpret_cast<u32x4 *>(qa.q + row * qa.q_ld + hd * 64 + 8 * c) = v;
+          continue;
+        }
+        const bool is_k = hd < qa.H + qa.HKV;
+        const int hk = is_k ? hd - qa.H : hd - qa.H - qa.HKV;
+        bf16_t *cdst = is_k ? qa.kc : qa.vc;
+        if (cdst != nullptr) {
+          const int64_t sq = qa.seq[row], ps = qa.pos[row];
+          if (sq >= 0 && sq < qa.cache_rows && ps >= 0 && ps < qa.cache_len)
+            *reinterpret_cast<u32x4 *>(cdst + sq * qa.stride_cb + ps * qa.stride_cs + hk * 64 + 8 * c) = v;
+        }
+        bf16_t *odst = is_k ? qa.ko : qa.vo;
+        if (odst != nullptr) *reinterpret_cast<u32x4 *>(odst + row * qa.kv_ld + hk * 64 + 8 * c) = v;
+        continue;
+      }
       if (row < M && col < N)
         *reinterpret_cast<u32x4 *>(static_cast<char *>(y) + (row * N + col) * ESZ) = v;
     }
   }
 }
 
-template <bool SWIGLU, bool OUT_F32>
-static int launch_big(const bf16_t *x, const bf16_t *w, void *y, int64_t M, int N, int K, hipStream_t s) {
+template <int EPI>
+static int launch_big(const bf16_t *x, const bf16_t *w, void *y, int64_t M, int N, int K, const GbQkv &qa,
+                      hipStream_t s) {
   static bool configured = false;
   if (!configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_big_kernel<SWIGLU, OUT_F32>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_big_kernel<EPI>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(GB_SMEM)) != hipSuccess)
       return fail(VK_ERR_LAUNCH, "linear: cannot reserve %zu bytes of LDS", GB_SMEM);
     configured = true;
   }
-  constexpr int OUT_COLS = SWIGLU ? 64 : 128;
+  constexpr int OUT_COLS = EPI == GB_SWIGLU ? 64 : 128;
   const int tiles_n = (N + OUT_COLS - 1) / OUT_COLS;
   const int64_t tiles_m = (M + GB_BM - 1) / GB_BM;
   const int64_t total = tiles_m * tiles_n;
   if (total >= (int64_t(1) << 31)) return fail(VK_ERR_ARG, "linear: too many tiles");
-  gemm_big_kernel<SWIGLU, OUT_F32><<<static_cast<unsigned>(total), 256, GB_SMEM, s>>>(
-      x, w, y, M, N, K, tiles_n, static_cast<int>(total));
+  gemm_big_kernel<EPI><<<static_cast<unsigned>(total), 256, GB_SMEM, s>>>(x, w, y, M, N, K, tiles_n,
+                                                                           static_cast<int>(total), qa);
   return VK_OK;
 }
 
@@ -230,9 +337,68 @@ static int launch_big(const bf16_t *x, const bf16_t *w, void *y, int64_t M, int 
 // whole 16-byte output chunks).
 int gemm_big(const bf16_t *x, const bf16_t *w, void *y, int64_t M, int N, int K, bool swiglu, bool out_f32,
              hipStream_t s) {
-  if (swiglu) return launch_big<true, false>(x, w, y, M, N, K, s);
-  if (out_f32) return launch_big<false, true>(x, w, y, M, N, K, s);
-  return launch_big<false, false>(x, w, y, M, N, K, s);
+  const GbQkv none{};
+  if (swiglu) return launch_big<GB_SWIGLU>(x, w, y, M, N, K, none, s);
+  if (out_f32) return launch_big<GB_F32>(x, w, y, M, N, K, none, s);
+  return launch_big<GB_BF16>(x, w, y, M, N, K, none, s);
 }
 
 }  // namespace vk
+
+using namespace vk;
+
+extern "C" int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32_t K, const void *q_norm_w,
+                                  const void *k_norm_w, float eps, const void *cos_t, const void *sin_t,
+                                  int32_t table_dtype, int64_t table_rows, const int32_t *pos, const int32_t *rope_pos,
+                                  const int32_t *seq, void *q, int64_t q_ld, void *k_cache, void *v_cache,
+                                  int64_t stride_cb, int64_t stride_cs, int64_t cache_rows, int64_t cache_len,
+                                  void *k_out, void *v_out, int64_t kv_ld, int32_t n_heads, int32_t n_kv_heads,
+                                  int32_t head_dim, void *stream) {
+  VK_CHECK_ARG(x && w && cos_t && sin_t && q, "linear_qkv_rope: null pointer");
+  VK_CHECK_ARG(head_dim == 64, "linear_qkv_rope: built for head_dim 64 (got %d)", head_dim);
+  VK_CHECK_ARG(n_heads > 0 && n_kv_heads > 0, "linear_qkv_rope: bad head counts");
+  const int N = 64 * (n_heads + 2 * n_kv_heads);
+  VK_CHECK_ARG(M >= 0 && K > 0 && K % 64 == 0, "linear_qkv_rope: need K %% 64 == 0");
+  VK_CHECK_ARG(M < (int64_t(1) << 31) / 256 * 256, "linear_qkv_rope: M too large");
+  VK_CHECK_ARG((q_norm_w == nullptr) == (k_norm_w == nullptr), "linear_qkv_rope: q and k norm weights go together");
+  VK_CHECK_ARG(table_dtype == VK_DTYPE_BF16 || table_dtype == VK_DTYPE_F32, "linear_qkv_rope: bad table dtype");
+  VK_CHECK_ARG(table_rows > 0 && (pos != nullptr || rope_pos != nullptr), "linear_qkv_rope: rotary positions");
+  VK_CHECK_ARG((k_cache == nullptr) == (v_cache == nullptr), "linear_qkv_rope: k_cache and v_cache go together");
+  VK_CHECK_ARG(k_cache == nullptr || (seq != nullptr && pos != nullptr), "linear_qkv_rope: cache writes need seq and pos");
+  VK_CHECK_ARG((k_out == nullptr) == (v_out == nullptr), "linear_qkv_rope: k_out and v_out go together");
+  VK_CHECK_ARG(q_ld % 8 == 0 && kv_ld % 8 == 0 && stride_cb % 8 == 0 && stride_cs % 8 == 0,
+               "linear_qkv_rope: row strides must be multiples of 8 elements");
+  VK_CHECK_ARG(vk_aligned16(cos_t) && vk_aligned16(sin_t), "linear_qkv_rope: rotary tables must be 16-byte aligned");
+  VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w) && vk_aligned16(q) && (k_cache == nullptr || (vk_aligned16(k_cache) &&
+               vk_aligned16(v_cache))) && (k_out == nullptr || (vk_aligned16(k_out) && vk_aligned16(v_out))),
+               "linear_qkv_rope: pointers must be 16-byte aligned");
+  if (M == 0) return VK_OK;
+  GbQkv qa;
+  qa.qw = static_cast<const bf16_t *>(q_norm_w);
+  qa.kw = static_cast<const bf16_t *>(k_norm_w);
+  qa.eps = eps;
+  qa.cos_t = cos_t;
+  qa.sin_t = sin_t;
+  qa.table_f32 = table_dtype == VK_DTYPE_F32;
+  qa.table_rows = table_rows;
+  qa.pos = pos;
+  qa.rope_pos = rope_pos;
+  qa.seq = seq;
+  qa.q = static_cast<bf16_t *>(q);
+  qa.q_ld = q_ld;
+  qa.kc = static_cast<bf16_t *>(k_cache);
+  qa.vc = static_cast<bf16_t *>(v_cache);
+  qa.stride_cb = stride_cb;
+  qa.stride_cs = stride_cs;
+  qa.cache_rows = cache_rows;
+  qa.cache_len = cache_len;
+  qa.ko = static_cast<bf16_t *>(k_out);
+  qa.vo = static_cast<bf16_t *>(v_out);
+  qa.kv_ld = kv_ld;
+  qa.H = n_heads;
+  qa.HKV = n_kv_heads;
+  const int rc = launch_big<GB_QKV>(static_cast<const bf16_t *>(x), static_cast<const bf16_t *>(w), nullptr, M, N, K,
+                                    qa, VK_STREAM(stream));
+  if (rc != VK_OK) return rc;
+  return launch_status("linear_qkv_rope");
+}

@@ -8,8 +8,8 @@ on ONT's closed koi kernels (viktor/koi.py, viktor/csrc/koi_tx.cpp:120-423) or i
     margins scaled by the strides) so that every layer is one launch over the whole batch:
     vk_encoder_conv_first for the C_in = 1 layer, vk_encoder_conv (a strided-A GEMM) for the others, the
     last one writing the transformer's packed [frames, 512] input;
-  * each transformer layer is five launches: the Wqkv product (vk_gemm_rows), sliding-window attention
-    with the rotary embedding applied as Q and K are staged (vk_window_attention), out_proj into fp32 then
+  * each transformer layer is seven launches: the Wqkv product with the rotary embedding in its epilogue
+    (vk_linear_qkv_rope), sliding-window attention (vk_window_attention), out_proj into fp32 then
     bias + DeepNorm residual + RMSNorm (vk_deepnorm_rmsnorm), fc1 with the SwiGLU epilogue, fc2 into fp32
     then the second DeepNorm residual + RMSNorm.
 
@@ -103,6 +103,8 @@ class _ConvPlan:
         self.dst0 = torch.from_numpy(cu[:-1].copy()).to(device)
         sig_off = np.concatenate([[0], np.cumsum(np.asarray(lens, dtype=np.int64))[:-1]])
         self.sig_off = torch.from_numpy(sig_off.astype(np.int64)).to(device)
+        # rotary position of every frame: its index within its chunk
+        self.rope_pos = torch.from_numpy(np.concatenate([np.arange(f, dtype=np.int32) for f in self.frames])).to(device)
         # attention plan: (chunk, first query row) per 128-row block
         blocks = [(c, qs) for c, f in enumerate(self.frames) for qs in range(0, f, 128)]
         self.n_blocks = len(blocks)
@@ -314,11 +316,15 @@ class DoradoEncoder:
         y = torch.empty(M, C, dtype=torch.float32, device=dev)
         g = torch.empty(M, Fd, dtype=torch.bfloat16, device=dev)
         n = len(plan.frames)
+        hd = self.head_dim
         for Lw in self.weights["layers"]:
-            call("vk_gemm_rows", ptr(x), ptr(Lw["wqkv"]), ptr(qkv), M, 3 * C, C, 0, st)
+            # Wqkv with the rotary embedding in its epilogue: q, k (rotated) and v back into the packed rows
+            call("vk_linear_qkv_rope", ptr(x), ptr(Lw["wqkv"]), M, C, ptr(None), ptr(None), 0.0, ptr(self.cos),
+                 ptr(self.sin), _lib.VK_DTYPE_F32, self.cos.shape[0], ptr(plan.rope_pos), ptr(None), ptr(None),
+                 ptr(qkv), 3 * C, ptr(None), ptr(None), 0, 0, 0, 0, ptr(qkv[:, C:]), ptr(qkv[:, 2 * C:]), 3 * C, H, H,
+                 hd, st)
             call("vk_window_attention", ptr(qkv), 3 * C, ptr(plan.cu), ptr(plan.plan), plan.n_blocks, n,
-                 plan.max_frames, H, self.head_dim, ptr(self.cos), ptr(self.sin), self.cos.shape[0],
-                 self.window[0], self.window[1], ptr(o), C, st)
+                 plan.max_frames, H, hd, ptr(None), ptr(None), 0, self.window[0], self.window[1], ptr(o), C, st)
             call("vk_gemm_rows", ptr(o), ptr(Lw["wo"]), ptr(y), M, C, C, 1, st)
             call("vk_deepnorm_rmsnorm", ptr(y), ptr(Lw["bo"]), ptr(x), Lw["alpha"], ptr(Lw["n1"]), 1e-5, M, C, st)
             call("vk_gemm_rows", ptr(x), ptr(Lw["w1"]), ptr(g), M, Fd, C, 2, st)

@@ -124,11 +124,17 @@ class FastDecoder:
         n_layers = len(layers)
         for i, blk in enumerate(layers):
             a = blk.attn
-            qkv = ops.linear(h, W(a.qkv_proj.weight))
             kc = cache.k[i] if cache is not None else None
             vc = cache.v[i] if cache is not None else None
-            r = ops.qkv_rope_cache(qkv, W(a.q_norm.weight), W(a.k_norm.weight), cos, sin, pos, seq, kc, vc, eps,
-                                   cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, return_kv=return_kv, rope_pos=rope_pos)
+            if h.shape[0] >= 4096:  # large packed batches: QK-norm + RoPE + cache write in the product's epilogue
+                r = ops.linear_qkv_rope(h, W(a.qkv_proj.weight), W(a.q_norm.weight), W(a.k_norm.weight), cos, sin, pos,
+                                        seq, kc, vc, eps, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+                                        return_kv=return_kv, rope_pos=rope_pos)
+            else:
+                qkv = ops.linear(h, W(a.qkv_proj.weight))
+                r = ops.qkv_rope_cache(qkv, W(a.q_norm.weight), W(a.k_norm.weight), cos, sin, pos, seq, kc, vc, eps,
+                                       cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, return_kv=return_kv,
+                                       rope_pos=rope_pos)
             last = last_idx is not None and i == n_layers - 1
             if last:
                 # rows without a consumer are dropped: all K/V are kept, only the kept rows finish the layer

@@ -96,6 +96,49 @@ def qkv_rope_cache(qkv, q_norm_w, k_norm_w, cos, sin, pos, seq, k_cache, v_cache
     return (q, k, v) if return_kv else q
 
 
+def linear_qkv_rope(x, w, q_norm_w, k_norm_w, cos, sin, pos, seq, k_cache, v_cache, eps, n_heads, n_kv_heads,
+                    head_dim, return_kv=False, rope_pos=None, q_out=None, kv_out=None):
+    """The Wqkv product with qkv_rope_cache fused into its epilogue: x [n, K] @ w [(H + 2 Hkv) D, K]^T, then
+    per-head QK-norm (q_norm_w / k_norm_w; both None: none) and RoPE at pos (or rope_pos) on the q and k heads,
+    q to [n, H, D], k / v to the cache rows (seq, pos) and / or packed [n, Hkv, D] (return_kv). The rounding
+    points of linear + qkv_rope_cache (viktor/triton_ops.py:43-108, 138-146). q_out / kv_out: caller's buffers
+    (q_out [n, >= H D] rows; kv_out = (k, v) [n, >= Hkv D] rows, any row stride)."""
+    require_device(x, "linear_qkv_rope")
+    n, K = x.shape
+    H, HKV, D = n_heads, n_kv_heads, head_dim
+    _require(x.dtype == w.dtype == BF16 and w.shape == ((H + 2 * HKV) * D, K) and _contig(x, w),
+             "linear_qkv_rope: x / w")
+    _require(cos.shape == sin.shape and cos.dim() == 2 and cos.shape[1] == D // 2 and cos.dtype == sin.dtype
+             and cos.dtype in (torch.float32, BF16) and _contig(cos, sin), "linear_qkv_rope: cos/sin tables")
+    for t in (pos, rope_pos, seq):
+        _require(t is None or (t.dtype == torch.int32 and t.shape == (n,) and t.is_contiguous()),
+                 "linear_qkv_rope: pos / rope_pos / seq int32 [n]")
+    q = q_out if q_out is not None else torch.empty(n, H, D, dtype=BF16, device=x.device)
+    _require(q.stride(-1) == 1, "linear_qkv_rope: q rows")
+    k = v = None
+    if return_kv:
+        if kv_out is not None:
+            k, v = kv_out
+        else:
+            k = torch.empty(n, HKV, D, dtype=BF16, device=x.device)
+            v = torch.empty_like(k)
+        _require(k.stride(0) == v.stride(0) and k.stride(-1) == 1 and v.stride(-1) == 1, "linear_qkv_rope: k / v rows")
+    if k_cache is not None:
+        _require(seq is not None and pos is not None and k_cache.shape == v_cache.shape and
+                 k_cache.stride() == v_cache.stride() and k_cache.dim() == 4 and k_cache.shape[2:] == (HKV, D) and
+                 k_cache.stride(3) == 1 and k_cache.stride(2) == D and k_cache.dtype == BF16,
+                 "linear_qkv_rope: cache layout")
+        sb, ss, rows, clen = k_cache.stride(0), k_cache.stride(1), k_cache.shape[0], k_cache.shape[1]
+    else:
+        _require(return_kv, "linear_qkv_rope: nowhere to write k/v")
+        sb = ss = rows = clen = 0
+    tdt = VK_DTYPE_F32 if cos.dtype == torch.float32 else VK_DTYPE_BF16
+    call("vk_linear_qkv_rope", ptr(x), ptr(w), n, K, ptr(q_norm_w), ptr(k_norm_w), float(eps), ptr(cos), ptr(sin), tdt,
+         cos.shape[0], ptr(pos), ptr(rope_pos), ptr(seq), ptr(q), q.stride(0), ptr(k_cache), ptr(v_cache), sb, ss,
+         rows, clen, ptr(k), ptr(v), 0 if k is None else k.stride(0), H, HKV, D, stream_handle())
+    return (q, k, v) if return_kv else q
+
+
 def linear(x, w, swiglu=False, out_dtype=None, out=None):
     """x [M, K] @ w[N, K]^T on bf16 MFMA. swiglu: w is gate_up [2F, K] and the result silu(gate) * up
     [M, F]. out_dtype: torch.float32 for unrounded logits. Reference: viktor/triton_ops.py:138-146
