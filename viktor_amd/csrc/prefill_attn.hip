@@ -10,7 +10,8 @@
 //     32-key halves; halves that lie entirely above the causal diagonal of the wave's rows are skipped.
 //   * Transposed products as in the decode kernel: S^T = K Q^T (A = key rows from LDS, B = Q^T held in
 //     registers for the whole loop) leaves each lane the scores of one query row; O^T = V^T P^T consumes
-//     those probabilities in place and the online-softmax rescale stays lane-local.
+//     those probabilities in place and the online-softmax rescale stays lane-local. V is staged transposed
+//     (V^T rows of 68 keys), so the V^T operand is two 8-byte LDS reads per lane.
 //   * Per-wave state is 32 query rows (Q^T 16, O^T 32, scores 16 VGPRs) so the kernel fits 4 waves per
 //     SIMD: two workgroups per CU.
 //   * Keys of sequence i live at base + k_off[i] + j * stride_tok (+ kv head * 64): the same kernel
@@ -28,6 +29,7 @@ constexpr int PA_Q = 64;      // query rows per workgroup (plan granularity)
 constexpr int PA_WAVES = 8;   // 4 query heads x 2 halves of 32 rows
 constexpr int PA_KT = 64;     // keys per LDS tile
 constexpr int PA_PITCH = 72;  // 64 + 8 bf16
+constexpr int PA_VTP = 68;    // keys per row of the transposed V tile (136 B: 8-byte operand reads conflict-free)
 
 __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ k, const bf16_t *__restrict__ v,
@@ -35,7 +37,7 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
     const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok, bf16_t *__restrict__ out, int causal,
     float scale_log2, float *__restrict__ lse) {
   __shared__ __attribute__((aligned(16))) bf16_t Ks[2][PA_KT * PA_PITCH];
-  __shared__ __attribute__((aligned(16))) bf16_t Vs[2][PA_KT * PA_PITCH];
+  __shared__ __attribute__((aligned(16))) bf16_t Vt[2][PA_D * PA_VTP];  // V^T: [d][key]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wid = tid >> 6;
@@ -92,7 +94,12 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
   };
   auto store_tile = [&](int buf) {
     *reinterpret_cast<u32x4 *>(&Ks[buf][lrow * PA_PITCH + lchunk * 8]) = rk;
-    *reinterpret_cast<u32x4 *>(&Vs[buf][lrow * PA_PITCH + lchunk * 8]) = rv;
+    // V transposed, so the O^T = V^T P^T operand is two 8-byte reads per lane
+#pragma unroll
+    for (int wv = 0; wv < 4; ++wv) {
+      Vt[buf][(lchunk * 8 + 2 * wv) * PA_VTP + lrow] = static_cast<bf16_t>(rv[wv] & 0xffffu);
+      Vt[buf][(lchunk * 8 + 2 * wv + 1) * PA_VTP + lrow] = static_cast<bf16_t>(rv[wv] >> 16);
+    }
   };
 
   load_tile(0);
@@ -106,7 +113,7 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
       const int kbase = t * PA_KT + 32 * ks;
       if (kbase > wave_kmax) continue;  // wave-uniform: every key of this half is masked for every row
       const bf16_t *kt = &Ks[buf][32 * ks * PA_PITCH];
-      const bf16_t *vt = &Vs[buf][32 * ks * PA_PITCH];
+      const bf16_t *vt = &Vt[buf][32 * ks];
       // S^T[key][query] for two 16-key blocks x two 16-query blocks
       f32x4 st[2][2];
 #pragma unroll
@@ -175,12 +182,10 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
       // O^T += V^T P^T (key order {4g..4g+3, 16+4g..16+4g+3} in both operands)
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        bf16x8 va;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int kl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
-          va[jj] = __builtin_bit_cast(__bf16, vt[kl * PA_PITCH + 16 * dt + col]);
-        }
+        const bf16_t *vr = vt + (16 * dt + col) * PA_VTP;
+        const u32x2 lo = *reinterpret_cast<const u32x2 *>(vr + 4 * g);
+        const u32x2 hi = *reinterpret_cast<const u32x2 *>(vr + 16 + 4 * g);
+        const bf16x8 va = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) acc[dt][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[qb], acc[dt][qb], 0, 0, 0);
       }
