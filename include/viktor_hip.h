@@ -94,6 +94,14 @@ int vk_linear(const void *x, const void *w, void *y, int64_t M, int32_t N, int32
 int vk_swiglu(const void *gu, void *out, int64_t n, int32_t f, void *stream);
 
 /*
+ * Group check of DecodeEngine(group_size=G) before its one-prefill-per-window: x holds groups x G members of
+ * member_bytes each (16-byte aligned, member_bytes % 16 == 0); stores 1 to *flag when any member differs from its
+ * group's first member bit for bit (the caller zeroes *flag first; nothing is stored when all are equal).
+ * No reference counterpart: the reference prefills every repeated window (scripts/gspo.py:444).
+ */
+int vk_group_rows_equal(const void *x, int64_t groups, int32_t G, int64_t member_bytes, int32_t *flag, void *stream);
+
+/*
  * The Wqkv product with vk_qkv_rope_cache fused into its epilogue (prefill and the encoder): qkv = x w^T
  * (x [M, K], w [(H + 2 HKV) 64, K] bf16, K % 64 == 0) rounded to bf16 as the unfused product stores it; the
  * q and k heads get the per-head RMSNorm (q_norm_w / k_norm_w, both NULL: none) and the half-split RoPE at

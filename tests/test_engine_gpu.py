@@ -115,6 +115,13 @@ def test_grouped_rejects_unshared_prefix():
         eng.generate(fr, [20, 20, 20, 20])
     with pytest.raises(ValueError, match="prefix lengths"):
         eng.generate(fr, [20, 21, 20, 19])
+    # groups equal except one element of one member: caught by the one-pass device compare
+    same = fr[:40].view(2, 20, 512).repeat_interleave(2, 0).reshape(80, 512).contiguous()
+    eng.generate(same, [20, 20, 20, 20])
+    bad = same.clone()
+    bad[79, 511] += 1
+    with pytest.raises(ValueError, match="share"):
+        eng.generate(bad, [20, 20, 20, 20])
 
 
 def test_sampled_stream_parity_k4_temperature():

@@ -64,6 +64,7 @@ SIGNATURES = {
     "vk_window_attention": [_P, _I64, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _I32, _I32, _I32, _P, _I64, _P],
     "vk_deepnorm_rmsnorm": [_P, _P, _P, _F, _P, _F, _I64, _I32, _P],
     "vk_gemm_rows": [_P, _P, _P, _I64, _I32, _I32, _I32, _P],
+    "vk_group_rows_equal": [_P, _I64, _I32, _I64, _P, _P],
     "vk_linear_qkv_rope": [_P, _P, _I64, _I32, _P, _P, _F, _P, _P, _I32, _I64, _P, _P, _P, _P, _I64, _P, _P, _I64, _I64,
                            _I64, _I64, _P, _P, _I64, _I32, _I32, _I32, _P],
 }

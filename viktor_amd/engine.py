@@ -22,8 +22,8 @@ reduced separately, then merged).
 
 import torch
 
-from . import hip_ops as ops
-from ._lib import HipLibraryError
+from . import _lib, hip_ops as ops
+from ._lib import HipLibraryError, call, ptr
 from .decoder import KVCache
 from .fast_decoder import FastDecoder, PrefillPlan
 from .tokenizer import BOS, EOS, PAD
@@ -233,9 +233,13 @@ class DecodeEngine:
         for b in range(0, self.B, G):
             if any(frame_lens[b + m] != frame_lens[b] for m in range(G)):
                 raise ValueError(f"group_size={G}: sequences {b}..{b + G - 1} have different prefix lengths")
-        if len(set(frame_lens)) == 1:  # equal lengths: compare each group against its first member in place
-            f = frames.view(self.B // G, G, frame_lens[0], -1)
-            if not torch.equal(f[:, 1:], f[:, :1].expand(-1, G - 1, -1, -1)):
+        member_bytes = frame_lens[0] * frames.shape[1] * frames.element_size()
+        if (len(set(frame_lens)) == 1 and frames.is_contiguous() and member_bytes % 16 == 0
+                and frames.data_ptr() % 16 == 0):
+            # equal lengths: one pass comparing each member with its group's first, bit for bit
+            flag = torch.zeros(1, dtype=torch.int32, device=frames.device)
+            call("vk_group_rows_equal", ptr(frames), self.B // G, G, member_bytes, ptr(flag), _lib.stream_handle())
+            if int(flag.item()) != 0:
                 raise ValueError(f"group_size={G}: the sequences of a group must share their prefix frames")
             return
         dev = frames.device
