@@ -207,9 +207,9 @@ class FastDecoder:
         return ops.add_rmsnorm(xr, self.w(self.dec.norm.weight), self.cfg.norm_eps)
 
     def decode_residual(self, pos, seq, cache_seqlens, cache, rope_pos=None, tok=None, x=None, prefix=None):
-        """The decoder layers of one decode step on the small-M kernels, five launches per layer (+1 in
-        layer 0): norm_qkv_rope_cache (attn norm + qkv GEMM + QK-norm + RoPE + cache write; layer 0 runs
-        embed_rmsnorm, the token-embedding gather + norm, before it), decode_attention, linear_residual
+        """The decoder layers of one decode step on the small-M kernels, five launches per layer:
+        norm_qkv_rope_cache (attn norm + qkv GEMM + QK-norm + RoPE + cache write; in layer 0 with the
+        token-embedding gather in its prologue), decode_attention, linear_residual
         (o proj + residual add), norm_linear (mlp norm + gate_up + SwiGLU), linear_residual (down proj +
         residual add). The residual GEMMs leave the row sums of squares of x (per 64-column block), so the
         norms inside the next GEMMs need no pass of their own over x.
@@ -237,10 +237,13 @@ class FastDecoder:
         for i, blk in enumerate(layers):
             a = blk.attn
             kc, vc = cache.k[i], cache.v[i]
-            if xr is None:  # layer 0 of a step fed with token ids: the embedding gather + norm
-                xr, h = ops.embed_rmsnorm(tok, W(self.dec.embed.weight), W(blk.attn_norm.weight), eps)
-                q = ops.norm_qkv_rope_cache(h, None, eps, W(a.qkv_proj.weight), W(a.q_norm.weight),
-                                            W(a.k_norm.weight), cos, sin, pos, seq, kc, vc, H, HKV, D, rope_pos=rope_pos)
+            if xr is None:  # layer 0 of a step fed with token ids: the embedding gather + norm in the qkv launch,
+                # which also stores the gathered rows as the residual stream
+                emb = W(self.dec.embed.weight)
+                xr = torch.empty(B, emb.shape[1], dtype=BF16, device=tok.device)
+                q = ops.norm_qkv_rope_cache(emb, W(blk.attn_norm.weight), eps, W(a.qkv_proj.weight), W(a.q_norm.weight),
+                                            W(a.k_norm.weight), cos, sin, pos, seq, kc, vc, H, HKV, D, rope_pos=rope_pos,
+                                            tok=tok, x_store=xr)
             elif i == 0:  # x handed in by the caller: no row sums yet
                 h = ops.add_rmsnorm(xr, W(blk.attn_norm.weight), eps)
                 q = ops.norm_qkv_rope_cache(h, None, eps, W(a.qkv_proj.weight), W(a.q_norm.weight),
