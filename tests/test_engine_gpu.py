@@ -187,6 +187,69 @@ def test_rollout_deterministic_and_grammar_invariants():
     assert torch.equal(c[0], c[1])
 
 
+def test_varlen_kmer_batch_at_scale():
+    """The varlen + 4-mer configuration at its batch and prefix sizes (1024 sequences, prefixes uniform in
+    [1200, 2048] frames, vocab 343, greedy, 8 layers), a few steps: deterministic, grammar invariants on every
+    row (tokens in range, no BOS, a k-mer tail is followed by EOS, only PAD after EOS), and the first and last
+    sequences checked against the oracle (bar 1)."""
+    from viktor_amd.synthetic import varlen_lengths
+    m = make_model(4, n_layers=8, seed=9, norm_jitter=0.1, bias_jitter=0.1)
+    gm = gpu_copy(m)
+    B, steps = 1024, 10
+    lens = [int(n) for n in varlen_lengths(B, 1200, 2048, seed=10)]
+    fr = synth_frames(1, sum(lens), 512, seed=11)[0]
+    eng = DecodeEngine(gm, B, steps, max(lens), temperature=0.0)
+    frd = fr.to(DEV)
+    a = eng.generate(frd, lens, steps=steps).clone()
+    b = eng.generate(frd, lens, steps=steps).clone()
+    assert torch.equal(a, b)
+    a = a.cpu()
+    V = m.tokenizer.vocab_size
+    tail = m.tokenizer.tail_mask
+    assert V == 343 and bool(((a >= 0) & (a < V)).all()) and not bool((a == R.BOS).any())
+    for row in a.tolist():
+        for j, t in enumerate(row[:-1]):
+            if t == R.EOS or t == R.PAD:
+                assert row[j + 1] == R.PAD
+            elif bool(tail[t]):
+                assert row[j + 1] == R.EOS
+    del eng, frd
+    torch.cuda.empty_cache()
+    parts = list(fr.split(lens))
+    pick = [0, B - 1]
+    ref = R.RefEngine(R.RefModel(m, "fused"), steps, temperature=0.0, max_homopolymer=64)
+    res = ref.run([parts[i] for i in pick], forced=a[pick])
+    check_stream(a[pick], res, steps, 1e-2)
+
+
+def test_stress_batch_at_scale():
+    """The large-batch stress configuration's sizes: 4096 sequences x 2048-frame prefixes, vocab 7, greedy, 8
+    layers, each sequence on its own cache rows (about 51.5 GB of KV cache; per-layer cache offsets reach
+    1.6G elements). A few steps: deterministic, in-range tokens, and the first and last sequences against
+    the oracle (bar 1). Frames come from a device generator (4096 x 2048 x 512 fp32 would be 17 GB of host
+    memory); the two checked sequences are copied back."""
+    m = make_model(1, n_layers=8, seed=12, norm_jitter=0.1, bias_jitter=0.1)
+    gm = gpu_copy(m)
+    B, P, steps = 4096, 2048, 4
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(13)
+    fr = torch.randn(B * P, 512, generator=gen, device=DEV, dtype=torch.float32)
+    eng = DecodeEngine(gm, B, 1024, P, temperature=0.0)
+    assert eng.cache.k.numel() * 2 * 2 > 51e9
+    a = eng.generate(fr, [P] * B, steps=steps)[:, :steps].clone()
+    b = eng.generate(fr, [P] * B, steps=steps)[:, :steps].clone()
+    assert torch.equal(a, b)
+    a = a.cpu()
+    assert bool(((a >= 0) & (a < 7)).all()) and not bool((a == R.BOS).any())
+    pick = [0, B - 1]
+    parts = [fr[i * P:(i + 1) * P].cpu() for i in pick]
+    del eng, fr
+    torch.cuda.empty_cache()
+    ref = R.RefEngine(R.RefModel(m, "fused"), steps, temperature=0.0, max_homopolymer=64)
+    res = ref.run(parts, forced=a[pick])
+    check_stream(a[pick], res, steps, 1e-2)
+
+
 def test_teacher_forced_logprobs_parity():
     m = make_model(1, n_layers=2, seed=8, norm_jitter=0.1, bias_jitter=0.1)
     gm = gpu_copy(m)
