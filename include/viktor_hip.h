@@ -102,6 +102,24 @@ int vk_swiglu(const void *gu, void *out, int64_t n, int32_t f, void *stream);
 int vk_group_rows_equal(const void *x, int64_t groups, int32_t G, int64_t member_bytes, int32_t *flag, void *stream);
 
 /*
+ * Large-M residual product, in place: x[M, N] = bf16(bf16(a w^T + bias) + bf16(alpha x)) (a [M, K], w [N, K] bf16,
+ * bias fp32 [N] or NULL; N % 128 == 0, K % 64 == 0), and ss_out[M, N / 64] = the fp32 sum of squares of each row's
+ * new values per 64-column block. alpha = 1 without bias is the residual add of add_rmsnorm
+ * (viktor/triton_ops.py:17-31, x += delta after the o / down projections of viktor/fast_decoder.py:56-58); with
+ * the out_proj bias and the DeepNorm alpha it is the encoder's norm input (viktor/encoder.py:106-108).
+ */
+int vk_linear_residual_big(const void *a, const void *w, void *x, int64_t M, int32_t N, int32_t K, const float *bias,
+                           float alpha, float *ss_out, void *stream);
+
+/*
+ * RMSNorm from handed-over sums of squares: h = bf16(x * rsqrt(sum_b ss[row, b] / d + eps) * w) (x, w, h bf16,
+ * ss [n, nb] fp32 summed in block order; h may be x). The norm half of add_rmsnorm (viktor/triton_ops.py:28-31)
+ * after vk_linear_residual_big.
+ */
+int vk_rmsnorm_apply_ss(const void *x, const float *ss, int32_t nb, const void *w, void *h, int64_t n, int32_t d,
+                        float eps, void *stream);
+
+/*
  * The Wqkv product with vk_qkv_rope_cache fused into its epilogue (prefill and the encoder): qkv = x w^T
  * (x [M, K], w [(H + 2 HKV) 64, K] bf16, K % 64 == 0) rounded to bf16 as the unfused product stores it; the
  * q and k heads get the per-head RMSNorm (q_norm_w / k_norm_w, both NULL: none) and the half-split RoPE at

@@ -581,6 +581,35 @@ def test_linear_qkv_rope(M, tables):
         assert (d > 0).float().mean() < 1e-3 and bf_close(a, b.float().cpu(), ulps=2, atol=2e-2)[0]
 
 
+@pytest.mark.parametrize("M,N,K,alpha,bias", [(4500, 512, 512, 1.0, False), (700, 512, 2048, 2.4494897, True)])
+def test_linear_residual_big_and_rmsnorm_apply(M, N, K, alpha, bias):
+    """x = bf16(bf16(a w^T + b) + bf16(alpha x)) in place with per-64-column sums of squares, then the RMSNorm from
+    those sums, against the formulas (and, for alpha 1 without bias, against add_rmsnorm of the unfused product)."""
+    g = gen(M + K)
+    a = R.bf(torch.randn(M, K, generator=g))
+    w = R.bf(torch.randn(N, K, generator=g) / math.sqrt(K))
+    x = R.bf(torch.randn(M, N, generator=g) * 2)
+    b = R.bf(0.1 * torch.randn(N, generator=g)) if bias else None
+    nw = R.bf(torch.rand(N, generator=g) + 0.5)
+    xd = to_dev(x, BF)
+    ss = ops.linear_residual_big(to_dev(a, BF), to_dev(w, BF), xd, bias=None if b is None else to_dev(b), alpha=alpha)
+    acc = (a.double() @ w.double().t()).float() + (0 if b is None else b)
+    want = R.bf(R.bf(acc) + R.bf(alpha * x))
+    ok, err = bf_close(xd, want, ulps=1, atol=2e-2)  # an accumulation-order flip of bf16(acc) moves the sum one ulp
+    assert ok, err
+    xn = xd.float().cpu().double()
+    ss_ref = (xn * xn).view(M, N // 64, 64).sum(-1)
+    assert torch.allclose(ss.cpu().double(), ss_ref, rtol=1e-5, atol=1e-6)
+    h = ops.rmsnorm_apply(xd, ss, to_dev(nw, BF), 1e-6)
+    ok, err = bf_close(h, R.rmsnorm_fused(xd.float().cpu(), nw, 1e-6), ulps=1, atol=1e-5)
+    assert ok, err
+    if alpha == 1.0 and b is None:
+        xu = to_dev(x, BF)
+        hu = ops.add_rmsnorm(xu, to_dev(nw, BF), 1e-6, delta=ops.linear(to_dev(a, BF), to_dev(w, BF)))
+        assert torch.equal(xu, xd)  # the same residual (the product is the same kernel)
+        assert bf_close(h, hu.float().cpu(), ulps=1, atol=1e-5)[0]
+
+
 def test_linear_qkv_rope_no_norm_in_place():
     """The encoder's use: no QK-norm, rotary positions per row, q / k / v written back into the packed qkv rows."""
     g = gen(11)

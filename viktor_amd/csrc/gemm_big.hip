@@ -47,7 +47,12 @@ constexpr int vmcnt_imm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((
 // the half-split rotary embedding at the row's position (bf16(y1 c - y2 s), bf16(y1 s + y2 c), with the
 // table entries as stored), the rounding points of vk_qkv_rope_cache; then every head goes to its
 // destination -- q rows, the KV cache and / or k / v rows.
-enum GbEpi { GB_BF16 = 0, GB_F32 = 1, GB_SWIGLU = 2, GB_QKV = 3 };
+//
+// GB_RESID: y is a bf16 residual stream updated in place, y = bf16(bf16(acc + bias) + bf16(alpha y)) (alpha = 1,
+// no bias: add_rmsnorm's x += bf16(delta); the encoder's DeepNorm sum with its out_proj bias and alpha), and
+// ss_out[row, col / 64] receives the fp32 sum of squares of the row's new bf16 values over each 64-column block
+// (the RMSNorm that follows reads them instead of a pass of its own over the row).
+enum GbEpi { GB_BF16 = 0, GB_F32 = 1, GB_SWIGLU = 2, GB_QKV = 3, GB_RESID = 4 };
 
 struct GbQkv {
   const bf16_t *qw, *kw;  // per-head RMSNorm weights [64] (both NULL: no norm)
@@ -63,6 +68,10 @@ struct GbQkv {
   bf16_t *ko, *vo;  // k / v head h of row t at ko + t kv_ld + 64 h (NULL: none)
   int64_t kv_ld;
   int H, HKV;
+  // GB_RESID
+  const float *bias;  // [N] or NULL
+  float alpha;
+  float *ss_out;      // [M, N / 64]
 };
 
 template <int EPI>
@@ -70,7 +79,7 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
                                                           void *__restrict__ y, int64_t M, int N, int K, int tiles_n,
                                                           int tiles_total, const GbQkv qa) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  constexpr bool SWIGLU = EPI == GB_SWIGLU, OUT_F32 = EPI == GB_F32, QKV = EPI == GB_QKV;
+  constexpr bool SWIGLU = EPI == GB_SWIGLU, OUT_F32 = EPI == GB_F32, QKV = EPI == GB_QKV, RESID = EPI == GB_RESID;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int wm = wid >> 1, wn = wid & 1;
   constexpr int OUT_COLS = SWIGLU ? 64 : 128;
@@ -195,7 +204,32 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
     for (int jj = 0; jj < PASS_ROWS / 16; ++jj) {
       const int j = pass * (PASS_ROWS / 16) + jj;
       char *rowp = stg + (16 * jj + fr) * PITCH;
-      if (QKV) {
+      if (RESID) {
+        // lane: row 16 j + fr, columns qcol0 + 16 i + 4 fg + e; the old residual is read right here (each element
+        // by the lane that overwrites it)
+        int64_t rrow = qrow0 + 16 * j + fr;
+        const bool live = rrow < M;
+        rrow = live ? rrow : M - 1;
+        bf16_t *yrow = static_cast<bf16_t *>(y) + rrow * N + qcol0;
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const u32x2 old = *reinterpret_cast<const u32x2 *>(yrow + 16 * i + 4 * fg);
+          f32x4 b4 = {0.f, 0.f, 0.f, 0.f};
+          if (qa.bias != nullptr) b4 = *reinterpret_cast<const f32x4 *>(qa.bias + qcol0 + 16 * i + 4 * fg);
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float xo = (e & 1) ? hi_bf(old[e >> 1]) : lo_bf(old[e >> 1]);
+            o[e] = round_bf(round_bf(acc[i][j][e] + b4[e]) + round_bf(qa.alpha * xo));
+            ss += o[e] * o[e];
+          }
+          *reinterpret_cast<u32x2 *>(rowp + (16 * i + 4 * fg) * 2) = u32x2{pack_bf(o[0], o[1]), pack_bf(o[2], o[3])};
+        }
+        ss += __shfl_xor(ss, 16, 64);  // the row's other 48 columns of this block: lanes fr + 16, + 32, + 48
+        ss += __shfl_xor(ss, 32, 64);
+        if (live && fg == 0) qa.ss_out[rrow * (N >> 6) + (qcol0 >> 6)] = ss;
+      } else if (QKV) {
         // this wavefront's 64 columns are one head (wave-uniform); lane: row 16 j + fr, columns 16 i + 4 fg + e
         const int hd = qcol0 >> 6;
         float v[4][4];
@@ -401,4 +435,23 @@ extern "C" int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32
                                     qa, VK_STREAM(stream));
   if (rc != VK_OK) return rc;
   return launch_status("linear_qkv_rope");
+}
+
+extern "C" int vk_linear_residual_big(const void *a, const void *w, void *x, int64_t M, int32_t N, int32_t K,
+                                      const float *bias, float alpha, float *ss_out, void *stream) {
+  VK_CHECK_ARG(a && w && x && ss_out, "linear_residual_big: null pointer");
+  VK_CHECK_ARG(M >= 0 && N > 0 && N % 128 == 0 && K > 0 && K % 64 == 0,
+               "linear_residual_big: need N %% 128 == 0 and K %% 64 == 0 (N=%d K=%d)", N, K);
+  VK_CHECK_ARG(M < (int64_t(1) << 31) / 256 * 256, "linear_residual_big: M too large");
+  VK_CHECK_ARG(vk_aligned16(a) && vk_aligned16(w) && vk_aligned16(x) && (bias == nullptr || vk_aligned16(bias)),
+               "linear_residual_big: pointers must be 16-byte aligned");
+  if (M == 0) return VK_OK;
+  GbQkv qa{};
+  qa.bias = bias;
+  qa.alpha = alpha;
+  qa.ss_out = ss_out;
+  const int rc = launch_big<GB_RESID>(static_cast<const bf16_t *>(a), static_cast<const bf16_t *>(w), x, M, N, K, qa,
+                                      VK_STREAM(stream));
+  if (rc != VK_OK) return rc;
+  return launch_status("linear_residual_big");
 }

@@ -107,6 +107,29 @@ static int launch_rows(bf16_t *x, const bf16_t *delta, const int64_t *tok, const
   return launch_status(name);
 }
 
+// h = bf16(x * rsqrt(sum(ss[row]) / d + eps) * w) with the row's sum of squares handed over in nb block partials
+// (ss [n, nb] fp32, summed in block order); one wavefront per row, 8 columns per lane (d <= 512 * 8 / 8).
+// h may be x (each lane rewrites the chunk it read).
+__global__ __launch_bounds__(256) void rmsnorm_apply_ss_kernel(const bf16_t *x, const float *__restrict__ ss, int nb,
+                                                               const bf16_t *__restrict__ w, bf16_t *h, int64_t n,
+                                                               int d, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= n) return;
+  float tot = 0.f;
+  for (int b = 0; b < nb; ++b) tot += ss[row * nb + b];
+  const float r = rsqrtf(tot / static_cast<float>(d) + eps);
+  for (int c = lane * 8; c < d; c += 64 * 8) {
+    const u32x4 xv = *reinterpret_cast<const u32x4 *>(x + row * d + c);
+    const u32x4 wv = *reinterpret_cast<const u32x4 *>(w + c);
+    u32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      o[k] = pack_bf(lo_bf(xv[k]) * r * lo_bf(wv[k]), hi_bf(xv[k]) * r * hi_bf(wv[k]));
+    *reinterpret_cast<u32x4 *>(h + row * d + c) = o;
+  }
+}
+
 // Whether every member of every group of G equal-size members equals the group's first member, bit for bit:
 // a thread per 16-byte chunk of members 1..G-1; a difference stores 1 to *flag (every writer stores the same
 // value).
@@ -136,6 +159,17 @@ extern "C" int vk_group_rows_equal(const void *x, int64_t groups, int32_t G, int
   group_rows_equal_kernel<<<static_cast<unsigned>((total + 255) / 256), 256, 0, VK_STREAM(stream)>>>(
       static_cast<const u32x4 *>(x), groups, G, member_bytes / 16, flag);
   return launch_status("group_rows_equal");
+}
+
+extern "C" int vk_rmsnorm_apply_ss(const void *x, const float *ss, int32_t nb, const void *w, void *h, int64_t n,
+                                   int32_t d, float eps, void *stream) {
+  VK_CHECK_ARG(x && ss && w && h, "rmsnorm_apply_ss: null pointer");
+  VK_CHECK_ARG(n >= 0 && d > 0 && d % 8 == 0 && nb > 0, "rmsnorm_apply_ss: bad sizes (d=%d nb=%d)", d, nb);
+  VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w) && vk_aligned16(h), "rmsnorm_apply_ss: pointers must be 16-byte aligned");
+  if (n == 0) return VK_OK;
+  rmsnorm_apply_ss_kernel<<<static_cast<unsigned>((n + 3) / 4), 256, 0, VK_STREAM(stream)>>>(
+      static_cast<const bf16_t *>(x), ss, nb, static_cast<const bf16_t *>(w), static_cast<bf16_t *>(h), n, d, eps);
+  return launch_status("rmsnorm_apply_ss");
 }
 
 extern "C" int vk_version(void) { return 100; }

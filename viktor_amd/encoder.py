@@ -9,9 +9,10 @@ on ONT's closed koi kernels (viktor/koi.py, viktor/csrc/koi_tx.cpp:120-423) or i
     vk_encoder_conv_first for the C_in = 1 layer, vk_encoder_conv (a strided-A GEMM) for the others, the
     last one writing the transformer's packed [frames, 512] input;
   * each transformer layer is seven launches: the Wqkv product with the rotary embedding in its epilogue
-    (vk_linear_qkv_rope), sliding-window attention (vk_window_attention), out_proj into fp32 then
-    bias + DeepNorm residual + RMSNorm (vk_deepnorm_rmsnorm), fc1 with the SwiGLU epilogue, fc2 into fp32
-    then the second DeepNorm residual + RMSNorm.
+    (vk_linear_qkv_rope), sliding-window attention (vk_window_attention), out_proj with the bias and the
+    DeepNorm residual in its epilogue (vk_linear_residual_big, which also hands over the row sums of squares)
+    then the RMSNorm (vk_rmsnorm_apply_ss), fc1 with the SwiGLU epilogue, fc2 with the second DeepNorm
+    residual in its epilogue, then the second RMSNorm.
 
 Every kernel computes a chunk's rows with the same code whatever else is in the batch (row-deterministic
 GEMMs, chunk-relative attention tiles, per-row convolutions), so a mixed batch gives each chunk exactly the
@@ -200,8 +201,8 @@ class DoradoEncoder:
                 # y, gate = fc1(x).chunk(2): the kernel's SwiGLU takes the gate rows first
                 "w1": torch.cat([fc1[Fd:], fc1[:Fd]]).to(torch.bfloat16).contiguous().to(dev),
                 "w2": sd[pre + "ff.fc2.weight"].detach().to(torch.bfloat16).contiguous().to(dev),
-                "n1": _bf16_valued(sd[pre + "norm1.weight"]).contiguous().to(dev),
-                "n2": _bf16_valued(sd[pre + "norm2.weight"]).contiguous().to(dev),
+                "n1": sd[pre + "norm1.weight"].detach().to(torch.bfloat16).contiguous().to(dev),
+                "n2": sd[pre + "norm2.weight"].detach().to(torch.bfloat16).contiguous().to(dev),
                 "alpha": float(alpha) if alpha is not None else self.default_alpha,
             })
         self.weights = W
@@ -313,7 +314,7 @@ class DoradoEncoder:
         M, C, Fd, H = x.shape[0], self.d_model, self.dim_feedforward, self.nhead
         qkv = torch.empty(M, 3 * C, dtype=torch.bfloat16, device=dev)
         o = torch.empty(M, C, dtype=torch.bfloat16, device=dev)
-        y = torch.empty(M, C, dtype=torch.float32, device=dev)
+        ss = torch.empty(M, C // 64, dtype=torch.float32, device=dev)
         g = torch.empty(M, Fd, dtype=torch.bfloat16, device=dev)
         n = len(plan.frames)
         hd = self.head_dim
@@ -325,11 +326,15 @@ class DoradoEncoder:
                  hd, st)
             call("vk_window_attention", ptr(qkv), 3 * C, ptr(plan.cu), ptr(plan.plan), plan.n_blocks, n,
                  plan.max_frames, H, hd, ptr(None), ptr(None), 0, self.window[0], self.window[1], ptr(o), C, st)
-            call("vk_gemm_rows", ptr(o), ptr(Lw["wo"]), ptr(y), M, C, C, 1, st)
-            call("vk_deepnorm_rmsnorm", ptr(y), ptr(Lw["bo"]), ptr(x), Lw["alpha"], ptr(Lw["n1"]), 1e-5, M, C, st)
+            # out_proj: bias + DeepNorm residual in the product's epilogue (x in place, row sums of squares out),
+            # then the RMSNorm in place; the same for fc2 without bias
+            call("vk_linear_residual_big", ptr(o), ptr(Lw["wo"]), ptr(x), M, C, C, ptr(Lw["bo"]), Lw["alpha"], ptr(ss),
+                 st)
+            call("vk_rmsnorm_apply_ss", ptr(x), ptr(ss), C // 64, ptr(Lw["n1"]), ptr(x), M, C, 1e-5, st)
             call("vk_gemm_rows", ptr(x), ptr(Lw["w1"]), ptr(g), M, Fd, C, 2, st)
-            call("vk_gemm_rows", ptr(g), ptr(Lw["w2"]), ptr(y), M, C, Fd, 1, st)
-            call("vk_deepnorm_rmsnorm", ptr(y), ptr(None), ptr(x), Lw["alpha"], ptr(Lw["n2"]), 1e-5, M, C, st)
+            call("vk_linear_residual_big", ptr(g), ptr(Lw["w2"]), ptr(x), M, C, Fd, ptr(None), Lw["alpha"], ptr(ss),
+                 st)
+            call("vk_rmsnorm_apply_ss", ptr(x), ptr(ss), C // 64, ptr(Lw["n2"]), ptr(x), M, C, 1e-5, st)
 
     def flops_per_chunk(self, samples: int) -> float:
         """Matrix FLOPs of one chunk: convolutions, the four products per layer and the window attention's

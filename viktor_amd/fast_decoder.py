@@ -145,13 +145,20 @@ class FastDecoder:
                 else:
                     r = r[last_idx]
             o = attend(i, r, last)
-            h = ops.add_rmsnorm(x, W(blk.mlp_norm.weight), eps,
-                                delta=ops.linear(o.reshape(x.shape[0], -1), W(a.o_proj.weight)))
+            h = self._residual_norm(x, o.reshape(x.shape[0], -1), W(a.o_proj.weight), W(blk.mlp_norm.weight))
             g = ops.linear(h, W(blk.gate_up.weight), swiglu=True)
-            m = ops.linear(g, W(blk.down.weight))
             w_next = layers[i + 1].attn_norm.weight if i + 1 < n_layers else self.dec.norm.weight
-            h = ops.add_rmsnorm(x, W(w_next), eps, delta=m)
+            h = self._residual_norm(x, g, W(blk.down.weight), W(w_next))
         return h
+
+    def _residual_norm(self, x, a, w, norm_w):
+        """x += a @ w^T in place, then RMSNorm(x) * norm_w (viktor/fast_decoder.py:56-58 with
+        viktor/triton_ops.py:34-40). Large batches add the residual in the product's epilogue, which hands the
+        row sums of squares to the norm; the bf16 product never goes through HBM."""
+        eps = self.cfg.norm_eps
+        if x.shape[0] >= 4096 and x.shape[1] % 128 == 0 and a.shape[1] % 64 == 0:
+            return ops.rmsnorm_apply(x, ops.linear_residual_big(a, w, x), norm_w, eps)
+        return ops.add_rmsnorm(x, norm_w, eps, delta=ops.linear(a, w))
 
     def prefill(self, x, pos, seq, cu_seqlens, max_seqlen, cache, last_indices=None, cu_queries=None, rope_pos=None,
                 plan=None):

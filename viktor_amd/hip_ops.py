@@ -139,6 +139,34 @@ def linear_qkv_rope(x, w, q_norm_w, k_norm_w, cos, sin, pos, seq, k_cache, v_cac
     return (q, k, v) if return_kv else q
 
 
+def linear_residual_big(a, w, x, bias=None, alpha=1.0):
+    """Large-M residual product, in place: x = bf16(bf16(a @ w^T + bias) + bf16(alpha x)) (alpha 1, no bias:
+    add_rmsnorm's x += delta, viktor/triton_ops.py:17-31; with the out_proj bias and the DeepNorm alpha:
+    viktor/encoder.py:106-108). Returns the row sums of squares of the new x per 64-column block [M, N / 64]
+    fp32, for rmsnorm_apply."""
+    require_device(a, "linear_residual_big")
+    M, K = a.shape
+    N = w.shape[0]
+    _require(a.dtype == w.dtype == x.dtype == BF16 and w.shape[1] == K and x.shape == (M, N) and _contig(a, w, x, bias),
+             "linear_residual_big: shapes")
+    _require(bias is None or (bias.dtype == torch.float32 and bias.shape == (N,)), "linear_residual_big: bias fp32 [N]")
+    ss = torch.empty(M, N // 64, dtype=torch.float32, device=a.device)
+    call("vk_linear_residual_big", ptr(a), ptr(w), ptr(x), M, N, K, ptr(bias), float(alpha), ptr(ss), stream_handle())
+    return ss
+
+
+def rmsnorm_apply(x, ss, w, eps, out=None):
+    """h = bf16(x * rsqrt(sum(ss[row]) / d + eps) * w): the RMSNorm of x with its row sums of squares handed over
+    in block partials (linear_residual_big). out may be x itself."""
+    require_device(x, "rmsnorm_apply")
+    n, d = x.shape
+    _require(x.dtype == w.dtype == BF16 and ss.dtype == torch.float32 and ss.shape[0] == n and _contig(x, ss, w),
+             "rmsnorm_apply: shapes")
+    h = out if out is not None else torch.empty_like(x)
+    call("vk_rmsnorm_apply_ss", ptr(x), ptr(ss), ss.shape[1], ptr(w), ptr(h), n, d, float(eps), stream_handle())
+    return h
+
+
 def linear(x, w, swiglu=False, out_dtype=None, out=None):
     """x [M, K] @ w[N, K]^T on bf16 MFMA. swiglu: w is gate_up [2F, K] and the result silu(gate) * up
     [M, F]. out_dtype: torch.float32 for unrounded logits. Reference: viktor/triton_ops.py:138-146
