@@ -353,6 +353,22 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     load(vf, cur.v, cur);
   }
 
+  // Q^T fragments (loaded before the lengths, so both round trips overlap): column j = 16 cb + col -> member
+  // j / 4, head kvh * 4 + j % 4, the two 32-wide halves of D
+  bf16x8 bq[NCB][2];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    const int j = 16 * cb + col;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      u32x4 v = u32x4{0u, 0u, 0u, 0u};
+      if (j < NC) {
+        const int64_t row = static_cast<int64_t>(p) * G + j / 4;
+        v = *reinterpret_cast<const u32x4 *>(q + (row * DA_H + kvh * 4 + (j & 3)) * DA_D + 32 * c + 8 * g);
+      }
+      bq[cb][c] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
   // lengths, per wave in registers: lane m < G = member m's own rows, lane G = the prefix; incl = inclusive
   // prefix sum of the members' own-tile counts
   int len = 0, cnt = 0;
@@ -374,21 +390,6 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   const int ou0 = static_cast<int>(static_cast<int64_t>(own_all) * part / nparts);
   const int T = npre + static_cast<int>(static_cast<int64_t>(own_all) * (part + 1) / nparts) - ou0;  // tiles
 
-  // Q^T fragments: column j = 16 cb + col -> member j / 4, head kvh * 4 + j % 4, the two 32-wide halves of D
-  bf16x8 bq[NCB][2];
-#pragma unroll
-  for (int cb = 0; cb < NCB; ++cb) {
-    const int j = 16 * cb + col;
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      u32x4 v = u32x4{0u, 0u, 0u, 0u};
-      if (j < NC) {
-        const int64_t row = static_cast<int64_t>(p) * G + j / 4;
-        v = *reinterpret_cast<const u32x4 *>(q + (row * DA_H + kvh * 4 + (j & 3)) * DA_D + 32 * c + 8 * g);
-      }
-      bq[cb][c] = __builtin_bit_cast(bf16x8, v);
-    }
-  }
   f32x4 acc[NCB][4];
   float m_run[NCB], l_run[NCB];
 #pragma unroll
@@ -541,9 +542,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     const int j = 16 * cb + col;
     if (j < NC) {
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) Os[(wid * NC + j) * 64 + 16 * dt + 4 * g + i] = acc[cb][dt][i];
+      for (int dt = 0; dt < 4; ++dt) *reinterpret_cast<f32x4 *>(&Os[(wid * NC + j) * 64 + 16 * dt + 4 * g]) = acc[cb][dt];
       if (g == 0) {
         Ms[wid * NC + j] = m_run[cb];
         Ls[wid * NC + j] = l_run[cb];
@@ -553,29 +552,34 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   __syncthreads();
   // partial of (subgroup p, KV head, part, column j); a column no row of this part reaches: (-inf, 0, 0).
   // One part: the output itself, bf16(N / L) -- what the combine computes from a single partial, bit for
-  // bit (its weight is exp2(0) = 1); every column then has at least the first prefix row.
-  for (int o = threadIdx.x; o < NC * 64; o += GU_WAVES * 64) {
-    const int j = o / 64, d = o % 64;
+  // bit (its weight is exp2(0) = 1); every column then has at least the first prefix row. A thread merges
+  // 4 consecutive d of one column (16-byte LDS reads, one 8-byte store).
+  for (int o = threadIdx.x; o < NC * 16; o += GU_WAVES * 64) {
+    const int j = o >> 4, d0 = (o & 15) * 4;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < GU_WAVES; ++w) M = fmaxf(M, Ms[w * NC + j]);
-    float L = 0.f, N = 0.f;
+    float L = 0.f;
+    f32x4 N = {0.f, 0.f, 0.f, 0.f};
     if (M != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < GU_WAVES; ++w) {
         const float e = exp2f(Ms[w * NC + j] - M);
         L += e * Ls[w * NC + j];
-        N += e * Os[(w * NC + j) * 64 + d];
+        const f32x4 ow = *reinterpret_cast<const f32x4 *>(&Os[(w * NC + j) * 64 + d0]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) N[i] += e * ow[i];
       }
     }
     if (nparts == 1) {
       const int64_t b = static_cast<int64_t>(p) * G + j / 4;
-      out[(b * DA_H + kvh * 4 + (j & 3)) * DA_D + d] = f2bf(N / L);
+      *reinterpret_cast<u32x2 *>(out + (b * DA_H + kvh * 4 + (j & 3)) * DA_D + d0) =
+          u32x2{pack_bf(N[0] / L, N[1] / L), pack_bf(N[2] / L, N[3] / L)};
       continue;
     }
     const int64_t base = ((static_cast<int64_t>(p) * DA_HKV + kvh) * nparts + part) * NC + j;
-    ws_o[base * DA_D + d] = N;
-    if (d == 0) {
+    *reinterpret_cast<f32x4 *>(ws_o + base * DA_D + d0) = N;
+    if (d0 == 0) {
       ws_ml[base * 2] = M;
       ws_ml[base * 2 + 1] = L;
     }
