@@ -15,12 +15,14 @@
 //     heads x 2 halves of 32 rows), K / V tiles of 64 keys double buffered in LDS. Per key half:
 //     S^T = K Q^T, dP^T = V dO^T (A = key rows from LDS, B = Q^T / dO^T held in registers), dS^T in the
 //     accumulator layout, dQ^T += K^T dS^T (A = K^T read column-wise from LDS).
-//   * dK/dV kernel: a workgroup per 128-key block x KV head, 8 wavefronts of 16 keys (K^T / V^T fragments
-//     in registers), looping over the 32-query tiles at or below the diagonal, Q / dO / lse / D of the 4
-//     query heads staged in LDS (the next tile's loads in flight during the current one), with transposed
-//     copies of Q and dO: S = Q K^T, dP = dO V^T (A = query rows), then dV^T += dO^T P and dK^T += Q^T dS
-//     (A = the transposed copies) with P / dS consumed in their accumulator layout; the 4 heads accumulate
-//     in place. 128 keys per staged tile halve the re-reads of Q / dO against 64.
+//   * dK/dV kernel: a workgroup per 128-key block x KV head, 4 wavefronts of 32 keys (two 16-key blocks;
+//     K^T / V^T fragments in registers), looping over the 32-query tiles at or below the diagonal, Q / dO /
+//     lse / D of the 4 query heads staged in LDS (the next tile's loads in flight during the current one),
+//     with transposed copies of Q and dO: S = Q K^T, dP = dO V^T (A = query rows), then dV^T += dO^T P and
+//     dK^T += Q^T dS (A = the transposed copies) with P / dS consumed in their accumulator layout; the 4
+//     heads accumulate in place. Each operand fragment read from LDS feeds both key blocks of the wave, so
+//     the LDS reads per MFMA are half those of 16-key waves (the kernel was bound by them). 128 keys per
+//     staged tile halve the re-reads of Q / dO against 64.
 // Gradients are written in fp32 (the consumers -- QK-norm / RoPE backward, the qkv weight gradient -- work
 // in fp32 and round once).
 #include <math.h>
@@ -31,8 +33,8 @@ namespace vk {
 
 constexpr int AB_H = 8, AB_HKV = 2, AB_D = 64;
 constexpr int AB_PITCH = 72;  // 64 + 8 bf16 per LDS row
-constexpr int AB_KW = 8;      // wavefronts of a dK/dV workgroup (16 keys each: 128 keys per staged query tile)
-constexpr int AB_KB = 16 * AB_KW;
+constexpr int AB_KW = 4;      // wavefronts of a dK/dV workgroup (32 keys each: 128 keys per staged query tile)
+constexpr int AB_KB = 32 * AB_KW;
 
 // D[r, h] = sum_d dO[r, h, d] * o[r, h, d]: one thread per (row, head)
 __global__ __launch_bounds__(256) void attn_bwd_dot_kernel(const bf16_t *__restrict__ dout,
@@ -193,7 +195,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
 }
 
 // ---- dK / dV: workgroup = AB_KB keys of one sequence x one KV head ----------------------------------------
-__global__ __launch_bounds__(AB_KW * 64) void attn_bwd_dkdv_kernel(
+__global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ k, const bf16_t *__restrict__ v,
     const bf16_t *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ dd,
     const int32_t *__restrict__ cu, const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok,
@@ -217,20 +219,27 @@ __global__ __launch_bounds__(AB_KW * 64) void attn_bwd_dkdv_kernel(
   const int len = cu[seq + 1] - static_cast<int>(r0);
   if (len <= 0 || ks >= len) return;
 
-  // this wave's 16 keys (lane col -> key), K^T / V^T fragments of the B operand
-  const int key = ks + 16 * wid + col;
-  const int keyc = key < len ? key : len - 1;
-  bf16x8 bk[2], bv[2];
+  // this wave's 32 keys, two blocks of 16 (lane col -> key of each), K^T / V^T fragments of the B operand
+  int keyb[2];
+  bf16x8 bk[2][2], bv[2][2];
 #pragma unroll
-  for (int dc = 0; dc < 2; ++dc) {
-    const int64_t off = (r0 + keyc) * stride_tok + hk * AB_D + 32 * dc + 8 * g;
-    bk[dc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(k + off));
-    bv[dc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(v + off));
+  for (int kb = 0; kb < 2; ++kb) {
+    keyb[kb] = ks + 32 * wid + 16 * kb + col;
+    const int keyc = keyb[kb] < len ? keyb[kb] : len - 1;
+#pragma unroll
+    for (int dc = 0; dc < 2; ++dc) {
+      const int64_t off = (r0 + keyc) * stride_tok + hk * AB_D + 32 * dc + 8 * g;
+      bk[kb][dc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(k + off));
+      bv[kb][dc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(v + off));
+    }
   }
-  f32x4 accv[4], acck[4];  // dV^T / dK^T tiles [d tile] (lane col -> key, 4 g + i -> d within the tile)
+  // dV^T / dK^T tiles [key block][d tile] (lane col -> key, 4 g + i -> d within the tile)
+  f32x4 accv[2][4], acck[2][4];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) accv[dt] = acck[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int wave_kmin = ks + 16 * wid;  // rows below it see none of this wave's keys
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) accv[kb][dt] = acck[kb][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int wave_kmin = ks + 32 * wid;  // rows below it see none of this wave's keys
 
   // staging: thread t loads 16-byte chunks t + NT c (c < 1024 / NT) of the Q tile and of the dO tile:
   // chunk -> (head hh = chunk / 256, row rr = chunk / 8 % 32, d chunk dc8 = chunk % 8), and threads t < 256
@@ -285,40 +294,50 @@ __global__ __launch_bounds__(AB_KW * 64) void attn_bwd_dkdv_kernel(
     for (int hh = 0; hh < 4; ++hh) {
       const bf16_t *qt = &Qs[hh * 32 * AB_PITCH];
       const bf16_t *ot = &Os[hh * 32 * AB_PITCH];
-      // S / dP [row 16 rb + 4 g + i][key col]
-      f32x4 st[2], dpt[2];
+      // S / dP [key block][row 16 rb + 4 g + i][key col]: each Q / dO fragment serves both key blocks
+      f32x4 st[2][2], dpt[2][2];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        st[rb] = dpt[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) st[kb][rb] = dpt[kb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int dc = 0; dc < 2; ++dc) {
           const bf16x8 qa = *reinterpret_cast<const bf16x8 *>(&qt[(16 * rb + col) * AB_PITCH + 32 * dc + 8 * g]);
           const bf16x8 oa = *reinterpret_cast<const bf16x8 *>(&ot[(16 * rb + col) * AB_PITCH + 32 * dc + 8 * g]);
-          st[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa, bk[dc], st[rb], 0, 0, 0);
-          dpt[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(oa, bv[dc], dpt[rb], 0, 0, 0);
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            st[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa, bk[kb][dc], st[kb][rb], 0, 0, 0);
+            dpt[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(oa, bv[kb][dc], dpt[kb][rb], 0, 0, 0);
+          }
         }
       }
       // row order {4g..4g+3, 16+4g..16+4g+3}; branch-free: a masked entry's exponent is -inf (exp2 -> 0),
       // exponents are <= 0 (bare v_exp_f32)
-      float pv[8], dv8[8];
+      bf16x8 pf[2], dsf[2];
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
+      for (int kb = 0; kb < 2; ++kb) {
+        const int key = keyb[kb];
+        float pv[8], dv8[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int rr = 16 * rb + 4 * g + i;
-          const int r = rs + rr;
-          const bool ok = (r < len) & (key <= r) & (key < len);
-          const float x = ok ? st[rb][i] * scale_log2 - Ls[hh * 32 + rr] : -INFINITY;
-          const float p = __builtin_amdgcn_exp2f(x);
-          pv[rb * 4 + i] = p;
-          dv8[rb * 4 + i] = p * (dpt[rb][i] - Ds[hh * 32 + rr]);
-        }
-      const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pack_bf(pv[0], pv[1]), pack_bf(pv[2], pv[3]),
-                                                          pack_bf(pv[4], pv[5]), pack_bf(pv[6], pv[7])});
-      const bf16x8 dsf = __builtin_bit_cast(bf16x8, u32x4{pack_bf(dv8[0], dv8[1]), pack_bf(dv8[2], dv8[3]),
-                                                           pack_bf(dv8[4], dv8[5]), pack_bf(dv8[6], dv8[7])});
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int rr = 16 * rb + 4 * g + i;
+            const int r = rs + rr;
+            const bool ok = (r < len) & (key <= r) & (key < len);
+            const float x = ok ? st[kb][rb][i] * scale_log2 - Ls[hh * 32 + rr] : -INFINITY;
+            const float p = __builtin_amdgcn_exp2f(x);
+            pv[rb * 4 + i] = p;
+            dv8[rb * 4 + i] = p * (dpt[kb][rb][i] - Ds[hh * 32 + rr]);
+          }
+        pf[kb] = __builtin_bit_cast(bf16x8, u32x4{pack_bf(pv[0], pv[1]), pack_bf(pv[2], pv[3]), pack_bf(pv[4], pv[5]),
+                                                   pack_bf(pv[6], pv[7])});
+        dsf[kb] = __builtin_bit_cast(bf16x8, u32x4{pack_bf(dv8[0], dv8[1]), pack_bf(dv8[2], dv8[3]),
+                                                    pack_bf(dv8[4], dv8[5]), pack_bf(dv8[6], dv8[7])});
+      }
       // dV^T += dO^T P, dK^T += Q^T dS (A = dO^T / Q^T from the transposed copies: lane col -> d, rows
-      // {4g..4g+3} and {16+4g..16+4g+3} as four 32-bit reads, the row order of P / dS above)
+      // {4g..4g+3} and {16+4g..16+4g+3} as four 32-bit reads, the row order of P / dS above; each fragment
+      // serves both key blocks)
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         const bf16_t *qtr = &QTs[(hh * 64 + 16 * dt + col) * TP];
@@ -326,18 +345,25 @@ __global__ __launch_bounds__(AB_KW * 64) void attn_bwd_dkdv_kernel(
         const uint32_t *qw = reinterpret_cast<const uint32_t *>(qtr), *ow = reinterpret_cast<const uint32_t *>(otr);
         const bf16x8 qa = __builtin_bit_cast(bf16x8, u32x4{qw[2 * g], qw[2 * g + 1], qw[8 + 2 * g], qw[9 + 2 * g]});
         const bf16x8 oa = __builtin_bit_cast(bf16x8, u32x4{ow[2 * g], ow[2 * g + 1], ow[8 + 2 * g], ow[9 + 2 * g]});
-        accv[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(oa, pf, accv[dt], 0, 0, 0);
-        acck[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa, dsf, acck[dt], 0, 0, 0);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          accv[kb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(oa, pf[kb], accv[kb][dt], 0, 0, 0);
+          acck[kb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa, dsf[kb], acck[kb][dt], 0, 0, 0);
+        }
       }
     }
   }
-  if (key >= len) return;
-  float *dkp = dk + ((r0 + key) * AB_HKV + hk) * AB_D + 4 * g;
-  float *dvp = dv + ((r0 + key) * AB_HKV + hk) * AB_D + 4 * g;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) {
-    *reinterpret_cast<f32x4 *>(dkp + 16 * dt) = acck[dt] * scale;
-    *reinterpret_cast<f32x4 *>(dvp + 16 * dt) = accv[dt];
+  for (int kb = 0; kb < 2; ++kb) {
+    if (keyb[kb] < len) {
+      float *dkp = dk + ((r0 + keyb[kb]) * AB_HKV + hk) * AB_D + 4 * g;
+      float *dvp = dv + ((r0 + keyb[kb]) * AB_HKV + hk) * AB_D + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        *reinterpret_cast<f32x4 *>(dkp + 16 * dt) = acck[kb][dt] * scale;
+        *reinterpret_cast<f32x4 *>(dvp + 16 * dt) = accv[kb][dt];
+      }
+    }
   }
 }
 
