@@ -9,7 +9,8 @@ The model keeps fp32 master weights, as the reference's trainable model does; ev
 bf16 (the autocast the reference trains under) and every weight gradient arrives in fp32 through that cast.
 The decoder stack is one autograd node (`_DecoderStack`): its forward runs the prefill kernels over the
 packed windows and keeps each layer's activations, its backward runs the HIP backward kernels (attention,
-RMSNorm, QK-norm + RoPE, SwiGLU) and the plain weight / input GEMMs (hipBLASLt through torch.matmul).
+RMSNorm, QK-norm + RoPE, SwiGLU) and the plain input GEMMs (hipBLASLt through torch.matmul); the weight
+gradients are split-K batched products (hipBLASLt, fp32 slices summed in order).
 The projector, the embedding gather and the LM head (V = 7 columns) stay torch autograd ops, as in the
 reference. The residual stream is bf16, the rounding points of the inference path.
 """
@@ -38,6 +39,28 @@ def _mm(a, b):
     place); b is contiguous."""
     assert b.is_contiguous()
     return torch.matmul(a, b)
+
+
+_WGRAD_SPLIT = 16
+
+
+def _wgrad(a, b):
+    """Weight gradient a^T @ b [Ka, Kb] over the packed rows of a [n, Ka] and b [n, Kb] (bf16, contiguous),
+    rounded to bf16 once as the reference's autocast matmul output. The reduction over ~10^5 rows with a
+    small output has too few output tiles for one product, so the rows are split into 16 slices computed as
+    one batched product with fp32 outputs, and the slices are summed in fp32 in slice order (deterministic).
+    The right operand of every batched product is contiguous."""
+    assert a.is_contiguous() and b.is_contiguous() and a.shape[0] == b.shape[0]
+    n = a.shape[0]
+    c = n // _WGRAD_SPLIT
+    if c < 1024:
+        return torch.matmul(a.t(), b)
+    m = c * _WGRAD_SPLIT
+    acc = torch.bmm(a[:m].view(_WGRAD_SPLIT, c, -1).transpose(1, 2), b[:m].view(_WGRAD_SPLIT, c, -1),
+                    out_dtype=torch.float32).sum(0)
+    if m < n:
+        acc += torch.bmm(a[m:].t().unsqueeze(0), b[m:].unsqueeze(0), out_dtype=torch.float32)[0]
+    return acc.to(BF16)
 
 
 class _TokenEmbed(torch.autograd.Function):
@@ -109,19 +132,19 @@ class _DecoderStack(torch.autograd.Function):
             wa, wqkv, wqn, wkn, wo, wm, wgu, wd = w[8 * i:8 * i + 8]
             # x_{i+1} = x_mid + g Wd^T
             dm = dx.to(BF16)
-            gd = _mm(dm.t(), g)
+            gd = _wgrad(dm, g)
             dg = _mm(dm, wd)
             dgu = ops.swiglu_backward(gu, dg)
-            ggu = _mm(dgu.t(), h2)
+            ggu = _wgrad(dgu, h2)
             dh2 = _mm(dgu, wgu)
             dx, gm = ops.rmsnorm_backward(x_mid, wm, dh2, eps, dres=dx)  # d / d x_mid
             # x_mid = x_in + o Wo^T
             da = dx.to(BF16)
-            go = _mm(da.t(), o.view(N, H * D))
+            go = _wgrad(da, o.view(N, H * D))
             do = _mm(da, wo).view(N, H, D).contiguous()
             dq, dk, dv = ops.attention_backward(q, k, v, o, do, lse, plan.attn, plan.keys)
             dqkv, gqn, gkn = ops.qknorm_rope_backward(qkv, wqn, wkn, cos, sin, rpos, dq, dk, dv, eps, H, HKV, D)
-            gqkv = _mm(dqkv.t(), h)
+            gqkv = _wgrad(dqkv, h)
             dhh = _mm(dqkv, wqkv)
             dx, ga = ops.rmsnorm_backward(x_in, wa, dhh, eps, dres=dx)  # d / d x_in
             grads[8 * i:8 * i + 8] = [ga, gqkv, gqn, gkn, go, gm, ggu, gd]
