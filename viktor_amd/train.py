@@ -41,6 +41,15 @@ def _mm(a, b):
     return torch.matmul(a, b)
 
 
+def _residual_norm(x, a, w, norm_w, eps):
+    """x += a @ w^T in place, then RMSNorm(x) * norm_w (add_rmsnorm after a linear, viktor/triton_ops.py:34-40).
+    Packed batches of >= 4096 rows add the residual in the product's epilogue, which hands the row sums of
+    squares to the norm."""
+    if x.shape[0] >= 4096 and x.shape[1] % 128 == 0 and a.shape[1] % 64 == 0:
+        return ops.rmsnorm_apply(x, ops.linear_residual_big(a, w, x), norm_w, eps)
+    return ops.add_rmsnorm(x, norm_w, eps, delta=ops.linear(a, w))
+
+
 _WGRAD_SPLIT = 16
 
 
@@ -103,12 +112,12 @@ class _DecoderStack(torch.autograd.Function):
                                          return_kv=True)
             lse = torch.empty(N, H, dtype=torch.float32, device=x.device)
             o = ops.varlen_attention(q, k, v, plan.attn, lse=lse)
-            h2 = ops.add_rmsnorm(x, wm, eps, delta=ops.linear(o.view(N, H * D), wo))
+            h2 = _residual_norm(x, o.view(N, H * D), wo, wm, eps)
             x_mid = x.clone()
             gu = ops.linear(h2, wgu)
             g = ops.swiglu(gu)
             w_next = w[8 * (i + 1)] if i + 1 < L else w[8 * L]
-            h_next = ops.add_rmsnorm(x, w_next, eps, delta=ops.linear(g, wd))
+            h_next = _residual_norm(x, g, wd, w_next, eps)
             saved.append((x_in, h, qkv, q, k, v, o, lse, x_mid, h2, gu, g))
             h = h_next
         ctx.meta, ctx.saved_acts, ctx.w, ctx.x_final = meta, saved, w, x
