@@ -109,12 +109,15 @@ __global__ __launch_bounds__(256) void colsum_kernel(const float *__restrict__ p
 // dq / dk [n, H|HKV, 64] fp32), v heads (dv passed through). qkv [n, (H + 2 HKV) 64] bf16 is the forward's
 // projection output, cos/sin [S, 32] fp32 (or bf16) at row position rpos. dw_part [gridDim.x, 128]: q-norm
 // weight gradient partials (0..63) and k-norm (64..127).
-template <typename TT>
+// HT / HKVT > 0: the head counts as compile-time constants (the decoder's 8 / 2), so the head loops unroll and
+// every head's loads and reductions of a row are in flight together; 0: the run-time H / HKV.
+template <typename TT, int HT, int HKVT>
 __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(
     const bf16_t *__restrict__ qkv, const bf16_t *__restrict__ qw, const bf16_t *__restrict__ kw,
     const TT *__restrict__ cos_t, const TT *__restrict__ sin_t, int64_t table_rows, const int32_t *__restrict__ rpos,
     const float *__restrict__ dq, const float *__restrict__ dk, const float *__restrict__ dv,
-    bf16_t *__restrict__ dqkv, float *__restrict__ dw_part, int64_t n, int H, int HKV, float eps) {
+    bf16_t *__restrict__ dqkv, float *__restrict__ dw_part, int64_t n, int H_rt, int HKV_rt, float eps) {
+  const int H = HT > 0 ? HT : H_rt, HKV = HKVT > 0 ? HKVT : HKV_rt;
   __shared__ float red[4][128];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int half = lane >> 5, fi = lane & 31;  // rotation half, frequency index
@@ -125,6 +128,7 @@ __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(
     int64_t p = rpos[row];
     p = p < 0 ? 0 : (p >= table_rows ? table_rows - 1 : p);
     const float c = ld(cos_t, p * 32 + fi), s = ld(sin_t, p * 32 + fi);
+#pragma unroll
     for (int h = 0; h < H + HKV; ++h) {
       const bool isq = h < H;
       const float go = isq ? dq[(row * H + h) * 64 + lane] : dk[(row * HKV + (h - H)) * 64 + lane];
@@ -143,6 +147,7 @@ __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(
       else
         dwk += gy * xv * r;
     }
+#pragma unroll
     for (int h = 0; h < HKV; ++h)
       dqkv[row * NH * 64 + (H + HKV + h) * 64 + lane] = f2bf(dv[(row * HKV + h) * 64 + lane]);
   }
@@ -288,14 +293,24 @@ extern "C" int vk_qknorm_rope_backward(const void *qkv, const void *q_norm_w, co
   const auto qw = static_cast<const bf16_t *>(q_norm_w);
   const auto kw = static_cast<const bf16_t *>(k_norm_w);
   auto out = static_cast<bf16_t *>(dqkv);
-  if (table_dtype == VK_DTYPE_F32)
-    qknorm_rope_bwd_kernel<float><<<grid, 256, 0, s>>>(qb, qw, kw, static_cast<const float *>(cos_t),
-                                                       static_cast<const float *>(sin_t), table_rows, rope_pos, dq, dk,
-                                                       dv, out, dw_part, n, H, HKV, eps);
-  else
-    qknorm_rope_bwd_kernel<bf16_t><<<grid, 256, 0, s>>>(qb, qw, kw, static_cast<const bf16_t *>(cos_t),
-                                                        static_cast<const bf16_t *>(sin_t), table_rows, rope_pos, dq,
-                                                        dk, dv, out, dw_part, n, H, HKV, eps);
+  const bool fixed = H == 8 && HKV == 2;
+  if (table_dtype == VK_DTYPE_F32) {
+    const auto ct = static_cast<const float *>(cos_t), st = static_cast<const float *>(sin_t);
+    if (fixed)
+      qknorm_rope_bwd_kernel<float, 8, 2><<<grid, 256, 0, s>>>(qb, qw, kw, ct, st, table_rows, rope_pos, dq, dk, dv,
+                                                               out, dw_part, n, H, HKV, eps);
+    else
+      qknorm_rope_bwd_kernel<float, 0, 0><<<grid, 256, 0, s>>>(qb, qw, kw, ct, st, table_rows, rope_pos, dq, dk, dv,
+                                                               out, dw_part, n, H, HKV, eps);
+  } else {
+    const auto ct = static_cast<const bf16_t *>(cos_t), st = static_cast<const bf16_t *>(sin_t);
+    if (fixed)
+      qknorm_rope_bwd_kernel<bf16_t, 8, 2><<<grid, 256, 0, s>>>(qb, qw, kw, ct, st, table_rows, rope_pos, dq, dk,
+                                                                dv, out, dw_part, n, H, HKV, eps);
+    else
+      qknorm_rope_bwd_kernel<bf16_t, 0, 0><<<grid, 256, 0, s>>>(qb, qw, kw, ct, st, table_rows, rope_pos, dq, dk,
+                                                                dv, out, dw_part, n, H, HKV, eps);
+  }
   return launch_status("qknorm_rope_backward");
 }
 
