@@ -57,8 +57,27 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const bf16_t *__restri
       xv[2 * e] = lo_bf(xr[e]);
       xv[2 * e + 1] = hi_bf(xr[e]);
     }
+    if constexpr (sizeof(DT) == 2) {  // 8 bf16 gradients: one 16-byte load
+      const u32x4 gr = *reinterpret_cast<const u32x4 *>(dy + row * TR_D + 8 * lane);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) gv[j] = ld(dy, row * TR_D + 8 * lane + j);
+      for (int e = 0; e < 4; ++e) {
+        gv[2 * e] = lo_bf(gr[e]);
+        gv[2 * e + 1] = hi_bf(gr[e]);
+      }
+    } else {
+      const f32x4 g0 = *reinterpret_cast<const f32x4 *>(dy + row * TR_D + 8 * lane);
+      const f32x4 g1 = *reinterpret_cast<const f32x4 *>(dy + row * TR_D + 8 * lane + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        gv[e] = g0[e];
+        gv[4 + e] = g1[e];
+      }
+    }
+    f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+    if (dres) {
+      d0 = *reinterpret_cast<const f32x4 *>(dres + row * TR_D + 8 * lane);
+      d1 = *reinterpret_cast<const f32x4 *>(dres + row * TR_D + 8 * lane + 4);
+    }
     float ss = 0.f, dot = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -73,7 +92,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const bf16_t *__restri
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       o[j] = r * gv[j] * wv[j] - xv[j] * c;
-      if (dres) o[j] += dres[row * TR_D + 8 * lane + j];
+      if (dres) o[j] += j < 4 ? d0[j] : d1[j - 4];
       dwa[j] += gv[j] * xv[j] * r;
     }
     float *dst = dx + row * TR_D + 8 * lane;
@@ -254,7 +273,9 @@ extern "C" int vk_rmsnorm_backward(const void *x, const void *w, const void *dy,
   VK_CHECK_ARG(x && w && dy && dx && dw_part, "rmsnorm_backward: null pointer");
   if (d != TR_D) return fail(VK_ERR_UNSUPPORTED, "rmsnorm_backward: built for d = %d (got %d)", TR_D, d);
   VK_CHECK_ARG(n >= 0 && (dy_dtype == VK_DTYPE_BF16 || dy_dtype == VK_DTYPE_F32), "rmsnorm_backward: bad arguments");
-  VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w) && vk_aligned16(dx), "rmsnorm_backward: alignment");
+  VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w) && vk_aligned16(dx) && vk_aligned16(dy) &&
+                   (!dres || vk_aligned16(dres)),
+               "rmsnorm_backward: alignment");
   if (n == 0) return VK_OK;
   const unsigned grid = row_grid(n);
   hipStream_t s = VK_STREAM(stream);
