@@ -270,3 +270,18 @@ def test_gspo_update_steps_move_weights():
     moved = sum(int(not torch.equal(p.detach(), b)) for p, b in zip(m.parameters(), before))
     assert moved >= len(before) - 1  # (the embedding rows of unused tokens still move: Adam on zero grads
     #                                     does nothing only at step 1, so allow one untouched tensor)
+
+
+@pytest.mark.parametrize("n", [16 * 1024, 16 * 1024 + 37, 1000])
+def test_weight_gradient_split_k(n):
+    """a^T b of the update's weight gradients: the 16-slice split-K product (with a remainder of rows past the
+    last whole slice, and the single-product path below 16 x 1024 rows) equals the fp64 product rounded once
+    to bf16, up to one bf16 rounding step."""
+    g = gen(n)
+    a = (torch.randn(n, 192, generator=g) * 0.1).to(BF)
+    b = (torch.randn(n, 320, generator=g) * 0.1).to(BF)
+    got = TR._wgrad(a.to(DEV), b.to(DEV)).float().cpu()
+    want = a.double().t() @ b.double()
+    assert got.shape == (192, 320)
+    err = (got.double() - want).abs()
+    assert bool((err <= want.abs() * 2.0 ** -8 + 1e-6).all()), err.max().item()
