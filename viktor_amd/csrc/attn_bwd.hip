@@ -14,7 +14,7 @@
 //   * dQ kernel = the forward's shape: a workgroup per 64-query block x KV head, 8 wavefronts (4 query
 //     heads x 2 halves of 32 rows), K / V tiles of 64 keys double buffered in LDS. Per key half:
 //     S^T = K Q^T, dP^T = V dO^T (A = key rows from LDS, B = Q^T / dO^T held in registers), dS^T in the
-//     accumulator layout, dQ^T += K^T dS^T (A = K^T read column-wise from LDS).
+//     accumulator layout, dQ^T += K^T dS^T (A = K^T from a transposed LDS copy of the tile).
 //   * dK/dV kernel: a workgroup per 128-key block x KV head, 4 wavefronts of 32 keys (two 16-key blocks;
 //     K^T / V^T fragments in registers), looping over the 32-query tiles at or below the diagonal, Q / dO /
 //     lse / D of the 4 query heads staged in LDS (the next tile's loads in flight during the current one),
@@ -33,6 +33,7 @@ namespace vk {
 
 constexpr int AB_H = 8, AB_HKV = 2, AB_D = 64;
 constexpr int AB_PITCH = 72;  // 64 + 8 bf16 per LDS row
+constexpr int AB_KTP = 68;    // keys per row of a transposed K tile (136 B: 8-byte operand reads conflict-free)
 constexpr int AB_KW = 4;      // wavefronts of a dK/dV workgroup (32 keys each: 128 keys per staged query tile)
 constexpr int AB_KB = 32 * AB_KW;
 
@@ -64,8 +65,11 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
     const bf16_t *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ dd,
     const int32_t *__restrict__ cu, const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok,
     float *__restrict__ dq, float scale_log2, float scale) {
+  // K and V rows (the A operands of S^T and dP^T) and a transposed copy of K, [d][key] at AB_KTP keys per row
+  // (the A operand of dQ^T = K^T dS^T: a lane's 8 keys are two 8-byte reads instead of eight 2-byte ones)
   __shared__ __attribute__((aligned(16))) bf16_t Ks[2][64 * AB_PITCH];
   __shared__ __attribute__((aligned(16))) bf16_t Vs[2][64 * AB_PITCH];
+  __shared__ __attribute__((aligned(16))) bf16_t Kt[2][AB_D * AB_KTP];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int col = lane & 15, g = lane >> 4;
   const int hk = blockIdx.y, hq = hk * 4 + (wid & 3), half = wid >> 2;
@@ -116,6 +120,11 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
   auto store_tile = [&](int buf) {
     *reinterpret_cast<u32x4 *>(&Ks[buf][lrow * AB_PITCH + lchunk * 8]) = rk;
     *reinterpret_cast<u32x4 *>(&Vs[buf][lrow * AB_PITCH + lchunk * 8]) = rv;
+#pragma unroll
+    for (int wv = 0; wv < 4; ++wv) {
+      Kt[buf][(lchunk * 8 + 2 * wv) * AB_KTP + lrow] = static_cast<bf16_t>(rk[wv] & 0xffffu);
+      Kt[buf][(lchunk * 8 + 2 * wv + 1) * AB_KTP + lrow] = static_cast<bf16_t>(rk[wv] >> 16);
+    }
   };
   load_tile(0);
   store_tile(0);
@@ -169,14 +178,13 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
                                                     pack_bf(d[6], d[7])});
       }
       // dQ^T += K^T dS^T (key order {4g..4g+3, 16+4g..16+4g+3} in both operands)
+      const bf16_t *ktt = &Kt[buf][32 * ks];
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        bf16x8 ka;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int kl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
-          ka[jj] = __builtin_bit_cast(__bf16, kt[kl * AB_PITCH + 16 * dt + col]);
-        }
+        const bf16_t *kr = ktt + (16 * dt + col) * AB_KTP;
+        const u32x2 lo = *reinterpret_cast<const u32x2 *>(kr + 4 * g);
+        const u32x2 hi = *reinterpret_cast<const u32x2 *>(kr + 16 + 4 * g);
+        const bf16x8 ka = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) acc[dt][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, dsf[qb], acc[dt][qb], 0, 0, 0);
       }
