@@ -37,6 +37,8 @@ Extra objects on the JSON line:
                 (127, 128)) with seeded random weights; ms, chunks/s and the MFMA fraction of its algorithmic
                 flops (convolutions, 4 products per layer, window attention over the keys each frame sees).
 Usage: python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--no-cpu]
+       python bench.py --mode encoder|prefill [--steps N]   (that object alone, N timed repetitions)
+       python bench.py --mode kernels [--group-size G]      (the decode-attention traffic probe)
 """
 
 import argparse
@@ -215,6 +217,34 @@ def encoder_timing(reps=3):
             "achieved_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
 
 
+def prefill_timing(reps=3, prefill_batch=128, group_size=GROUP):
+    """The rollout's shared-prefix prefill alone (64 windows of 2048 frames, one prefill per group): ms per
+    prefill with HIP events, and the achieved rate on prefill_flops."""
+    from viktor_amd import DecodeEngine
+    from viktor_amd.synthetic import frames, uniforms
+    dev = torch.device("cuda", 0)
+    _, gm = build_model(dev)
+    B = PREFIXES * group_size
+    fr = frames(PREFIXES, P, 512, seed=0).to(dev).repeat_interleave(group_size, 0).reshape(-1, 512)
+    eng = DecodeEngine(gm, B, NEW, P, temperature=1.0, prefill_batch=prefill_batch, group_size=group_size)
+    eng.set_uniforms(uniforms(B, NEW, seed=1).to(dev))
+    for _ in range(2):
+        eng.prefill(fr, [P] * B)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for _ in range(reps):
+        eng.prefill(fr, [P] * B)
+    ev[1].record()
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / reps
+    windows = PREFIXES if group_size > 1 else B
+    flops = prefill_flops(windows, P)
+    tflops = flops / (ms / 1e3) / 1e12
+    return {"windows_prefilled": windows, "ms": round(ms, 2), "alg_tflop": round(flops / 1e12, 3),
+            "achieved_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+
 def update_timing(steps=3, warmup=2):
     """One GSPO update micro-batch on the HIP training path (see the module docstring): times and flops."""
     from viktor_amd import train as TR
@@ -310,8 +340,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-batch", type=int, default=128)
-    ap.add_argument("--mode", choices=["rollout", "kernels", "encoder"], default="rollout",
-                    help="kernels: decode-attention traffic probe; encoder: the encoder timing object alone")
+    ap.add_argument("--mode", choices=["rollout", "kernels", "encoder", "prefill"], default="rollout",
+                    help="kernels: decode-attention traffic probe; encoder / prefill: that timing object alone")
     ap.add_argument("--group-size", type=int, default=GROUP, help="sequences sharing one prefix KV copy (1: none)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -323,6 +353,10 @@ def main():
         return
     if args.mode == "encoder":
         print(json.dumps({"encoder": encoder_timing(reps=max(args.steps, 1))}), flush=True)
+        return
+    if args.mode == "prefill":
+        print(json.dumps({"prefill": prefill_timing(reps=max(args.steps, 1), prefill_batch=args.prefill_batch,
+                                                    group_size=args.group_size)}), flush=True)
         return
     from viktor_amd import DecodeEngine
     from viktor_amd.synthetic import frames, uniforms

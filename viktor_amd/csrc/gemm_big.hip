@@ -27,6 +27,7 @@ namespace vk {
 constexpr int GB_BM = 256;   // rows of x per workgroup
 constexpr int GB_BW = 128;   // rows of w per workgroup
 constexpr int GB_BK = 32;    // K per stage
+constexpr int GB_GM = 8;     // row blocks per group of the tile order
 constexpr int GB_STAGES = 3;
 constexpr int GB_ROWB = GB_BK * 2;                   // bytes per LDS row
 constexpr int GB_XTILEB = GB_BM * GB_ROWB;           // 16 KB
@@ -90,7 +91,13 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
   const int xcd = p & 7, idx = p >> 3;
   const int q8 = tiles_total >> 3, r8 = tiles_total & 7;
   const int tile = xcd * q8 + min(xcd, r8) + idx;
-  const int mt = tile / tiles_n, nt = tile % tiles_n;
+  // logical order: groups of GB_GM row blocks, each walked column block by column block (GB_GM row blocks
+  // per column block), so an XCD's resident workgroups share GB_GM A blocks and a few weight blocks in its
+  // L2 instead of every weight block (a bijection: the last group has the remaining row blocks)
+  const int tiles_m = tiles_total / tiles_n;
+  const int grp = tile / (GB_GM * tiles_n), first_m = grp * GB_GM;
+  const int gm = min(tiles_m - first_m, GB_GM), in_grp = tile - grp * GB_GM * tiles_n;
+  const int mt = first_m + in_grp % gm, nt = in_grp / gm;
   const int64_t m0 = static_cast<int64_t>(mt) * GB_BM;
   const int n0 = nt * OUT_COLS;
 
