@@ -51,6 +51,12 @@ def test_argument_errors_return_status_without_device_work():
     assert rc == 1 and b"K" in lib.vk_last_error()
     rc = lib.vk_decode_attention(p, p, p, p, p, 4, 8, 2, 128, 128, 128, 16, None, 0, None)  # head_dim 128
     assert rc == 3
+    rc = lib.vk_linear_residual_big(p, p, p, 4, 96, 64, None, 1.0, p, None)  # N % 128 != 0
+    assert rc == 1 and b"N" in lib.vk_last_error()
+    rc = lib.vk_linear_residual_big(p, p, p, 4, 128, 64, None, 1.0, None, None)  # no sums-of-squares output
+    assert rc == 1 and b"null" in lib.vk_last_error()
+    rc = lib.vk_rmsnorm_apply_ss(p, p, 8, p, p, 4, 12, 1e-6, None)  # d % 8 != 0
+    assert rc == 1 and b"d=12" in lib.vk_last_error()
     with pytest.raises(_lib.HipLibraryError):
         _lib.check(rc, "decode_attention")
 
