@@ -131,18 +131,22 @@ __global__ __launch_bounds__(256) void rmsnorm_apply_ss_kernel(const bf16_t *x, 
 }
 
 // Whether every member of every group of G equal-size members equals the group's first member, bit for bit:
-// a thread per 16-byte chunk of members 1..G-1; a difference stores 1 to *flag (every writer stores the same
-// value).
+// a thread per 16-byte chunk of a group's first member, which it loads once and compares with the same chunk
+// of members 1..G-1 (every byte of the group read once); a difference stores 1 to *flag (every writer stores
+// the same value).
 __global__ __launch_bounds__(256) void group_rows_equal_kernel(const u32x4 *__restrict__ x, int64_t groups, int G,
                                                                int64_t chunks_per_member, int32_t *__restrict__ flag) {
-  const int64_t per_group = static_cast<int64_t>(G - 1) * chunks_per_member;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= groups * per_group) return;
-  const int64_t grp = i / per_group, r = i - grp * per_group;
-  const int64_t m = 1 + r / chunks_per_member, c = r - (m - 1) * chunks_per_member;
-  const u32x4 a = x[(grp * G + m) * chunks_per_member + c];
-  const u32x4 b = x[grp * G * chunks_per_member + c];
-  if (a[0] != b[0] || a[1] != b[1] || a[2] != b[2] || a[3] != b[3]) *flag = 1;
+  if (i >= groups * chunks_per_member) return;
+  const int64_t grp = i / chunks_per_member, c = i - grp * chunks_per_member;
+  const u32x4 *g0 = x + grp * G * chunks_per_member + c;
+  const u32x4 a = g0[0];
+  uint32_t diff = 0;
+  for (int m = 1; m < G; ++m) {
+    const u32x4 b = g0[static_cast<int64_t>(m) * chunks_per_member];
+    diff |= (a[0] ^ b[0]) | (a[1] ^ b[1]) | (a[2] ^ b[2]) | (a[3] ^ b[3]);
+  }
+  if (diff != 0) *flag = 1;
 }
 
 }  // namespace vk
@@ -154,7 +158,7 @@ extern "C" int vk_group_rows_equal(const void *x, int64_t groups, int32_t G, int
   VK_CHECK_ARG(x && flag, "group_rows_equal: null pointer");
   VK_CHECK_ARG(groups >= 0 && G >= 1 && member_bytes >= 0 && member_bytes % 16 == 0 && vk_aligned16(x),
                "group_rows_equal: need 16-byte aligned members of a multiple of 16 bytes");
-  const int64_t total = groups * (G - 1) * (member_bytes / 16);
+  const int64_t total = G > 1 ? groups * (member_bytes / 16) : 0;
   if (total == 0) return VK_OK;
   group_rows_equal_kernel<<<static_cast<unsigned>((total + 255) / 256), 256, 0, VK_STREAM(stream)>>>(
       static_cast<const u32x4 *>(x), groups, G, member_bytes / 16, flag);
