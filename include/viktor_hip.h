@@ -139,19 +139,21 @@ int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32_t K, const
 
 /*
  * Single-query GQA attention against one layer of the KV cache:
- * out[b, h, :] = softmax(q[b, h] . K[b, :len_b, h / (H/HKV)]^T / sqrt(D)) V[b, :len_b, ...]
- * with len_b = clamp(lengths[b], 1, max_len); k_cache/v_cache element (b, s, hk, d) at
- * b * stride_b + s * stride_s + hk * D + d. fp32 online softmax, probabilities rounded to bf16
- * before the PV product (as the reference kernel). Each K/V row is read once for its query-head group.
+ * out[b, h, :] = softmax(q[b, h] . K[r, :len_b, h / (H/HKV)]^T / sqrt(D)) V[r, :len_b, ...]
+ * with len_b = clamp(lengths[b], 1, max_len) and cache row r = rows[b] (rows NULL: r = b);
+ * k_cache/v_cache element (r, s, hk, d) at r * stride_b + s * stride_s + hk * D + d, for
+ * 0 <= r < cache_rows (a sequence whose row falls outside gets a zero output; with rows NULL,
+ * cache_rows must be >= B). fp32 online softmax, probabilities rounded to bf16 before the PV product
+ * (as the reference kernel). Each K/V row is read once for its query-head group.
  * Built for H = 8, HKV = 2, D = 64. workspace: vk_decode_attention_workspace() bytes (may be 0 bytes
  * when no split of the key range is needed; then workspace may be NULL).
- * Replaces decode_attention, viktor/decode_attention.py:11-53 (and the flash_attn_with_kvcache
- * decode of viktor/fast_decoder.py:86-89).
+ * Replaces decode_attention, viktor/decode_attention.py:11-53, and the flash_attn_with_kvcache decode
+ * with cache_batch_idx = seq of viktor/fast_decoder.py:86-89 (rows).
  */
 int vk_decode_attention(const void *q, const void *k_cache, const void *v_cache, const int32_t *lengths,
-                        void *out, int64_t B, int32_t H, int32_t HKV, int32_t D, int64_t stride_b,
-                        int64_t stride_s, int64_t max_len, void *workspace, int64_t workspace_bytes,
-                        void *stream);
+                        const int32_t *rows, int64_t cache_rows, void *out, int64_t B, int32_t H, int32_t HKV,
+                        int32_t D, int64_t stride_b, int64_t stride_s, int64_t max_len, void *workspace,
+                        int64_t workspace_bytes, void *stream);
 
 /* Workspace bytes vk_decode_attention needs for this batch and cache length. */
 int vk_decode_attention_workspace(int64_t B, int32_t H, int64_t max_len, int64_t *bytes);
@@ -209,7 +211,9 @@ int vk_varlen_attention(const void *q, const void *k, const void *v, const int32
  * Logits come either from `logits` [B, V] fp32 (h and w_head NULL), or are computed here as
  * h[B, d] @ w_head[V, d]^T (bf16 inputs, fp32 accumulation), the fused LM head; with norm_w non-NULL, h is
  * the residual stream and the final RMSNorm (weight norm_w, eps) is applied to it first (rounded to bf16).
- * logp_out (optional): log softmax(z / T or z)[nxt] of the chosen token before the grammar rules.
+ * logp_out (optional): log softmax(z / T or z)[nxt] of the chosen token before the grammar rules, stored to
+ * logp_out[b] when logp_stride == 0, else to logp_out[b * logp_stride + col] (the output column, when
+ * 0 <= col < out_cols): one row of per-token log-probabilities per sequence over a whole rollout.
  * Replaces greedy_update (viktor/triton_ops.py:172-209), DecodeEngine._select (viktor/engine.py:79-89)
  * and the head + index_copy bookkeeping of DecodeEngine._step (viktor/engine.py:91-116).
  */
@@ -220,7 +224,8 @@ int vk_select_update(const float *logits, const void *h, const void *norm_w, flo
                      int64_t *run, int64_t *pos, const int64_t *plen, const int64_t *rope_off,
                      const int64_t *cache_base, int64_t *out,
                      int64_t out_stride, int64_t out_cols, int32_t *pos32, int32_t *seqlens, int32_t *rpos32,
-                     float *logp_out, int64_t B, int32_t V, int32_t eos, int32_t pad, void *stream);
+                     float *logp_out, int64_t logp_stride, int64_t B, int32_t V, int32_t eos, int32_t pad,
+                     void *stream);
 
 /*
  * Decode-step fusions (small M: one row per sequence). Same rounding points as the unfused ops.

@@ -74,30 +74,41 @@ def qk_norm_rope_fused(x, w, cos, sin, eps):
     return torch.cat([bf(y1 * c - y2 * s), bf(y1 * s + y2 * c)], -1)
 
 
-def attention_rows(q, k, v, causal_shift=None):
-    """Exact fp32 softmax attention of one sequence. q [Tq, H, D], k/v [Tk, Hkv, D]; query r sits at key
-    position causal_shift + r when causal_shift is not None. Returns [Tq, H, D] fp32."""
+def attention_rows(q, k, v, causal_shift=None, p_bf16=False):
+    """Exact fp32 softmax attention of one sequence. q [Tq, H, D], k/v [Tk, Hkv, D]; query head h reads KV
+    head h // (H / Hkv) (GQA, viktor/decoder.py:91-105 repeat_interleave); query r sits at key position
+    causal_shift + r when causal_shift is not None. Returns [Tq, H, D] fp32.
+    p_bf16: the flash-attention rounding point -- the unnormalised weights exp(s - max) are rounded to bf16
+    for the PV product while the normaliser sums them unrounded (viktor/decode_attention.py:27-37 stores
+    p.to(v.dtype) the same way): o = sum_j bf16(e_j) v_j / sum_j e_j."""
     Tq, H, D = q.shape
     Tk, Hkv, _ = k.shape
     rep = H // Hkv
-    kk = k.repeat_interleave(rep, 1)  # [Tk, H, D]
-    vv = v.repeat_interleave(rep, 1)
-    s = torch.einsum("qhd,khd->hqk", q, kk) / math.sqrt(D)
+    qg = q.reshape(Tq, Hkv, rep, D)
+    s = torch.einsum("qgrd,kgd->grqk", qg, k) / math.sqrt(D)  # [Hkv, rep, Tq, Tk]
     if causal_shift is not None:
         qp = causal_shift + torch.arange(Tq)[:, None]
         kp = torch.arange(Tk)[None, :]
-        s = s.masked_fill((kp > qp)[None], float("-inf"))
-    p = torch.softmax(s, -1)
-    return torch.einsum("hqk,khd->qhd", p, vv)
+        s = s.masked_fill((kp > qp)[None, None], float("-inf"))
+    if not p_bf16:
+        p = torch.softmax(s, -1)
+        return torch.einsum("grqk,kgd->qgrd", p, v).reshape(Tq, H, D)
+    e = torch.exp(s - s.amax(-1, keepdim=True))
+    o = torch.einsum("grqk,kgd->grqd", bf(e), v) / e.sum(-1, keepdim=True)
+    return o.permute(2, 0, 1, 3).reshape(Tq, H, D)
 
 
 # ---------------------------------------------------------------------------------------------
 class RefModel:
     """fp32 CPU copy of a Basecaller's projector + decoder weights, run in one numerics mode."""
 
-    def __init__(self, model, mode="fp32", table_bf16=None):
+    def __init__(self, model, mode="fp32", table_bf16=None, p_bf16=False):
+        """p_bf16 (fused mode): attention weights rounded to bf16 before the PV product, the rounding point of
+        flash-attention and of the reference's decode kernel (attention_rows). Off by default: the two choices
+        bracket the reference's bf16 rounding noise."""
         assert mode in ("fp32", "fused")
         self.mode = mode
+        self.p_bf16 = bool(p_bf16) and mode == "fused"
         self.cfg = model.decoder.cfg
         self.k = model.tokenizer.k
         self.strings = list(model.tokenizer.strings)
@@ -120,6 +131,7 @@ class RefModel:
         """A RefModel of a bare Decoder (no projector / tokenizer): for decoder_forward and head only."""
         self = cls.__new__(cls)
         self.mode, self.cfg = mode, dec.cfg
+        self.p_bf16 = False
         sd = {f"decoder.{n}": p.detach().float().cpu().clone() for n, p in dec.named_parameters()}
         self.p = {n: bf(t) for n, t in sd.items()} if mode == "fused" else sd
         cos, sin = rope_tables(dec.cfg.head_dim, dec.cfg.max_seq_len, dec.cfg.rope_theta)
@@ -167,7 +179,7 @@ class RefModel:
         K = torch.cat([K0, k]) if K0 is not None else k
         Vv = torch.cat([V0, v]) if V0 is not None else v
         kv[i] = (K, Vv)
-        o = attention_rows(q, K, Vv, causal_shift=causal_shift)
+        o = attention_rows(q, K, Vv, causal_shift=causal_shift, p_bf16=self.p_bf16)
         if fused:
             o = bf(o)
             x, h = add_rmsnorm_fused(x, linear_fused(o.reshape(T, -1), self.L(i, "attn.o_proj.weight")),
@@ -300,13 +312,18 @@ class RefEngine:
     """DecodeEngine semantics on the CPU (viktor/engine.py:31-220, torch backend; supplied-uniform
     sampling instead of device Gumbel noise). One sequence at a time; KV cache as per-layer tensors."""
 
-    def __init__(self, ref: RefModel, max_new, temperature=0.0, max_homopolymer=64):
+    def __init__(self, ref: RefModel, max_new, temperature=0.0, max_homopolymer=64, bias=None):
+        """bias: [V] additive logit bias replacing the engine's default (-inf at PAD and BOS), e.g. one that
+        also bans EOS so that every sequence runs to max_new (DecodeEngine.bias is the same tensor)."""
         self.ref = ref
         self.max_new = max_new
         self.T = float(temperature)
         V = ref.V
-        self.bias = torch.zeros(V)
-        self.bias[[PAD, BOS]] = float("-inf")
+        if bias is None:
+            bias = torch.zeros(V)
+            bias[[PAD, BOS]] = float("-inf")
+        self.bias = bias.detach().float().cpu().clone()
+        assert self.bias.shape == (V,)
         self.homo_stop = max_homopolymer // ref.k if max_homopolymer else 0
 
     def _choose(self, logits, prev, run, u):
@@ -322,7 +339,7 @@ class RefEngine:
     def run(self, frames_list, steps=None, uniforms=None, forced=None):
         """frames_list: per sequence [L_b, d_enc] fp32. steps: output tokens (default max_new).
         forced [B, steps]: tokens to feed back instead of the oracle's own (teacher forcing on another
-        implementation's stream). Returns dict(tokens, choice, margin, logits) with choice = the oracle's
+        implementation's stream). Entries of frames_list that are the same tensor object are prefilled once. Returns dict(tokens, choice, margin, logits) with choice = the oracle's
         token at each position given the (forced) history, margin = top-2 gap (greedy) or distance of the
         uniform to a CDF boundary (sampled)."""
         ref = self.ref
@@ -334,12 +351,18 @@ class RefEngine:
         logit_rows = torch.zeros(B, steps, ref.V)
         fused = ref.mode == "fused"
         s = ref.pos_scale
+        prefilled = {}  # id(frames) -> (kv after the prefix, BOS hidden): members of one group share it
         for b, fr in enumerate(frames_list):
             n = fr.shape[0]
-            kv = ref.new_kv()
-            x = torch.cat([ref.project(fr), ref.embed(torch.tensor([BOS]))])
-            rpos = torch.arange(n + 1) * s if s != 1 else torch.arange(n + 1)
-            h = ref.run(x, rpos, kv, 0)[-1:]
+            hit = prefilled.get(id(fr))
+            if hit is None:
+                kv = ref.new_kv()
+                x = torch.cat([ref.project(fr), ref.embed(torch.tensor([BOS]))])
+                rpos = torch.arange(n + 1) * s if s != 1 else torch.arange(n + 1)
+                h = ref.run(x, rpos, kv, 0)[-1:]
+                prefilled[id(fr)] = (list(kv), h)
+            else:  # layer() appends by concatenation, so the shared prefix tensors are never written
+                kv, h = list(hit[0]), hit[1]
             prev, run = BOS, 0
             for j in range(steps):
                 # prefill token from bf16 logits; later greedy steps fp32, sampled steps bf16

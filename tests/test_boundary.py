@@ -49,8 +49,15 @@ def test_argument_errors_return_status_without_device_work():
     p = ctypes.cast(buf, ctypes.c_void_p)
     rc = lib.vk_linear(p, p, p, 4, 8, 30, 0, 0, None)  # K % 32 != 0
     assert rc == 1 and b"K" in lib.vk_last_error()
-    rc = lib.vk_decode_attention(p, p, p, p, p, 4, 8, 2, 128, 128, 128, 16, None, 0, None)  # head_dim 128
+    rc = lib.vk_decode_attention(p, p, p, p, None, 4, p, 4, 8, 2, 128, 128, 128, 16, None, 0, None)  # head_dim 128
     assert rc == 3
+    # a cache of 2 sequence rows cannot serve 4 queries without a row map
+    rc = lib.vk_decode_attention(p, p, p, p, None, 2, p, 4, 8, 2, 64, 3072 * 128, 128, 3072, None, 0, None)
+    assert rc == 1 and b"cache holds 2 rows" in lib.vk_last_error()
+    # logp_stride below the output columns would overlap rows
+    rc = lib.vk_select_update(p, None, None, 1e-6, None, 0, 0, p, p, p, 0, 0.0, None, 0, 0, p, None, p, None,
+                              None, None, p, 16, 16, None, None, None, p, 8, 4, 7, 2, 0, None)
+    assert rc == 1 and b"logp_stride" in lib.vk_last_error()
     rc = lib.vk_linear_residual_big(p, p, p, 4, 96, 64, None, 1.0, p, None)  # N % 128 != 0
     assert rc == 1 and b"N" in lib.vk_last_error()
     rc = lib.vk_linear_residual_big(p, p, p, 4, 128, 64, None, 1.0, None, None)  # no sums-of-squares output
@@ -77,6 +84,21 @@ def test_product_has_no_cpu_fallback():
         m.decoder(torch.zeros(1, 4, 512))
     with pytest.raises(_lib.HipLibraryError):
         DecodeEngine(m, 2, 4, 8)
+
+
+def test_unknown_backends_raise_value_error():
+    """viktor/fast_decoder.py:29-30 and the engine's backend argument: only the HIP kernels exist here
+    ('auto' / 'hip'; 'triton' is accepted as the reference's other in-tree name), anything else is a
+    ValueError before any device work."""
+    from viktor_amd import DecodeEngine
+    from viktor_amd.fast_decoder import FastDecoder
+    m = make_model(1, n_layers=1)
+    for name in ("flash", "torch", ""):
+        with pytest.raises(ValueError, match="backend"):
+            FastDecoder(m.decoder, attention_backend=name)
+    with pytest.raises(ValueError, match="backend"):
+        DecodeEngine(m, 2, 4, 8, backend="torch")
+    assert FastDecoder(m.decoder, attention_backend="triton").attention_backend == "hip"
 
 
 def test_missing_library_fails_loudly(tmp_path):

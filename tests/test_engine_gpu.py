@@ -11,6 +11,7 @@ Bars (from the benchmark definition):
 
 import copy
 
+import numpy as np
 import pytest
 import torch
 
@@ -33,18 +34,78 @@ def gpu_copy(m):
     return g.eval()
 
 
-def check_stream(gpu_out, oracle_res, steps, thr):
+def check_stream(gpu_out, oracle_res, steps, thr, min_live=None):
+    """Bar 1 (and bar 3 for the token ids) over the first `steps` columns. Returns (agreement, mismatches).
+    min_live: the smallest allowed fraction of compared positions that are live -- not a PAD after EOS,
+    which the grammar forces whatever the logits are."""
     choice, margin = oracle_res["choice"], oracle_res["margin"]
     got = gpu_out[:, :steps].cpu()
     agree = got == choice
     exempt = margin < thr
     bad = ~(agree | exempt)
     assert not bool(bad.any()), f"mismatch at {bad.nonzero()[:8].tolist()}"
+    if min_live is not None:
+        live = float((got != R.PAD).float().mean())
+        assert live >= min_live, f"only {live:.3f} of the compared positions are live"
     return float(agree.float().mean()), int((~agree).sum())
 
 
+def no_eos_bias(V):
+    """The engine's default bias with EOS banned too: sequences stay live for every step, so each compared
+    position is a real choice (with max_homopolymer=None no grammar rule ends them either, k = 1)."""
+    b = torch.zeros(V)
+    b[[R.PAD, R.BOS, R.EOS]] = float("-inf")
+    return b
+
+
+def _chosen_logprobs(res, forced, bias, T):
+    z = res["logits"] + bias
+    if T > 0:
+        z = z / T
+    steps = z.shape[1]
+    return torch.log_softmax(z.double(), -1).gather(-1, forced[:, :steps, None].long())[..., 0]
+
+
+def check_logprobs(eng_logp, oracle_res, forced, bias, T, tol=2e-2, pair_res=None):
+    """Bar 2 on the rollout's own log-probabilities: the engine's logp[b, j] against log softmax of the
+    oracle's teacher-forced logits (+ bias, / T) at the engine's token. Returns (max difference, fraction
+    of positions within tol).
+
+    pair_res None: every position within tol (greedy decode steps choose from fp32 logits).
+    pair_res: the same teacher-forced run of an oracle that differs in one rounding point (bf16 attention
+    weights). Sampled steps choose from bf16-rounded logits, as the reference's bf16 nn.Linear head makes
+    them (viktor/engine.py:112, 191), where one ulp is 1.6e-2 at |z| in [2, 4): a hidden state that moves by
+    bf16 rounding noise moves some log-probs past 2e-2, and the oracle pair shows how far. Then >= 97% of the
+    positions lie within tol; against the pair's spread, the mean and the fraction beyond tol stay within
+    1.25x / 1.5x, the 99.5th percentile within 1.3x and the max within 2x (a single extreme is a noisy
+    statistic); per sequence, mean_j(lp - lp_oracle) -- the GSPO ratio's log -- stays within 2x of the pair's
+    largest plus 1e-3, and the ratio itself within 5e-3 of 1."""
+    steps = oracle_res["logits"].shape[1]
+    want = _chosen_logprobs(oracle_res, forced, bias, T)
+    signed = eng_logp[:, :steps].double().cpu() - want
+    diff = signed.abs()
+    err, within = float(diff.max()), float((diff <= tol).float().mean())
+    if pair_res is None:
+        assert err <= tol, (err, (diff > tol).nonzero()[:5].tolist())
+        return err, within
+    dps = _chosen_logprobs(pair_res, forced, bias, T) - want
+    dp = dps.abs()
+    p_max, p_mean, p_out = float(dp.max()), float(dp.mean()), float((dp > tol).float().mean())
+    q, pq = float(torch.quantile(diff.flatten(), 0.995)), float(torch.quantile(dp.flatten(), 0.995))
+    seq, pseq = signed.mean(1).abs(), dps.mean(1).abs()
+    print(f"  logprobs: HIP-oracle max {err:.2e} q99.5 {q:.2e} mean {float(diff.mean()):.2e} beyond {1 - within:.4f}"
+          f" seq {float(seq.max()):.1e}; oracle pair max {p_max:.2e} q99.5 {pq:.2e} mean {p_mean:.2e} beyond "
+          f"{p_out:.4f} seq {float(pseq.max()):.1e}")
+    assert within >= 0.97, within
+    assert float(diff.mean()) <= 1.25 * p_mean + 1e-4 and 1 - within <= 1.5 * p_out + 5e-3, (diff.mean(), p_mean)
+    assert q <= 1.3 * pq + 2e-3 and err <= 2 * p_max + 1e-3, (q, pq, err, p_max)
+    assert float(seq.max()) <= 2 * float(pseq.max()) + 1e-3, (seq.tolist(), pseq.tolist())
+    assert float((signed.mean(1).exp() - 1).abs().max()) <= 5e-3
+    return err, within
+
+
 def run_case(k=1, n_layers=2, lens=(40, 130, 257, 75), steps=24, T=0.0, mh=8, seed=0, ps=1, graph=True, group=1,
-             check_every=32, decode_steps="fixed"):
+             check_every=32, decode_steps="fixed", ban_eos=False):
     m = make_model(k, n_layers=n_layers, seed=seed, norm_jitter=0.1, bias_jitter=0.1)
     m.pos_scale = ps
     lens = list(lens)
@@ -56,19 +117,31 @@ def run_case(k=1, n_layers=2, lens=(40, 130, 257, 75), steps=24, T=0.0, mh=8, se
     gm = gpu_copy(m)
     eng = DecodeEngine(gm, len(lens), steps, max(lens), cuda_graph=graph, temperature=T, max_homopolymer=mh,
                        prefill_batch=3, group_size=group, check_every=check_every)
+    bias = None
+    if ban_eos:
+        bias = no_eos_bias(m.tokenizer.vocab_size)
+        eng.bias.copy_(bias)
     if T > 0:
         eng.set_uniforms(u.to(DEV))
     out = eng.generate(fr.to(DEV), lens, steps=steps if decode_steps == "fixed" else None).clone()
     torch.cuda.synchronize()
-    ref = R.RefEngine(R.RefModel(m, "fused"), steps, temperature=T, max_homopolymer=mh)
+    ref = R.RefEngine(R.RefModel(m, "fused"), steps, temperature=T, max_homopolymer=mh, bias=bias)
     res = ref.run(list(fr.split(lens)), uniforms=u if T > 0 else None, forced=out.cpu())
     return out, res, eng
 
 
 def test_greedy_stream_parity_k1():
-    out, res, _ = run_case(k=1)
-    agree, n_exempt = check_stream(out, res, 24, 1e-2)
+    out, res, _ = run_case(k=1, mh=None, ban_eos=True)
+    agree, n_exempt = check_stream(out, res, 24, 1e-2, min_live=1.0)
     assert agree > 0.95
+
+
+def test_greedy_stream_grammar_rules_fire():
+    """The grammar's own path (homopolymer cap of 8 bases, EOS allowed): streams end early and the PAD after
+    EOS is checked as well."""
+    out, res, _ = run_case(k=1)
+    check_stream(out, res, 24, 1e-2)
+    assert bool((out.cpu() == R.EOS).any())
 
 
 def test_greedy_stream_parity_k4():
@@ -77,8 +150,8 @@ def test_greedy_stream_parity_k4():
 
 
 def test_sampled_stream_parity():
-    out, res, _ = run_case(k=1, T=1.0, steps=32, lens=(50, 300, 120, 9))
-    check_stream(out, res, 32, 5e-3)
+    out, res, _ = run_case(k=1, T=1.0, steps=32, lens=(50, 300, 120, 9), mh=None, ban_eos=True)
+    check_stream(out, res, 32, 5e-3, min_live=1.0)
 
 
 def test_grouped_greedy_stream_parity():
@@ -92,8 +165,8 @@ def test_grouped_greedy_stream_parity():
 
 
 def test_grouped_sampled_stream_parity():
-    out, res, _ = run_case(k=1, T=1.0, steps=32, lens=(50, 300, 9), group=8)
-    check_stream(out, res, 32, 5e-3)
+    out, res, _ = run_case(k=1, T=1.0, steps=32, lens=(50, 300, 9), group=8, mh=None, ban_eos=True)
+    check_stream(out, res, 32, 5e-3, min_live=1.0)
 
 
 def test_grouped_matches_ungrouped_engine():
@@ -135,9 +208,9 @@ def test_pos_scale_stream_parity():
 
 
 def test_full_depth_long_prefix_parity():
-    """8 layers, 2048-frame prefixes (the rollout configuration's shapes), 2 sequences."""
-    out, res, _ = run_case(k=1, n_layers=8, lens=(2048, 1500), steps=12, T=1.0, mh=64, seed=3)
-    check_stream(out, res, 12, 5e-3)
+    """8 layers, 2048-frame prefixes (the rollout configuration's shapes), 2 sequences, 48 live steps."""
+    out, res, _ = run_case(k=1, n_layers=8, lens=(2048, 1500), steps=48, T=1.0, mh=None, seed=3, ban_eos=True)
+    check_stream(out, res, 48, 5e-3, min_live=1.0)
 
 
 def test_graph_equals_eager_bitwise():
@@ -274,11 +347,18 @@ def test_teacher_forced_logprobs_parity():
 
 def test_scoring_at_scale():
     """The scoring configuration's sizes: 512 sequences x (2048-frame prefix + 700..1024 response tokens),
-    8 layers, vocab 7: token log-probs and masks. Finite everywhere; the first and last sequences against the
-    oracle. At this depth and length two bf16 computations of the reference already differ by about 0.04 at the
-    worst token (the oracle's bf16 rounding-point mode against its fp32 mode), so the 2e-2 bar of the small
-    shapes is replaced here by: the HIP path is as accurate as the oracle's bf16 mode, both measured against fp32
-    (max within 1.5x, mean within 1.2x), and its mean deviation from the bf16 mode is under 1e-2."""
+    8 layers, vocab 7: token log-probs and masks, finite everywhere, and four sequences (first, last, two
+    inner) against the oracle.
+
+    Bar 2 per token (2e-2 abs) holds at the small shapes (test_teacher_forced_logprobs_parity). At 3072
+    positions x 8 layers the bf16 rounding points alone spread a token's log-prob by sigma ~ 9e-3: two
+    restatements of the reference that differ in ONE rounding point (attention weights rounded to bf16 before
+    the PV product, as flash-attention does, or not) already disagree by up to ~4e-2 with ~4% of the tokens
+    beyond 2e-2. So here the HIP path must be indistinguishable from that noise:
+      * against the oracle (fused rounding points): |dlp| <= 2e-2 on >= 95% of the masked tokens, and the
+        max / mean / fraction beyond 2e-2 within 1.5x / 1.15x / 1.5x of the oracle pair's own;
+      * against fp32: no further off than the oracle's bf16 mode (max, mean, fraction beyond 2e-2 within 1.15x);
+      * the GSPO ratio (bar 2 on ratios): per sequence, exp(mean_t(lp - lp_oracle)) within 2e-3 of 1."""
     from viktor_amd.synthetic import scoring_inputs
     m = make_model(1, n_layers=8, seed=14, norm_jitter=0.1, bias_jitter=0.1)
     gm = gpu_copy(m)
@@ -292,19 +372,79 @@ def test_scoring_at_scale():
     assert lp.shape[0] == B and bool(torch.isfinite(lp[mask]).all())
     n_tok = mask.sum(1)
     assert n_tok.tolist() == [len(s) + 1 for s in seqs]  # every base + the EOS of an ended call (k = 1)
-    pick = [0, B - 1]
+    pick = [0, 171, 342, B - 1]
     tin, tgt, _ = m.batch([seqs[i] for i in pick], pad_to=128)
     f, pl = fr[pick].cpu(), plens[pick].cpu()
     l16 = R.token_logprobs_ref(R.RefModel(m, "fused").logits(f, tin, pl), tgt)
+    l16p = R.token_logprobs_ref(R.RefModel(m, "fused", p_bf16=True).logits(f, tin, pl), tgt)
     l32 = R.token_logprobs_ref(R.RefModel(m, "fp32").logits(f, tin, pl), tgt)
     m_ref = R.sampled_mask_ref(tgt, [seqs[i] for i in pick], [ended[i] for i in pick], 1)
     T = l16.shape[1]
     got = lp[pick][:, :T].cpu()
     assert torch.equal(mask[pick][:, :T].cpu(), m_ref)
-    e_hip, e_bf16 = (got - l32)[m_ref].abs(), (l16 - l32)[m_ref].abs()
-    assert e_hip.max() <= 1.5 * e_bf16.max() and e_hip.mean() <= 1.2 * e_bf16.mean(), (
-        float(e_hip.max()), float(e_bf16.max()), float(e_hip.mean()), float(e_bf16.mean()))
-    assert (got - l16)[m_ref].abs().mean() < 1e-2
+
+    def spread(a, b):
+        d = (a - b)[m_ref].abs()
+        return float(d.max()), float(d.mean()), float((d > 2e-2).float().mean())
+
+    hip_or, pair, hip_32, or_32 = spread(got, l16), spread(l16p, l16), spread(got, l32), spread(l16, l32)
+    print("scoring (max, mean, frac > 2e-2): HIP-oracle %s, oracle pair %s, HIP-fp32 %s, oracle-fp32 %s" % tuple(
+        "(%.2e, %.2e, %.3f)" % t for t in (hip_or, pair, hip_32, or_32)))
+    assert hip_or[2] <= 0.05, hip_or
+    assert hip_or[0] <= 1.5 * pair[0] and hip_or[1] <= 1.15 * pair[1] and hip_or[2] <= 1.5 * pair[2] + 1e-3
+    assert hip_32[0] <= 1.15 * or_32[0] and hip_32[1] <= 1.15 * or_32[1] and hip_32[2] <= 1.15 * or_32[2] + 1e-3
+    log_ratio = torch.stack([(got - l16)[b][m_ref[b]].mean() for b in range(len(pick))])
+    print("per-sequence mean lp - oracle:", ["%.1e" % float(x) for x in log_ratio])
+    assert float((log_ratio.exp() - 1).abs().max()) <= 2e-3
+
+
+def test_scoring_loss_and_gradient_at_scale():
+    """The scoring configuration's loss: [512, 1024, 7] logits, responses of 700..1024 tokens, old = new +
+    N(0, 0.05), clip [1 - 3e-4, 1 + 4e-4], advantages of Beta(8, 2) rewards in groups of 8
+    (scripts/gspo.py:446-450, 459-477). The kernel's lp, s, loss and dL/dlogits against the fp64 closed form
+    of the oracle (and the ratio's clip branches both taken)."""
+    g = torch.Generator().manual_seed(40)
+    B, T, V = 512, 1024, 7
+    logits = R.bf(torch.randn(B, T, V, generator=g) * 2)
+    lens = torch.randint(700, T + 1, (B,), generator=g)
+    targets = torch.randint(3, V, (B, T), generator=g)
+    pos = torch.arange(T)[None]
+    targets[pos == (lens - 1)[:, None]] = R.EOS
+    targets[pos >= lens[:, None]] = R.PAD
+    mask = targets != R.PAD
+    lp_true = R.token_logprobs_ref(logits, targets)
+    old = lp_true + torch.randn(B, T, generator=g) * 0.05
+    n_bases = (lens - 1).float()
+    r = np.random.default_rng(41).beta(8.0, 2.0, size=(B // 8, 8))  # the rollout's rewards: 64 groups of 8
+    adv_np, _ = R.advantages_ref(r)
+    adv = torch.from_numpy(adv_np).float().reshape(B)
+    eps_lo, eps_hi = 3e-4, 4e-4
+    res = G.ops.gspo_score(logits.to(BF).to(DEV), targets.to(DEV), mask.to(DEV), old.to(DEV), n_bases.to(DEV),
+                           adv.to(DEV), eps_lo, eps_hi, inv_n=1.0 / B)
+    want = R.gspo_grad_closed_form(logits, targets, mask, old, n_bases, adv, eps_lo, eps_hi, 1.0 / B)
+    lp64 = torch.log_softmax(logits.double(), -1).gather(-1, targets.clamp(min=0)[..., None])[..., 0]
+    s64 = torch.exp(((lp64 - old.double()) * mask).sum(1) / n_bases.double())
+    A = adv.double()
+    pg64 = -torch.minimum(s64 * A, s64.clamp(1 - eps_lo, 1 + eps_hi) * A)
+    loss64 = float(pg64.sum() / B)
+    assert (res["lp"].cpu().double() - lp64)[mask].abs().max() < 1e-5
+    assert torch.allclose(res["s"].cpu().double(), s64, rtol=1e-4)
+    assert abs(float(res["loss"]) - loss64) <= 1e-4 * abs(loss64) + 1e-7
+    d = res["dlogits"].cpu().double()
+    assert torch.allclose(d, want, rtol=1e-3, atol=1e-9), float((d - want).abs().max())
+    clipped_hi = (A > 0) & (s64 > 1 + eps_hi)
+    clipped_lo = (A < 0) & (s64 < 1 - eps_lo)
+    assert bool(clipped_hi.any()) and bool(clipped_lo.any()) and bool((~clipped_hi & ~clipped_lo).any())
+    assert bool((d[clipped_hi | clipped_lo] == 0).all())
+    # the same through the autograd surface (sequence_ratio_loss), which the update's backward runs
+    z = logits.to(DEV).requires_grad_(True)
+    loss, s_, pg_, lp_ = G.sequence_ratio_loss(z, targets.to(DEV), mask.to(DEV), old.to(DEV), n_bases.to(DEV),
+                                              adv.to(DEV), eps_lo, eps_hi)
+    loss.backward()
+    assert abs(float(loss) - loss64) <= 1e-4 * abs(loss64) + 1e-7
+    assert torch.allclose(z.grad.cpu().double(), want, rtol=1e-3, atol=1e-9)
+    with pytest.raises(RuntimeError):  # s / pg / lp carry no gradient of their own
+        s_.sum().backward()
 
 
 def test_decoder_forward_parity():

@@ -211,6 +211,31 @@ def test_decode_attention_cache_view_and_graph():
     assert (eager.float().cpu() - ref).abs().max() < 1e-2
 
 
+@pytest.mark.parametrize("B,S", [(6, 300), (700, 97)])
+def test_decode_attention_row_map(B, S):
+    """rows[b] picks sequence b's cache row (flash_attn_with_kvcache's cache_batch_idx at
+    viktor/fast_decoder.py:86-89): a permutation over a larger cache, a repeated row, and a row outside the
+    cache (zero output). Small B splits the key range (combine kernel), large B does not."""
+    torch.manual_seed(B)
+    Bc = B + 3
+    q = torch.randn(B, 8, 64).to(BF)
+    k = torch.randn(Bc, S, 2, 64).to(BF)
+    v = torch.randn(Bc, S, 2, 64).to(BF)
+    rows = torch.randperm(Bc)[:B].int()
+    rows[1] = rows[0]
+    rows[2] = Bc + 5  # outside the cache
+    lens = torch.randint(1, S + 1, (B,)).int()
+    out = ops.decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), lens.to(DEV), rows=rows.to(DEV)).float().cpu()
+    valid = (rows >= 0) & (rows < Bc)
+    r = rows.clamp(0, Bc - 1).long()
+    ref = _sdpa_ref(q, k[r], v[r], lens)
+    assert (out[valid] - ref[valid]).abs().max() < 1e-2
+    assert torch.equal(out[2], torch.zeros(8, 64))
+    # without a row map the cache must hold one row per query: checked before any launch
+    with pytest.raises(AssertionError, match="cache holds"):
+        ops.decode_attention(q.to(DEV), k[:B - 1].to(DEV), v[:B - 1].to(DEV), lens.to(DEV))
+
+
 @pytest.mark.parametrize("G,pre_max,suf_max", [(8, 2049, 1024), (4, 700, 33), (2, 65, 300), (16, 513, 64)])
 def test_decode_attention_grouped(G, pre_max, suf_max):
     """Groups of G sequences share prefix rows [0, prefix_len) and own suffix rows [0, suffix_len): equal to
@@ -443,6 +468,71 @@ def test_select_update(V, T, fused_head):
     for b in range(B):
         if 0 <= int(c[b]) < max_new:
             assert int(oc[b, c[b]]) == int(got[b])
+
+
+@pytest.mark.parametrize("T", [0.0, 0.8])
+def test_select_update_logprob_rows(T):
+    """logp_out [B, T]: the chosen token's log-probability goes to the column the token is written to,
+    log softmax((z + bias) / T)[token] (greedy: of z + bias), computed here in fp64."""
+    g = gen(31)
+    B, V, max_new = 50, 343, 16
+    bias = torch.zeros(V)
+    bias[[R.PAD, R.BOS, R.EOS]] = float("-inf")
+    logits = torch.randn(B, V, generator=g) * 2
+    plen = torch.randint(10, 40, (B,), generator=g)
+    pos = plen + torch.randint(0, max_new, (B,), generator=g)
+    tok = torch.full((B,), 5, dtype=torch.long)
+    u = torch.rand(B, max_new, generator=g)
+    d_tok, d_pos = to_dev(tok), to_dev(pos)
+    lp = torch.full((B, max_new), 7.0, device=DEV)
+    out = torch.full((B, max_new), R.PAD, dtype=torch.long, device=DEV)
+    ops.select_update(to_dev(bias), torch.zeros(V, dtype=torch.bool, device=DEV), torch.zeros(V, dtype=torch.bool,
+                      device=DEV), 0, d_tok, torch.zeros(B, dtype=torch.long, device=DEV), d_pos, to_dev(plen),
+                      torch.zeros(B, dtype=torch.long, device=DEV), out, None, None, None, R.EOS, R.PAD,
+                      logits=to_dev(logits), temperature=T, uniforms=to_dev(u), logp_out=lp)
+    z = (logits.double() + bias.double()) / (T if T > 0 else 1.0)
+    want = torch.log_softmax(z, -1).gather(1, d_tok.cpu()[:, None])[:, 0]
+    col = (pos - plen).long()
+    got = lp.cpu()
+    assert (got[torch.arange(B), col].double() - want).abs().max() < 1e-5
+    untouched = torch.ones(B, max_new, dtype=torch.bool)
+    untouched[torch.arange(B), col] = False
+    assert bool((got[untouched] == 7.0).all())
+
+
+def test_greedy_update_reference_signature():
+    """hip_ops.greedy_update with viktor/triton_ops.py:200-209's argument list: first-index argmax of
+    logits + bias, tail -> EOS, homopolymer run -> EOS, PAD after EOS / PAD, out[b, pos - plen] and the
+    pos / pos32 / seqlens / rpos32 advance."""
+    g = gen(77)
+    B, V, max_new = 64, 7, 32
+    bias = torch.zeros(V)
+    bias[[R.PAD, R.BOS]] = float("-inf")
+    tail = torch.zeros(V, dtype=torch.bool)
+    tail[6] = True
+    homo = torch.zeros(V, dtype=torch.bool)
+    homo[3:7] = True
+    homo_stop = 3
+    tok, run, pos, plen, rope_off = _state(B, V, g)
+    logits = torch.randn(B, V, generator=g) * 2
+    logits[7, 3] = logits[7, 5] = 40.0  # tie: the first index wins
+    tok[7], run[7] = 4, 0
+    want_tok, want_run, _ = _select_ref(logits, tok, run, bias, tail, homo, homo_stop, 0.0, torch.zeros(B))
+    d = {n: to_dev(t) for n, t in dict(tok=tok, run=run, pos=pos, plen=plen, rope_off=rope_off).items()}
+    out = torch.full((B, max_new), R.PAD, dtype=torch.long, device=DEV)
+    pos32 = torch.zeros(B, dtype=torch.int32, device=DEV)
+    seql, rpos = torch.zeros_like(pos32), torch.zeros_like(pos32)
+    ops.greedy_update(to_dev(logits), to_dev(bias), to_dev(tail), to_dev(homo), homo_stop, d["tok"], d["run"],
+                      d["pos"], d["plen"], d["rope_off"], out, pos32, seql, rpos, R.EOS, R.PAD)
+    assert torch.equal(d["tok"].cpu(), want_tok) and torch.equal(d["run"].cpu(), want_run)
+    assert int(want_tok[7]) == 3
+    assert torch.equal(d["pos"].cpu(), pos + 1) and torch.equal(pos32.cpu(), (pos + 1).int())
+    assert torch.equal(seql.cpu(), (pos + 2).int()) and torch.equal(rpos.cpu(), (pos + 1 + rope_off).int())
+    oc = out.cpu()
+    for b in range(B):
+        c = int(pos[b] - plen[b])
+        if 0 <= c < max_new:
+            assert int(oc[b, c]) == int(want_tok[b])
 
 
 @pytest.mark.parametrize("V,dtype", [(7, torch.float32), (7, BF), (343, BF)])

@@ -213,6 +213,37 @@ def test_attention_rows_brute_force():
     assert torch.allclose(oe[0], v.mean(0).repeat_interleave(4, 0), atol=1e-5)
 
 
+def test_attention_rows_bf16_weights_brute_force():
+    """p_bf16: o = sum_j bf16(exp(s_j - max)) v_j / sum_j exp(s_j - max), per query row and head, in fp64 on a
+    tiny case; equal keys give exactly the mean of the values (every weight is exp(0) = 1, exact in bf16); and a
+    planted mistake -- normalising by the rounded weights -- is caught by the brute force."""
+    g = torch.Generator().manual_seed(12)
+    q = torch.randn(3, 8, 64, generator=g)
+    k = torch.randn(7, 2, 64, generator=g)
+    v = torch.randn(7, 2, 64, generator=g)
+    o = R.attention_rows(q, k, v, causal_shift=4, p_bf16=True)
+
+    def brute(o, rounded_norm=False):
+        for r in range(3):
+            for h in range(8):
+                n = 4 + r + 1
+                s = (q[r, h].double() @ k[:n, h // 4].double().t()) / 8.0
+                e = torch.exp(s - s.max())
+                eb = e.float().to(torch.bfloat16).double()
+                ref = eb @ v[:n, h // 4].double() / (eb.sum() if rounded_norm else e.sum())
+                if not torch.allclose(o[r, h].double(), ref, atol=2e-6):
+                    return False
+        return True
+
+    assert brute(o)
+    assert not brute(o, rounded_norm=True)
+    exact = R.attention_rows(q, k, v, causal_shift=4)
+    assert 0 < float((o - exact).abs().max()) < 2e-2  # a bf16 rounding of the weights, no more
+    ke = k[:1].expand(7, 2, 64)
+    oe = R.attention_rows(q[:1], ke, v, p_bf16=True)
+    assert torch.allclose(oe[0], v.mean(0).repeat_interleave(4, 0), atol=1e-6)
+
+
 def test_swiglu_fused_closed_form():
     g = R.bf(torch.linspace(-6, 6, 97))
     u = R.bf(torch.linspace(2, -3, 97))

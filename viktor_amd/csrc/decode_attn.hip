@@ -59,14 +59,23 @@ static DecodeSplit decode_split(int64_t B, int64_t max_len, int cus) {
 template <bool SPLIT>
 __global__ __launch_bounds__(DA_WAVES * 64) void decode_attn_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc, const bf16_t *__restrict__ vc,
-    const int32_t *__restrict__ lengths, bf16_t *__restrict__ out, int64_t stride_b, int64_t stride_s,
-    int64_t max_len, int tps, int nsplit, float *__restrict__ ws_o, float *__restrict__ ws_ml, float scale_log2) {
+    const int32_t *__restrict__ lengths, const int32_t *__restrict__ rows, int64_t cache_rows,
+    bf16_t *__restrict__ out, int64_t stride_b, int64_t stride_s, int64_t max_len, int tps, int nsplit,
+    float *__restrict__ ws_o, float *__restrict__ ws_ml, float scale_log2) {
   __shared__ __attribute__((aligned(16))) bf16_t Vs[DA_WAVES][DA_TILE * DA_PITCH];
 
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   const int64_t b = blockIdx.y;
   const int split = blockIdx.x;
+  // cache row of sequence b (rows == NULL: row b); a row outside the cache gives a zero output (the
+  // combine kernel writes it when the key range is split)
+  const int64_t crow = rows ? static_cast<int64_t>(rows[b]) : b;
+  if (crow < 0 || crow >= cache_rows) {
+    if (!SPLIT && split == 0)
+      for (int o = threadIdx.x; o < DA_H * DA_D; o += DA_WAVES * 64) out[b * DA_H * DA_D + o] = 0;
+    return;  // uniform over the workgroup
+  }
   int64_t len = lengths[b];
   len = len < 1 ? 1 : (len > max_len ? max_len : len);
   const int ntiles = static_cast<int>((len + DA_TILE - 1) / DA_TILE);
@@ -92,8 +101,8 @@ __global__ __launch_bounds__(DA_WAVES * 64) void decode_attn_kernel(
   for (int j = 0; j < 8; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  const bf16_t *kb = kc + b * stride_b;
-  const bf16_t *vb = vc + b * stride_b;
+  const bf16_t *kb = kc + crow * stride_b;
+  const bf16_t *vb = vc + crow * stride_b;
   bf16_t *vs = Vs[wid];
 
   // Software pipeline: the next tile's K loads are issued as soon as the score MFMAs have consumed the
@@ -239,10 +248,16 @@ __global__ __launch_bounds__(DA_WAVES * 64) void decode_attn_kernel(
 __global__ __launch_bounds__(DA_H * DA_D) void decode_attn_combine(const float *__restrict__ ws_o,
                                                                     const float *__restrict__ ws_ml,
                                                                     const int32_t *__restrict__ lengths,
-                                                                    bf16_t *__restrict__ out, int64_t max_len,
-                                                                    int tps, int nsplit) {
+                                                                    const int32_t *__restrict__ rows,
+                                                                    int64_t cache_rows, bf16_t *__restrict__ out,
+                                                                    int64_t max_len, int tps, int nsplit) {
   const int64_t b = blockIdx.x;
   const int h = threadIdx.x / DA_D, d = threadIdx.x % DA_D;
+  const int64_t crow = rows ? static_cast<int64_t>(rows[b]) : b;
+  if (crow < 0 || crow >= cache_rows) {  // no partials were written for a row outside the cache
+    out[(b * DA_H + h) * DA_D + d] = 0;
+    return;
+  }
   int64_t len = lengths[b];
   len = len < 1 ? 1 : (len > max_len ? max_len : len);
   const int ntiles = static_cast<int>((len + DA_TILE - 1) / DA_TILE);
@@ -682,10 +697,14 @@ extern "C" int vk_decode_attention_workspace(int64_t B, int32_t H, int64_t max_l
 }
 
 extern "C" int vk_decode_attention(const void *q, const void *k_cache, const void *v_cache, const int32_t *lengths,
-                                   void *out, int64_t B, int32_t H, int32_t HKV, int32_t D, int64_t stride_b,
-                                   int64_t stride_s, int64_t max_len, void *workspace, int64_t workspace_bytes,
-                                   void *stream) {
+                                   const int32_t *rows, int64_t cache_rows, void *out, int64_t B, int32_t H,
+                                   int32_t HKV, int32_t D, int64_t stride_b, int64_t stride_s, int64_t max_len,
+                                   void *workspace, int64_t workspace_bytes, void *stream) {
   VK_CHECK_ARG(q && k_cache && v_cache && lengths && out, "decode_attention: null pointer");
+  VK_CHECK_ARG(cache_rows > 0, "decode_attention: the cache must hold at least one sequence row");
+  VK_CHECK_ARG(rows != nullptr || cache_rows >= B,
+               "decode_attention: %lld sequences but the cache holds %lld rows (pass rows to map them)",
+               static_cast<long long>(B), static_cast<long long>(cache_rows));
   if (H != DA_H || HKV != DA_HKV || D != DA_D)
     return fail(VK_ERR_UNSUPPORTED, "decode_attention: built for H=8 HKV=2 D=64 (got %d/%d/%d)", H, HKV, D);
   VK_CHECK_ARG(B >= 0 && max_len > 0 && stride_s >= DA_ROW && stride_s % 8 == 0 && stride_b % 8 == 0,
@@ -704,19 +723,20 @@ extern "C" int vk_decode_attention(const void *q, const void *k_cache, const voi
   if (sp.nsplit == 1) {
     decode_attn_kernel<false><<<grid, DA_WAVES * 64, 0, s>>>(
         static_cast<const bf16_t *>(q), static_cast<const bf16_t *>(k_cache), static_cast<const bf16_t *>(v_cache),
-        lengths, static_cast<bf16_t *>(out), stride_b, stride_s, max_len, sp.tps, 1, nullptr, nullptr, scale_log2);
+        lengths, rows, cache_rows, static_cast<bf16_t *>(out), stride_b, stride_s, max_len, sp.tps, 1, nullptr,
+        nullptr, scale_log2);
     return launch_status("decode_attention");
   }
   float *ws_o = static_cast<float *>(workspace);
   float *ws_ml = ws_o + B * sp.nsplit * DA_H * DA_D;
   decode_attn_kernel<true><<<grid, DA_WAVES * 64, 0, s>>>(
       static_cast<const bf16_t *>(q), static_cast<const bf16_t *>(k_cache), static_cast<const bf16_t *>(v_cache),
-      lengths, static_cast<bf16_t *>(out), stride_b, stride_s, max_len, sp.tps, sp.nsplit, ws_o, ws_ml, scale_log2);
+      lengths, rows, cache_rows, static_cast<bf16_t *>(out), stride_b, stride_s, max_len, sp.tps, sp.nsplit, ws_o,
+      ws_ml, scale_log2);
   int st = launch_status("decode_attention");
   if (st != VK_OK) return st;
-  decode_attn_combine<<<static_cast<unsigned>(B), DA_H * DA_D, 0, s>>>(ws_o, ws_ml, lengths,
-                                                                       static_cast<bf16_t *>(out), max_len, sp.tps,
-                                                                       sp.nsplit);
+  decode_attn_combine<<<static_cast<unsigned>(B), DA_H * DA_D, 0, s>>>(
+      ws_o, ws_ml, lengths, rows, cache_rows, static_cast<bf16_t *>(out), max_len, sp.tps, sp.nsplit);
   return launch_status("decode_attention_combine");
 }
 

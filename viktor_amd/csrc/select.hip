@@ -27,7 +27,8 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
     int64_t u_stride, int64_t u_cols, int64_t *__restrict__ tok, int64_t *__restrict__ run, int64_t *__restrict__ pos,
     const int64_t *__restrict__ plen, const int64_t *__restrict__ rope_off, const int64_t *__restrict__ cache_base,
     int64_t *__restrict__ out, int64_t out_stride, int64_t out_cols, int32_t *__restrict__ pos32,
-    int32_t *__restrict__ seqlens, int32_t *__restrict__ rpos32, float *__restrict__ logp_out, int V, int eos, int pad) {
+    int32_t *__restrict__ seqlens, int32_t *__restrict__ rpos32, float *__restrict__ logp_out, int64_t logp_stride,
+    int V, int eos, int pad) {
   __shared__ float z[SEL_MAXV];
   __shared__ float red_v[SEL_THREADS / 64];
   __shared__ int red_i[SEL_THREADS / 64];
@@ -153,7 +154,11 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
     }
     nxt = pick >= 0 ? pick : last_pos;
   }
-  if (logp_out) logp_out[b] = z[nxt] - zmax - logf(sum);
+  if (logp_out) {
+    const float lp = z[nxt] - zmax - logf(sum);
+    if (logp_stride == 0) logp_out[b] = lp;
+    else if (ocol >= 0 && ocol < out_cols) logp_out[b * logp_stride + ocol] = lp;
+  }
 
   // 4. grammar and bookkeeping
   const int64_t prev = tok[b];
@@ -186,8 +191,8 @@ extern "C" int vk_select_update(const float *logits, const void *h, const void *
                                 float temperature, const float *uniforms, int64_t u_stride, int64_t u_cols,
                                 int64_t *tok, int64_t *run, int64_t *pos, const int64_t *plen, const int64_t *rope_off,
                                 const int64_t *cache_base, int64_t *out, int64_t out_stride, int64_t out_cols, int32_t *pos32, int32_t *seqlens,
-                                int32_t *rpos32, float *logp_out, int64_t B, int32_t V, int32_t eos, int32_t pad,
-                                void *stream) {
+                                int32_t *rpos32, float *logp_out, int64_t logp_stride, int64_t B, int32_t V,
+                                int32_t eos, int32_t pad, void *stream) {
   VK_CHECK_ARG(bias && is_tail && is_homo && tok && pos && out, "select_update: null pointer");
   VK_CHECK_ARG(V > 0 && V <= SEL_MAXV, "select_update: vocab must be in 1..%d (got %d)", SEL_MAXV, V);
   VK_CHECK_ARG(B >= 0 && B < (int64_t(1) << 31), "select_update: bad batch");
@@ -199,12 +204,13 @@ extern "C" int vk_select_update(const float *logits, const void *h, const void *
   VK_CHECK_ARG(homo_stop <= 0 || run != nullptr, "select_update: homopolymer rule needs run");
   VK_CHECK_ARG(!(temperature > 0.f) || (uniforms != nullptr && u_cols > 0), "select_update: sampling needs uniforms");
   VK_CHECK_ARG(out_cols > 0, "select_update: empty output buffer");
+  VK_CHECK_ARG(logp_stride == 0 || logp_stride >= out_cols, "select_update: logp_stride must be 0 or >= out_cols");
   if (B == 0) return VK_OK;
   select_update_kernel<<<static_cast<unsigned>(B), SEL_THREADS, 0, VK_STREAM(stream)>>>(
       logits, static_cast<const bf16_t *>(h), static_cast<const bf16_t *>(norm_w), eps,
       static_cast<const bf16_t *>(w_head), d, round_bf16, bias, is_tail,
       is_homo, homo_stop, temperature, uniforms, u_stride, u_cols, tok, run, pos, plen, rope_off, cache_base, out,
       out_stride,
-      out_cols, pos32, seqlens, rpos32, logp_out, V, eos, pad);
+      out_cols, pos32, seqlens, rpos32, logp_out, logp_stride, V, eos, pad);
   return launch_status("select_update");
 }

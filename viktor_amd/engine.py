@@ -32,7 +32,8 @@ from .tokenizer import BOS, EOS, PAD
 class DecodeEngine:
     def __init__(self, model, batch_size: int, max_new_tokens: int, max_frames: int, backend: str = "auto",
                  cuda_graph: bool = True, prefill_batch: int = 128, check_every: int = 32,
-                 attention_backend: str = "auto", temperature: float = 0.0, max_homopolymer=64, group_size: int = 1):
+                 attention_backend: str = "auto", temperature: float = 0.0, max_homopolymer=64, group_size: int = 1,
+                 logprobs: bool = False):
         self.model, self.dec = model, model.decoder
         self.temperature = float(temperature)
         dev = self.dec.lm_head.weight.device
@@ -86,6 +87,9 @@ class DecodeEngine:
         self.plen = torch.zeros(batch_size, dtype=torch.long, device=dev)  # output column = pos - plen
         self.uniforms = torch.zeros(batch_size, max_new_tokens, dtype=torch.float32, device=dev)
         self._uniforms_set = False
+        # logprobs=True: logp[b, j] = log-probability of output token j under the distribution it was chosen
+        # from (log softmax of (logits + bias) / T, or of logits + bias when greedy), before the grammar rules
+        self.logp = torch.zeros(batch_size, max_new_tokens, dtype=torch.float32, device=dev) if logprobs else None
         self.fast.decode_workspace = ops.decode_attention_workspace(batch_size, self.dec.cfg.n_heads,
                                                                     self.cache.max_len, dev)
         self.graph = None  # one captured step
@@ -109,7 +113,7 @@ class DecodeEngine:
                           self.plen, self.rope_off, self.out, self.pos32, self.seqlens, self.rpos32, EOS, PAD,
                           h=x, norm_w=self.dec.norm.weight, eps=self.dec.cfg.norm_eps, w_head=self.dec.lm_head.weight,
                           round_bf16=self.temperature > 0, temperature=self.temperature, uniforms=self.uniforms,
-                          cache_base=None if self.G == 1 else self.cache_base)
+                          cache_base=None if self.G == 1 else self.cache_base, logp_out=self.logp)
 
     def _reset_state(self):
         self.pos.fill_(1)
@@ -140,32 +144,43 @@ class DecodeEngine:
         self.out.fill_(PAD)
 
     # ---- prefill -------------------------------------------------------------------------------
-    def _prefill_hip(self, prefix, lens, row0, cache):
-        """prefix [sum(lens), d] projected frames of cache rows row0.. ; returns the final hidden at each BOS."""
-        dev = prefix.device
+    def _packing(self, lens, row0, cache, dev):
+        """Index layout of one prefill sub-batch, built on the host from the frame counts and uploaded once
+        (the engine keeps it while the sub-batch's lengths repeat). Sequence j occupies packed rows
+        [s_j, s_j + lens[j] + 1): its frames, then BOS in the last row; every row carries its cache position
+        (0 .. lens[j]), cache row (row0 + j) and RoPE position (position * pos_scale)."""
+        import numpy as np
         n = len(lens)
+        seq_lens = [L + 1 for L in lens]
+        plan = PrefillPlan(seq_lens, dev, rows=list(range(row0, row0 + n)), keep=[1] * n, cache=cache)
+        starts = np.asarray(plan.cu[:-1], dtype=np.int64)
+        within = np.concatenate([np.arange(m, dtype=np.int64) for m in seq_lens])  # position inside the sequence
+        owner = np.repeat(np.arange(n, dtype=np.int64), seq_lens)                  # sequence of each packed row
+        is_frame = within < np.repeat(np.asarray(lens, dtype=np.int64), seq_lens)
+        frame_rows = (starts[owner] + within)[is_frame]                             # where frame rows land
+        bos_rows = starts + np.asarray(lens, dtype=np.int64)
+
+        def up(a, dt):
+            return torch.from_numpy(np.ascontiguousarray(a)).to(device=dev, dtype=dt)
+
+        pos = up(within, torch.int32)
+        rpos = None if self.pos_scale == 1 else up(within * self.pos_scale, torch.int32)
+        return plan, up(frame_rows, torch.long), up(bos_rows, torch.long), pos, up(owner + row0, torch.int32), rpos
+
+    def _prefill_hip(self, prefix, lens, row0, cache):
+        """Packs the projected frames prefix [sum(lens), d] of cache rows row0.. with a BOS row after each
+        sequence, runs the layers (the last one for the BOS rows only) and returns the final-normed hidden
+        state of each BOS row [len(lens), d]."""
+        dev = prefix.device
         key = tuple(lens)
-        entry = self._prefill_plans.get(row0)
-        if entry is None or entry[0] != key:
-            seq_lens = [L + 1 for L in lens]
-            plan = PrefillPlan(seq_lens, dev, rows=list(range(row0, row0 + n)), keep=[1] * n, cache=cache)
-            L = torch.tensor(lens, device=dev)
-            total, frames = plan.total, sum(lens)
-            cu = torch.tensor(plan.cu, dtype=torch.int32, device=dev)
-            frame_seg = torch.repeat_interleave(torch.arange(n, device=dev), L, output_size=frames)
-            frame_idx = torch.arange(frames, device=dev) + frame_seg
-            last = cu[1:].long() - 1
-            pos = (torch.arange(total, device=dev)
-                   - torch.repeat_interleave(cu[:-1].long(), L + 1, output_size=total)).int()
-            seq = torch.repeat_interleave(torch.arange(row0, row0 + n, device=dev, dtype=torch.int32), L + 1,
-                                          output_size=total)
-            rpos = None if self.pos_scale == 1 else (pos * self.pos_scale).int()
-            entry = key, (plan, frame_idx, last, pos, seq, rpos)
-            self._prefill_plans[row0] = entry
-        plan, frame_idx, last, pos, seq, rpos = entry[1]
+        cached = self._prefill_plans.get(row0)
+        if cached is None or cached[0] != key:
+            cached = key, self._packing(lens, row0, cache, dev)
+            self._prefill_plans[row0] = cached
+        plan, frame_rows, bos_rows, pos, seq, rpos = cached[1]
         x = torch.empty(plan.total, prefix.shape[1], dtype=self.dtype, device=dev)
-        x[frame_idx] = prefix
-        x[last] = self.dec.embed.weight[BOS].to(self.dtype)
+        x.index_copy_(0, frame_rows, prefix)
+        x[bos_rows] = self.dec.embed.weight[BOS].to(self.dtype)
         return self.fast.prefill(x, pos, seq, None, plan.max_len, cache, rope_pos=rpos, plan=plan)
 
     def set_uniforms(self, u):
@@ -176,9 +191,12 @@ class DecodeEngine:
 
     @torch.no_grad()
     def prefill(self, frames, frame_lens):
-        """frames [sum(frame_lens), d_enc]: encoder frames of B chunks, concatenated; frame_lens [B].
-        Fills the cache and emits the first token of every sequence (chosen from bf16 logits, as the
-        reference does at viktor/engine.py:191)."""
+        """Encodes every sequence's prefix into the KV cache and picks its first output token.
+
+        frames: the B windows' encoder frames stacked along dim 0 ([sum(frame_lens), d_enc]); frame_lens: B
+        frame counts. Windows go through the projector and the decoder in sub-batches of prefill_batch; the
+        first token comes from the BOS row's bf16-rounded logits (viktor/engine.py:191 rounds them the same
+        way) and lands in out[:, 0]; the decode state then points at position frame_lens[b] + 1."""
         frame_lens = [int(n) for n in frame_lens]
         assert len(frame_lens) == self.B and frames.shape[0] == sum(frame_lens)
         assert all(0 < n <= self.max_frames for n in frame_lens), "frame count outside 1..max_frames"
@@ -224,7 +242,7 @@ class DecodeEngine:
                           self.plen, self.rope_off, self.out, self.pos32, self.seqlens, self.rpos32, EOS, PAD,
                           h=h.contiguous(), w_head=self.dec.lm_head.weight, round_bf16=True,
                           temperature=self.temperature, uniforms=self.uniforms,
-                          cache_base=None if G == 1 else self.cache_base)
+                          cache_base=None if G == 1 else self.cache_base, logp_out=self.logp)
         self.step_idx.fill_(1)
 
     def _check_groups(self, frames, frame_lens, offs):
@@ -253,9 +271,14 @@ class DecodeEngine:
 
     @torch.no_grad()
     def decode(self, steps=None):
-        """Run decode steps after prefill. steps=None: stop when all sequences ended (checked every
-        check_every steps) or at max_new_tokens. steps=n: run exactly n-1 steps (n output tokens)."""
-        n = self.max_new - 1 if steps is None else steps - 1
+        """Continues every sequence after prefill and returns `out` [B, max_new_tokens].
+
+        With steps=n the engine replays exactly n - 1 steps, so out[:, :n] holds n tokens per sequence
+        (1 <= n <= max_new_tokens). With steps=None it runs up to max_new_tokens tokens and stops early once
+        every sequence has emitted EOS (looked at after each check_every steps)."""
+        if steps is not None and not 1 <= int(steps) <= self.max_new:
+            raise ValueError(f"decode: steps must be in 1..max_new_tokens={self.max_new} (got {steps})")
+        n = self.max_new - 1 if steps is None else int(steps) - 1
         done = 0
         while done < n:
             if self.graph_multi is not None and done % self.check_every == 0 and n - done >= self.check_every:
@@ -274,6 +297,7 @@ class DecodeEngine:
         return self.out
 
     def generate(self, frames, frame_lens, steps=None):
-        """Returns token ids [B, max_new_tokens] (PAD after EOS). The buffer is reused by the next call."""
+        """prefill + decode. The returned [B, max_new_tokens] token ids (PAD once a sequence has ended) are
+        the engine's own `out` buffer, which the next call overwrites."""
         self.prefill(frames, frame_lens)
         return self.decode(steps)

@@ -208,8 +208,9 @@ class FastDecoder:
 
     def decode(self, x, pos, seq, cache_seqlens, cache, rope_pos=None, tok=None):
         """One token per sequence: x [B, d] (or tok [B] token ids with x None: the embedding is looked up in
-        the first layer's kernel), pos/seq [B] int32, cache_seqlens = pos + 1 (int32). Returns the
-        final-normed hidden [B, d]. Reference: viktor/fast_decoder.py:76-90."""
+        the first layer's kernel), pos/seq [B] int32 (sequence b's token goes to cache row seq[b], position
+        pos[b], and attends to that row's positions < cache_seqlens[b]), cache_seqlens = pos + 1 (int32).
+        Returns the final-normed hidden [B, d]. Reference: viktor/fast_decoder.py:76-90."""
         xr = self.decode_residual(pos, seq, cache_seqlens, cache, rope_pos=rope_pos, tok=tok, x=x)
         return ops.add_rmsnorm(xr, self.w(self.dec.norm.weight), self.cfg.norm_eps)
 
@@ -260,7 +261,7 @@ class FastDecoder:
                                             W(a.k_norm.weight), cos, sin, pos, seq, kc, vc, H, HKV, D, rope_pos=rope_pos,
                                             ss=ss_attn)
             if prefix is None:
-                o = ops.decode_attention(q, kc, vc, cache_seqlens, workspace=ws)
+                o = ops.decode_attention(q, kc, vc, cache_seqlens, workspace=ws, rows=seq)
             else:
                 pc, plen32, G, gws = prefix
                 o = ops.decode_attention_grouped(q, pc.k[i], pc.v[i], plen32, kc, vc, cache_seqlens, G, workspace=gws)
@@ -272,15 +273,23 @@ class FastDecoder:
 
     # ---- Decoder.forward on this path ----------------------------------------------------------
     def forward(self, x, cache=None, batch_slice=slice(None), pos=None, positions=None):
+        """Decoder.forward on this path (reference: viktor/decoder.py:135-144 with Attention.forward at 69-79).
+        Prefill mode (pos None): a causal pass over x [B, T, d]; with a cache, k / v of position t go to cache
+        rows batch_slice (B of them) at positions 0..T-1. Decode mode (pos [B]): T == 1, one row per cache
+        sequence (the reference writes cache rows 0..B-1 at pos and ignores batch_slice)."""
         require_device(x, "Decoder.forward")
         B, T, d = x.shape
         dev = x.device
         xb = x.to(BF16).reshape(B * T, d).contiguous()
+        _require(batch_slice.step in (None, 1), "Decoder.forward: batch_slice must be contiguous")
         row0 = 0 if batch_slice.start is None else int(batch_slice.start)
         if pos is not None:
             _require(T == 1 and cache is not None, "Decoder.forward: decode mode needs T == 1 and a cache")
+            _require(cache.k.shape[1] == B, f"Decoder.forward: decode mode needs one cache row per sequence "
+                                            f"({B} sequences, {cache.k.shape[1]} cache rows)")
+            _require(pos.shape == (B,), "Decoder.forward: pos [B]")
             pos32 = pos.to(torch.int32).contiguous()
-            rows = torch.arange(row0, row0 + B, dtype=torch.int32, device=dev)
+            rows = torch.arange(B, dtype=torch.int32, device=dev)
             seqlens = (pos32 + 1).contiguous()
             rp = None if positions is None else positions.reshape(B).to(torch.int32).contiguous()
             if cache is not None and self.decode_workspace is None:
@@ -288,6 +297,11 @@ class FastDecoder:
                                                                        cache.k.shape[2], dev)
             h = self.decode(xb, pos32, rows, seqlens, cache, rope_pos=rp)
             return h.view(B, 1, d)
+        if cache is not None:
+            stop = row0 + B if batch_slice.stop is None else int(batch_slice.stop)
+            _require(stop - row0 == B and 0 <= row0 and stop <= cache.k.shape[1],
+                     "Decoder.forward: batch_slice must select B rows of the cache")
+            _require(T <= cache.k.shape[2], "Decoder.forward: T exceeds the cache length")
         key = (B, T, row0, cache is not None)
         plan = self._plans.get(key)
         if plan is None:

@@ -104,6 +104,9 @@ class _GspoLoss(torch.autograd.Function):
                              grad=logits.requires_grad)
         ctx.save_for_backward(res.get("dlogits", torch.empty(0, device=logits.device)))
         ctx.logits_dtype = logits.dtype
+        # the kernel's gradient is that of the loss only: s, pg and lp are outputs to read, not to backpropagate
+        # through (a backward from them raises instead of returning zeros)
+        ctx.mark_non_differentiable(res["s"], res["pg"], res["lp"])
         return res["loss"], res["s"], res["pg"], res["lp"]
 
     @staticmethod

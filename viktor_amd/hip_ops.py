@@ -211,19 +211,26 @@ def decode_attention_workspace(B, H, max_len, device):
     return torch.empty(nbytes.value, dtype=torch.uint8, device=device)
 
 
-def decode_attention(q, k, v, lengths, block=64, workspace=None):
-    """q [B, H, D]; k/v [B, S, Hkv, D] (one layer of the cache); lengths [B] int32, including the current
-    token, 1 <= lengths <= S. Only the valid prefix of each row is read. Returns [B, H, D] bf16.
+def decode_attention(q, k, v, lengths, block=64, workspace=None, rows=None):
+    """q [B, H, D]; k/v [Bc, S, Hkv, D] (one layer of the cache); lengths [B] int32, including the current
+    token, 1 <= lengths <= S. Sequence b attends to cache row rows[b] (rows [B] int32; None: row b, which
+    needs Bc >= B). Only the valid prefix of each row is read. Returns [B, H, D] bf16.
     workspace: preallocated key-split scratch (needed inside graph capture; allocated here otherwise).
-    Reference: viktor/decode_attention.py:41-53 (block is accepted for the signature)."""
+    Reference: viktor/decode_attention.py:41-53 (block is accepted for the signature); rows is the
+    cache_batch_idx of flash_attn_with_kvcache at viktor/fast_decoder.py:86-89."""
     require_device(q, "decode_attention")
     B, H, D = q.shape
     HK = k.shape[2]
     _require(q.is_contiguous() and H % HK == 0 and H // HK <= 16 and D == 64, "decode_attention: q layout")
     _require(q.dtype == k.dtype == v.dtype == BF16, "decode_attention: bf16 tensors")
+    _require(k.shape == v.shape and k.dim() == 4, "decode_attention: k / v shapes")
     _require(k.stride() == v.stride() and k.stride(-1) == 1 and k.stride(-2) == D, "decode_attention: cache layout")
     _require(lengths.shape == (B,) and lengths.dtype == torch.int32 and lengths.is_contiguous(),
              "decode_attention: lengths")
+    if rows is None:
+        _require(k.shape[0] >= B, f"decode_attention: {B} queries but the cache holds {k.shape[0]} sequences")
+    else:
+        _require(rows.shape == (B,) and rows.dtype == torch.int32 and rows.is_contiguous(), "decode_attention: rows")
     S = k.shape[1]
     if workspace is None:
         key = (B, H, S, q.device)
@@ -233,7 +240,8 @@ def decode_attention(q, k, v, lengths, block=64, workspace=None):
             _ws_cache[key] = workspace
     out = torch.empty_like(q)
     wsz = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    call("vk_decode_attention", ptr(q), ptr(k), ptr(v), ptr(lengths), ptr(out), B, H, HK, D, k.stride(0), k.stride(1),
+    call("vk_decode_attention", ptr(q), ptr(k), ptr(v), ptr(lengths), ptr(rows), k.shape[0], ptr(out), B, H, HK, D,
+         k.stride(0), k.stride(1),
          S, ptr(workspace), wsz, stream_handle())
     return out
 
@@ -340,7 +348,8 @@ def select_update(bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_o
                   logp_out=None, norm_w=None, eps=1e-6, cache_base=None):
     """One step's token choice + state update for every sequence (fused LM head when h, w_head are given;
     with norm_w, h is the residual stream and the final RMSNorm runs first). See vk_select_update in
-    include/viktor_hip.h for the exact rule order."""
+    include/viktor_hip.h for the exact rule order. logp_out: [B] fp32 (this step's chosen-token log-prob), or
+    [B, >= out columns] fp32, where the log-prob goes to the output column the token is written to."""
     ref = logits if logits is not None else h
     require_device(ref, "select_update")
     B = tok.shape[0]
@@ -363,10 +372,17 @@ def select_update(bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_o
                  and uniforms.shape[0] == B and uniforms.stride(1) == 1, "select_update: uniforms [B, T] fp32")
     us, uc = (uniforms.stride(0), uniforms.shape[1]) if uniforms is not None else (0, 0)
     _require(norm_w is None or (norm_w.shape == (d,) and norm_w.dtype == BF16), "select_update: norm_w")
+    lp_stride = 0
+    if logp_out is not None:
+        _require(logp_out.dtype == torch.float32 and logp_out.shape[0] == B and logp_out.dim() in (1, 2)
+                 and logp_out.stride(-1) == 1, "select_update: logp_out [B] or [B, T] fp32")
+        if logp_out.dim() == 2:
+            _require(logp_out.shape[1] >= out.shape[1], "select_update: logp_out columns")
+            lp_stride = logp_out.stride(0)
     call("vk_select_update", ptr(logits), ptr(h), ptr(norm_w), float(eps), ptr(w_head), d, int(bool(round_bf16)),
          ptr(bias), ptr(is_tail),
          ptr(is_homo), int(homo_stop), float(temperature), ptr(uniforms), us, uc, ptr(tok), ptr(run), ptr(pos), ptr(plen),
-         ptr(rope_off), ptr(cache_base), ptr(out), out.stride(0), out.shape[1], ptr(pos32), ptr(seqlens), ptr(rpos32), ptr(logp_out), B, V,
+         ptr(rope_off), ptr(cache_base), ptr(out), out.stride(0), out.shape[1], ptr(pos32), ptr(seqlens), ptr(rpos32), ptr(logp_out), lp_stride, B, V,
          int(eos), int(pad), stream_handle())
 
 
