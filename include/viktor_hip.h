@@ -159,6 +159,20 @@ int vk_decode_attention(const void *q, const void *k_cache, const void *v_cache,
 int vk_decode_attention_workspace(int64_t B, int32_t H, int64_t max_len, int64_t *bytes);
 
 /*
+ * vk_decode_attention without a workspace argument and without any allocation: the key-split partials go to a
+ * 4 MiB static device array of the library (one per GPU, held until the process ends; its device address is
+ * looked up once per device, on the first call there). Same arguments (minus workspace), kernels and results,
+ * bit for bit, as vk_decode_attention. Returns VK_ERR_ARG when the split needs more than 4 MiB of partials
+ * (B x splits x 8 heads x 66 floats; at most ~2 x CUs + B rows of them, so never on a 256-CU MI355X).
+ * Calls that overlap on one GPU (two streams, or two host threads) share that array and race: serialise them.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).
+ */
+int vk_decode_attention_noalloc(const void *q, const void *k_cache, const void *v_cache, const int32_t *lengths,
+                                const int32_t *rows, int64_t cache_rows, void *out, int64_t B, int32_t H, int32_t HKV,
+                                int32_t D, int64_t stride_b, int64_t stride_s, int64_t max_len, void *stream);
+
+/*
  * Decode attention for groups of G consecutive sequences that share a prefix (GSPO: the G samples of one
  * window). Sequence b (group p = b / G) attends to prefix rows [0, prefix_len[p]) of k_prefix/v_prefix
  * (row r of group p at p * stride_pb + r * stride_ps) followed by its own rows [0, suffix_len[b]) of

@@ -26,6 +26,8 @@
 //     small combine kernel merges the split partials from the workspace.
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace vk {
@@ -696,10 +698,10 @@ extern "C" int vk_decode_attention_workspace(int64_t B, int32_t H, int64_t max_l
   return VK_OK;
 }
 
-extern "C" int vk_decode_attention(const void *q, const void *k_cache, const void *v_cache, const int32_t *lengths,
-                                   const int32_t *rows, int64_t cache_rows, void *out, int64_t B, int32_t H,
-                                   int32_t HKV, int32_t D, int64_t stride_b, int64_t stride_s, int64_t max_len,
-                                   void *workspace, int64_t workspace_bytes, void *stream) {
+// Argument checks shared by both decode-attention entry points (status VK_OK when the launch may go ahead).
+static int check_decode_args(const void *q, const void *k_cache, const void *v_cache, const int32_t *lengths,
+                             const int32_t *rows, int64_t cache_rows, void *out, int64_t B, int32_t H, int32_t HKV,
+                             int32_t D, int64_t stride_b, int64_t stride_s, int64_t max_len) {
   VK_CHECK_ARG(q && k_cache && v_cache && lengths && out, "decode_attention: null pointer");
   VK_CHECK_ARG(cache_rows > 0, "decode_attention: the cache must hold at least one sequence row");
   VK_CHECK_ARG(rows != nullptr || cache_rows >= B,
@@ -712,11 +714,14 @@ extern "C" int vk_decode_attention(const void *q, const void *k_cache, const voi
   VK_CHECK_ARG(vk_aligned16(q) && vk_aligned16(k_cache) && vk_aligned16(v_cache),
                "decode_attention: q and the caches must be 16-byte aligned");
   VK_CHECK_ARG(B < 65536, "decode_attention: B must be < 65536");
-  if (B == 0) return VK_OK;
-  const DecodeSplit sp = decode_split(B, max_len, device_cus_cached());
-  const int64_t need = workspace_bytes_for(B, sp);
-  VK_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace != nullptr),
-               "decode_attention: workspace of %lld bytes needed", static_cast<long long>(need));
+  return VK_OK;
+}
+
+// The split kernel (when the key range is split, partials go to `workspace`) and its combine launch.
+static int launch_decode_attention(const void *q, const void *k_cache, const void *v_cache, const int32_t *lengths,
+                                   const int32_t *rows, int64_t cache_rows, void *out, int64_t B, int64_t stride_b,
+                                   int64_t stride_s, int64_t max_len, const DecodeSplit &sp, void *workspace,
+                                   void *stream) {
   const float scale_log2 = static_cast<float>(1.0 / sqrt(static_cast<double>(DA_D)) * 1.4426950408889634);
   hipStream_t s = VK_STREAM(stream);
   const dim3 grid(sp.nsplit, static_cast<unsigned>(B));
@@ -738,6 +743,77 @@ extern "C" int vk_decode_attention(const void *q, const void *k_cache, const voi
   decode_attn_combine<<<static_cast<unsigned>(B), DA_H * DA_D, 0, s>>>(
       ws_o, ws_ml, lengths, rows, cache_rows, static_cast<bf16_t *>(out), max_len, sp.tps, sp.nsplit);
   return launch_status("decode_attention_combine");
+}
+
+extern "C" int vk_decode_attention(const void *q, const void *k_cache, const void *v_cache, const int32_t *lengths,
+                                   const int32_t *rows, int64_t cache_rows, void *out, int64_t B, int32_t H,
+                                   int32_t HKV, int32_t D, int64_t stride_b, int64_t stride_s, int64_t max_len,
+                                   void *workspace, int64_t workspace_bytes, void *stream) {
+  const int st = check_decode_args(q, k_cache, v_cache, lengths, rows, cache_rows, out, B, H, HKV, D, stride_b,
+                                   stride_s, max_len);
+  if (st != VK_OK || B == 0) return st;
+  const DecodeSplit sp = decode_split(B, max_len, device_cus_cached());
+  const int64_t need = workspace_bytes_for(B, sp);
+  VK_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+               "decode_attention: workspace of %lld bytes needed", static_cast<long long>(need));
+  return launch_decode_attention(q, k_cache, v_cache, lengths, rows, cache_rows, out, B, stride_b, stride_s, max_len,
+                                 sp, workspace, stream);
+}
+
+// ---- decode attention without an allocation ------------------------------------------------------------
+// The key-split partials live in a file-scope device array instead of a caller-supplied workspace. Each GPU
+// holds its own copy (for the life of the process); the host reaches it through the address that
+// hipGetSymbolAddress returns on that device, looked up once per device and kept here -- the array's name in
+// host code is only a stand-in, never a device address. Nothing in it needs clearing between calls: the
+// combine kernel reads only the partials of splits that the same call's split kernel wrote.
+constexpr int64_t kNoallocScratchBytes = int64_t(4) << 20;
+static __device__ __align__(256) float scratch[kNoallocScratchBytes / sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+static int scratch_of_current_device(void **ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0)
+    return fail(VK_ERR_LAUNCH, "decode_attention_noalloc: no current HIP device");
+  if (dev >= kMaxDevices) return fail(VK_ERR_UNSUPPORTED, "decode_attention_noalloc: device %d >= %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(VK_ERR_LAUNCH, "decode_attention_noalloc: hipGetSymbolAddress failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return VK_OK;
+}
+
+extern "C" int vk_decode_attention_noalloc(const void *q, const void *k_cache, const void *v_cache,
+                                           const int32_t *lengths, const int32_t *rows, int64_t cache_rows,
+                                           void *out, int64_t B, int32_t H, int32_t HKV, int32_t D, int64_t stride_b,
+                                           int64_t stride_s, int64_t max_len, void *stream) {
+  const int st = check_decode_args(q, k_cache, v_cache, lengths, rows, cache_rows, out, B, H, HKV, D, stride_b,
+                                   stride_s, max_len);
+  if (st != VK_OK || B == 0) return st;
+  const DecodeSplit sp = decode_split(B, max_len, device_cus_cached());
+  const int64_t need = workspace_bytes_for(B, sp);
+  VK_CHECK_ARG(need <= kNoallocScratchBytes,
+               "decode_attention_noalloc: %lld sequences x %d key splits need %lld bytes of partials, more than the "
+               "%lld-byte static scratch (use vk_decode_attention with a workspace)",
+               static_cast<long long>(B), sp.nsplit, static_cast<long long>(need),
+               static_cast<long long>(kNoallocScratchBytes));
+  void *ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_of_current_device(&ws);
+    if (rc != VK_OK) return rc;
+  }
+  return launch_decode_attention(q, k_cache, v_cache, lengths, rows, cache_rows, out, B, stride_b, stride_s, max_len,
+                                 sp, ws, stream);
 }
 
 extern "C" int vk_decode_attention_grouped_workspace(int64_t B, int32_t G, int64_t pre_max, int64_t suf_max,
