@@ -11,11 +11,18 @@ Extra objects on the JSON line:
   roofline      decode attention, the dominant kernel: algorithmic bytes per call (every K/V byte the call
                 must read once -- the shared prefix once per group, each sequence's own rows -- plus q and
                 out) / its average duration, measured here with HIP events on the launch stream over calls
-                at the rollout's attended lengths;
+                at the lengths of 32 evenly spaced decode steps, rotating over the 8 layers' caches as the
+                captured step does (so no call finds its bytes in the Infinity Cache); the back-to-back
+                figure on one layer is kept as warm_*;
                 traffic = measured HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by a copy
                 kernel; read from profiles/decode_attention_traffic.json when present, else null).
-  cpu_baseline  the CPU oracle (the reference's fp32 torch path restated) on this host, on a bounded sample:
-                rounds of 2 sequences x 2048-frame prefix x 64 sampled tokens for about 12 s; tokens/s.
+  cpu_baseline  the CPU oracle (the reference's fp32 torch path restated) on this host's usable cores: the
+                CPU-plumbing configuration at full size (4 sequences x 2048-frame prefix x 64 greedy tokens,
+                8 layers, seed 0); tokens/s, with the host's CPU count, affinity, quota and model.
+  configs       the other configurations, each against its own roofline: the rollout without prefix sharing
+                (every sequence prefilled and cached alone, as the reference does), varlen prefill + 4-mer
+                decode (1024 sequences, 340 tokens, vocab 343), scoring (512 x (2048 + 700..1024) forward +
+                loss + dL/dlogits) and the 4096-sequence stress decode (51.5 GB of KV cache).
   prefill       the rollout's prefill (projector + 8 layers with a BOS-only last layer, once per window
                 when the prefix KV is shared): algorithmic flops (projector, 2 x weights per row less what the
                 BOS-only last layer skips, causal attention 1024 n (n + 1) per layer and window, the LM head of
@@ -36,8 +43,9 @@ Extra objects on the JSON line:
                 frames) through the SUP-shaped encoder (5 convolutions, 18 DeepNorm layers, d_model 512, window
                 (127, 128)) with seeded random weights; ms, chunks/s and the MFMA fraction of its algorithmic
                 flops (convolutions, 4 products per layer, window attention over the keys each frame sees).
-Usage: python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--no-cpu] [--no-configs]
        python bench.py --mode encoder|prefill [--steps N]   (that object alone, N timed repetitions)
+       python bench.py --mode configs                       (the other configurations alone)
        python bench.py --mode kernels [--group-size G]      (the decode-attention traffic probe)
 """
 
@@ -89,67 +97,304 @@ def prefill_flops(windows, frames, layers=8, d=512, weights_per_layer=3014656, v
     return windows * (proj + gemm + attn + head)
 
 
-def decode_attention_timing(eng, n_points=32, reps=5):
-    """Average duration (HIP events on the current stream) and algorithmic bytes of one decode-attention
-    call at the attended lengths of a rollout's decode steps j = 0..NEW-2 (P + 1 prefix positions + j + 1
-    own positions), sampled at n_points evenly spaced steps, reps back-to-back calls each."""
+def _attention_call(eng, layer, q, lens, plen=None):
+    """One decode-attention launch of the engine's kind on layer `layer` of its caches."""
     from viktor_amd import hip_ops as ops
-    B, G = eng.B, eng.G
     cache = eng.cache
-    dev = cache.k.device
+    if eng.G > 1:
+        pc = eng.prefix_cache
+        return lambda: ops.decode_attention_grouped(q, pc.k[layer], pc.v[layer], plen, cache.k[layer],
+                                                    cache.v[layer], lens, eng.G, workspace=eng.grouped_workspace)
+    return lambda: ops.decode_attention(q, cache.k[layer], cache.v[layer], lens, workspace=eng.fast.decode_workspace)
+
+
+WEIGHT_BYTES = 2 * (8 * 3014656)  # the decoder's matmul weights in bf16, read once per decode step
+
+
+def prefill_flops_lens(frame_lens, vocab=7):
+    """prefill_flops summed over windows of the given frame counts."""
+    return sum(prefill_flops(1, int(n), vocab=vocab) for n in frame_lens)
+
+
+def decode_roofline_ms(attended, steps, B):
+    """HBM-roofline time of `steps` decode steps: each step reads every attended K/V position of every layer
+    (attended(j) positions at step j, 4096 B each over the 8 layers), writes B new positions and reads the
+    weights once."""
+    total = sum(attended(j) * 8 * KV_ROW_BYTES + B * 8 * KV_ROW_BYTES + WEIGHT_BYTES for j in range(steps))
+    return total / (HBM_PEAK_GBS * 1e9) * 1e3
+
+
+def _timed(fn, reps=1):
+    """ms per call of fn() with HIP events on the current stream (after one untimed call)."""
+    fn()
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    torch.cuda.synchronize()
+    e[0].record()
+    for _ in range(reps):
+        fn()
+    e[1].record()
+    torch.cuda.synchronize()
+    return e[0].elapsed_time(e[1]) / reps
+
+
+def _bf16_model(k, dev, seed=0):
+    from viktor_amd.synthetic import make_model
+    m = make_model(k, n_layers=8, seed=seed, rope_theta=1e6)
+    g = copy.deepcopy(m).to(dev)
+    g.projector.to(torch.bfloat16)
+    g.decoder.to(torch.bfloat16)
+    return g.eval()
+
+
+def rollout_ungrouped(dev, gm, fr, u):
+    """The rollout configuration as the reference runs it: every one of the 512 sequences prefilled and cached
+    on its own (no prefix sharing, scripts/gspo.py:444 + viktor/engine.py:168-201); 1024 sampled tokens."""
+    from viktor_amd import DecodeEngine
+    B = PREFIXES * GROUP
+    eng = DecodeEngine(gm, B, NEW, P, temperature=1.0, group_size=1)
+    plens = [P] * B
+
+    def run():
+        eng.set_uniforms(u)
+        eng.generate(fr, plens, steps=NEW)
+
+    ms = _timed(run)
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    eng.set_uniforms(u)
+    e[0].record()
+    eng.prefill(fr, plens)
+    e[1].record()
+    eng.decode(NEW)
+    e[2].record()
+    torch.cuda.synchronize()
+    avg_s, alg = decode_attention_timing(eng, plens, NEW - 1)
+    roof = decode_roofline_ms(lambda j: B * (P + 2 + j), NEW - 1, B)
+    out = {"tokens_per_s": round(B * NEW / (ms / 1e3), 1), "ms_per_rollout": round(ms, 2),
+           "prefill_ms": round(e[0].elapsed_time(e[1]), 2), "decode_ms": round(e[1].elapsed_time(e[2]), 2),
+           "decode_roofline_ms": round(roof, 1), "decode_hbm_frac": round(roof / e[1].elapsed_time(e[2]), 4),
+           "attention": {"avg_launch_us": round(avg_s * 1e6, 2), "alg_bytes_per_launch": int(alg),
+                         "achieved_gbs": round(alg / avg_s / 1e9, 1),
+                         "frac": round(alg / avg_s / 1e9 / HBM_PEAK_GBS, 4)}}
+    del eng
+    torch.cuda.empty_cache()
+    return out
+
+
+def varlen_kmer_config(dev, steps=340):
+    """Variable-length prefill + 4-mer decode: 1024 sequences, prefixes uniform in [1200, 2048] frames (packed,
+    no padding frames), vocab 343, greedy, 340 tokens (prefill token + 339 graph steps)."""
+    from viktor_amd import DecodeEngine
+    from viktor_amd.synthetic import varlen_lengths
+    gm = _bf16_model(4, dev)
+    B = 1024
+    lens = [int(n) for n in varlen_lengths(B, 1200, 2048, seed=3)]
+    g = torch.Generator(device=dev).manual_seed(4)
+    fr = torch.randn(sum(lens), 512, generator=g, device=dev).to(torch.bfloat16)
+    eng = DecodeEngine(gm, B, steps, max(lens), temperature=0.0)
+    eng.generate(fr, lens, steps=steps)
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    torch.cuda.synchronize()
+    e[0].record()
+    eng.prefill(fr, lens)
+    e[1].record()
+    eng.decode(steps)
+    e[2].record()
+    torch.cuda.synchronize()
+    pre, dec = e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2])
+    pf = prefill_flops_lens(lens, vocab=343)
+    tot = sum(lens)
+    roof = decode_roofline_ms(lambda j: tot + B * (2 + j), steps - 1, B)
+    avg_s, alg = decode_attention_timing(eng, lens, steps - 1, n_points=16)
+    out = {"sequences": B, "prefix_frames": "U[1200, 2048]", "vocab": 343, "new_tokens": steps,
+           "tokens_per_s": round(B * steps / ((pre + dec) / 1e3), 1), "prefill_ms": round(pre, 2),
+           "decode_ms": round(dec, 2), "prefill_alg_tflop": round(pf / 1e12, 2),
+           "prefill_mfma_frac": round(pf / (pre / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+           "decode_roofline_ms": round(roof, 1), "decode_hbm_frac": round(roof / dec, 4),
+           "attention_frac": round(alg / avg_s / 1e9 / HBM_PEAK_GBS, 4)}
+    del eng, fr
+    torch.cuda.empty_cache()
+    return out
+
+
+def scoring_config(dev, reps=2):
+    """GSPO scoring: 512 sequences x (2048-frame prefix + 700..1024 response tokens), the teacher-forced forward
+    of token_logprobs (scripts/gspo.py:340-353), then the sequence-ratio loss and its gradient w.r.t. the
+    logits (scripts/gspo.py:459-477).
+    Algorithmic flops per sequence of n = 2048 + L rows: the projector per frame, 2 x weights per row less the
+    last layer's products for the prefix rows (only the L token rows need logits), causal attention
+    1024 n (n + 1) per layer, the LM head per token."""
+    from viktor_amd import gspo as G
+    from viktor_amd.synthetic import scoring_inputs
+    gm = _bf16_model(1, dev)
+    B = PREFIXES * GROUP
+    seqs, ended = scoring_inputs(B, 700, 1024, k=1, seed=5)
+    g = torch.Generator(device=dev).manual_seed(6)
+    fr = torch.randn(B, P, 512, generator=g, device=dev).to(torch.bfloat16)
+    plens = torch.full((B,), P, device=dev)
+    lp, mask = G.token_logprobs(gm, fr, plens, seqs, ended)  # the old policy's log-probs
+    old = (lp + 0.05 * torch.randn(lp.shape, generator=g, device=dev)).contiguous()
+    nb = torch.tensor([max(len(q), 1) for q in seqs], dtype=torch.float32, device=dev)
+    adv = torch.randn(B, generator=g, device=dev)
+    tin, tgt, _ = gm.batch(seqs, pad_to=128)
+    tin, tgt = tin.to(dev), tgt.clamp(min=0).to(dev).contiguous()
+    mask = mask.to(dev)
+
+    def run():  # teacher-forced logits, then log-probs + ratio + clipped loss + dL/dlogits in one kernel
+        logits = gm.logits(fr, tin, plens)
+        G.ops.gspo_score(logits.contiguous(), tgt, mask, old, nb, adv, 3e-4, 4e-4, grad=True)
+
+    ms = _timed(run, reps)
+    L = [len(q) + 1 for q in seqs]
+    flops = 0
+    for n_tok in L:
+        n = P + n_tok
+        flops += 2 * 2 * 512 * 512 * P + 2 * 3014656 * 8 * n - P * 5242880 + 8 * 1024 * n * (n + 1) + 2 * 512 * 7 * n_tok
+    out = {"sequences": B, "response_tokens": "U[700, 1024]", "ms": round(ms, 2),
+           "tokens_per_s": round(sum(L) / (ms / 1e3), 1), "alg_tflop": round(flops / 1e12, 2),
+           "achieved_tflops": round(flops / (ms / 1e3) / 1e12, 1),
+           "mfma_frac": round(flops / (ms / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+           "includes": "projector + teacher-forced 8-layer forward (padded to a multiple of 128 tokens, as the "
+                       "reference pads) + LM head + log-probs, ratio, clipped loss and dL/dlogits [512, T, 7]"}
+    del fr
+    torch.cuda.empty_cache()
+    return out
+
+
+def stress_config(dev, steps=32):
+    """Large-batch greedy decode: 4096 sequences x 2048-frame prefixes, each on its own cache rows (51.5 GB of
+    KV cache), vocab 7. Measured: the prefill, `steps` graph-replayed decode steps right after it, and the
+    decode-attention kernel at the lengths of the whole 1024-step decode (8-layer rotation)."""
+    from viktor_amd import DecodeEngine
+    gm = _bf16_model(1, dev)
+    B = 4096
+    g = torch.Generator(device=dev).manual_seed(7)
+    fr = torch.randn(B * P, 512, generator=g, device=dev).to(torch.bfloat16)
+    eng = DecodeEngine(gm, B, NEW, P, temperature=0.0)
+    plens = [P] * B
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    eng.generate(fr, plens, steps=steps)
+    torch.cuda.synchronize()
+    e[0].record()
+    eng.prefill(fr, plens)
+    e[1].record()
+    eng.decode(steps)
+    e[2].record()
+    torch.cuda.synchronize()
+    pre, dec = e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2])
+    avg_s, alg = decode_attention_timing(eng, plens, NEW - 1, n_points=8, rounds=1)
+    early_roof = decode_roofline_ms(lambda j: B * (P + 2 + j), steps - 1, B)
+    out = {"sequences": B, "kv_cache_gb": round(2 * eng.cache.k.numel() * 2 / 1e9, 2), "prefill_ms": round(pre, 1),
+           "prefill_mfma_frac": round(prefill_flops(B, P) / (pre / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+           "decode_ms_per_step_early": round(dec / (steps - 1), 3),
+           "decode_hbm_frac_early": round(early_roof / dec, 4),
+           "attention": {"avg_launch_us": round(avg_s * 1e6, 1), "alg_bytes_per_launch": int(alg),
+                         "achieved_gbs": round(alg / avg_s / 1e9, 1),
+                         "frac": round(alg / avg_s / 1e9 / HBM_PEAK_GBS, 4)}}
+    del eng, fr
+    torch.cuda.empty_cache()
+    return out
+
+
+def other_configs(dev, gm, fr, u):
+    """The benchmark's other configurations, each with its own roofline (see the functions)."""
+    log("config: rollout without prefix sharing")
+    res = {"gspo_rollout_unshared": rollout_ungrouped(dev, gm, fr, u)}
+    log("config: varlen prefill + 4-mer decode")
+    res["varlen_kmer"] = varlen_kmer_config(dev)
+    log("config: scoring")
+    res["scoring"] = scoring_config(dev)
+    log("config: 4096-sequence stress")
+    res["stress_4096"] = stress_config(dev)
+    return res
+
+
+def decode_attention_timing(eng, prefix_lens, steps, n_points=32, rounds=2, warm=False):
+    """Average duration (HIP events on the launch stream) and algorithmic bytes of one decode-attention call at
+    the attended lengths of decode steps j = 0 .. steps - 1, sampled at n_points evenly spaced steps. Sequence
+    b attends prefix_lens[b] + 1 positions (frames + BOS) and j + 1 own tokens at step j.
+
+    As in the captured rollout, each timed call reads a layer whose K/V no recent call has touched: the calls
+    rotate over the 8 layers' caches (`rounds` passes of 8 calls per point, after one untimed pass), so
+    nothing the call reads is still in the 256 MB Infinity Cache from the call before -- exactly the situation
+    of layer i's attention inside a decode step, which follows the other 7 layers' attention reads. warm=True
+    instead repeats one layer's call back to back (5 calls), whose bytes then come partly from that cache."""
+    B, G = eng.B, eng.G
+    dev = eng.cache.k.device
+    layers = eng.cache.k.shape[0]
     q = torch.randn(B, 8, 64, device=dev).to(torch.bfloat16)
-    js = [round(i * (NEW - 2) / (n_points - 1)) for i in range(n_points)]
+    pl = torch.as_tensor(prefix_lens, dtype=torch.int64)
+    js = [round(i * (steps - 1) / (n_points - 1)) for i in range(n_points)]
     total_ms, total_bytes, launches = 0.0, 0.0, 0
     stream = torch.cuda.current_stream()
+    plen = None
     if G > 1:
-        pc, ws = eng.prefix_cache, eng.grouped_workspace
-        plen = torch.full((B // G,), P + 1, dtype=torch.int32, device=dev)
+        plen = (pl[::G] + 1).to(torch.int32).to(dev)
     for j in js:
         if G > 1:
             lens = torch.full((B,), j + 1, dtype=torch.int32, device=dev)
-            call = lambda: ops.decode_attention_grouped(q, pc.k[3], pc.v[3], plen, cache.k[3], cache.v[3], lens, G,
-                                                        workspace=ws)
-            kv_rows = (B // G) * (P + 1) + B * (j + 1)
+            kv_rows = int((pl[::G] + 1).sum()) + B * (j + 1)
         else:
-            lens = torch.full((B,), P + 2 + j, dtype=torch.int32, device=dev)
-            call = lambda: ops.decode_attention(q, cache.k[3], cache.v[3], lens, workspace=eng.fast.decode_workspace)
-            kv_rows = B * (P + 2 + j)
-        call()  # warm
+            lens = (pl + 2 + j).to(torch.int32).to(dev)
+            kv_rows = int((pl + 2 + j).sum())
+        calls = [_attention_call(eng, i, q, lens, plen) for i in range(layers)]
+        seq = [calls[3]] * 5 if warm else calls * rounds
+        for c in ([calls[3]] if warm else calls):  # untimed: first-launch costs, and the rotation's start state
+            c()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        for _ in range(reps):
-            call()
+        for c in seq:
+            c()
         e1.record(stream)
         e1.synchronize()
         total_ms += e0.elapsed_time(e1)
-        launches += reps
-        total_bytes += reps * (kv_rows * KV_ROW_BYTES + 2 * B * 8 * 64 * 2)
+        launches += len(seq)
+        total_bytes += len(seq) * (kv_rows * KV_ROW_BYTES + 2 * B * 8 * 64 * 2)
     avg_s = total_ms / 1e3 / launches
     return avg_s, total_bytes / launches
 
 
-def cpu_baseline(seconds_budget=12.0, max_rounds=20):
-    """The CPU oracle (fp32 reference semantics) on a bounded sample of the same workload: rounds of 2
-    sequences x 2048-frame prefix x 64 sampled tokens (prefill + decode, fresh frames each round) until
-    seconds_budget of CPU time has been spent; tokens/s over the whole sample."""
+def _cpu_info():
+    """Host CPU facts for the baseline: logical CPUs, the ones this process may run on, the cgroup quota."""
+    info = {"os_cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()
+        if quota != "max":
+            info["cgroup_cpus"] = round(int(quota) / int(period), 2)
+    except (OSError, ValueError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            info["model"] = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "?")
+    except OSError:
+        info["model"] = "?"
+    return info
+
+
+def cpu_baseline(runs=3):
+    """The CPU oracle in fp32 (the reference's torch path restated: viktor/decoder.py + viktor/engine.py with the
+    torch backend) on the CPU-plumbing configuration at full size: 4 sequences x 2048-frame prefixes of N(0, 1)
+    features, 8 layers, 64 greedy steps, weights and frames from seed 0 -- `runs` runs (about 3.4 s each on 16
+    EPYC cores). Threads: every CPU this process may use (the affinity set, capped by a cgroup CPU quota)."""
     from oracle import reference as R
-    from viktor_amd.synthetic import frames, make_model, uniforms
-    threads = min(16, os.cpu_count() or 1)
+    from viktor_amd.synthetic import frames, make_model
+    info = _cpu_info()
+    threads = info["affinity"]
+    if "cgroup_cpus" in info:
+        threads = max(1, min(threads, int(info["cgroup_cpus"])))
     torch.set_num_threads(threads)
     m = make_model(1, n_layers=8, seed=0, rope_theta=1e6)
-    n_seq, steps = 2, 64
-    eng = R.RefEngine(R.RefModel(m, "fp32"), steps, temperature=1.0)
-    dt, rounds = 0.0, 0
-    while dt < seconds_budget and rounds < max_rounds:
-        fr = frames(n_seq, P, 512, seed=10 + rounds)
-        u = uniforms(n_seq, steps, seed=100 + rounds)
-        t0 = time.perf_counter()
-        eng.run([fr[i] for i in range(n_seq)], uniforms=u)
-        dt += time.perf_counter() - t0
-        rounds += 1
-    return {"value": rounds * n_seq * steps / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{rounds} rounds of {n_seq} sequences x {P}-frame prefix x {steps} sampled tokens "
-                      f"(prefill + decode), fp32 CPU restatement of the reference torch path; {dt:.1f} s"}
+    n_seq, steps = 4, 64
+    eng = R.RefEngine(R.RefModel(m, "fp32"), steps, temperature=0.0)
+    fr = frames(n_seq, P, 512, seed=0)
+    t0 = time.perf_counter()
+    for _ in range(runs):
+        eng.run([fr[i] for i in range(n_seq)])
+    dt = time.perf_counter() - t0
+    return {"value": round(runs * n_seq * steps / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"the CPU-plumbing configuration at full size, {runs} runs: {n_seq} sequences x {P}-frame "
+                      f"prefix x {steps} greedy tokens (prefill + decode), 8 layers, fp32 CPU restatement of the "
+                      f"reference torch path; {dt:.1f} s", "host": info}
 
 
 def reward_timing(tokenizer, reps=5):
@@ -339,9 +584,10 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other configurations' measurements")
     ap.add_argument("--prefill-batch", type=int, default=128)
-    ap.add_argument("--mode", choices=["rollout", "kernels", "encoder", "prefill"], default="rollout",
-                    help="kernels: decode-attention traffic probe; encoder / prefill: that timing object alone")
+    ap.add_argument("--mode", choices=["rollout", "kernels", "encoder", "prefill", "configs"], default="rollout",
+                    help="kernels: decode-attention traffic probe; encoder / prefill / configs: that object alone")
     ap.add_argument("--group-size", type=int, default=GROUP, help="sequences sharing one prefix KV copy (1: none)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -353,6 +599,14 @@ def main():
         return
     if args.mode == "encoder":
         print(json.dumps({"encoder": encoder_timing(reps=max(args.steps, 1))}), flush=True)
+        return
+    if args.mode == "configs":
+        from viktor_amd.synthetic import frames, uniforms
+        dev = torch.device("cuda", 0)
+        _, gm = build_model(dev)
+        fr = frames(PREFIXES, P, 512, seed=0).to(dev).repeat_interleave(GROUP, 0).reshape(-1, 512)
+        u = uniforms(PREFIXES * GROUP, NEW, seed=1).to(dev)
+        print(json.dumps({"configs": other_configs(dev, gm, fr, u)}), flush=True)
         return
     if args.mode == "prefill":
         print(json.dumps({"prefill": prefill_timing(reps=max(args.steps, 1), prefill_batch=args.prefill_batch,
@@ -402,7 +656,8 @@ def main():
     value = B * NEW * args.steps / dt
 
     log("decode-attention timing")
-    avg_s, alg_bytes = decode_attention_timing(eng)
+    avg_s, alg_bytes = decode_attention_timing(eng, plens, NEW - 1)
+    warm_s, warm_bytes = decode_attention_timing(eng, plens, NEW - 1, warm=True)
     if args.group_size == 1:
         attn_kernels = "decode_attention (decode_attn_kernel)"
     else:
@@ -424,11 +679,14 @@ def main():
                    "mfma_frac": round(pf / (prefill_ms / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
     out = tokens_check = eng.out[:, :NEW].cpu()
     live = int(((out != 0) & (out != 2)).sum())
+    del eng
+    torch.cuda.empty_cache()
+    configs = {}
+    if not args.no_configs:
+        configs = other_configs(dev, gm, fr, u)
     log("gspo reward")
     reward = reward_timing(gm.tokenizer)
     log("gspo update micro-batch")
-    del eng
-    torch.cuda.empty_cache()
     update = update_timing()
     log("encoder")
     torch.cuda.empty_cache()
@@ -454,8 +712,14 @@ def main():
                      "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "avg_launch_us": round(avg_s * 1e6, 2),
-                     "alg_bytes_per_launch": int(alg_bytes)},
+                     "alg_bytes_per_launch": int(alg_bytes),
+                     "timing": "HIP events over calls at 32 evenly spaced decode steps' lengths, rotating over the "
+                               "8 layers' caches as the captured step does (no call reads what the one before "
+                               "left in the 256 MB Infinity Cache)",
+                     "warm_avg_launch_us": round(warm_s * 1e6, 2),
+                     "warm_frac": round(warm_bytes / warm_s / 1e9 / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,
+        "configs": configs,
         "gspo_reward": reward,
         "gspo_update": update,
         "encoder": encoder,
