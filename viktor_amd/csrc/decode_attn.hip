@@ -352,8 +352,8 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
 #pragma unroll
       for (int c = 0; c < 2; ++c) f[pb][c] = *reinterpret_cast<const u32x4 *>(base + row_off(r, pb) + 32 * c);
   };
-  // the first tile is a prefix tile whenever wid < npre: its loads go out before anything else (rows
-  // clamped to pre_max - 1, always valid; its mask waits for the length)
+  // the first tile is a prefix tile whenever wid < npre: its loads need no length (rows clamped to pre_max - 1,
+  // always valid; its mask waits for the length)
   TileRef cur;
   cur.k = kpre;
   cur.v = vpre;
@@ -364,13 +364,9 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   cur.seg = 0;
   cur.mc = 0;
   const bool spec = wid < npre;
-  if (spec) {
-    load(kf, cur.k, cur);
-    asm volatile("" ::: "memory");
-    load(vf, cur.v, cur);
-  }
 
-  // Q^T fragments (loaded before the lengths, so both round trips overlap): column j = 16 cb + col -> member
+  // Q^T fragments (loaded before the lengths, so both round trips overlap, and before the first tile's K / V, see
+  // below): column j = 16 cb + col -> member
   // j / 4, head kvh * 4 + j % 4, the two 32-wide halves of D
   bf16x8 bq[NCB][2];
 #pragma unroll
@@ -396,6 +392,14 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   } else if (lane == G) {
     const int64_t l = pre_len[pp];
     len = static_cast<int>(l < 1 ? 1 : (l > pre_max ? pre_max : l));
+  }
+  // The first tile's K / V go out after the query and length loads. Those are consumed before the loop, so with
+  // them older than K / V the compiler's counted waits at the loop head are for K alone, V staying in flight; the
+  // other order (K / V first) made every iteration wait for all loads, as if q were still outstanding.
+  if (spec) {
+    load(kf, cur.k, cur);
+    asm volatile("" ::: "memory");
+    load(vf, cur.v, cur);
   }
   int incl = cnt;
 #pragma unroll
