@@ -320,6 +320,20 @@ int vk_attention_backward(const void *q, const void *k, const void *v, const voi
                           const int32_t *k_plan, int32_t n_kblocks, int64_t n_rows, int64_t stride_tok, float *dd,
                           float *dq, float *dk, float *dv, int32_t H, int32_t HKV, int32_t D, void *stream);
 
+/*
+ * Weight gradient of a linear layer over packed rows: out[Ka, Kb] = a^T b = sum_r a[r, ka] b[r, kb] for a [N, Ka]
+ * (the layer's output gradient) and b [N, Kb] (its input), bf16 row-major with row strides lda / ldb (elements,
+ * multiples of 8); fp32 accumulation, the N rows split into slices whose fp32 partials are summed in slice order
+ * (deterministic), then rounded to bf16 (out_dtype VK_DTYPE_BF16, the autocast matmul output) or kept fp32.
+ * Ka % 256 == 0, Kb % 128 == 0; workspace: vk_wgrad_workspace() bytes.
+ * Replaces the weight-gradient products of nn.Linear under autocast in the update's backward
+ * (viktor/decoder.py:58-59, 114-115, viktor/model.py:35 differentiated by loss.backward(), scripts/gspo.py:477).
+ */
+int vk_wgrad(const void *a, int64_t lda, const void *b, int64_t ldb, int64_t N, int32_t Ka, int32_t Kb, void *out,
+             int32_t out_dtype, void *workspace, int64_t workspace_bytes, void *stream);
+
+int vk_wgrad_workspace(int64_t N, int32_t Ka, int32_t Kb, int64_t *bytes);
+
 /* Workgroups (= rows of the weight-gradient partials) vk_rmsnorm_backward uses for n rows. */
 int vk_rmsnorm_backward_blocks(int64_t n, int32_t *blocks);
 

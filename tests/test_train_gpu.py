@@ -272,6 +272,31 @@ def test_gspo_update_steps_move_weights():
     #                                     does nothing only at step 1, so allow one untouched tensor)
 
 
+@pytest.mark.parametrize("n,ka,kb", [(90112, 3072, 512), (90112, 512, 1536), (4099, 512, 512), (33, 768, 512),
+                                     (1000, 256, 128), (64 * 1024 + 17, 768, 512)])
+def test_wgrad_kernel_against_fp64(n, ka, kb):
+    """vk_wgrad (MFMA over LDS transpose reads, row slices summed in order): a^T b against the fp64 product, fp32
+    output within fp32 accumulation error, bf16 output within one rounding of it; ragged row counts (the masked
+    last step), a single slice (33 rows) and the update's shapes (gate_up, down at 90112 packed rows)."""
+    g = gen(n + ka)
+    a = (torch.randn(n, ka, generator=g) * 0.1).to(BF)
+    b = (torch.randn(n, kb, generator=g) * 0.1).to(BF)
+    ad, bd = a.to(DEV), b.to(DEV)
+    a64, b64 = ad.double(), bd.double()  # the fp64 reference products on the device (exact bf16 inputs)
+    want = a64.t() @ b64
+    scale = a64.abs().t() @ b64.abs()  # sum of |terms|: the scale of the fp32 accumulation error
+    del a64, b64
+    got32 = ops.wgrad(ad, bd, out_dtype=torch.float32).double()
+    assert bool(((got32 - want).abs() <= scale * 2.0 ** -20 + 1e-9).all()), float((got32 - want).abs().max())
+    got16 = ops.wgrad(ad, bd).double()
+    assert bool(((got16 - want).abs() <= want.abs() * 2.0 ** -8 + scale * 2.0 ** -20 + 1e-9).all())
+    assert torch.equal(ops.wgrad(ad, bd), ops.wgrad(ad, bd))  # deterministic
+    # a strided view (rows of a wider buffer), as the backward's slices of packed activations are
+    wide = torch.zeros(n, ka + 64, dtype=BF, device=DEV)
+    wide[:, 32:32 + ka] = ad
+    assert torch.equal(ops.wgrad(wide[:, 32:32 + ka], bd, out_dtype=torch.float32).double(), got32)
+
+
 @pytest.mark.parametrize("n", [16 * 1024, 16 * 1024 + 37, 1000])
 def test_weight_gradient_split_k(n):
     """a^T b of the update's weight gradients: the 16-slice split-K product (with a remainder of rows past the

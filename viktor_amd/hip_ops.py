@@ -552,6 +552,34 @@ def attention_backward(q, k, v, out, dout, lse, q_plan: AttentionPlan, k_plan: K
     return dq, dk, dv
 
 
+_wgrad_ws = {}
+
+
+def wgrad(a, b, out_dtype=BF16):
+    """Weight gradient a^T b [Ka, Kb] over the rows of a [N, Ka] and b [N, Kb] (bf16, unit column stride):
+    fp32 accumulation in row slices summed in a fixed order, rounded to bf16 once (or fp32). Ka % 256 == 0,
+    Kb % 128 == 0. The workspace is cached per (N, Ka, Kb, device)."""
+    require_device(a, "wgrad")
+    _require(a.dim() == 2 and b.dim() == 2 and a.shape[0] == b.shape[0] and a.dtype == b.dtype == BF16,
+             "wgrad: a [N, Ka], b [N, Kb] bf16")
+    _require(a.stride(1) == 1 and b.stride(1) == 1, "wgrad: unit column stride")
+    N, Ka = a.shape
+    Kb = b.shape[1]
+    key = (N, Ka, Kb, a.device)
+    ws = _wgrad_ws.get(key)
+    if ws is None:
+        n = ctypes.c_int64(0)
+        call("vk_wgrad_workspace", N, Ka, Kb, ctypes.byref(n))
+        ws = torch.empty(max(int(n.value), 16), dtype=torch.uint8, device=a.device)
+        if len(_wgrad_ws) >= 8:  # a backward uses a handful of shapes; keep the cache bounded
+            _wgrad_ws.clear()
+        _wgrad_ws[key] = ws
+    out = torch.empty(Ka, Kb, dtype=out_dtype, device=a.device)
+    call("vk_wgrad", ptr(a), a.stride(0), ptr(b), b.stride(0), N, Ka, Kb, ptr(out),
+         VK_DTYPE_BF16 if out_dtype == BF16 else VK_DTYPE_F32, ptr(ws), ws.numel(), stream_handle())
+    return out
+
+
 def _norm_blocks(n):
     b = ctypes.c_int32(0)
     _lib.check(_lib.load().vk_rmsnorm_backward_blocks(n, ctypes.byref(b)), "rmsnorm_backward_blocks")
