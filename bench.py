@@ -586,8 +586,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the other configurations' measurements")
     ap.add_argument("--prefill-batch", type=int, default=128)
-    ap.add_argument("--mode", choices=["rollout", "kernels", "encoder", "prefill", "configs"], default="rollout",
-                    help="kernels: decode-attention traffic probe; encoder / prefill / configs: that object alone")
+    ap.add_argument("--mode", choices=["rollout", "kernels", "encoder", "prefill", "configs", "update"],
+                    default="rollout",
+                    help="kernels: decode-attention traffic probe; encoder / prefill / configs / update: that object alone")
     ap.add_argument("--group-size", type=int, default=GROUP, help="sequences sharing one prefix KV copy (1: none)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -607,6 +608,9 @@ def main():
         fr = frames(PREFIXES, P, 512, seed=0).to(dev).repeat_interleave(GROUP, 0).reshape(-1, 512)
         u = uniforms(PREFIXES * GROUP, NEW, seed=1).to(dev)
         print(json.dumps({"configs": other_configs(dev, gm, fr, u)}), flush=True)
+        return
+    if args.mode == "update":
+        print(json.dumps({"gspo_update": update_timing(steps=max(args.steps, 1), warmup=args.warmup)}), flush=True)
         return
     if args.mode == "prefill":
         print(json.dumps({"prefill": prefill_timing(reps=max(args.steps, 1), prefill_batch=args.prefill_batch,

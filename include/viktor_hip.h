@@ -334,6 +334,39 @@ int vk_wgrad(const void *a, int64_t lda, const void *b, int64_t ldb, int64_t N, 
 
 int vk_wgrad_workspace(int64_t N, int32_t Ka, int32_t Kb, int64_t *bytes);
 
+/*
+ * Epilogue of the per-frame projector's linears (viktor/model.py:35: nn.Linear -> nn.GELU() -> nn.Linear under
+ * torch.autocast bf16, applied at viktor/model.py:74): over an fp32 product y [n, d] and an fp32 bias [d],
+ * gelu == 0: out = bf16(y + b); gelu != 0: pre = bf16(y + b) and out = bf16(gelu(pre)), the exact erf GELU.
+ * d % 8 == 0; 16-byte aligned tensors.
+ */
+int vk_bias_act(const float *y, const float *bias, void *pre, void *out, int64_t n, int32_t d, int32_t gelu,
+                void *stream);
+
+/* Workgroups (= rows of the column-sum partials) vk_act_backward uses for n rows of width d. */
+int vk_act_backward_blocks(int64_t n, int32_t d, int32_t *blocks);
+
+/*
+ * Backward rows of the projector (the backward of vk_bias_act's forward): gelu != 0: din = bf16(dout gelu'(pre))
+ * [n, d] bf16 and part[blocks, d] = per-workgroup column sums of din (the first linear's bias gradient);
+ * gelu == 0: part = per-workgroup column sums of dout (the second linear's bias gradient; pre / din unused).
+ * blocks from vk_act_backward_blocks; reduce part with vk_colsum. d % 8 == 0, d <= 2048.
+ */
+int vk_act_backward(const void *pre, const void *dout, void *din, float *part, int32_t blocks, int64_t n, int32_t d,
+                    int32_t gelu, void *stream);
+
+/* Bytes of workspace vk_embed_grad needs for n rows, V token ids and width d. */
+int vk_embed_grad_workspace(int64_t n, int32_t V, int32_t d, int64_t *bytes);
+
+/*
+ * Token-embedding gradient (the backward of nn.Embedding, viktor/decoder.py:127, gathered at viktor/model.py:77):
+ * out[v, :] = sum of d_rows[r, :] over the rows r with tokens[r] == v, fp32 [V, d], from d_rows [n, d] bf16 (row
+ * stride ld elements) and tokens [n] int64. Row slices summed in a fixed order (deterministic, no atomics); ids
+ * outside [0, V) add nothing. d % 8 == 0; workspace: vk_embed_grad_workspace() bytes.
+ */
+int vk_embed_grad(const void *d_rows, int64_t ld, const int64_t *tokens, int64_t n, int32_t V, int32_t d, float *out,
+                  void *workspace, int64_t workspace_bytes, void *stream);
+
 /* Workgroups (= rows of the weight-gradient partials) vk_rmsnorm_backward uses for n rows. */
 int vk_rmsnorm_backward_blocks(int64_t n, int32_t *blocks);
 

@@ -297,16 +297,80 @@ def test_wgrad_kernel_against_fp64(n, ka, kb):
     assert torch.equal(ops.wgrad(wide[:, 32:32 + ka], bd, out_dtype=torch.float32).double(), got32)
 
 
-@pytest.mark.parametrize("n", [16 * 1024, 16 * 1024 + 37, 1000])
-def test_weight_gradient_split_k(n):
-    """a^T b of the update's weight gradients: the 16-slice split-K product (with a remainder of rows past the
-    last whole slice, and the single-product path below 16 x 1024 rows) equals the fp64 product rounded once
-    to bf16, up to one bf16 rounding step."""
-    g = gen(n)
-    a = (torch.randn(n, 192, generator=g) * 0.1).to(BF)
-    b = (torch.randn(n, 320, generator=g) * 0.1).to(BF)
-    got = TR._wgrad(a.to(DEV), b.to(DEV)).float().cpu()
-    want = a.double().t() @ b.double()
-    assert got.shape == (192, 320)
-    err = (got.double() - want).abs()
-    assert bool((err <= want.abs() * 2.0 ** -8 + 1e-6).all()), err.max().item()
+@pytest.mark.parametrize("n,d", [(3000, 512), (77, 136), (4099, 1024)])
+def test_projector_bias_gelu_forward_and_backward(n, d):
+    """vk_bias_act / vk_act_backward against fp64 on the CPU: pre = bf16(y + b) exactly; out = bf16(gelu(pre)) and
+    din = bf16(dout gelu'(pre)) within one bf16 rounding of the fp64 values plus the fp32 cancellation of
+    1 + erf(x / sqrt 2) at negative x (2^-21 |x| for gelu, 2^-19 |dout| for its derivative); the bias gradients
+    (column sums) to fp32 accumulation error."""
+    g = gen(n + d)
+    y = torch.randn(n, d, generator=g) * 3
+    b = torch.randn(d, generator=g).to(BF).float()
+    pre, out = (t.cpu().float() for t in ops.bias_act(y.to(DEV), b.to(DEV), gelu=True))
+    want_pre = (y + b).to(BF).float()
+    assert torch.equal(pre, want_pre)
+    x64 = want_pre.double()
+    cdf = 0.5 * (1 + torch.special.erf(x64 / math.sqrt(2)))
+    want_out = x64 * cdf
+    err = (out.double() - want_out).abs()
+    assert bool((err <= want_out.abs() * 2.0 ** -8 + x64.abs() * 2.0 ** -21 + 1e-30).all()), float(err.max())
+    plain = ops.bias_act(y.to(DEV), b.to(DEV), gelu=False).cpu().float()
+    assert torch.equal(plain, want_pre)
+    dout = torch.randn(n, d, generator=g).to(BF)
+    din, gb = ops.act_backward(dout.to(DEV), pre.to(BF).to(DEV))
+    want_din = dout.double() * (cdf + x64 * torch.exp(-0.5 * x64 * x64) / math.sqrt(2 * math.pi))
+    got_din = din.cpu().float()
+    err = (got_din.double() - want_din).abs()
+    assert bool((err <= want_din.abs() * 2.0 ** -8 + dout.double().abs() * 2.0 ** -19 + 1e-30).all()), float(err.max())
+    ref_gb = got_din.double().sum(0)
+    scale = got_din.double().abs().sum(0)
+    assert bool(((gb.cpu().double() - ref_gb).abs() <= scale * 2.0 ** -20).all())
+    gb2 = ops.act_backward(dout.to(DEV)).cpu().double()
+    assert bool(((gb2 - dout.double().sum(0)).abs() <= dout.double().abs().sum(0) * 2.0 ** -20).all())
+    assert torch.equal(ops.act_backward(dout.to(DEV)), ops.act_backward(dout.to(DEV)))  # fixed order
+
+
+@pytest.mark.parametrize("n,V,d", [(32 * 1024 + 5, 7, 512), (5000, 343, 512), (999, 70, 1024), (300, 7, 136),
+                                   (0, 7, 512)])
+def test_embed_grad_against_fp64(n, V, d):
+    """vk_embed_grad: per-token sums of the gradient rows against the fp64 index_add on the CPU: 7 ids (the base
+    vocabulary), 343 and 70 (several 32-id chunks, the last ragged), two 512-column blocks, a partial block
+    (d = 136), no rows at all; ids outside [0, V) add nothing; repeated calls are bit-identical."""
+    g = gen(n + V + d)
+    tok = torch.randint(0, V, (n,), generator=g)
+    if n > 10:
+        tok[3], tok[7] = V, -1  # out of range: ignored
+    rows = torch.randn(n, d, generator=g).to(BF)
+    got = ops.embed_grad(rows.to(DEV), tok.to(DEV), V).cpu().double()
+    keep = (tok >= 0) & (tok < V)
+    want = torch.zeros(V, d, dtype=torch.float64).index_add_(0, tok[keep], rows[keep].double())
+    scale = torch.zeros(V, d, dtype=torch.float64).index_add_(0, tok[keep], rows[keep].double().abs())
+    assert bool(((got - want).abs() <= scale * 2.0 ** -20).all()), float((got - want).abs().max())
+    if n:
+        assert torch.equal(ops.embed_grad(rows.to(DEV), tok.to(DEV), V), ops.embed_grad(rows.to(DEV), tok.to(DEV), V))
+        # a strided view (rows of a wider buffer)
+        wide = torch.zeros(n, d + 16, dtype=BF, device=DEV)
+        wide[:, 8:8 + d] = rows.to(DEV)
+        assert torch.equal(ops.embed_grad(wide[:, 8:8 + d], tok.to(DEV), V).cpu().double(), got)
+
+
+@pytest.mark.parametrize("V", [7, 343])
+def test_lm_head_backward_products(V):
+    """_LMHead: logits = bf16(h W^T) and its backward (dh = dz W, dW = dz^T h through the zero-padded V-wide
+    operand) against fp64 products of the same bf16 operands, each within one bf16 rounding plus fp32 error."""
+    g = gen(V)
+    n = 4500
+    h = (torch.randn(n, 512, generator=g)).to(BF)
+    w = torch.randn(V, 512, generator=g) * 0.05
+    dz = (torch.randn(n, V, generator=g) * 0.1).to(BF)
+    hd = h.to(DEV).requires_grad_(True)
+    wd = w.to(DEV).requires_grad_(True)
+    z = TR._LMHead.apply(hd, wd)
+    z.backward(dz.to(DEV))
+    wb = w.to(BF).double()
+    for got, want, scale in ((z.detach(), h.double() @ wb.t(), h.double().abs() @ wb.abs().t()),
+                             (hd.grad, dz.double() @ wb, dz.double().abs() @ wb.abs()),
+                             (wd.grad, dz.double().t() @ h.double(), dz.double().abs().t() @ h.double().abs())):
+        got = got.cpu().double()
+        assert bool(((got - want).abs() <= want.abs() * 2.0 ** -8 + scale * 2.0 ** -20 + 1e-12).all()), \
+            float((got - want).abs().max())

@@ -54,6 +54,11 @@ SIGNATURES = {
                               _I32, _I32, _P],
     "vk_wgrad": [_P, _I64, _P, _I64, _I64, _I32, _I32, _P, _I32, _P, _I64, _P],
     "vk_wgrad_workspace": [_I64, _I32, _I32, ctypes.POINTER(_I64)],
+    "vk_bias_act": [_P, _P, _P, _P, _I64, _I32, _I32, _P],
+    "vk_act_backward_blocks": [_I64, _I32, ctypes.POINTER(_I32)],
+    "vk_act_backward": [_P, _P, _P, _P, _I32, _I64, _I32, _I32, _P],
+    "vk_embed_grad_workspace": [_I64, _I32, _I32, ctypes.POINTER(_I64)],
+    "vk_embed_grad": [_P, _I64, _P, _I64, _I32, _I32, _P, _P, _I64, _P],
     "vk_rmsnorm_backward_blocks": [_I64, ctypes.POINTER(_I32)],
     "vk_rmsnorm_backward": [_P, _P, _P, _I32, _P, _P, _P, _I64, _I32, _F, _P],
     "vk_colsum": [_P, _P, _I32, _I32, _I32, _P],

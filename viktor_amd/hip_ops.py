@@ -580,6 +580,55 @@ def wgrad(a, b, out_dtype=BF16):
     return out
 
 
+def bias_act(y, bias, gelu):
+    """Projector linear epilogue: y [n, d] fp32 (the product), bias [d] fp32 -> gelu False: bf16(y + b);
+    gelu True: (pre, out) = (bf16(y + b), bf16(gelu(pre))), the exact erf GELU. Reference: viktor/model.py:35
+    (nn.Linear, nn.GELU() under torch.autocast bf16)."""
+    require_device(y, "bias_act")
+    _require(y.dim() == 2 and y.dtype == torch.float32 and bias.dtype == torch.float32 and bias.shape == (y.shape[1],)
+             and _contig(y, bias), "bias_act: y [n, d] fp32, bias [d] fp32, contiguous")
+    n, d = y.shape
+    out = torch.empty(n, d, dtype=BF16, device=y.device)
+    pre = torch.empty(n, d, dtype=BF16, device=y.device) if gelu else None
+    call("vk_bias_act", ptr(y), ptr(bias), ptr(pre), ptr(out), n, d, int(bool(gelu)), stream_handle())
+    return (pre, out) if gelu else out
+
+
+def act_backward(dout, pre=None):
+    """Projector backward rows: dout [n, d] bf16. With pre (the GELU input, bf16 [n, d]): returns (din bf16 =
+    dout gelu'(pre), bias gradient fp32 [d] = column sums of din); without: the column sums of dout (fp32 [d]).
+    Column sums in a fixed order."""
+    require_device(dout, "act_backward")
+    _require(dout.dim() == 2 and dout.dtype == BF16 and _contig(dout, pre)
+             and (pre is None or (pre.shape == dout.shape and pre.dtype == BF16)), "act_backward: shapes")
+    n, d = dout.shape
+    b = ctypes.c_int32(0)
+    call("vk_act_backward_blocks", n, d, ctypes.byref(b))
+    part = torch.empty(b.value, d, dtype=torch.float32, device=dout.device)
+    din = torch.empty_like(dout) if pre is not None else None
+    call("vk_act_backward", ptr(pre), ptr(dout), ptr(din), ptr(part), b.value, n, d, int(pre is not None),
+         stream_handle())
+    return (din, colsum(part)) if pre is not None else colsum(part)
+
+
+def embed_grad(d_rows, tokens, vocab):
+    """Token-embedding gradient: fp32 [vocab, d] with row v = the sum of d_rows[r] (bf16 [n, d], unit column
+    stride) over tokens[r] == v (int64 [n]), summed in a fixed order. Reference: the backward of nn.Embedding,
+    viktor/decoder.py:127, as viktor/model.py:77 gathers it."""
+    require_device(d_rows, "embed_grad")
+    _require(d_rows.dim() == 2 and d_rows.dtype == BF16 and d_rows.stride(1) == 1, "embed_grad: d_rows [n, d] bf16")
+    _require(tokens.shape == (d_rows.shape[0],) and tokens.dtype == torch.long and tokens.is_contiguous(),
+             "embed_grad: tokens [n] int64")
+    n, d = d_rows.shape
+    nb = ctypes.c_int64(0)
+    call("vk_embed_grad_workspace", n, vocab, d, ctypes.byref(nb))
+    ws = torch.empty(max(int(nb.value) // 4, 4), dtype=torch.float32, device=d_rows.device)
+    out = torch.empty(vocab, d, dtype=torch.float32, device=d_rows.device)
+    call("vk_embed_grad", ptr(d_rows), d_rows.stride(0), ptr(tokens), n, vocab, d, ptr(out), ptr(ws), 4 * ws.numel(),
+         stream_handle())
+    return out
+
+
 def _norm_blocks(n):
     b = ctypes.c_int32(0)
     _lib.check(_lib.load().vk_rmsnorm_backward_blocks(n, ctypes.byref(b)), "rmsnorm_backward_blocks")

@@ -7,12 +7,16 @@ viktor/model.py:55-60 (Basecaller.logits), viktor/decoder.py:54-144 (the decoder
 
 The model keeps fp32 master weights, as the reference's trainable model does; every forward casts them to
 bf16 (the autocast the reference trains under) and every weight gradient arrives in fp32 through that cast.
-The decoder stack is one autograd node (`_DecoderStack`): its forward runs the prefill kernels over the
-packed windows and keeps each layer's activations, its backward runs the HIP backward kernels (attention,
-RMSNorm, QK-norm + RoPE, SwiGLU) and the plain input GEMMs (hipBLASLt through torch.matmul); the weight
-gradients are split-K batched products (hipBLASLt, fp32 slices summed in order).
-The projector, the embedding gather and the LM head (V = 7 columns) stay torch autograd ops, as in the
-reference. The residual stream is bf16, the rounding points of the inference path.
+Every product of the update runs on the HIP kernels:
+  * the decoder stack is one autograd node (`_DecoderStack`): its forward runs the prefill kernels over the
+    packed windows and keeps each layer's activations; its backward runs the HIP backward kernels (attention,
+    RMSNorm, QK-norm + RoPE, SwiGLU), the input gradients dX = dY W as MFMA products against W^T (formed once
+    per backward) and the weight gradients dW = dY^T X as split-K MFMA reductions (vk_wgrad: fp32 row slices
+    summed in a fixed order, rounded to bf16 once as the autocast matmul output);
+  * the per-frame projector (`_Projector`: linear, bias + GELU, linear, bias) and the LM head (`_LMHead`,
+    V = 7 or 343 columns: the V-wide operand zero-padded to the products' tile width) likewise;
+  * the token-embedding gradient is a deterministic segmented row sum (vk_embed_grad).
+The residual stream is bf16, the rounding points of the inference path.
 """
 
 from typing import List, Optional, Sequence
@@ -34,13 +38,6 @@ def decoder_params(dec) -> List[torch.Tensor]:
     return out + [sd["norm.weight"]]
 
 
-def _mm(a, b):
-    """bf16 product a @ b (hipBLASLt, fp32 accumulation). a may be a transposed view (hipBLASLt reads it in
-    place); b is contiguous."""
-    assert b.is_contiguous()
-    return torch.matmul(a, b)
-
-
 def _residual_norm(x, a, w, norm_w, eps):
     """x += a @ w^T in place, then RMSNorm(x) * norm_w (add_rmsnorm after a linear, viktor/triton_ops.py:34-40).
     Packed batches of >= 4096 rows add the residual in the product's epilogue, which hands the row sums of
@@ -50,31 +47,9 @@ def _residual_norm(x, a, w, norm_w, eps):
     return ops.add_rmsnorm(x, norm_w, eps, delta=ops.linear(a, w))
 
 
-_WGRAD_SPLIT = 16
-
-
-def _wgrad(a, b):
-    """Weight gradient a^T @ b [Ka, Kb] over the packed rows of a [n, Ka] and b [n, Kb] (bf16, contiguous),
-    rounded to bf16 once as the reference's autocast matmul output. The reduction over ~10^5 rows with a
-    small output has too few output tiles for one product, so the rows are split into 16 slices computed as
-    one batched product with fp32 outputs, and the slices are summed in fp32 in slice order (deterministic).
-    The right operand of every batched product is contiguous."""
-    assert a.is_contiguous() and b.is_contiguous() and a.shape[0] == b.shape[0]
-    n = a.shape[0]
-    c = n // _WGRAD_SPLIT
-    if c < 1024:
-        return torch.matmul(a.t(), b)
-    m = c * _WGRAD_SPLIT
-    acc = torch.bmm(a[:m].view(_WGRAD_SPLIT, c, -1).transpose(1, 2), b[:m].view(_WGRAD_SPLIT, c, -1),
-                    out_dtype=torch.float32).sum(0)
-    if m < n:
-        acc += torch.bmm(a[m:].t().unsqueeze(0), b[m:].unsqueeze(0), out_dtype=torch.float32)[0]
-    return acc.to(BF16)
-
-
 class _TokenEmbed(torch.autograd.Function):
-    """emb_bf16[tokens] with the table's gradient as onehot(tokens)^T @ d_rows: with V = 7 (or 343) rows a
-    small deterministic GEMM instead of a sorted scatter-add (the gather of viktor/model.py:78)."""
+    """emb_bf16[tokens] (the gather of viktor/model.py:77) with the table's gradient as the fp32 sum of the
+    gradient rows of each token id (vk_embed_grad: deterministic, no atomics)."""
 
     @staticmethod
     def forward(ctx, weight, tokens):
@@ -85,9 +60,67 @@ class _TokenEmbed(torch.autograd.Function):
     @staticmethod
     def backward(ctx, d_rows):
         (tokens,) = ctx.saved_tensors
-        d = d_rows.reshape(-1, d_rows.shape[-1]).to(BF16)
-        onehot = torch.nn.functional.one_hot(tokens.reshape(-1), ctx.vocab).to(BF16)
-        return torch.matmul(onehot.t(), d).float(), None
+        d = d_rows.reshape(-1, d_rows.shape[-1]).to(BF16).contiguous()
+        return ops.embed_grad(d, tokens.reshape(-1).contiguous(), ctx.vocab), None
+
+
+def _pad_cols(t, width):
+    """t [n, c] bf16 -> [n, width] with zero columns past c."""
+    out = torch.zeros(t.shape[0], width, dtype=BF16, device=t.device)
+    out[:, :t.shape[1]] = t
+    return out
+
+
+class _Projector(torch.autograd.Function):
+    """Per-frame projector nn.Linear(d_enc, d) -> nn.GELU() -> nn.Linear(d, d) under torch.autocast bf16
+    (viktor/model.py:35, 74): x [n, d_enc] bf16 -> [n, d] bf16. Each linear is an MFMA product with fp32 output
+    whose epilogue adds the bf16-cast bias and rounds once (vk_bias_act, GELU fused after the first). Backward:
+    bias gradients as fixed-order column sums, weight gradients by vk_wgrad, the GELU backward fused with the
+    first bias's column sums (vk_act_backward); no input gradient (the frames are data)."""
+
+    @staticmethod
+    def forward(ctx, x, w1, b1, w2, b2):
+        w1b, w2b = w1.detach().to(BF16).contiguous(), w2.detach().to(BF16).contiguous()
+        b1b, b2b = (b.detach().to(BF16).float().contiguous() for b in (b1, b2))
+        pre, a = ops.bias_act(ops.linear(x, w1b, out_dtype=torch.float32), b1b, gelu=True)
+        y = ops.bias_act(ops.linear(a, w2b, out_dtype=torch.float32), b2b, gelu=False)
+        ctx.save_for_backward(x, pre, a, w2b)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, pre, a, w2b = ctx.saved_tensors
+        dy = dy.to(BF16).contiguous()
+        gb2 = ops.act_backward(dy)
+        gw2 = ops.wgrad(dy, a)
+        da = ops.linear(dy, w2b.t().contiguous())
+        dz, gb1 = ops.act_backward(da, pre)
+        gw1 = ops.wgrad(dz, x)
+        # autocast rounds the bias gradients to bf16 like the weight gradients
+        return None, gw1.float(), gb1.to(BF16).float(), gw2.float(), gb2.to(BF16).float()
+
+
+class _LMHead(torch.autograd.Function):
+    """logits = h lm_head^T in bf16 (viktor/decoder.py:130, 163-164 under autocast): h [n, d] bf16, weight
+    [V, d] fp32 master. The V-wide gradient operand is zero-padded to a multiple of 128 columns so that both
+    backward products run on the MFMA kernels: dh = dz W (vk_linear against W^T padded) and dW = dz^T h
+    (vk_wgrad, computed as (h^T dz)^T)."""
+
+    @staticmethod
+    def forward(ctx, h, weight):
+        wb = weight.detach().to(BF16).contiguous()
+        ctx.save_for_backward(h, wb)
+        return ops.linear(h, wb)
+
+    @staticmethod
+    def backward(ctx, dz):
+        h, wb = ctx.saved_tensors
+        V = wb.shape[0]
+        width = -(-V // 128) * 128
+        zp = _pad_cols(dz.to(BF16), width)
+        dh = ops.linear(zp, _pad_cols(wb.t(), width))
+        gw = ops.wgrad(h, zp)[:, :V].t().float()
+        return dh, gw
 
 
 class _DecoderStack(torch.autograd.Function):
@@ -141,20 +174,20 @@ class _DecoderStack(torch.autograd.Function):
             wa, wqkv, wqn, wkn, wo, wm, wgu, wd = w[8 * i:8 * i + 8]
             # x_{i+1} = x_mid + g Wd^T
             dm = dx.to(BF16)
-            gd = _wgrad(dm, g)
-            dg = _mm(dm, wd)
+            gd = ops.wgrad(dm, g)
+            dg = ops.linear(dm, wd.t().contiguous())
             dgu = ops.swiglu_backward(gu, dg)
-            ggu = _wgrad(dgu, h2)
-            dh2 = _mm(dgu, wgu)
+            ggu = ops.wgrad(dgu, h2)
+            dh2 = ops.linear(dgu, wgu.t().contiguous())
             dx, gm = ops.rmsnorm_backward(x_mid, wm, dh2, eps, dres=dx)  # d / d x_mid
             # x_mid = x_in + o Wo^T
             da = dx.to(BF16)
-            go = _wgrad(da, o.view(N, H * D))
-            do = _mm(da, wo).view(N, H, D).contiguous()
+            go = ops.wgrad(da, o.view(N, H * D))
+            do = ops.linear(da, wo.t().contiguous()).view(N, H, D)
             dq, dk, dv = ops.attention_backward(q, k, v, o, do, lse, plan.attn, plan.keys)
             dqkv, gqn, gkn = ops.qknorm_rope_backward(qkv, wqn, wkn, cos, sin, rpos, dq, dk, dv, eps, H, HKV, D)
-            gqkv = _wgrad(dqkv, h)
-            dhh = _mm(dqkv, wqkv)
+            gqkv = ops.wgrad(dqkv, h)
+            dhh = ops.linear(dqkv, wqkv.t().contiguous())
             dx, ga = ops.rmsnorm_backward(x_in, wa, dhh, eps, dres=dx)  # d / d x_in
             grads[8 * i:8 * i + 8] = [ga, gqkv, gqn, gkn, go, gm, ggu, gd]
         ctx.saved_acts = None
@@ -184,8 +217,9 @@ def train_logits(model, frames, tokens_in, plens=None):
     dev = frames.device
     plens_h = [P] * B if plens is None else [int(p) for p in plens.tolist()]
     assert all(0 < p <= P for p in plens_h), "plens outside 1..P"
-    with torch.autocast("cuda", dtype=BF16):
-        prefix = model.projector(frames.to(model.projector[0].weight.dtype)).to(BF16)  # [B, P, d]
+    proj = model.projector
+    prefix = _Projector.apply(frames.reshape(B * P, -1).to(BF16).contiguous(), proj[0].weight, proj[0].bias,
+                              proj[2].weight, proj[2].bias).view(B, P, -1)             # [B, P, d] bf16
     emb = _TokenEmbed.apply(dec.embed.weight, tokens_in.to(dev))                       # [B, T, d] bf16
     x = torch.cat([torch.cat([prefix[b, :plens_h[b]], emb[b]]) for b in range(B)]).contiguous()
     seq_lens = [p + T for p in plens_h]
@@ -200,8 +234,7 @@ def train_logits(model, frames, tokens_in, plens=None):
     cos, sin = dec.cos.contiguous(), dec.sin.contiguous()
     meta = {"cfg": cfg, "plan": plan, "rpos": rpos, "cos": cos, "sin": sin, "tok_rows": tok_rows}
     h = _DecoderStack.apply(x, meta, *decoder_params(dec))
-    logits = torch.matmul(h, dec.lm_head.weight.to(BF16).t())
-    return logits.view(B, T, -1)
+    return _LMHead.apply(h, dec.lm_head.weight).view(B, T, -1)
 
 
 class HipAdamW:
