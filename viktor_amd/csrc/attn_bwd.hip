@@ -14,12 +14,12 @@
 //   * dQ kernel = the forward's shape: a workgroup per 64-query block x KV head, 8 wavefronts (4 query
 //     heads x 2 halves of 32 rows), K / V tiles of 64 keys double buffered in LDS. Per key half:
 //     S^T = K Q^T, dP^T = V dO^T (A = key rows from LDS, B = Q^T / dO^T held in registers), dS^T in the
-//     accumulator layout, dQ^T += K^T dS^T (A = K^T from a transposed LDS copy of the tile).
+//     accumulator layout, dQ^T += K^T dS^T (A = K^T by LDS transpose reads of the row-major K tile).
 //   * dK/dV kernel: a workgroup per 128-key block x KV head, 4 wavefronts of 32 keys (two 16-key blocks;
 //     K^T / V^T fragments in registers), looping over the 32-query tiles at or below the diagonal, Q / dO /
-//     lse / D of the 4 query heads staged in LDS (the next tile's loads in flight during the current one),
-//     with transposed copies of Q and dO: S = Q K^T, dP = dO V^T (A = query rows), then dV^T += dO^T P and
-//     dK^T += Q^T dS (A = the transposed copies) with P / dS consumed in their accumulator layout; the 4
+//     lse / D of the 4 query heads staged in LDS (the next tile's loads in flight during the current one):
+//     S = Q K^T, dP = dO V^T (A = query rows), then dV^T += dO^T P and dK^T += Q^T dS (A = dO^T / Q^T by
+//     LDS transpose reads of the row-major tiles) with P / dS consumed in their accumulator layout; the 4
 //     heads accumulate in place. Each operand fragment read from LDS feeds both key blocks of the wave, so
 //     the LDS reads per MFMA are half those of 16-key waves (the kernel was bound by them). 128 keys per
 //     staged tile halve the re-reads of Q / dO against 64.
@@ -33,9 +33,25 @@ namespace vk {
 
 constexpr int AB_H = 8, AB_HKV = 2, AB_D = 64;
 constexpr int AB_PITCH = 72;  // 64 + 8 bf16 per LDS row
-constexpr int AB_KTP = 68;    // keys per row of a transposed K tile (136 B: 8-byte operand reads conflict-free)
 constexpr int AB_KW = 4;      // wavefronts of a dK/dV workgroup (32 keys each: 128 keys per staged query tile)
 constexpr int AB_KB = 32 * AB_KW;
+
+typedef short ab_s4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) ab_s4 ab_lds_s4;
+
+// The MFMA operand "column 16 dt + lane % 16 of a row-major LDS tile (AB_PITCH elements per row) at rows
+// r0 + 4 g .. + 3 and r0 + 16 + 4 g .. + 3" (g = lane / 16) as one bf16x8, from two gfx950 transpose reads
+// ds_read_b64_tr_b16: in each 16-lane group, source lane s reads 4 consecutive columns 4 (s % 4) .. of row
+// R0 + s / 4, and output lane j receives column j at rows R0 .. R0 + 3.
+__device__ __forceinline__ bf16x8 ab_tr_frag(const bf16_t *tile, int r0, int dt, int lane) {
+  const int g = lane >> 4, s = lane & 15;
+  const bf16_t *p0 = tile + (r0 + 4 * g + (s >> 2)) * AB_PITCH + 16 * dt + 4 * (s & 3);
+  const ab_s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((ab_lds_s4 *)(const __attribute__((address_space(3))) bf16_t *)p0);
+  const ab_s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (ab_lds_s4 *)(const __attribute__((address_space(3))) bf16_t *)(p0 + 16 * AB_PITCH));
+  typedef short s8 __attribute__((ext_vector_type(8)));
+  return __builtin_bit_cast(bf16x8, s8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+}
 
 // D[r, h] = sum_d dO[r, h, d] * o[r, h, d]: one thread per (row, head)
 __global__ __launch_bounds__(256) void attn_bwd_dot_kernel(const bf16_t *__restrict__ dout,
@@ -65,11 +81,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
     const bf16_t *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ dd,
     const int32_t *__restrict__ cu, const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok,
     float *__restrict__ dq, float scale_log2, float scale) {
-  // K and V rows (the A operands of S^T and dP^T) and a transposed copy of K, [d][key] at AB_KTP keys per row
-  // (the A operand of dQ^T = K^T dS^T: a lane's 8 keys are two 8-byte reads instead of eight 2-byte ones)
+  // K and V rows: the A operands of S^T and dP^T, and (through transpose reads of K) of dQ^T = K^T dS^T
   __shared__ __attribute__((aligned(16))) bf16_t Ks[2][64 * AB_PITCH];
   __shared__ __attribute__((aligned(16))) bf16_t Vs[2][64 * AB_PITCH];
-  __shared__ __attribute__((aligned(16))) bf16_t Kt[2][AB_D * AB_KTP];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int col = lane & 15, g = lane >> 4;
   const int hk = blockIdx.y, hq = hk * 4 + (wid & 3), half = wid >> 2;
@@ -120,11 +134,6 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
   auto store_tile = [&](int buf) {
     *reinterpret_cast<u32x4 *>(&Ks[buf][lrow * AB_PITCH + lchunk * 8]) = rk;
     *reinterpret_cast<u32x4 *>(&Vs[buf][lrow * AB_PITCH + lchunk * 8]) = rv;
-#pragma unroll
-    for (int wv = 0; wv < 4; ++wv) {
-      Kt[buf][(lchunk * 8 + 2 * wv) * AB_KTP + lrow] = static_cast<bf16_t>(rk[wv] & 0xffffu);
-      Kt[buf][(lchunk * 8 + 2 * wv + 1) * AB_KTP + lrow] = static_cast<bf16_t>(rk[wv] >> 16);
-    }
   };
   load_tile(0);
   store_tile(0);
@@ -158,33 +167,38 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
           }
         }
       }
-      // dS^T in the accumulator layout (key 16 kb + 4 g + i, query col), as the B operand of K^T dS^T
-      // branch-free: a masked score's exponent is -inf (exp2 -> 0); exponents are <= 0 (the row's
-      // log-sum-exp bounds every score), so the bare v_exp_f32 serves
+      // dS^T in the accumulator layout (key 16 kb + 4 g + i, query col), as the B operand of K^T dS^T;
+      // exponents are <= 0 (the row's log-sum-exp bounds every score), so the bare v_exp_f32 serves. Only a
+      // half that reaches a row's diagonal is masked (a wave-uniform branch; a masked score's exponent is -inf)
+      const bool need_mask = kbase + 31 > r_first;
       bf16x8 dsf[2];
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         const int hi_k = min(qpos[qb], len - 1);
+        float x[8];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[kb * 4 + i] = fmaf(st[kb][qb][i], scale_log2, -lse2[qb]);
+        if (need_mask) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[kb * 4 + i] = kbase + 16 * kb + 4 * g + i <= hi_k ? x[kb * 4 + i] : -INFINITY;
+        }
         float d[8];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = kbase + 16 * kb + 4 * g + i;
-            const float x = key <= hi_k ? st[kb][qb][i] * scale_log2 - lse2[qb] : -INFINITY;
-            d[kb * 4 + i] = __builtin_amdgcn_exp2f(x) * (dpt[kb][qb][i] - dr[qb]);
-          }
+          for (int i = 0; i < 4; ++i)
+            d[kb * 4 + i] = __builtin_amdgcn_exp2f(x[kb * 4 + i]) * (dpt[kb][qb][i] - dr[qb]);
         dsf[qb] = __builtin_bit_cast(bf16x8, u32x4{pack_bf(d[0], d[1]), pack_bf(d[2], d[3]), pack_bf(d[4], d[5]),
                                                     pack_bf(d[6], d[7])});
       }
-      // dQ^T += K^T dS^T (key order {4g..4g+3, 16+4g..16+4g+3} in both operands)
-      const bf16_t *ktt = &Kt[buf][32 * ks];
+      // dQ^T += K^T dS^T (key order {4g..4g+3, 16+4g..16+4g+3} in both operands; K^T by transpose reads)
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const bf16_t *kr = ktt + (16 * dt + col) * AB_KTP;
-        const u32x2 lo = *reinterpret_cast<const u32x2 *>(kr + 4 * g);
-        const u32x2 hi = *reinterpret_cast<const u32x2 *>(kr + 16 + 4 * g);
-        const bf16x8 ka = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        const bf16x8 ka = ab_tr_frag(kt, 0, dt, lane);
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) acc[dt][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, dsf[qb], acc[dt][qb], 0, 0, 0);
       }
@@ -208,15 +222,9 @@ __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
     const bf16_t *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ dd,
     const int32_t *__restrict__ cu, const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok,
     float *__restrict__ dk, float *__restrict__ dv, float scale_log2, float scale) {
-  // row-major Q / dO tiles (the A operands of S and dP) and transposed copies [head][d][row] (the A operands of
-  // dK^T and dV^T: a lane's 8 rows of one d are four 32-bit reads instead of eight 16-bit ones)
-  // 32 rows + 6 pad: the staging stores (lanes: 8 d chunks x 8 rows) then fall on 64 distinct banks
-  // (row stride 76 bytes = 19 banks); the rows are 4-byte aligned, read as 32-bit words
-  constexpr int TP = 38;
+  // row-major Q / dO tiles [head][row]: the A operands of S and dP, and (through transpose reads) of dK^T and dV^T
   __shared__ __attribute__((aligned(16))) bf16_t Qs[4 * 32 * AB_PITCH];
   __shared__ __attribute__((aligned(16))) bf16_t Os[4 * 32 * AB_PITCH];  // dO
-  __shared__ __attribute__((aligned(16))) bf16_t QTs[4 * 64 * TP];
-  __shared__ __attribute__((aligned(16))) bf16_t OTs[4 * 64 * TP];
   __shared__ float Ls[4 * 32], Ds[4 * 32];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int col = lane & 15, g = lane >> 4;
@@ -281,14 +289,6 @@ __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
       const int hh = chunk >> 8, rr = (chunk >> 3) & 31, dc8 = chunk & 7;
       *reinterpret_cast<u32x4 *>(&Qs[(hh * 32 + rr) * AB_PITCH + 8 * dc8]) = qv[c];
       *reinterpret_cast<u32x4 *>(&Os[(hh * 32 + rr) * AB_PITCH + 8 * dc8]) = ov[c];
-      // (16-bit halves by integer shifts: element extraction from a __bf16 vector with a bit_cast to
-      // uint16_t was lowered to the same register for every element by this compiler)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t qw = qv[c][e >> 1], ow = ov[c][e >> 1];
-        QTs[(hh * 64 + 8 * dc8 + e) * TP + rr] = static_cast<bf16_t>((e & 1) ? (qw >> 16) : (qw & 0xffffu));
-        OTs[(hh * 64 + 8 * dc8 + e) * TP + rr] = static_cast<bf16_t>((e & 1) ? (ow >> 16) : (ow & 0xffffu));
-      }
     }
     if (tid < 128)
       Ls[tid] = lv;
@@ -319,40 +319,49 @@ __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
           }
         }
       }
-      // row order {4g..4g+3, 16+4g..16+4g+3}; branch-free: a masked entry's exponent is -inf (exp2 -> 0),
-      // exponents are <= 0 (bare v_exp_f32)
+      // row order {4g..4g+3, 16+4g..16+4g+3}; exponents are <= 0 (bare v_exp_f32). A tile wholly below the
+      // diagonal and inside the sequence needs no mask (a wave-uniform branch); else a masked entry's exponent
+      // is -inf (exp2 -> 0)
+      const bool full = wave_kmin + 31 <= rs && rs + 31 < len;
       bf16x8 pf[2], dsf[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const int key = keyb[kb];
+        float x[8];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[rb * 4 + i] = fmaf(st[kb][rb][i], scale_log2, -Ls[hh * 32 + 16 * rb + 4 * g + i]);
+        if (!full) {
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int r = rs + 16 * rb + 4 * g + i;
+              const bool ok = (r < len) & (key <= r) & (key < len);
+              x[rb * 4 + i] = ok ? x[rb * 4 + i] : -INFINITY;
+            }
+        }
         float pv[8], dv8[8];
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int rr = 16 * rb + 4 * g + i;
-            const int r = rs + rr;
-            const bool ok = (r < len) & (key <= r) & (key < len);
-            const float x = ok ? st[kb][rb][i] * scale_log2 - Ls[hh * 32 + rr] : -INFINITY;
-            const float p = __builtin_amdgcn_exp2f(x);
+            const float p = __builtin_amdgcn_exp2f(x[rb * 4 + i]);
             pv[rb * 4 + i] = p;
-            dv8[rb * 4 + i] = p * (dpt[kb][rb][i] - Ds[hh * 32 + rr]);
+            dv8[rb * 4 + i] = p * (dpt[kb][rb][i] - Ds[hh * 32 + 16 * rb + 4 * g + i]);
           }
         pf[kb] = __builtin_bit_cast(bf16x8, u32x4{pack_bf(pv[0], pv[1]), pack_bf(pv[2], pv[3]), pack_bf(pv[4], pv[5]),
                                                    pack_bf(pv[6], pv[7])});
         dsf[kb] = __builtin_bit_cast(bf16x8, u32x4{pack_bf(dv8[0], dv8[1]), pack_bf(dv8[2], dv8[3]),
                                                     pack_bf(dv8[4], dv8[5]), pack_bf(dv8[6], dv8[7])});
       }
-      // dV^T += dO^T P, dK^T += Q^T dS (A = dO^T / Q^T from the transposed copies: lane col -> d, rows
-      // {4g..4g+3} and {16+4g..16+4g+3} as four 32-bit reads, the row order of P / dS above; each fragment
-      // serves both key blocks)
+      // dV^T += dO^T P, dK^T += Q^T dS (A = dO^T / Q^T by transpose reads of the row-major tiles: lane col -> d,
+      // rows {4g..4g+3} and {16+4g..16+4g+3}, the row order of P / dS above; each fragment serves both key blocks)
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const bf16_t *qtr = &QTs[(hh * 64 + 16 * dt + col) * TP];
-        const bf16_t *otr = &OTs[(hh * 64 + 16 * dt + col) * TP];
-        const uint32_t *qw = reinterpret_cast<const uint32_t *>(qtr), *ow = reinterpret_cast<const uint32_t *>(otr);
-        const bf16x8 qa = __builtin_bit_cast(bf16x8, u32x4{qw[2 * g], qw[2 * g + 1], qw[8 + 2 * g], qw[9 + 2 * g]});
-        const bf16x8 oa = __builtin_bit_cast(bf16x8, u32x4{ow[2 * g], ow[2 * g + 1], ow[8 + 2 * g], ow[9 + 2 * g]});
+        const bf16x8 qa = ab_tr_frag(qt, 0, dt, lane);
+        const bf16x8 oa = ab_tr_frag(ot, 0, dt, lane);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
           accv[kb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(oa, pf[kb], accv[kb][dt], 0, 0, 0);

@@ -10,8 +10,8 @@
 //     32-key halves; halves that lie entirely above the causal diagonal of the wave's rows are skipped.
 //   * Transposed products as in the decode kernel: S^T = K Q^T (A = key rows from LDS, B = Q^T held in
 //     registers for the whole loop) leaves each lane the scores of one query row; O^T = V^T P^T consumes
-//     those probabilities in place and the online-softmax rescale stays lane-local. V is staged transposed
-//     (V^T rows of 68 keys), so the V^T operand is two 8-byte LDS reads per lane.
+//     those probabilities in place and the online-softmax rescale stays lane-local. V is staged row-major like
+//     K and the V^T operand is two LDS transpose reads (ds_read_b64_tr_b16) per lane.
 //   * Per-wave state is 32 query rows (Q^T 16, O^T 32, scores 16 VGPRs) so the kernel fits 4 waves per
 //     SIMD: two workgroups per CU.
 //   * Keys of sequence i live at base + k_off[i] + j * stride_tok (+ kv head * 64): the same kernel
@@ -29,7 +29,31 @@ constexpr int PA_Q = 64;      // query rows per workgroup (plan granularity)
 constexpr int PA_WAVES = 8;   // 4 query heads x 2 halves of 32 rows
 constexpr int PA_KT = 64;     // keys per LDS tile
 constexpr int PA_PITCH = 72;  // 64 + 8 bf16
-constexpr int PA_VTP = 68;    // keys per row of the transposed V tile (136 B: 8-byte operand reads conflict-free)
+typedef short pa_s4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) pa_s4 pa_lds_s4;
+constexpr float PA_SLACK = 8.0f;  // log2 units a row's score may pass its reference max before it moves
+
+// max of three floats as one v_max3_f32. Written as asm: the compiler's fmaxf quiets signalling NaNs with an
+// extra max per operand; the scores are MFMA outputs or -inf, never NaN.
+__device__ __forceinline__ float pa_max3(float a, float b, float c) {
+  float d;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+__device__ __forceinline__ float pa_max2(float a, float b) {
+  float d;
+  asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+// max over lanes l, l ^ 16, l ^ 32, l ^ 48 with gfx950's lane swaps (VALU, no LDS round trip):
+// v_permlane32_swap(x, x) returns {x of lanes l % 32, x of lanes l % 32 + 32} and v_permlane16_swap(x, x)
+// {x of the even 16-lane row of l's pair, x of the odd one}
+__device__ __forceinline__ float pa_max_lanes(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float m = pa_max2(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  return pa_max2(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
 
 __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ k, const bf16_t *__restrict__ v,
@@ -37,7 +61,7 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
     const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok, bf16_t *__restrict__ out, int causal,
     float scale_log2, float *__restrict__ lse) {
   __shared__ __attribute__((aligned(16))) bf16_t Ks[2][PA_KT * PA_PITCH];
-  __shared__ __attribute__((aligned(16))) bf16_t Vt[2][PA_D * PA_VTP];  // V^T: [d][key]
+  __shared__ __attribute__((aligned(16))) bf16_t Vs[2][PA_KT * PA_PITCH];  // V rows, as K
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wid = tid >> 6;
@@ -80,7 +104,8 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int c = 0; c < 2; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};  // raw-score reference max, row sum
+  const float slack_raw = PA_SLACK / scale_log2;
 
   // cooperative tile load: 512 threads -> (key row 0..63, 16-byte chunk 0..7) of K and of V
   const int lrow = tid >> 3, lchunk = tid & 7;
@@ -94,12 +119,7 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
   };
   auto store_tile = [&](int buf) {
     *reinterpret_cast<u32x4 *>(&Ks[buf][lrow * PA_PITCH + lchunk * 8]) = rk;
-    // V transposed, so the O^T = V^T P^T operand is two 8-byte reads per lane
-#pragma unroll
-    for (int wv = 0; wv < 4; ++wv) {
-      Vt[buf][(lchunk * 8 + 2 * wv) * PA_VTP + lrow] = static_cast<bf16_t>(rv[wv] & 0xffffu);
-      Vt[buf][(lchunk * 8 + 2 * wv + 1) * PA_VTP + lrow] = static_cast<bf16_t>(rv[wv] >> 16);
-    }
+    *reinterpret_cast<u32x4 *>(&Vs[buf][lrow * PA_PITCH + lchunk * 8]) = rv;
   };
 
   load_tile(0);
@@ -113,7 +133,7 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
       const int kbase = t * PA_KT + 32 * ks;
       if (kbase > wave_kmax) continue;  // wave-uniform: every key of this half is masked for every row
       const bf16_t *kt = &Ks[buf][32 * ks * PA_PITCH];
-      const bf16_t *vt = &Vt[buf][32 * ks];
+      const bf16_t *vt = &Vs[buf][32 * ks * PA_PITCH];
       // S^T[key][query] for two 16-key blocks x two 16-query blocks
       f32x4 st[2][2];
 #pragma unroll
@@ -131,8 +151,9 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
         }
       }
       const bool need_mask = kbase + 31 >= klen || (causal && kbase + 31 > qshift + r_first);
-      // branch-free softmax step: the mask is a compare per score under one wave-uniform branch (a
-      // short-circuit test per score compiles to a divergent branch per score)
+      // softmax step on the raw scores (the scale enters through the exponent's fma, and max commutes with a
+      // positive scale); the mask is a compare per score under one wave-uniform branch (a short-circuit test
+      // per score compiles to a divergent branch per score)
       bf16x8 pf[2];
       float alpha_q[2];
       bool grew = false;
@@ -142,7 +163,7 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) sv[kb * 4 + i] = st[kb][qb][i] * scale_log2;
+          for (int i = 0; i < 4; ++i) sv[kb * 4 + i] = st[kb][qb][i];
         if (need_mask) {
           const int hi_k = causal ? min(qpos[qb], klen - 1) : klen - 1;  // last key this row sees
 #pragma unroll
@@ -151,27 +172,29 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
             for (int i = 0; i < 4; ++i)
               sv[kb * 4 + i] = kbase + 16 * kb + 4 * g + i <= hi_k ? sv[kb * 4 + i] : -INFINITY;
         }
-        float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        // m_new is finite: tile 0 always holds key 0, visible to every query; exponents are <= 0, so the
-        // bare v_exp_f32 (no range reduction) serves
-        const float m_new = fmaxf(m_run[qb], mx);
+        float mx = pa_max3(pa_max3(sv[0], sv[1], sv[2]), pa_max3(sv[3], sv[4], sv[5]), pa_max3(sv[6], sv[7], sv[7]));
+        mx = pa_max_lanes(mx);
+        // The row's reference max moves only when a score passes it by more than PA_SLACK in log2 units of the
+        // scaled scores: the probabilities are then exp2(s c - m c) <= 2^PA_SLACK (bf16 and the fp32 sums carry
+        // them with the same relative precision as values <= 1), and the rescale of the row's sum and output
+        // (a multiply per accumulator) is rare after the first tiles. m_run = -inf before the first key: any
+        // finite score moves it. Tile 0 holds key 0, visible to every query, so m_run is finite after it.
+        const bool moved = mx > m_run[qb] + slack_raw;
+        const float m_ref = moved ? mx : m_run[qb];
+        const float nmc = -m_ref * scale_log2;
         float e[8], ps = 0.f;
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
-          e[jj] = __builtin_amdgcn_exp2f(sv[jj] - m_new);
+          e[jj] = __builtin_amdgcn_exp2f(fmaf(sv[jj], scale_log2, nmc));
           ps += e[jj];
         }
         pf[qb] = __builtin_bit_cast(bf16x8, u32x4{pack_bf(e[0], e[1]), pack_bf(e[2], e[3]), pack_bf(e[4], e[5]),
                                                    pack_bf(e[6], e[7])});
-        // the running max moved: rescale the row's sum (and, below, its output); else alpha is exactly 1
-        const bool moved = m_new != m_run[qb];
-        const float alpha = moved ? __builtin_amdgcn_exp2f(m_run[qb] - m_new) : 1.0f;
+        const float alpha = moved ? __builtin_amdgcn_exp2f((m_run[qb] - m_ref) * scale_log2) : 1.0f;
         alpha_q[qb] = alpha;
         grew |= moved;
         l_run[qb] = l_run[qb] * alpha + ps;
-        m_run[qb] = m_new;
+        m_run[qb] = m_ref;
       }
       if (__builtin_amdgcn_ballot_w64(grew) != 0) {
 #pragma unroll
@@ -179,13 +202,19 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
 #pragma unroll
           for (int dt = 0; dt < 4; ++dt) acc[dt][qb] *= alpha_q[qb];
       }
-      // O^T += V^T P^T (key order {4g..4g+3, 16+4g..16+4g+3} in both operands)
+      // O^T += V^T P^T (key order {4g..4g+3, 16+4g..16+4g+3} in both operands). The V^T operand comes from
+      // the row-major V tile through gfx950's transpose read ds_read_b64_tr_b16: in each 16-lane group, source
+      // lane s reads 4 consecutive d of key row R0 + s / 4 and output lane j receives d = 16 dt + j at keys
+      // R0 .. R0 + 3; two reads (R0 = 4 g and 16 + 4 g) give the lane's 8 keys.
+      const int tr_row = 4 * g + (col >> 2), tr_d = 4 * (col & 3);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const bf16_t *vr = vt + (16 * dt + col) * PA_VTP;
-        const u32x2 lo = *reinterpret_cast<const u32x2 *>(vr + 4 * g);
-        const u32x2 hi = *reinterpret_cast<const u32x2 *>(vr + 16 + 4 * g);
-        const bf16x8 va = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        const pa_s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (pa_lds_s4 *)(const __attribute__((address_space(3))) bf16_t *)(vt + tr_row * PA_PITCH + 16 * dt + tr_d));
+        const pa_s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((pa_lds_s4 *)(
+            const __attribute__((address_space(3))) bf16_t *)(vt + (16 + tr_row) * PA_PITCH + 16 * dt + tr_d));
+        typedef short s8 __attribute__((ext_vector_type(8)));
+        const bf16x8 va = __builtin_bit_cast(bf16x8, s8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) acc[dt][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[qb], acc[dt][qb], 0, 0, 0);
       }
@@ -202,8 +231,8 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
     const int r = r_first + 16 * qb + col;
     if (r >= q_len || r >= qs + nq) continue;
     const float inv = 1.0f / l;
-    // the row's log-sum-exp in log2 units of the scaled scores (m + log2 l), for the backward pass
-    if (lse != nullptr && g == 0) lse[(q0 + r) * PA_H + hq] = m_run[qb] + log2f(l);
+    // the row's log-sum-exp in log2 units of the scaled scores (m c + log2 l), for the backward pass
+    if (lse != nullptr && g == 0) lse[(q0 + r) * PA_H + hq] = m_run[qb] * scale_log2 + log2f(l);
     bf16_t *dst = out + ((q0 + r) * PA_H + hq) * PA_D + 4 * g;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {

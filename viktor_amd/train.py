@@ -21,6 +21,7 @@ The residual stream is bf16, the rounding points of the inference path.
 
 from typing import List, Optional, Sequence
 
+import numpy as np
 import torch
 
 from . import hip_ops as ops
@@ -123,6 +124,34 @@ class _LMHead(torch.autograd.Function):
         return dh, gw
 
 
+class _PackRows(torch.autograd.Function):
+    """The packed decoder input x [N, d] bf16: the real prefix rows of each window followed by its token rows
+    (the sequence viktor/model.py:72-86 builds per window, without its padding). prefix [B P, d] and emb
+    [B T, d]: the projector's and the embedding's rows; pre_src / pre_dst: the real prefix rows and their packed
+    rows; tok_rows: the packed rows of the tokens, in emb's order. Each source row is used once, so the backward
+    is two row gathers (no accumulation); all_prefix: every prefix row is real (pre_src is 0 .. B P - 1)."""
+
+    @staticmethod
+    def forward(ctx, prefix, emb, pre_src, pre_dst, tok_rows, all_prefix):
+        x = torch.empty(pre_dst.numel() + tok_rows.numel(), prefix.shape[1], dtype=BF16, device=prefix.device)
+        x.index_copy_(0, pre_dst, prefix if all_prefix else prefix.index_select(0, pre_src))
+        x.index_copy_(0, tok_rows, emb)
+        ctx.save_for_backward(pre_src, pre_dst, tok_rows)
+        ctx.n_prefix, ctx.all_prefix = prefix.shape[0], all_prefix
+        return x
+
+    @staticmethod
+    def backward(ctx, dx):
+        pre_src, pre_dst, tok_rows = ctx.saved_tensors
+        g = dx.index_select(0, pre_dst)
+        if ctx.all_prefix:
+            dp = g
+        else:
+            dp = dx.new_zeros(ctx.n_prefix, dx.shape[1])
+            dp.index_copy_(0, pre_src, g)
+        return dp, dx.index_select(0, tok_rows), None, None, None, None
+
+
 class _DecoderStack(torch.autograd.Function):
     """x [N, d] bf16 packed rows -> final-normed hidden of the token rows [n_tok, d] bf16."""
 
@@ -219,17 +248,23 @@ def train_logits(model, frames, tokens_in, plens=None):
     assert all(0 < p <= P for p in plens_h), "plens outside 1..P"
     proj = model.projector
     prefix = _Projector.apply(frames.reshape(B * P, -1).to(BF16).contiguous(), proj[0].weight, proj[0].bias,
-                              proj[2].weight, proj[2].bias).view(B, P, -1)             # [B, P, d] bf16
-    emb = _TokenEmbed.apply(dec.embed.weight, tokens_in.to(dev))                       # [B, T, d] bf16
-    x = torch.cat([torch.cat([prefix[b, :plens_h[b]], emb[b]]) for b in range(B)]).contiguous()
+                              proj[2].weight, proj[2].bias)                            # [B P, d] bf16
+    emb = _TokenEmbed.apply(dec.embed.weight, tokens_in.to(dev).reshape(-1))          # [B T, d] bf16
+    # packed layout, window b: its plens[b] real prefix rows, then its T token rows; row indices on the host
     seq_lens = [p + T for p in plens_h]
     s = model.pos_scale
-    rpos = torch.cat([torch.cat([torch.arange(p, device=dev) * s, s * p + torch.arange(T, device=dev)])
-                      for p in plens_h]).to(torch.int32)
-    off = [0]
-    for n in seq_lens:
-        off.append(off[-1] + n)
-    tok_rows = torch.cat([torch.arange(off[b] + plens_h[b], off[b + 1], device=dev) for b in range(B)])
+    pl = np.asarray(plens_h, dtype=np.int64)
+    off = np.concatenate([[0], np.cumsum(pl + T)])
+    pre_dst = np.concatenate([np.arange(off[b], off[b] + pl[b]) for b in range(B)])
+    pre_src = np.concatenate([b * P + np.arange(pl[b]) for b in range(B)])
+    tok_rows_h = np.concatenate([np.arange(off[b] + pl[b], off[b + 1]) for b in range(B)])
+    rpos_h = np.concatenate([np.concatenate([np.arange(p) * s, s * p + np.arange(T)]) for p in plens_h])
+    idx = torch.from_numpy(np.concatenate([pre_src, pre_dst, tok_rows_h, rpos_h])).to(dev)
+    n_pre, n_tok = len(pre_src), len(tok_rows_h)
+    pre_src_d, pre_dst_d = idx[:n_pre], idx[n_pre:2 * n_pre]
+    tok_rows = idx[2 * n_pre:2 * n_pre + n_tok]
+    rpos = idx[2 * n_pre + n_tok:].to(torch.int32)
+    x = _PackRows.apply(prefix, emb, pre_src_d, pre_dst_d, tok_rows, n_pre == B * P)
     plan = TrainPlan(seq_lens, dev)
     cos, sin = dec.cos.contiguous(), dec.sin.contiguous()
     meta = {"cfg": cfg, "plan": plan, "rpos": rpos, "cos": cos, "sin": sin, "tok_rows": tok_rows}
