@@ -106,20 +106,23 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const bf16_t *__restri
     dw_part[static_cast<int64_t>(blockIdx.x) * TR_D + c] = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
 }
 
-// sum over the rows of part [rows, cols], out[c] = sum (+ out[c] when accumulate). Workgroup = 64 columns x
-// 4 row slices (one wave each, rows s, s + 4, ...), then the 4 slices added in a fixed order.
+// sum over the rows of part [rows, cols], out[c] = sum (+ out[c] when accumulate). Workgroup = 16 columns x
+// 16 row slices (slice s: rows s, s + 16, ...), then the 16 slice sums added in a fixed order: a short
+// dependency chain per thread and cols / 16 workgroups.
 __global__ __launch_bounds__(256) void colsum_kernel(const float *__restrict__ part, float *__restrict__ out, int rows,
                                                     int cols, int accumulate) {
-  __shared__ float red[4][64];
-  const int lane = threadIdx.x & 63, sl = threadIdx.x >> 6;
-  const int c = blockIdx.x * 64 + lane;
+  __shared__ float red[16][16];
+  const int ci = threadIdx.x & 15, sl = threadIdx.x >> 4;
+  const int c = blockIdx.x * 16 + ci;
   float s = 0.f;
   if (c < cols)
-    for (int r = sl; r < rows; r += 4) s += part[static_cast<int64_t>(r) * cols + c];
-  red[sl][lane] = s;
+    for (int r = sl; r < rows; r += 16) s += part[static_cast<int64_t>(r) * cols + c];
+  red[sl][ci] = s;
   __syncthreads();
   if (sl == 0 && c < cols) {
-    const float t = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+    float t = red[0][ci];
+#pragma unroll
+    for (int k = 1; k < 16; ++k) t += red[k][ci];
     out[c] = accumulate ? out[c] + t : t;
   }
 }
@@ -291,7 +294,7 @@ extern "C" int vk_rmsnorm_backward(const void *x, const void *w, const void *dy,
 extern "C" int vk_colsum(const float *part, float *out, int32_t rows, int32_t cols, int32_t accumulate, void *stream) {
   VK_CHECK_ARG(part && out && rows >= 0 && cols >= 0, "colsum: bad arguments");
   if (cols == 0) return VK_OK;
-  colsum_kernel<<<static_cast<unsigned>((cols + 63) / 64), 256, 0, VK_STREAM(stream)>>>(part, out, rows, cols,
+  colsum_kernel<<<static_cast<unsigned>((cols + 15) / 16), 256, 0, VK_STREAM(stream)>>>(part, out, rows, cols,
                                                                                       accumulate);
   return launch_status("colsum");
 }

@@ -300,17 +300,24 @@ class HipAdamW:
         self.max_grad_norm = max_grad_norm
         self.step_count = 0
         self.last_norm = None
+        self.zero_grad()
 
     def zero_grad(self):
-        for p in self.params:
-            p.grad = None
-
-    def step(self):
-        """Gather the gradients (a missing one counts as zero), clip by the global norm, AdamW-update."""
+        """Zero the flat gradient buffer and make every parameter's .grad a view of its slice, so backward
+        accumulates into the buffer in place (no gather before the step)."""
         self.grad.zero_()
         for p, (o, k) in zip(self.params, self.slices):
-            if p.grad is not None:
-                self.grad[o:o + k].copy_(p.grad.reshape(-1))
+            p.grad = self.grad[o:o + k].view_as(p)
+
+    def step(self):
+        """Clip by the global norm and AdamW-update. A gradient that is not the bound view (set by the caller,
+        or left None) is copied in (None counts as zero)."""
+        for p, (o, k) in zip(self.params, self.slices):
+            view = self.grad[o:o + k]
+            if p.grad is None:
+                view.zero_()
+            elif p.grad.data_ptr() != view.data_ptr():
+                view.copy_(p.grad.reshape(-1))
         coef = None
         if self.max_grad_norm is not None:
             coef = ops.grad_norm_clip(self.grad, self.max_grad_norm)
