@@ -466,24 +466,28 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     for (int t = t0; t < t_end; t += GU_WAVES) {
       const int tn = t + GU_WAVES < t_end ? t + GU_WAVES : t;
       const TileRef nxt = locate(tn, cur.mc);
+      const int member = cur.seg - 1;  // -1: prefix tile, every column attends
+      // an own-row tile feeds only its member's 4 columns: the other column blocks are skipped (wave-uniform)
+      const int cb_only = member < 0 ? -1 : (4 * member) >> 4;
       f32x4 st[2][NCB];
 #pragma unroll
       for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb) {
           st[pb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (NCB > 1 && cb_only >= 0 && cb != cb_only) continue;
 #pragma unroll
           for (int c = 0; c < 2; ++c)
             st[pb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[pb][c]), bq[cb][c],
                                                                  st[pb][cb], 0, 0, 0);
         }
       load(kf, nxt.k, nxt);
-      const int member = cur.seg - 1;  // -1: prefix tile, every column attends
       // a prefix tile inside the prefix needs no mask (the common case: a uniform branch)
       const bool full = member < 0 && cur.row0 + GU_TILE <= cur.len;
       bf16x8 pf[NCB];
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
+        if (NCB > 1 && cb_only >= 0 && cb != cb_only) continue;
         float sv[8];
         if (full) {
 #pragma unroll
@@ -543,7 +547,8 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
         }
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb)
-          acc[cb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[cb], acc[cb][dt], 0, 0, 0);
+          if (NCB == 1 || cb_only < 0 || cb == cb_only)
+            acc[cb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[cb], acc[cb][dt], 0, 0, 0);
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       cur = nxt;
