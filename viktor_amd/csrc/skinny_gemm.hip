@@ -384,6 +384,55 @@ __device__ __forceinline__ void pg_issue_dword(char *dst, const int32_t *src) {
   __builtin_amdgcn_global_load_lds(src, (lds_void_t *)dst, 4, 0, 0);
 }
 
+// Wait until at most `ahead` stages of this wave's direct loads (LOADS instructions each) are outstanding.
+// s_waitcnt takes an immediate, so one branch per count (ahead is wave-uniform).
+template <int LOADS, int MAXA>
+__device__ __forceinline__ void pg_wait_ahead(int ahead) {
+  if constexpr (MAXA >= 1) {
+    if (ahead >= MAXA) {
+      __builtin_amdgcn_s_waitcnt(pg_vmcnt(MAXA * LOADS));
+      return;
+    }
+    pg_wait_ahead<LOADS, MAXA - 1>(ahead);
+  } else {
+    __builtin_amdgcn_s_waitcnt(pg_vmcnt(0));
+  }
+}
+
+// RMSNorm of a resident A tile in place (rows of K = 512 bf16, chunk c of row r in slot c ^ (r & 15)) from
+// the row sums of squares handed over by the producing residual product (ssx: [rows][8] fp32 in LDS) and the
+// norm weight (nwx: 512 bf16 in LDS): x = bf16(x * (1 / rms) * w), 1 / rms = rsqrt(sum / 512 + eps) with the
+// row's 8 partials summed in a fixed order. This wave takes rows r = wid + RSTEP i (i < NR), a whole 1 KB row
+// per step (lane l takes slot l, conflict-free). Lane l first computes 1 / rms of row l, and a row's value is
+// read from its lane; all rows' reads are issued before the first write, so the LDS round trips overlap
+// (a read after a write to the same tile would wait for it).
+template <int NR, int RSTEP>
+__device__ __forceinline__ void pg_normalise_rows(char *tile, const char *nwx, const char *ssx, int rows, int wid,
+                                                  int lane, float eps) {
+  const int lr = lane < rows ? lane : 0;
+  const f32x4 sa = *reinterpret_cast<const f32x4 *>(ssx + 32 * lr);
+  const f32x4 sb = *reinterpret_cast<const f32x4 *>(ssx + 32 * lr + 16);
+  const float ss = ((sa[0] + sa[1]) + (sa[2] + sa[3])) + ((sb[0] + sb[1]) + (sb[2] + sb[3]));
+  const float rn_lane = rsqrtf(ss * (1.0f / PG_NORM_K) + eps);
+  u32x4 xr[NR], wr[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int r = wid + RSTEP * i;
+    xr[i] = *reinterpret_cast<const u32x4 *>(tile + r * (PG_NORM_K * 2) + 16 * lane);
+    wr[i] = *reinterpret_cast<const u32x4 *>(nwx + 16 * (lane ^ (r & 15)));
+  }
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int r = wid + RSTEP * i;
+    const float rn = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rn_lane), r));
+    u32x4 xn;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      xn[e] = pack_bf(lo_bf(xr[i][e]) * rn * lo_bf(wr[i][e]), hi_bf(xr[i][e]) * rn * hi_bf(wr[i][e]));
+    *reinterpret_cast<u32x4 *>(tile + r * (PG_NORM_K * 2) + 16 * lane) = xn;
+  }
+}
+
 template <int PRO, int EPI, int KS>
 struct PanelShape {
   static constexpr bool SWI = EPI == EPI_SWIGLU;
@@ -392,9 +441,10 @@ struct PanelShape {
   static constexpr int ROWS = (XRES ? 0 : PG_BM) + WR;  // LDS rows per ring stage
   static constexpr int STAGEB = ROWS * PG_ROWB;
   static constexpr int LOADS = ROWS / 8 / 4;          // direct-load instructions per wave per stage
-  // the K loop is latency-bound (little MFMA work per stage): as many stages in flight as LDS allows
-  // with 2 workgroups per CU -- 4 slots (3 in flight) for 12 KB stages, 3 for the 20 KB SwiGLU stages
-  // (and for the 16 KB SwiGLU weight stages beside a resident A tile)
+  // ring depth: 4 slots (3 stages in flight) for 12 KB stages, 3 for the 20 KB SwiGLU stages (and for the
+  // 16 KB SwiGLU weight stages beside a resident A tile), so two workgroups share a CU where the grid has
+  // more workgroups than CUs. The K loop moves stages at the per-CU L2 -> LDS rate (about 90 GB/s, from
+  // per-phase timestamps): 5 or 6 slots for the one-workgroup-per-CU K-split shapes measured no faster.
   static constexpr int STAGES = SWI ? 3 : 4;
   static constexpr int XB = XRES ? PG_BM * PG_NORM_K * 2 : 0;  // resident A tile: 32 rows x 1 KB
   static constexpr int PARTB = PG_BM * (WR + 1) * 4;
@@ -416,6 +466,9 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
   static_assert(KS == 1 || (KS == 2 && (PRO == PRO_NONE || PRO == PRO_NORM_SS)),
                 "K halves only without the pre-pass norm prologue");
   using S = PanelShape<PRO, EPI, KS>;
+  static_assert(!S::XRES || S::STAGES - 1 <= PG_NORM_K / PG_BK / KS,
+                "resident-A variants issue STAGES - 1 whole stages before the normalisation");
+  static_assert(S::LOADS * (S::STAGES - 1) <= 63, "a wave's stages in flight must fit the vmcnt counter");
   constexpr bool XRES = S::XRES;
   constexpr bool SWI = S::SWI;
   constexpr bool ROPE = EPI == EPI_ROPE;
@@ -574,22 +627,7 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-#pragma unroll
-    for (int i = 0; i < PG_BM / (4 * KS); ++i) {
-      const int r = wid + 4 * KS * i;
-      const f32x4 sa = *reinterpret_cast<const f32x4 *>(ssx + 32 * r);
-      const f32x4 sb = *reinterpret_cast<const f32x4 *>(ssx + 32 * r + 16);
-      const float ss = ((sa[0] + sa[1]) + (sa[2] + sa[3])) + ((sb[0] + sb[1]) + (sb[2] + sb[3]));
-      const float rn = rsqrtf(ss * (1.0f / PG_NORM_K) + p.eps);  // exactly ss / K (K = 512)
-      u32x4 *xc = reinterpret_cast<u32x4 *>(smem + r * (PG_NORM_K * 2) + 16 * lane);
-      const u32x4 xr = *xc;
-      const u32x4 wr = *reinterpret_cast<const u32x4 *>(nwx + 16 * (lane ^ (r & 15)));
-      u32x4 xn;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        xn[e] = pack_bf(lo_bf(xr[e]) * rn * lo_bf(wr[e]), hi_bf(xr[e]) * rn * hi_bf(wr[e]));
-      *xc = xn;
-    }
+    pg_normalise_rows<PG_BM / (4 * KS), 4 * KS>(smem, nwx, ssx, PG_BM, wid, lane, p.eps);
     if constexpr (ROPE) {  // read before the barrier below, which retires them: the loop reuses the slot
       const int32_t *ps = reinterpret_cast<const int32_t *>(psx);
       e_pos = ps[rr];
@@ -652,13 +690,7 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
 
   for (int kt = 0; kt < nk; ++kt) {
     // this wave's loads of stage kt are done once at most (stages issued after it) x LOADS remain
-    const int ahead = min(nk - 1 - kt, S::STAGES - 2);
-    if (ahead >= 2)
-      __builtin_amdgcn_s_waitcnt(pg_vmcnt(2 * S::LOADS));
-    else if (ahead == 1)
-      __builtin_amdgcn_s_waitcnt(pg_vmcnt(S::LOADS));
-    else
-      __builtin_amdgcn_s_waitcnt(pg_vmcnt(0));
+    pg_wait_ahead<S::LOADS, S::STAGES - 2>(min(nk - 1 - kt, S::STAGES - 2));
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
