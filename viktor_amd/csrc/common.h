@@ -69,6 +69,26 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// The 16 x 16 x 32 MFMA operand "column c0 + lane % 16 of a row-major bf16 LDS tile (PITCH elements per row) at
+// rows r0 + 4 g .. + 3 and r0 + 16 + 4 g .. + 3" (g = lane / 16) as one bf16x8 -- a transposed fragment -- from
+// two gfx950 transpose reads ds_read_b64_tr_b16: within each 16-lane group, source lane s reads 4 consecutive
+// columns c0 + 4 (s % 4) .. + 3 of row R0 + s / 4, and output lane j receives column c0 + j at rows R0 .. R0 + 3.
+// PITCH % 4 == 0 and c0 % 4 == 0 keep every read 8-byte aligned.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+template <int PITCH>
+__device__ __forceinline__ bf16x8 lds_tr_frag(const bf16_t *tile, int r0, int c0, int lane) {
+  static_assert(PITCH % 4 == 0, "8-byte aligned transpose reads");
+  const int g = lane >> 4, s = lane & 15;
+  const bf16_t *p0 = tile + (r0 + 4 * g + (s >> 2)) * PITCH + c0 + 4 * (s & 3);
+  const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s16x4_t *)(const __attribute__((address_space(3))) bf16_t *)p0);
+  const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s16x4_t *)(const __attribute__((address_space(3))) bf16_t *)(p0 + 16 * PITCH));
+  typedef short s16x8_t __attribute__((ext_vector_type(8)));
+  return __builtin_bit_cast(bf16x8, s16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+}
+
 }  // namespace vk
 
 // ---- host side: status + message -------------------------------------------------------------

@@ -18,8 +18,8 @@
 //     rescale of O^T is lane-local too. The K-order of a 32-position tile is permuted consistently in
 //     both operands ({4g..4g+3, 16+4g..16+4g+3} for lane group g).
 //   * V^T needs position-contiguous fragments, the cache is column-contiguous: each wavefront stages
-//     its 32 x 128 V tile in its own LDS slice (16-byte writes) and gathers the transposed fragments
-//     with 2-byte reads (rows padded so the four lane groups hit disjoint banks).
+//     its 32 x 128 V tile in its own LDS slice (16-byte writes) and reads the transposed fragments with
+//     gfx950's transpose reads (two ds_read_b64_tr_b16 per fragment, in place of eight 2-byte reads).
 //   * Work split: a workgroup of WAVES wavefronts per (sequence, key split); its wavefronts take
 //     interleaved 32-position tiles; per-wave (max, sum, O) partials are merged through LDS. When the
 //     batch alone cannot fill the chip (B < 2 x CUs) the key range is split across workgroups and a
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(DA_WAVES * 64) void decode_attn_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] *= alpha;
 
-    // stage V (row-major) in this wave's LDS slice, gather transposed fragments
+    // stage V (row-major) in this wave's LDS slice, read transposed fragments
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
@@ -190,12 +190,8 @@ __global__ __launch_bounds__(DA_WAVES * 64) void decode_attn_kernel(
     load_v(tn);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      bf16x8 va;
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const int pl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
-        va[jj] = __builtin_bit_cast(__bf16, vs[pl * DA_PITCH + 16 * j + qrow]);
-      }
+      // V^T fragment: column 16 j + qrow at positions 4 g .. + 3 and 16 + 4 g .. + 3, by transpose reads
+      const bf16x8 va = lds_tr_frag<DA_PITCH>(vs, 0, 16 * j, lane);
       acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf, acc[j], 0, 0, 0);
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -539,12 +535,8 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
       load(vf, nxt.v, nxt);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        bf16x8 va;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int pl = jj < 4 ? 4 * g + jj : 16 + 4 * g + (jj - 4);
-          va[jj] = __builtin_bit_cast(__bf16, vsh[pl * GU_PITCH + 16 * dt + col]);
-        }
+        // V^T fragment: column 16 dt + col at tile rows 4 g .. + 3 and 16 + 4 g .. + 3, by transpose reads
+        const bf16x8 va = lds_tr_frag<GU_PITCH>(vsh, 0, 16 * dt, lane);
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb)
           if (NCB == 1 || cb_only < 0 || cb == cb_only)
