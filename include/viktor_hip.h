@@ -248,7 +248,7 @@ int vk_select_update(const float *logits, const void *h, const void *norm_w, flo
  * emb = the `x` argument [vocab, K], and the gathered rows are also stored to x_store; norm_w NULL: h = x,
  * the activation normalised by vk_add_rmsnorm / vk_embed_rmsnorm beforehand), then
  * qkv = bf16(h @ w_qkv^T) and the vk_qkv_rope_cache transform of qkv: q -> q [M, H, 64], k / v -> caches.
- * ss_in (may be NULL): the row sums of squares of x left by vk_linear_residual ([M, K / 64] fp32, K = 512);
+ * ss_in (may be NULL): the row sums of squares of x left by vk_linear_residual ([M, K / 32] fp32, K = 512);
  * then 1 / rms comes from them instead of a pass over x.
  * Replaces embed_rmsnorm / add_rmsnorm + linear + qkv_rope_cache (viktor/triton_ops.py:17-108, 149-169;
  * viktor/fast_decoder.py:41-46, 76-90).
@@ -264,8 +264,8 @@ int vk_norm_qkv_rope_cache(const void *x, const int64_t *tok, int64_t vocab, voi
 /*
  * vk_linear_residual: x[M, N] = bf16(x + bf16(a[M, K] @ w[N, K]^T)) in place (the o / down projections
  * followed by the residual add of add_rmsnorm, viktor/triton_ops.py:24-27, viktor/fast_decoder.py:51-57).
- * ss_out (may be NULL; N = 512): per-row partial sums of squares of the updated x, one per 64-column
- * block ([M, N / 64] fp32, each block's sum in a fixed order), for the next norm (the norm half of
+ * ss_out (may be NULL; N = 512): per-row partial sums of squares of the updated x, one per 32-column
+ * block ([M, N / 32] fp32, each block's sum in a fixed order), for the next norm (the norm half of
  * add_rmsnorm, viktor/triton_ops.py:28-40).
  */
 int vk_linear_residual(const void *a, const void *w, void *x, int64_t M, int32_t N, int32_t K, float *ss_out,

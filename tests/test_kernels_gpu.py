@@ -575,10 +575,11 @@ def test_group_advantage():
 
 
 # ---- decode-step fusions: against the oracle's composition of the unfused ops ------------------------
-def _row_ss(x):
-    """[M, K / 64] fp32 partial sums of squares of the rows of x, one per 64-column block."""
+def _row_ss(x, block=32):
+    """[M, K / block] fp32 partial sums of squares of the rows of x, one per block of columns (32: the
+    decode-step products' hand-over)."""
     M, K = x.shape
-    return (x.double() ** 2).view(M, K // 64, 64).sum(-1).float()
+    return (x.double() ** 2).view(M, K // block, block).sum(-1).float()
 
 
 @pytest.mark.parametrize("M", [1, 45, 512])
@@ -720,8 +721,11 @@ def test_linear_qkv_rope_no_norm_in_place():
     assert ok, err
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 512, 512), (512, 512, 512), (77, 512, 1536), (512, 512, 1536)])
+@pytest.mark.parametrize("M,N,K", [(1, 512, 512), (512, 512, 512), (77, 512, 1536), (512, 512, 1536),
+                                   (1100, 512, 1536), (300, 100, 512), (40, 512, 576)])
 def test_linear_residual(M, N, K):
+    """32 x 32 tiles while they fit one round of the chip (up to 512 rows of N = 512), the panel kernel beyond
+    (1100 rows) and for K % 128 != 0 (576), ragged N (100)."""
     g = gen(M * 7 + K)
     a = R.bf(torch.randn(M, K, generator=g))
     w = R.bf(torch.randn(N, K, generator=g) / math.sqrt(K))
@@ -736,16 +740,17 @@ def test_linear_residual(M, N, K):
     assert ok, err
 
 
-@pytest.mark.parametrize("M", [1, 77, 512])
-def test_linear_residual_row_sums(M):
-    """ss_out: the per-64-column-block sums of squares of the updated rows, and x unchanged by asking."""
-    g = gen(M * 3 + 1)
-    K = N = 512
+@pytest.mark.parametrize("M,K", [(1, 512), (77, 512), (512, 512), (512, 1536), (1024, 512), (1100, 1536), (64, 576)])
+def test_linear_residual_row_sums(M, K):
+    """ss_out: the per-32-column-block sums of squares of the updated rows, and x unchanged by asking -- from the
+    32 x 32 tiles and from the panel kernel (1024 and 1100 rows, K = 576)."""
+    g = gen(M * 3 + K)
+    N = 512
     a = R.bf(torch.randn(M, K, generator=g))
     w = R.bf(torch.randn(N, K, generator=g) / math.sqrt(K))
     x = R.bf(torch.randn(M, N, generator=g) * 2)
     xd, xd2 = to_dev(x, BF), to_dev(x, BF)
-    ss = torch.full((M, N // 64), float("nan"), device=DEV)
+    ss = torch.full((M, N // 32), float("nan"), device=DEV)
     ops.linear_residual(to_dev(a, BF), to_dev(w, BF), xd, ss_out=ss)
     ops.linear_residual(to_dev(a, BF), to_dev(w, BF), xd2)
     assert torch.equal(xd, xd2)

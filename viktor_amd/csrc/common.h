@@ -69,6 +69,28 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// max of three / two floats as one v_max3_f32 / v_max_f32. Written as asm: the compiler's fmaxf quiets
+// signalling NaNs with an extra max per operand; the attention kernels' scores are MFMA outputs or -inf, never NaN.
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float d;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+__device__ __forceinline__ float vmax2(float a, float b) {
+  float d;
+  asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+// max over lanes l, l ^ 16, l ^ 32, l ^ 48 with gfx950's lane swaps (VALU, no LDS round trip):
+// v_permlane32_swap(x, x) returns {x of lanes l % 32, x of lanes l % 32 + 32} and v_permlane16_swap(x, x)
+// {x of the even 16-lane row of l's pair, x of the odd one}
+__device__ __forceinline__ float max_lane_groups(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float m = vmax2(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  return vmax2(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // The 16 x 16 x 32 MFMA operand "column c0 + lane % 16 of a row-major bf16 LDS tile (PITCH elements per row) at
 // rows r0 + 4 g .. + 3 and r0 + 16 + 4 g .. + 3" (g = lane / 16) as one bf16x8 -- a transposed fragment -- from
 // two gfx950 transpose reads ds_read_b64_tr_b16: within each 16-lane group, source lane s reads 4 consecutive

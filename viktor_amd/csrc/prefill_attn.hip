@@ -33,28 +33,6 @@ typedef short pa_s4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) pa_s4 pa_lds_s4;
 constexpr float PA_SLACK = 8.0f;  // log2 units a row's score may pass its reference max before it moves
 
-// max of three floats as one v_max3_f32. Written as asm: the compiler's fmaxf quiets signalling NaNs with an
-// extra max per operand; the scores are MFMA outputs or -inf, never NaN.
-__device__ __forceinline__ float pa_max3(float a, float b, float c) {
-  float d;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-  return d;
-}
-__device__ __forceinline__ float pa_max2(float a, float b) {
-  float d;
-  asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
-  return d;
-}
-// max over lanes l, l ^ 16, l ^ 32, l ^ 48 with gfx950's lane swaps (VALU, no LDS round trip):
-// v_permlane32_swap(x, x) returns {x of lanes l % 32, x of lanes l % 32 + 32} and v_permlane16_swap(x, x)
-// {x of the even 16-lane row of l's pair, x of the odd one}
-__device__ __forceinline__ float pa_max_lanes(float x) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  const float m = pa_max2(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-  return pa_max2(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-
 __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ k, const bf16_t *__restrict__ v,
     const int32_t *__restrict__ cu_q, const int64_t *__restrict__ k_off, const int32_t *__restrict__ k_lens,
@@ -172,8 +150,8 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
             for (int i = 0; i < 4; ++i)
               sv[kb * 4 + i] = kbase + 16 * kb + 4 * g + i <= hi_k ? sv[kb * 4 + i] : -INFINITY;
         }
-        float mx = pa_max3(pa_max3(sv[0], sv[1], sv[2]), pa_max3(sv[3], sv[4], sv[5]), pa_max3(sv[6], sv[7], sv[7]));
-        mx = pa_max_lanes(mx);
+        float mx = vmax3(vmax3(sv[0], sv[1], sv[2]), vmax3(sv[3], sv[4], sv[5]), vmax3(sv[6], sv[7], sv[7]));
+        mx = max_lane_groups(mx);
         // The row's reference max moves only when a score passes it by more than PA_SLACK in log2 units of the
         // scaled scores: the probabilities are then exp2(s c - m c) <= 2^PA_SLACK (bf16 and the fp32 sums carry
         // them with the same relative precision as values <= 1), and the rescale of the row's sum and output

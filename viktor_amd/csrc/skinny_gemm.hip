@@ -43,11 +43,10 @@ struct SkinnyArgs {
   bf16_t *kc, *vc;
   int64_t stride_cb, stride_cs, cache_rows, cache_len;
   int H, HKV;
-  // EPI_RESID: per-row partial sums of squares of the updated residual, one per 64-column block
-  // ([M, N / 64] fp32; NULL: none). PRO_NORM_SS: those sums for the A rows ([M, ss_blocks]).
+  // EPI_RESID: per-row partial sums of squares of the updated residual, one per 32-column block
+  // ([M, N / 32] fp32, N = 512; NULL: none). PRO_NORM_SS: those sums for the A rows ([M, K / 32], K = 512).
   float *ss_out;
   const float *ss_in;
-  int ss_blocks;
 };
 
 constexpr int SK_BM = 32;
@@ -357,6 +356,8 @@ constexpr int PG_BN = 64;
 constexpr int PG_BK = 64;
 constexpr int PG_ROWB = PG_BK * 2;
 constexpr int PG_NORM_K = 512;  // the RMSNorm prologue is built for K = 512 (d_model)
+constexpr int PG_SS_COLS = 32;  // columns per handed-over partial sum of squares
+constexpr int PG_SS_N = PG_NORM_K / PG_SS_COLS;  // partials per row (16)
 
 // s_waitcnt immediate: vmcnt <= n, expcnt / lgkmcnt unconstrained (gfx9 encoding: vmcnt[3:0] bits 3:0,
 // vmcnt[5:4] bits 15:14, expcnt bits 6:4, lgkmcnt bits 11:8)
@@ -400,9 +401,9 @@ __device__ __forceinline__ void pg_wait_ahead(int ahead) {
 }
 
 // RMSNorm of a resident A tile in place (rows of K = 512 bf16, chunk c of row r in slot c ^ (r & 15)) from
-// the row sums of squares handed over by the producing residual product (ssx: [rows][8] fp32 in LDS) and the
-// norm weight (nwx: 512 bf16 in LDS): x = bf16(x * (1 / rms) * w), 1 / rms = rsqrt(sum / 512 + eps) with the
-// row's 8 partials summed in a fixed order. This wave takes rows r = wid + RSTEP i (i < NR), a whole 1 KB row
+// the row sums of squares handed over by the producing residual product (ssx: [rows][16] fp32 in LDS, one per
+// 32 columns) and the norm weight (nwx: 512 bf16 in LDS): x = bf16(x * (1 / rms) * w), 1 / rms =
+// rsqrt(sum / 512 + eps) with the row's 16 partials summed pairwise in a fixed order. This wave takes rows r = wid + RSTEP i (i < NR), a whole 1 KB row
 // per step (lane l takes slot l, conflict-free). Lane l first computes 1 / rms of row l, and a row's value is
 // read from its lane; all rows' reads are issued before the first write, so the LDS round trips overlap
 // (a read after a write to the same tile would wait for it).
@@ -410,9 +411,13 @@ template <int NR, int RSTEP>
 __device__ __forceinline__ void pg_normalise_rows(char *tile, const char *nwx, const char *ssx, int rows, int wid,
                                                   int lane, float eps) {
   const int lr = lane < rows ? lane : 0;
-  const f32x4 sa = *reinterpret_cast<const f32x4 *>(ssx + 32 * lr);
-  const f32x4 sb = *reinterpret_cast<const f32x4 *>(ssx + 32 * lr + 16);
-  const float ss = ((sa[0] + sa[1]) + (sa[2] + sa[3])) + ((sb[0] + sb[1]) + (sb[2] + sb[3]));
+  float s4[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(ssx + PG_SS_N * 4 * lr + 16 * q);
+    s4[q] = (v[0] + v[1]) + (v[2] + v[3]);
+  }
+  const float ss = (s4[0] + s4[1]) + (s4[2] + s4[3]);
   const float rn_lane = rsqrtf(ss * (1.0f / PG_NORM_K) + eps);
   u32x4 xr[NR], wr[NR];
 #pragma unroll
@@ -541,18 +546,21 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
   // after the normalisation; every wave loads it (the same bytes) ahead of its tile rows, so the one counted
   // wait before the normalisation covers it. Register loads are kept out of this stretch: one consumed while
   // direct loads are in flight makes the compiler wait for all of them.
-  // The tile's row sums of squares (32 rows x 8 fp32 = 1 KB) follow it there the same way: lane l brings
-  // half l % 2 of row l / 2; and for RoPE the rows' int32 positions: [pos x 32 | seq x 32] and
+  // The tile's row sums of squares (32 rows x 16 fp32 = 2 KB) follow it there the same way: lane l of load h
+  // brings quarter l % 4 of row 16 h + l / 4; and for RoPE the rows' int32 positions: [pos x 32 | seq x 32] and
   // [rope pos x 32 | again], 4 bytes per lane (rows past M read row M - 1; their results are not stored).
   char *const nwx = smem + S::XB + (S::STAGES - 1) * S::STAGEB;
   char *const ssx = nwx + PG_NORM_K * 2;
-  char *const psx = ssx + PG_BM * 8 * 4;
-  static_assert(!XRES || PG_NORM_K * 2 + PG_BM * 8 * 4 + 2 * 64 * 4 <= S::STAGEB, "staging fits one ring slot");
+  char *const psx = ssx + PG_BM * PG_SS_N * 4;
+  static_assert(!XRES || PG_NORM_K * 2 + PG_BM * PG_SS_N * 4 + 2 * 64 * 4 <= S::STAGEB, "staging fits one ring slot");
   if constexpr (XRES) {
     pg_issue_row(nwx, p.norm_w + 8 * lane);
-    int64_t srow = m0 + (lane >> 1);
-    srow = srow < p.M ? srow : p.M - 1;
-    pg_issue_row(ssx, reinterpret_cast<const bf16_t *>(p.ss_in + srow * 8 + 4 * (lane & 1)));
+#pragma unroll
+    for (int h = 0; h < PG_BM * PG_SS_N * 4 / 1024; ++h) {
+      int64_t srow = m0 + 16 * h + (lane >> 2);
+      srow = srow < p.M ? srow : p.M - 1;
+      pg_issue_row(ssx + 1024 * h, reinterpret_cast<const bf16_t *>(p.ss_in + srow * PG_SS_N + 4 * (lane & 3)));
+    }
     if constexpr (ROPE) {
       int64_t prow = m0 + (lane & 31);
       prow = prow < p.M ? prow : p.M - 1;
@@ -619,8 +627,8 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
   }
 
   // 4'. PRO_NORM_SS: normalise the resident A tile in place, a whole 1 KB row per wave and step (lane l takes
-  //     slot l, conflict-free). 1 / rms comes from the row's ss_blocks (= K / 64) partial sums, summed in a
-  //     fixed order. K = 512 (checked on the host), so the first STAGES - 1 ring stages were all issued:
+  //     slot l, conflict-free). 1 / rms comes from the row's 16 partial sums (one per 32 columns), summed in
+  //     a fixed order. K = 512 (checked on the host), so the first STAGES - 1 ring stages were all issued:
   //     waiting until only their loads are outstanding retires this wave's weight, row sums and tile rows.
   if constexpr (XRES) {
     __builtin_amdgcn_s_waitcnt(pg_vmcnt(S::LOADS * (S::STAGES - 1)));
@@ -821,7 +829,7 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
     }
     return;
   }
-  float ssq = 0.f;  // EPI_RESID: this thread's share of the row's sum of squares over the block
+  float ssq[HALVES] = {};  // EPI_RESID: this thread's share of the row's sum of squares over each 32-column half
 #pragma unroll
   for (int hf = 0; hf < HALVES; ++hf) {
     const int col = n0 + 32 * hf + 4 * sub;
@@ -853,19 +861,165 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const float lo = lo_bf(packed[e]), hi = hi_bf(packed[e]);
-          ssq += lo * lo + hi * hi;
+          ssq[hf] += lo * lo + hi * hi;
         }
       }
     }
   }
   if constexpr (EPI == EPI_RESID) {
     if (p.ss_out) {  // the 8 lanes of a row (consecutive) reduce their shares in a fixed order
-      ssq += __shfl_xor(ssq, 1, 64);
-      ssq += __shfl_xor(ssq, 2, 64);
-      ssq += __shfl_xor(ssq, 4, 64);
-      if (row_ok && sub == 0) p.ss_out[erow * ((p.N + PG_BN - 1) / PG_BN) + nb] = ssq;
+#pragma unroll
+      for (int hf = 0; hf < HALVES; ++hf) {
+        float v = ssq[hf];
+        v += __shfl_xor(v, 1, 64);
+        v += __shfl_xor(v, 2, 64);
+        v += __shfl_xor(v, 4, 64);
+        if (row_ok && sub == 0) p.ss_out[erow * (p.N / PG_SS_COLS) + 2 * nb + hf] = v;
+      }
     }
   }
+}
+
+// ---- residual product on 32 x 32 tiles (the decode step's o / down projections) ------------------------
+//
+// x[M, N] += bf16(A[M, K] W[N, K]^T) with the rounding points of add_rmsnorm, and (optionally) the row's sum of
+// squares of the updated x over each 32-column block. A workgroup's time hardly depends on how many run beside
+// it (measured at K = 512: 4.2 us for 32 workgroups, 4.6 us for 256): it is set by the bytes one CU moves from
+// L2 into LDS (about 100 GB/s per CU) plus a fixed cost. 32 x 32 tiles put the decode step's 512 x 512 output on
+// 256 workgroups moving 64 x K x 2 bytes each, against 128 panel workgroups of 32 x 64 moving 96 x K x 2.
+//   * 8 wavefronts, two K halves of 4; each half streams its 32 A and 32 W rows through its own 6-slot ring of
+//     64-wide K stages (8 KB) by direct global->LDS loads (lane l of an instruction lands at slot base + 16 l);
+//   * wave (half h, q) multiplies A block q >> 1 by weight block q & 1 (one 16 x 16 x 32 MFMA tile, C^T
+//     formulation: the weight fragment is the A operand);
+//   * the halves' tiles meet in LDS and the epilogue adds them in a fixed order (first half + second half).
+constexpr int RS_BM = 32, RS_BN = 32, RS_STAGES = 6;
+constexpr int RS_ROWS = RS_BM + RS_BN;          // LDS rows per ring stage (A rows, then W rows)
+constexpr int RS_STAGEB = RS_ROWS * PG_ROWB;    // 8 KB
+constexpr int RS_LOADS = RS_ROWS / 8 / 4;       // direct loads per wave per stage
+constexpr int RS_RING = RS_STAGES * RS_STAGEB;  // one ring per K half
+constexpr int RS_PITCH = RS_BN + 1;             // fp32 row pitch of a half's tile
+static_assert(2 * RS_BM * RS_PITCH * 4 <= 2 * RS_RING, "both halves' fp32 tiles fit the rings");
+static_assert(RS_BN == PG_SS_COLS, "one partial sum of squares per tile row");
+
+__global__ __launch_bounds__(512) void resid_gemm_kernel(const SkinnyArgs p, int m_blocks, int tiles) {
+  __shared__ __attribute__((aligned(16))) char smem[2 * RS_RING];
+  const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wq = wid & 3, kh = wid >> 2;  // wave within its K half, K half
+  // XCD-aware order (as the panel kernel): workgroup p runs on XCD p % 8, which owns a contiguous range of the
+  // n-block-major tiles
+  const int pid = blockIdx.x, xcd = pid & 7, idx = pid >> 3;
+  const int q8 = tiles >> 3, r8 = tiles & 7;
+  const int tile = xcd * q8 + min(xcd, r8) + idx;
+  const int nb = tile / m_blocks, mb = tile % m_blocks;
+  const int64_t m0 = static_cast<int64_t>(mb) * RS_BM;
+  const int n0 = nb * RS_BN;
+  // run-time K (a constant trip count lets the compiler unroll the loop, see the ring offsets and drain every
+  // load before each LDS read)
+  const int K = p.K, nk = K / (PG_BK * 2), kbase = kh * (K / 2);
+  const int fr = lane & 15, fg = lane >> 4;
+
+  // sources: instruction q = wq + 4 j of a stage covers ring rows 8 q .. 8 q + 7; lane l -> row 8 q + l / 8,
+  // slot l % 8, K chunk slot ^ ((row >> 1) & 7); rows past M or N read the last row (not stored)
+  const bf16_t *src[RS_LOADS];
+#pragma unroll
+  for (int j = 0; j < RS_LOADS; ++j) {
+    const int r = 8 * (wq + 4 * j) + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    if (r < RS_BM) {
+      int64_t row = m0 + r;
+      row = row < p.M ? row : p.M - 1;
+      src[j] = p.a + row * K + 8 * c + kbase;
+    } else {
+      int col = n0 + r - RS_BM;
+      col = col < p.N ? col : p.N - 1;
+      src[j] = p.w + static_cast<int64_t>(col) * K + 8 * c + kbase;
+    }
+  }
+  char *const ring = smem + kh * RS_RING;
+#pragma unroll
+  for (int s = 0; s < RS_STAGES - 1; ++s)
+    if (s < nk) pg_issue<RS_LOADS>(ring + s * RS_STAGEB, src, s * PG_BK, wq);
+
+  // epilogue mapping: thread t < 256 -> row m0 + t / 8, columns 4 (t % 8) .. + 3; the old residual is loaded
+  // now, unconditionally (row and column clamped): a load under a branch makes the compiler wait for every
+  // outstanding load, the ring's included, where its register is merged
+  const int rr = (tid >> 3) & (RS_BM - 1), sub = tid & 7;
+  const int64_t erow = m0 + rr;
+  const int ecol = n0 + 4 * sub;
+  u32x2 old;
+  {
+    const int64_t orow = erow < p.M ? erow : p.M - 1;
+    const int ocol = ecol < p.N ? ecol : p.N - 4;
+    old = *reinterpret_cast<const u32x2 *>(static_cast<const bf16_t *>(p.y) + orow * p.N + ocol);
+  }
+
+  const int ta = wq >> 1, wb = wq & 1;
+  int xoff[2], woff[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int c = 4 * ks + fg;
+    const int RA = 16 * ta + fr, RW = RS_BM + 16 * wb + fr;
+    xoff[ks] = RA * PG_ROWB + 16 * (c ^ ((RA >> 1) & 7));
+    woff[ks] = RW * PG_ROWB + 16 * (c ^ ((RW >> 1) & 7));
+  }
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int kt = 0; kt < nk; ++kt) {
+    pg_wait_ahead<RS_LOADS, RS_STAGES - 2>(min(nk - 1 - kt, RS_STAGES - 2));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // every wave's stage kt has landed; every wave is done with stage kt - 1
+    asm volatile("" ::: "memory");
+    if (kt + RS_STAGES - 1 < nk)
+      pg_issue<RS_LOADS>(ring + ((kt + RS_STAGES - 1) % RS_STAGES) * RS_STAGEB, src, (kt + RS_STAGES - 1) * PG_BK, wq);
+    const char *base = ring + (kt % RS_STAGES) * RS_STAGEB;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const u32x4 xf = *reinterpret_cast<const u32x4 *>(base + xoff[ks]);
+      const u32x4 wf = *reinterpret_cast<const u32x4 *>(base + woff[ks]);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf), __builtin_bit_cast(bf16x8, xf), acc,
+                                                    0, 0, 0);
+    }
+  }
+
+  // tiles -> LDS: acc lane holds C^T[weight row 16 wb + 4 fg + e][A row 16 ta + fr] of its K half
+  lds_barrier();
+  float *part = reinterpret_cast<float *>(smem);  // [2][RS_BM][RS_PITCH]
+#pragma unroll
+  for (int e = 0; e < 4; ++e) part[(kh * RS_BM + 16 * ta + fr) * RS_PITCH + 16 * wb + 4 * fg + e] = acc[e];
+  lds_barrier();
+  if (tid >= 256) return;
+
+  // x = bf16(x + bf16(first half + second half)); the row's sum of squares over the 32 columns from the 8 lanes
+  // of the row (consecutive) in a fixed order
+  float o[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    o[c] = round_bf(part[rr * RS_PITCH + 4 * sub + c] + part[(RS_BM + rr) * RS_PITCH + 4 * sub + c]);
+  o[0] += lo_bf(old[0]);
+  o[1] += hi_bf(old[0]);
+  o[2] += lo_bf(old[1]);
+  o[3] += hi_bf(old[1]);
+  const u32x2 packed = u32x2{pack_bf(o[0], o[1]), pack_bf(o[2], o[3])};
+  const bool ok = erow < p.M && ecol < p.N;  // N is a multiple of 4 (checked on the host)
+  if (ok) *reinterpret_cast<u32x2 *>(static_cast<bf16_t *>(p.y) + erow * p.N + ecol) = packed;
+  if (p.ss_out) {
+    float ssq = 0.f;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float lo = lo_bf(packed[e]), hi = hi_bf(packed[e]);
+      ssq += lo * lo + hi * hi;
+    }
+    ssq += __shfl_xor(ssq, 1, 64);
+    ssq += __shfl_xor(ssq, 2, 64);
+    ssq += __shfl_xor(ssq, 4, 64);
+    if (erow < p.M && sub == 0) p.ss_out[erow * (p.N / PG_SS_COLS) + nb] = ssq;
+  }
+}
+
+static int launch_resid(const SkinnyArgs &a, hipStream_t s) {
+  const int64_t m_blocks = (a.M + RS_BM - 1) / RS_BM;
+  const int64_t tiles = m_blocks * ((a.N + RS_BN - 1) / RS_BN);
+  resid_gemm_kernel<<<static_cast<unsigned>(tiles), 512, 0, s>>>(a, static_cast<int>(m_blocks), static_cast<int>(tiles));
+  return VK_OK;
 }
 
 template <int PRO, int EPI>
@@ -991,8 +1145,12 @@ extern "C" int vk_linear_residual(const void *a, const void *w, void *x, int64_t
   p.ss_out = ss_out;
   VK_CHECK_ARG(!ss_out || (panel_ok(p, PRO_NONE) && N == PG_NORM_K),
                "linear_residual: row sums of squares need K %% 64 == 0 and N = %d", PG_NORM_K);
-  const int rc = panel_ok(p, PRO_NONE) ? launch_panel<PRO_NONE, EPI_RESID>(p, VK_STREAM(stream))
-                                       : dispatch_k<32, PRO_NONE, EPI_RESID>(p, VK_STREAM(stream));
+  // 32 x 32 tiles while they fit one resident round of the chip (the decode step's 512 rows), else the panel
+  const int64_t rs_tiles = ((M + RS_BM - 1) / RS_BM) * ((N + RS_BN - 1) / RS_BN);
+  const int rc = (K % (2 * PG_BK) == 0 && rs_tiles <= device_cus_cached())
+                     ? launch_resid(p, VK_STREAM(stream))
+                     : (panel_ok(p, PRO_NONE) ? launch_panel<PRO_NONE, EPI_RESID>(p, VK_STREAM(stream))
+                                              : dispatch_k<32, PRO_NONE, EPI_RESID>(p, VK_STREAM(stream)));
   if (rc != VK_OK) return rc;
   return launch_status("linear_residual");
 }

@@ -238,9 +238,9 @@ class FastDecoder:
             _require(x.dtype == BF16 and x.is_contiguous(), "decode: x must be contiguous bf16")
             B, xr = x.shape[0], x
         ws = self.decode_workspace
-        # row sums of squares of the residual, left by each residual GEMM for the next norm (one per 64-column
+        # row sums of squares of the residual, left by each residual GEMM for the next norm (one per 32-column
         # block): the norms run inside the qkv / gate_up GEMMs without a pass of their own over x
-        ss_attn = torch.empty(B, cfg.d_model // 64, dtype=torch.float32, device=(tok if tok is not None else x).device)
+        ss_attn = torch.empty(B, cfg.d_model // 32, dtype=torch.float32, device=(tok if tok is not None else x).device)
         ss_mlp = torch.empty_like(ss_attn)
         for i, blk in enumerate(layers):
             a = blk.attn

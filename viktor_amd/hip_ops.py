@@ -391,7 +391,7 @@ def norm_qkv_rope_cache(x, norm_w, eps, w_qkv, q_norm_w, k_norm_w, cos, sin, pos
     """Decode-step fusion: h = RMSNorm(x) * norm_w (or, with tok, x = emb[tok] where `x` is the embedding
     table, stored into x_store; norm_w None: h = x), qkv = h @ w_qkv^T, then QK-norm + RoPE + KV-cache write
     as qkv_rope_cache. Returns q [M, H, D]. Same rounding points as add_rmsnorm + linear + qkv_rope_cache.
-    ss: the [M, K / 64] fp32 row sums of squares linear_residual(ss_out=...) left for x (K = 512)."""
+    ss: the [M, K / 32] fp32 row sums of squares linear_residual(ss_out=...) left for x (K = 512)."""
     require_device(x, "norm_qkv_rope_cache")
     M = tok.shape[0] if tok is not None else x.shape[0]
     K = x.shape[1]
@@ -409,7 +409,7 @@ def norm_qkv_rope_cache(x, norm_w, eps, w_qkv, q_norm_w, k_norm_w, cos, sin, pos
              and k_cache.stride(2) == head_dim, "norm_qkv_rope_cache: cache layout")
     _require(_contig(x, norm_w, w_qkv, q_norm_w, k_norm_w, cos, sin, pos, seq, rope_pos, tok, x_store, ss),
              "norm_qkv_rope_cache: contiguous tensors")
-    _require(ss is None or (ss.dtype == torch.float32 and ss.shape == (M, K // 64)), "norm_qkv_rope_cache: ss [M, K/64]")
+    _require(ss is None or (ss.dtype == torch.float32 and ss.shape == (M, K // 32)), "norm_qkv_rope_cache: ss [M, K/32]")
     q = torch.empty(M, n_heads, head_dim, dtype=BF16, device=x.device)
     call("vk_norm_qkv_rope_cache", ptr(x), ptr(tok), x.shape[0] if tok is not None else 0, ptr(x_store), ptr(norm_w),
          float(eps), ptr(w_qkv), ptr(q_norm_w), ptr(k_norm_w), ptr(cos), ptr(sin),
@@ -421,26 +421,27 @@ def norm_qkv_rope_cache(x, norm_w, eps, w_qkv, q_norm_w, k_norm_w, cos, sin, pos
 
 def linear_residual(a, w, x, ss_out=None):
     """x += a @ w^T in place (bf16 GEMM output added to the bf16 residual, rounded as linear + add_rmsnorm).
-    ss_out [M, N / 64] fp32 (N = 512): per-row partial sums of squares of the updated x, for the next norm."""
+    ss_out [M, N / 32] fp32 (N = 512): per-row partial sums of squares of the updated x (one per 32 columns),
+    for the next norm."""
     require_device(a, "linear_residual")
     M, K = a.shape
     _require(a.dtype == w.dtype == x.dtype == BF16 and w.shape[1] == K and x.shape == (M, w.shape[0]),
              "linear_residual: shapes")
     _require(_contig(a, w, x, ss_out), "linear_residual: contiguous tensors")
-    _require(ss_out is None or (ss_out.dtype == torch.float32 and ss_out.shape == (M, w.shape[0] // 64)),
-             "linear_residual: ss_out [M, N/64] fp32")
+    _require(ss_out is None or (ss_out.dtype == torch.float32 and ss_out.shape == (M, w.shape[0] // 32)),
+             "linear_residual: ss_out [M, N/32] fp32")
     call("vk_linear_residual", ptr(a), ptr(w), ptr(x), M, w.shape[0], K, ptr(ss_out), stream_handle())
     return x
 
 
 def norm_linear(x, norm_w, eps, w, swiglu=False, out_dtype=None, ss=None):
     """act(RMSNorm(x) * norm_w @ w^T) for small M (norm_w None: no norm); act = SwiGLU over [gate; up].
-    ss: the [M, K / 64] fp32 row sums of squares linear_residual(ss_out=...) left for x (K = 512)."""
+    ss: the [M, K / 32] fp32 row sums of squares linear_residual(ss_out=...) left for x (K = 512)."""
     require_device(x, "norm_linear")
     M, K = x.shape
     _require(x.dtype == w.dtype == BF16 and w.shape[1] == K, "norm_linear: shapes")
     _require(_contig(x, norm_w, w, ss), "norm_linear: contiguous tensors")
-    _require(ss is None or (ss.dtype == torch.float32 and ss.shape == (M, K // 64)), "norm_linear: ss [M, K/64]")
+    _require(ss is None or (ss.dtype == torch.float32 and ss.shape == (M, K // 32)), "norm_linear: ss [M, K/32]")
     N = w.shape[0] // 2 if swiglu else w.shape[0]
     odt = out_dtype or BF16
     y = torch.empty(M, N, dtype=odt, device=x.device)
