@@ -758,9 +758,10 @@ def test_linear_residual_row_sums(M, K):
     assert torch.allclose(ss.cpu(), want, rtol=1e-5, atol=0), float((ss.cpu() - want).abs().max())
 
 
-@pytest.mark.parametrize("M", [1, 100, 512])
+@pytest.mark.parametrize("M", [1, 100, 512, 1024])
 @pytest.mark.parametrize("mode", ["swiglu", "bf16", "f32", "nonorm", "swiglu_ss", "bf16_ss", "f32_ss"])
 def test_norm_linear(M, mode):
+    """swiglu_ss: the 32 x 96 tiles up to one round of the chip (512 rows), the panel kernel at 1024 rows."""
     use_ss = mode.endswith("_ss")
     mode = mode.replace("_ss", "")
     g = gen(M + len(mode))

@@ -880,6 +880,166 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
   }
 }
 
+// ---- norm + gate_up + SwiGLU on 32 rows x 96 output columns (the decode step's MLP input product) ---------
+//
+// The panel kernel's 32 x 64 SwiGLU tiles put the decode step's 512 x 1536 output on 384 workgroups, two per CU
+// on half the chip: those CUs move 2 x (32 + 128) KB from L2 into LDS, at about 100 GB/s per CU. Here a
+// workgroup owns 32 rows x 96 output columns (96 gate + 96 up weight rows): 256 workgroups, one per CU, each
+// moving 32 + 192 KB.
+//   * A (32 rows x K = 512) is resident in LDS, normalised in place from the handed-over row sums of squares
+//     (pg_normalise_rows, as the panel kernel: the same bits);
+//   * the 192 weight rows stream through a 4-slot ring of 64-wide K stages (24 KB) by direct global->LDS loads;
+//   * wave w multiplies both A blocks by weight blocks 3 w .. 3 w + 2 (16 x 16 x 32 MFMA, C^T formulation):
+//     five fragment reads per six MFMAs;
+//   * the tile goes through LDS to the SwiGLU epilogue, with the panel kernel's rounding points.
+constexpr int GW_BM = 32, GW_BN = 96, GW_WR = 2 * GW_BN, GW_STAGES = 4;
+constexpr int GW_XB = GW_BM * PG_NORM_K * 2;           // resident A: 32 KB
+constexpr int GW_STAGEB = GW_WR * PG_ROWB;              // 24 KB
+constexpr int GW_LOADS = GW_WR / 8 / 4;                 // direct loads per wave per stage
+constexpr int GW_PITCH = GW_WR + 1;                     // fp32 row pitch of the tile handed to the epilogue
+constexpr int GW_SMEM = GW_XB + GW_STAGES * GW_STAGEB;  // 128 KB: one workgroup per CU
+static_assert(GW_BM * GW_PITCH * 4 <= GW_STAGES * GW_STAGEB, "the fp32 tile reuses the ring");
+static_assert(PG_NORM_K * 2 + GW_BM * PG_SS_N * 4 <= GW_STAGEB, "norm weight and row sums fit one ring slot");
+static_assert(GW_WR == 4 * 3 * 16, "four waves of three 16-row weight blocks");
+static_assert(GW_LOADS * (GW_STAGES - 1) + GW_BM / 4 + 3 <= 63, "a wave's loads in flight fit the vmcnt counter");
+
+__global__ __launch_bounds__(256) void gate_up_wide_kernel(const SkinnyArgs p, int m_blocks, int tiles) {
+  __shared__ __attribute__((aligned(16))) char smem[GW_SMEM];
+  const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // XCD-aware order (as the panel kernel): workgroup p runs on XCD p % 8, which owns a contiguous range of the
+  // n-block-major tiles, so the workgroups of one XCD share weight tiles
+  const int pid = blockIdx.x, xcd = pid & 7, idx = pid >> 3;
+  const int q8 = tiles >> 3, r8 = tiles & 7;
+  const int tile = xcd * q8 + min(xcd, r8) + idx;
+  const int nb = tile / m_blocks, mb = tile % m_blocks;
+  const int64_t m0 = static_cast<int64_t>(mb) * GW_BM;
+  const int n0 = nb * GW_BN;
+  // run-time K (512, checked on the host): a constant trip count lets the compiler unroll the K loop, see the
+  // ring offsets and drain every load before each LDS read
+  const int K = p.K, nk = K / PG_BK;
+  // weight sources: instruction q = wid + 4 j of a stage covers ring rows 8 q .. 8 q + 7 (gate rows, then up
+  // rows); lane l -> row 8 q + l / 8, slot l % 8, K chunk slot ^ ((row >> 1) & 7)
+  const bf16_t *src[GW_LOADS];
+#pragma unroll
+  for (int j = 0; j < GW_LOADS; ++j) {
+    const int r = 8 * (wid + 4 * j) + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    const int wrow = r < GW_BN ? n0 + r : p.N + n0 + (r - GW_BN);  // n0 + 95 < N (N % 96 == 0)
+    src[j] = p.w + static_cast<int64_t>(wrow) * K + 8 * c;
+  }
+  // the norm weight (1 KB) and the 32 rows' 16 partial sums of squares (2 KB) go to the last ring slot, which the
+  // K loop fills only after the normalisation; every wave loads them (the same bytes), so its own counted wait
+  // covers them. Lane l of load h brings quarter l % 4 of row 16 h + l / 4.
+  char *const nwx = smem + GW_XB + (GW_STAGES - 1) * GW_STAGEB;
+  char *const ssx = nwx + PG_NORM_K * 2;
+  pg_issue_row(nwx, p.norm_w + 8 * lane);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    int64_t srow = m0 + 16 * h + (lane >> 2);
+    srow = srow < p.M ? srow : p.M - 1;
+    pg_issue_row(ssx + 1024 * h, reinterpret_cast<const bf16_t *>(p.ss_in + srow * PG_SS_N + 4 * (lane & 3)));
+  }
+  // the resident A tile: row i is one instruction, issued by wave i % 4; chunk c of row r in slot c ^ (r & 15)
+#pragma unroll
+  for (int i = 0; i < GW_BM / 4; ++i) {
+    const int r = wid + 4 * i;
+    int64_t row = m0 + r;
+    row = row < p.M ? row : p.M - 1;
+    pg_issue_row(smem + r * (PG_NORM_K * 2), p.a + row * K + 8 * (lane ^ (r & 15)));
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int s = 0; s < GW_STAGES - 1; ++s) pg_issue<GW_LOADS>(smem + GW_XB + s * GW_STAGEB, src, s * PG_BK, wid);
+  asm volatile("" ::: "memory");
+  // waiting until only the ring's loads are outstanding retires this wave's staging and tile rows; the barrier,
+  // every wave's
+  __builtin_amdgcn_s_waitcnt(pg_vmcnt(GW_LOADS * (GW_STAGES - 1)));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  pg_normalise_rows<GW_BM / 4, 4>(smem, nwx, ssx, GW_BM, wid, lane, p.eps);
+  lds_barrier();
+
+  const int fr = lane & 15, fg = lane >> 4;
+  int woff[3][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int R = 16 * (3 * wid + j) + fr, c = 4 * ks + fg;
+      woff[j][ks] = R * PG_ROWB + 16 * (c ^ ((R >> 1) & 7));
+    }
+  f32x4 acc[2][3];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kt = 0; kt < nk; ++kt) {
+    pg_wait_ahead<GW_LOADS, GW_STAGES - 2>(min(nk - 1 - kt, GW_STAGES - 2));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // every wave's stage kt has landed; every wave is done with stage kt - 1
+    asm volatile("" ::: "memory");
+    if (kt + GW_STAGES - 1 < nk)
+      pg_issue<GW_LOADS>(smem + GW_XB + ((kt + GW_STAGES - 1) % GW_STAGES) * GW_STAGEB, src,
+                         (kt + GW_STAGES - 1) * PG_BK, wid);
+    const char *base = smem + GW_XB + (kt % GW_STAGES) * GW_STAGEB;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      u32x4 xf[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {  // resident row 16 t + fr, K chunk 8 kt + 4 ks + fg
+        const int c = 8 * kt + 4 * ks + fg;
+        xf[t] = *reinterpret_cast<const u32x4 *>(smem + (16 * t + fr) * (PG_NORM_K * 2) + 16 * (c ^ fr));
+      }
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const u32x4 wf = *reinterpret_cast<const u32x4 *>(base + woff[j][ks]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf),
+                                                              __builtin_bit_cast(bf16x8, xf[t]), acc[t][j], 0, 0, 0);
+      }
+    }
+  }
+
+  // tile -> LDS: acc[t][j] lane holds C^T[weight row 16 (3 wid + j) + 4 fg + e][A row 16 t + fr]
+  lds_barrier();
+  float *part = reinterpret_cast<float *>(smem + GW_XB);  // [GW_BM][GW_PITCH]
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) part[(16 * t + fr) * GW_PITCH + 16 * (3 * wid + j) + 4 * fg + e] = acc[t][j][e];
+  lds_barrier();
+
+  // SwiGLU epilogue: 32 rows x 24 groups of 4 columns, three per thread; out = bf16(bf16(silu(bf16(g))) bf16(u))
+#pragma unroll
+  for (int it = 0; it < 3; ++it) {
+    const int i = tid + 256 * it, rr = i / 24, grp = i - 24 * rr;
+    const int64_t erow = m0 + rr;
+    if (erow >= p.M) continue;
+    float o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float g = round_bf(part[rr * GW_PITCH + 4 * grp + c]);
+      const float u = round_bf(part[rr * GW_PITCH + GW_BN + 4 * grp + c]);
+      o[c] = round_bf(g / (1.0f + __expf(-g))) * u;
+    }
+    *reinterpret_cast<u32x2 *>(static_cast<bf16_t *>(p.y) + erow * p.N + n0 + 4 * grp) =
+        u32x2{pack_bf(o[0], o[1]), pack_bf(o[2], o[3])};
+  }
+}
+
+static int launch_gate_up_wide(const SkinnyArgs &a, hipStream_t s) {
+  const int64_t m_blocks = (a.M + GW_BM - 1) / GW_BM;
+  const int64_t tiles = m_blocks * (a.N / GW_BN);
+  gate_up_wide_kernel<<<static_cast<unsigned>(tiles), 256, 0, s>>>(a, static_cast<int>(m_blocks),
+                                                                   static_cast<int>(tiles));
+  return VK_OK;
+}
+
 // ---- residual product on 32 x 32 tiles (the decode step's o / down projections) ------------------------
 //
 // x[M, N] += bf16(A[M, K] W[N, K]^T) with the rounding points of add_rmsnorm, and (optionally) the row's sum of
@@ -1104,8 +1264,11 @@ extern "C" int vk_norm_linear(const void *x, const void *norm_w, float eps, cons
   if (ss_in) {  // the norm from the producing GEMM's row sums of squares
     VK_CHECK_ARG(norm_w && K == PG_NORM_K && vk_aligned16(ss_in), "norm_linear: ss_in needs norm_w and K = %d",
                  PG_NORM_K);
-    rc = swiglu ? launch_panel<PRO_NORM_SS, EPI_SWIGLU>(p, s)
-                : (out_dtype == VK_DTYPE_F32 ? launch_panel<PRO_NORM_SS, EPI_F32>(p, s)
+    // 32 x 96 SwiGLU tiles while they fit one resident round of the chip (the decode step's 512 rows)
+    const bool wide = swiglu && N % GW_BN == 0 && ((M + GW_BM - 1) / GW_BM) * (N / GW_BN) <= device_cus_cached();
+    rc = wide     ? launch_gate_up_wide(p, s)
+         : swiglu ? launch_panel<PRO_NORM_SS, EPI_SWIGLU>(p, s)
+                  : (out_dtype == VK_DTYPE_F32 ? launch_panel<PRO_NORM_SS, EPI_F32>(p, s)
                                              : launch_panel<PRO_NORM_SS, EPI_BF16>(p, s));
   } else if (panel_ok(p, norm_w ? PRO_NORM : PRO_NONE)) {
     if (norm_w)
