@@ -1047,24 +1047,29 @@ static int launch_gate_up_wide(const SkinnyArgs &a, hipStream_t s) {
 // it (measured at K = 512: 4.2 us for 32 workgroups, 4.6 us for 256): it is set by the bytes one CU moves from
 // L2 into LDS (about 100 GB/s per CU) plus a fixed cost. 32 x 32 tiles put the decode step's 512 x 512 output on
 // 256 workgroups moving 64 x K x 2 bytes each, against 128 panel workgroups of 32 x 64 moving 96 x K x 2.
-//   * 8 wavefronts, two K halves of 4; each half streams its 32 A and 32 W rows through its own 6-slot ring of
-//     64-wide K stages (8 KB) by direct global->LDS loads (lane l of an instruction lands at slot base + 16 l);
-//   * wave (half h, q) multiplies A block q >> 1 by weight block q & 1 (one 16 x 16 x 32 MFMA tile, C^T
+//   * KSP K slices of 4 wavefronts (the decode step runs KSP = 2); each slice streams its 32 A and 32 W rows
+//     through its own ring of 64-wide K stages (8 KB; 12 / KSP slots) by direct global->LDS loads (lane l of an
+//     instruction lands at slot base + 16 l);
+//   * wave (slice h, q) multiplies A block q >> 1 by weight block q & 1 (one 16 x 16 x 32 MFMA tile, C^T
 //     formulation: the weight fragment is the A operand);
-//   * the halves' tiles meet in LDS and the epilogue adds them in a fixed order (first half + second half).
-constexpr int RS_BM = 32, RS_BN = 32, RS_STAGES = 6;
+//   * the slices' tiles meet in LDS and the epilogue adds them in slice order (with two slices the panel
+//     kernel's K-split sum, bit for bit).
+constexpr int RS_BM = 32, RS_BN = 32;
 constexpr int RS_ROWS = RS_BM + RS_BN;          // LDS rows per ring stage (A rows, then W rows)
 constexpr int RS_STAGEB = RS_ROWS * PG_ROWB;    // 8 KB
 constexpr int RS_LOADS = RS_ROWS / 8 / 4;       // direct loads per wave per stage
-constexpr int RS_RING = RS_STAGES * RS_STAGEB;  // one ring per K half
 constexpr int RS_PITCH = RS_BN + 1;             // fp32 row pitch of a half's tile
-static_assert(2 * RS_BM * RS_PITCH * 4 <= 2 * RS_RING, "both halves' fp32 tiles fit the rings");
+constexpr int RS_SMEM = 12 * RS_STAGEB;         // 96 KB: 12 ring slots in all
+static_assert(4 * RS_BM * RS_PITCH * 4 <= RS_SMEM, "every K slice's fp32 tile fits the rings");
 static_assert(RS_BN == PG_SS_COLS, "one partial sum of squares per tile row");
 
-__global__ __launch_bounds__(512) void resid_gemm_kernel(const SkinnyArgs p, int m_blocks, int tiles) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * RS_RING];
+template <int KSP>
+__global__ __launch_bounds__(256 * KSP) void resid_gemm_kernel(const SkinnyArgs p, int m_blocks, int tiles) {
+  constexpr int RS_STAGES = 12 / KSP;               // slots per ring (one ring per K slice)
+  constexpr int RS_RING = RS_STAGES * RS_STAGEB;
+  __shared__ __attribute__((aligned(16))) char smem[RS_SMEM];
   const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wq = wid & 3, kh = wid >> 2;  // wave within its K half, K half
+  const int wq = wid & 3, kh = wid >> 2;  // wave within its K slice, K slice
   // XCD-aware order (as the panel kernel): workgroup p runs on XCD p % 8, which owns a contiguous range of the
   // n-block-major tiles
   const int pid = blockIdx.x, xcd = pid & 7, idx = pid >> 3;
@@ -1075,7 +1080,7 @@ __global__ __launch_bounds__(512) void resid_gemm_kernel(const SkinnyArgs p, int
   const int n0 = nb * RS_BN;
   // run-time K (a constant trip count lets the compiler unroll the loop, see the ring offsets and drain every
   // load before each LDS read)
-  const int K = p.K, nk = K / (PG_BK * 2), kbase = kh * (K / 2);
+  const int K = p.K, nk = K / (PG_BK * KSP), kbase = kh * (K / KSP);
   const int fr = lane & 15, fg = lane >> 4;
 
   // sources: instruction q = wq + 4 j of a stage covers ring rows 8 q .. 8 q + 7; lane l -> row 8 q + l / 8,
@@ -1148,12 +1153,16 @@ __global__ __launch_bounds__(512) void resid_gemm_kernel(const SkinnyArgs p, int
   lds_barrier();
   if (tid >= 256) return;
 
-  // x = bf16(x + bf16(first half + second half)); the row's sum of squares over the 32 columns from the 8 lanes
+  // x = bf16(x + bf16(sum of the slices' tiles in slice order)); the row's sum of squares over the 32 columns from the 8 lanes
   // of the row (consecutive) in a fixed order
   float o[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
-    o[c] = round_bf(part[rr * RS_PITCH + 4 * sub + c] + part[(RS_BM + rr) * RS_PITCH + 4 * sub + c]);
+  for (int c = 0; c < 4; ++c) {
+    float v = part[rr * RS_PITCH + 4 * sub + c];
+#pragma unroll
+    for (int h = 1; h < KSP; ++h) v += part[(h * RS_BM + rr) * RS_PITCH + 4 * sub + c];
+    o[c] = round_bf(v);
+  }
   o[0] += lo_bf(old[0]);
   o[1] += hi_bf(old[0]);
   o[2] += lo_bf(old[1]);
@@ -1178,7 +1187,10 @@ __global__ __launch_bounds__(512) void resid_gemm_kernel(const SkinnyArgs p, int
 static int launch_resid(const SkinnyArgs &a, hipStream_t s) {
   const int64_t m_blocks = (a.M + RS_BM - 1) / RS_BM;
   const int64_t tiles = m_blocks * ((a.N + RS_BN - 1) / RS_BN);
-  resid_gemm_kernel<<<static_cast<unsigned>(tiles), 512, 0, s>>>(a, static_cast<int>(m_blocks), static_cast<int>(tiles));
+  // two K slices: one slice of 4 wavefronts measured 18% slower at K = 1536 (fewer loads in flight per CU),
+  // four slices no faster in the decode step
+  resid_gemm_kernel<2><<<static_cast<unsigned>(tiles), 512, 0, s>>>(a, static_cast<int>(m_blocks),
+                                                                    static_cast<int>(tiles));
   return VK_OK;
 }
 
