@@ -582,7 +582,7 @@ def _row_ss(x, block=32):
     return (x.double() ** 2).view(M, K // block, block).sum(-1).float()
 
 
-@pytest.mark.parametrize("M", [1, 45, 512])
+@pytest.mark.parametrize("M", [1, 45, 512, 1100])
 @pytest.mark.parametrize("embed", [False, True, "ss"])
 def test_norm_qkv_rope_cache(M, embed):
     use_ss = embed == "ss"

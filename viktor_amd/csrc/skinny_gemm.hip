@@ -19,8 +19,10 @@
 
 namespace vk {
 
-// PRO_NORM_SS: RMSNorm with the row sums of squares handed over by the residual GEMM that produced x
-enum Prologue { PRO_NONE = 0, PRO_NORM = 1, PRO_EMBED_NORM = 2, PRO_NORM_SS = 3 };
+// PRO_NORM_SS: RMSNorm with the row sums of squares handed over by the residual GEMM that produced x.
+// PRO_EMBED_RES: the embedding gather + RMSNorm with the rows resident in LDS (the panel kernel's form of
+// PRO_EMBED_NORM).
+enum Prologue { PRO_NONE = 0, PRO_NORM = 1, PRO_EMBED_NORM = 2, PRO_NORM_SS = 3, PRO_EMBED_RES = 4 };
 enum Epilogue { EPI_BF16 = 0, EPI_F32 = 1, EPI_SWIGLU = 2, EPI_RESID = 3, EPI_ROPE = 4 };
 
 struct SkinnyArgs {
@@ -29,7 +31,7 @@ struct SkinnyArgs {
   int64_t vocab;
   const bf16_t *norm_w;  // PRO_NORM / PRO_EMBED_NORM: RMSNorm weight [K]
   float eps;
-  bf16_t *x_store;       // PRO_EMBED_NORM: gathered rows are stored here (the residual stream) [M, K]
+  bf16_t *x_store;       // PRO_EMBED_NORM / _RES: gathered rows are stored here (the residual stream) [M, K]
   const bf16_t *w;       // weights [N, K] ([2N, K] gate | up for EPI_SWIGLU)
   void *y;               // output [M, N] (EPI_RESID: the residual, updated in place)
   int64_t M;
@@ -438,10 +440,46 @@ __device__ __forceinline__ void pg_normalise_rows(char *tile, const char *nwx, c
   }
 }
 
+// The same normalisation with each row's sum of squares taken from the tile itself (the embedding rows of
+// the first layer have none handed over): a row's 512 squares summed per lane, then across the wave in a
+// fixed butterfly order. With store, the raw rows also go to x_store (the residual stream) first; chunk c of
+// the row sits in slot c ^ (r & 15).
+template <int NR, int RSTEP>
+__device__ __forceinline__ void pg_normalise_rows_own(char *tile, const char *nwx, int wid, int lane, float eps,
+                                                      bf16_t *x_store, int64_t m0, int64_t M, bool store) {
+  u32x4 xr[NR], wr[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int r = wid + RSTEP * i;
+    xr[i] = *reinterpret_cast<const u32x4 *>(tile + r * (PG_NORM_K * 2) + 16 * lane);
+    wr[i] = *reinterpret_cast<const u32x4 *>(nwx + 16 * (lane ^ (r & 15)));
+  }
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int r = wid + RSTEP * i;
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = lo_bf(xr[i][e]), hi = hi_bf(xr[i][e]);
+      ss += lo * lo + hi * hi;
+    }
+    ss = wave_sum(ss);
+    const float rn = rsqrtf(ss * (1.0f / PG_NORM_K) + eps);
+    const int64_t grow = m0 + r;
+    if (store && grow < M)
+      *reinterpret_cast<u32x4 *>(x_store + grow * PG_NORM_K + 8 * (lane ^ (r & 15))) = xr[i];
+    u32x4 xn;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      xn[e] = pack_bf(lo_bf(xr[i][e]) * rn * lo_bf(wr[i][e]), hi_bf(xr[i][e]) * rn * hi_bf(wr[i][e]));
+    *reinterpret_cast<u32x4 *>(tile + r * (PG_NORM_K * 2) + 16 * lane) = xn;
+  }
+}
+
 template <int PRO, int EPI, int KS>
 struct PanelShape {
   static constexpr bool SWI = EPI == EPI_SWIGLU;
-  static constexpr bool XRES = PRO == PRO_NORM_SS;    // A resident in LDS (K = 512), the ring carries W
+  static constexpr bool XRES = PRO == PRO_NORM_SS || PRO == PRO_EMBED_RES;  // A resident in LDS (K = 512)
   static constexpr int WR = SWI ? 2 * PG_BN : PG_BN;  // weight rows per tile
   static constexpr int ROWS = (XRES ? 0 : PG_BM) + WR;  // LDS rows per ring stage
   static constexpr int STAGEB = ROWS * PG_ROWB;
@@ -468,7 +506,7 @@ struct PanelShape {
 // producing residual GEMM left, bf16(x / rms * w) -- and read from there; the ring carries only W.
 template <int PRO, int EPI, int KS>
 __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p, int m_blocks, int tiles) {
-  static_assert(KS == 1 || (KS == 2 && (PRO == PRO_NONE || PRO == PRO_NORM_SS)),
+  static_assert(KS == 1 || (KS == 2 && (PRO == PRO_NONE || PRO == PRO_NORM_SS || PRO == PRO_EMBED_RES)),
                 "K halves only without the pre-pass norm prologue");
   using S = PanelShape<PRO, EPI, KS>;
   static_assert(!S::XRES || S::STAGES - 1 <= PG_NORM_K / PG_BK / KS,
@@ -514,7 +552,7 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
   auto a_row = [&](int r) {
     int64_t row = m0 + r;
     row = row < p.M ? row : p.M - 1;
-    if (PRO == PRO_EMBED_NORM) {
+    if (PRO == PRO_EMBED_NORM || PRO == PRO_EMBED_RES) {
       int64_t t = p.tok[row];
       t = (t < 0 || t >= p.vocab) ? 0 : t;
       return p.a + t * K;
@@ -556,7 +594,7 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
   if constexpr (XRES) {
     pg_issue_row(nwx, p.norm_w + 8 * lane);
 #pragma unroll
-    for (int h = 0; h < PG_BM * PG_SS_N * 4 / 1024; ++h) {
+    for (int h = 0; h < (PRO == PRO_NORM_SS ? PG_BM * PG_SS_N * 4 / 1024 : 0); ++h) {
       int64_t srow = m0 + 16 * h + (lane >> 2);
       srow = srow < p.M ? srow : p.M - 1;
       pg_issue_row(ssx + 1024 * h, reinterpret_cast<const bf16_t *>(p.ss_in + srow * PG_SS_N + 4 * (lane & 3)));
@@ -635,7 +673,10 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    pg_normalise_rows<PG_BM / (4 * KS), 4 * KS>(smem, nwx, ssx, PG_BM, wid, lane, p.eps);
+    if constexpr (PRO == PRO_EMBED_RES)  // the gathered rows' own sums; the nb == 0 tiles keep the raw rows
+      pg_normalise_rows_own<PG_BM / (4 * KS), 4 * KS>(smem, nwx, wid, lane, p.eps, p.x_store, m0, p.M, nb == 0);
+    else
+      pg_normalise_rows<PG_BM / (4 * KS), 4 * KS>(smem, nwx, ssx, PG_BM, wid, lane, p.eps);
     if constexpr (ROPE) {  // read before the barrier below, which retires them: the loop reuses the slot
       const int32_t *ps = reinterpret_cast<const int32_t *>(psx);
       e_pos = ps[rr];
@@ -1210,7 +1251,7 @@ static int launch_panel(const SkinnyArgs &a, hipStream_t s) {
   const int64_t tiles = m_blocks * n_blocks;
   if (tiles >= (int64_t(1) << 31)) return fail(VK_ERR_ARG, "linear: too many tiles");
   // two K slices when the 8-wave workgroups (one per CU: two rings of LDS) still fit in one round
-  constexpr bool can_split = (PRO == PRO_NONE || PRO == PRO_NORM_SS) && EPI != EPI_SWIGLU;
+  constexpr bool can_split = (PRO == PRO_NONE || PRO == PRO_NORM_SS || PRO == PRO_EMBED_RES) && EPI != EPI_SWIGLU;
   if (can_split && a.K % (2 * PG_BK) == 0 && tiles <= device_cus_cached()) {
     panel_gemm_kernel<PRO, EPI, can_split ? 2 : 1><<<static_cast<unsigned>(tiles), 512, 0, s>>>(
         a, static_cast<int>(m_blocks), static_cast<int>(tiles));
@@ -1390,7 +1431,7 @@ extern "C" int vk_norm_qkv_rope_cache(const void *x, const int64_t *tok, int64_t
   } else if (!norm_w)  // x is the normalised activation already
     rc = panel_ok(p, PRO_NONE) ? launch_panel<PRO_NONE, EPI_ROPE>(p, s) : dispatch_k<64, PRO_NONE, EPI_ROPE>(p, s);
   else if (panel_ok(p, PRO_NORM))
-    rc = tok ? launch_panel<PRO_EMBED_NORM, EPI_ROPE>(p, s) : launch_panel<PRO_NORM, EPI_ROPE>(p, s);
+    rc = tok ? launch_panel<PRO_EMBED_RES, EPI_ROPE>(p, s) : launch_panel<PRO_NORM, EPI_ROPE>(p, s);
   else
     rc = tok ? dispatch_k<64, PRO_EMBED_NORM, EPI_ROPE>(p, s) : dispatch_k<64, PRO_NORM, EPI_ROPE>(p, s);
   if (rc != VK_OK) return rc;
