@@ -20,6 +20,24 @@ namespace vk {
 constexpr int SEL_THREADS = 256;
 constexpr int SEL_MAXV = 512;
 
+// Sum over the 64 lanes, every lane receiving it, with no LDS round trip: DPP lane swaps within quads (xor 1,
+// xor 2), the mirrors within 8 and 16 lanes, then gfx950's permlane16 / permlane32 swaps. Each step adds two
+// values that are also added, in the other order, on the partner lane, so all lanes hold the same bits.
+__device__ __forceinline__ float sel_wave_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // half mirror
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));  // row mirror
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(c[0]) + __uint_as_float(c[1]);
+}
+
+// MAXC: 512-wide chunks of the hidden row per lane (d <= 512 MAXC). Every global load the choice needs is
+// issued before the first use of any (the sequence state, the uniform, the hidden slice, the norm weight and
+// the first two LM-head rows of each wave): loads in branches or after a use would each cost a round trip.
+template <int MAXC>
 __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
     const float *__restrict__ logits, const bf16_t *__restrict__ h, const bf16_t *__restrict__ norm_w, float eps,
     const bf16_t *__restrict__ w_head, int d, int round_bf16, const float *__restrict__ bias, const uint8_t *__restrict__ is_tail,
@@ -30,68 +48,95 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
     int32_t *__restrict__ seqlens, int32_t *__restrict__ rpos32, float *__restrict__ logp_out, int64_t logp_stride,
     int V, int eos, int pad) {
   __shared__ float z[SEL_MAXV];
+  __shared__ uint8_t homo_s[SEL_MAXV];
   __shared__ float red_v[SEL_THREADS / 64];
   __shared__ int red_i[SEL_THREADS / 64];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const bool sample = temperature > 0.f;
+
+  // 0. the sequence's state (wave-uniform loads; an optional pointer that is NULL reads pos instead, discarded)
+  const int64_t p = pos[b];
+  const int64_t pl_raw = (plen ? plen : pos)[b];
+  const int64_t prev = tok[b];
+  const int64_t run_raw = (run ? run : pos)[b];
+  const int64_t ro_raw = (rope_off ? rope_off : pos)[b];
+  const int64_t cb_raw = (cache_base ? cache_base : pos)[b];
+  const int64_t pl = plen ? pl_raw : 0;
+  const int64_t ocol = p - pl;
+  const int64_t uc = ocol < 0 ? 0 : (ocol >= u_cols ? u_cols - 1 : ocol);
+  const float u = sample ? uniforms[b * u_stride + uc] : 0.f;
+  const int64_t pv = prev >= 0 && prev < V ? prev : 0;
+  const bool prev_tail = prev >= 0 && prev < V && is_tail[pv] != 0;
 
   // 1. logits (+ bias), fp32
   if (logits != nullptr) {
     for (int v = tid; v < V; v += SEL_THREADS) z[v] = logits[b * V + v] + bias[v];
   } else {
-    // this lane's slice of the hidden row (chunks of 8 at lane * 8 + 512 c), RMSNorm'ed when norm_w is given
-    constexpr int MAXC = 4;
+    // this lane's slice of the hidden row (chunks of 8 at lane * 8 + 512 c; past d: column 0, unused), the norm
+    // weight and this wave's first two LM-head rows (v = wid, wid + 4; past V: row V - 1, unused)
     const bf16_t *hr = h + b * d;
+    const bf16_t *nw = norm_w ? norm_w : hr;
+    const int v0 = wid < V ? wid : V - 1, v1 = wid + 4 < V ? wid + 4 : V - 1;
+    u32x4 hraw[MAXC], nraw[MAXC], w0raw[MAXC], w1raw[MAXC];
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      const int k = lane * 8 + 512 * c, kk = k < d ? k : 0;
+      hraw[c] = *reinterpret_cast<const u32x4 *>(hr + kk);
+      nraw[c] = *reinterpret_cast<const u32x4 *>(nw + kk);
+      w0raw[c] = *reinterpret_cast<const u32x4 *>(w_head + static_cast<int64_t>(v0) * d + kk);
+      w1raw[c] = *reinterpret_cast<const u32x4 *>(w_head + static_cast<int64_t>(v1) * d + kk);
+    }
+    const float b0 = bias[v0], b1 = bias[v1];
     float hv[MAXC][8];
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
-      const int k = lane * 8 + 512 * c;
-      if (k < d) {
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(hr + k);
+      const bool live = lane * 8 + 512 * c < d;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          hv[c][2 * j] = lo_bf(v[j]);
-          hv[c][2 * j + 1] = hi_bf(v[j]);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ss += hv[c][j] * hv[c][j];
+      for (int j = 0; j < 4; ++j) {
+        hv[c][2 * j] = live ? lo_bf(hraw[c][j]) : 0.f;
+        hv[c][2 * j + 1] = live ? hi_bf(hraw[c][j]) : 0.f;
       }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += hv[c][j] * hv[c][j];
     }
     if (norm_w != nullptr) {
-      const float r = rsqrtf(wave_sum(ss) / static_cast<float>(d) + eps);
+      const float r = rsqrtf(sel_wave_sum(ss) / static_cast<float>(d) + eps);
 #pragma unroll
-      for (int c = 0; c < MAXC; ++c) {
-        const int k = lane * 8 + 512 * c;
-        if (k < d) {
-          const u32x4 wv = *reinterpret_cast<const u32x4 *>(norm_w + k);
+      for (int c = 0; c < MAXC; ++c)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            hv[c][2 * j] = round_bf(hv[c][2 * j] * r * lo_bf(wv[j]));
-            hv[c][2 * j + 1] = round_bf(hv[c][2 * j + 1] * r * hi_bf(wv[j]));
-          }
+        for (int j = 0; j < 4; ++j) {
+          hv[c][2 * j] = round_bf(hv[c][2 * j] * r * lo_bf(nraw[c][j]));
+          hv[c][2 * j + 1] = round_bf(hv[c][2 * j + 1] * r * hi_bf(nraw[c][j]));
         }
-      }
     }
-    for (int v = wid; v < V; v += SEL_THREADS / 64) {
-      const bf16_t *wr = w_head + static_cast<int64_t>(v) * d;
+    auto dot = [&](const u32x4 (&wr)[MAXC]) {
       float acc = 0.f;
 #pragma unroll
-      for (int c = 0; c < MAXC; ++c) {
-        const int k = lane * 8 + 512 * c;
-        if (k < d) {
-          const u32x4 wv = *reinterpret_cast<const u32x4 *>(wr + k);
+      for (int c = 0; c < MAXC; ++c)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc += hv[c][2 * j] * lo_bf(wv[j]) + hv[c][2 * j + 1] * hi_bf(wv[j]);
-        }
+        for (int j = 0; j < 4; ++j) acc += hv[c][2 * j] * lo_bf(wr[c][j]) + hv[c][2 * j + 1] * hi_bf(wr[c][j]);
+      return sel_wave_sum(acc);
+    };
+    const float a0 = dot(w0raw), a1 = dot(w1raw);
+    if (lane == 0 && wid < V) z[wid] = (round_bf16 ? round_bf(a0) : a0) + b0;
+    if (lane == 0 && wid + 4 < V) z[wid + 4] = (round_bf16 ? round_bf(a1) : a1) + b1;
+    for (int v = wid + 8; v < V; v += SEL_THREADS / 64) {  // larger vocabularies
+      u32x4 wr[MAXC];
+#pragma unroll
+      for (int c = 0; c < MAXC; ++c) {
+        const int k = lane * 8 + 512 * c, kk = k < d ? k : 0;
+        wr[c] = *reinterpret_cast<const u32x4 *>(w_head + static_cast<int64_t>(v) * d + kk);
       }
-      acc = wave_sum(acc);
+      const float acc = dot(wr);
       if (lane == 0) z[v] = (round_bf16 ? round_bf(acc) : acc) + bias[v];
     }
   }
+  if (homo_stop > 0)
+    for (int v = tid; v < V; v += SEL_THREADS) homo_s[v] = is_homo[v];
   __syncthreads();
 
-  const bool sample = temperature > 0.f;
   if (sample)
     for (int v = tid; v < V; v += SEL_THREADS) z[v] = z[v] / temperature;
   __syncthreads();
@@ -137,12 +182,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
   if (sample || logp_out) {
     for (int v = 0; v < V; ++v) sum += expf(z[v] - zmax);
   }
-  const int64_t p = pos[b];
-  const int64_t pl = plen ? plen[b] : 0;
-  const int64_t ocol = p - pl;
   if (sample) {
-    int64_t uc = ocol < 0 ? 0 : (ocol >= u_cols ? u_cols - 1 : ocol);
-    const float u = uniforms[b * u_stride + uc];
     const float inv = 1.0f / sum;
     float cdf = 0.f;
     int64_t pick = -1, last_pos = bi;
@@ -161,11 +201,10 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
   }
 
   // 4. grammar and bookkeeping
-  const int64_t prev = tok[b];
-  if (prev >= 0 && prev < V && is_tail[prev]) nxt = eos;
+  if (prev_tail) nxt = eos;
   if (homo_stop > 0) {
-    const bool same = nxt == prev && nxt >= 0 && nxt < V && is_homo[nxt];
-    const int64_t r = same ? run[b] + 1 : 0;
+    const bool same = nxt == prev && nxt >= 0 && nxt < V && homo_s[nxt];
+    const int64_t r = same ? run_raw + 1 : 0;
     run[b] = r;
     if (r + 1 >= homo_stop) nxt = eos;
   }
@@ -175,10 +214,10 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
   const int64_t np = p + 1;
   pos[b] = np;
   // cache_base: the KV-cache row of position p is p - cache_base[b] (a per-sequence suffix cache)
-  const int64_t cp = np - (cache_base ? cache_base[b] : 0);
+  const int64_t cp = np - (cache_base ? cb_raw : 0);
   if (pos32) pos32[b] = static_cast<int32_t>(cp);
   if (seqlens) seqlens[b] = static_cast<int32_t>(cp + 1);
-  if (rpos32) rpos32[b] = static_cast<int32_t>(np + (rope_off ? rope_off[b] : 0));
+  if (rpos32) rpos32[b] = static_cast<int32_t>(np + (rope_off ? ro_raw : 0));
 }
 
 }  // namespace vk
@@ -206,7 +245,8 @@ extern "C" int vk_select_update(const float *logits, const void *h, const void *
   VK_CHECK_ARG(out_cols > 0, "select_update: empty output buffer");
   VK_CHECK_ARG(logp_stride == 0 || logp_stride >= out_cols, "select_update: logp_stride must be 0 or >= out_cols");
   if (B == 0) return VK_OK;
-  select_update_kernel<<<static_cast<unsigned>(B), SEL_THREADS, 0, VK_STREAM(stream)>>>(
+  auto kern = (logits != nullptr || d <= 512) ? select_update_kernel<1> : select_update_kernel<4>;
+  kern<<<static_cast<unsigned>(B), SEL_THREADS, 0, VK_STREAM(stream)>>>(
       logits, static_cast<const bf16_t *>(h), static_cast<const bf16_t *>(norm_w), eps,
       static_cast<const bf16_t *>(w_head), d, round_bf16, bias, is_tail,
       is_homo, homo_stop, temperature, uniforms, u_stride, u_cols, tok, run, pos, plen, rope_off, cache_base, out,
