@@ -29,8 +29,6 @@ constexpr int PA_Q = 64;      // query rows per workgroup (plan granularity)
 constexpr int PA_WAVES = 8;   // 4 query heads x 2 halves of 32 rows
 constexpr int PA_KT = 64;     // keys per LDS tile
 constexpr int PA_PITCH = 72;  // 64 + 8 bf16
-typedef short pa_s4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) pa_s4 pa_lds_s4;
 constexpr float PA_SLACK = 8.0f;  // log2 units a row's score may pass its reference max before it moves
 
 __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
@@ -133,8 +131,8 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
       // positive scale); the mask is a compare per score under one wave-uniform branch (a short-circuit test
       // per score compiles to a divergent branch per score)
       bf16x8 pf[2];
-      float alpha_q[2];
-      bool grew = false;
+      float m_old[2], ps_q[2];
+      bool moved_q[2], grew = false;
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         float sv[8];
@@ -160,39 +158,39 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
         const bool moved = mx > m_run[qb] + slack_raw;
         const float m_ref = moved ? mx : m_run[qb];
         const float nmc = -m_ref * scale_log2;
-        float e[8], ps = 0.f;
+        float e[8];
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          e[jj] = __builtin_amdgcn_exp2f(fmaf(sv[jj], scale_log2, nmc));
-          ps += e[jj];
-        }
+        for (int jj = 0; jj < 8; ++jj) e[jj] = __builtin_amdgcn_exp2f(fmaf(sv[jj], scale_log2, nmc));
+        float ps = e[0];
+#pragma unroll
+        for (int jj = 1; jj < 8; ++jj) ps += e[jj];
         pf[qb] = __builtin_bit_cast(bf16x8, u32x4{pack_bf(e[0], e[1]), pack_bf(e[2], e[3]), pack_bf(e[4], e[5]),
                                                    pack_bf(e[6], e[7])});
-        const float alpha = moved ? __builtin_amdgcn_exp2f((m_run[qb] - m_ref) * scale_log2) : 1.0f;
-        alpha_q[qb] = alpha;
+        m_old[qb] = m_run[qb];
+        moved_q[qb] = moved;
+        ps_q[qb] = ps;
         grew |= moved;
-        l_run[qb] = l_run[qb] * alpha + ps;
         m_run[qb] = m_ref;
       }
+      // the rescale (its two exponentials included) only when some row of the wave moved its reference max
       if (__builtin_amdgcn_ballot_w64(grew) != 0) {
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < 2; ++qb) {
+          const float alpha = moved_q[qb] ? __builtin_amdgcn_exp2f((m_old[qb] - m_run[qb]) * scale_log2) : 1.0f;
+          l_run[qb] *= alpha;
 #pragma unroll
-          for (int dt = 0; dt < 4; ++dt) acc[dt][qb] *= alpha_q[qb];
+          for (int dt = 0; dt < 4; ++dt) acc[dt][qb] *= alpha;
+        }
       }
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) l_run[qb] += ps_q[qb];
       // O^T += V^T P^T (key order {4g..4g+3, 16+4g..16+4g+3} in both operands). The V^T operand comes from
       // the row-major V tile through gfx950's transpose read ds_read_b64_tr_b16: in each 16-lane group, source
       // lane s reads 4 consecutive d of key row R0 + s / 4 and output lane j receives d = 16 dt + j at keys
       // R0 .. R0 + 3; two reads (R0 = 4 g and 16 + 4 g) give the lane's 8 keys.
-      const int tr_row = 4 * g + (col >> 2), tr_d = 4 * (col & 3);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const pa_s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (pa_lds_s4 *)(const __attribute__((address_space(3))) bf16_t *)(vt + tr_row * PA_PITCH + 16 * dt + tr_d));
-        const pa_s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((pa_lds_s4 *)(
-            const __attribute__((address_space(3))) bf16_t *)(vt + (16 + tr_row) * PA_PITCH + 16 * dt + tr_d));
-        typedef short s8 __attribute__((ext_vector_type(8)));
-        const bf16x8 va = __builtin_bit_cast(bf16x8, s8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+        const bf16x8 va = lds_tr_frag<PA_PITCH>(vt, 0, 16 * dt, lane);
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) acc[dt][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[qb], acc[dt][qb], 0, 0, 0);
       }
