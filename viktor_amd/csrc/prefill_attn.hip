@@ -148,15 +148,21 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
             for (int i = 0; i < 4; ++i)
               sv[kb * 4 + i] = kbase + 16 * kb + 4 * g + i <= hi_k ? sv[kb * 4 + i] : -INFINITY;
         }
-        float mx = vmax3(vmax3(sv[0], sv[1], sv[2]), vmax3(sv[3], sv[4], sv[5]), vmax3(sv[6], sv[7], sv[7]));
-        mx = max_lane_groups(mx);
         // The row's reference max moves only when a score passes it by more than PA_SLACK in log2 units of the
         // scaled scores: the probabilities are then exp2(s c - m c) <= 2^PA_SLACK (bf16 and the fp32 sums carry
         // them with the same relative precision as values <= 1), and the rescale of the row's sum and output
         // (a multiply per accumulator) is rare after the first tiles. m_run = -inf before the first key: any
         // finite score moves it. Tile 0 holds key 0, visible to every query, so m_run is finite after it.
-        const bool moved = mx > m_run[qb] + slack_raw;
-        const float m_ref = moved ? mx : m_run[qb];
+        // The row's max over its 4 lanes is needed only when some lane's own max passes the slack, so the lane
+        // swaps run under a wave-uniform test that is rarely true after the first tiles.
+        const float mx_lane = vmax3(vmax3(sv[0], sv[1], sv[2]), vmax3(sv[3], sv[4], sv[5]), vmax3(sv[6], sv[7], sv[7]));
+        bool moved = false;
+        float m_ref = m_run[qb];
+        if (__builtin_amdgcn_ballot_w64(mx_lane > m_run[qb] + slack_raw) != 0) {
+          const float mx = max_lane_groups(mx_lane);
+          moved = mx > m_run[qb] + slack_raw;
+          m_ref = moved ? mx : m_run[qb];
+        }
         const float nmc = -m_ref * scale_log2;
         float e[8];
 #pragma unroll
