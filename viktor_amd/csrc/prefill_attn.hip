@@ -141,12 +141,13 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) sv[kb * 4 + i] = st[kb][qb][i];
         if (need_mask) {
-          const int hi_k = causal ? min(qpos[qb], klen - 1) : klen - 1;  // last key this row sees
+          // last key this row sees, relative to this lane's first key (key kbase + 4 g): one subtraction,
+          // then compares against constants
+          const int lim = (causal ? min(qpos[qb], klen - 1) : klen - 1) - kbase - 4 * g;
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              sv[kb * 4 + i] = kbase + 16 * kb + 4 * g + i <= hi_k ? sv[kb * 4 + i] : -INFINITY;
+            for (int i = 0; i < 4; ++i) sv[kb * 4 + i] = 16 * kb + i <= lim ? sv[kb * 4 + i] : -INFINITY;
         }
         // The row's reference max moves only when a score passes it by more than PA_SLACK in log2 units of the
         // scaled scores: the probabilities are then exp2(s c - m c) <= 2^PA_SLACK (bf16 and the fp32 sums carry
