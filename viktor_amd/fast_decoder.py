@@ -219,7 +219,7 @@ class FastDecoder:
         norm_qkv_rope_cache (attn norm + qkv GEMM + QK-norm + RoPE + cache write; in layer 0 with the
         token-embedding gather in its prologue), decode_attention, linear_residual
         (o proj + residual add), norm_linear (mlp norm + gate_up + SwiGLU), linear_residual (down proj +
-        residual add). The residual GEMMs leave the row sums of squares of x (per 64-column block), so the
+        residual add). The residual GEMMs leave the row sums of squares of x (per 32-column block), so the
         norms inside the next GEMMs need no pass of their own over x.
         Returns the residual stream [B, d] after the last layer (x, updated in place, when given); the
         final RMSNorm is left to the consumer (the LM-head kernel applies it).
