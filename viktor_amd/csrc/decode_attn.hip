@@ -292,11 +292,67 @@ static int64_t workspace_bytes_for(int64_t B, const DecodeSplit &sp) {
 // output itself. With msplit > 1 the subgroups of one prefix group read the same prefix rows, launched
 // next to each other on one XCD, so the second read comes from its L2.
 
-// resident workgroups per CU the part count aims for, per wave count (LDS of the epilogue merge grows
-// with the 4 G columns; registers with the column blocks)
-constexpr int gu_wg_per_cu(int waves) { return waves >= 8 ? 1 : 4; }
+// resident workgroups per CU the part count aims for, per wave count (each wave's K / V ring takes 16 KB of
+// LDS)
+constexpr int gu_wg_per_cu(int waves) { return waves >= 8 ? 1 : 2; }
 constexpr int GU_TILE = 32;
-constexpr int GU_PITCH = 72;  // one KV head: 64 + 8 pad
+// Each wave streams its K / V tiles through a ring of two LDS stages (K tile 4 KB, V tile 4 KB) by direct
+// global->LDS loads. A tile row (one KV head: 64 bf16 = 128 B) keeps its 16-byte chunk c in slot c ^ swz(row),
+// which spreads the 16 rows of an MFMA fragment read over all bank groups.
+constexpr int GU_TILEB = GU_TILE * 128;   // 4 KB
+constexpr int GU_STAGEB = 2 * GU_TILEB;   // K + V
+constexpr int GU_WAVEB = 2 * GU_STAGEB;   // two stages per wave
+__device__ __forceinline__ int gu_swz(int row) { return (row >> 1) & 7; }
+// s_waitcnt immediate: vmcnt <= n, expcnt / lgkmcnt unconstrained
+constexpr int gu_vmcnt(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | (((n >> 4) & 3) << 14); }
+typedef __attribute__((address_space(3))) void gu_lds_void_t;
+// one 32-row tile of K or V (rows row0 .. row0 + 31 of base, clamped to clamp - 1) into dst: 4 direct loads,
+// instruction j -> rows 8 j .. 8 j + 7, lane l -> row 8 j + l / 8, LDS slot l % 8 holding chunk (l % 8) ^ swz(row)
+__device__ __forceinline__ void gu_issue_tile(char *dst, const bf16_t *base, int64_t stride, int row0, int clamp,
+                                              int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 8 * j + (lane >> 3);
+    int rr = row0 + r;
+    rr = rr < clamp ? rr : clamp - 1;
+    const int gc = (lane & 7) ^ gu_swz(r);
+    __builtin_amdgcn_global_load_lds(base + static_cast<int64_t>(rr) * stride + 8 * gc,
+                                     (gu_lds_void_t *)(dst + 1024 * j), 16, 0, 0);
+  }
+}
+// The four transposed V fragments of lds_tr_frag (dt = 0..3: column 16 dt + lane % 16 at rows 4 g .. + 3 and
+// 16 + 4 g .. + 3) from a swizzled tile: eight ds_read_b64_tr_b16 in one asm statement that also waits for them.
+// (Written as the builtin, each transpose read makes the compiler first wait for every outstanding direct
+// global->LDS load, which would drain the ring's prefetch.)
+__device__ __forceinline__ void gu_tr_frags(const char *tile, int lane, bf16x8 (&va)[4]) {
+  const int g = lane >> 4, s = lane & 15;
+  const int r = 4 * g + (s >> 2), h = (s & 3) >> 1, half = 8 * (s & 1);
+  unsigned a[8];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    a[2 * dt] = static_cast<unsigned>(reinterpret_cast<uintptr_t>(tile + r * 128 + 16 * ((2 * dt + h) ^ gu_swz(r)) + half));
+    a[2 * dt + 1] = static_cast<unsigned>(
+        reinterpret_cast<uintptr_t>(tile + (r + 16) * 128 + 16 * ((2 * dt + h) ^ gu_swz(r + 16)) + half));
+  }
+  s16x4_t v[8];
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8\n\t"
+      "ds_read_b64_tr_b16 %1, %9\n\t"
+      "ds_read_b64_tr_b16 %2, %10\n\t"
+      "ds_read_b64_tr_b16 %3, %11\n\t"
+      "ds_read_b64_tr_b16 %4, %12\n\t"
+      "ds_read_b64_tr_b16 %5, %13\n\t"
+      "ds_read_b64_tr_b16 %6, %14\n\t"
+      "ds_read_b64_tr_b16 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7])
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]));
+  typedef short s16x8_t __attribute__((ext_vector_type(8)));
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+    va[dt] = __builtin_bit_cast(bf16x8, s16x8_t{v[2 * dt][0], v[2 * dt][1], v[2 * dt][2], v[2 * dt][3],
+                                                v[2 * dt + 1][0], v[2 * dt + 1][1], v[2 * dt + 1][2], v[2 * dt + 1][3]});
+}
 
 template <int G, int GU_WAVES>
 __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
@@ -307,7 +363,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     float *__restrict__ ws_ml, bf16_t *__restrict__ out, float scale_log2) {
   constexpr int NC = 4 * G;            // query columns of one KV head (G members x 4 heads)
   constexpr int NCB = (NC + 15) / 16;  // 16-column MFMA blocks
-  constexpr int LDS_V = GU_WAVES * GU_TILE * GU_PITCH * 2;
+  constexpr int LDS_V = GU_WAVES * GU_WAVEB;
   constexpr int LDS_M = (GU_WAVES * NC * 64 + 2 * GU_WAVES * NC) * 4;
   __shared__ __attribute__((aligned(16))) char smem[LDS_V > LDS_M ? LDS_V : LDS_M];
 
@@ -336,18 +392,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     int64_t stride;
     int row0, len, clamp, seg, mc;  // seg: 0 = prefix, 1 + m = member m's own rows; mc: member cursor
   };
-  auto row_off = [&](const TileRef &r, int pb) {
-    int rr = r.row0 + 16 * pb + col;
-    rr = rr < r.clamp ? rr : r.clamp - 1;
-    return static_cast<int64_t>(rr) * r.stride + 8 * g;
-  };
-  u32x4 kf[2][2], vf[2][2];
-  auto load = [&](u32x4 (&f)[2][2], const bf16_t *base, const TileRef &r) {
-#pragma unroll
-    for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-      for (int c = 0; c < 2; ++c) f[pb][c] = *reinterpret_cast<const u32x4 *>(base + row_off(r, pb) + 32 * c);
-  };
+  char *const wring = smem + wid * GU_WAVEB;  // this wave's two stages
   // the first tile is a prefix tile whenever wid < npre: its loads need no length (rows clamped to pre_max - 1,
   // always valid; its mask waits for the length)
   TileRef cur;
@@ -389,13 +434,10 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     const int64_t l = pre_len[pp];
     len = static_cast<int>(l < 1 ? 1 : (l > pre_max ? pre_max : l));
   }
-  // The first tile's K / V go out after the query and length loads. Those are consumed before the loop, so with
-  // them older than K / V the compiler's counted waits at the loop head are for K alone, V staying in flight; the
-  // other order (K / V first) made every iteration wait for all loads, as if q were still outstanding.
+  // The first tile's K / V go out right after the query and length loads, before the lengths are known.
   if (spec) {
-    load(kf, cur.k, cur);
-    asm volatile("" ::: "memory");
-    load(vf, cur.v, cur);
+    gu_issue_tile(wring, cur.k, cur.stride, cur.row0, cur.clamp, lane);
+    gu_issue_tile(wring + GU_TILEB, cur.v, cur.stride, cur.row0, cur.clamp, lane);
   }
   int incl = cnt;
 #pragma unroll
@@ -416,7 +458,6 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     m_run[cb] = -INFINITY;
     l_run[cb] = 0.f;
   }
-  bf16_t *vsh = reinterpret_cast<bf16_t *>(smem) + wid * GU_TILE * GU_PITCH;
 
   // local tile t -> prefix tile pt0 + t (t < npre) or own-row tile ou0 + t - npre (member found by a
   // monotone search from the cursor), first row, lengths, row pointers
@@ -447,24 +488,40 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     return r;
   };
 
-  // This wave's tiles are t0 = wid, wid + W, ... (< T). The next tile's K / V are loaded while the current
-  // one is consumed; at the end the current tile is loaded again, so every load is unconditional.
+  // This wave's tiles are t0 = wid, wid + W, ... (< T), two ahead in its LDS ring: tile t + 2W's K goes into
+  // the stage of tile t once t's scores are formed, its V once t's V has been read. Past the end the current
+  // tile is loaded again (into a stage no later iteration reads), so the loads per iteration and the counted
+  // waits never change: at each wait 12 younger loads (one tile's V and two tiles' K / V) may stay in flight.
   const int t0 = wid, t_end = T;
   if (t0 < t_end) {
     if (spec) {
       cur.len = __builtin_amdgcn_readlane(len, G);
     } else {
       cur = locate(t0, 0);
-      load(kf, cur.k, cur);
-      asm volatile("" ::: "memory");
-      load(vf, cur.v, cur);
+      gu_issue_tile(wring, cur.k, cur.stride, cur.row0, cur.clamp, lane);
+      gu_issue_tile(wring + GU_TILEB, cur.v, cur.stride, cur.row0, cur.clamp, lane);
     }
+    TileRef nxt = t0 + GU_WAVES < t_end ? locate(t0 + GU_WAVES, cur.mc) : cur;
+    gu_issue_tile(wring + GU_STAGEB, nxt.k, nxt.stride, nxt.row0, nxt.clamp, lane);
+    gu_issue_tile(wring + GU_STAGEB + GU_TILEB, nxt.v, nxt.stride, nxt.row0, nxt.clamp, lane);
+    // (the compiler waits for every outstanding load before the loop, the first two tiles included: the loop uses
+    // the query fragments loaded before it and its own loads return no registers)
+    int stage = 0;
     for (int t = t0; t < t_end; t += GU_WAVES) {
-      const int tn = t + GU_WAVES < t_end ? t + GU_WAVES : t;
-      const TileRef nxt = locate(tn, cur.mc);
+      const TileRef nn = t + 2 * GU_WAVES < t_end ? locate(t + 2 * GU_WAVES, nxt.mc) : cur;
+      char *const kst = wring + stage * GU_STAGEB, *const vst = kst + GU_TILEB;
       const int member = cur.seg - 1;  // -1: prefix tile, every column attends
       // an own-row tile feeds only its member's 4 columns: the other column blocks are skipped (wave-uniform)
       const int cb_only = member < 0 ? -1 : (4 * member) >> 4;
+      __builtin_amdgcn_s_waitcnt(gu_vmcnt(12));  // this tile's K has landed
+      u32x4 kf[2][2];
+#pragma unroll
+      for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int R = 16 * pb + col;
+          kf[pb][c] = *reinterpret_cast<const u32x4 *>(kst + R * 128 + 16 * ((4 * c + g) ^ gu_swz(R)));
+        }
       f32x4 st[2][NCB];
 #pragma unroll
       for (int pb = 0; pb < 2; ++pb)
@@ -477,7 +534,8 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
             st[pb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[pb][c]), bq[cb][c],
                                                                  st[pb][cb], 0, 0, 0);
         }
-      load(kf, nxt.k, nxt);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // the K reads are done: the stage's K tile may be overwritten
+      gu_issue_tile(kst, nn.k, nn.stride, nn.row0, nn.clamp, lane);
       // a prefix tile inside the prefix needs no mask (the common case: a uniform branch)
       const bool full = member < 0 && cur.row0 + GU_TILE <= cur.len;
       bf16x8 pf[NCB];
@@ -526,25 +584,22 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
         l_run[cb] += ps;
         m_run[cb] = m_new;
       }
-#pragma unroll
-      for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-          *reinterpret_cast<u32x4 *>(&vsh[(16 * pb + col) * GU_PITCH + 32 * c + 8 * g]) = vf[pb][c];
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      load(vf, nxt.v, nxt);
+      __builtin_amdgcn_s_waitcnt(gu_vmcnt(12));  // this tile's V has landed
+      bf16x8 va[4];
+      gu_tr_frags(vst, lane, va);  // (waits for its reads: the stage's V tile may then be overwritten)
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        // V^T fragment: column 16 dt + col at tile rows 4 g .. + 3 and 16 + 4 g .. + 3, by transpose reads
-        const bf16x8 va = lds_tr_frag<GU_PITCH>(vsh, 0, 16 * dt, lane);
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb)
           if (NCB == 1 || cb_only < 0 || cb == cb_only)
-            acc[cb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[cb], acc[cb][dt], 0, 0, 0);
+            acc[cb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], pf[cb], acc[cb][dt], 0, 0, 0);
       }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      gu_issue_tile(vst, nn.v, nn.stride, nn.row0, nn.clamp, lane);
       cur = nxt;
+      nxt = nn;
+      stage ^= 1;
     }
+    __builtin_amdgcn_s_waitcnt(gu_vmcnt(0));  // the ring's last loads, before its LDS is reused below
   }
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
