@@ -489,9 +489,9 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   };
 
   // This wave's tiles are t0 = wid, wid + W, ... (< T), two ahead in its LDS ring: tile t + 2W's K goes into
-  // the stage of tile t once t's scores are formed, its V once t's V has been read. Past the end the current
-  // tile is loaded again (into a stage no later iteration reads), so the loads per iteration and the counted
-  // waits never change: at each wait 12 younger loads (one tile's V and two tiles' K / V) may stay in flight.
+  // the stage of tile t once t's scores are formed, its V once t's V has been read. Each wait counts this
+  // wave's loads issued after the ones it needs (4 per K or V tile): before the scores, t's V and tile t + W's
+  // K / V; before P V, tile t + W's K / V and t + 2W's K, each while that tile exists.
   const int t0 = wid, t_end = T;
   if (t0 < t_end) {
     if (spec) {
@@ -501,19 +501,26 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
       gu_issue_tile(wring, cur.k, cur.stride, cur.row0, cur.clamp, lane);
       gu_issue_tile(wring + GU_TILEB, cur.v, cur.stride, cur.row0, cur.clamp, lane);
     }
-    TileRef nxt = t0 + GU_WAVES < t_end ? locate(t0 + GU_WAVES, cur.mc) : cur;
-    gu_issue_tile(wring + GU_STAGEB, nxt.k, nxt.stride, nxt.row0, nxt.clamp, lane);
-    gu_issue_tile(wring + GU_STAGEB + GU_TILEB, nxt.v, nxt.stride, nxt.row0, nxt.clamp, lane);
+    TileRef nxt = cur;
+    if (t0 + GU_WAVES < t_end) {
+      nxt = locate(t0 + GU_WAVES, cur.mc);
+      gu_issue_tile(wring + GU_STAGEB, nxt.k, nxt.stride, nxt.row0, nxt.clamp, lane);
+      gu_issue_tile(wring + GU_STAGEB + GU_TILEB, nxt.v, nxt.stride, nxt.row0, nxt.clamp, lane);
+    }
     // (the compiler waits for every outstanding load before the loop, the first two tiles included: the loop uses
     // the query fragments loaded before it and its own loads return no registers)
     int stage = 0;
     for (int t = t0; t < t_end; t += GU_WAVES) {
-      const TileRef nn = t + 2 * GU_WAVES < t_end ? locate(t + 2 * GU_WAVES, nxt.mc) : cur;
+      const bool has1 = t + GU_WAVES < t_end, has2 = t + 2 * GU_WAVES < t_end;
+      const TileRef nn = has2 ? locate(t + 2 * GU_WAVES, nxt.mc) : cur;
       char *const kst = wring + stage * GU_STAGEB, *const vst = kst + GU_TILEB;
       const int member = cur.seg - 1;  // -1: prefix tile, every column attends
       // an own-row tile feeds only its member's 4 columns: the other column blocks are skipped (wave-uniform)
       const int cb_only = member < 0 ? -1 : (4 * member) >> 4;
-      __builtin_amdgcn_s_waitcnt(gu_vmcnt(12));  // this tile's K has landed
+      if (has1)  // this tile's K has landed
+        __builtin_amdgcn_s_waitcnt(gu_vmcnt(12));
+      else
+        __builtin_amdgcn_s_waitcnt(gu_vmcnt(4));
       u32x4 kf[2][2];
 #pragma unroll
       for (int pb = 0; pb < 2; ++pb)
@@ -535,7 +542,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
                                                                  st[pb][cb], 0, 0, 0);
         }
       __builtin_amdgcn_s_waitcnt(0xC07F);  // the K reads are done: the stage's K tile may be overwritten
-      gu_issue_tile(kst, nn.k, nn.stride, nn.row0, nn.clamp, lane);
+      if (has2) gu_issue_tile(kst, nn.k, nn.stride, nn.row0, nn.clamp, lane);
       // a prefix tile inside the prefix needs no mask (the common case: a uniform branch)
       const bool full = member < 0 && cur.row0 + GU_TILE <= cur.len;
       bf16x8 pf[NCB];
@@ -584,7 +591,12 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
         l_run[cb] += ps;
         m_run[cb] = m_new;
       }
-      __builtin_amdgcn_s_waitcnt(gu_vmcnt(12));  // this tile's V has landed
+      if (has2)  // this tile's V has landed
+        __builtin_amdgcn_s_waitcnt(gu_vmcnt(12));
+      else if (has1)
+        __builtin_amdgcn_s_waitcnt(gu_vmcnt(8));
+      else
+        __builtin_amdgcn_s_waitcnt(gu_vmcnt(0));
       bf16x8 va[4];
       gu_tr_frags(vst, lane, va);  // (waits for its reads: the stage's V tile may then be overwritten)
 #pragma unroll
@@ -594,7 +606,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
           if (NCB == 1 || cb_only < 0 || cb == cb_only)
             acc[cb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], pf[cb], acc[cb][dt], 0, 0, 0);
       }
-      gu_issue_tile(vst, nn.v, nn.stride, nn.row0, nn.clamp, lane);
+      if (has2) gu_issue_tile(vst, nn.v, nn.stride, nn.row0, nn.clamp, lane);
       cur = nxt;
       nxt = nn;
       stage ^= 1;
