@@ -108,12 +108,65 @@ static int launch_rows(bf16_t *x, const bf16_t *delta, const int64_t *tok, const
 }
 
 // h = bf16(x * rsqrt(sum(ss[row]) / d + eps) * w) with the row's sum of squares handed over in nb block partials
-// (ss [n, nb] fp32, summed in block order); one wavefront per row, 8 columns per lane (d <= 512 * 8 / 8).
-// h may be x (each lane rewrites the chunk it read).
+// (ss [n, nb] fp32, summed in block order); 8 columns per lane. h may be x (each lane rewrites the chunk it read).
+// d = 512 (one 16-byte chunk per lane per row): a wavefront takes RN_ROWS rows and issues all their loads before
+// the first use, so 4 KB per wavefront are in flight rather than one row's 1 KB (the kernel streams 2 x n x 1 KB
+// and, with one row per wavefront, was bound by the loads in flight at about 4.3 TB/s). Other d: one row per
+// wavefront.
+constexpr int RN_ROWS = 4;
 __global__ __launch_bounds__(256) void rmsnorm_apply_ss_kernel(const bf16_t *x, const float *__restrict__ ss, int nb,
                                                                const bf16_t *__restrict__ w, bf16_t *h, int64_t n,
-                                                               int d, float eps) {
+                                                               int d, float eps, bool vec_ss) {
   const int lane = threadIdx.x & 63;
+  if (d == 512) {
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * RN_ROWS;
+    if (row0 >= n) return;
+    u32x4 xv[RN_ROWS];
+#pragma unroll
+    for (int i = 0; i < RN_ROWS; ++i) {
+      const int64_t row = row0 + i < n ? row0 + i : n - 1;
+      xv[i] = *reinterpret_cast<const u32x4 *>(x + row * 512 + lane * 8);
+    }
+    const u32x4 wv = *reinterpret_cast<const u32x4 *>(w + lane * 8);
+    float r[RN_ROWS];
+    if (vec_ss) {  // nb % 4 == 0, nb <= 16, ss 16-byte aligned: the partials as 16-byte loads, all issued before the
+                   // sums (block order kept)
+      f32x4 sv[RN_ROWS][4];
+#pragma unroll
+      for (int i = 0; i < RN_ROWS; ++i) {
+        const int64_t row = row0 + i < n ? row0 + i : n - 1;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (4 * q < nb) sv[i][q] = *reinterpret_cast<const f32x4 *>(ss + row * nb + 4 * q);
+      }
+#pragma unroll
+      for (int i = 0; i < RN_ROWS; ++i) {
+        float tot = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (4 * q < nb) tot = (((tot + sv[i][q][0]) + sv[i][q][1]) + sv[i][q][2]) + sv[i][q][3];
+        r[i] = rsqrtf(tot / static_cast<float>(d) + eps);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < RN_ROWS; ++i) {
+        const int64_t row = row0 + i < n ? row0 + i : n - 1;
+        float tot = 0.f;
+        for (int b = 0; b < nb; ++b) tot += ss[row * nb + b];
+        r[i] = rsqrtf(tot / static_cast<float>(d) + eps);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RN_ROWS; ++i) {
+      if (row0 + i >= n) break;
+      u32x4 o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        o[k] = pack_bf(lo_bf(xv[i][k]) * r[i] * lo_bf(wv[k]), hi_bf(xv[i][k]) * r[i] * hi_bf(wv[k]));
+      *reinterpret_cast<u32x4 *>(h + (row0 + i) * 512 + lane * 8) = o;
+    }
+    return;
+  }
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= n) return;
   float tot = 0.f;
@@ -171,8 +224,10 @@ extern "C" int vk_rmsnorm_apply_ss(const void *x, const float *ss, int32_t nb, c
   VK_CHECK_ARG(n >= 0 && d > 0 && d % 8 == 0 && nb > 0, "rmsnorm_apply_ss: bad sizes (d=%d nb=%d)", d, nb);
   VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w) && vk_aligned16(h), "rmsnorm_apply_ss: pointers must be 16-byte aligned");
   if (n == 0) return VK_OK;
-  rmsnorm_apply_ss_kernel<<<static_cast<unsigned>((n + 3) / 4), 256, 0, VK_STREAM(stream)>>>(
-      static_cast<const bf16_t *>(x), ss, nb, static_cast<const bf16_t *>(w), static_cast<bf16_t *>(h), n, d, eps);
+  const int64_t waves = d == 512 ? (n + RN_ROWS - 1) / RN_ROWS : n;
+  rmsnorm_apply_ss_kernel<<<static_cast<unsigned>((waves + 3) / 4), 256, 0, VK_STREAM(stream)>>>(
+      static_cast<const bf16_t *>(x), ss, nb, static_cast<const bf16_t *>(w), static_cast<bf16_t *>(h), n, d, eps,
+      nb % 4 == 0 && nb <= 16 && vk_aligned16(ss));
   return launch_status("rmsnorm_apply_ss");
 }
 
