@@ -48,12 +48,14 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
     int32_t *__restrict__ seqlens, int32_t *__restrict__ rpos32, float *__restrict__ logp_out, int64_t logp_stride,
     int V, int eos, int pad) {
   __shared__ float z[SEL_MAXV];
+  __shared__ float ez[SEL_MAXV];
   __shared__ uint8_t homo_s[SEL_MAXV];
   __shared__ float red_v[SEL_THREADS / 64];
   __shared__ int red_i[SEL_THREADS / 64];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const bool sample = temperature > 0.f;
+  const float tdiv = sample ? temperature : 1.f;  // z / 1 is z: one expression for both modes
 
   // 0. the sequence's state (wave-uniform loads; an optional pointer that is NULL reads pos instead, discarded)
   const int64_t p = pos[b];
@@ -71,7 +73,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
 
   // 1. logits (+ bias), fp32
   if (logits != nullptr) {
-    for (int v = tid; v < V; v += SEL_THREADS) z[v] = logits[b * V + v] + bias[v];
+    for (int v = tid; v < V; v += SEL_THREADS) z[v] = (logits[b * V + v] + bias[v]) / tdiv;
   } else {
     // this lane's slice of the hidden row (chunks of 8 at lane * 8 + 512 c; past d: column 0, unused), the norm
     // weight and this wave's first two LM-head rows (v = wid, wid + 4; past V: row V - 1, unused)
@@ -120,8 +122,8 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
       return sel_wave_sum(acc);
     };
     const float a0 = dot(w0raw), a1 = dot(w1raw);
-    if (lane == 0 && wid < V) z[wid] = (round_bf16 ? round_bf(a0) : a0) + b0;
-    if (lane == 0 && wid + 4 < V) z[wid + 4] = (round_bf16 ? round_bf(a1) : a1) + b1;
+    if (lane == 0 && wid < V) z[wid] = ((round_bf16 ? round_bf(a0) : a0) + b0) / tdiv;
+    if (lane == 0 && wid + 4 < V) z[wid + 4] = ((round_bf16 ? round_bf(a1) : a1) + b1) / tdiv;
     for (int v = wid + 8; v < V; v += SEL_THREADS / 64) {  // larger vocabularies
       u32x4 wr[MAXC];
 #pragma unroll
@@ -130,15 +132,11 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
         wr[c] = *reinterpret_cast<const u32x4 *>(w_head + static_cast<int64_t>(v) * d + kk);
       }
       const float acc = dot(wr);
-      if (lane == 0) z[v] = (round_bf16 ? round_bf(acc) : acc) + bias[v];
+      if (lane == 0) z[v] = ((round_bf16 ? round_bf(acc) : acc) + bias[v]) / tdiv;
     }
   }
   if (homo_stop > 0)
     for (int v = tid; v < V; v += SEL_THREADS) homo_s[v] = is_homo[v];
-  __syncthreads();
-
-  if (sample)
-    for (int v = tid; v < V; v += SEL_THREADS) z[v] = z[v] / temperature;
   __syncthreads();
 
   // 2. max with first-index tie-break (greedy choice and softmax shift)
@@ -165,7 +163,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
     red_i[wid] = bi;
   }
   __syncthreads();
-  if (tid != 0) return;
+  // every thread merges the waves' (max, index) the same way, so all know the shift
   best = red_v[0];
   bi = red_i[0];
   for (int w = 1; w < SEL_THREADS / 64; ++w)
@@ -174,20 +172,26 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
       bi = red_i[w];
     }
   if (bi >= V) bi = 0;  // all -inf / NaN row: fall back to token 0 (PAD)
+  const float zmax = best;
+  const bool need_e = sample || logp_out;
+  if (need_e) {  // the exponentials, one token per thread (summed in token order below)
+    for (int v = tid; v < V; v += SEL_THREADS) ez[v] = expf(z[v] - zmax);
+    __syncthreads();
+  }
+  if (tid != 0) return;
 
   // 3. choice (single thread: the CDF is accumulated in token order)
   int64_t nxt = bi;
   float sum = 0.f;
-  const float zmax = best;
-  if (sample || logp_out) {
-    for (int v = 0; v < V; ++v) sum += expf(z[v] - zmax);
+  if (need_e) {
+    for (int v = 0; v < V; ++v) sum += ez[v];
   }
   if (sample) {
     const float inv = 1.0f / sum;
     float cdf = 0.f;
     int64_t pick = -1, last_pos = bi;
     for (int v = 0; v < V; ++v) {
-      const float pv = expf(z[v] - zmax) * inv;
+      const float pv = ez[v] * inv;
       if (pv > 0.f) last_pos = v;
       cdf += pv;
       if (pick < 0 && u < cdf) pick = v;
