@@ -701,6 +701,29 @@ def test_linear_residual_big_and_rmsnorm_apply(M, N, K, alpha, bias):
         assert bf_close(h, hu.float().cpu(), ulps=1, atol=1e-5)[0]
 
 
+@pytest.mark.parametrize("n,d,nb", [(4099, 512, 8), (1, 512, 16), (6, 512, 2), (37, 256, 4), (9, 1024, 16)])
+def test_rmsnorm_apply_paths(n, d, nb):
+    """The norm from handed-over block sums on each path: d = 512 with four rows per wavefront (partials as vector
+    loads when nb % 4 == 0, one by one otherwise; row counts that leave a wavefront's group partly empty) and
+    one row per wavefront for other d; bit-equal in place and out of place, against the formula in fp64."""
+    g = gen(n + d + nb)
+    x = R.bf(torch.randn(n, d, generator=g) * 2)
+    nw = R.bf(torch.rand(d, generator=g) + 0.5)
+    xd = x.double()
+    ss = (xd * xd).view(n, nb, d // nb).sum(-1).float()
+    h = ops.rmsnorm_apply(to_dev(x, BF), to_dev(ss), to_dev(nw, BF), 1e-6)
+    xi = to_dev(x, BF)
+    ops.rmsnorm_apply(xi, to_dev(ss), to_dev(nw, BF), 1e-6, out=xi)
+    assert torch.equal(h, xi)
+    tot = torch.zeros(n)
+    for b in range(nb):  # the kernel's order: block 0 first
+        tot = tot + ss[:, b]
+    r = torch.rsqrt(tot / d + 1e-6)
+    want = R.bf((x.float() * r[:, None]) * nw.float())
+    ok, err = bf_close(h, want, ulps=1, atol=1e-5)
+    assert ok, err
+
+
 def test_linear_qkv_rope_no_norm_in_place():
     """The encoder's use: no QK-norm, rotary positions per row, q / k / v written back into the packed qkv rows."""
     g = gen(11)
