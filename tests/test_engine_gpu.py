@@ -75,11 +75,13 @@ def check_logprobs(eng_logp, oracle_res, forced, bias, T, tol=2e-2, pair_res=Non
     pair_res: the same teacher-forced run of an oracle that differs in one rounding point (bf16 attention
     weights). Sampled steps choose from bf16-rounded logits, as the reference's bf16 nn.Linear head makes
     them (viktor/engine.py:112, 191), where one ulp is 1.6e-2 at |z| in [2, 4): a hidden state that moves by
-    bf16 rounding noise moves some log-probs past 2e-2, and the oracle pair shows how far. Then >= 97% of the
-    positions lie within tol; against the pair's spread, the mean and the fraction beyond tol stay within
-    1.25x / 1.5x, the 99.5th percentile within 1.3x and the max within 2x (a single extreme is a noisy
-    statistic); per sequence, mean_j(lp - lp_oracle) -- the GSPO ratio's log -- stays within 2x of the pair's
-    largest plus 1e-3, and the ratio itself within 5e-3 of 1."""
+    bf16 rounding noise moves some log-probs past 2e-2, and the oracle pair shows how far. Then, against the
+    pair's spread, the mean and the fraction beyond tol stay within 1.25x / 1.5x, the 99.5th percentile within
+    1.3x and the max within 2x (a single extreme is a noisy statistic); at least 95% of the positions lie
+    within tol (a floor below the pair's own 97-98% at these lengths: over 2048 positions the fraction has
+    about 0.4% of sampling noise, so a 97% floor would reject benign rounding changes at random); per
+    sequence, mean_j(lp - lp_oracle) -- the GSPO ratio's log -- stays within 2x of the pair's largest plus
+    1e-3, and the ratio itself within 5e-3 of 1."""
     steps = oracle_res["logits"].shape[1]
     want = _chosen_logprobs(oracle_res, forced, bias, T)
     signed = eng_logp[:, :steps].double().cpu() - want
@@ -96,7 +98,7 @@ def check_logprobs(eng_logp, oracle_res, forced, bias, T, tol=2e-2, pair_res=Non
     print(f"  logprobs: HIP-oracle max {err:.2e} q99.5 {q:.2e} mean {float(diff.mean()):.2e} beyond {1 - within:.4f}"
           f" seq {float(seq.max()):.1e}; oracle pair max {p_max:.2e} q99.5 {pq:.2e} mean {p_mean:.2e} beyond "
           f"{p_out:.4f} seq {float(pseq.max()):.1e}")
-    assert within >= 0.97, within
+    assert within >= 0.95, within
     assert float(diff.mean()) <= 1.25 * p_mean + 1e-4 and 1 - within <= 1.5 * p_out + 5e-3, (diff.mean(), p_mean)
     assert q <= 1.3 * pq + 2e-3 and err <= 2 * p_max + 1e-3, (q, pq, err, p_max)
     assert float(seq.max()) <= 2 * float(pseq.max()) + 1e-3, (seq.tolist(), pseq.tolist())
