@@ -306,6 +306,22 @@ __device__ __forceinline__ int gu_swz(int row) { return (row >> 1) & 7; }
 // s_waitcnt immediate: vmcnt <= n, expcnt / lgkmcnt unconstrained
 constexpr int gu_vmcnt(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | (((n >> 4) & 3) << 14); }
 typedef __attribute__((address_space(3))) void gu_lds_void_t;
+// Loads whose wait the kernel places itself: the compiler's wait placement does not count the direct
+// global->LDS loads, so after them it would wait for every outstanding load before the first use of an
+// ordinary load's result, the ring's prefetch included. These loads are invisible to it; each use follows
+// an explicit s_waitcnt and a register touch (gu_touch) that orders the use after it.
+__device__ __forceinline__ u32x4 gu_load16(const void *ptr) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(ptr));
+  return v;
+}
+__device__ __forceinline__ int gu_load4(const void *ptr) {
+  int v;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(ptr));
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ void gu_touch(T &v) { asm volatile("" : "+v"(v)); }
 // one 32-row tile of K or V (rows row0 .. row0 + 31 of base, clamped to clamp - 1) into dst: 4 direct loads,
 // instruction j -> rows 8 j .. 8 j + 7, lane l -> row 8 j + l / 8, LDS slot l % 8 holding chunk (l % 8) ^ swz(row)
 __device__ __forceinline__ void gu_issue_tile(char *dst, const bf16_t *base, int64_t stride, int row0, int clamp,
@@ -404,40 +420,64 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   cur.clamp = static_cast<int>(pre_max);
   cur.seg = 0;
   cur.mc = 0;
-  const bool spec = wid < npre;
+  // the wave's first two tiles t0 = wid and t0 + W are prefix tiles whenever they are inside the static prefix
+  // share: their loads go out with the query and length loads, before any length is known
+  const bool spec = wid < npre, spec2 = wid + GU_WAVES < npre;
 
   // Q^T fragments (loaded before the lengths, so both round trips overlap, and before the first tile's K / V, see
   // below): column j = 16 cb + col -> member
   // j / 4, head kvh * 4 + j % 4, the two 32-wide halves of D
-  bf16x8 bq[NCB][2];
+  // (a column past NC loads column NC - 1 and is zeroed once the loads have landed)
+  u32x4 qraw[NCB][2];
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
-    const int j = 16 * cb + col;
+    const int j = min(16 * cb + col, NC - 1);
+    const int64_t row = static_cast<int64_t>(p) * G + j / 4;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      u32x4 v = u32x4{0u, 0u, 0u, 0u};
-      if (j < NC) {
-        const int64_t row = static_cast<int64_t>(p) * G + j / 4;
-        v = *reinterpret_cast<const u32x4 *>(q + (row * DA_H + kvh * 4 + (j & 3)) * DA_D + 32 * c + 8 * g);
-      }
-      bq[cb][c] = __builtin_bit_cast(bf16x8, v);
-    }
+    for (int c = 0; c < 2; ++c)
+      qraw[cb][c] = gu_load16(q + (row * DA_H + kvh * 4 + (j & 3)) * DA_D + 32 * c + 8 * g);
   }
   // lengths, per wave in registers: lane m < G = member m's own rows, lane G = the prefix; incl = inclusive
   // prefix sum of the members' own-tile counts
+  // (loaded without a branch, so no wait lands between these loads and the first tiles' loads: a lane past the
+  // members reads member G - 1's entry, and the prefix length is one scalar load)
+  int own_raw = gu_load4(own_len + static_cast<int64_t>(p) * G + (lane < G ? lane : G - 1));
+  const int pre_raw = pre_len[pp];
+  // The first two tiles' K / V go out right after the query and length loads, before the lengths are known.
+  TileRef nxt = cur;
+  nxt.row0 = (pt0 + wid + GU_WAVES) * GU_TILE;
+  // Then the query and length loads are waited for by a count that leaves those tiles in flight, in the same
+  // branch that issued them (after a join of paths with different load counts the compiler would drain all).
+  if (spec2) {
+    gu_issue_tile(wring, cur.k, cur.stride, cur.row0, cur.clamp, lane);
+    gu_issue_tile(wring + GU_TILEB, cur.v, cur.stride, cur.row0, cur.clamp, lane);
+    gu_issue_tile(wring + GU_STAGEB, nxt.k, nxt.stride, nxt.row0, nxt.clamp, lane);
+    gu_issue_tile(wring + GU_STAGEB + GU_TILEB, nxt.v, nxt.stride, nxt.row0, nxt.clamp, lane);
+    asm volatile("s_waitcnt vmcnt(16)");
+  } else if (spec) {
+    gu_issue_tile(wring, cur.k, cur.stride, cur.row0, cur.clamp, lane);
+    gu_issue_tile(wring + GU_TILEB, cur.v, cur.stride, cur.row0, cur.clamp, lane);
+    asm volatile("s_waitcnt vmcnt(8)");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)");
+  }
+  gu_touch(own_raw);
+  bf16x8 bq[NCB][2];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      gu_touch(qraw[cb][c]);
+      bq[cb][c] = __builtin_bit_cast(bf16x8, 16 * cb + col < NC ? qraw[cb][c] : u32x4{0u, 0u, 0u, 0u});
+    }
   int len = 0, cnt = 0;
   if (lane < G) {
-    const int64_t l = own_len[static_cast<int64_t>(p) * G + lane];
+    const int64_t l = own_raw;
     len = static_cast<int>(l < 0 ? 0 : (l > own_max ? own_max : l));
     cnt = (len + GU_TILE - 1) / GU_TILE;
   } else if (lane == G) {
-    const int64_t l = pre_len[pp];
+    const int64_t l = pre_raw;
     len = static_cast<int>(l < 1 ? 1 : (l > pre_max ? pre_max : l));
-  }
-  // The first tile's K / V go out right after the query and length loads, before the lengths are known.
-  if (spec) {
-    gu_issue_tile(wring, cur.k, cur.stride, cur.row0, cur.clamp, lane);
-    gu_issue_tile(wring + GU_TILEB, cur.v, cur.stride, cur.row0, cur.clamp, lane);
   }
   int incl = cnt;
 #pragma unroll
@@ -501,14 +541,15 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
       gu_issue_tile(wring, cur.k, cur.stride, cur.row0, cur.clamp, lane);
       gu_issue_tile(wring + GU_TILEB, cur.v, cur.stride, cur.row0, cur.clamp, lane);
     }
-    TileRef nxt = cur;
-    if (t0 + GU_WAVES < t_end) {
+    if (spec2) {
+      nxt.len = cur.len;
+    } else if (t0 + GU_WAVES < t_end) {
       nxt = locate(t0 + GU_WAVES, cur.mc);
       gu_issue_tile(wring + GU_STAGEB, nxt.k, nxt.stride, nxt.row0, nxt.clamp, lane);
       gu_issue_tile(wring + GU_STAGEB + GU_TILEB, nxt.v, nxt.stride, nxt.row0, nxt.clamp, lane);
+    } else {
+      nxt = cur;
     }
-    // (the compiler waits for every outstanding load before the loop, the first two tiles included: the loop uses
-    // the query fragments loaded before it and its own loads return no registers)
     int stage = 0;
     for (int t = t0; t < t_end; t += GU_WAVES) {
       const bool has1 = t + GU_WAVES < t_end, has2 = t + 2 * GU_WAVES < t_end;
