@@ -20,6 +20,8 @@
 //     and the epilogue stores bf16(bf16(silu(bf16(g))) * bf16(u)) over 64 output columns.
 //   * Every row of y is computed by the same code whatever M is (no split of K), so a row's result does not
 //     depend on the other rows of the product.
+#include <type_traits>
+
 #include "common.h"
 
 namespace vk {
@@ -53,7 +55,9 @@ constexpr int vmcnt_imm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((
 // no bias: add_rmsnorm's x += bf16(delta); the encoder's DeepNorm sum with its out_proj bias and alpha), and
 // ss_out[row, col / 64] receives the fp32 sum of squares of the row's new bf16 values over each 64-column block
 // (the RMSNorm that follows reads them instead of a pass of its own over the row).
-enum GbEpi { GB_BF16 = 0, GB_F32 = 1, GB_SWIGLU = 2, GB_QKV = 3, GB_RESID = 4 };
+// GB_QKV reads fp32 rotary tables, GB_QKV_BF16 bf16 ones (the table type is a compile-time choice, so the epilogue's
+// prefetched table registers are not merged across two load shapes)
+enum GbEpi { GB_BF16 = 0, GB_F32 = 1, GB_SWIGLU = 2, GB_QKV = 3, GB_RESID = 4, GB_QKV_BF16 = 5 };
 
 struct GbQkv {
   const bf16_t *qw, *kw;  // per-head RMSNorm weights [64] (both NULL: no norm)
@@ -80,8 +84,10 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
                                                           void *__restrict__ y, int64_t M, int N, int K, int tiles_n,
                                                           int tiles_total, const GbQkv qa) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  constexpr bool SWIGLU = EPI == GB_SWIGLU, OUT_F32 = EPI == GB_F32, QKV = EPI == GB_QKV, RESID = EPI == GB_RESID;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  constexpr bool SWIGLU = EPI == GB_SWIGLU, OUT_F32 = EPI == GB_F32, RESID = EPI == GB_RESID;
+  constexpr bool QKV = EPI == GB_QKV || EPI == GB_QKV_BF16, TAB_F32 = EPI == GB_QKV;
+  // wid through readfirstlane: wave-uniform for the compiler, so branches on the wavefront's quadrant or head are scalar
+  const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wid >> 1, wn = wid & 1;
   constexpr int OUT_COLS = SWIGLU ? 64 : 128;
 
@@ -194,6 +200,63 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
   // write 16 rows x 16-32 B per instruction. Each wavefront instead stages its 128-row quadrant in its own
   // quarter of the (now idle) ring, a pass of rows at a time (row pitch + 16 B against bank conflicts), and
   // stores 16-byte chunks whose lanes cover whole rows.
+  // The epilogue's global operands are loaded here, before the barrier, so their round trips overlap the other
+  // wavefronts' last MFMAs instead of being taken one 16-row group at a time: the residual rows and the bias
+  // (GB_RESID), the QK-norm weights and every row's rotary position (GB_QKV; the table rows, which depend on the
+  // positions, go one group ahead inside the loop).
+  const int fr_e = lane & 15, fg_e = lane >> 4;
+  u32x2 res_old[RESID ? 8 : 1][4];
+  f32x4 res_b4[RESID ? 4 : 1];
+  u32x2 qk_nw[QKV ? 4 : 1];
+  int qk_rp[QKV ? 8 : 1];
+  const int qk_hd = (n0 + wn * 64) >> 6;  // GB_QKV: this wavefront's head (64 columns, wave-uniform)
+  const bool qk_rot = QKV && qk_hd < qa.H + qa.HKV;
+  const bf16_t *qk_w = QKV ? (qk_hd < qa.H ? qa.qw : qa.kw) : nullptr;
+  if (RESID) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      int64_t rrow = m0 + wm * 128 + 16 * j + fr_e;
+      rrow = rrow < M ? rrow : M - 1;
+      const bf16_t *yrow = static_cast<const bf16_t *>(y) + rrow * N + n0 + wn * 64;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) res_old[j][i] = *reinterpret_cast<const u32x2 *>(yrow + 16 * i + 4 * fg_e);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      res_b4[i] = qa.bias != nullptr ? *reinterpret_cast<const f32x4 *>(qa.bias + n0 + wn * 64 + 16 * i + 4 * fg_e)
+                                     : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  if (qk_rot) {
+    if (qk_w != nullptr) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qk_nw[i] = *reinterpret_cast<const u32x2 *>(qk_w + 16 * i + 4 * fg_e);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      int64_t rrow = m0 + wm * 128 + 16 * j + fr_e;
+      rrow = rrow < M ? rrow : M - 1;
+      int64_t rp = qa.rope_pos != nullptr ? qa.rope_pos[rrow] : qa.pos[rrow];
+      qk_rp[j] = static_cast<int>(rp < 0 ? 0 : (rp >= qa.table_rows ? qa.table_rows - 1 : rp));
+    }
+  }
+  // GB_QKV: the rotary table entries of 16-row group j (lane: its row's 4 consecutive entries at 16 i + 4 fg,
+  // i = 0, 1): four fp32 values (GB_QKV) or four bf16 values in two words (GB_QKV_BF16) per table and i
+  using TabT = typename std::conditional<TAB_F32, f32x4, u32x2>::type;
+  auto qk_tables = [&](int j, TabT (&c)[2], TabT (&sn)[2]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int64_t ti = static_cast<int64_t>(qk_rp[j]) * 32 + 16 * i + 4 * fg_e;
+      if constexpr (TAB_F32) {
+        c[i] = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(qa.cos_t) + ti);
+        sn[i] = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(qa.sin_t) + ti);
+      } else {
+        c[i] = *reinterpret_cast<const u32x2 *>(static_cast<const bf16_t *>(qa.cos_t) + ti);
+        sn[i] = *reinterpret_cast<const u32x2 *>(static_cast<const bf16_t *>(qa.sin_t) + ti);
+      }
+    }
+  };
+  TabT qk_c[2][2], qk_s[2][2];  // two row groups' table entries: the current one and the next
+  if (qk_rot) qk_tables(0, qk_c[0], qk_s[0]);
   __syncthreads();  // every wavefront has finished reading the ring
   constexpr int ESZ = OUT_F32 ? 4 : 2;                // output element bytes
   constexpr int QCOLS = SWIGLU ? 32 : 64;             // output columns of a wavefront
@@ -217,13 +280,11 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
         int64_t rrow = qrow0 + 16 * j + fr;
         const bool live = rrow < M;
         rrow = live ? rrow : M - 1;
-        bf16_t *yrow = static_cast<bf16_t *>(y) + rrow * N + qcol0;
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const u32x2 old = *reinterpret_cast<const u32x2 *>(yrow + 16 * i + 4 * fg);
-          f32x4 b4 = {0.f, 0.f, 0.f, 0.f};
-          if (qa.bias != nullptr) b4 = *reinterpret_cast<const f32x4 *>(qa.bias + qcol0 + 16 * i + 4 * fg);
+          const u32x2 old = res_old[j][i];
+          const f32x4 b4 = res_b4[i];
           float o[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -245,10 +306,9 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[i][e] = round_bf(acc[i][j][e]);
         if (hd < qa.H + qa.HKV) {  // q or k head: QK-norm, then the rotation
-          int64_t rrow = qrow0 + 16 * j + fr;
-          rrow = rrow < M ? rrow : M - 1;
-          const bf16_t *nw = hd < qa.H ? qa.qw : qa.kw;
-          if (nw != nullptr) {
+          // the next group's table entries go out before this group's arithmetic
+          if (j + 1 < 8) qk_tables(j + 1, qk_c[(j + 1) & 1], qk_s[(j + 1) & 1]);
+          if (qk_w != nullptr) {
             float ss = 0.f;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -260,30 +320,27 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-              for (int e = 0; e < 4; ++e) v[i][e] = round_bf(v[i][e] * r * bf2f(nw[16 * i + 4 * fg + e]));
+              for (int e = 0; e < 4; ++e) {
+                const uint32_t wpair = qk_nw[i][e >> 1];
+                v[i][e] = round_bf(v[i][e] * r * ((e & 1) ? hi_bf(wpair) : lo_bf(wpair)));
+              }
           }
-          int64_t rp = qa.rope_pos != nullptr ? qa.rope_pos[rrow] : qa.pos[rrow];
-          rp = rp < 0 ? 0 : (rp >= qa.table_rows ? qa.table_rows - 1 : rp);
 #pragma unroll
           for (int i = 0; i < 2; ++i) {
-            // the lane's 4 consecutive table entries: one 16-byte (fp32) or 8-byte (bf16) load each
-            const int64_t ti = rp * 32 + 16 * i + 4 * fg;
+            // the lane's 4 consecutive table entries (loaded one group ahead)
+            const TabT c4 = qk_c[j & 1][i], s4 = qk_s[j & 1][i];
             float cs[4], sn[4];
-            if (qa.table_f32) {
-              const f32x4 c4 = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(qa.cos_t) + ti);
-              const f32x4 s4 = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(qa.sin_t) + ti);
+            if constexpr (TAB_F32) {
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 cs[e] = c4[e];
                 sn[e] = s4[e];
               }
             } else {
-              const u32x2 c2 = *reinterpret_cast<const u32x2 *>(static_cast<const bf16_t *>(qa.cos_t) + ti);
-              const u32x2 s2 = *reinterpret_cast<const u32x2 *>(static_cast<const bf16_t *>(qa.sin_t) + ti);
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
-                cs[e] = (e & 1) ? hi_bf(c2[e >> 1]) : lo_bf(c2[e >> 1]);
-                sn[e] = (e & 1) ? hi_bf(s2[e >> 1]) : lo_bf(s2[e >> 1]);
+                cs[e] = (e & 1) ? hi_bf(c4[e >> 1]) : lo_bf(c4[e >> 1]);
+                sn[e] = (e & 1) ? hi_bf(s4[e >> 1]) : lo_bf(s4[e >> 1]);
               }
             }
 #pragma unroll
@@ -321,6 +378,16 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
         }
       }
     }
+    // GB_QKV with a cache: the cache row and position of the quadrant's 128 rows, one pair of rows per lane (rows
+    // lane and 64 + lane), handed to the lane that stores a row's chunk by a lane shuffle below
+    int cs_lo = 0, cs_hi = 0, cp_lo = 0, cp_hi = 0;
+    if (QKV && (qcol0 >> 6) >= qa.H && qa.kc != nullptr) {
+      const int64_t r0 = min(qrow0 + pass * PASS_ROWS + lane, M - 1), r1 = min(qrow0 + pass * PASS_ROWS + 64 + lane, M - 1);
+      cs_lo = qa.seq[r0];
+      cp_lo = qa.pos[r0];
+      cs_hi = qa.seq[r1];
+      cp_hi = qa.pos[r1];
+    }
     // same wavefront reads back (LDS keeps a wavefront's accesses in order): chunk id -> (row, chunk)
 #pragma unroll
     for (int it = 0; it < PASS_ROWS * CPR / 64; ++it) {
@@ -331,6 +398,10 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
       const int col = qcol0 + c * (16 / ESZ);
       if (QKV) {
         const int hd = qcol0 >> 6;  // c: the 16-byte chunk (8 columns) of the head
+        // (every lane takes part in the shuffles, before any lane leaves the iteration; r < 64 is fixed per it)
+        const bool lo_half = it * 64 / CPR < 64;
+        const int64_t sq = __shfl(lo_half ? cs_lo : cs_hi, r & 63, 64);
+        const int64_t ps = __shfl(lo_half ? cp_lo : cp_hi, r & 63, 64);
         if (row >= M || hd >= qa.H + 2 * qa.HKV) continue;
         if (hd < qa.H) {
           *reinterpret_cast<u32x4 *>(qa.q + row * qa.q_ld + hd * 64 + 8 * c) = v;
@@ -340,7 +411,6 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
         const int hk = is_k ? hd - qa.H : hd - qa.H - qa.HKV;
         bf16_t *cdst = is_k ? qa.kc : qa.vc;
         if (cdst != nullptr) {
-          const int64_t sq = qa.seq[row], ps = qa.pos[row];
           if (sq >= 0 && sq < qa.cache_rows && ps >= 0 && ps < qa.cache_len)
             *reinterpret_cast<u32x4 *>(cdst + sq * qa.stride_cb + ps * qa.stride_cs + hk * 64 + 8 * c) = v;
         }
@@ -438,7 +508,9 @@ extern "C" int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32
   qa.kv_ld = kv_ld;
   qa.H = n_heads;
   qa.HKV = n_kv_heads;
-  const int rc = launch_big<GB_QKV>(static_cast<const bf16_t *>(x), static_cast<const bf16_t *>(w), nullptr, M, N, K,
+  const int rc = qa.table_f32 ? launch_big<GB_QKV>(static_cast<const bf16_t *>(x), static_cast<const bf16_t *>(w), nullptr, M, N, K,
+                                    qa, VK_STREAM(stream))
+                                : launch_big<GB_QKV_BF16>(static_cast<const bf16_t *>(x), static_cast<const bf16_t *>(w), nullptr, M, N, K,
                                     qa, VK_STREAM(stream));
   if (rc != VK_OK) return rc;
   return launch_status("linear_qkv_rope");
