@@ -84,7 +84,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
   // K and V rows: the A operands of S^T and dP^T, and (through transpose reads of K) of dQ^T = K^T dS^T
   __shared__ __attribute__((aligned(16))) bf16_t Ks[2][64 * AB_PITCH];
   __shared__ __attribute__((aligned(16))) bf16_t Vs[2][64 * AB_PITCH];
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
   const int col = lane & 15, g = lane >> 4;
   const int hk = blockIdx.y, hq = hk * 4 + (wid & 3), half = wid >> 2;
   const int seq = plan[2 * blockIdx.x], qs = plan[2 * blockIdx.x + 1];
@@ -226,7 +226,7 @@ __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
   __shared__ __attribute__((aligned(16))) bf16_t Qs[4 * 32 * AB_PITCH];
   __shared__ __attribute__((aligned(16))) bf16_t Os[4 * 32 * AB_PITCH];  // dO
   __shared__ float Ls[4 * 32], Ds[4 * 32];
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
   const int col = lane & 15, g = lane >> 4;
   const int hk = blockIdx.y;
   const int seq = plan[2 * blockIdx.x], ks = plan[2 * blockIdx.x + 1];

@@ -100,7 +100,7 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(const bf16_t *__restrict
                                                         int compact, bf16_t *__restrict__ out, int64_t ldo) {
   __shared__ __attribute__((aligned(16))) char As[2][CG_BM * 64];
   __shared__ __attribute__((aligned(16))) char Ws[2][CG_BN * 64];
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
   const int fr = lane & 15, fg = lane >> 4;
   const int64_t m0 = static_cast<int64_t>(blockIdx.x) * CG_BM;
   const int n0 = blockIdx.y * CG_BN;
@@ -216,7 +216,7 @@ __global__ __launch_bounds__(256, 4) void window_attn_kernel(const bf16_t *__res
                                                           float scale_log2, bf16_t *__restrict__ out, int64_t ldo) {
   __shared__ __attribute__((aligned(16))) bf16_t Ks[2][WA_KT * WA_PITCH];
   __shared__ __attribute__((aligned(16))) bf16_t Vt[2][WA_D * WA_VTP];  // V^T: [d][key]
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
   const int col = lane & 15, g = lane >> 4;
 
   // XCD-aware order: workgroup p runs on XCD p % 8; XCD x takes a contiguous range of (head, block) pairs,

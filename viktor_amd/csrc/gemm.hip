@@ -30,7 +30,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const bf16_t *__restrict
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wid = tid >> 6;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
   const int wm = wid >> 1, wn = wid & 1;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
   const int n0 = blockIdx.x * BN;

@@ -40,7 +40,7 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
   __shared__ __attribute__((aligned(16))) bf16_t Vs[2][PA_KT * PA_PITCH];  // V rows, as K
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wid = tid >> 6;
+  const int lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
   const int col = lane & 15, g = lane >> 4;
   const int hk = blockIdx.y;
   const int hq = hk * (PA_H / PA_HKV) + (wid & 3);

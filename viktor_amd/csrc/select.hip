@@ -53,7 +53,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
   __shared__ float red_v[SEL_THREADS / 64];
   __shared__ int red_i[SEL_THREADS / 64];
   const int64_t b = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
   const bool sample = temperature > 0.f;
   const float tdiv = sample ? temperature : 1.f;  // z / 1 is z: one expression for both modes
 
