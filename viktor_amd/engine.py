@@ -179,8 +179,14 @@ class DecodeEngine:
             self._prefill_plans[row0] = cached
         plan, frame_rows, bos_rows, pos, seq, rpos = cached[1]
         x = torch.empty(plan.total, prefix.shape[1], dtype=self.dtype, device=dev)
-        x.index_copy_(0, frame_rows, prefix)
-        x[bos_rows] = self.dec.embed.weight[BOS].to(self.dtype)
+        if len(set(lens)) == 1:  # equal lengths: the frame rows and the BOS rows are two strided views
+            n, L = len(lens), lens[0]
+            xv = x.view(n, L + 1, -1)
+            xv[:, :L].copy_(prefix.view(n, L, -1))
+            xv[:, L] = self.dec.embed.weight[BOS].to(self.dtype)
+        else:
+            x.index_copy_(0, frame_rows, prefix)
+            x[bos_rows] = self.dec.embed.weight[BOS].to(self.dtype)
         return self.fast.prefill(x, pos, seq, None, plan.max_len, cache, rope_pos=rpos, plan=plan)
 
     def set_uniforms(self, u):
@@ -210,11 +216,12 @@ class DecodeEngine:
         if G > 1:  # one prefill per window: the first sequence of every group
             self._check_groups(frames, frame_lens, offs)
             lens_p = frame_lens[::G]
+            # each group's first member's frames, gathered and converted to the compute dtype in one pass
             if len(set(frame_lens)) == 1:
                 n = frame_lens[0]
-                frames_p = frames.view(self.B // G, G, n, -1)[:, 0].reshape(-1, frames.shape[1])
+                frames_p = frames.view(self.B // G, G, n, -1)[:, 0].to(self.dtype).reshape(-1, frames.shape[1])
             else:
-                frames_p = torch.cat([frames[offs[b]:offs[b + 1]] for b in range(0, self.B, G)])
+                frames_p = torch.cat([frames[offs[b]:offs[b + 1]].to(self.dtype) for b in range(0, self.B, G)])
             offs_p = [0]
             for n in lens_p:
                 offs_p.append(offs_p[-1] + n)
