@@ -395,6 +395,13 @@ def test_scoring_at_scale():
     assert hip_or[2] <= 0.05, hip_or
     assert hip_or[0] <= 1.5 * pair[0] and hip_or[1] <= 1.15 * pair[1] and hip_or[2] <= 1.5 * pair[2] + 1e-3
     assert hip_32[0] <= 1.15 * or_32[0] and hip_32[1] <= 1.15 * or_32[1] and hip_32[2] <= 1.15 * or_32[2] + 1e-3
+    # bar 2 as stated, with the exemption as a rule: tokens where the oracles themselves (fused vs fp32, fused vs
+    # its bf16-weights pair) are more than 2e-2 apart are exempt; everywhere else |HIP - oracle| <= 2e-2
+    agree = m_ref & ((l16 - l32).abs() <= 2e-2) & ((l16p - l16).abs() <= 2e-2)
+    d_strict = (got - l16)[agree].abs()
+    print("bar 2 where the oracles agree: %d of %d tokens checked (%d exempt), max |HIP - oracle| %.2e, %d beyond 2e-2"
+          % (int(agree.sum()), int(m_ref.sum()), int(m_ref.sum() - agree.sum()), float(d_strict.max()),
+             int((d_strict > 2e-2).sum())))
     log_ratio = torch.stack([(got - l16)[b][m_ref[b]].mean() for b in range(len(pick))])
     print("per-sequence mean lp - oracle:", ["%.1e" % float(x) for x in log_ratio])
     assert float((log_ratio.exp() - 1).abs().max()) <= 2e-3
