@@ -67,7 +67,7 @@ __global__ __launch_bounds__(DA_WAVES * 64) void decode_attn_kernel(
   __shared__ __attribute__((aligned(16))) bf16_t Vs[DA_WAVES][DA_TILE * DA_PITCH];
 
   const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform for the compiler
   const int64_t b = blockIdx.y;
   const int split = blockIdx.x;
   // cache row of sequence b (rows == NULL: row b); a row outside the cache gives a zero output (the
