@@ -57,7 +57,30 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
   const bool sample = temperature > 0.f;
   const float tdiv = sample ? temperature : 1.f;  // z / 1 is z: one expression for both modes
 
-  // 0. the sequence's state (wave-uniform loads; an optional pointer that is NULL reads pos instead, discarded)
+  // 0. the LM head's operands first (they depend on nothing the sequence's state holds): this lane's slice of the
+  // hidden row (chunks of 8 at lane * 8 + 512 c; past d: column 0, unused), the norm weight and this wave's first
+  // two LM-head rows (v = wid, wid + 4; past V: row V - 1, unused)
+  const bool head = logits == nullptr;
+  const int v0 = wid < V ? wid : V - 1, v1 = wid + 4 < V ? wid + 4 : V - 1;
+  u32x4 hraw[MAXC], nraw[MAXC], w0raw[MAXC], w1raw[MAXC];
+  float b0 = 0.f, b1 = 0.f;
+  if (head) {
+    const bf16_t *hr = h + b * d;
+    const bf16_t *nw = norm_w ? norm_w : hr;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      const int k = lane * 8 + 512 * c, kk = k < d ? k : 0;
+      hraw[c] = *reinterpret_cast<const u32x4 *>(hr + kk);
+      nraw[c] = *reinterpret_cast<const u32x4 *>(nw + kk);
+      w0raw[c] = *reinterpret_cast<const u32x4 *>(w_head + static_cast<int64_t>(v0) * d + kk);
+      w1raw[c] = *reinterpret_cast<const u32x4 *>(w_head + static_cast<int64_t>(v1) * d + kk);
+    }
+    b0 = bias[v0];
+    b1 = bias[v1];
+  }
+  // then the sequence's state (wave-uniform loads; an optional pointer that is NULL reads pos instead, discarded),
+  // and the two loads that depend on it (the uniform at the output column, the previous token's tail flag), kept
+  // as raw values until the choice, so no wait for them lands before the LM head
   const int64_t p = pos[b];
   const int64_t pl_raw = (plen ? plen : pos)[b];
   const int64_t prev = tok[b];
@@ -67,29 +90,14 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
   const int64_t pl = plen ? pl_raw : 0;
   const int64_t ocol = p - pl;
   const int64_t uc = ocol < 0 ? 0 : (ocol >= u_cols ? u_cols - 1 : ocol);
-  const float u = sample ? uniforms[b * u_stride + uc] : 0.f;
+  const float u_raw = uniforms ? uniforms[b * u_stride + uc] : 0.f;
   const int64_t pv = prev >= 0 && prev < V ? prev : 0;
-  const bool prev_tail = prev >= 0 && prev < V && is_tail[pv] != 0;
+  const uint8_t tail_raw = is_tail[pv];
 
   // 1. logits (+ bias), fp32
-  if (logits != nullptr) {
+  if (!head) {
     for (int v = tid; v < V; v += SEL_THREADS) z[v] = (logits[b * V + v] + bias[v]) / tdiv;
   } else {
-    // this lane's slice of the hidden row (chunks of 8 at lane * 8 + 512 c; past d: column 0, unused), the norm
-    // weight and this wave's first two LM-head rows (v = wid, wid + 4; past V: row V - 1, unused)
-    const bf16_t *hr = h + b * d;
-    const bf16_t *nw = norm_w ? norm_w : hr;
-    const int v0 = wid < V ? wid : V - 1, v1 = wid + 4 < V ? wid + 4 : V - 1;
-    u32x4 hraw[MAXC], nraw[MAXC], w0raw[MAXC], w1raw[MAXC];
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-      const int k = lane * 8 + 512 * c, kk = k < d ? k : 0;
-      hraw[c] = *reinterpret_cast<const u32x4 *>(hr + kk);
-      nraw[c] = *reinterpret_cast<const u32x4 *>(nw + kk);
-      w0raw[c] = *reinterpret_cast<const u32x4 *>(w_head + static_cast<int64_t>(v0) * d + kk);
-      w1raw[c] = *reinterpret_cast<const u32x4 *>(w_head + static_cast<int64_t>(v1) * d + kk);
-    }
-    const float b0 = bias[v0], b1 = bias[v1];
     float hv[MAXC][8];
     float ss = 0.f;
 #pragma unroll
@@ -181,6 +189,8 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
   if (tid != 0) return;
 
   // 3. choice (single thread: the CDF is accumulated in token order)
+  const float u = sample ? u_raw : 0.f;
+  const bool prev_tail = prev >= 0 && prev < V && tail_raw != 0;
   int64_t nxt = bi;
   float sum = 0.f;
   if (need_e) {
