@@ -154,3 +154,36 @@ def test_key_block_plan_covers_every_key_once():
     assert sorted(blocks) == sorted([[0, 0], [1, 0], [2, 0], [2, 128], [3, 0], [3, 128], [3, 256]])
     work = [[1, 128, 129, 300][s] - k for s, k in blocks]
     assert work == sorted(work, reverse=True)  # longest work (most rows at or below the block) first
+
+
+def _attention_plan_loops(q_lens, k_lens, causal, block=64):
+    """The work list as nested loops: (work, sequence, first query) per 64-query block, sorted stably by
+    decreasing work."""
+    blocks = []
+    for i, (ql, kl) in enumerate(zip(q_lens, k_lens)):
+        for qs in range(0, ql, block):
+            blocks.append((min(kl, kl - ql + qs + block) if causal else kl, i, qs))
+    blocks.sort(key=lambda b: -b[0])
+    return [v for _, i, qs in blocks for v in (i, qs)] or [0, 0]
+
+
+def test_attention_and_prefill_plans_match_loop_forms():
+    """The host-built plans (vectorised) against their loop forms: block order, offsets, kept-row indices."""
+    import random
+    from viktor_amd.fast_decoder import PrefillPlan
+    from viktor_amd.hip_ops import AttentionPlan
+    rng = random.Random(3)
+    for trial in range(20):
+        n = rng.randint(1, 40)
+        k_lens = [rng.choice([1, 63, 64, 65, 128, rng.randint(1, 3000)]) for _ in range(n)]
+        causal = trial % 3 != 0
+        q_lens = [rng.randint(0, kl) if causal else rng.randint(0, 300) for kl in k_lens]
+        plan = AttentionPlan(q_lens, k_lens, [7 * i for i in range(n)], "cpu", causal=causal)
+        assert plan.plan.tolist() == _attention_plan_loops(q_lens, k_lens, causal)
+        assert plan.cu_q.tolist() == [sum(q_lens[:j]) for j in range(n + 1)]
+        assert plan.k_lens.tolist() == k_lens and plan.n_blocks == sum((q + 63) // 64 for q in q_lens)
+        seq = [max(1, kl) for kl in k_lens]
+        keep = [rng.randint(1, s) for s in seq]
+        pp = PrefillPlan(seq, "cpu", keep=keep)
+        cu = pp.cu
+        assert pp.last_idx.tolist() == [cu[j + 1] - kk + i for j, kk in enumerate(keep) for i in range(kk)]

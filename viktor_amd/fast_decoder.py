@@ -10,6 +10,7 @@ last layer of a prefill can keep only some rows of each sequence (the BOS row fo
 response rows for teacher-forced scoring), which then attend to their whole sequence.
 """
 
+import numpy as np
 import torch
 
 from . import hip_ops as ops
@@ -62,8 +63,11 @@ class PrefillPlan:
         if self.keep is not None:
             _require(len(self.keep) == self.n_seq and all(0 < k <= n for k, n in zip(self.keep, seq_lens)),
                      "PrefillPlan: keep counts")
-            idx = [cu[j + 1] - k + i for j, k in enumerate(self.keep) for i in range(k)]
-            self.last_idx = torch.tensor(idx, dtype=torch.long).to(device)
+            # rows cu[j + 1] - keep[j] .. cu[j + 1] - 1 of every sequence j, in order
+            kp = np.asarray(self.keep, dtype=np.int64)
+            idx = np.repeat(np.asarray(cu[1:], dtype=np.int64) - kp, kp) + (
+                np.arange(int(kp.sum()), dtype=np.int64) - np.repeat(np.cumsum(kp) - kp, kp))
+            self.last_idx = torch.from_numpy(idx).to(device)
             if cache is not None:
                 self.last = ops.AttentionPlan(self.keep, seq_lens, k_off, device, causal=True)
                 contiguous_rows = all(r == self.rows[0] + j for j, r in enumerate(self.rows))

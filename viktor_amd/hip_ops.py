@@ -295,27 +295,28 @@ class AttentionPlan:
     BLOCK = 64
 
     def __init__(self, q_lens, k_lens, k_off, device, causal=True):
-        q_lens = [int(a) for a in q_lens]
-        k_lens = [int(a) for a in k_lens]
-        _require(len(q_lens) == len(k_lens) == len(k_off), "AttentionPlan: length mismatch")
-        blocks = []
-        for i, (ql, kl) in enumerate(zip(q_lens, k_lens)):
-            _require(ql >= 0 and kl >= 0 and (not causal or kl >= ql), "AttentionPlan: causal needs k_len >= q_len")
-            for qs in range(0, ql, self.BLOCK):
-                work = min(kl, kl - ql + qs + self.BLOCK) if causal else kl
-                blocks.append((work, i, qs))
-        blocks.sort(key=lambda b: -b[0])
-        cu = [0]
-        for ql in q_lens:
-            cu.append(cu[-1] + ql)
-        self.n_seq = len(q_lens)
-        self.n_blocks = len(blocks)
-        self.total_q = cu[-1]
+        import numpy as np
+        q = np.asarray([int(a) for a in q_lens], dtype=np.int64)
+        k = np.asarray([int(a) for a in k_lens], dtype=np.int64)
+        _require(len(q) == len(k) == len(k_off), "AttentionPlan: length mismatch")
+        _require(bool(((q >= 0) & (k >= 0) & ((k >= q) | (not causal))).all()),
+                 "AttentionPlan: causal needs k_len >= q_len")
+        # blocks (sequence i, first query qs) for qs = 0, 64, .. < q_len, in sequence order, then stably sorted by
+        # decreasing key count (ties keep that order)
+        nb = (q + self.BLOCK - 1) // self.BLOCK
+        seq = np.repeat(np.arange(len(q), dtype=np.int64), nb)
+        qs = (np.arange(int(nb.sum()), dtype=np.int64) - np.repeat(np.cumsum(nb) - nb, nb)) * self.BLOCK
+        work = np.minimum(k[seq], k[seq] - q[seq] + qs + self.BLOCK) if causal else k[seq]
+        order = np.argsort(-work, kind="stable")
+        cu = np.concatenate([[0], np.cumsum(q)]).astype(np.int64)
+        self.n_seq = len(q)
+        self.n_blocks = len(order)
+        self.total_q = int(cu[-1])
         self.causal = causal
-        flat = [v for _, i, qs in blocks for v in (i, qs)] or [0, 0]
-        self.plan = torch.tensor(flat, dtype=torch.int32).to(device)
-        self.cu_q = torch.tensor(cu, dtype=torch.int32).to(device)
-        self.k_lens = torch.tensor(k_lens or [0], dtype=torch.int32).to(device)
+        flat = np.stack([seq[order], qs[order]], 1).reshape(-1) if len(order) else np.zeros(2, dtype=np.int64)
+        self.plan = torch.from_numpy(flat.astype(np.int32)).to(device)
+        self.cu_q = torch.from_numpy(cu.astype(np.int32)).to(device)
+        self.k_lens = torch.from_numpy((k if len(k) else np.zeros(1, np.int64)).astype(np.int32)).to(device)
         self.k_off = torch.tensor([int(o) for o in k_off] or [0], dtype=torch.int64).to(device)
 
 

@@ -104,14 +104,21 @@ class Basecaller(nn.Module):
         # packed rows: window b = [prefix[b, :plens[b]] | emb[b]]
         pl = torch.tensor(plens_h, device=dev)
         cu = torch.tensor(plan.cu[:-1], device=dev)
-        frame_rows = torch.repeat_interleave(torch.arange(B, device=dev), pl)
-        frame_pos = torch.arange(int(pl.sum()), device=dev) - torch.repeat_interleave(
-            torch.cumsum(pl, 0) - pl, pl)
         x = torch.empty(plan.total, prefix.shape[-1], dtype=BF16, device=dev)
-        x[cu[frame_rows] + frame_pos] = prefix[frame_rows, frame_pos]
-        tok_dst = (cu + pl)[:, None] + torch.arange(T, device=dev)[None, :]
-        x[tok_dst.reshape(-1)] = emb.reshape(B * T, -1)
-        pos = torch.cat([torch.arange(n, dtype=torch.int32, device=dev) for n in seq_lens])
+        if all(p == P for p in plens_h):  # full windows: two strided copies
+            xv = x.view(B, P + T, -1)
+            xv[:, :P] = prefix
+            xv[:, P:] = emb
+        else:
+            frame_rows = torch.repeat_interleave(torch.arange(B, device=dev), pl)
+            frame_pos = torch.arange(int(pl.sum()), device=dev) - torch.repeat_interleave(
+                torch.cumsum(pl, 0) - pl, pl)
+            x[cu[frame_rows] + frame_pos] = prefix[frame_rows, frame_pos]
+            tok_dst = (cu + pl)[:, None] + torch.arange(T, device=dev)[None, :]
+            x[tok_dst.reshape(-1)] = emb.reshape(B * T, -1)
+        # each row's position inside its window
+        pos = (torch.arange(plan.total, device=dev) - torch.repeat_interleave(
+            cu, torch.tensor(seq_lens, device=dev))).to(torch.int32)
         rpos = None
         if self.pos_scale != 1:
             s = self.pos_scale
