@@ -132,15 +132,28 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
     const float a0 = dot(w0raw), a1 = dot(w1raw);
     if (lane == 0 && wid < V) z[wid] = ((round_bf16 ? round_bf(a0) : a0) + b0) / tdiv;
     if (lane == 0 && wid + 4 < V) z[wid + 4] = ((round_bf16 ? round_bf(a1) : a1) + b1) / tdiv;
-    for (int v = wid + 8; v < V; v += SEL_THREADS / 64) {  // larger vocabularies
-      u32x4 wr[MAXC];
+    // larger vocabularies: this wave's further rows v = wid + 8 + 4 i, eight rows' loads in flight per round trip
+    // (rows past V load row V - 1 and are not written)
+    constexpr int RB = 8;
+    for (int v0b = wid + 8; v0b < V; v0b += RB * (SEL_THREADS / 64)) {
+      u32x4 wr[RB][MAXC];
+      float bv[RB];
 #pragma unroll
-      for (int c = 0; c < MAXC; ++c) {
-        const int k = lane * 8 + 512 * c, kk = k < d ? k : 0;
-        wr[c] = *reinterpret_cast<const u32x4 *>(w_head + static_cast<int64_t>(v) * d + kk);
+      for (int r = 0; r < RB; ++r) {
+        const int v = v0b + r * (SEL_THREADS / 64), vc = v < V ? v : V - 1;
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) {
+          const int k = lane * 8 + 512 * c, kk = k < d ? k : 0;
+          wr[r][c] = *reinterpret_cast<const u32x4 *>(w_head + static_cast<int64_t>(vc) * d + kk);
+        }
+        bv[r] = bias[vc];
       }
-      const float acc = dot(wr);
-      if (lane == 0) z[v] = ((round_bf16 ? round_bf(acc) : acc) + bias[v]) / tdiv;
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const int v = v0b + r * (SEL_THREADS / 64);
+        const float acc = dot(wr[r]);
+        if (lane == 0 && v < V) z[v] = ((round_bf16 ? round_bf(acc) : acc) + bv[r]) / tdiv;
+      }
     }
   }
   if (homo_stop > 0)
