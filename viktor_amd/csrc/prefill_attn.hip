@@ -47,12 +47,17 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
   const int half = wid >> 2;
   const int seq = plan[2 * blockIdx.x];
   const int qs = plan[2 * blockIdx.x + 1];
+  // the sequence's metadata is loaded before the checks below (index clamped into 0 .. n_seq - 1; n_seq > 0 is
+  // checked on the host), so these loads go out together instead of one round trip per check
+  const int seq_c = seq < 0 ? 0 : (seq >= n_seq ? n_seq - 1 : seq);
+  const int64_t q0 = cu_q[seq_c];
+  const int q_end = cu_q[seq_c + 1];
+  const int klen = k_lens[seq_c];
+  const int64_t koff = k_off[seq_c];
+  asm volatile("" ::"s"(q0), "s"(q_end), "s"(klen), "s"(koff));  // (kept ahead of the checks: the compiler would sink them)
   if (seq < 0 || seq >= n_seq || qs < 0) return;
-  const int64_t q0 = cu_q[seq];
-  const int q_len = cu_q[seq + 1] - static_cast<int>(q0);
-  const int klen = k_lens[seq];
+  const int q_len = q_end - static_cast<int>(q0);
   if (q_len <= 0 || klen <= 0 || qs >= q_len) return;
-  const int64_t koff = k_off[seq];
   const int qshift = klen - q_len;  // query r sits at key position qshift + r
   const int nq = min(PA_Q, q_len - qs);
   const int kend = causal ? min(klen, qshift + qs + nq) : klen;
@@ -240,7 +245,7 @@ extern "C" int vk_varlen_attention(const void *q, const void *k, const void *v, 
     return fail(VK_ERR_UNSUPPORTED, "varlen_attention: built for H=8 HKV=2 D=64 (got %d/%d/%d)", H, HKV, D);
   VK_CHECK_ARG(n_blocks >= 0 && n_seq >= 0 && stride_tok >= PA_HKV * PA_D && stride_tok % 8 == 0,
                "varlen_attention: bad sizes");
-  VK_CHECK_ARG(n_blocks == 0 || plan != nullptr, "varlen_attention: missing plan");
+  VK_CHECK_ARG(n_blocks == 0 || (plan != nullptr && n_seq > 0), "varlen_attention: missing plan or sequences");
   VK_CHECK_ARG(vk_aligned16(q) && vk_aligned16(k) && vk_aligned16(v) && vk_aligned16(out),
                "varlen_attention: pointers must be 16-byte aligned");
   if (n_blocks == 0) return VK_OK;
