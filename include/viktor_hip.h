@@ -203,7 +203,8 @@ int vk_decode_attention_grouped_layout(int64_t B, int32_t G, int64_t pre_max, in
  * causal != 0: query r of sequence i sits at position k_len_i - q_len_i + r and sees keys <= it
  * (bottom-right alignment). out[*, H, D] bf16. lse (NULL: not written): [*, H] fp32, each row's
  * log-sum-exp of its scaled scores in log2 units, log2(sum_j 2^(s_j * log2(e) / sqrt(D))), for the backward.
- * plan: n_blocks entries of (sequence, first query row) built by the host, one per 64-query block.
+ * plan: n_blocks entries of (sequence, first query row) built by the host, one per 64-query block
+ * (n_blocks > 0 needs n_seq > 0).
  * Built for H = 8, HKV = 2, D = 64.
  * Replaces flash_attn_varlen_func (viktor/fast_decoder.py:68-73) and flash_attn_func (viktor/decoder.py:82-87).
  */
