@@ -65,11 +65,12 @@ int vk_embed_rmsnorm(const int64_t *tok, const void *emb, int64_t vocab, const v
  * q[n, H, D] receives the rotated q heads; k (rotated) and v go to
  * k_cache/v_cache + seq[t] * stride_cb + pos[t] * stride_cs (+ head * D) when the cache pointers are
  * non-NULL and seq[t] < cache_rows, pos[t] < cache_len; and to k_out/v_out[n, HKV, D] when non-NULL.
- * rope_pos may be NULL (then pos is used).
+ * rope_pos may be NULL (then pos is used). Norm weights bf16 or fp32 per norm_w_dtype (fp32: the master weights
+ * autocast keeps in fp32; same rounding points).
  * Replaces qkv_rope_cache, viktor/triton_ops.py:43-108.
  */
-int vk_qkv_rope_cache(const void *qkv, const void *q_norm_w, const void *k_norm_w, const void *cos_t,
-                      const void *sin_t, int32_t table_dtype, int64_t table_rows, const int32_t *pos,
+int vk_qkv_rope_cache(const void *qkv, const void *q_norm_w, const void *k_norm_w, int32_t norm_w_dtype,
+                      const void *cos_t, const void *sin_t, int32_t table_dtype, int64_t table_rows, const int32_t *pos,
                       const int32_t *rope_pos, const int32_t *seq, void *q, void *k_cache, void *v_cache,
                       int64_t stride_cb, int64_t stride_cs, int64_t cache_rows, int64_t cache_len, void *k_out,
                       void *v_out, int64_t n, float eps, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
@@ -102,22 +103,34 @@ int vk_swiglu(const void *gu, void *out, int64_t n, int32_t f, void *stream);
 int vk_group_rows_equal(const void *x, int64_t groups, int32_t G, int64_t member_bytes, int32_t *flag, void *stream);
 
 /*
- * Large-M residual product, in place: x[M, N] = bf16(bf16(a w^T + bias) + bf16(alpha x)) (a [M, K], w [N, K] bf16,
- * bias fp32 [N] or NULL; N % 128 == 0, K % 64 == 0), and ss_out[M, N / 64] = the fp32 sum of squares of each row's
- * new values per 64-column block. alpha = 1 without bias is the residual add of add_rmsnorm
- * (viktor/triton_ops.py:17-31, x += delta after the o / down projections of viktor/fast_decoder.py:56-58); with
- * the out_proj bias and the DeepNorm alpha it is the encoder's norm input (viktor/encoder.py:106-108).
+ * Large-M residual product, in place (a [M, K], w [N, K] bf16, bias fp32 [N] or NULL; N % 128 == 0, K % 64 == 0):
+ *   x_dtype bf16: x[M, N] = bf16(bf16(a w^T + bias) + bf16(alpha x)). alpha = 1 without bias is the residual add
+ *     of add_rmsnorm (viktor/triton_ops.py:17-31, x += delta after the o / down projections of
+ *     viktor/fast_decoder.py:56-58); with the out_proj bias and the DeepNorm alpha it is the encoder's norm input
+ *     (viktor/encoder.py:106-108);
+ *   x_dtype f32: x[M, N] = alpha x + bf16(a w^T + bias) in fp32, the residual add x + sublayer(x) of an fp32 stream
+ *     under torch.autocast bf16 (viktor/decoder.py:118-120 as scripts/gspo.py:345-347 runs it).
+ * ss_out[M, N / 64] = the fp32 sum of squares of each row's new values per 64-column block.
  */
-int vk_linear_residual_big(const void *a, const void *w, void *x, int64_t M, int32_t N, int32_t K, const float *bias,
-                           float alpha, float *ss_out, void *stream);
+int vk_linear_residual_big(const void *a, const void *w, void *x, int32_t x_dtype, int64_t M, int32_t N, int32_t K,
+                           const float *bias, float alpha, float *ss_out, void *stream);
 
 /*
- * RMSNorm from handed-over sums of squares: h = bf16(x * rsqrt(sum_b ss[row, b] / d + eps) * w) (x, w, h bf16,
- * ss [n, nb] fp32 summed in block order; h may be x). The norm half of add_rmsnorm (viktor/triton_ops.py:28-31)
- * after vk_linear_residual_big.
+ * RMSNorm from handed-over sums of squares: h = bf16(x * rsqrt(sum_b ss[row, b] / d + eps) * w) (x and w bf16 or
+ * fp32 per x_dtype / w_dtype, h bf16, ss [n, nb] fp32 summed in block order; h may be x when x is bf16). The norm
+ * half of add_rmsnorm (viktor/triton_ops.py:28-31) after vk_linear_residual_big; with fp32 x and w, nn.RMSNorm of
+ * the fp32 residual stream rounded once at the next product's autocast input (viktor/decoder.py:119, 144).
  */
-int vk_rmsnorm_apply_ss(const void *x, const float *ss, int32_t nb, const void *w, void *h, int64_t n, int32_t d,
-                        float eps, void *stream);
+int vk_rmsnorm_apply_ss(const void *x, int32_t x_dtype, const float *ss, int32_t nb, const void *w, int32_t w_dtype,
+                        void *h, int64_t n, int32_t d, float eps, void *stream);
+
+/*
+ * RMSNorm of an fp32 residual stream with fp32 weights, rounded once to bf16: h = bf16(x rsqrt(mean x^2 + eps) w)
+ * (x [n, d], w [d] fp32; d % 8 == 0, d <= 2048). The first attention norm of the autocast teacher-forced forward
+ * (nn.RMSNorm at viktor/decoder.py:118 on the fp32 rows viktor/model.py:81-84 builds, cast to bf16 by autocast at
+ * qkv_proj).
+ */
+int vk_rmsnorm_f32(const float *x, const float *w, void *h, int64_t n, int32_t d, float eps, void *stream);
 
 /*
  * The Wqkv product with vk_qkv_rope_cache fused into its epilogue (prefill and the encoder): qkv = x w^T
@@ -128,10 +141,12 @@ int vk_rmsnorm_apply_ss(const void *x, const float *ss, int32_t nb, const void *
  * (k_cache + seq[t] stride_cb + pos[t] stride_cs + 64 h, when seq[t] < cache_rows and pos[t] < cache_len) and /
  * or to k_out / v_out + t kv_ld + 64 h. head_dim must be 64; 16-byte aligned pointers, strides % 8 == 0.
  * Replaces linear + qkv_rope_cache (viktor/triton_ops.py:43-108, 138-146; viktor/fast_decoder.py:39-47) and
- * the Wqkv product + apply_rope of the encoder (viktor/encoder.py:71-75).
+ * the Wqkv product + apply_rope of the encoder (viktor/encoder.py:71-75). norm_w_dtype f32 (with f32 tables):
+ * fp32 norm weights, the autocast forward's Attention.project (viktor/decoder.py:63-67): nn.RMSNorm of a bf16 head
+ * with fp32 weights returns bf16(x / rms * w), then apply_rope in fp32 rounds back to bf16.
  */
 int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32_t K, const void *q_norm_w, const void *k_norm_w,
-                       float eps, const void *cos_t, const void *sin_t, int32_t table_dtype, int64_t table_rows,
+                       int32_t norm_w_dtype, float eps, const void *cos_t, const void *sin_t, int32_t table_dtype, int64_t table_rows,
                        const int32_t *pos, const int32_t *rope_pos, const int32_t *seq, void *q, int64_t q_ld,
                        void *k_cache, void *v_cache, int64_t stride_cb, int64_t stride_cs, int64_t cache_rows,
                        int64_t cache_len, void *k_out, void *v_out, int64_t kv_ld, int32_t n_heads, int32_t n_kv_heads,
@@ -361,24 +376,26 @@ int vk_embed_grad_workspace(int64_t n, int32_t V, int32_t d, int64_t *bytes);
 
 /*
  * Token-embedding gradient (the backward of nn.Embedding, viktor/decoder.py:127, gathered at viktor/model.py:77):
- * out[v, :] = sum of d_rows[r, :] over the rows r with tokens[r] == v, fp32 [V, d], from d_rows [n, d] bf16 (row
- * stride ld elements) and tokens [n] int64. Row slices summed in a fixed order (deterministic, no atomics); ids
+ * out[v, :] = sum of d_rows[r, :] over the rows r with tokens[r] == v, fp32 [V, d], from d_rows [n, d] bf16 or fp32
+ * per d_dtype (row stride ld elements) and tokens [n] int64. Row slices summed in a fixed order (deterministic, no atomics); ids
  * outside [0, V) add nothing. d % 8 == 0; workspace: vk_embed_grad_workspace() bytes.
  */
-int vk_embed_grad(const void *d_rows, int64_t ld, const int64_t *tokens, int64_t n, int32_t V, int32_t d, float *out,
-                  void *workspace, int64_t workspace_bytes, void *stream);
+int vk_embed_grad(const void *d_rows, int32_t d_dtype, int64_t ld, const int64_t *tokens, int64_t n, int32_t V, int32_t d,
+                  float *out, void *workspace, int64_t workspace_bytes, void *stream);
 
 /* Workgroups (= rows of the weight-gradient partials) vk_rmsnorm_backward uses for n rows. */
 int vk_rmsnorm_backward_blocks(int64_t n, int32_t *blocks);
 
 /*
- * RMSNorm backward (nn.RMSNorm of the decoder blocks, viktor/decoder.py:110-124), d = 512: given x [n, d]
- * bf16, weight w [d] bf16 and dy [n, d] (bf16 or fp32 per dy_dtype): dx = r w dy - x r^3 mean(w dy x)
+ * RMSNorm backward (nn.RMSNorm of the decoder blocks, viktor/decoder.py:110-124), d = 512: given x [n, d] and
+ * weight w [d] (both bf16, or both fp32: the autocast forward's residual stream and master weights) and dy [n, d]
+ * (bf16 or fp32 per dy_dtype): dx = r w dy - x r^3 mean(w dy x)
  * (+ dres when not NULL: the residual stream's incoming gradient; dx may alias dres), fp32;
  * dw_part [vk_rmsnorm_backward_blocks(n), d] fp32: per-workgroup sums of dy x r (reduce with vk_colsum).
  */
-int vk_rmsnorm_backward(const void *x, const void *w, const void *dy, int32_t dy_dtype, const float *dres,
-                        float *dx, float *dw_part, int64_t n, int32_t d, float eps, void *stream);
+int vk_rmsnorm_backward(const void *x, int32_t x_dtype, const void *w, int32_t w_dtype, const void *dy,
+                        int32_t dy_dtype, const float *dres, float *dx, float *dw_part, int64_t n, int32_t d, float eps,
+                        void *stream);
 
 /* out[c] = sum_r part[r, c] (+ out[c] when accumulate), fixed order. */
 int vk_colsum(const float *part, float *out, int32_t rows, int32_t cols, int32_t accumulate, void *stream);
@@ -388,10 +405,11 @@ int vk_colsum(const float *part, float *out, int32_t rows, int32_t cols, int32_t
  * qkv [n, (H + 2 HKV) 64] bf16 (the projection output), dq [n, H, 64] / dk / dv [n, HKV, 64] fp32 (the
  * attention's input gradients), RoPE rows rope_pos [n] of cos/sin [table_rows, 32]. Writes dqkv [n, (H + 2 HKV) 64]
  * bf16 (q / k heads through the rotation and the 64-wide norm, v heads copied) and dw_part
- * [vk_rmsnorm_backward_blocks(n), 128] fp32 (q-norm weight partials 0..63, k-norm 64..127). D = 64.
+ * [vk_rmsnorm_backward_blocks(n), 128] fp32 (q-norm weight partials 0..63, k-norm 64..127). D = 64. Norm weights
+ * bf16 or fp32 per norm_w_dtype.
  */
-int vk_qknorm_rope_backward(const void *qkv, const void *q_norm_w, const void *k_norm_w, const void *cos_t,
-                            const void *sin_t, int32_t table_dtype, int64_t table_rows, const int32_t *rope_pos,
+int vk_qknorm_rope_backward(const void *qkv, const void *q_norm_w, const void *k_norm_w, int32_t norm_w_dtype,
+                            const void *cos_t, const void *sin_t, int32_t table_dtype, int64_t table_rows, const int32_t *rope_pos,
                             const float *dq, const float *dk, const float *dv, void *dqkv, float *dw_part, int64_t n,
                             int32_t H, int32_t HKV, int32_t D, float eps, void *stream);
 

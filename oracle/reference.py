@@ -1,11 +1,28 @@
 """CPU restatement of the reference decoder path (test infrastructure; see oracle/__init__.py).
 
 Numerics modes:
-  "fp32"  -- viktor/decoder.py in fp32: F.rms_norm, apply_rope, SDPA, F.linear, fp32 residual stream.
-  "fused" -- the fused inference path's rounding points (viktor/triton_ops.py:1-10, 25-31, 44-49, 132-134,
-             219; viktor/fast_decoder.py:33-60): every op reads bf16, computes in fp32 and stores bf16;
-             weights are bf16; logits fp32 for greedy decode steps, bf16 for the prefill token and for
-             sampled steps (viktor/engine.py:96, 112, 191).
+  "fp32"     -- viktor/decoder.py in fp32: F.rms_norm, apply_rope, SDPA, F.linear, fp32 residual stream.
+  "fused"    -- the fused inference path's rounding points (viktor/triton_ops.py:1-10, 25-31, 44-49, 132-134,
+                219; viktor/fast_decoder.py:33-60): every op reads bf16, computes in fp32 and stores bf16;
+                weights are bf16; logits fp32 for greedy decode steps, bf16 for the prefill token and for
+                sampled steps (viktor/engine.py:96, 112, 191).
+  "autocast" -- the reference's scoring path: Basecaller.logits of the fp32 master model under
+                torch.autocast("cuda", bf16) (scripts/gspo.py:345-347; viktor/model.py:55-60, 71-85;
+                viktor/decoder.py:63-67, 82-87, 117-120, 144). Rounding points, as torch 2.10's autocast
+                applies them on the GPU (ops outside autocast's lists run in their inputs' dtype):
+                  * nn.Linear: input and weight (and bias) cast to bf16, fp32 accumulation, bf16 output;
+                  * the residual stream is fp32: prefix rows fp32(bf16 projector output), token rows the fp32
+                    embedding (nn.Embedding is not cast), and x + sublayer(x) adds a bf16 output in fp32;
+                  * nn.RMSNorm of the fp32 stream runs in fp32 with the fp32 weights; the next nn.Linear rounds
+                    it to bf16 (the final norm too, at the LM head);
+                  * the QK-norm of a bf16 head with fp32 weights returns bf16(x / rms * w) (torch's rms_norm
+                    computes in fp32 and casts back to its input's dtype when the weight dtype differs);
+                    apply_rope runs in fp32 with the fp32 tables and casts back to bf16 -- the rounding points
+                    of the fused path's qkv_rope_cache, with fp32 weights and tables;
+                  * F.silu(gate) * up: silu of the bf16 gate rounded to bf16, the product rounded to bf16;
+                  * flash_attn_func: bf16 q / k / v, fp32 scores, bf16 probabilities in the PV product
+                    (attention_rows with p_bf16), bf16 output;
+                  * logits bf16; log_softmax of their fp32 cast.
 """
 
 import math
@@ -74,13 +91,18 @@ def qk_norm_rope_fused(x, w, cos, sin, eps):
     return torch.cat([bf(y1 * c - y2 * s), bf(y1 * s + y2 * c)], -1)
 
 
-def attention_rows(q, k, v, causal_shift=None, p_bf16=False):
+def attention_rows(q, k, v, causal_shift=None, p_bf16=False, block=None):
     """Exact fp32 softmax attention of one sequence. q [Tq, H, D], k/v [Tk, Hkv, D]; query head h reads KV
     head h // (H / Hkv) (GQA, viktor/decoder.py:91-105 repeat_interleave); query r sits at key position
     causal_shift + r when causal_shift is not None. Returns [Tq, H, D] fp32.
     p_bf16: the flash-attention rounding point -- the unnormalised weights exp(s - max) are rounded to bf16
     for the PV product while the normaliser sums them unrounded (viktor/decode_attention.py:27-37 stores
-    p.to(v.dtype) the same way): o = sum_j bf16(e_j) v_j / sum_j e_j."""
+    p.to(v.dtype) the same way): o = sum_j bf16(e_j) v_j / sum_j e_j.
+    block (with p_bf16): the weights rounded the way a tiled online-softmax kernel rounds them -- key blocks of
+    `block` visited from the last to the first, as flash-attention 2's forward walks them (flash_attn_func, the
+    reference's scoring attention; a third-party kernel that is not here, restated from its published design), each
+    block's weights exp(s - running max) rounded to bf16 for the PV product, the accumulator and the unrounded
+    normaliser rescaled when the running max grows."""
     Tq, H, D = q.shape
     Tk, Hkv, _ = k.shape
     rep = H // Hkv
@@ -93,6 +115,21 @@ def attention_rows(q, k, v, causal_shift=None, p_bf16=False):
     if not p_bf16:
         p = torch.softmax(s, -1)
         return torch.einsum("grqk,kgd->qgrd", p, v).reshape(Tq, H, D)
+    if block is not None:
+        m = torch.full((Hkv, rep, Tq, 1), float("-inf"))
+        lsum = torch.zeros(Hkv, rep, Tq, 1)
+        acc = torch.zeros(Hkv, rep, Tq, D)
+        for b0 in reversed(range(0, Tk, block)):
+            sb = s[..., b0:b0 + block]
+            m_new = torch.maximum(m, sb.amax(-1, keepdim=True))
+            live = torch.isfinite(m_new)  # rows with no unmasked key yet keep their (empty) state
+            mn = torch.where(live, m_new, torch.zeros_like(m_new))
+            scale = torch.where(torch.isfinite(m), torch.exp(m - mn), torch.zeros_like(m))
+            e = torch.exp(sb - mn)
+            lsum = lsum * scale + e.sum(-1, keepdim=True)
+            acc = acc * scale + torch.einsum("grqk,kgd->grqd", bf(e), v[b0:b0 + block])
+            m = torch.where(live, m_new, m)
+        return (acc / lsum).permute(2, 0, 1, 3).reshape(Tq, H, D)
     e = torch.exp(s - s.amax(-1, keepdim=True))
     o = torch.einsum("grqk,kgd->grqd", bf(e), v) / e.sum(-1, keepdim=True)
     return o.permute(2, 0, 1, 3).reshape(Tq, H, D)
@@ -102,13 +139,16 @@ def attention_rows(q, k, v, causal_shift=None, p_bf16=False):
 class RefModel:
     """fp32 CPU copy of a Basecaller's projector + decoder weights, run in one numerics mode."""
 
-    def __init__(self, model, mode="fp32", table_bf16=None, p_bf16=False):
+    def __init__(self, model, mode="fp32", table_bf16=None, p_bf16=False, attn_block=None):
         """p_bf16 (fused mode): attention weights rounded to bf16 before the PV product, the rounding point of
         flash-attention and of the reference's decode kernel (attention_rows). Off by default: the two choices
-        bracket the reference's bf16 rounding noise."""
-        assert mode in ("fp32", "fused")
+        bracket the reference's bf16 rounding noise. Autocast mode always rounds them (flash_attn_func); attn_block
+        (autocast mode): round them blockwise as a tiled kernel does (attention_rows), instead of against the row's
+        final maximum -- two equally faithful restatements whose spread is the reference's own rounding noise."""
+        self.attn_block = attn_block if mode == "autocast" else None
+        assert mode in ("fp32", "fused", "autocast")
         self.mode = mode
-        self.p_bf16 = bool(p_bf16) and mode == "fused"
+        self.p_bf16 = (bool(p_bf16) and mode == "fused") or mode == "autocast"
         self.cfg = model.decoder.cfg
         self.k = model.tokenizer.k
         self.strings = list(model.tokenizer.strings)
@@ -118,6 +158,9 @@ class RefModel:
         sd = {n: p.detach().float().cpu().clone() for n, p in model.named_parameters()}
         if mode == "fused":
             sd = {n: bf(t) for n, t in sd.items()}
+        elif mode == "autocast":  # products take bf16 copies (biases too); norms and the embedding stay fp32
+            sd = {n: bf(t) if (t.dim() == 2 and not n.endswith("embed.weight")) or n.endswith("bias") else t
+                  for n, t in sd.items()}
         self.p = sd
         cos, sin = rope_tables(self.cfg.head_dim, self.cfg.max_seq_len, self.cfg.rope_theta)
         if table_bf16 is None:
@@ -132,6 +175,7 @@ class RefModel:
         self = cls.__new__(cls)
         self.mode, self.cfg = mode, dec.cfg
         self.p_bf16 = False
+        self.attn_block = None
         sd = {f"decoder.{n}": p.detach().float().cpu().clone() for n, p in dec.named_parameters()}
         self.p = {n: bf(t) for n, t in sd.items()} if mode == "fused" else sd
         cos, sin = rope_tables(dec.cfg.head_dim, dec.cfg.max_seq_len, dec.cfg.rope_theta)
@@ -142,7 +186,7 @@ class RefModel:
     def L(self, i, name):
         return self.p[f"decoder.layers.{i}.{name}"]
 
-    # projector: Linear -> GELU -> Linear (viktor/model.py:35), bf16 activations in fused mode
+    # projector: Linear -> GELU -> Linear (viktor/model.py:35), bf16 activations in fused and autocast modes
     def project(self, frames):
         p = self.p
         if self.mode == "fp32":
@@ -165,6 +209,8 @@ class RefModel:
         eps = cfg.norm_eps
         T = x.shape[0]
         cos, sin = self.cos[rpos], self.sin[rpos]
+        if self.mode == "autocast":
+            return self._layer_autocast(i, x, h, cos, sin, kv, causal_shift)
         fused = self.mode == "fused"
         qkv = linear_fused(h, self.L(i, "attn.qkv_proj.weight")) if fused else h @ self.L(i, "attn.qkv_proj.weight").t()
         qkv = qkv.view(T, H + 2 * Hkv, D)
@@ -199,10 +245,37 @@ class RefModel:
         w_next = self.L(i + 1, "attn_norm.weight") if i + 1 < cfg.n_layers else self.p["decoder.norm.weight"]
         return x, F.rms_norm(x, (cfg.d_model,), w_next, eps)
 
+    def _layer_autocast(self, i, x, h, cos, sin, kv, causal_shift):
+        """One block under torch.autocast bf16 (viktor/decoder.py:117-120 with Attention at 63-87): x fp32,
+        h = bf16 operand of qkv_proj. Returns (x, bf16 operand of the next product)."""
+        cfg = self.cfg
+        H, Hkv, D = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+        eps = cfg.norm_eps
+        T = x.shape[0]
+        qkv = linear_fused(h, self.L(i, "attn.qkv_proj.weight")).view(T, H + 2 * Hkv, D)
+        q, k, v = qkv[:, :H], qkv[:, H:H + Hkv], qkv[:, H + Hkv:]
+        q = qk_norm_rope_fused(q, self.L(i, "attn.q_norm.weight"), cos, sin, eps)
+        k = qk_norm_rope_fused(k, self.L(i, "attn.k_norm.weight"), cos, sin, eps)
+        K0, V0 = kv[i]
+        K = torch.cat([K0, k]) if K0 is not None else k
+        Vv = torch.cat([V0, v]) if V0 is not None else v
+        kv[i] = (K, Vv)
+        o = bf(attention_rows(q, K, Vv, causal_shift=causal_shift, p_bf16=True, block=self.attn_block))
+        x = x + linear_fused(o.reshape(T, -1), self.L(i, "attn.o_proj.weight"))
+        h2 = bf(F.rms_norm(x, (cfg.d_model,), self.L(i, "mlp_norm.weight"), eps))
+        gu = self.L(i, "gate_up.weight")
+        Fd = gu.shape[0] // 2
+        m = swiglu_fused(linear_fused(h2, gu[:Fd]), linear_fused(h2, gu[Fd:]))
+        x = x + linear_fused(m, self.L(i, "down.weight"))
+        w_next = self.L(i + 1, "attn_norm.weight") if i + 1 < cfg.n_layers else self.p["decoder.norm.weight"]
+        return x, bf(F.rms_norm(x, (cfg.d_model,), w_next, eps))
+
     def first_norm(self, x):
         w = self.L(0, "attn_norm.weight")
         if self.mode == "fused":
             return rmsnorm_fused(x, w, self.cfg.norm_eps)
+        if self.mode == "autocast":
+            return bf(F.rms_norm(x, (self.cfg.d_model,), w, self.cfg.norm_eps))
         return F.rms_norm(x, (self.cfg.d_model,), w, self.cfg.norm_eps)
 
     def run(self, x, rpos, kv, start):
@@ -236,12 +309,13 @@ class RefModel:
         return torch.stack(out)
 
     @torch.no_grad()
-    def logits(self, frames, tokens_in, plens=None):
-        """Teacher-forced logits [B, T, V] (fp32 mode) or bf16-rounded (fused mode), reference:
-        viktor/model.py:55-85 with the window packed as [plens[b] frames | tokens]."""
-        return self._logits(frames, tokens_in, plens)
+    def logits(self, frames, tokens_in, plens=None, round_logits=True):
+        """Teacher-forced logits [B, T, V] (fp32 mode) or bf16-rounded (fused and autocast modes), reference:
+        viktor/model.py:55-85 with the window packed as [plens[b] frames | tokens]. round_logits False: the
+        head's fp32 products before that rounding."""
+        return self._logits(frames, tokens_in, plens, round_logits)
 
-    def _logits(self, frames, tokens_in, plens=None):
+    def _logits(self, frames, tokens_in, plens=None, round_logits=True):
         B, P, _ = frames.shape
         T = tokens_in.shape[1]
         out = []
@@ -256,7 +330,7 @@ class RefModel:
             else:
                 rpos = torch.cat([torch.arange(n) * s, s * n + torch.arange(T)])
             h = self.run(x, rpos, self.new_kv(), 0)[n:]
-            out.append(self.head(h, round_bf16=self.mode == "fused"))
+            out.append(self.head(h, round_bf16=round_logits and self.mode in ("fused", "autocast")))
         return torch.stack(out)
 
 

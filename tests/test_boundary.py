@@ -58,12 +58,24 @@ def test_argument_errors_return_status_without_device_work():
     rc = lib.vk_select_update(p, None, None, 1e-6, None, 0, 0, p, p, p, 0, 0.0, None, 0, 0, p, None, p, None,
                               None, None, p, 16, 16, None, None, None, p, 8, 4, 7, 2, 0, None)
     assert rc == 1 and b"logp_stride" in lib.vk_last_error()
-    rc = lib.vk_linear_residual_big(p, p, p, 4, 96, 64, None, 1.0, p, None)  # N % 128 != 0
+    rc = lib.vk_linear_residual_big(p, p, p, 0, 4, 96, 64, None, 1.0, p, None)  # N % 128 != 0
     assert rc == 1 and b"N" in lib.vk_last_error()
-    rc = lib.vk_linear_residual_big(p, p, p, 4, 128, 64, None, 1.0, None, None)  # no sums-of-squares output
+    rc = lib.vk_linear_residual_big(p, p, p, 0, 4, 128, 64, None, 1.0, None, None)  # no sums-of-squares output
     assert rc == 1 and b"null" in lib.vk_last_error()
-    rc = lib.vk_rmsnorm_apply_ss(p, p, 8, p, p, 4, 12, 1e-6, None)  # d % 8 != 0
+    rc = lib.vk_linear_residual_big(p, p, p, 7, 4, 128, 64, None, 1.0, p, None)  # residual dtype
+    assert rc == 1 and b"dtype" in lib.vk_last_error()
+    rc = lib.vk_rmsnorm_apply_ss(p, 0, p, 8, p, 0, p, 4, 12, 1e-6, None)  # d % 8 != 0
     assert rc == 1 and b"d=12" in lib.vk_last_error()
+    rc = lib.vk_rmsnorm_apply_ss(p, 1, p, 8, p, 1, p, 4, 512, 1e-6, None)  # fp32 x written over by bf16 h
+    assert rc == 1 and b"fp32 x" in lib.vk_last_error()
+    rc = lib.vk_rmsnorm_f32(p, p, p, 4, 4096, 1e-6, None)  # d above 2048
+    assert rc == 1 and b"d=4096" in lib.vk_last_error()
+    # fp32 QK-norm weights with bf16 rotary tables
+    rc = lib.vk_linear_qkv_rope(p, p, 4, 512, p, p, 1, 1e-6, p, p, 0, 16, p, None, None, p, 512, None, None, 0, 0, 0,
+                                0, p, p, 128, 8, 2, 64, None)
+    assert rc == 1 and b"fp32 rotary tables" in lib.vk_last_error()
+    rc = lib.vk_rmsnorm_backward(p, 1, p, 0, p, 0, None, p, p, 4, 512, 1e-6, None)  # fp32 x with bf16 weights
+    assert rc == 3
     with pytest.raises(_lib.HipLibraryError):
         _lib.check(rc, "decode_attention")
 

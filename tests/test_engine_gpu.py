@@ -325,9 +325,36 @@ def test_stress_batch_at_scale():
     check_stream(a[pick], res, steps, 1e-2)
 
 
+def master_copy(m):
+    """The fp32 master model on the device: what the reference's token_logprobs scores with, under autocast
+    (scripts/gspo.py:345-347, 455)."""
+    g = copy.deepcopy(m).to(DEV)
+    g.decoder._fast = None
+    return g.eval()
+
+
+def bf16_residual_logits(gm, frames, tokens_in):
+    """Teacher-forced logits of full windows through the inference path's rounding points (a bf16 residual stream,
+    FastDecoder.prefill with a kept-rows plan): the scoring numerics before the autocast forward, kept here to show
+    that the scoring bar tells the two apart."""
+    from viktor_amd.fast_decoder import PrefillPlan
+    B, P = frames.shape[:2]
+    T = tokens_in.shape[1]
+    fast = gm.decoder.fast()
+    prefix = gm.project(frames)
+    emb = fast.w(gm.decoder.embed.weight)[tokens_in]
+    x = torch.cat([prefix, emb], 1).reshape(B * (P + T), -1).contiguous()
+    plan = PrefillPlan([P + T] * B, frames.device, keep=[T] * B)
+    pos = torch.arange(P + T, dtype=torch.int32, device=frames.device).repeat(B)
+    h = fast.prefill(x, pos, None, None, plan.max_len, None, plan=plan)
+    return gm.decoder.head(h).view(B, T, -1)
+
+
 def test_teacher_forced_logprobs_parity():
+    """token_logprobs of the fp32 master model (the reference scores with it under torch.autocast bf16) against the
+    oracle's autocast mode: bar 2 (2e-2) on every masked token, ragged prefixes; and the fp32 reference within 5e-2."""
     m = make_model(1, n_layers=2, seed=8, norm_jitter=0.1, bias_jitter=0.1)
-    gm = gpu_copy(m)
+    gm = master_copy(m)
     P = 300
     fr = synth_frames(3, P, 512, seed=9)
     plens = torch.tensor([300, 180, 41])
@@ -335,35 +362,30 @@ def test_teacher_forced_logprobs_parity():
     ended = [True, False, True]
     lp, mask = G.token_logprobs(gm, fr.to(DEV), plens.to(DEV), seqs, ended)
     tin, tgt, _ = m.batch(seqs, pad_to=128)
-    ref = R.RefModel(m, "fused")
-    lg = ref.logits(fr, tin, plens)
-    lp_ref = R.token_logprobs_ref(lg, tgt)
+    lp_ref = R.token_logprobs_ref(R.RefModel(m, "autocast").logits(fr, tin, plens), tgt)
     m_ref = R.sampled_mask_ref(tgt, seqs, ended, 1)
     assert torch.equal(mask.cpu(), m_ref)
     err = (lp.cpu() - lp_ref)[m_ref].abs().max()
     assert err < 2e-2, float(err)
-    # against the fp32 reference semantics too (the training path runs fp32 weights under bf16 autocast)
     lp32 = R.token_logprobs_ref(R.RefModel(m, "fp32").logits(fr, tin, plens), tgt)
     assert (lp.cpu() - lp32)[m_ref].abs().max() < 5e-2
 
 
 def test_scoring_at_scale():
     """The scoring configuration's sizes: 512 sequences x (2048-frame prefix + 700..1024 response tokens),
-    8 layers, vocab 7: token log-probs and masks, finite everywhere, and four sequences (first, last, two
-    inner) against the oracle.
+    8 layers, vocab 7, scored with the fp32 master model as the reference does: token log-probs and masks
+    finite everywhere, and eight sequences (first, last and six inner) against the oracle's autocast mode.
 
-    Bar 2 per token (2e-2 abs) holds at the small shapes (test_teacher_forced_logprobs_parity). At 3072
-    positions x 8 layers the bf16 rounding points alone spread a token's log-prob by sigma ~ 9e-3: two
-    restatements of the reference that differ in ONE rounding point (attention weights rounded to bf16 before
-    the PV product, as flash-attention does, or not) already disagree by up to ~4e-2 with ~4% of the tokens
-    beyond 2e-2. So here the HIP path must be indistinguishable from that noise:
-      * against the oracle (fused rounding points): |dlp| <= 2e-2 on >= 95% of the masked tokens, and the
-        max / mean / fraction beyond 2e-2 within 1.5x / 1.15x / 1.5x of the oracle pair's own;
-      * against fp32: no further off than the oracle's bf16 mode (max, mean, fraction beyond 2e-2 within 1.15x);
-      * the GSPO ratio (bar 2 on ratios): per sequence, exp(mean_t(lp - lp_oracle)) within 2e-3 of 1."""
+    At 3072 positions x 8 layers, bf16 rounding alone spreads a token's log-prob: two restatements of the
+    reference's scoring numerics that differ only in how the attention weights are rounded (against the row's final
+    maximum, or blockwise as flash-attention's tiles do) disagree by up to ~3e-2, with ~0.15% of the tokens beyond
+    2e-2. Bar 2 is asserted with that noise as the stated exemption (the count of tokens beyond 2e-2 bounded by the
+    pair's, the largest excursion and the mean by the pair's); the GSPO ratio per sequence within 1e-3 and within 2x
+    the pair's; and the same sequences through a bf16 residual stream (the inference path's rounding points) must
+    fail the bar, so the test tells the two numerics apart."""
     from viktor_amd.synthetic import scoring_inputs
     m = make_model(1, n_layers=8, seed=14, norm_jitter=0.1, bias_jitter=0.1)
-    gm = gpu_copy(m)
+    gm = master_copy(m)
     B, P = 512, 2048
     seqs, ended = scoring_inputs(B, 700, 1024, k=1, seed=15)
     gen = torch.Generator(device=DEV)
@@ -374,37 +396,68 @@ def test_scoring_at_scale():
     assert lp.shape[0] == B and bool(torch.isfinite(lp[mask]).all())
     n_tok = mask.sum(1)
     assert n_tok.tolist() == [len(s) + 1 for s in seqs]  # every base + the EOS of an ended call (k = 1)
-    pick = [0, 171, 342, B - 1]
-    tin, tgt, _ = m.batch([seqs[i] for i in pick], pad_to=128)
-    f, pl = fr[pick].cpu(), plens[pick].cpu()
-    l16 = R.token_logprobs_ref(R.RefModel(m, "fused").logits(f, tin, pl), tgt)
-    l16p = R.token_logprobs_ref(R.RefModel(m, "fused", p_bf16=True).logits(f, tin, pl), tgt)
-    l32 = R.token_logprobs_ref(R.RefModel(m, "fp32").logits(f, tin, pl), tgt)
-    m_ref = R.sampled_mask_ref(tgt, [seqs[i] for i in pick], [ended[i] for i in pick], 1)
-    T = l16.shape[1]
+    pick = [0, 73, 146, 219, 292, 365, 438, B - 1]
+    sub = [seqs[i] for i in pick]
+    tin, tgt, _ = m.batch(seqs, pad_to=128)  # the batch's own padded width, so the picked rows are those scored
+    tin, tgt = tin[pick], tgt[pick]
+    f = fr[pick].cpu()
+    ref = R.RefModel(m, "autocast")
+    u = ref.logits(f, tin, None, round_logits=False)  # the oracle's fp32 head products, before the bf16 rounding
+    zo = R.bf(u)
+    lo = R.token_logprobs_ref(zo, tgt)
+    m_ref = R.sampled_mask_ref(tgt, sub, [ended[i] for i in pick], 1)
+    T = lo.shape[1]
     got = lp[pick][:, :T].cpu()
     assert torch.equal(mask[pick][:, :T].cpu(), m_ref)
+    with torch.no_grad():
+        # the picked windows alone give the same log-probs as inside the 512-sequence batch (rows are independent)
+        zh = gm.logits(fr[pick], tin.to(DEV), None)
+        lp_alone = G.ops.gspo_score(zh.contiguous(), tgt.clamp(min=0).to(DEV))["lp"].cpu()
+        hh = gm.hidden(fr[pick], tin.to(DEV), None)
+        uh = G.ops.linear(hh, gm.decoder.fast().w(gm.decoder.lm_head.weight), out_dtype=torch.float32)
+        uh = uh.view(len(pick), T, -1).cpu()
+        lb = G.ops.gspo_score(bf16_residual_logits(gm, fr[pick], tin.to(DEV)).contiguous(),
+                              tgt.clamp(min=0).to(DEV))["lp"].cpu()
+    assert torch.equal(lp_alone[:, :T], got)
+    n_bases = torch.tensor([max(len(x), 1) for x in sub], dtype=torch.float64)
 
-    def spread(a, b):
-        d = (a - b)[m_ref].abs()
-        return float(d.max()), float(d.mean()), float((d > 2e-2).float().mean())
+    def stats(a):
+        dd = (a - lo)[m_ref].abs()
+        lr = torch.stack([(a - lo)[b][m_ref[b]].double().sum() for b in range(len(pick))]) / n_bases
+        return dd, lr
 
-    hip_or, pair, hip_32, or_32 = spread(got, l16), spread(l16p, l16), spread(got, l32), spread(l16, l32)
-    print("scoring (max, mean, frac > 2e-2): HIP-oracle %s, oracle pair %s, HIP-fp32 %s, oracle-fp32 %s" % tuple(
-        "(%.2e, %.2e, %.3f)" % t for t in (hip_or, pair, hip_32, or_32)))
-    assert hip_or[2] <= 0.05, hip_or
-    assert hip_or[0] <= 1.5 * pair[0] and hip_or[1] <= 1.15 * pair[1] and hip_or[2] <= 1.5 * pair[2] + 1e-3
-    assert hip_32[0] <= 1.15 * or_32[0] and hip_32[1] <= 1.15 * or_32[1] and hip_32[2] <= 1.15 * or_32[2] + 1e-3
-    # bar 2 as stated, with the exemption as a rule: tokens where the oracles themselves (fused vs fp32, fused vs
-    # its bf16-weights pair) are more than 2e-2 apart are exempt; everywhere else |HIP - oracle| <= 2e-2
-    agree = m_ref & ((l16 - l32).abs() <= 2e-2) & ((l16p - l16).abs() <= 2e-2)
-    d_strict = (got - l16)[agree].abs()
-    print("bar 2 where the oracles agree: %d of %d tokens checked (%d exempt), max |HIP - oracle| %.2e, %d beyond 2e-2"
-          % (int(agree.sum()), int(m_ref.sum()), int(m_ref.sum() - agree.sum()), float(d_strict.max()),
-             int((d_strict > 2e-2).sum())))
-    log_ratio = torch.stack([(got - l16)[b][m_ref[b]].mean() for b in range(len(pick))])
-    print("per-sequence mean lp - oracle:", ["%.1e" % float(x) for x in log_ratio])
-    assert float((log_ratio.exp() - 1).abs().max()) <= 2e-3
+    d, log_ratio = stats(got)
+    # the reference's own rounding noise: the same autocast restatement with flash-attention's blockwise rounding of
+    # the attention weights (128-key blocks, last to first) instead of the rounding against each row's final maximum
+    lo2 = R.token_logprobs_ref(R.RefModel(m, "autocast", attn_block=128).logits(f, tin, None), tgt)
+    dp, log_ratio_p = stats(lo2)
+    d_pre = (R.token_logprobs_ref(uh, tgt) - R.token_logprobs_ref(u, tgt))[m_ref].abs()
+    db, log_ratio_b = stats(lb)
+    n = int(m_ref.sum())
+    beyond, beyond_p = int((d > 2e-2).sum()), int((dp > 2e-2).sum())
+    print("scoring vs the autocast oracle over %d tokens of %d sequences (max, mean, beyond 2e-2, per-sequence "
+          "|log ratio| max):\n"
+          "  HIP                  %.2e %.2e %4d %.1e\n"
+          "  oracle pair          %.2e %.2e %4d %.1e\n"
+          "  bf16-residual path   %.2e %.2e %4d %.1e\n"
+          "  HIP before the logits' bf16 rounding (fp32 head products): %.2e %.2e"
+          % (n, len(pick), float(d.max()), float(d.mean()), beyond, float(log_ratio.abs().max()),
+             float(dp.max()), float(dp.mean()), beyond_p, float(log_ratio_p.abs().max()),
+             float(db.max()), float(db.mean()), int((db > 2e-2).sum()), float(log_ratio_b.abs().max()),
+             float(d_pre.max()), float(d_pre.mean())))
+    # bar 2 (2e-2) on every masked token, with the reference's own rounding noise as the stated exemption: no more
+    # tokens beyond the bar than twice the count of the oracle pair (two faithful restatements of the same
+    # numerics) or 0.2% of the tokens, and none beyond it by more than the pair's own largest excursion allows
+    assert beyond <= max(2 * beyond_p, 2e-3 * n), (beyond, beyond_p)
+    assert float(d.max()) <= min(1.5 * float(dp.max()), 3e-2), (float(d.max()), float(dp.max()))
+    # indistinguishable from that noise on average
+    assert float(d.mean()) <= 1.25 * float(dp.mean()), (float(d.mean()), float(dp.mean()))
+    # the ratio: the factor by which each sequence's s moves, within 1e-3 and within 2x the pair's (1e-4, the bar of
+    # the fp32 reductions, holds for the ratio given the log-probs: test_scoring_loss_and_gradient_at_scale)
+    assert float((log_ratio.exp() - 1).abs().max()) <= 1e-3
+    assert float(log_ratio.abs().max()) <= 2 * float(log_ratio_p.abs().max()) + 1e-4
+    # and the bar tells a bf16 residual stream apart
+    assert int((db > 2e-2).sum()) > max(2 * beyond_p, 2e-3 * n) and float(db.mean()) > 1.25 * float(dp.mean())
 
 
 def test_scoring_loss_and_gradient_at_scale():

@@ -724,6 +724,90 @@ def test_rmsnorm_apply_paths(n, d, nb):
     assert ok, err
 
 
+@pytest.mark.parametrize("M,K,alpha,bias", [(4500, 512, 1.0, False), (300, 1536, 1.0, False), (700, 512, 0.5, True)])
+def test_linear_residual_big_fp32_stream(M, K, alpha, bias):
+    """The autocast residual add on an fp32 stream: x = alpha x + bf16(a w^T + b) in place (fp32), bit for bit
+    against the same product's fp32 accumulator (and that against fp64), the per-64-column sums of squares of the
+    new fp32 values, then the norm from those sums with fp32 weights (rmsnorm_apply) and the norm that takes its own
+    sums (rmsnorm_f32), each against fp64 with one bf16 rounding."""
+    g = gen(M + K + 1)
+    N = 512
+    a = R.bf(torch.randn(M, K, generator=g))
+    w = R.bf(torch.randn(N, K, generator=g) / math.sqrt(K))
+    x = torch.randn(M, N, generator=g) * 2  # fp32 values, not bf16
+    b = R.bf(0.1 * torch.randn(N, generator=g)) if bias else None
+    nw = torch.rand(N, generator=g) + 0.5  # fp32 master weights
+    xd = to_dev(x)
+    ss = ops.linear_residual_big(to_dev(a, BF), to_dev(w, BF), xd, bias=None if b is None else to_dev(b), alpha=alpha)
+    # the same kernel's fp32 accumulator (its fp32-output epilogue): the residual is then exact --
+    # alpha x + bf16(acc + b) with one fp32 rounding (alpha is a power of two here, so alpha x is exact)
+    from viktor_amd._lib import call, ptr, stream_handle
+    ad, wd = to_dev(a, BF), to_dev(w, BF)
+    acc32 = torch.empty(M, N, dtype=torch.float32, device=DEV)
+    call("vk_gemm_rows", ptr(ad), ptr(wd), ptr(acc32), M, N, K, 1, stream_handle())  # the large-M kernel, fp32 out
+    acc32 = acc32.cpu()
+    prod = R.bf(acc32 + (0 if b is None else b))
+    got = xd.cpu().double()
+    assert torch.equal(xd.cpu(), alpha * x + prod)
+    acc = a.double() @ w.double().t()
+    assert torch.allclose(acc32.double(), acc, rtol=1e-5, atol=1e-5)
+    ss_ref = (got * got).view(M, N // 64, 64).sum(-1)
+    assert torch.allclose(ss.cpu().double(), ss_ref, rtol=1e-5, atol=1e-6)
+    ref_h = R.bf(F.rms_norm(xd.cpu(), (N,), nw, 1e-6))
+    for h in (ops.rmsnorm_apply(xd, ss, to_dev(nw), 1e-6), ops.rmsnorm_f32(xd, to_dev(nw), 1e-6)):
+        assert h.dtype == BF
+        ok, err = bf_close(h, ref_h, ulps=1, atol=1e-5)
+        assert ok, err
+
+
+@pytest.mark.parametrize("n,d", [(1, 512), (333, 512), (40, 256), (17, 1536), (5, 64)])
+def test_rmsnorm_f32(n, d):
+    """bf16(x rsqrt(mean x^2 + eps) w) of fp32 x and w: one rounding of the fp64 value (1 ulp)."""
+    g = gen(n * d)
+    x = torch.randn(n, d, generator=g) * 3
+    w = torch.rand(d, generator=g) + 0.5
+    h = ops.rmsnorm_f32(to_dev(x), to_dev(w), 1e-6)
+    xd = x.double()
+    want = xd * torch.rsqrt((xd * xd).mean(-1, keepdim=True) + 1e-6) * w.double()
+    ok, err = bf_close(h, want.float(), ulps=1, atol=1e-6)
+    assert ok, err
+
+
+@pytest.mark.parametrize("M", [300, 4500])
+def test_linear_qkv_rope_fp32_norm_weights(M):
+    """The autocast Wqkv stage: fp32 QK-norm weights that bf16 cannot hold and fp32 tables -- bf16(x / rms * w) with
+    the fp32 weight, then the rotation rounded to bf16 -- against the oracle's composition, and against the unfused
+    pair (linear, then qkv_rope_cache with the same fp32 weights)."""
+    g = gen(M + 77)
+    H, HKV, D, K = 8, 2, 64, 512
+    x = R.bf(torch.randn(M, K, generator=g) * 2)
+    wq = R.bf(torch.randn((H + 2 * HKV) * D, K, generator=g) / math.sqrt(K))
+    qw = 1 + 0.1 * torch.randn(D, generator=g)
+    kw = 1 + 0.1 * torch.randn(D, generator=g)
+    assert not torch.equal(R.bf(qw), qw)
+    cos, sin = R.rope_tables(D, 4096, 1e6)
+    rpos = torch.randint(0, 4096, (M,), generator=g).int()
+    pos = torch.arange(M).int()
+    q, k, v = ops.linear_qkv_rope(to_dev(x, BF), to_dev(wq, BF), to_dev(qw), to_dev(kw), to_dev(cos), to_dev(sin),
+                                  to_dev(pos), None, None, None, 1e-6, H, HKV, D, return_kv=True, rope_pos=to_dev(rpos))
+    qkv = R.linear_fused(x, wq).view(M, H + 2 * HKV, D)
+    rp = rpos.long()
+    for got, part, nw in ((q, qkv[:, :H], qw), (k, qkv[:, H:H + HKV], kw)):
+        ok, err = bf_close(got, R.qk_norm_rope_fused(part, nw, cos[rp], sin[rp], 1e-6), ulps=4, atol=4e-2)
+        assert ok, err
+    # with the weights rounded to bf16 instead, some values move: the fp32 weights are used as given
+    qb = ops.linear_qkv_rope(to_dev(x, BF), to_dev(wq, BF), to_dev(qw, BF), to_dev(kw, BF), to_dev(cos), to_dev(sin),
+                             to_dev(pos), None, None, None, 1e-6, H, HKV, D, return_kv=True, rope_pos=to_dev(rpos))[0]
+    assert not torch.equal(qb, q)
+    qkv_d = ops.linear(to_dev(x, BF), to_dev(wq, BF))
+    q2, k2, v2 = ops.qkv_rope_cache(qkv_d, to_dev(qw), to_dev(kw), to_dev(cos), to_dev(sin), to_dev(pos), None, None,
+                                    None, 1e-6, H, HKV, D, return_kv=True, rope_pos=to_dev(rpos))
+    assert torch.equal(v2, v)
+    for a, b in ((q, q2), (k, k2)):
+        d = (a.float() - b.float()).abs()
+        assert (d > 0).float().mean() < 1e-3 and bf_close(a, b.float().cpu(), ulps=2, atol=2e-2)[0]
+
+
 def test_linear_qkv_rope_no_norm_in_place():
     """The encoder's use: no QK-norm, rotary positions per row, q / k / v written back into the packed qkv rows."""
     g = gen(11)

@@ -158,6 +158,44 @@ def test_oracle_teacher_forced_logits_match_reference(name):
     assert torch.allclose(lg, torch.from_numpy(z[f"{name}_logits"]), rtol=1e-4, atol=2e-5)
 
 
+@pytest.mark.parametrize("name", ["tiny_k4", "full2_k1", "tiny_k1_ps4"])
+def test_oracle_autocast_logits_near_reference_and_closer_than_fused(name):
+    """The autocast mode (the reference's scoring numerics) against the reference's fp32 golden logits: within the
+    bf16 rounding of the logits themselves (one ulp is 1.6e-2 at |z| in [2, 4)), and on average closer than the
+    fused mode -- whose bf16 residual stream rounds every block's sum -- so a restatement that let the residual
+    fall back to bf16 fails. The two modes differ on most logits."""
+    z = npz("logits.npz")
+    k, seed, ps, d_enc = [int(v) for v in z[f"{name}_meta"]]
+    cfg = TINY if name.startswith("tiny") else FULL2
+    m = make_model(k, seed=seed, d_enc=d_enc, norm_jitter=0.1, bias_jitter=0.1, **cfg)
+    m.pos_scale = ps
+    tin, _, _ = m.batch([str(s) for s in z[f"{name}_seqs"]], pad_to=8)
+    gold = torch.from_numpy(z[f"{name}_logits"])
+    fr, pl = torch.from_numpy(z[f"{name}_frames"]), torch.from_numpy(z[f"{name}_plens"])
+    ac = R.RefModel(m, "autocast").logits(fr, tin, pl)
+    fu = R.RefModel(m, "fused").logits(fr, tin, pl)
+    assert torch.equal(ac, R.bf(ac))  # bf16 logits
+    e_ac, e_fu = (ac - gold).abs(), (fu - gold).abs()
+    assert float(e_ac.max()) < 3e-2, float(e_ac.max())
+    assert float(e_ac.mean()) < 0.85 * float(e_fu.mean()), (float(e_ac.mean()), float(e_fu.mean()))
+    assert float((ac != fu).float().mean()) > 0.3
+
+
+def test_oracle_autocast_parameters():
+    """What autocast casts: every nn.Linear weight and bias of the projector and decoder is used as its bf16
+    rounding; the RMSNorm weights (QK-norm included), the embedding and the rotary tables stay fp32."""
+    m = make_model(4, seed=3, norm_jitter=0.1, bias_jitter=0.1, **FULL2)
+    ref = R.RefModel(m, "autocast")
+    for n, p in m.named_parameters():
+        want = p.detach().float()
+        if n.endswith("bias") or (p.dim() == 2 and not n.endswith("embed.weight")):
+            want = R.bf(want)
+        assert torch.equal(ref.p[n], want), n
+    assert any(not torch.equal(R.bf(p), p) for n, p in m.named_parameters() if "norm" in n)
+    cos, sin = rope_tables(64, 4096, 1e6)
+    assert torch.equal(ref.cos, cos) and torch.equal(ref.sin, sin)
+
+
 # ---- closed forms / brute force for the fused-mode ops ---------------------------------------------
 def test_fused_rmsnorm_closed_form():
     g = torch.Generator().manual_seed(0)
@@ -242,6 +280,37 @@ def test_attention_rows_bf16_weights_brute_force():
     ke = k[:1].expand(7, 2, 64)
     oe = R.attention_rows(q[:1], ke, v, p_bf16=True)
     assert torch.allclose(oe[0], v.mean(0).repeat_interleave(4, 0), atol=1e-6)
+
+
+def test_attention_rows_blockwise_bf16_weights_brute_force():
+    """block: each query row's keys in blocks visited from the last to the first; a block's weights are
+    bf16(exp(s - m_b)) with m_b the running max after that block, the accumulator and the fp32 normaliser rescaled
+    by exp(m_old - m_b). Brute force per row in fp64 of that recurrence; one block covering every key equals the
+    final-maximum rounding exactly; causal rows whose first visited blocks are fully masked."""
+    g = torch.Generator().manual_seed(13)
+    q = torch.randn(20, 8, 64, generator=g)
+    k = torch.randn(45, 2, 64, generator=g) * 2
+    v = torch.randn(45, 2, 64, generator=g)
+    o = R.attention_rows(q, k, v, causal_shift=25, p_bf16=True, block=8)
+    for r in (0, 7, 19):
+        for h in (0, 5):
+            n = 25 + r + 1
+            s = (q[r, h].double() @ k[:n, h // 4].double().t()) / 8.0
+            m, l, acc = -math.inf, 0.0, torch.zeros(64, dtype=torch.float64)
+            for b0 in reversed(range(0, 45, 8)):
+                sb = s[b0:min(b0 + 8, n)]
+                if sb.numel() == 0:
+                    continue
+                mb = max(m, float(sb.max()))
+                sc = math.exp(m - mb) if m > -math.inf else 0.0
+                e = torch.exp(sb - mb)
+                l = l * sc + float(e.sum())
+                acc = acc * sc + e.float().to(torch.bfloat16).double() @ v[b0:b0 + sb.numel(), h // 4].double()
+                m = mb
+            assert torch.allclose(o[r, h].double(), acc / l, atol=2e-6)
+    whole = R.attention_rows(q, k, v, causal_shift=25, p_bf16=True, block=64)
+    assert torch.allclose(whole, R.attention_rows(q, k, v, causal_shift=25, p_bf16=True), atol=1e-6)
+    assert 0 < float((o - whole).abs().max()) < 2e-2
 
 
 def test_swiglu_fused_closed_form():

@@ -84,12 +84,33 @@ def test_rmsnorm_backward():
         assert torch.allclose(dw.cpu(), ww.grad, rtol=1e-4, atol=1e-3)
 
 
-def test_qknorm_rope_backward():
+def test_rmsnorm_backward_fp32_stream():
+    """The autocast forward's norms: fp32 x (the residual stream) and fp32 weights, with bf16 and fp32 dy."""
+    g = gen(15)
+    n = 133
+    x = torch.randn(n, 512, generator=g) * 2
+    w = 1 + 0.1 * torch.randn(512, generator=g)
+    dy = torch.randn(n, 512, generator=g)
+    dres = torch.randn(n, 512, generator=g)
+    for dy_use in (dy, dy.to(BF).float()):
+        xx = x.clone().requires_grad_(True)
+        ww = w.clone().requires_grad_(True)
+        (F.rms_norm(xx, (512,), ww, 1e-6) * dy_use).sum().backward()
+        dy_dev = dy_use.to(DEV) if dy_use is dy else dy_use.to(BF).to(DEV)
+        dx, dw = ops.rmsnorm_backward(x.to(DEV), w.to(DEV), dy_dev, 1e-6, dres=dres.to(DEV).clone())
+        assert torch.allclose(dx.cpu(), xx.grad + dres, rtol=1e-4, atol=1e-4)
+        assert torch.allclose(dw.cpu(), ww.grad, rtol=1e-4, atol=1e-3)
+
+
+@pytest.mark.parametrize("wdtype", ["bf16", "f32"])
+def test_qknorm_rope_backward(wdtype):
     g = gen(6)
     n, H, HKV = 50, 8, 2
     qkv = (torch.randn(n, (H + 2 * HKV) * 64, generator=g) * 2).to(BF)
-    wq = (torch.rand(64, generator=g) + 0.5).to(BF)
-    wk = (torch.rand(64, generator=g) + 0.5).to(BF)
+    wq = (torch.rand(64, generator=g) + 0.5)
+    wk = (torch.rand(64, generator=g) + 0.5)
+    if wdtype == "bf16":
+        wq, wk = wq.to(BF), wk.to(BF)
     cos, sin = R.rope_tables(64, 4096, 1e6)
     rpos = torch.randint(0, 4096, (n,), generator=g).int()
     dq = torch.randn(n, H, 64, generator=g)
@@ -342,6 +363,21 @@ def test_embed_grad_against_fp64(n, V, d):
         tok[3], tok[7] = V, -1  # out of range: ignored
     rows = torch.randn(n, d, generator=g).to(BF)
     got = ops.embed_grad(rows.to(DEV), tok.to(DEV), V).cpu().double()
+    if n > 10:  # an id that only its low 32 bits would put in range is ignored too
+        tok2 = tok.clone()
+        tok2[5] = (1 << 32) + 3
+        keep2 = (tok2 >= 0) & (tok2 < V)
+        want2 = torch.zeros(V, d, dtype=torch.float64).index_add_(0, tok2[keep2], rows[keep2].double())
+        got2 = ops.embed_grad(rows.to(DEV), tok2.to(DEV), V).cpu().double()
+        assert torch.allclose(got2, want2, rtol=0, atol=1e-4)
+        # fp32 gradient rows (the autocast forward's fp32 residual gradient): fp32 sums of the fp32 rows
+        r32 = torch.randn(n, d, generator=g)
+        g32 = ops.embed_grad(r32.to(DEV), tok.to(DEV), V).cpu().double()
+        w32 = torch.zeros(V, d, dtype=torch.float64).index_add_(0, tok[(tok >= 0) & (tok < V)],
+                                                              r32[(tok >= 0) & (tok < V)].double())
+        s32 = torch.zeros(V, d, dtype=torch.float64).index_add_(0, tok[(tok >= 0) & (tok < V)],
+                                                              r32[(tok >= 0) & (tok < V)].double().abs())
+        assert bool(((g32 - w32).abs() <= s32 * 2.0 ** -20).all())
     keep = (tok >= 0) & (tok < V)
     want = torch.zeros(V, d, dtype=torch.float64).index_add_(0, tok[keep], rows[keep].double())
     scale = torch.zeros(V, d, dtype=torch.float64).index_add_(0, tok[keep], rows[keep].double().abs())

@@ -30,7 +30,7 @@ SIGNATURES = {
     "vk_device_cus": [],
     "vk_add_rmsnorm": [_P, _P, _P, _P, _I64, _I32, _F, _P],
     "vk_embed_rmsnorm": [_P, _P, _I64, _P, _P, _P, _I64, _I32, _F, _P],
-    "vk_qkv_rope_cache": [_P, _P, _P, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P,
+    "vk_qkv_rope_cache": [_P, _P, _P, _I32, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P,
                           _I64, _F, _I32, _I32, _I32, _P],
     "vk_linear": [_P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P],
     "vk_swiglu": [_P, _P, _I64, _I32, _P],
@@ -58,11 +58,12 @@ SIGNATURES = {
     "vk_act_backward_blocks": [_I64, _I32, ctypes.POINTER(_I32)],
     "vk_act_backward": [_P, _P, _P, _P, _I32, _I64, _I32, _I32, _P],
     "vk_embed_grad_workspace": [_I64, _I32, _I32, ctypes.POINTER(_I64)],
-    "vk_embed_grad": [_P, _I64, _P, _I64, _I32, _I32, _P, _P, _I64, _P],
+    "vk_embed_grad": [_P, _I32, _I64, _P, _I64, _I32, _I32, _P, _P, _I64, _P],
     "vk_rmsnorm_backward_blocks": [_I64, ctypes.POINTER(_I32)],
-    "vk_rmsnorm_backward": [_P, _P, _P, _I32, _P, _P, _P, _I64, _I32, _F, _P],
+    "vk_rmsnorm_backward": [_P, _I32, _P, _I32, _P, _I32, _P, _P, _P, _I64, _I32, _F, _P],
     "vk_colsum": [_P, _P, _I32, _I32, _I32, _P],
-    "vk_qknorm_rope_backward": [_P, _P, _P, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _F, _P],
+    "vk_qknorm_rope_backward": [_P, _P, _P, _I32, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _F,
+                                _P],
     "vk_swiglu_backward": [_P, _P, _P, _I64, _I32, _P],
     "vk_grad_norm_clip": [_P, _I64, _F, _P, _I32, _P, _P],
     "vk_adamw": [_P, _P, _P, _P, _I64, _P, _F, _F, _F, _F, _F, _I64, _P],
@@ -73,9 +74,10 @@ SIGNATURES = {
     "vk_deepnorm_rmsnorm": [_P, _P, _P, _F, _P, _F, _I64, _I32, _P],
     "vk_gemm_rows": [_P, _P, _P, _I64, _I32, _I32, _I32, _P],
     "vk_group_rows_equal": [_P, _I64, _I32, _I64, _P, _P],
-    "vk_linear_residual_big": [_P, _P, _P, _I64, _I32, _I32, _P, _F, _P, _P],
-    "vk_rmsnorm_apply_ss": [_P, _P, _I32, _P, _P, _I64, _I32, _F, _P],
-    "vk_linear_qkv_rope": [_P, _P, _I64, _I32, _P, _P, _F, _P, _P, _I32, _I64, _P, _P, _P, _P, _I64, _P, _P, _I64, _I64,
+    "vk_linear_residual_big": [_P, _P, _P, _I32, _I64, _I32, _I32, _P, _F, _P, _P],
+    "vk_rmsnorm_apply_ss": [_P, _I32, _P, _I32, _P, _I32, _P, _I64, _I32, _F, _P],
+    "vk_rmsnorm_f32": [_P, _P, _P, _I64, _I32, _F, _P],
+    "vk_linear_qkv_rope": [_P, _P, _I64, _I32, _P, _P, _I32, _F, _P, _P, _I32, _I64, _P, _P, _P, _P, _I64, _P, _P, _I64, _I64,
                            _I64, _I64, _P, _P, _I64, _I32, _I32, _I32, _P],
 }
 

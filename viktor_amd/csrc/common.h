@@ -50,6 +50,28 @@ __device__ __forceinline__ uint32_t pack_bf(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v));
 }
 
+// Eight consecutive row elements as loaded (bf16: one 16-byte load; fp32: two), unpacked to fp32 on use, so a
+// kernel can issue every row's loads before it reads the first one.
+template <typename T>
+struct Raw8;
+template <>
+struct Raw8<bf16_t> {
+  u32x4 v;
+  __device__ __forceinline__ void load(const bf16_t *p) { v = *reinterpret_cast<const u32x4 *>(p); }
+  __device__ __forceinline__ void zero() { v = u32x4{0u, 0u, 0u, 0u}; }
+  __device__ __forceinline__ float get(int k) const { return (k & 1) ? hi_bf(v[k >> 1]) : lo_bf(v[k >> 1]); }
+};
+template <>
+struct Raw8<float> {
+  f32x4 a, b;
+  __device__ __forceinline__ void load(const float *p) {
+    a = *reinterpret_cast<const f32x4 *>(p);
+    b = *reinterpret_cast<const f32x4 *>(p + 4);
+  }
+  __device__ __forceinline__ void zero() { a = b = f32x4{0.f, 0.f, 0.f, 0.f}; }
+  __device__ __forceinline__ float get(int k) const { return k < 4 ? a[k] : b[k - 4]; }
+};
+
 // Butterfly reductions over the 64 lanes of a wavefront (every lane gets the result).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

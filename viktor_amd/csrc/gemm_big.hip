@@ -56,11 +56,18 @@ constexpr int vmcnt_imm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((
 // ss_out[row, col / 64] receives the fp32 sum of squares of the row's new bf16 values over each 64-column block
 // (the RMSNorm that follows reads them instead of a pass of its own over the row).
 // GB_QKV reads fp32 rotary tables, GB_QKV_BF16 bf16 ones (the table type is a compile-time choice, so the epilogue's
-// prefetched table registers are not merged across two load shapes)
-enum GbEpi { GB_BF16 = 0, GB_F32 = 1, GB_SWIGLU = 2, GB_QKV = 3, GB_RESID = 4, GB_QKV_BF16 = 5 };
+// prefetched table registers are not merged across two load shapes); both take bf16 QK-norm weights. GB_QKV_W32 is
+// GB_QKV with fp32 QK-norm weights: nn.RMSNorm under torch.autocast bf16 with fp32 master weights, which returns
+// bf16(x / rms * w) for a bf16 head (the multiply by w in fp32, one rounding), before the fp32 rotation.
+//
+// GB_RESID_F32: y is an fp32 residual stream updated in place, y = alpha y + bf16(acc + bias): the autocast residual
+// add x + sublayer(x) of an fp32 stream and a bf16 product (viktor/decoder.py:118-120 under torch.autocast bf16);
+// ss_out as GB_RESID, over the new fp32 values.
+enum GbEpi { GB_BF16 = 0, GB_F32 = 1, GB_SWIGLU = 2, GB_QKV = 3, GB_RESID = 4, GB_QKV_BF16 = 5, GB_RESID_F32 = 6,
+             GB_QKV_W32 = 7 };
 
 struct GbQkv {
-  const bf16_t *qw, *kw;  // per-head RMSNorm weights [64] (both NULL: no norm)
+  const void *qw, *kw;  // per-head RMSNorm weights [64], bf16 (fp32 for GB_QKV_W32); both NULL: no norm
   float eps;
   const void *cos_t, *sin_t;  // [table_rows, 32], fp32 (table_f32) or bf16
   int table_f32;
@@ -85,7 +92,9 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
                                                           int tiles_total, const GbQkv qa) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr bool SWIGLU = EPI == GB_SWIGLU, OUT_F32 = EPI == GB_F32, RESID = EPI == GB_RESID;
-  constexpr bool QKV = EPI == GB_QKV || EPI == GB_QKV_BF16, TAB_F32 = EPI == GB_QKV;
+  constexpr bool RESID32 = EPI == GB_RESID_F32;
+  constexpr bool QKV = EPI == GB_QKV || EPI == GB_QKV_BF16 || EPI == GB_QKV_W32;
+  constexpr bool TAB_F32 = EPI == GB_QKV || EPI == GB_QKV_W32, W32 = EPI == GB_QKV_W32;
   // wid through readfirstlane: wave-uniform for the compiler, so branches on the wavefront's quadrant or head are scalar
   const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wid >> 1, wn = wid & 1;
@@ -206,12 +215,30 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
   // positions, go one group ahead inside the loop).
   const int fr_e = lane & 15, fg_e = lane >> 4;
   u32x2 res_old[RESID ? 8 : 1][4];
-  f32x4 res_b4[RESID ? 4 : 1];
-  u32x2 qk_nw[QKV ? 4 : 1];
+  f32x4 res_b4[(RESID || RESID32) ? 4 : 1];
+  // GB_RESID_F32: the old fp32 residual of two 16-row groups (the current one and the next, loaded one group ahead;
+  // all 8 would take 128 registers beside the accumulators)
+  f32x4 r32_old[RESID32 ? 2 : 1][4];
+  auto r32_load = [&](int j, f32x4 (&dst)[4]) {
+    int64_t rrow = m0 + wm * 128 + 16 * j + fr_e;
+    rrow = rrow < M ? rrow : M - 1;
+    const float *yrow = static_cast<const float *>(y) + rrow * N + n0 + wn * 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = *reinterpret_cast<const f32x4 *>(yrow + 16 * i + 4 * fg_e);
+  };
+  using NwT = typename std::conditional<W32, f32x4, u32x2>::type;
+  NwT qk_nw[QKV ? 4 : 1];
   int qk_rp[QKV ? 8 : 1];
   const int qk_hd = (n0 + wn * 64) >> 6;  // GB_QKV: this wavefront's head (64 columns, wave-uniform)
   const bool qk_rot = QKV && qk_hd < qa.H + qa.HKV;
-  const bf16_t *qk_w = QKV ? (qk_hd < qa.H ? qa.qw : qa.kw) : nullptr;
+  const void *qk_w = QKV ? (qk_hd < qa.H ? qa.qw : qa.kw) : nullptr;
+  if (RESID32) {
+    r32_load(0, r32_old[0]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      res_b4[i] = qa.bias != nullptr ? *reinterpret_cast<const f32x4 *>(qa.bias + n0 + wn * 64 + 16 * i + 4 * fg_e)
+                                     : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   if (RESID) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -229,7 +256,12 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
   if (qk_rot) {
     if (qk_w != nullptr) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) qk_nw[i] = *reinterpret_cast<const u32x2 *>(qk_w + 16 * i + 4 * fg_e);
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (W32)
+          qk_nw[i] = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(qk_w) + 16 * i + 4 * fg_e);
+        else
+          qk_nw[i] = *reinterpret_cast<const u32x2 *>(static_cast<const bf16_t *>(qk_w) + 16 * i + 4 * fg_e);
+      }
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -258,11 +290,11 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
   TabT qk_c[2][2], qk_s[2][2];  // two row groups' table entries: the current one and the next
   if (qk_rot) qk_tables(0, qk_c[0], qk_s[0]);
   __syncthreads();  // every wavefront has finished reading the ring
-  constexpr int ESZ = OUT_F32 ? 4 : 2;                // output element bytes
+  constexpr int ESZ = (OUT_F32 || RESID32) ? 4 : 2;   // output element bytes
   constexpr int QCOLS = SWIGLU ? 32 : 64;             // output columns of a wavefront
   constexpr int RB = QCOLS * ESZ;                     // bytes of one quadrant row
   constexpr int PITCH = RB + 16;
-  constexpr int PASS_ROWS = OUT_F32 ? 64 : 128;       // rows staged per pass (<= GB_SMEM / 4 bytes)
+  constexpr int PASS_ROWS = ESZ == 4 ? 64 : 128;      // rows staged per pass (<= GB_SMEM / 4 bytes)
   constexpr int CPR = RB / 16;                        // 16-byte chunks per row
   static_assert(PASS_ROWS * PITCH <= static_cast<int>(GB_SMEM / 4), "epilogue staging exceeds a quarter of LDS");
   char *stg = smem + wid * (GB_SMEM / 4);
@@ -297,6 +329,26 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
         ss += __shfl_xor(ss, 16, 64);  // the row's other 48 columns of this block: lanes fr + 16, + 32, + 48
         ss += __shfl_xor(ss, 32, 64);
         if (live && fg == 0) qa.ss_out[rrow * (N >> 6) + (qcol0 >> 6)] = ss;
+      } else if (RESID32) {
+        // lane: row 16 j + fr, columns qcol0 + 16 i + 4 fg + e (the same elements r32_load read for it)
+        if (j + 1 < 8) r32_load(j + 1, r32_old[(j + 1) & 1]);
+        const int64_t rrow = qrow0 + 16 * j + fr;
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 old = r32_old[j & 1][i];
+          const f32x4 b4 = res_b4[i];
+          f32x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            o[e] = qa.alpha * old[e] + round_bf(acc[i][j][e] + b4[e]);
+            ss += o[e] * o[e];
+          }
+          *reinterpret_cast<f32x4 *>(rowp + (16 * i + 4 * fg) * 4) = o;
+        }
+        ss += __shfl_xor(ss, 16, 64);
+        ss += __shfl_xor(ss, 32, 64);
+        if (rrow < M && fg == 0) qa.ss_out[rrow * (N >> 6) + (qcol0 >> 6)] = ss;
       } else if (QKV) {
         // this wavefront's 64 columns are one head (wave-uniform); lane: row 16 j + fr, columns 16 i + 4 fg + e
         const int hd = qcol0 >> 6;
@@ -321,8 +373,12 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
             for (int i = 0; i < 4; ++i)
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
-                const uint32_t wpair = qk_nw[i][e >> 1];
-                v[i][e] = round_bf(v[i][e] * r * ((e & 1) ? hi_bf(wpair) : lo_bf(wpair)));
+                float wv;
+                if constexpr (W32)
+                  wv = qk_nw[i][e];
+                else
+                  wv = (e & 1) ? hi_bf(qk_nw[i][e >> 1]) : lo_bf(qk_nw[i][e >> 1]);
+                v[i][e] = round_bf(v[i][e] * r * wv);
               }
           }
 #pragma unroll
@@ -459,7 +515,7 @@ int gemm_big(const bf16_t *x, const bf16_t *w, void *y, int64_t M, int N, int K,
 using namespace vk;
 
 extern "C" int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32_t K, const void *q_norm_w,
-                                  const void *k_norm_w, float eps, const void *cos_t, const void *sin_t,
+                                  const void *k_norm_w, int32_t norm_w_dtype, float eps, const void *cos_t, const void *sin_t,
                                   int32_t table_dtype, int64_t table_rows, const int32_t *pos, const int32_t *rope_pos,
                                   const int32_t *seq, void *q, int64_t q_ld, void *k_cache, void *v_cache,
                                   int64_t stride_cb, int64_t stride_cs, int64_t cache_rows, int64_t cache_len,
@@ -473,6 +529,11 @@ extern "C" int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32
   VK_CHECK_ARG(M < (int64_t(1) << 31) / 256 * 256, "linear_qkv_rope: M too large");
   VK_CHECK_ARG((q_norm_w == nullptr) == (k_norm_w == nullptr), "linear_qkv_rope: q and k norm weights go together");
   VK_CHECK_ARG(table_dtype == VK_DTYPE_BF16 || table_dtype == VK_DTYPE_F32, "linear_qkv_rope: bad table dtype");
+  VK_CHECK_ARG(norm_w_dtype == VK_DTYPE_BF16 || norm_w_dtype == VK_DTYPE_F32, "linear_qkv_rope: bad norm weight dtype");
+  VK_CHECK_ARG(norm_w_dtype == VK_DTYPE_BF16 || table_dtype == VK_DTYPE_F32,
+               "linear_qkv_rope: fp32 norm weights go with fp32 rotary tables");
+  VK_CHECK_ARG(q_norm_w == nullptr || norm_w_dtype == VK_DTYPE_BF16 || (vk_aligned16(q_norm_w) && vk_aligned16(k_norm_w)),
+               "linear_qkv_rope: fp32 norm weights must be 16-byte aligned");
   VK_CHECK_ARG(table_rows > 0 && (pos != nullptr || rope_pos != nullptr), "linear_qkv_rope: rotary positions");
   VK_CHECK_ARG((k_cache == nullptr) == (v_cache == nullptr), "linear_qkv_rope: k_cache and v_cache go together");
   VK_CHECK_ARG(k_cache == nullptr || (seq != nullptr && pos != nullptr), "linear_qkv_rope: cache writes need seq and pos");
@@ -485,8 +546,8 @@ extern "C" int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32
                "linear_qkv_rope: pointers must be 16-byte aligned");
   if (M == 0) return VK_OK;
   GbQkv qa;
-  qa.qw = static_cast<const bf16_t *>(q_norm_w);
-  qa.kw = static_cast<const bf16_t *>(k_norm_w);
+  qa.qw = q_norm_w;
+  qa.kw = k_norm_w;
   qa.eps = eps;
   qa.cos_t = cos_t;
   qa.sin_t = sin_t;
@@ -508,17 +569,18 @@ extern "C" int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32
   qa.kv_ld = kv_ld;
   qa.H = n_heads;
   qa.HKV = n_kv_heads;
-  const int rc = qa.table_f32 ? launch_big<GB_QKV>(static_cast<const bf16_t *>(x), static_cast<const bf16_t *>(w), nullptr, M, N, K,
-                                    qa, VK_STREAM(stream))
-                                : launch_big<GB_QKV_BF16>(static_cast<const bf16_t *>(x), static_cast<const bf16_t *>(w), nullptr, M, N, K,
-                                    qa, VK_STREAM(stream));
+  const auto xb = static_cast<const bf16_t *>(x), wb = static_cast<const bf16_t *>(w);
+  const int rc = norm_w_dtype == VK_DTYPE_F32 ? launch_big<GB_QKV_W32>(xb, wb, nullptr, M, N, K, qa, VK_STREAM(stream))
+                 : qa.table_f32               ? launch_big<GB_QKV>(xb, wb, nullptr, M, N, K, qa, VK_STREAM(stream))
+                                              : launch_big<GB_QKV_BF16>(xb, wb, nullptr, M, N, K, qa, VK_STREAM(stream));
   if (rc != VK_OK) return rc;
   return launch_status("linear_qkv_rope");
 }
 
-extern "C" int vk_linear_residual_big(const void *a, const void *w, void *x, int64_t M, int32_t N, int32_t K,
-                                      const float *bias, float alpha, float *ss_out, void *stream) {
+extern "C" int vk_linear_residual_big(const void *a, const void *w, void *x, int32_t x_dtype, int64_t M, int32_t N,
+                                      int32_t K, const float *bias, float alpha, float *ss_out, void *stream) {
   VK_CHECK_ARG(a && w && x && ss_out, "linear_residual_big: null pointer");
+  VK_CHECK_ARG(x_dtype == VK_DTYPE_BF16 || x_dtype == VK_DTYPE_F32, "linear_residual_big: bad residual dtype");
   VK_CHECK_ARG(M >= 0 && N > 0 && N % 128 == 0 && K > 0 && K % 64 == 0,
                "linear_residual_big: need N %% 128 == 0 and K %% 64 == 0 (N=%d K=%d)", N, K);
   VK_CHECK_ARG(M < (int64_t(1) << 31) / 256 * 256, "linear_residual_big: M too large");
@@ -529,8 +591,9 @@ extern "C" int vk_linear_residual_big(const void *a, const void *w, void *x, int
   qa.bias = bias;
   qa.alpha = alpha;
   qa.ss_out = ss_out;
-  const int rc = launch_big<GB_RESID>(static_cast<const bf16_t *>(a), static_cast<const bf16_t *>(w), x, M, N, K, qa,
-                                      VK_STREAM(stream));
+  const auto ab = static_cast<const bf16_t *>(a), wb = static_cast<const bf16_t *>(w);
+  const int rc = x_dtype == VK_DTYPE_F32 ? launch_big<GB_RESID_F32>(ab, wb, x, M, N, K, qa, VK_STREAM(stream))
+                                         : launch_big<GB_RESID>(ab, wb, x, M, N, K, qa, VK_STREAM(stream));
   if (rc != VK_OK) return rc;
   return launch_status("linear_residual_big");
 }

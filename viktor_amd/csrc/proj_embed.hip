@@ -105,8 +105,11 @@ constexpr int EG_COLS = 512;  // columns per workgroup: 8 per lane
 constexpr int EG_UNROLL = 8;  // rows whose loads are in flight together
 
 // grid (slices, vocab chunks, column blocks), one wavefront; bins: min(V, 32) x 512 fp32 of dynamic LDS.
-// part [slices, V, d]: slice s's sums of its rows.
-__global__ __launch_bounds__(64) void embed_grad_kernel(const bf16_t *__restrict__ drows, int64_t ld,
+// part [slices, V, d]: slice s's sums of its rows. d_rows bf16 (the inference-precision residual's gradient) or
+// fp32 (the autocast forward's fp32 residual gradient: the embedding rows enter it unrounded). A token id is tested
+// against this workgroup's vocabulary chunk as an int64, before it is narrowed.
+template <typename DT>
+__global__ __launch_bounds__(64) void embed_grad_kernel(const DT *__restrict__ drows, int64_t ld,
                                                         const int64_t *__restrict__ tokens, int64_t n, int V, int d,
                                                         float *__restrict__ part) {
   extern __shared__ __attribute__((aligned(16))) float bins[];
@@ -120,21 +123,27 @@ __global__ __launch_bounds__(64) void embed_grad_kernel(const bf16_t *__restrict
   const int64_t r0 = n * sl / slices, r1 = n * (sl + 1) / slices;
   for (int64_t r = r0; r < r1; r += EG_UNROLL) {
     int t[EG_UNROLL];
-    u32x4 x[EG_UNROLL];
+    Raw8<DT> x[EG_UNROLL];
 #pragma unroll
     for (int u = 0; u < EG_UNROLL; ++u) {
       const bool in = r + u < r1;
-      t[u] = in ? static_cast<int>(tokens[r + u]) - v0 : -1;
-      x[u] = (in && live && t[u] >= 0 && t[u] < vc) ? *reinterpret_cast<const u32x4 *>(drows + (r + u) * ld + c0)
-                                                    : u32x4{0u, 0u, 0u, 0u};
+      const int64_t rel = in ? tokens[r + u] - v0 : -1;
+      t[u] = (rel >= 0 && rel < vc) ? static_cast<int>(rel) : -1;
+      if (live && t[u] >= 0)
+        x[u].load(drows + (r + u) * ld + c0);
+      else
+        x[u].zero();
     }
 #pragma unroll
     for (int u = 0; u < EG_UNROLL; ++u) {
-      if (t[u] < 0 || t[u] >= vc) continue;  // wave-uniform: every lane reads the same token
+      if (t[u] < 0) continue;  // wave-uniform: every lane reads the same token
       float *b = bins + t[u] * EG_COLS + 8 * lane;
       f32x4 lo = *reinterpret_cast<f32x4 *>(b), hi = *reinterpret_cast<f32x4 *>(b + 4);
-      lo += f32x4{lo_bf(x[u][0]), hi_bf(x[u][0]), lo_bf(x[u][1]), hi_bf(x[u][1])};
-      hi += f32x4{lo_bf(x[u][2]), hi_bf(x[u][2]), lo_bf(x[u][3]), hi_bf(x[u][3])};
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = x[u].get(e);
+      lo += f32x4{v[0], v[1], v[2], v[3]};
+      hi += f32x4{v[4], v[5], v[6], v[7]};
       *reinterpret_cast<f32x4 *>(b) = lo;
       *reinterpret_cast<f32x4 *>(b + 4) = hi;
     }
@@ -226,9 +235,10 @@ extern "C" int vk_embed_grad_workspace(int64_t n, int32_t V, int32_t d, int64_t 
   return VK_OK;
 }
 
-extern "C" int vk_embed_grad(const void *d_rows, int64_t ld, const int64_t *tokens, int64_t n, int32_t V, int32_t d,
-                             float *out, void *workspace, int64_t workspace_bytes, void *stream) {
+extern "C" int vk_embed_grad(const void *d_rows, int32_t d_dtype, int64_t ld, const int64_t *tokens, int64_t n, int32_t V,
+                             int32_t d, float *out, void *workspace, int64_t workspace_bytes, void *stream) {
   VK_CHECK_ARG(out && workspace && (n == 0 || (d_rows && tokens)), "embed_grad: null pointer");
+  VK_CHECK_ARG(d_dtype == VK_DTYPE_BF16 || d_dtype == VK_DTYPE_F32, "embed_grad: bad row dtype");
   VK_CHECK_ARG(n >= 0 && V > 0 && d > 0 && d % 8 == 0 && ld >= d && ld % 8 == 0,
                "embed_grad: need d %% 8 == 0 and a row stride >= d, multiple of 8");
   VK_CHECK_ARG(vk_aligned16(d_rows) && vk_aligned16(out) && vk_aligned16(workspace), "embed_grad: alignment");
@@ -241,7 +251,10 @@ extern "C" int vk_embed_grad(const void *d_rows, int64_t ld, const int64_t *toke
   const dim3 grid(static_cast<unsigned>(slices), static_cast<unsigned>((V + EG_VC - 1) / EG_VC),
                   static_cast<unsigned>((d + EG_COLS - 1) / EG_COLS));
   const size_t lds = static_cast<size_t>(V < EG_VC ? V : EG_VC) * EG_COLS * sizeof(float);  // <= 64 KB
-  embed_grad_kernel<<<grid, 64, lds, s>>>(static_cast<const bf16_t *>(d_rows), ld, tokens, n, V, d, part);
+  if (d_dtype == VK_DTYPE_F32)
+    embed_grad_kernel<float><<<grid, 64, lds, s>>>(static_cast<const float *>(d_rows), ld, tokens, n, V, d, part);
+  else
+    embed_grad_kernel<bf16_t><<<grid, 64, lds, s>>>(static_cast<const bf16_t *>(d_rows), ld, tokens, n, V, d, part);
   const int rc = launch_status("embed_grad");
   if (rc != VK_OK) return rc;
   embed_reduce_kernel<<<static_cast<unsigned>((vd + 63) / 64), 256, 0, s>>>(part, slices, vd, out);

@@ -16,6 +16,8 @@
 // All math in fp32; every reduction runs in a fixed order (deterministic).
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace vk {
@@ -31,8 +33,10 @@ __device__ __forceinline__ float ld<bf16_t>(const bf16_t *p, int64_t i) { return
 
 // one wavefront per row; lane l owns columns 8 l .. 8 l + 7. Workgroup = 4 waves; the grid strides over rows.
 // dw_part [gridDim.x, 512]: this workgroup's sum over its rows of dy x r.
-template <typename DT>
-__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const bf16_t *__restrict__ x, const bf16_t *__restrict__ w,
+// x, w: bf16 (the inference-precision residual stream) or fp32 (the autocast forward's fp32 stream and master
+// norm weights); dy bf16 or fp32.
+template <typename XT, typename WT, typename DT>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const XT *__restrict__ x, const WT *__restrict__ w,
                                                          const DT *__restrict__ dy, const float *__restrict__ dres,
                                                          float *__restrict__ dx, float *__restrict__ dw_part,
                                                          int64_t n, float eps) {
@@ -40,38 +44,23 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const bf16_t *__restri
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   float wv[8], dwa[8];
   {
-    const u32x4 wr = *reinterpret_cast<const u32x4 *>(w + 8 * lane);
+    Raw8<WT> wr;
+    wr.load(w + 8 * lane);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      wv[2 * e] = lo_bf(wr[e]);
-      wv[2 * e + 1] = hi_bf(wr[e]);
-    }
+    for (int e = 0; e < 8; ++e) wv[e] = wr.get(e);
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) dwa[j] = 0.f;
   for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wid; row < n; row += static_cast<int64_t>(gridDim.x) * 4) {
-    const u32x4 xr = *reinterpret_cast<const u32x4 *>(x + row * TR_D + 8 * lane);
+    Raw8<XT> xr;
+    Raw8<DT> gr;
+    xr.load(x + row * TR_D + 8 * lane);
+    gr.load(dy + row * TR_D + 8 * lane);
     float xv[8], gv[8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      xv[2 * e] = lo_bf(xr[e]);
-      xv[2 * e + 1] = hi_bf(xr[e]);
-    }
-    if constexpr (sizeof(DT) == 2) {  // 8 bf16 gradients: one 16-byte load
-      const u32x4 gr = *reinterpret_cast<const u32x4 *>(dy + row * TR_D + 8 * lane);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        gv[2 * e] = lo_bf(gr[e]);
-        gv[2 * e + 1] = hi_bf(gr[e]);
-      }
-    } else {
-      const f32x4 g0 = *reinterpret_cast<const f32x4 *>(dy + row * TR_D + 8 * lane);
-      const f32x4 g1 = *reinterpret_cast<const f32x4 *>(dy + row * TR_D + 8 * lane + 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        gv[e] = g0[e];
-        gv[4 + e] = g1[e];
-      }
+    for (int e = 0; e < 8; ++e) {
+      xv[e] = xr.get(e);
+      gv[e] = gr.get(e);
     }
     f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
     if (dres) {
@@ -133,9 +122,10 @@ __global__ __launch_bounds__(256) void colsum_kernel(const float *__restrict__ p
 // weight gradient partials (0..63) and k-norm (64..127).
 // HT / HKVT > 0: the head counts as compile-time constants (the decoder's 8 / 2), so the head loops unroll and
 // every head's loads and reductions of a row are in flight together; 0: the run-time H / HKV.
-template <typename TT, int HT, int HKVT>
+// WT: the norm weights' type (bf16, or the fp32 master weights of the autocast forward).
+template <typename TT, typename WT, int HT, int HKVT>
 __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(
-    const bf16_t *__restrict__ qkv, const bf16_t *__restrict__ qw, const bf16_t *__restrict__ kw,
+    const bf16_t *__restrict__ qkv, const WT *__restrict__ qw, const WT *__restrict__ kw,
     const TT *__restrict__ cos_t, const TT *__restrict__ sin_t, int64_t table_rows, const int32_t *__restrict__ rpos,
     const float *__restrict__ dq, const float *__restrict__ dk, const float *__restrict__ dv,
     bf16_t *__restrict__ dqkv, float *__restrict__ dw_part, int64_t n, int H_rt, int HKV_rt, float eps) {
@@ -144,7 +134,7 @@ __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int half = lane >> 5, fi = lane & 31;  // rotation half, frequency index
   const int NH = H + 2 * HKV;
-  const float wq = bf2f(qw[lane]), wk = bf2f(kw[lane]);
+  const float wq = ld(qw, lane), wk = ld(kw, lane);
   float dwq = 0.f, dwk = 0.f;
   for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wid; row < n; row += static_cast<int64_t>(gridDim.x) * 4) {
     int64_t p = rpos[row];
@@ -271,23 +261,38 @@ extern "C" int vk_rmsnorm_backward_blocks(int64_t n, int32_t *blocks) {
   return VK_OK;
 }
 
-extern "C" int vk_rmsnorm_backward(const void *x, const void *w, const void *dy, int32_t dy_dtype, const float *dres,
-                                   float *dx, float *dw_part, int64_t n, int32_t d, float eps, void *stream) {
+extern "C" int vk_rmsnorm_backward(const void *x, int32_t x_dtype, const void *w, int32_t w_dtype, const void *dy,
+                                   int32_t dy_dtype, const float *dres, float *dx, float *dw_part, int64_t n, int32_t d,
+                                   float eps, void *stream) {
   VK_CHECK_ARG(x && w && dy && dx && dw_part, "rmsnorm_backward: null pointer");
   if (d != TR_D) return fail(VK_ERR_UNSUPPORTED, "rmsnorm_backward: built for d = %d (got %d)", TR_D, d);
   VK_CHECK_ARG(n >= 0 && (dy_dtype == VK_DTYPE_BF16 || dy_dtype == VK_DTYPE_F32), "rmsnorm_backward: bad arguments");
+  VK_CHECK_ARG((x_dtype == VK_DTYPE_BF16 || x_dtype == VK_DTYPE_F32) && (w_dtype == VK_DTYPE_BF16 || w_dtype == VK_DTYPE_F32),
+               "rmsnorm_backward: bad dtypes");
   VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w) && vk_aligned16(dx) && vk_aligned16(dy) &&
                    (!dres || vk_aligned16(dres)),
                "rmsnorm_backward: alignment");
   if (n == 0) return VK_OK;
   const unsigned grid = row_grid(n);
   hipStream_t s = VK_STREAM(stream);
-  const auto xb = static_cast<const bf16_t *>(x);
-  const auto wb = static_cast<const bf16_t *>(w);
-  if (dy_dtype == VK_DTYPE_F32)
-    rmsnorm_bwd_kernel<float><<<grid, 256, 0, s>>>(xb, wb, static_cast<const float *>(dy), dres, dx, dw_part, n, eps);
-  else
-    rmsnorm_bwd_kernel<bf16_t><<<grid, 256, 0, s>>>(xb, wb, static_cast<const bf16_t *>(dy), dres, dx, dw_part, n, eps);
+  // the inference-precision combination (bf16 x and w) and the autocast one (fp32 x and w), each with either dy
+  if (x_dtype == VK_DTYPE_BF16 && w_dtype == VK_DTYPE_BF16) {
+    const auto xb = static_cast<const bf16_t *>(x);
+    const auto wb = static_cast<const bf16_t *>(w);
+    if (dy_dtype == VK_DTYPE_F32)
+      rmsnorm_bwd_kernel<bf16_t, bf16_t, float><<<grid, 256, 0, s>>>(xb, wb, static_cast<const float *>(dy), dres, dx, dw_part, n, eps);
+    else
+      rmsnorm_bwd_kernel<bf16_t, bf16_t, bf16_t><<<grid, 256, 0, s>>>(xb, wb, static_cast<const bf16_t *>(dy), dres, dx, dw_part, n, eps);
+  } else if (x_dtype == VK_DTYPE_F32 && w_dtype == VK_DTYPE_F32) {
+    const auto xf = static_cast<const float *>(x);
+    const auto wf = static_cast<const float *>(w);
+    if (dy_dtype == VK_DTYPE_F32)
+      rmsnorm_bwd_kernel<float, float, float><<<grid, 256, 0, s>>>(xf, wf, static_cast<const float *>(dy), dres, dx, dw_part, n, eps);
+    else
+      rmsnorm_bwd_kernel<float, float, bf16_t><<<grid, 256, 0, s>>>(xf, wf, static_cast<const bf16_t *>(dy), dres, dx, dw_part, n, eps);
+  } else {
+    return fail(VK_ERR_UNSUPPORTED, "rmsnorm_backward: x and w are both bf16 or both fp32");
+  }
   return launch_status("rmsnorm_backward");
 }
 
@@ -299,8 +304,8 @@ extern "C" int vk_colsum(const float *part, float *out, int32_t rows, int32_t co
   return launch_status("colsum");
 }
 
-extern "C" int vk_qknorm_rope_backward(const void *qkv, const void *q_norm_w, const void *k_norm_w, const void *cos_t,
-                                       const void *sin_t, int32_t table_dtype, int64_t table_rows,
+extern "C" int vk_qknorm_rope_backward(const void *qkv, const void *q_norm_w, const void *k_norm_w, int32_t norm_w_dtype,
+                                       const void *cos_t, const void *sin_t, int32_t table_dtype, int64_t table_rows,
                                        const int32_t *rope_pos, const float *dq, const float *dk, const float *dv,
                                        void *dqkv, float *dw_part, int64_t n, int32_t H, int32_t HKV, int32_t D,
                                        float eps, void *stream) {
@@ -308,32 +313,40 @@ extern "C" int vk_qknorm_rope_backward(const void *qkv, const void *q_norm_w, co
                "qknorm_rope_backward: null pointer");
   if (D != 64) return fail(VK_ERR_UNSUPPORTED, "qknorm_rope_backward: built for head_dim 64 (got %d)", D);
   VK_CHECK_ARG(n >= 0 && H > 0 && HKV > 0 && table_rows > 0 &&
-                   (table_dtype == VK_DTYPE_F32 || table_dtype == VK_DTYPE_BF16),
+                   (table_dtype == VK_DTYPE_F32 || table_dtype == VK_DTYPE_BF16) &&
+                   (norm_w_dtype == VK_DTYPE_F32 || norm_w_dtype == VK_DTYPE_BF16),
                "qknorm_rope_backward: bad arguments");
   if (n == 0) return VK_OK;
   const unsigned grid = row_grid(n);
   hipStream_t s = VK_STREAM(stream);
   const auto qb = static_cast<const bf16_t *>(qkv);
-  const auto qw = static_cast<const bf16_t *>(q_norm_w);
-  const auto kw = static_cast<const bf16_t *>(k_norm_w);
   auto out = static_cast<bf16_t *>(dqkv);
   const bool fixed = H == 8 && HKV == 2;
+  // table and weight types, then the head counts as constants (8 / 2) or at run time
+  auto run = [&](auto ct, auto wt) {
+    using TT = typename std::remove_pointer<decltype(ct)>::type;
+    using WT = typename std::remove_pointer<decltype(wt)>::type;
+    const auto c = static_cast<const TT *>(cos_t), sn = static_cast<const TT *>(sin_t);
+    const auto qw = static_cast<const WT *>(q_norm_w), kw = static_cast<const WT *>(k_norm_w);
+    if (fixed)
+      qknorm_rope_bwd_kernel<TT, WT, 8, 2><<<grid, 256, 0, s>>>(qb, qw, kw, c, sn, table_rows, rope_pos, dq, dk, dv,
+                                                                out, dw_part, n, H, HKV, eps);
+    else
+      qknorm_rope_bwd_kernel<TT, WT, 0, 0><<<grid, 256, 0, s>>>(qb, qw, kw, c, sn, table_rows, rope_pos, dq, dk, dv,
+                                                                out, dw_part, n, H, HKV, eps);
+  };
+  const float *f = nullptr;
+  const bf16_t *b = nullptr;
   if (table_dtype == VK_DTYPE_F32) {
-    const auto ct = static_cast<const float *>(cos_t), st = static_cast<const float *>(sin_t);
-    if (fixed)
-      qknorm_rope_bwd_kernel<float, 8, 2><<<grid, 256, 0, s>>>(qb, qw, kw, ct, st, table_rows, rope_pos, dq, dk, dv,
-                                                               out, dw_part, n, H, HKV, eps);
+    if (norm_w_dtype == VK_DTYPE_F32)
+      run(f, f);
     else
-      qknorm_rope_bwd_kernel<float, 0, 0><<<grid, 256, 0, s>>>(qb, qw, kw, ct, st, table_rows, rope_pos, dq, dk, dv,
-                                                               out, dw_part, n, H, HKV, eps);
+      run(f, b);
   } else {
-    const auto ct = static_cast<const bf16_t *>(cos_t), st = static_cast<const bf16_t *>(sin_t);
-    if (fixed)
-      qknorm_rope_bwd_kernel<bf16_t, 8, 2><<<grid, 256, 0, s>>>(qb, qw, kw, ct, st, table_rows, rope_pos, dq, dk,
-                                                                dv, out, dw_part, n, H, HKV, eps);
+    if (norm_w_dtype == VK_DTYPE_F32)
+      run(b, f);
     else
-      qknorm_rope_bwd_kernel<bf16_t, 0, 0><<<grid, 256, 0, s>>>(qb, qw, kw, ct, st, table_rows, rope_pos, dq, dk,
-                                                                dv, out, dw_part, n, H, HKV, eps);
+      run(b, b);
   }
   return launch_status("qknorm_rope_backward");
 }

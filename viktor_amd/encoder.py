@@ -318,9 +318,10 @@ class DoradoEncoder:
         g = torch.empty(M, Fd, dtype=torch.bfloat16, device=dev)
         n = len(plan.frames)
         hd = self.head_dim
+        BF = _lib.VK_DTYPE_BF16  # the encoder's residual stream, norm weights and activations are bf16
         for Lw in self.weights["layers"]:
             # Wqkv with the rotary embedding in its epilogue: q, k (rotated) and v back into the packed rows
-            call("vk_linear_qkv_rope", ptr(x), ptr(Lw["wqkv"]), M, C, ptr(None), ptr(None), 0.0, ptr(self.cos),
+            call("vk_linear_qkv_rope", ptr(x), ptr(Lw["wqkv"]), M, C, ptr(None), ptr(None), BF, 0.0, ptr(self.cos),
                  ptr(self.sin), _lib.VK_DTYPE_F32, self.cos.shape[0], ptr(plan.rope_pos), ptr(None), ptr(None),
                  ptr(qkv), 3 * C, ptr(None), ptr(None), 0, 0, 0, 0, ptr(qkv[:, C:]), ptr(qkv[:, 2 * C:]), 3 * C, H, H,
                  hd, st)
@@ -328,13 +329,13 @@ class DoradoEncoder:
                  plan.max_frames, H, hd, ptr(None), ptr(None), 0, self.window[0], self.window[1], ptr(o), C, st)
             # out_proj: bias + DeepNorm residual in the product's epilogue (x in place, row sums of squares out),
             # then the RMSNorm in place; the same for fc2 without bias
-            call("vk_linear_residual_big", ptr(o), ptr(Lw["wo"]), ptr(x), M, C, C, ptr(Lw["bo"]), Lw["alpha"], ptr(ss),
-                 st)
-            call("vk_rmsnorm_apply_ss", ptr(x), ptr(ss), C // 64, ptr(Lw["n1"]), ptr(x), M, C, 1e-5, st)
+            call("vk_linear_residual_big", ptr(o), ptr(Lw["wo"]), ptr(x), BF, M, C, C, ptr(Lw["bo"]), Lw["alpha"],
+                 ptr(ss), st)
+            call("vk_rmsnorm_apply_ss", ptr(x), BF, ptr(ss), C // 64, ptr(Lw["n1"]), BF, ptr(x), M, C, 1e-5, st)
             call("vk_gemm_rows", ptr(x), ptr(Lw["w1"]), ptr(g), M, Fd, C, 2, st)
-            call("vk_linear_residual_big", ptr(g), ptr(Lw["w2"]), ptr(x), M, C, Fd, ptr(None), Lw["alpha"], ptr(ss),
-                 st)
-            call("vk_rmsnorm_apply_ss", ptr(x), ptr(ss), C // 64, ptr(Lw["n2"]), ptr(x), M, C, 1e-5, st)
+            call("vk_linear_residual_big", ptr(g), ptr(Lw["w2"]), ptr(x), BF, M, C, Fd, ptr(None), Lw["alpha"],
+                 ptr(ss), st)
+            call("vk_rmsnorm_apply_ss", ptr(x), BF, ptr(ss), C // 64, ptr(Lw["n2"]), BF, ptr(x), M, C, 1e-5, st)
 
     def flops_per_chunk(self, samples: int) -> float:
         """Matrix FLOPs of one chunk: convolutions, the four products per layer and the window attention's

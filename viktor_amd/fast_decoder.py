@@ -114,8 +114,65 @@ class FastDecoder:
         self._wcache[key] = (ver, conv)
         return conv
 
+    def w32(self, p):
+        """fp32 contiguous view of a parameter (the module's own tensor when it is fp32; a converted copy,
+        refreshed on change, otherwise): the norm weights autocast leaves in fp32."""
+        if p.dtype == torch.float32 and p.is_contiguous():
+            return p
+        key = ("f32", id(p))
+        ver = (p.data_ptr(), p._version)
+        hit = self._wcache.get(key)
+        if hit is not None and hit[0] == ver:
+            return hit[1]
+        conv = p.detach().float().contiguous()
+        self._wcache[key] = (ver, conv)
+        return conv
+
     def _tables(self):
         return self.dec.cos, self.dec.sin
+
+    def teacher_forced(self, x, pos, plan, rope_pos=None):
+        """The teacher-forced causal forward of packed windows with the rounding points of the reference's
+        scoring path, Basecaller.logits under torch.autocast bf16 over fp32 master weights (scripts/gspo.py:345-347,
+        viktor/model.py:55-60, viktor/decoder.py:63-67, 82-87, 117-120, 144):
+          * the residual stream x [n, d] is fp32 (updated in place); every sublayer output is a bf16 product
+            added to it in fp32 (vk_linear_residual_big on an fp32 stream);
+          * each RMSNorm runs in fp32 with fp32 weights and is rounded once, to the bf16 operand of the next
+            product (vk_rmsnorm_f32, vk_rmsnorm_apply_ss on fp32);
+          * the GEMM weights are the parameters cast to bf16; the QK-norm keeps fp32 weights and returns
+            bf16(x / rms * w) for a bf16 head, the rotation runs in fp32 with fp32 tables, rounded to bf16
+            (vk_linear_qkv_rope with fp32 norm weights);
+          * attention as flash-attention: bf16 q / k / v, fp32 scores, bf16 probabilities in the PV product.
+        pos [n] int32: each row's position in its window (the rotary row unless rope_pos is given); plan: a
+        PrefillPlan without a cache (its keep rows finish the last layer). Returns the final-normed hidden state
+        of the kept rows (all rows without keep), bf16, the operand of the LM head."""
+        require_device(x, "FastDecoder.teacher_forced")
+        cfg, layers, W, F = self.cfg, self.dec.layers, self.w, self.w32
+        _require(x.dtype == torch.float32 and x.is_contiguous() and x.shape == (plan.total, cfg.d_model),
+                 "teacher_forced: x fp32 [plan rows, d]")
+        _require(not plan.from_cache, "teacher_forced: a plan without a cache")
+        eps = cfg.norm_eps
+        H, HKV, D = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+        cos, sin = (F(t) for t in self._tables())
+        full, lastp = plan.packed_plans(HKV * D)
+        n_layers = len(layers)
+        h = ops.rmsnorm_f32(x, F(layers[0].attn_norm.weight), eps)
+        for i, blk in enumerate(layers):
+            a = blk.attn
+            q, k, v = ops.linear_qkv_rope(h, W(a.qkv_proj.weight), F(a.q_norm.weight), F(a.k_norm.weight), cos, sin,
+                                          pos, None, None, None, eps, H, HKV, D, return_kv=True, rope_pos=rope_pos)
+            last = plan.last_idx is not None and i == n_layers - 1
+            if last:  # only the kept rows finish the last layer; they attend to every key of their window
+                x = x[plan.last_idx]
+                q = q[plan.last_idx]
+            o = ops.varlen_attention(q, k, v, lastp if last else full, stride_tok=k.stride(0))
+            ss = ops.linear_residual_big(o.reshape(x.shape[0], -1), W(a.o_proj.weight), x)
+            h = ops.rmsnorm_apply(x, ss, F(blk.mlp_norm.weight), eps)
+            g = ops.linear(h, W(blk.gate_up.weight), swiglu=True)
+            w_next = layers[i + 1].attn_norm.weight if i + 1 < n_layers else self.dec.norm.weight
+            ss = ops.linear_residual_big(g, W(blk.down.weight), x)
+            h = ops.rmsnorm_apply(x, ss, F(w_next), eps)
+        return h
 
     def _layers(self, x, pos, seq, cache, attend, return_kv, last_idx=None, rope_pos=None, h=None):
         """x [n, d] residual stream (updated in place); h: its first attention norm when already computed.

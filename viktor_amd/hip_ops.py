@@ -90,7 +90,9 @@ def qkv_rope_cache(qkv, q_norm_w, k_norm_w, cos, sin, pos, seq, k_cache, v_cache
         sb, ss, rows, clen = k_cache.stride(0), k_cache.stride(1), k_cache.shape[0], k_cache.shape[1]
     else:
         sb = ss = rows = clen = 0
-    call("vk_qkv_rope_cache", ptr(qkv), ptr(q_norm_w), ptr(k_norm_w), ptr(cos), ptr(sin), tdt, cos.shape[0], ptr(pos),
+    _require(q_norm_w.dtype == k_norm_w.dtype and q_norm_w.dtype in (BF16, torch.float32), "qkv_rope_cache: norm weights")
+    wdt = VK_DTYPE_F32 if q_norm_w.dtype == torch.float32 else VK_DTYPE_BF16
+    call("vk_qkv_rope_cache", ptr(qkv), ptr(q_norm_w), ptr(k_norm_w), wdt, ptr(cos), ptr(sin), tdt, cos.shape[0], ptr(pos),
          ptr(rope_pos), ptr(seq), ptr(q), ptr(k_cache), ptr(v_cache), sb, ss, rows, clen, ptr(k), ptr(v), n,
          float(eps), n_heads, n_kv_heads, head_dim, stream_handle())
     return (q, k, v) if return_kv else q
@@ -102,7 +104,8 @@ def linear_qkv_rope(x, w, q_norm_w, k_norm_w, cos, sin, pos, seq, k_cache, v_cac
     per-head QK-norm (q_norm_w / k_norm_w; both None: none) and RoPE at pos (or rope_pos) on the q and k heads,
     q to [n, H, D], k / v to the cache rows (seq, pos) and / or packed [n, Hkv, D] (return_kv). The rounding
     points of linear + qkv_rope_cache (viktor/triton_ops.py:43-108, 138-146). q_out / kv_out: caller's buffers
-    (q_out [n, >= H D] rows; kv_out = (k, v) [n, >= Hkv D] rows, any row stride)."""
+    (q_out [n, >= H D] rows; kv_out = (k, v) [n, >= Hkv D] rows, any row stride). fp32 norm weights (with fp32
+    tables): the autocast forward's QK-norm with fp32 master weights (viktor/decoder.py:63-67 under autocast)."""
     require_device(x, "linear_qkv_rope")
     n, K = x.shape
     H, HKV, D = n_heads, n_kv_heads, head_dim
@@ -133,37 +136,63 @@ def linear_qkv_rope(x, w, q_norm_w, k_norm_w, cos, sin, pos, seq, k_cache, v_cac
         _require(return_kv, "linear_qkv_rope: nowhere to write k/v")
         sb = ss = rows = clen = 0
     tdt = VK_DTYPE_F32 if cos.dtype == torch.float32 else VK_DTYPE_BF16
-    call("vk_linear_qkv_rope", ptr(x), ptr(w), n, K, ptr(q_norm_w), ptr(k_norm_w), float(eps), ptr(cos), ptr(sin), tdt,
+    _require((q_norm_w is None) == (k_norm_w is None), "linear_qkv_rope: q and k norm weights go together")
+    wdt = VK_DTYPE_BF16
+    if q_norm_w is not None:
+        _require(q_norm_w.dtype == k_norm_w.dtype and q_norm_w.dtype in (BF16, torch.float32) and q_norm_w.shape == (D,)
+                 and k_norm_w.shape == (D,) and _contig(q_norm_w, k_norm_w), "linear_qkv_rope: norm weights [D]")
+        wdt = VK_DTYPE_F32 if q_norm_w.dtype == torch.float32 else VK_DTYPE_BF16
+        _require(wdt == VK_DTYPE_BF16 or tdt == VK_DTYPE_F32, "linear_qkv_rope: fp32 norm weights need fp32 tables")
+    call("vk_linear_qkv_rope", ptr(x), ptr(w), n, K, ptr(q_norm_w), ptr(k_norm_w), wdt, float(eps), ptr(cos), ptr(sin), tdt,
          cos.shape[0], ptr(pos), ptr(rope_pos), ptr(seq), ptr(q), q.stride(0), ptr(k_cache), ptr(v_cache), sb, ss,
          rows, clen, ptr(k), ptr(v), 0 if k is None else k.stride(0), H, HKV, D, stream_handle())
     return (q, k, v) if return_kv else q
 
 
 def linear_residual_big(a, w, x, bias=None, alpha=1.0):
-    """Large-M residual product, in place: x = bf16(bf16(a @ w^T + bias) + bf16(alpha x)) (alpha 1, no bias:
-    add_rmsnorm's x += delta, viktor/triton_ops.py:17-31; with the out_proj bias and the DeepNorm alpha:
-    viktor/encoder.py:106-108). Returns the row sums of squares of the new x per 64-column block [M, N / 64]
-    fp32, for rmsnorm_apply."""
+    """Large-M residual product, in place. bf16 x: x = bf16(bf16(a @ w^T + bias) + bf16(alpha x)) (alpha 1, no
+    bias: add_rmsnorm's x += delta, viktor/triton_ops.py:17-31; with the out_proj bias and the DeepNorm alpha:
+    viktor/encoder.py:106-108). fp32 x: x = alpha x + bf16(a @ w^T + bias), the residual add of an fp32 stream and
+    a bf16 product under torch.autocast (viktor/decoder.py:118-120). Returns the row sums of squares of the new x
+    per 64-column block [M, N / 64] fp32, for rmsnorm_apply."""
     require_device(a, "linear_residual_big")
     M, K = a.shape
     N = w.shape[0]
-    _require(a.dtype == w.dtype == x.dtype == BF16 and w.shape[1] == K and x.shape == (M, N) and _contig(a, w, x, bias),
-             "linear_residual_big: shapes")
+    _require(a.dtype == w.dtype == BF16 and x.dtype in (BF16, torch.float32) and w.shape[1] == K and x.shape == (M, N)
+             and _contig(a, w, x, bias), "linear_residual_big: shapes")
     _require(bias is None or (bias.dtype == torch.float32 and bias.shape == (N,)), "linear_residual_big: bias fp32 [N]")
     ss = torch.empty(M, N // 64, dtype=torch.float32, device=a.device)
-    call("vk_linear_residual_big", ptr(a), ptr(w), ptr(x), M, N, K, ptr(bias), float(alpha), ptr(ss), stream_handle())
+    xdt = VK_DTYPE_F32 if x.dtype == torch.float32 else VK_DTYPE_BF16
+    call("vk_linear_residual_big", ptr(a), ptr(w), ptr(x), xdt, M, N, K, ptr(bias), float(alpha), ptr(ss),
+         stream_handle())
     return ss
 
 
 def rmsnorm_apply(x, ss, w, eps, out=None):
     """h = bf16(x * rsqrt(sum(ss[row]) / d + eps) * w): the RMSNorm of x with its row sums of squares handed over
-    in block partials (linear_residual_big). out may be x itself."""
+    in block partials (linear_residual_big). x and w bf16, or fp32 (the autocast forward's residual stream and
+    master weights); h bf16. out may be x itself when x is bf16."""
     require_device(x, "rmsnorm_apply")
     n, d = x.shape
-    _require(x.dtype == w.dtype == BF16 and ss.dtype == torch.float32 and ss.shape[0] == n and _contig(x, ss, w),
-             "rmsnorm_apply: shapes")
-    h = out if out is not None else torch.empty_like(x)
-    call("vk_rmsnorm_apply_ss", ptr(x), ptr(ss), ss.shape[1], ptr(w), ptr(h), n, d, float(eps), stream_handle())
+    _require(x.dtype in (BF16, torch.float32) and w.dtype in (BF16, torch.float32) and w.shape == (d,) and
+             ss.dtype == torch.float32 and ss.shape[0] == n and _contig(x, ss, w), "rmsnorm_apply: shapes")
+    h = out if out is not None else torch.empty(n, d, dtype=BF16, device=x.device)
+    _require(h.dtype == BF16 and h.shape == (n, d) and h.is_contiguous(), "rmsnorm_apply: out bf16 [n, d]")
+    xdt = VK_DTYPE_F32 if x.dtype == torch.float32 else VK_DTYPE_BF16
+    wdt = VK_DTYPE_F32 if w.dtype == torch.float32 else VK_DTYPE_BF16
+    call("vk_rmsnorm_apply_ss", ptr(x), xdt, ptr(ss), ss.shape[1], ptr(w), wdt, ptr(h), n, d, float(eps),
+         stream_handle())
+    return h
+
+
+def rmsnorm_f32(x, w, eps, out=None):
+    """h = bf16(x * rsqrt(mean(x^2) + eps) * w) of an fp32 stream x [n, d] with fp32 weights w [d]: nn.RMSNorm
+    (fp32) cast to bf16 at the next product's autocast input (viktor/decoder.py:118 under torch.autocast)."""
+    require_device(x, "rmsnorm_f32")
+    n, d = x.shape
+    _require(x.dtype == w.dtype == torch.float32 and w.shape == (d,) and _contig(x, w), "rmsnorm_f32: x, w fp32")
+    h = out if out is not None else torch.empty(n, d, dtype=BF16, device=x.device)
+    call("vk_rmsnorm_f32", ptr(x), ptr(w), ptr(h), n, d, float(eps), stream_handle())
     return h
 
 
@@ -614,11 +643,12 @@ def act_backward(dout, pre=None):
 
 
 def embed_grad(d_rows, tokens, vocab):
-    """Token-embedding gradient: fp32 [vocab, d] with row v = the sum of d_rows[r] (bf16 [n, d], unit column
-    stride) over tokens[r] == v (int64 [n]), summed in a fixed order. Reference: the backward of nn.Embedding,
-    viktor/decoder.py:127, as viktor/model.py:77 gathers it."""
+    """Token-embedding gradient: fp32 [vocab, d] with row v = the sum of d_rows[r] (bf16 or fp32 [n, d], unit
+    column stride) over tokens[r] == v (int64 [n]), summed in a fixed order. Reference: the backward of
+    nn.Embedding, viktor/decoder.py:127, as viktor/model.py:77 gathers it."""
     require_device(d_rows, "embed_grad")
-    _require(d_rows.dim() == 2 and d_rows.dtype == BF16 and d_rows.stride(1) == 1, "embed_grad: d_rows [n, d] bf16")
+    _require(d_rows.dim() == 2 and d_rows.dtype in (BF16, torch.float32) and d_rows.stride(1) == 1,
+             "embed_grad: d_rows [n, d] bf16 or fp32")
     _require(tokens.shape == (d_rows.shape[0],) and tokens.dtype == torch.long and tokens.is_contiguous(),
              "embed_grad: tokens [n] int64")
     n, d = d_rows.shape
@@ -626,8 +656,9 @@ def embed_grad(d_rows, tokens, vocab):
     call("vk_embed_grad_workspace", n, vocab, d, ctypes.byref(nb))
     ws = torch.empty(max(int(nb.value) // 4, 4), dtype=torch.float32, device=d_rows.device)
     out = torch.empty(vocab, d, dtype=torch.float32, device=d_rows.device)
-    call("vk_embed_grad", ptr(d_rows), d_rows.stride(0), ptr(tokens), n, vocab, d, ptr(out), ptr(ws), 4 * ws.numel(),
-         stream_handle())
+    ddt = VK_DTYPE_F32 if d_rows.dtype == torch.float32 else VK_DTYPE_BF16
+    call("vk_embed_grad", ptr(d_rows), ddt, d_rows.stride(0), ptr(tokens), n, vocab, d, ptr(out), ptr(ws),
+         4 * ws.numel(), stream_handle())
     return out
 
 
@@ -649,20 +680,22 @@ def colsum(part, out=None, accumulate=False):
 
 
 def rmsnorm_backward(x, w, dy, eps, dres=None, dx=None):
-    """Backward of h = rmsnorm(x) * w (x [n, 512] bf16, w [512] bf16, dy [n, 512] bf16 or fp32):
+    """Backward of h = rmsnorm(x) * w (x [n, 512] and w [512] both bf16 or both fp32, dy [n, 512] bf16 or fp32):
     returns (dx fp32 [n, 512] = the norm's input gradient + dres, dw fp32 [512]). dx may be dres (in place).
     Reference: nn.RMSNorm of the decoder blocks, viktor/decoder.py:110-124."""
     require_device(x, "rmsnorm_backward")
     n, d = x.shape
-    _require(x.dtype == w.dtype == BF16 and dy.shape == x.shape and dy.dtype in (BF16, torch.float32),
-             "rmsnorm_backward: dtypes")
+    _require(x.dtype == w.dtype and x.dtype in (BF16, torch.float32) and dy.shape == x.shape
+             and dy.dtype in (BF16, torch.float32), "rmsnorm_backward: dtypes")
     _require(_contig(x, w, dy, dres) and (dres is None or (dres.dtype == torch.float32 and dres.shape == x.shape)),
              "rmsnorm_backward: layouts")
     if dx is None:
         dx = dres if dres is not None else torch.empty(n, d, dtype=torch.float32, device=x.device)
     part = torch.empty(_norm_blocks(n), d, dtype=torch.float32, device=x.device)
-    call("vk_rmsnorm_backward", ptr(x), ptr(w), ptr(dy), VK_DTYPE_F32 if dy.dtype == torch.float32 else VK_DTYPE_BF16,
-         ptr(dres), ptr(dx), ptr(part), n, d, float(eps), stream_handle())
+    xdt = VK_DTYPE_F32 if x.dtype == torch.float32 else VK_DTYPE_BF16
+    call("vk_rmsnorm_backward", ptr(x), xdt, ptr(w), xdt, ptr(dy),
+         VK_DTYPE_F32 if dy.dtype == torch.float32 else VK_DTYPE_BF16, ptr(dres), ptr(dx), ptr(part), n, d, float(eps),
+         stream_handle())
     return dx, colsum(part)
 
 
@@ -677,10 +710,13 @@ def qknorm_rope_backward(qkv, q_norm_w, k_norm_w, cos, sin, rope_pos, dq, dk, dv
              and dq.dtype == dk.dtype == dv.dtype == torch.float32, "qknorm_rope_backward: gradients")
     _require(rope_pos.dtype == torch.int32 and rope_pos.shape == (n,), "qknorm_rope_backward: rope_pos")
     _require(_contig(qkv, q_norm_w, k_norm_w, cos, sin, rope_pos, dq, dk, dv), "qknorm_rope_backward: layouts")
+    _require(q_norm_w.dtype == k_norm_w.dtype and q_norm_w.dtype in (BF16, torch.float32),
+             "qknorm_rope_backward: norm weights bf16 or fp32")
+    wdt = VK_DTYPE_F32 if q_norm_w.dtype == torch.float32 else VK_DTYPE_BF16
     dqkv = torch.empty_like(qkv)
     part = torch.empty(_norm_blocks(n), 2 * head_dim, dtype=torch.float32, device=qkv.device)
     tdt = VK_DTYPE_F32 if cos.dtype == torch.float32 else VK_DTYPE_BF16
-    call("vk_qknorm_rope_backward", ptr(qkv), ptr(q_norm_w), ptr(k_norm_w), ptr(cos), ptr(sin), tdt, cos.shape[0],
+    call("vk_qknorm_rope_backward", ptr(qkv), ptr(q_norm_w), ptr(k_norm_w), wdt, ptr(cos), ptr(sin), tdt, cos.shape[0],
          ptr(rope_pos), ptr(dq), ptr(dk), ptr(dv), ptr(dqkv), ptr(part), n, n_heads, n_kv_heads, head_dim, float(eps),
          stream_handle())
     dw = colsum(part)

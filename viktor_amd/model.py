@@ -5,7 +5,9 @@ None (then `d_enc` gives the frame width) or the HIP encoder (viktor_amd.encoder
 `encode` runs.
 Teacher-forced logits run on the HIP kernels: every window is packed as [its plens[b] frames | tokens]
 (the causal decoder never reads the padding the reference appends after them), the decoder runs over the
-packed tokens with its last layer kept for the token rows only, and the LM head gives bf16 logits.
+packed tokens with its last layer kept for the token rows only, and the LM head gives bf16 logits. They keep
+the rounding points of the reference's scoring call, which runs under torch.autocast bf16 (an fp32 residual
+stream; see FastDecoder.teacher_forced).
 """
 
 from typing import Optional
@@ -89,8 +91,17 @@ class Basecaller(nn.Module):
 
     def logits(self, frames, tokens_in, plens=None):
         """Teacher forcing from encoder frames [B, P, d_enc]: bf16 logits [B, T, vocab] of every token
-        position. plens [B]: real prefix frames per window (default P). Reference: viktor/model.py:55-60."""
-        require_device(frames, "Basecaller.logits")
+        position. plens [B]: real prefix frames per window (default P). Reference: viktor/model.py:55-60, with
+        the rounding points it has where scripts/gspo.py:345-347 calls it, under torch.autocast bf16: the
+        projector's bf16 output and the token embeddings gathered into an fp32 residual stream
+        (viktor/model.py:81-84; fp32 embedding rows from fp32 weights), the decoder on that fp32 stream
+        (FastDecoder.teacher_forced) and the LM head as a bf16 product."""
+        return self.decoder.head(self.hidden(frames, tokens_in, plens)).view(frames.shape[0], tokens_in.shape[1], -1)
+
+    def hidden(self, frames, tokens_in, plens=None):
+        """The final-normed hidden state of every token position [B T, d] bf16 (the LM head's operand) of the
+        teacher-forced forward that logits() runs."""
+        require_device(frames, "Basecaller.hidden")
         B, P = frames.shape[:2]
         T = tokens_in.shape[1]
         dev = frames.device
@@ -98,13 +109,13 @@ class Basecaller(nn.Module):
         assert all(0 < p <= P for p in plens_h), "plens outside 1..P"
         prefix = self.project(frames)                                       # [B, P, d] bf16
         fast = self.decoder.fast()
-        emb = fast.w(self.decoder.embed.weight)[tokens_in.to(dev)]          # [B, T, d] bf16
+        emb = fast.w32(self.decoder.embed.weight)[tokens_in.to(dev)]        # [B, T, d] fp32
         seq_lens = [p + T for p in plens_h]
         plan = PrefillPlan(seq_lens, dev, keep=[T] * B)
         # packed rows: window b = [prefix[b, :plens[b]] | emb[b]]
         pl = torch.tensor(plens_h, device=dev)
         cu = torch.tensor(plan.cu[:-1], device=dev)
-        x = torch.empty(plan.total, prefix.shape[-1], dtype=BF16, device=dev)
+        x = torch.empty(plan.total, prefix.shape[-1], dtype=torch.float32, device=dev)
         if all(p == P for p in plens_h):  # full windows: two strided copies
             xv = x.view(B, P + T, -1)
             xv[:, :P] = prefix
@@ -113,7 +124,7 @@ class Basecaller(nn.Module):
             frame_rows = torch.repeat_interleave(torch.arange(B, device=dev), pl)
             frame_pos = torch.arange(int(pl.sum()), device=dev) - torch.repeat_interleave(
                 torch.cumsum(pl, 0) - pl, pl)
-            x[cu[frame_rows] + frame_pos] = prefix[frame_rows, frame_pos]
+            x[cu[frame_rows] + frame_pos] = prefix[frame_rows, frame_pos].float()
             tok_dst = (cu + pl)[:, None] + torch.arange(T, device=dev)[None, :]
             x[tok_dst.reshape(-1)] = emb.reshape(B * T, -1)
         # each row's position inside its window
@@ -124,8 +135,7 @@ class Basecaller(nn.Module):
             s = self.pos_scale
             rpos = torch.cat([torch.cat([torch.arange(p, device=dev) * s, s * p + torch.arange(T, device=dev)])
                               for p in plens_h]).to(torch.int32)
-        h = fast.prefill(x, pos, None, None, plan.max_len, None, rope_pos=rpos, plan=plan)  # [B * T, d]
-        return self.decoder.head(h).view(B, T, -1)
+        return fast.teacher_forced(x, pos, plan, rope_pos=rpos)            # [B * T, d] bf16
 
     def batch(self, seqs, weights=None, pad_to=1):
         """CPU teacher-forcing tensors: tokens_in, targets [B, T] and target weights [B, T], T padded up to a

@@ -5,8 +5,12 @@ Reference: scripts/gspo.py:340-353 (token_logprobs under torch.autocast bf16), 4
 loss.backward() through Basecaller.logits, clip_grad_norm_, AdamW(fused).step()), 113-126 (bf16_copy / sync);
 viktor/model.py:55-60 (Basecaller.logits), viktor/decoder.py:54-144 (the decoder blocks).
 
-The model keeps fp32 master weights, as the reference's trainable model does; every forward casts them to
-bf16 (the autocast the reference trains under) and every weight gradient arrives in fp32 through that cast.
+The model keeps fp32 master weights, as the reference's trainable model does, and the forward keeps the rounding
+points of torch.autocast bf16 over them (the autocast token_logprobs runs under, scripts/gspo.py:345-347): the
+products take the weights cast to bf16 and give bf16 outputs, and every product-weight gradient arrives in fp32
+through that cast; the residual stream, the token-embedding rows and the RMSNorm weights stay fp32
+(viktor/model.py:81-84, viktor/decoder.py:117-120), and each RMSNorm is rounded once, to the bf16 operand of the
+next product.
 Every product of the update runs on the HIP kernels:
   * the decoder stack is one autograd node (`_DecoderStack`): its forward runs the prefill kernels over the
     packed windows and keeps each layer's activations; its backward runs the HIP backward kernels (attention,
@@ -15,8 +19,8 @@ Every product of the update runs on the HIP kernels:
     summed in a fixed order, rounded to bf16 once as the autocast matmul output);
   * the per-frame projector (`_Projector`: linear, bias + GELU, linear, bias) and the LM head (`_LMHead`,
     V = 7 or 343 columns: the V-wide operand zero-padded to the products' tile width) likewise;
-  * the token-embedding gradient is a deterministic segmented row sum (vk_embed_grad).
-The residual stream is bf16, the rounding points of the inference path.
+  * the token-embedding gradient is a deterministic segmented row sum (vk_embed_grad) of the fp32 residual
+    gradient rows.
 """
 
 from typing import List, Optional, Sequence
@@ -40,28 +44,27 @@ def decoder_params(dec) -> List[torch.Tensor]:
 
 
 def _residual_norm(x, a, w, norm_w, eps):
-    """x += a @ w^T in place, then RMSNorm(x) * norm_w (add_rmsnorm after a linear, viktor/triton_ops.py:34-40).
-    Packed batches of >= 4096 rows add the residual in the product's epilogue, which hands the row sums of
-    squares to the norm."""
-    if x.shape[0] >= 4096 and x.shape[1] % 128 == 0 and a.shape[1] % 64 == 0:
-        return ops.rmsnorm_apply(x, ops.linear_residual_big(a, w, x), norm_w, eps)
-    return ops.add_rmsnorm(x, norm_w, eps, delta=ops.linear(a, w))
+    """x += bf16(a @ w^T) in place on the fp32 residual stream x, then bf16(RMSNorm(x) * norm_w) with fp32
+    norm_w: `x = x + sublayer(...)` and the next nn.RMSNorm under autocast (viktor/decoder.py:118-120). The
+    residual add rides in the product's epilogue, which hands the row sums of squares to the norm."""
+    return ops.rmsnorm_apply(x, ops.linear_residual_big(a, w, x), norm_w, eps)
 
 
 class _TokenEmbed(torch.autograd.Function):
-    """emb_bf16[tokens] (the gather of viktor/model.py:77) with the table's gradient as the fp32 sum of the
-    gradient rows of each token id (vk_embed_grad: deterministic, no atomics)."""
+    """emb[tokens] in fp32 (the gather of viktor/model.py:77, 81-84: nn.Embedding of fp32 weights, which autocast
+    leaves in fp32) with the table's gradient as the fp32 sum of the gradient rows of each token id (vk_embed_grad:
+    deterministic, no atomics)."""
 
     @staticmethod
     def forward(ctx, weight, tokens):
         ctx.save_for_backward(tokens)
         ctx.vocab = weight.shape[0]
-        return weight.detach().to(BF16)[tokens]
+        return weight.detach().float()[tokens]
 
     @staticmethod
     def backward(ctx, d_rows):
         (tokens,) = ctx.saved_tensors
-        d = d_rows.reshape(-1, d_rows.shape[-1]).to(BF16).contiguous()
+        d = d_rows.reshape(-1, d_rows.shape[-1]).float().contiguous()
         return ops.embed_grad(d, tokens.reshape(-1).contiguous(), ctx.vocab), None
 
 
@@ -125,16 +128,17 @@ class _LMHead(torch.autograd.Function):
 
 
 class _PackRows(torch.autograd.Function):
-    """The packed decoder input x [N, d] bf16: the real prefix rows of each window followed by its token rows
-    (the sequence viktor/model.py:72-86 builds per window, without its padding). prefix [B P, d] and emb
-    [B T, d]: the projector's and the embedding's rows; pre_src / pre_dst: the real prefix rows and their packed
-    rows; tok_rows: the packed rows of the tokens, in emb's order. Each source row is used once, so the backward
-    is two row gathers (no accumulation); all_prefix: every prefix row is real (pre_src is 0 .. B P - 1)."""
+    """The packed decoder input x [N, d] fp32: the real prefix rows of each window followed by its token rows
+    (the sequence viktor/model.py:72-86 builds per window with fp32 gathers, without its padding). prefix [B P, d]
+    bf16 and emb [B T, d] fp32: the projector's and the embedding's rows; pre_src / pre_dst: the real prefix rows
+    and their packed rows; tok_rows: the packed rows of the tokens, in emb's order. Each source row is used once,
+    so the backward is two row gathers (no accumulation), the prefix rows' gradient rounded to bf16 as the
+    backward of prefix.float() rounds it; all_prefix: every prefix row is real (pre_src is 0 .. B P - 1)."""
 
     @staticmethod
     def forward(ctx, prefix, emb, pre_src, pre_dst, tok_rows, all_prefix):
-        x = torch.empty(pre_dst.numel() + tok_rows.numel(), prefix.shape[1], dtype=BF16, device=prefix.device)
-        x.index_copy_(0, pre_dst, prefix if all_prefix else prefix.index_select(0, pre_src))
+        x = torch.empty(pre_dst.numel() + tok_rows.numel(), prefix.shape[1], dtype=torch.float32, device=prefix.device)
+        x.index_copy_(0, pre_dst, (prefix if all_prefix else prefix.index_select(0, pre_src)).float())
         x.index_copy_(0, tok_rows, emb)
         ctx.save_for_backward(pre_src, pre_dst, tok_rows)
         ctx.n_prefix, ctx.all_prefix = prefix.shape[0], all_prefix
@@ -143,17 +147,22 @@ class _PackRows(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dx):
         pre_src, pre_dst, tok_rows = ctx.saved_tensors
-        g = dx.index_select(0, pre_dst)
+        g = dx.index_select(0, pre_dst).to(BF16)
         if ctx.all_prefix:
             dp = g
         else:
-            dp = dx.new_zeros(ctx.n_prefix, dx.shape[1])
+            dp = g.new_zeros(ctx.n_prefix, dx.shape[1])
             dp.index_copy_(0, pre_src, g)
         return dp, dx.index_select(0, tok_rows), None, None, None, None
 
 
+_NORMS = ("attn_norm.weight", "attn.q_norm.weight", "attn.k_norm.weight", "mlp_norm.weight")
+
+
 class _DecoderStack(torch.autograd.Function):
-    """x [N, d] bf16 packed rows -> final-normed hidden of the token rows [n_tok, d] bf16."""
+    """x [N, d] fp32 packed rows -> final-normed hidden of the token rows [n_tok, d] bf16, with the rounding
+    points of FastDecoder.teacher_forced (torch.autocast bf16 over fp32 master weights): products on bf16 weights,
+    the RMSNorms (QK-norm included) on the fp32 weights, an fp32 residual stream."""
 
     @staticmethod
     def forward(ctx, x, meta, *params):
@@ -161,10 +170,12 @@ class _DecoderStack(torch.autograd.Function):
         H, HKV, D, eps = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.norm_eps
         L = cfg.n_layers
         N = x.shape[0]
-        w = [p.detach().to(BF16).contiguous() for p in params]
+        norm_slot = {8 * i + _LAYER_PARAMS.index(n) for i in range(L) for n in _NORMS} | {8 * L}
+        w = [p.detach().float().contiguous() if j in norm_slot else p.detach().to(BF16).contiguous()
+             for j, p in enumerate(params)]
         plan, rpos, cos, sin = meta["plan"], meta["rpos"], meta["cos"], meta["sin"]
-        x = x.detach().contiguous().clone()
-        h = ops.add_rmsnorm(x, w[0], eps)
+        x = x.detach().float().contiguous().clone()
+        h = ops.rmsnorm_f32(x, w[0], eps)
         saved = []
         for i in range(L):
             wa, wqkv, wqn, wkn, wo, wm, wgu, wd = w[8 * i:8 * i + 8]
@@ -220,7 +231,7 @@ class _DecoderStack(torch.autograd.Function):
             dx, ga = ops.rmsnorm_backward(x_in, wa, dhh, eps, dres=dx)  # d / d x_in
             grads[8 * i:8 * i + 8] = [ga, gqkv, gqn, gkn, go, gm, ggu, gd]
         ctx.saved_acts = None
-        return (dx.to(BF16), None, *[gr.float() for gr in grads])
+        return (dx, None, *[gr.float() for gr in grads])
 
 
 class TrainPlan:
@@ -249,7 +260,7 @@ def train_logits(model, frames, tokens_in, plens=None):
     proj = model.projector
     prefix = _Projector.apply(frames.reshape(B * P, -1).to(BF16).contiguous(), proj[0].weight, proj[0].bias,
                               proj[2].weight, proj[2].bias)                            # [B P, d] bf16
-    emb = _TokenEmbed.apply(dec.embed.weight, tokens_in.to(dev).reshape(-1))          # [B T, d] bf16
+    emb = _TokenEmbed.apply(dec.embed.weight, tokens_in.to(dev).reshape(-1))          # [B T, d] fp32
     # packed layout, window b: its plens[b] real prefix rows, then its T token rows; row indices on the host
     seq_lens = [p + T for p in plens_h]
     s = model.pos_scale
@@ -266,7 +277,7 @@ def train_logits(model, frames, tokens_in, plens=None):
     rpos = idx[2 * n_pre + n_tok:].to(torch.int32)
     x = _PackRows.apply(prefix, emb, pre_src_d, pre_dst_d, tok_rows, n_pre == B * P)
     plan = TrainPlan(seq_lens, dev)
-    cos, sin = dec.cos.contiguous(), dec.sin.contiguous()
+    cos, sin = dec.cos.float().contiguous(), dec.sin.float().contiguous()
     meta = {"cfg": cfg, "plan": plan, "rpos": rpos, "cos": cos, "sin": sin, "tok_rows": tok_rows}
     h = _DecoderStack.apply(x, meta, *decoder_params(dec))
     return _LMHead.apply(h, dec.lm_head.weight).view(B, T, -1)
