@@ -10,15 +10,19 @@ once and keeps one prefix KV copy per group (--group-size 1: every sequence pref
 Extra objects on the JSON line:
   roofline      decode attention, the dominant kernel: algorithmic bytes per call (every K/V byte the call
                 must read once -- the shared prefix once per group, each sequence's own rows -- plus q and
-                out) / its average duration, measured here with HIP events on the launch stream over calls
-                at the lengths of 32 evenly spaced decode steps, rotating over the 8 layers' caches as the
-                captured step does (so no call finds its bytes in the Infinity Cache); the back-to-back
-                figure on one layer is kept as warm_*;
+                out) / its average duration inside the captured decode step: device timestamp nodes captured
+                right before and after each layer's attention launch (less the dispatch gap a back-to-back pair
+                of them measures), read at 32 evenly spaced steps of a rollout. Also
+                kept: eager_* (HIP events over eager calls at the same lengths, rotating over the 8 layers'
+                caches so no call finds its bytes in the Infinity Cache) and warm_* (back to back on one layer);
                 traffic = measured HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by a copy
                 kernel; read from profiles/decode_attention_traffic.json when present, else null).
   cpu_baseline  the CPU oracle (the reference's fp32 torch path restated) on this host's usable cores: the
                 CPU-plumbing configuration at full size (4 sequences x 2048-frame prefix x 64 greedy tokens,
                 8 layers, seed 0); tokens/s, with the host's CPU count, affinity, quota and model.
+  decode_roofline_ms / decode_hbm_frac  the rollout's decode against its own HBM roofline: every attended K/V
+                position once per step (the shared prefix once per group), the new positions written, the
+                weights read once per step, at 8 TB/s.
   configs       the other configurations, each against its own roofline: the rollout without prefix sharing
                 (every sequence prefilled and cached alone, as the reference does), varlen prefill + 4-mer
                 decode (1024 sequences, 340 tokens, vocab 343), scoring (512 x (2048 + 700..1024) forward +
@@ -146,6 +150,12 @@ def _bf16_model(k, dev, seed=0):
     return g.eval()
 
 
+def _master_model(k, dev, seed=0):
+    """The fp32 master model on the device, as the reference's scoring runs it (under torch.autocast)."""
+    from viktor_amd.synthetic import make_model
+    return make_model(k, n_layers=8, seed=seed, rope_theta=1e6).to(dev).eval()
+
+
 def rollout_ungrouped(dev, gm, fr, u):
     """The rollout configuration as the reference runs it: every one of the 512 sequences prefilled and cached
     on its own (no prefix sharing, scripts/gspo.py:444 + viktor/engine.py:168-201); 1024 sampled tokens."""
@@ -219,13 +229,14 @@ def varlen_kmer_config(dev, steps=340):
 def scoring_config(dev, reps=2):
     """GSPO scoring: 512 sequences x (2048-frame prefix + 700..1024 response tokens), the teacher-forced forward
     of token_logprobs (scripts/gspo.py:340-353), then the sequence-ratio loss and its gradient w.r.t. the
-    logits (scripts/gspo.py:459-477).
+    logits (scripts/gspo.py:459-477), with the fp32 master model and the autocast rounding points the reference
+    scores with (an fp32 residual stream).
     Algorithmic flops per sequence of n = 2048 + L rows: the projector per frame, 2 x weights per row less the
     last layer's products for the prefix rows (only the L token rows need logits), causal attention
     1024 n (n + 1) per layer, the LM head per token."""
     from viktor_amd import gspo as G
     from viktor_amd.synthetic import scoring_inputs
-    gm = _bf16_model(1, dev)
+    gm = _master_model(1, dev)
     B = PREFIXES * GROUP
     seqs, ended = scoring_inputs(B, 700, 1024, k=1, seed=5)
     g = torch.Generator(device=dev).manual_seed(6)
@@ -253,8 +264,9 @@ def scoring_config(dev, reps=2):
            "tokens_per_s": round(sum(L) / (ms / 1e3), 1), "alg_tflop": round(flops / 1e12, 2),
            "achieved_tflops": round(flops / (ms / 1e3) / 1e12, 1),
            "mfma_frac": round(flops / (ms / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-           "includes": "projector + teacher-forced 8-layer forward (padded to a multiple of 128 tokens, as the "
-                       "reference pads) + LM head + log-probs, ratio, clipped loss and dL/dlogits [512, T, 7]"}
+           "includes": "projector + teacher-forced 8-layer forward (fp32 master weights, autocast rounding points, "
+                       "padded to a multiple of 128 tokens as the reference pads) + LM head + log-probs, ratio, "
+                       "clipped loss and dL/dlogits [512, T, 7]"}
     del fr
     torch.cuda.empty_cache()
     return out
@@ -351,6 +363,62 @@ def decode_attention_timing(eng, prefix_lens, steps, n_points=32, rounds=2, warm
         total_bytes += len(seq) * (kv_rows * KV_ROW_BYTES + 2 * B * 8 * 64 * 2)
     avg_s = total_ms / 1e3 / launches
     return avg_s, total_bytes / launches
+
+
+def in_graph_attention_timing(gm, fr, u, plens, group_size, n_points=32):
+    """The decode attention inside the captured rollout step itself: a second engine of the benchmark's shape
+    captures its step with a device timestamp (vk_timestamp, a one-thread kernel storing the GPU's constant-rate
+    clock) right before and right after each layer's attention launch, and a back-to-back pair at the step's end;
+    it runs the rollout's prefill and its 1023 steps by single-step replays and, at n_points evenly spaced steps,
+    waits for the step and reads the stamps. A launch's time is its pair's interval less the back-to-back pair's
+    (the dispatch gap between two graph nodes). Returns (average seconds per launch, algorithmic bytes per launch
+    averaged over the same steps)."""
+    import ctypes
+    from viktor_amd import DecodeEngine
+    from viktor_amd._lib import call, stream_handle
+    B = PREFIXES * GROUP
+    eng = DecodeEngine(gm, B, NEW, P, temperature=1.0, group_size=group_size, cuda_graph=False, check_every=1)
+    layers = eng.cache.k.shape[0]
+    stamps = torch.zeros(2 * layers + 2, dtype=torch.int64, device=gm.decoder.lm_head.weight.device)
+    khz = ctypes.c_int64(0)
+    call("vk_timestamp_rate_khz", ctypes.byref(khz))
+    stamp = lambda i: call("vk_timestamp", stamps.data_ptr(), i, stream_handle())
+    eng.fast.attn_marks = lambda i, k: stamp(2 * i + k)
+    step = eng._step
+
+    def step_with_gap():  # the step, then the back-to-back pair
+        step()
+        stamp(2 * layers)
+        stamp(2 * layers + 1)
+
+    eng._step = step_with_gap
+    try:
+        eng._capture()
+    finally:
+        eng.fast.attn_marks = None
+        eng._step = step
+    eng.set_uniforms(u)
+    eng.prefill(fr, plens)
+    steps = NEW - 1
+    js = {round(i * (steps - 1) / (n_points - 1)) for i in range(n_points)}
+    pl = torch.as_tensor(plens, dtype=torch.int64)
+    total_ticks, total_bytes, launches = 0, 0.0, 0
+    for j in range(steps):
+        eng.graph.replay()
+        if j in js:
+            t = stamps.cpu()  # waits for the step
+            gap = int(t[2 * layers + 1] - t[2 * layers])
+            total_ticks += sum(int(t[2 * i + 1] - t[2 * i]) - gap for i in range(layers))
+            if group_size > 1:
+                kv_rows = int((pl[::group_size] + 1).sum()) + B * (j + 1)
+            else:
+                kv_rows = int((pl + 2 + j).sum())
+            total_bytes += layers * (kv_rows * KV_ROW_BYTES + 2 * B * 8 * 64 * 2)
+            launches += layers
+    torch.cuda.synchronize()
+    del eng
+    torch.cuda.empty_cache()
+    return total_ticks / (khz.value * 1e3) / launches, total_bytes / launches
 
 
 def _cpu_info():
@@ -660,7 +728,7 @@ def main():
     value = B * NEW * args.steps / dt
 
     log("decode-attention timing")
-    avg_s, alg_bytes = decode_attention_timing(eng, plens, NEW - 1)
+    eager_s, eager_bytes = decode_attention_timing(eng, plens, NEW - 1)
     warm_s, warm_bytes = decode_attention_timing(eng, plens, NEW - 1, warm=True)
     if args.group_size == 1:
         attn_kernels = "decode_attention (decode_attn_kernel)"
@@ -669,7 +737,7 @@ def main():
         members, parts = ops.decode_attention_grouped_layout(B, args.group_size, P + 1, eng.cache.k.shape[2])
         attn_kernels = (f"decode_attention_grouped (grouped_attn_kernel: {members} query members per workgroup, "
                         f"{parts} part(s)" + (" + grouped_combine_kernel)" if parts > 1 else ", no merge launch)"))
-    achieved = alg_bytes / avg_s / 1e9
+    achieved = None  # set from the in-graph timing below
     traffic = None
     tname = "decode_attention_traffic.json" if args.group_size == 1 else "decode_attention_grouped_traffic.json"
     tpath = os.path.join(ROOT, "profiles", tname)
@@ -685,6 +753,15 @@ def main():
     live = int(((out != 0) & (out != 2)).sum())
     del eng
     torch.cuda.empty_cache()
+    log("decode-attention timing inside the captured step")
+    avg_s, alg_bytes = in_graph_attention_timing(gm, fr, u, plens, args.group_size)
+    achieved = alg_bytes / avg_s / 1e9
+    # the decode's own HBM roofline: every attended K/V position once (the shared prefix once per group), the new
+    # positions written, the weights read once per step
+    if args.group_size > 1:
+        dec_roof = decode_roofline_ms(lambda j: PREFIXES * (P + 1) + B * (j + 1), NEW - 1, B)
+    else:
+        dec_roof = decode_roofline_ms(lambda j: B * (P + 2 + j), NEW - 1, B)
     configs = {}
     if not args.no_configs:
         configs = other_configs(dev, gm, fr, u)
@@ -710,6 +787,7 @@ def main():
                    "prefix_kv_shared_by": args.group_size,
                    "parallelism": "single GPU"},
         "prefill_ms": round(prefill_ms, 2), "decode_ms": round(decode_ms, 2),
+        "decode_roofline_ms": round(dec_roof, 1), "decode_hbm_frac": round(dec_roof / decode_ms, 4),
         "prefill": prefill_obj,
         "live_tokens_per_rollout": live,
         "roofline": {"kernel": attn_kernels,
@@ -717,9 +795,13 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "avg_launch_us": round(avg_s * 1e6, 2),
                      "alg_bytes_per_launch": int(alg_bytes),
-                     "timing": "HIP events over calls at 32 evenly spaced decode steps' lengths, rotating over the "
-                               "8 layers' caches as the captured step does (no call reads what the one before "
-                               "left in the 256 MB Infinity Cache)",
+                     "timing": "inside the captured decode step: device timestamp nodes right before and after each "
+                               "layer's attention launch, less the dispatch gap of a back-to-back pair, read at 32 "
+                               "evenly spaced steps of a rollout",
+                     "eager_avg_launch_us": round(eager_s * 1e6, 2),
+                     "eager_frac": round(eager_bytes / eager_s / 1e9 / HBM_PEAK_GBS, 4),
+                     "eager_timing": "HIP events over eager calls at the same steps' lengths, rotating over the 8 "
+                                     "layers' caches",
                      "warm_avg_launch_us": round(warm_s * 1e6, 2),
                      "warm_frac": round(warm_bytes / warm_s / 1e9 / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,

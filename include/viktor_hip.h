@@ -513,6 +513,16 @@ int vk_deepnorm_rmsnorm(const float *y, const float *bias, void *x, float alpha,
 int vk_gemm_rows(const void *x, const void *w, void *y, int64_t M, int32_t N, int32_t K, int32_t epilogue,
                  void *stream);
 
+/*
+ * Timing support, no counterpart in the reference (its benchmark times whole replays): vk_timestamp stores the
+ * device's constant-rate wall clock, read when its one-thread kernel runs, to stamps[index] (uint64, device
+ * memory). Launched on a capturing stream it becomes a graph node, so a pair around another node times that node
+ * inside the captured graph (less the dispatch gap a back-to-back pair measures). vk_timestamp_rate_khz: the
+ * clock's rate.
+ */
+int vk_timestamp(uint64_t *stamps, int64_t index, void *stream);
+int vk_timestamp_rate_khz(int64_t *khz);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,6 +76,10 @@ def test_argument_errors_return_status_without_device_work():
     assert rc == 1 and b"fp32 rotary tables" in lib.vk_last_error()
     rc = lib.vk_rmsnorm_backward(p, 1, p, 0, p, 0, None, p, p, 4, 512, 1e-6, None)  # fp32 x with bf16 weights
     assert rc == 3
+    rc = lib.vk_timestamp(None, 0, None)
+    assert rc == 1 and b"null" in lib.vk_last_error()
+    rc = lib.vk_timestamp(p, -1, None)
+    assert rc == 1 and b"negative" in lib.vk_last_error()
     with pytest.raises(_lib.HipLibraryError):
         _lib.check(rc, "decode_attention")
 

@@ -77,6 +77,8 @@ SIGNATURES = {
     "vk_linear_residual_big": [_P, _P, _P, _I32, _I64, _I32, _I32, _P, _F, _P, _P],
     "vk_rmsnorm_apply_ss": [_P, _I32, _P, _I32, _P, _I32, _P, _I64, _I32, _F, _P],
     "vk_rmsnorm_f32": [_P, _P, _P, _I64, _I32, _F, _P],
+    "vk_timestamp": [_P, _I64, _P],
+    "vk_timestamp_rate_khz": [ctypes.POINTER(_I64)],
     "vk_linear_qkv_rope": [_P, _P, _I64, _I32, _P, _P, _I32, _F, _P, _P, _I32, _I64, _P, _P, _P, _P, _I64, _P, _P, _I64, _I64,
                            _I64, _I64, _P, _P, _I64, _I32, _I32, _I32, _P],
 }

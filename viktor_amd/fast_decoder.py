@@ -99,6 +99,9 @@ class FastDecoder:
         self._wcache = {}
         self._plans = {}
         self.decode_workspace = None
+        # optional attn_marks(layer, k): called right before (k = 0) and after (k = 1) each decode step's attention
+        # launch, on the launching stream -- the benchmark records timing events there, inside the captured step
+        self.attn_marks = None
 
     # weights: bf16 views of the module's parameters (in place when the module is bf16, so weight syncs
     # into it stay visible to captured graphs; converted copies, refreshed on change, otherwise)
@@ -321,11 +324,15 @@ class FastDecoder:
                 q = ops.norm_qkv_rope_cache(xr, W(blk.attn_norm.weight), eps, W(a.qkv_proj.weight), W(a.q_norm.weight),
                                             W(a.k_norm.weight), cos, sin, pos, seq, kc, vc, H, HKV, D, rope_pos=rope_pos,
                                             ss=ss_attn)
+            if self.attn_marks is not None:
+                self.attn_marks(i, 0)
             if prefix is None:
                 o = ops.decode_attention(q, kc, vc, cache_seqlens, workspace=ws, rows=seq)
             else:
                 pc, plen32, G, gws = prefix
                 o = ops.decode_attention_grouped(q, pc.k[i], pc.v[i], plen32, kc, vc, cache_seqlens, G, workspace=gws)
+            if self.attn_marks is not None:
+                self.attn_marks(i, 1)
             ops.linear_residual(o.view(B, H * D), W(a.o_proj.weight), xr, ss_out=ss_mlp)
             g = ops.norm_linear(xr, W(blk.mlp_norm.weight), eps, W(blk.gate_up.weight), swiglu=True, ss=ss_mlp)
             last = i == len(layers) - 1
