@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/viktor_hip.h"
 
 namespace vk {
@@ -147,5 +149,19 @@ int launch_status(const char *what);
   } while (0)
 
 #define VK_STREAM(s) reinterpret_cast<hipStream_t>(s)
+
+// Raise a kernel's dynamic-LDS limit once per process, thread-safe: each call site keeps its own once_flag
+// and status (the hipFuncSetAttribute status of the first call, seen by every later caller).
+#define VK_RAISE_LDS_ONCE(kernel, bytes, what)                                                                 \
+  do {                                                                                                        \
+    static std::once_flag vk_lds_once_;                                                                       \
+    static hipError_t vk_lds_status_ = hipSuccess;                                                            \
+    std::call_once(vk_lds_once_, [] {                                                                         \
+      vk_lds_status_ = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),                           \
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)); \
+    });                                                                                                       \
+    if (vk_lds_status_ != hipSuccess)                                                                         \
+      return ::vk::fail(VK_ERR_LAUNCH, "%s: cannot reserve %zu bytes of LDS", what, static_cast<size_t>(bytes)); \
+  } while (0)
 
 static inline bool vk_aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

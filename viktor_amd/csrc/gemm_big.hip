@@ -483,13 +483,7 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
 template <int EPI>
 static int launch_big(const bf16_t *x, const bf16_t *w, void *y, int64_t M, int N, int K, const GbQkv &qa,
                       hipStream_t s) {
-  static bool configured = false;
-  if (!configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_big_kernel<EPI>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(GB_SMEM)) != hipSuccess)
-      return fail(VK_ERR_LAUNCH, "linear: cannot reserve %zu bytes of LDS", GB_SMEM);
-    configured = true;
-  }
+  VK_RAISE_LDS_ONCE(gemm_big_kernel<EPI>, GB_SMEM, "linear");
   constexpr int OUT_COLS = EPI == GB_SWIGLU ? 64 : 128;
   const int tiles_n = (N + OUT_COLS - 1) / OUT_COLS;
   const int64_t tiles_m = (M + GB_BM - 1) / GB_BM;

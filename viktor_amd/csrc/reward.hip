@@ -120,11 +120,11 @@ extern "C" int vk_strict_identity(const uint8_t *calls, const int64_t *call_off,
   // LDS: 3 diagonals x (distance, count) int16 of max_ref_len + 1 rows, the label, its mask and the call
   const size_t lds = 3 * 2 * 2 * static_cast<size_t>(max_ref_len + 1) + 2 * static_cast<size_t>(max_ref_len) +
                      static_cast<size_t>(max_call_len) + 16;
-  if (lds > 65536) {  // labels past about 3.3 kb need more than the default 64 KB of dynamic LDS
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(strict_identity_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    if (e != hipSuccess) return fail(VK_ERR_LAUNCH, "strict_identity: %zu bytes of LDS: %s", lds, hipGetErrorString(e));
-  }
+  // labels past about 3.3 kb need more than the default 64 KB of dynamic LDS: the limit is raised once, to what the
+  // largest label and call take, so concurrent callers never lower it under each other
+  constexpr size_t kMaxLds = 3 * 2 * 2 * static_cast<size_t>(RW_MAX_REF + 1) + 2 * static_cast<size_t>(RW_MAX_REF) +
+                             static_cast<size_t>(RW_MAX_CALL) + 16;
+  if (lds > 65536) VK_RAISE_LDS_ONCE(strict_identity_kernel, kMaxLds, "strict_identity");
   strict_identity_kernel<<<static_cast<unsigned>(n_calls), 64, lds, VK_STREAM(stream)>>>(
       calls, call_off, call_len, refs, ref_off, ref_len, scored, ref_of_call, n_refs, max_ref_len, max_call_len,
       empty_max, reward, edit_distance, scored_errors);

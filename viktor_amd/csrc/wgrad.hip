@@ -239,13 +239,7 @@ extern "C" int vk_wgrad(const void *a, int64_t lda, const void *b, int64_t ldb, 
   VK_CHECK_ARG(workspace_bytes >= need, "wgrad: workspace of %lld bytes needed", static_cast<long long>(need));
   VK_CHECK_ARG(static_cast<int64_t>(tiles) * slices < (int64_t(1) << 31), "wgrad: too many workgroups");
   const int64_t steps = (N + WG_BR - 1) / WG_BR;
-  static bool lds_ok = false;  // 96 KB of dynamic LDS is above the default limit: raise it once
-  if (!lds_ok) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(wgrad_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(WG_SMEM)) != hipSuccess)
-      return fail(VK_ERR_LAUNCH, "wgrad: cannot reserve %zu bytes of LDS", WG_SMEM);
-    lds_ok = true;
-  }
+  VK_RAISE_LDS_ONCE(wgrad_kernel, WG_SMEM, "wgrad");  // 96 KB of dynamic LDS is above the default limit
   hipStream_t s = VK_STREAM(stream);
   wgrad_kernel<<<static_cast<unsigned>(tiles * slices), (WG_CONS + WG_PROD) * 64, WG_SMEM, s>>>(
       static_cast<const bf16_t *>(a), lda, static_cast<const bf16_t *>(b), ldb, N, Ka, Kb, tiles_kb, tiles, slices,

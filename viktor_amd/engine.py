@@ -33,9 +33,13 @@ class DecodeEngine:
     def __init__(self, model, batch_size: int, max_new_tokens: int, max_frames: int, backend: str = "auto",
                  cuda_graph: bool = True, prefill_batch: int = 128, check_every: int = 32,
                  attention_backend: str = "auto", temperature: float = 0.0, max_homopolymer=64, group_size: int = 1,
-                 logprobs: bool = False):
+                 logprobs: bool = False, force_eos_last: bool = False):
         self.model, self.dec = model, model.decoder
         self.temperature = float(temperature)
+        # force_eos_last: the last output column (max_new_tokens - 1) is EOS for every sequence still running when
+        # it is produced (a rollout capped at max_new_tokens ends with EOS); off by default, as the reference
+        # scores a call that never ends as it stands (scripts/gspo.py:24-25)
+        self.force_eos_last = bool(force_eos_last)
         dev = self.dec.lm_head.weight.device
         self.dtype = self.dec.lm_head.weight.dtype
         self.pos_scale = getattr(model, "pos_scale", 1)
@@ -240,6 +244,8 @@ class DecodeEngine:
         self.tok.fill_(BOS)
         self.run.zero_()
         self.out.fill_(PAD)
+        if self.logp is not None:  # columns past an early stop read 0, as out reads PAD there
+            self.logp.zero_()
         self.plen.copy_(torch.tensor(frame_lens, device=self.pos.device))
         self.pos.copy_(self.plen)  # the select kernel writes column pos - plen = 0, then advances pos to plen + 1
         if G > 1:
@@ -301,6 +307,11 @@ class DecodeEngine:
                 n = done
                 break
         self.step_idx.add_(n)
+        if self.force_eos_last and n == self.max_new - 1:
+            # the last column holds a token only where the sequence was still running (PAD after its EOS
+            # otherwise): that token becomes EOS
+            last = self.out[:, self.max_new - 1]
+            last.masked_fill_(last != PAD, EOS)
         return self.out
 
     def generate(self, frames, frame_lens, steps=None):

@@ -29,9 +29,12 @@ class PrefillPlan:
 
     seq_lens[j]: tokens of sequence j (packed back to back); rows[j]: its KV-cache row (None without a
     cache); keep[j]: rows of sequence j kept by the last layer (its final keep[j] positions), None to keep
-    all. Construction uploads the few small index tensors once; engines cache plans per layout."""
+    all. last_rows[j] (instead of keep): the one packed row of sequence j that finishes the last layer, any of
+    its rows, attending to the whole sequence (the reference's last-layer call, viktor/fast_decoder.py:64-69:
+    flash_attn_varlen_func(q[last_indices], ..., max_seqlen_q=1, causal=False)). Construction uploads the few
+    small index tensors once; engines cache plans per layout."""
 
-    def __init__(self, seq_lens, device, rows=None, keep=None, cache=None):
+    def __init__(self, seq_lens, device, rows=None, keep=None, cache=None, last_rows=None):
         seq_lens = [int(n) for n in seq_lens]
         _require(all(n > 0 for n in seq_lens), "PrefillPlan: empty sequence")
         self.seq_lens = seq_lens
@@ -60,7 +63,21 @@ class PrefillPlan:
         self.last = None
         self.last_idx = None
         self.bos_lengths = None
-        if self.keep is not None:
+        self.last_causal = True
+        if last_rows is not None:
+            _require(keep is None, "PrefillPlan: keep and last_rows are exclusive")
+            lr = [int(r) for r in last_rows]
+            _require(len(lr) == self.n_seq and all(cu[j] <= r < cu[j + 1] for j, r in enumerate(lr)),
+                     "PrefillPlan: last_rows must name one row inside each sequence")
+            self.keep = [1] * self.n_seq
+            self.last_causal = False  # the one query attends to every key of its sequence
+            self.last_idx = torch.tensor(lr, dtype=torch.int64).to(device)
+            if cache is not None:
+                self.last = ops.AttentionPlan(self.keep, seq_lens, k_off, device, causal=False)
+                if all(r == self.rows[0] + j for j, r in enumerate(self.rows)):
+                    # one query per sequence over its whole cached row: the single-query decode kernel
+                    self.bos_lengths = torch.tensor(seq_lens, dtype=torch.int32).to(device)
+        elif self.keep is not None:
             _require(len(self.keep) == self.n_seq and all(0 < k <= n for k, n in zip(self.keep, seq_lens)),
                      "PrefillPlan: keep counts")
             # rows cu[j + 1] - keep[j] .. cu[j + 1] - 1 of every sequence j, in order
@@ -79,7 +96,8 @@ class PrefillPlan:
         """Attention plans over packed k/v rows [total, HKV, D] (no cache)."""
         k_off = [c * hkv_d for c in self.cu[:-1]]
         full = ops.AttentionPlan(self.seq_lens, self.seq_lens, k_off, self.device, causal=True)
-        last = None if self.keep is None else ops.AttentionPlan(self.keep, self.seq_lens, k_off, self.device, causal=True)
+        last = None if self.keep is None else ops.AttentionPlan(self.keep, self.seq_lens, k_off, self.device,
+                                                                causal=self.last_causal)
         return full, last
 
 
@@ -230,21 +248,30 @@ class FastDecoder:
         cu_seqlens [b+1] int32. Fills the cache rows of those sequences. Returns hidden [n, d], or the kept
         rows when last_indices and cu_queries are given together (e.g. [b, d] at each sequence's last
         position). plan: a PrefillPlan of this layout (built here from cu_seqlens / seq / cu_queries
-        otherwise, which reads them back to the host). Reference: viktor/fast_decoder.py:62-74."""
+        otherwise, which reads them back to the host). With last_indices, the last layer finishes row
+        last_indices[j] of each sequence j (any of its rows: the reference's engine passes the BOS rows), which
+        attends to the whole sequence, as the reference's last-layer attention (non-causal, one query per
+        sequence: cu_queries must be 0, 1, .., n; anything else raises ValueError). Reference:
+        viktor/fast_decoder.py:62-74."""
         require_device(x, "FastDecoder.prefill")
         _require((last_indices is None) == (cu_queries is None), "prefill: last_indices and cu_queries go together")
         if plan is None:
             cu = [int(c) for c in cu_seqlens.tolist()]
             lens = [b - a for a, b in zip(cu[:-1], cu[1:])]
-            keep = None
+            last_rows = None
             if cu_queries is not None:
                 cq = [int(c) for c in cu_queries.tolist()]
-                keep = [b - a for a, b in zip(cq[:-1], cq[1:])]
+                if cq != list(range(len(lens) + 1)):
+                    raise ValueError("prefill: cu_queries must hold one query per sequence (0, 1, .., n), as the "
+                                     "reference's last-layer call reads it with max_seqlen_q = 1")
+                last_rows = [int(r) for r in last_indices.tolist()]
+                if len(last_rows) != len(lens) or not all(cu[j] <= r < cu[j + 1] for j, r in enumerate(last_rows)):
+                    raise ValueError("prefill: last_indices must name one row inside each sequence")
             rows = None
             if cache is not None:
                 seq_h = seq.tolist()
                 rows = [int(seq_h[c]) for c in cu[:-1]]
-            plan = PrefillPlan(lens, x.device, rows=rows, keep=keep, cache=cache)
+            plan = PrefillPlan(lens, x.device, rows=rows, cache=cache, last_rows=last_rows)
         _require(x.shape[0] == plan.total, "prefill: x rows != plan tokens")
         x = x.to(BF16).contiguous() if x.dtype != BF16 else x
         if cache is not None:
