@@ -233,6 +233,8 @@ int vk_varlen_attention(const void *q, const void *k, const void *v, const int32
  *   z = (logits[b] + bias) (fp32 logits, or bf16-rounded when h/w are given with round_bf16) ;
  *   greedy (temperature <= 0): nxt = first argmax of z;
  *   sampled: p = softmax(z / temperature) in fp32, nxt = first v with u < sum_{w<=v} p_w, u = uniforms[b * u_stride + col];
+ *   sampled with gumbel != 0 (the reference's formula, viktor/engine.py:80-83): nxt = first argmax over v of
+ *   z_v / temperature - log(-log(max(u_v, 1e-20))), u_v = uniforms[b * u_stride + col * V + v] (u_stride >= u_cols V);
  *   tail rule: EOS after a tail token; homopolymer rule (homo_stop > 0): run = (nxt == prev && is_homo[nxt]) ? run + 1 : 0,
  *   EOS when run + 1 >= homo_stop; PAD after EOS or PAD.
  *   out[b * out_stride + col] = nxt with col = pos[b] - plen[b]; tok[b] = nxt; pos[b] += 1;
@@ -250,7 +252,8 @@ int vk_varlen_attention(const void *q, const void *k, const void *v, const int32
 int vk_select_update(const float *logits, const void *h, const void *norm_w, float eps, const void *w_head,
                      int32_t d, int32_t round_bf16,
                      const float *bias, const uint8_t *is_tail, const uint8_t *is_homo, int32_t homo_stop,
-                     float temperature, const float *uniforms, int64_t u_stride, int64_t u_cols, int64_t *tok,
+                     float temperature, const float *uniforms, int64_t u_stride, int64_t u_cols, int32_t gumbel,
+                     int64_t *tok,
                      int64_t *run, int64_t *pos, const int64_t *plen, const int64_t *rope_off,
                      const int64_t *cache_base, int64_t *out,
                      int64_t out_stride, int64_t out_cols, int32_t *pos32, int32_t *seqlens, int32_t *rpos32,

@@ -362,6 +362,19 @@ def sample_inverse_cdf(z, u):
     return (pick if pick >= 0 else last_pos), margin
 
 
+def sample_gumbel(z, u):
+    """z [V] fp32 (logits + bias, already / T); u [V] uniforms in [0, 1). The reference's Gumbel-max choice
+    (viktor/engine.py:80-83): the first index of the maximum of z - log(-log(max(u, 1e-20))), computed in float32;
+    returns (token, the top-1 minus top-2 gap of those perturbed scores)."""
+    zn = z.numpy().astype(np.float32)
+    un = np.maximum(np.asarray(u, dtype=np.float32), np.float32(1e-20))
+    g = (zn - np.log(-np.log(un).astype(np.float32)).astype(np.float32)).astype(np.float32)
+    v = int(np.argmax(g))  # numpy returns the first maximal index
+    finite = np.sort(g[np.isfinite(g)])
+    gap = float(finite[-1] - finite[-2]) if finite.size >= 2 else np.inf
+    return v, gap
+
+
 def greedy_choice(z):
     """First index of the maximum, and the top-1 minus top-2 gap."""
     v = int(torch.argmax(z))  # torch.argmax returns the first maximal index
@@ -386,9 +399,13 @@ class RefEngine:
     """DecodeEngine semantics on the CPU (viktor/engine.py:31-220, torch backend; supplied-uniform
     sampling instead of device Gumbel noise). One sequence at a time; KV cache as per-layer tensors."""
 
-    def __init__(self, ref: RefModel, max_new, temperature=0.0, max_homopolymer=64, bias=None):
+    def __init__(self, ref: RefModel, max_new, temperature=0.0, max_homopolymer=64, bias=None, sampling="inverse_cdf"):
         """bias: [V] additive logit bias replacing the engine's default (-inf at PAD and BOS), e.g. one that
-        also bans EOS so that every sequence runs to max_new (DecodeEngine.bias is the same tensor)."""
+        also bans EOS so that every sequence runs to max_new (DecodeEngine.bias is the same tensor).
+        sampling "gumbel": the reference's formula (viktor/engine.py:80-83), argmax of
+        z / T - log(-log(clamp(u, 1e-20))) with uniforms [B, steps, V]; "inverse_cdf": uniforms [B, steps]."""
+        assert sampling in ("inverse_cdf", "gumbel")
+        self.gumbel = sampling == "gumbel"
         self.ref = ref
         self.max_new = max_new
         self.T = float(temperature)
@@ -402,7 +419,9 @@ class RefEngine:
 
     def _choose(self, logits, prev, run, u):
         z = logits.float() + self.bias
-        if self.T > 0:
+        if self.T > 0 and self.gumbel:
+            raw, margin = sample_gumbel(z / self.T, u)
+        elif self.T > 0:
             raw, margin = sample_inverse_cdf(z / self.T, u)
         else:
             raw, margin = greedy_choice(z)
@@ -443,7 +462,10 @@ class RefEngine:
                 round_bf16 = fused and (j == 0 or self.T > 0)
                 z = ref.head(h, round_bf16)[0]
                 logit_rows[b, j] = z
-                u = float(uniforms[b, j]) if uniforms is not None else 0.0
+                if uniforms is None:
+                    u = 0.0
+                else:
+                    u = uniforms[b, j] if self.gumbel else float(uniforms[b, j])
                 raw, nxt, run_new, m = self._choose(z, prev, run, u)
                 choice[b, j] = nxt
                 margin[b, j] = m

@@ -55,9 +55,13 @@ def test_argument_errors_return_status_without_device_work():
     rc = lib.vk_decode_attention(p, p, p, p, None, 2, p, 4, 8, 2, 64, 3072 * 128, 128, 3072, None, 0, None)
     assert rc == 1 and b"cache holds 2 rows" in lib.vk_last_error()
     # logp_stride below the output columns would overlap rows
-    rc = lib.vk_select_update(p, None, None, 1e-6, None, 0, 0, p, p, p, 0, 0.0, None, 0, 0, p, None, p, None,
+    rc = lib.vk_select_update(p, None, None, 1e-6, None, 0, 0, p, p, p, 0, 0.0, None, 0, 0, 0, p, None, p, None,
                               None, None, p, 16, 16, None, None, None, p, 8, 4, 7, 2, 0, None)
     assert rc == 1 and b"logp_stride" in lib.vk_last_error()
+    # Gumbel uniforms whose row stride cannot hold u_cols x V entries
+    rc = lib.vk_select_update(p, None, None, 1e-6, None, 0, 0, p, p, p, 0, 1.0, p, 16, 16, 1, p, None, p, None,
+                              None, None, p, 16, 16, None, None, None, None, 0, 8, 7, 2, 0, None)
+    assert rc == 1 and b"Gumbel" in lib.vk_last_error()
     rc = lib.vk_linear_residual_big(p, p, p, 0, 4, 96, 64, None, 1.0, p, None)  # N % 128 != 0
     assert rc == 1 and b"N" in lib.vk_last_error()
     rc = lib.vk_linear_residual_big(p, p, p, 0, 4, 128, 64, None, 1.0, None, None)  # no sums-of-squares output

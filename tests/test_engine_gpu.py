@@ -110,7 +110,7 @@ def check_logprobs(eng_logp, oracle_res, forced, bias, T, tol=2e-2, pair_res=Non
 
 
 def run_case(k=1, n_layers=2, lens=(40, 130, 257, 75), steps=24, T=0.0, mh=8, seed=0, ps=1, graph=True, group=1,
-             check_every=32, decode_steps="fixed", ban_eos=False):
+             check_every=32, decode_steps="fixed", ban_eos=False, sampling="inverse_cdf"):
     m = make_model(k, n_layers=n_layers, seed=seed, norm_jitter=0.1, bias_jitter=0.1)
     m.pos_scale = ps
     lens = list(lens)
@@ -119,9 +119,11 @@ def run_case(k=1, n_layers=2, lens=(40, 130, 257, 75), steps=24, T=0.0, mh=8, se
         fr = torch.cat([w for w in fr.split(lens) for _ in range(group)])
         lens = [n for n in lens for _ in range(group)]
     u = synth_uniforms(len(lens), steps, seed=seed + 2)
+    if sampling == "gumbel":  # one uniform per vocabulary entry
+        u = torch.rand(len(lens), steps, m.tokenizer.vocab_size, generator=torch.Generator().manual_seed(seed + 2))
     gm = gpu_copy(m)
     eng = DecodeEngine(gm, len(lens), steps, max(lens), cuda_graph=graph, temperature=T, max_homopolymer=mh,
-                       prefill_batch=3, group_size=group, check_every=check_every)
+                       prefill_batch=3, group_size=group, check_every=check_every, sampling=sampling)
     bias = None
     if ban_eos:
         bias = no_eos_bias(m.tokenizer.vocab_size)
@@ -130,7 +132,7 @@ def run_case(k=1, n_layers=2, lens=(40, 130, 257, 75), steps=24, T=0.0, mh=8, se
         eng.set_uniforms(u.to(DEV))
     out = eng.generate(fr.to(DEV), lens, steps=steps if decode_steps == "fixed" else None).clone()
     torch.cuda.synchronize()
-    ref = R.RefEngine(R.RefModel(m, "fused"), steps, temperature=T, max_homopolymer=mh, bias=bias)
+    ref = R.RefEngine(R.RefModel(m, "fused"), steps, temperature=T, max_homopolymer=mh, bias=bias, sampling=sampling)
     res = ref.run(list(fr.split(lens)), uniforms=u if T > 0 else None, forced=out.cpu())
     return out, res, eng
 
@@ -198,6 +200,18 @@ def test_force_eos_last_and_logp_reset():
     e = eng.generate(fr, lens).cpu()
     assert bool((e[:, 0] == R.EOS).all()) and bool((e[:, 1:] == R.PAD).all())
     assert bool((eng.logp[:, 5:] == 0).all())
+
+
+def test_sampled_stream_parity_gumbel():
+    """The reference's Gumbel-max sampling (sampling="gumbel", one uniform per vocabulary entry): streams equal the
+    oracle's on the same uniforms, except where the perturbed scores' top-2 gap is under 3e-2 (one bf16 ulp of a
+    logit in [4, 8): sampled steps choose from bf16-rounded logits, as the reference's bf16 head makes them);
+    k-mer vocabulary too, in a captured graph."""
+    out, res, _ = run_case(k=1, T=1.0, steps=32, lens=(50, 300, 120, 9), mh=None, ban_eos=True, sampling="gumbel")
+    agree, _ = check_stream(out, res, 32, 3e-2, min_live=1.0)
+    assert agree > 0.9
+    out, res, _ = run_case(k=4, T=0.8, steps=16, lens=(64, 200, 31), mh=16, sampling="gumbel")
+    check_stream(out, res, 16, 3e-2)
 
 
 def test_grouped_greedy_stream_parity():

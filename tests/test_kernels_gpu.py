@@ -388,11 +388,13 @@ def test_varlen_attention_reads_cache_rows():
     assert (out.float().cpu() - ref).abs().max() < 1e-2
 
 
-def _select_ref(logits, prev, run, bias, tail, homo, homo_stop, T, u):
+def _select_ref(logits, prev, run, bias, tail, homo, homo_stop, T, u, gumbel=False):
     toks, runs, margins = [], [], []
     for b in range(logits.shape[0]):
         z = logits[b] + bias
-        if T > 0:
+        if T > 0 and gumbel:
+            raw, m = R.sample_gumbel(z / T, u[b].numpy())
+        elif T > 0:
             raw, m = R.sample_inverse_cdf(z / T, float(u[b]))
         else:
             raw, m = R.greedy_choice(z)
@@ -413,10 +415,16 @@ def _state(B, V, g, P=50):
     return tok, run, pos, plen, rope_off
 
 
-@pytest.mark.parametrize("V,T,fused_head", [(7, 0.0, False), (7, 1.0, False), (343, 0.0, False), (343, 0.7, False),
-                                             (7, 0.0, True), (343, 1.0, True)])
-def test_select_update(V, T, fused_head):
-    g = gen(V + int(T * 10) + int(fused_head))
+@pytest.mark.parametrize("V,T,fused_head,gumbel", [(7, 0.0, False, False), (7, 1.0, False, False),
+                                                    (343, 0.0, False, False), (343, 0.7, False, False),
+                                                    (7, 0.0, True, False), (343, 1.0, True, False),
+                                                    (7, 1.0, False, True), (343, 0.7, False, True),
+                                                    (343, 1.0, True, True)])
+def test_select_update(V, T, fused_head, gumbel):
+    """The choice + grammar + bookkeeping against the oracle's: greedy, inverse-CDF sampling and the reference's
+    Gumbel-max formula (uniforms [B, T, V]), from fp32 logits (exactly, ties to the first index) or from the fused
+    LM head (exempt where the oracle's margin is under the bf16 logits' rounding)."""
+    g = gen(V + int(T * 10) + int(fused_head) + 5 * int(gumbel))
     B, d, max_new = 300, 512, 64
     bias = torch.zeros(V)
     bias[[R.PAD, R.BOS]] = float("-inf")
@@ -429,7 +437,7 @@ def test_select_update(V, T, fused_head):
     homo[3:7] = True
     homo_stop = 4
     tok, run, pos, plen, rope_off = _state(B, V, g)
-    u = torch.rand(B, max_new, generator=g)
+    u = torch.rand(B, max_new, V, generator=g) if gumbel else torch.rand(B, max_new, generator=g)
     if fused_head:
         h = R.bf(torch.randn(B, d, generator=g))
         w = R.bf(torch.randn(V, d, generator=g) / math.sqrt(d) * 3)
@@ -441,7 +449,7 @@ def test_select_update(V, T, fused_head):
         tok[10], run[10] = 6, 0  # a previous token that triggers no grammar rule for 3 / 4
     col = (pos - plen).clamp(0, max_new - 1)
     ub = u[torch.arange(B), col]
-    want_tok, want_run, margin = _select_ref(logits, tok, run, bias, tail, homo, homo_stop, T, ub)
+    want_tok, want_run, margin = _select_ref(logits, tok, run, bias, tail, homo, homo_stop, T, ub, gumbel)
     out = torch.full((B, max_new), R.PAD, dtype=torch.long)
     d_tok, d_run, d_pos = to_dev(tok), to_dev(run), to_dev(pos)
     d_out = to_dev(out)
@@ -451,9 +459,10 @@ def test_select_update(V, T, fused_head):
     kw = dict(logits=to_dev(logits.float())) if not fused_head else dict(h=to_dev(h, BF), w_head=to_dev(w, BF),
                                                                           round_bf16=T > 0)
     ops.select_update(to_dev(bias), to_dev(tail), to_dev(homo), homo_stop, d_tok, d_run, d_pos, to_dev(plen),
-                      to_dev(rope_off), d_out, pos32, seql, rpos, R.EOS, R.PAD, temperature=T, uniforms=to_dev(u), **kw)
+                      to_dev(rope_off), d_out, pos32, seql, rpos, R.EOS, R.PAD, temperature=T, uniforms=to_dev(u),
+                      gumbel=gumbel, **kw)
     got = d_tok.cpu()
-    thr = 1e-2 if T == 0 else 5e-3
+    thr = 1e-2 if T == 0 else (3e-2 if gumbel else 5e-3)
     exempt = margin < thr if fused_head else torch.zeros(B, dtype=torch.bool)
     assert bool(((got == want_tok) | exempt).all()), (got != want_tok).nonzero()[:5]
     if not fused_head:

@@ -334,6 +334,29 @@ def test_inverse_cdf_boundaries():
     assert R.sample_inverse_cdf(z, 0.9999999)[0] == 6
 
 
+def test_gumbel_choice_closed_form_and_frequencies():
+    """sample_gumbel: the first argmax of z - log(-log(max(u, 1e-20))) (brute force in fp64 on random draws, and
+    u = 0 taking the clamp), banned entries never chosen; over 200k draws each token's frequency is softmax(z)
+    within 4 binomial standard deviations (Gumbel-max samples the softmax; a sign slip in either log would not)."""
+    z = torch.tensor([float("-inf"), float("-inf"), 0.3, -1.0, 2.0, 0.0, 0.5])
+    rng = np.random.default_rng(5)
+    for _ in range(200):
+        u = rng.random(7).astype(np.float32)
+        u[rng.integers(0, 7)] = 0.0 if rng.random() < 0.1 else u[0]
+        v, gap = R.sample_gumbel(z, u)
+        g = z.double().numpy() - np.log(-np.log(np.maximum(u.astype(np.float64), 1e-20)))
+        assert v == int(np.argmax(g)) and v >= 2 and gap >= 0
+    n = 200000
+    U = torch.from_numpy(rng.random((n, 7)).astype(np.float32)).clamp(min=1e-20)
+    G = z[None] - torch.log(-torch.log(U))
+    counts = torch.bincount(G.argmax(1), minlength=7).double()
+    picks = [R.sample_gumbel(z, U[i].numpy())[0] for i in range(2000)]
+    assert picks == G[:2000].argmax(1).tolist()
+    p = torch.softmax(z.double(), 0)
+    sd = torch.sqrt(n * p * (1 - p))
+    assert bool(((counts - n * p).abs() <= 4 * sd + 1e-9).all()), (counts / n, p)
+
+
 def test_inverse_cdf_frequencies():
     g = torch.Generator().manual_seed(3)
     z = torch.randn(7, generator=g) * 1.5

@@ -2,9 +2,10 @@
 //
 // Semantics (viktor/engine.py:79-116 and viktor/triton_ops.py:172-209):
 //   z = logits + bias (bias = -inf at PAD and BOS);
-//   greedy: first index of max(z); sampled: inverse CDF of softmax(z / T) at the supplied uniform
-//   (the reference draws Gumbel noise from the device RNG instead; the supplied uniform makes the
-//   stream reproducible);
+//   greedy: first index of max(z); sampled: inverse CDF of softmax(z / T) at the supplied uniform, or
+//   (gumbel) the reference's own formula, first index of max(z / T - log(-log(max(u_v, 1e-20)))) with one
+//   supplied uniform per vocabulary entry -- the reference draws those uniforms from the device RNG
+//   (viktor/engine.py:80-83), supplied ones make the stream reproducible;
 //   grammar, in the reference's order: EOS after a tail token; homopolymer run counter and EOS when the
 //   run reaches homo_stop tokens; PAD after EOS / PAD;
 //   out[b, pos - plen] = token; tok = token; pos += 1 and the int32 mirrors pos32 = pos,
@@ -42,7 +43,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
     const float *__restrict__ logits, const bf16_t *__restrict__ h, const bf16_t *__restrict__ norm_w, float eps,
     const bf16_t *__restrict__ w_head, int d, int round_bf16, const float *__restrict__ bias, const uint8_t *__restrict__ is_tail,
     const uint8_t *__restrict__ is_homo, int homo_stop, float temperature, const float *__restrict__ uniforms,
-    int64_t u_stride, int64_t u_cols, int64_t *__restrict__ tok, int64_t *__restrict__ run, int64_t *__restrict__ pos,
+    int64_t u_stride, int64_t u_cols, int gumbel, int64_t *__restrict__ tok, int64_t *__restrict__ run, int64_t *__restrict__ pos,
     const int64_t *__restrict__ plen, const int64_t *__restrict__ rope_off, const int64_t *__restrict__ cache_base,
     int64_t *__restrict__ out, int64_t out_stride, int64_t out_cols, int32_t *__restrict__ pos32,
     int32_t *__restrict__ seqlens, int32_t *__restrict__ rpos32, float *__restrict__ logp_out, int64_t logp_stride,
@@ -90,7 +91,16 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
   const int64_t pl = plen ? pl_raw : 0;
   const int64_t ocol = p - pl;
   const int64_t uc = ocol < 0 ? 0 : (ocol >= u_cols ? u_cols - 1 : ocol);
-  const float u_raw = uniforms ? uniforms[b * u_stride + uc] : 0.f;
+  const float u_raw = (uniforms && !gumbel) ? uniforms[b * u_stride + uc] : 0.f;
+  // gumbel: this thread's entries v = tid, tid + 256 of the column's V uniforms (past V: entry 0, unused)
+  float ug[SEL_MAXV / SEL_THREADS] = {};
+  if (gumbel && sample) {
+#pragma unroll
+    for (int i = 0; i < SEL_MAXV / SEL_THREADS; ++i) {
+      const int v = tid + SEL_THREADS * i;
+      ug[i] = uniforms[b * u_stride + uc * V + (v < V ? v : 0)];
+    }
+  }
   const int64_t pv = prev >= 0 && prev < V ? prev : 0;
   const uint8_t tail_raw = is_tail[pv];
 
@@ -194,6 +204,46 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
     }
   if (bi >= V) bi = 0;  // all -inf / NaN row: fall back to token 0 (PAD)
   const float zmax = best;
+  // gumbel: the first index of the maximum of z / T - log(-log(max(u, 1e-20))), merged like the max above
+  int gpick = bi;
+  if (gumbel && sample) {
+    float gb = -INFINITY;
+    int gi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < SEL_MAXV / SEL_THREADS; ++i) {
+      const int v = tid + SEL_THREADS * i;
+      if (v < V) {
+        const float zg = z[v] - logf(-logf(fmaxf(ug[i], 1e-20f)));
+        if (zg > gb || (zg == gb && v < gi)) {
+          gb = zg;
+          gi = v;
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(gb, o, 64);
+      const int oi = __shfl_xor(gi, o, 64);
+      if (ov > gb || (ov == gb && oi < gi)) {
+        gb = ov;
+        gi = oi;
+      }
+    }
+    __syncthreads();  // every thread has read the max's partials
+    if (lane == 0) {
+      red_v[wid] = gb;
+      red_i[wid] = gi;
+    }
+    __syncthreads();
+    gb = red_v[0];
+    gi = red_i[0];
+    for (int w = 1; w < SEL_THREADS / 64; ++w)
+      if (red_v[w] > gb || (red_v[w] == gb && red_i[w] < gi)) {
+        gb = red_v[w];
+        gi = red_i[w];
+      }
+    gpick = gi < V ? gi : bi;
+  }
   const bool need_e = sample || logp_out;
   if (need_e) {  // the exponentials, one token per thread (summed in token order below)
     for (int v = tid; v < V; v += SEL_THREADS) ez[v] = expf(z[v] - zmax);
@@ -209,7 +259,9 @@ __global__ __launch_bounds__(SEL_THREADS) void select_update_kernel(
   if (need_e) {
     for (int v = 0; v < V; ++v) sum += ez[v];
   }
-  if (sample) {
+  if (sample && gumbel) {
+    nxt = gpick;
+  } else if (sample) {
     const float inv = 1.0f / sum;
     float cdf = 0.f;
     int64_t pick = -1, last_pos = bi;
@@ -255,7 +307,7 @@ extern "C" int vk_select_update(const float *logits, const void *h, const void *
                                 int32_t d, int32_t round_bf16,
                                 const float *bias, const uint8_t *is_tail, const uint8_t *is_homo, int32_t homo_stop,
                                 float temperature, const float *uniforms, int64_t u_stride, int64_t u_cols,
-                                int64_t *tok, int64_t *run, int64_t *pos, const int64_t *plen, const int64_t *rope_off,
+                                int32_t gumbel, int64_t *tok, int64_t *run, int64_t *pos, const int64_t *plen, const int64_t *rope_off,
                                 const int64_t *cache_base, int64_t *out, int64_t out_stride, int64_t out_cols, int32_t *pos32, int32_t *seqlens,
                                 int32_t *rpos32, float *logp_out, int64_t logp_stride, int64_t B, int32_t V,
                                 int32_t eos, int32_t pad, void *stream) {
@@ -269,6 +321,8 @@ extern "C" int vk_select_update(const float *logits, const void *h, const void *
                "select_update: LM head needs d %% 8 == 0, d <= 2048 and 16-byte aligned h, w_head, norm_w");
   VK_CHECK_ARG(homo_stop <= 0 || run != nullptr, "select_update: homopolymer rule needs run");
   VK_CHECK_ARG(!(temperature > 0.f) || (uniforms != nullptr && u_cols > 0), "select_update: sampling needs uniforms");
+  VK_CHECK_ARG(!gumbel || u_stride >= u_cols * V, "select_update: Gumbel uniforms are [B, u_cols, V] (row stride %lld)",
+               static_cast<long long>(u_stride));
   VK_CHECK_ARG(out_cols > 0, "select_update: empty output buffer");
   VK_CHECK_ARG(logp_stride == 0 || logp_stride >= out_cols, "select_update: logp_stride must be 0 or >= out_cols");
   if (B == 0) return VK_OK;
@@ -276,7 +330,8 @@ extern "C" int vk_select_update(const float *logits, const void *h, const void *
   kern<<<static_cast<unsigned>(B), SEL_THREADS, 0, VK_STREAM(stream)>>>(
       logits, static_cast<const bf16_t *>(h), static_cast<const bf16_t *>(norm_w), eps,
       static_cast<const bf16_t *>(w_head), d, round_bf16, bias, is_tail,
-      is_homo, homo_stop, temperature, uniforms, u_stride, u_cols, tok, run, pos, plen, rope_off, cache_base, out,
+      is_homo, homo_stop, temperature, uniforms, u_stride, u_cols, gumbel != 0, tok, run, pos, plen, rope_off,
+      cache_base, out,
       out_stride,
       out_cols, pos32, seqlens, rpos32, logp_out, logp_stride, V, eos, pad);
   return launch_status("select_update");

@@ -8,9 +8,11 @@ running and emit PAD, which keeps every step shape-static and graph-capturable. 
 with all state in preallocated device tensors and no host synchronisation inside the step.
 
 Sampling (temperature > 0) draws each token from softmax(logits / T) by the inverse CDF at one uniform
-per (sequence, output column): `uniforms` [B, max_new_tokens]. The reference draws Gumbel noise from the
-device RNG inside its graph (viktor/engine.py:80-83); here the engine fills the uniforms from the torch
-RNG at prefill unless the caller supplied them (set_uniforms), which makes a rollout reproducible.
+per (sequence, output column): `uniforms` [B, max_new_tokens]; or, with sampling="gumbel", by the
+reference's own Gumbel-max formula at one uniform per (sequence, output column, vocabulary entry):
+`uniforms` [B, max_new_tokens, V]. The reference draws those uniforms from the device RNG inside its graph
+(viktor/engine.py:80-83); here the engine fills the uniforms from the torch RNG at prefill unless the caller
+supplied them (set_uniforms), which makes a rollout reproducible.
 
 group_size = G > 1 (GSPO rollouts: each window repeated G times, scripts/gspo.py:444): consecutive groups
 of G sequences must have identical prefixes (checked at prefill). The engine then prefills each window
@@ -33,13 +35,19 @@ class DecodeEngine:
     def __init__(self, model, batch_size: int, max_new_tokens: int, max_frames: int, backend: str = "auto",
                  cuda_graph: bool = True, prefill_batch: int = 128, check_every: int = 32,
                  attention_backend: str = "auto", temperature: float = 0.0, max_homopolymer=64, group_size: int = 1,
-                 logprobs: bool = False, force_eos_last: bool = False):
+                 logprobs: bool = False, force_eos_last: bool = False, sampling: str = "inverse_cdf"):
         self.model, self.dec = model, model.decoder
         self.temperature = float(temperature)
         # force_eos_last: the last output column (max_new_tokens - 1) is EOS for every sequence still running when
         # it is produced (a rollout capped at max_new_tokens ends with EOS); off by default, as the reference
         # scores a call that never ends as it stands (scripts/gspo.py:24-25)
         self.force_eos_last = bool(force_eos_last)
+        # sampling (temperature > 0): "inverse_cdf" -- one uniform per (sequence, output column) through the CDF of
+        # softmax(logits / T); "gumbel" -- the reference's formula, argmax(logits / T - log(-log(u))) with one uniform
+        # per (sequence, output column, vocabulary entry), viktor/engine.py:80-83
+        if sampling not in ("inverse_cdf", "gumbel"):
+            raise ValueError(f"unknown sampling {sampling!r}: 'inverse_cdf' or 'gumbel'")
+        self.gumbel = sampling == "gumbel"
         dev = self.dec.lm_head.weight.device
         self.dtype = self.dec.lm_head.weight.dtype
         self.pos_scale = getattr(model, "pos_scale", 1)
@@ -89,7 +97,8 @@ class DecodeEngine:
         self.homo_stop = max_homopolymer // tk.k if max_homopolymer else 0  # run length in tokens that ends it
         self.run = torch.zeros(batch_size, dtype=torch.long, device=dev)
         self.plen = torch.zeros(batch_size, dtype=torch.long, device=dev)  # output column = pos - plen
-        self.uniforms = torch.zeros(batch_size, max_new_tokens, dtype=torch.float32, device=dev)
+        u_shape = (batch_size, max_new_tokens) + ((tk.vocab_size,) if self.gumbel else ())
+        self.uniforms = torch.zeros(u_shape, dtype=torch.float32, device=dev)
         self._uniforms_set = False
         # logprobs=True: logp[b, j] = log-probability of output token j under the distribution it was chosen
         # from (log softmax of (logits + bias) / T, or of logits + bias when greedy), before the grammar rules
@@ -116,7 +125,7 @@ class DecodeEngine:
         ops.select_update(self.bias, self.is_tail, self.is_homo, self.homo_stop, self.tok, self.run, self.pos,
                           self.plen, self.rope_off, self.out, self.pos32, self.seqlens, self.rpos32, EOS, PAD,
                           h=x, norm_w=self.dec.norm.weight, eps=self.dec.cfg.norm_eps, w_head=self.dec.lm_head.weight,
-                          round_bf16=self.temperature > 0, temperature=self.temperature, uniforms=self.uniforms,
+                          round_bf16=self.temperature > 0, temperature=self.temperature, uniforms=self.uniforms, gumbel=self.gumbel,
                           cache_base=None if self.G == 1 else self.cache_base, logp_out=self.logp)
 
     def _reset_state(self):
@@ -194,7 +203,8 @@ class DecodeEngine:
         return self.fast.prefill(x, pos, seq, None, plan.max_len, cache, rope_pos=rpos, plan=plan)
 
     def set_uniforms(self, u):
-        """Uniforms [B, max_new_tokens] in [0, 1) driving the sampled tokens (column j -> output token j)."""
+        """Uniforms in [0, 1) driving the sampled tokens (column j -> output token j): [B, max_new_tokens], or
+        [B, max_new_tokens, vocab] with sampling="gumbel"."""
         assert u.shape == self.uniforms.shape
         self.uniforms.copy_(u)
         self._uniforms_set = True
@@ -254,7 +264,7 @@ class DecodeEngine:
         ops.select_update(self.bias, self.is_tail, self.is_homo, self.homo_stop, self.tok, self.run, self.pos,
                           self.plen, self.rope_off, self.out, self.pos32, self.seqlens, self.rpos32, EOS, PAD,
                           h=h.contiguous(), w_head=self.dec.lm_head.weight, round_bf16=True,
-                          temperature=self.temperature, uniforms=self.uniforms,
+                          temperature=self.temperature, uniforms=self.uniforms, gumbel=self.gumbel,
                           cache_base=None if G == 1 else self.cache_base, logp_out=self.logp)
         self.step_idx.fill_(1)
 

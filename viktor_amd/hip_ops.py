@@ -375,11 +375,13 @@ def varlen_attention(q, k, v, plan: AttentionPlan, stride_tok=None, out=None, ls
 
 def select_update(bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_off, out, pos32, seqlens, rpos32, eos,
                   pad, logits=None, h=None, w_head=None, round_bf16=False, temperature=0.0, uniforms=None,
-                  logp_out=None, norm_w=None, eps=1e-6, cache_base=None):
+                  logp_out=None, norm_w=None, eps=1e-6, cache_base=None, gumbel=False):
     """One step's token choice + state update for every sequence (fused LM head when h, w_head are given;
     with norm_w, h is the residual stream and the final RMSNorm runs first). See vk_select_update in
     include/viktor_hip.h for the exact rule order. logp_out: [B] fp32 (this step's chosen-token log-prob), or
-    [B, >= out columns] fp32, where the log-prob goes to the output column the token is written to."""
+    [B, >= out columns] fp32, where the log-prob goes to the output column the token is written to.
+    gumbel: sampled steps take the reference's Gumbel-max choice (viktor/engine.py:80-83) from uniforms
+    [B, T, V] (one per vocabulary entry) instead of the inverse CDF at uniforms [B, T]."""
     ref = logits if logits is not None else h
     require_device(ref, "select_update")
     B = tok.shape[0]
@@ -397,7 +399,11 @@ def select_update(bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_o
         _require(t is None or (t.dtype == dt and t.shape == (B,) and t.is_contiguous()), "select_update: state tensors")
     _require(out.dim() == 2 and out.shape[0] == B and out.dtype == torch.long and out.stride(1) == 1, "select_update: out")
     _require(is_tail.dtype in (torch.bool, torch.uint8) and is_homo.dtype in (torch.bool, torch.uint8), "select_update: masks")
-    if temperature > 0:
+    if temperature > 0 and gumbel:
+        _require(uniforms is not None and uniforms.dtype == torch.float32 and uniforms.dim() == 3
+                 and uniforms.shape[0] == B and uniforms.shape[2] == V and uniforms.stride(2) == 1
+                 and uniforms.stride(1) == V, "select_update: Gumbel uniforms [B, T, V] fp32")
+    elif temperature > 0:
         _require(uniforms is not None and uniforms.dtype == torch.float32 and uniforms.dim() == 2
                  and uniforms.shape[0] == B and uniforms.stride(1) == 1, "select_update: uniforms [B, T] fp32")
     us, uc = (uniforms.stride(0), uniforms.shape[1]) if uniforms is not None else (0, 0)
@@ -411,7 +417,7 @@ def select_update(bias, is_tail, is_homo, homo_stop, tok, run, pos, plen, rope_o
             lp_stride = logp_out.stride(0)
     call("vk_select_update", ptr(logits), ptr(h), ptr(norm_w), float(eps), ptr(w_head), d, int(bool(round_bf16)),
          ptr(bias), ptr(is_tail),
-         ptr(is_homo), int(homo_stop), float(temperature), ptr(uniforms), us, uc, ptr(tok), ptr(run), ptr(pos), ptr(plen),
+         ptr(is_homo), int(homo_stop), float(temperature), ptr(uniforms), us, uc, int(bool(gumbel)), ptr(tok), ptr(run), ptr(pos), ptr(plen),
          ptr(rope_off), ptr(cache_base), ptr(out), out.stride(0), out.shape[1], ptr(pos32), ptr(seqlens), ptr(rpos32), ptr(logp_out), lp_stride, B, V,
          int(eos), int(pad), stream_handle())
 
