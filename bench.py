@@ -51,6 +51,7 @@ Usage: python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--no-cpu] [--no-conf
        python bench.py --mode encoder|prefill [--steps N]   (that object alone, N timed repetitions)
        python bench.py --mode configs                       (the other configurations alone)
        python bench.py --mode kernels [--group-size G]      (the decode-attention traffic probe)
+       python bench.py --mode products [--steps N] [--phase-stamps]   (the decode step's layer loop, captured)
 """
 
 import argparse
@@ -646,6 +647,123 @@ def kernels_mode(group, reps=5):
     print(json.dumps({"group": group, "decode_attention_alg_bytes": alg, "copy_bytes_each_way": x.numel() * 2, "reps": reps}))
 
 
+# The decode step's small products at the rollout's 512 rows (d 512, ffn 1536, 8 + 2 x 2 heads of 64): their
+# operands (weights, activations, row sums, K/V rows written) per launch, the algorithmic bytes of each.
+PRODUCT_BYTES = {
+    "qkv": 512 * 512 * 2 + 512 * 16 * 4 + 768 * 512 * 2 + 512 * 512 * 2 + 512 * 512,
+    "o": 512 * 512 * 2 + 512 * 512 * 2 + 2 * 512 * 512 * 2 + 512 * 16 * 4,
+    "gate_up": 512 * 512 * 2 + 512 * 16 * 4 + 3072 * 512 * 2 + 512 * 1536 * 2,
+    "down": 512 * 1536 * 2 + 512 * 1536 * 2 + 2 * 512 * 512 * 2 + 512 * 16 * 4,
+}
+PRODUCT_FLOPS = {"qkv": 2 * 512 * 512 * 768, "o": 2 * 512 * 512 * 512, "gate_up": 2 * 512 * 512 * 3072,
+                 "down": 2 * 512 * 1536 * 512}
+PRODUCT_WGS = {"qkv": 192, "o": 256, "gate_up": 256, "down": 256}
+
+
+def products_mode(reps=50, stamps=False):
+    """The decode step's layer loop at the rollout's mean step (512 sequences in 64 groups of 8, 2049 shared
+    prefix positions + 512 own positions each) through FastDecoder.decode_residual: per layer norm + qkv + QK-norm
+    + RoPE + cache write, grouped attention, o + residual, norm + gate_up + SwiGLU, down + residual (layer 0 from a
+    handed-in residual stream instead of the embedding gather; no LM head). It is captured once in a HIP graph and
+    replayed `reps` times, so the four products run between attention launches that stream the caches, as in the
+    rollout; then a plain 256 MiB device copy (the counter scale of rocprofv3 FETCH_SIZE / WRITE_SIZE runs).
+    stamps: the profiling build (libviktor_hip_stamps.so) is loaded instead of the product library and the
+    per-workgroup phase timestamps of the last replay are summarised per product (layers 1-7: their qkv takes the
+    handed-over row sums, as in the rollout)."""
+    import ctypes
+    from viktor_amd import _lib as L
+    if stamps:
+        from viktor_amd.build import STAMPS_LIB
+        L.load(STAMPS_LIB)  # before anything else loads the product library
+    from viktor_amd import hip_ops as ops
+    from viktor_amd.decoder import KVCache
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    _, gm = build_model(dev)
+    fast, cfg = gm.decoder.fast(), gm.decoder.cfg
+    B, G = PREFIXES * GROUP, GROUP
+    own = (NEW - 2) // 2 + 1  # own rows attended at the rollout's mean step, the new one included
+    gen = torch.Generator(device=dev).manual_seed(0)
+    cache = KVCache(cfg, B, NEW, torch.bfloat16, dev)
+    pc = KVCache(cfg, B // G, P + 1, torch.bfloat16, dev)
+    for t in (cache.k, cache.v, pc.k, pc.v):
+        t.normal_(generator=gen)
+    plen32 = torch.full((B // G,), P + 1, dtype=torch.int32, device=dev)
+    seqlens = torch.full((B,), own, dtype=torch.int32, device=dev)
+    pos32 = torch.full((B,), own - 1, dtype=torch.int32, device=dev)
+    rpos32 = pos32 + (P + 1)
+    rows = torch.arange(B, dtype=torch.int32, device=dev)
+    gws = ops.decode_attention_grouped_workspace(B, G, P + 1, NEW, dev)
+    x0 = torch.randn(B, cfg.d_model, device=dev, generator=gen).to(torch.bfloat16)
+    x = x0.clone()
+
+    def step():
+        x.copy_(x0)
+        fast.decode_residual(pos32, rows, seqlens, cache, rope_pos=rpos32, x=x, prefix=(pc, plen32, G, gws))
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    layers = cfg.n_layers
+    order = ["qkv", "o", "gate_up", "down"]  # the stamped launches of a layer, in launch order
+    slots = 8 * sum(PRODUCT_WGS.values()) * layers
+    buf = torch.zeros(slots, dtype=torch.int64, device=dev)
+    if stamps:
+        L.call("vk_phase_stamps_set", ctypes.c_void_p(buf.data_ptr()), ctypes.c_int64(slots))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    if stamps:
+        used = ctypes.c_int64(0)
+        L.call("vk_phase_stamps_used", ctypes.byref(used))
+        assert used.value == slots, f"stamped launches took {used.value} slots, expected {slots}"
+        L.call("vk_phase_stamps_set", ctypes.c_void_p(0), ctypes.c_int64(0))
+    graph.replay()
+    ms = _timed(graph.replay, reps)
+    out = {"workload": "decode step layer loop, 512 sequences (64 groups x 8), 2049 prefix + 512 own positions, "
+                       "8 layers, captured", "reps": reps, "ms_per_step": round(ms, 4),
+           "product_alg_bytes": PRODUCT_BYTES, "product_flops": PRODUCT_FLOPS}
+    if stamps:
+        khz = ctypes.c_int64(0)
+        L.call("vk_timestamp_rate_khz", ctypes.byref(khz))
+        us = 1e3 / khz.value  # microseconds per tick
+        t = buf.cpu().view(-1, 8)
+        names = ["first_data", "normalise", "k_loop", "tile_sum", "epilogue"]
+        summary, off = {}, 0
+        spans = {k: [] for k in order}
+        phases = {k: [] for k in order}
+        starts = {k: [] for k in order}
+        for layer in range(layers):
+            for k in order:
+                n = PRODUCT_WGS[k]
+                w = t[off:off + n, :6].double()
+                off += n
+                if layer == 0:
+                    continue
+                spans[k].append(float(w[:, 5].max() - w[:, 0].min()) * us)
+                phases[k].append(((w[:, 1:6] - w[:, 0:5]) * us).mean(0))
+                starts[k].append(float((w[:, 0] - w[:, 0].min()).mean()) * us)
+        for k in order:
+            ph = torch.stack(phases[k]).mean(0)
+            summary[k] = {"workgroups": PRODUCT_WGS[k], "span_us": round(sum(spans[k]) / len(spans[k]), 3),
+                          "mean_start_offset_us": round(sum(starts[k]) / len(starts[k]), 3),
+                          **{f"{nm}_us": round(float(v), 3) for nm, v in zip(names, ph)},
+                          "workgroup_us": round(float(ph.sum()), 3)}
+        out["phases"] = summary
+        out["phase_slots"] = "0 entry, 1 first operands landed, 2 K loop start, 3 K loop end, 4 tile summed, 5 end"
+    print(json.dumps(out), flush=True)
+    del graph
+    cp = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)  # 256 MiB
+    cp2 = torch.empty_like(cp)
+    for _ in range(5):
+        cp2.copy_(cp)
+    torch.cuda.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -654,9 +772,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the other configurations' measurements")
     ap.add_argument("--prefill-batch", type=int, default=128)
-    ap.add_argument("--mode", choices=["rollout", "kernels", "encoder", "prefill", "configs", "update"],
+    ap.add_argument("--mode", choices=["rollout", "kernels", "products", "encoder", "prefill", "configs", "update"],
                     default="rollout",
-                    help="kernels: decode-attention traffic probe; encoder / prefill / configs / update: that object alone")
+                    help="kernels: decode-attention traffic probe; products: the decode step's layer loop captured "
+                         "(kernel traces, counters, --phase-stamps); encoder / prefill / configs / update: that object alone")
+    ap.add_argument("--phase-stamps", action="store_true",
+                    help="products mode: load the phase-timestamp profiling build and summarise its stamps")
     ap.add_argument("--group-size", type=int, default=GROUP, help="sequences sharing one prefix KV copy (1: none)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -665,6 +786,9 @@ def main():
         sys.exit(2)
     if args.mode == "kernels":
         kernels_mode(args.group_size)
+        return
+    if args.mode == "products":
+        products_mode(reps=max(args.steps, 1), stamps=args.phase_stamps)
         return
     if args.mode == "encoder":
         print(json.dumps({"encoder": encoder_timing(reps=max(args.steps, 1))}), flush=True)

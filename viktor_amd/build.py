@@ -1,8 +1,11 @@
 """Build libviktor_hip.so (all kernels of viktor_amd/csrc) for gfx950 with hipcc.
 
-Usage: python -m viktor_amd.build [--jobs N]
+Usage: python -m viktor_amd.build [--jobs N] [--phase-stamps]
 
 The library is written next to this file, in-tree, so it travels with the repository snapshot.
+--phase-stamps also links libviktor_hip_stamps.so, a profiling build whose decode-step product kernels
+(csrc/skinny_gemm.hip, compiled with -DVK_PHASE_STAMPS) write per-workgroup phase timestamps; everything else
+in it is the product build's objects.
 Every source is compiled to an object in parallel, then linked once. The HIP runtime is resolved by
 soname (libamdhip64.so.7) at load time, so after `import torch` the library binds to the runtime
 torch already loaded and shares its streams and graphs.
@@ -19,6 +22,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 LIB = os.path.join(HERE, "libviktor_hip.so")
+STAMPS_LIB = os.path.join(HERE, "libviktor_hip_stamps.so")
+STAMPED_SOURCE = "skinny_gemm.hip"
 OBJ_DIR = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 
@@ -41,9 +46,10 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def _compile(src):
-    obj = os.path.join(OBJ_DIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", "-c", src, "-o", obj]
+def _compile(src, defines=()):
+    tag = "_stamps" if defines else ""
+    obj = os.path.join(OBJ_DIR, os.path.basename(src)[:-4] + tag + ".o")
+    cmd = [hipcc(), *HIP_FLAGS, *[f"-D{d}" for d in defines], f"-I{INCLUDE}", "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the gfx feature flag above; that warning is expected
     noise = "is not a recognized feature for this target"
@@ -53,22 +59,34 @@ def _compile(src):
     return obj, err
 
 
-def build(jobs=None, verbose=False):
-    """Compile every kernel source and link libviktor_hip.so; returns the library path."""
+def _link(objs, out):
+    tmp = out + ".tmp"
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr}")
+    os.replace(tmp, out)
+
+
+def build(jobs=None, verbose=False, phase_stamps=False):
+    """Compile every kernel source and link libviktor_hip.so (and, with phase_stamps, the profiling build
+    libviktor_hip_stamps.so); returns the product library's path."""
     os.makedirs(OBJ_DIR, exist_ok=True)
     srcs = sources()
-    with ThreadPoolExecutor(max_workers=jobs or min(8, len(srcs))) as ex:
-        results = list(ex.map(_compile, srcs))
+    tasks = [(s, ()) for s in srcs]
+    if phase_stamps:
+        tasks.append((os.path.join(CSRC, STAMPED_SOURCE), ("VK_PHASE_STAMPS",)))
+    with ThreadPoolExecutor(max_workers=jobs or min(8, len(tasks))) as ex:
+        results = list(ex.map(lambda t: _compile(*t), tasks))
     if verbose:
         for obj, err in results:
             if err.strip():
                 print(err, file=sys.stderr)
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *[o for o, _ in results], "-o", tmp]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+    objs = [o for o, _ in results[:len(srcs)]]
+    _link(objs, LIB)
+    if phase_stamps:
+        stamped = results[-1][0]
+        _link([stamped if os.path.basename(s) == STAMPED_SOURCE else o for s, o in zip(srcs, objs)], STAMPS_LIB)
     return LIB
 
 
@@ -76,8 +94,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("--phase-stamps", action="store_true", help="also link the phase-timestamp profiling build")
     args = ap.parse_args()
-    print(build(args.jobs, args.verbose))
+    print(build(args.jobs, args.verbose, args.phase_stamps))
 
 
 if __name__ == "__main__":

@@ -49,9 +49,34 @@ struct SkinnyArgs {
   // ([M, N / 32] fp32, N = 512; NULL: none). PRO_NORM_SS: those sums for the A rows ([M, K / 32], K = 512).
   float *ss_out;
   const float *ss_in;
+#ifdef VK_PHASE_STAMPS
+  uint64_t *stamps;  // the profiling build's per-workgroup phase timestamps (8 slots each; null: none)
+#endif
 };
 
 constexpr int SK_BM = 32;
+
+// Phase timestamps of the profiling build (compiled with VK_PHASE_STAMPS; the product library has none): lane 0
+// of wave 0 of every workgroup writes the 100 MHz real-time counter to slot k of its 8: 0 entry, 1 first operands
+// landed, 2 K loop start, 3 K loop end, 4 epilogue start (the tile summed in LDS), 5 end (its own stores done).
+#ifdef VK_PHASE_STAMPS
+#define VK_PHASE(p, k)                                                                      \
+  do {                                                                                      \
+    if ((p).stamps && threadIdx.x == 0) (p).stamps[8 * blockIdx.x + (k)] = wall_clock64(); \
+  } while (0)
+#define VK_PHASE_END(p)            \
+  do {                             \
+    __builtin_amdgcn_s_waitcnt(0); \
+    VK_PHASE(p, 5);                \
+  } while (0)
+#else
+#define VK_PHASE(p, k) \
+  do {                 \
+  } while (0)
+#define VK_PHASE_END(p) \
+  do {                  \
+  } while (0)
+#endif
 
 // LDS writes of this wave done, then a plain s_barrier: __syncthreads() would also drain every
 // outstanding global load (its release fence), the prefetched operands and epilogue data included.
@@ -519,6 +544,7 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
   static_assert(S::ROWS % 32 == 0, "a stage is whole 8-row instructions for 4 waves");
   __shared__ __attribute__((aligned(16))) char smem[S::SMEM];
 
+  VK_PHASE(p, 0);
   const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wq = wid & 3, kh = wid >> 2;  // wave within its K slice, K slice
   // XCD-aware tile order: workgroup p runs on XCD p % 8, which owns a contiguous range of tiles; tiles are
@@ -673,6 +699,7 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    VK_PHASE(p, 1);
     if constexpr (PRO == PRO_EMBED_RES)  // the gathered rows' own sums; the nb == 0 tiles keep the raw rows
       pg_normalise_rows_own<PG_BM / (4 * KS), 4 * KS>(smem, nwx, wid, lane, p.eps, p.x_store, m0, p.M, nb == 0);
     else
@@ -737,12 +764,17 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
 #pragma unroll
     for (int t = 0; t < 2; ++t) acc[wt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  if (XRES) VK_PHASE(p, 2);
   for (int kt = 0; kt < nk; ++kt) {
     // this wave's loads of stage kt are done once at most (stages issued after it) x LOADS remain
     pg_wait_ahead<S::LOADS, S::STAGES - 2>(min(nk - 1 - kt, S::STAGES - 2));
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    if (!XRES && kt == 0) {
+      VK_PHASE(p, 1);
+      VK_PHASE(p, 2);
+    }
     if (kt + S::STAGES - 1 < nk) PG_ISSUE(kt + S::STAGES - 1);
     char *base = smem + S::XB + kh * S::RING + (kt % S::STAGES) * S::STAGEB;
     if constexpr (PRO == PRO_NORM || PRO == PRO_EMBED_NORM) {
@@ -783,6 +815,7 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
   }
 
 #undef PG_ISSUE
+  VK_PHASE(p, 3);
   // tile -> LDS: acc[wt][t] lane holds C^T[weight row 16 wq + 4 g + e (+ 64 for up)][A row 16 t + lane % 16];
   // with two K slices the second adds its partial tile to the first
   lds_barrier();
@@ -803,6 +836,7 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
     lds_barrier();
   }
   if (tid >= 256) return;
+  VK_PHASE(p, 4);
 
   // ---- epilogue: thread -> (row rr, 4-column group sub) of each 32-column half ----
   float v[HALVES][4], vu[HALVES][4];
@@ -868,6 +902,7 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
       *reinterpret_cast<u32x2 *>(dst) = u32x2{pack_bf(x1[0], x1[1]), pack_bf(x1[2], x1[3])};
       *reinterpret_cast<u32x2 *>(dst + 32) = u32x2{pack_bf(x2[0], x2[1]), pack_bf(x2[2], x2[3])};
     }
+    VK_PHASE_END(p);
     return;
   }
   float ssq[HALVES] = {};  // EPI_RESID: this thread's share of the row's sum of squares over each 32-column half
@@ -919,6 +954,7 @@ __global__ __launch_bounds__(256 * KS) void panel_gemm_kernel(const SkinnyArgs p
       }
     }
   }
+  VK_PHASE_END(p);
 }
 
 // ---- norm + gate_up + SwiGLU on 32 rows x 96 output columns (the decode step's MLP input product) ---------
@@ -949,6 +985,7 @@ __global__ __launch_bounds__(64 * NWV) void gate_up_wide_kernel(const SkinnyArgs
   constexpr int TA = 8 / NWV;                // A blocks per wave
   static_assert(GW_LOADS * (GW_STAGES - 1) + GW_BM / NWV + 3 <= 63, "a wave's loads in flight fit the vmcnt counter");
   __shared__ __attribute__((aligned(16))) char smem[GW_SMEM];
+  VK_PHASE(p, 0);
   const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   // XCD-aware order (as the panel kernel): workgroup p runs on XCD p % 8, which owns a contiguous range of the
   // n-block-major tiles, so the workgroups of one XCD share weight tiles
@@ -1002,8 +1039,10 @@ __global__ __launch_bounds__(64 * NWV) void gate_up_wide_kernel(const SkinnyArgs
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+  VK_PHASE(p, 1);
   pg_normalise_rows<GW_BM / NWV, NWV>(smem, nwx, ssx, GW_BM, wid, lane, p.eps);
   lds_barrier();
+  VK_PHASE(p, 2);
 
   // wave w: A blocks t0 .. t0 + TA - 1, weight blocks 3 wg .. 3 wg + 2
   const int t0 = NWV == 8 ? (wid & 1) : 0, wg = NWV == 8 ? (wid >> 1) : wid;
@@ -1050,6 +1089,7 @@ __global__ __launch_bounds__(64 * NWV) void gate_up_wide_kernel(const SkinnyArgs
     }
   }
 
+  VK_PHASE(p, 3);
   // tile -> LDS: acc[t][j] lane holds C^T[weight row 16 (3 wg + j) + 4 fg + e][A row 16 (t0 + t) + fr]
   lds_barrier();
   float *part = reinterpret_cast<float *>(smem + GW_XB);  // [GW_BM][GW_PITCH]
@@ -1061,6 +1101,7 @@ __global__ __launch_bounds__(64 * NWV) void gate_up_wide_kernel(const SkinnyArgs
       for (int e = 0; e < 4; ++e)
         part[(16 * (t0 + t) + fr) * GW_PITCH + 16 * (3 * wg + j) + 4 * fg + e] = acc[t][j][e];
   lds_barrier();
+  VK_PHASE(p, 4);
 
   // SwiGLU epilogue: 32 rows x 24 groups of 4 columns; out = bf16(bf16(silu(bf16(g))) bf16(u))
   constexpr int ITEMS = GW_BM * GW_BN / 4;
@@ -1079,13 +1120,31 @@ __global__ __launch_bounds__(64 * NWV) void gate_up_wide_kernel(const SkinnyArgs
     *reinterpret_cast<u32x2 *>(static_cast<bf16_t *>(p.y) + erow * p.N + n0 + 4 * grp) =
         u32x2{pack_bf(o[0], o[1]), pack_bf(o[2], o[3])};
   }
+  VK_PHASE_END(p);
 }
+
+#ifdef VK_PHASE_STAMPS
+// The profiling build's stamp buffer: each launch takes the next 8 x workgroups slots while they last.
+static uint64_t *g_stamps = nullptr;
+static int64_t g_stamp_cap = 0, g_stamp_used = 0;
+static SkinnyArgs with_stamps(const SkinnyArgs &a, int64_t wgs) {
+  SkinnyArgs p = a;
+  p.stamps = nullptr;
+  if (g_stamps && g_stamp_used + 8 * wgs <= g_stamp_cap) {
+    p.stamps = g_stamps + g_stamp_used;
+    g_stamp_used += 8 * wgs;
+  }
+  return p;
+}
+#else
+static const SkinnyArgs &with_stamps(const SkinnyArgs &a, int64_t) { return a; }
+#endif
 
 static int launch_gate_up_wide(const SkinnyArgs &a, hipStream_t s) {
   const int64_t m_blocks = (a.M + GW_BM - 1) / GW_BM;
   const int64_t tiles = m_blocks * (a.N / GW_BN);
   // 8 wavefronts: more of them issuing the direct loads (4 measured 7% slower)
-  gate_up_wide_kernel<8><<<static_cast<unsigned>(tiles), 512, 0, s>>>(a, static_cast<int>(m_blocks),
+  gate_up_wide_kernel<8><<<static_cast<unsigned>(tiles), 512, 0, s>>>(with_stamps(a, tiles), static_cast<int>(m_blocks),
                                                                       static_cast<int>(tiles));
   return VK_OK;
 }
@@ -1118,6 +1177,7 @@ __global__ __launch_bounds__(256 * KSP) void resid_gemm_kernel(const SkinnyArgs 
   constexpr int RS_STAGES = 12 / KSP;               // slots per ring (one ring per K slice)
   constexpr int RS_RING = RS_STAGES * RS_STAGEB;
   __shared__ __attribute__((aligned(16))) char smem[RS_SMEM];
+  VK_PHASE(p, 0);
   const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wq = wid & 3, kh = wid >> 2;  // wave within its K slice, K slice
   // XCD-aware order (as the panel kernel): workgroup p runs on XCD p % 8, which owns a contiguous range of the
@@ -1183,6 +1243,10 @@ __global__ __launch_bounds__(256 * KSP) void resid_gemm_kernel(const SkinnyArgs 
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();  // every wave's stage kt has landed; every wave is done with stage kt - 1
     asm volatile("" ::: "memory");
+    if (kt == 0) {
+      VK_PHASE(p, 1);
+      VK_PHASE(p, 2);
+    }
     if (kt + RS_STAGES - 1 < nk)
       pg_issue<RS_LOADS>(ring + ((kt + RS_STAGES - 1) % RS_STAGES) * RS_STAGEB, src, (kt + RS_STAGES - 1) * PG_BK, wq);
     const char *base = ring + (kt % RS_STAGES) * RS_STAGEB;
@@ -1195,6 +1259,7 @@ __global__ __launch_bounds__(256 * KSP) void resid_gemm_kernel(const SkinnyArgs 
     }
   }
 
+  VK_PHASE(p, 3);
   // tiles -> LDS: acc lane holds C^T[weight row 16 wb + 4 fg + e][A row 16 ta + fr] of its K half
   lds_barrier();
   float *part = reinterpret_cast<float *>(smem);  // [2][RS_BM][RS_PITCH]
@@ -1202,6 +1267,7 @@ __global__ __launch_bounds__(256 * KSP) void resid_gemm_kernel(const SkinnyArgs 
   for (int e = 0; e < 4; ++e) part[(kh * RS_BM + 16 * ta + fr) * RS_PITCH + 16 * wb + 4 * fg + e] = acc[e];
   lds_barrier();
   if (tid >= 256) return;
+  VK_PHASE(p, 4);
 
   // x = bf16(x + bf16(sum of the slices' tiles in slice order)); the row's sum of squares over the 32 columns from the 8 lanes
   // of the row (consecutive) in a fixed order
@@ -1232,6 +1298,7 @@ __global__ __launch_bounds__(256 * KSP) void resid_gemm_kernel(const SkinnyArgs 
     ssq += __shfl_xor(ssq, 4, 64);
     if (erow < p.M && sub == 0) p.ss_out[erow * (p.N / PG_SS_COLS) + nb] = ssq;
   }
+  VK_PHASE_END(p);
 }
 
 static int launch_resid(const SkinnyArgs &a, hipStream_t s) {
@@ -1239,7 +1306,7 @@ static int launch_resid(const SkinnyArgs &a, hipStream_t s) {
   const int64_t tiles = m_blocks * ((a.N + RS_BN - 1) / RS_BN);
   // two K slices: one slice of 4 wavefronts measured 18% slower at K = 1536 (fewer loads in flight per CU),
   // four slices no faster in the decode step
-  resid_gemm_kernel<2><<<static_cast<unsigned>(tiles), 512, 0, s>>>(a, static_cast<int>(m_blocks),
+  resid_gemm_kernel<2><<<static_cast<unsigned>(tiles), 512, 0, s>>>(with_stamps(a, tiles), static_cast<int>(m_blocks),
                                                                     static_cast<int>(tiles));
   return VK_OK;
 }
@@ -1254,9 +1321,10 @@ static int launch_panel(const SkinnyArgs &a, hipStream_t s) {
   constexpr bool can_split = (PRO == PRO_NONE || PRO == PRO_NORM_SS || PRO == PRO_EMBED_RES) && EPI != EPI_SWIGLU;
   if (can_split && a.K % (2 * PG_BK) == 0 && tiles <= device_cus_cached()) {
     panel_gemm_kernel<PRO, EPI, can_split ? 2 : 1><<<static_cast<unsigned>(tiles), 512, 0, s>>>(
-        a, static_cast<int>(m_blocks), static_cast<int>(tiles));
+        with_stamps(a, tiles), static_cast<int>(m_blocks), static_cast<int>(tiles));
   } else {
-    panel_gemm_kernel<PRO, EPI, 1><<<static_cast<unsigned>(tiles), 256, 0, s>>>(a, static_cast<int>(m_blocks),
+    panel_gemm_kernel<PRO, EPI, 1><<<static_cast<unsigned>(tiles), 256, 0, s>>>(with_stamps(a, tiles),
+                                                                             static_cast<int>(m_blocks),
                                                                              static_cast<int>(tiles));
   }
   return VK_OK;
@@ -1437,3 +1505,21 @@ extern "C" int vk_norm_qkv_rope_cache(const void *x, const int64_t *tok, int64_t
   if (rc != VK_OK) return rc;
   return launch_status("norm_qkv_rope_cache");
 }
+
+#ifdef VK_PHASE_STAMPS
+// Profiling build only (not part of the product library or its header): the stamp buffer ([cap] uint64 device
+// memory, 8 slots per workgroup of each later launch of the panel, gate_up and residual kernels; null: off), and
+// the slots taken so far.
+extern "C" int vk_phase_stamps_set(uint64_t *buf, int64_t cap) {
+  VK_CHECK_ARG(cap >= 0 && (buf || cap == 0), "phase_stamps_set: bad buffer");
+  g_stamps = buf;
+  g_stamp_cap = cap;
+  g_stamp_used = 0;
+  return VK_OK;
+}
+extern "C" int vk_phase_stamps_used(int64_t *used) {
+  VK_CHECK_ARG(used, "phase_stamps_used: null pointer");
+  *used = g_stamp_used;
+  return VK_OK;
+}
+#endif
