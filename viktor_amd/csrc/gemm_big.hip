@@ -173,36 +173,108 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
     woff[i] = GB_XTILEB + R * GB_ROWB + 16 * (fg ^ ((R >> 1) & 3));
   }
 
+  // The plain, fp32 and SwiGLU epilogues (whose values live across the loop leave room for a second set of
+  // fragment registers) run a software-pipelined K loop: a wavefront reads its 12 fragments of slice kt + 1
+  // while its 32 MFMAs of slice kt run, from two register sets (the loop unrolled by two). Slice kt + 1 must
+  // then be whole in LDS one slice earlier, and slice kt + 3 goes into slice kt's slot once every wavefront has
+  // its fragments of slice kt in registers, so two slices stay in flight during the MFMAs, as with reads right
+  // before them. The other epilogues would spill with the second set; they read a slice's fragments right
+  // before its MFMAs.
+  constexpr bool PIPE = EPI == GB_BF16 || EPI == GB_F32 || EPI == GB_SWIGLU;
   const int nk = K / GB_BK;
 #pragma unroll
   for (int s = 0; s < GB_STAGES - 1; ++s)
     if (s < nk) issue(s, s * GB_BK);
-  for (int kt = 0; kt < nk; ++kt) {
-    // this thread's loads of stage kt are done once at most (stages issued after it) x GB_LOADS remain
-    if (kt + 1 < nk)
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(GB_LOADS));
-    else
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    // Every thread's slice of stage kt has landed (the wait above), so after the barrier the whole stage is
-    // in LDS and stage kt - 1's slot is free. A bare s_barrier: __syncthreads() would add a release fence
-    // that drains every outstanding load, the prefetched stage included.
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    if (kt + GB_STAGES - 1 < nk) issue(kt + GB_STAGES - 1, (kt + GB_STAGES - 1) * GB_BK);
+  auto read_frags = [&](int kt, bf16x8(&xf)[8], bf16x8(&wf)[4]) {
     const char *base = smem + (kt % GB_STAGES) * GB_STAGEB;
-    bf16x8 xf[8], wf[4];
 #pragma unroll
     for (int j = 0; j < 8; ++j) xf[j] = *reinterpret_cast<const bf16x8 *>(base + xoff[j]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) wf[i] = *reinterpret_cast<const bf16x8 *>(base + woff[i]);
+  };
+  auto mfmas = [&](const bf16x8(&xf)[8], const bf16x8(&wf)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[i], xf[j], acc[i][j], 0, 0, 0);
-    // keep that order: the scheduler would otherwise sink each W read next to its 8 MFMAs
-    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // 12 LDS reads
-    __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);  // then the 32 MFMAs
+  };
+  if constexpr (PIPE) {
+    // this thread's loads of slice kt + 1 are done once at most slice kt + 2's remain, and its fragment reads
+    // of slice kt are done; after the barrier slice kt + 1 is whole in LDS and slice kt's slot is free for
+    // kt + 3. A bare s_barrier: __syncthreads() would add a release fence that drains every outstanding load,
+    // the prefetched slices included.
+    auto next_slice = [&](int kt) {
+      if (kt + 2 < nk)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(GB_LOADS));
+      else
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (kt + GB_STAGES < nk) issue(kt + GB_STAGES, (kt + GB_STAGES) * GB_BK);
+    };
+    // one LDS read of the next slice between every two MFMAs of this one, then the last 8 MFMAs
+#define GB_INTERLEAVE()                                  \
+  do {                                                   \
+    _Pragma("unroll") for (int r_ = 0; r_ < 12; ++r_) {  \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); \
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0); \
+    }                                                    \
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);   \
+  } while (0)
+    bf16x8 xa[8], wa[4], xb[8], wb[4];
+    // slice 0 whole in LDS (slice 2 then goes into the ring's third slot), its fragments read
+    if (nk > 1)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(GB_LOADS));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (GB_STAGES - 1 < nk) issue(GB_STAGES - 1, (GB_STAGES - 1) * GB_BK);
+    read_frags(0, xa, wa);
+    // Pairs of slices; the second step of the last pair may have no next slice: it then re-reads slice nk - 1
+    // (its LDS slot is no longer written), so no branch separates a step's reads from its MFMAs and the
+    // scheduler can interleave them. An odd count leaves slice nk - 1 in xa for the step after the loop.
+    // next_slice(j) with j + 1 == nk waits for every load and passes a barrier; it issues nothing.
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+      next_slice(kt);
+      read_frags(kt + 1, xb, wb);
+      mfmas(xa, wa);
+      GB_INTERLEAVE();
+      next_slice(kt + 1);  // (past the last slice: only the waits and the barrier)
+      read_frags(min(kt + 2, nk - 1), xa, wa);
+      mfmas(xb, wb);
+      GB_INTERLEAVE();
+    }
+    if (kt < nk) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      mfmas(xa, wa);
+    }
+#undef GB_INTERLEAVE
+  } else {
+    for (int kt = 0; kt < nk; ++kt) {
+      // this thread's loads of stage kt are done once at most (stages issued after it) x GB_LOADS remain
+      if (kt + 1 < nk)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(GB_LOADS));
+      else
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      // Every thread's slice of stage kt has landed (the wait above), so after the barrier the whole stage is
+      // in LDS and stage kt - 1's slot is free. A bare s_barrier: __syncthreads() would add a release fence
+      // that drains every outstanding load, the prefetched stage included.
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (kt + GB_STAGES - 1 < nk) issue(kt + GB_STAGES - 1, (kt + GB_STAGES - 1) * GB_BK);
+      bf16x8 xf[8], wf[4];
+      read_frags(kt, xf, wf);
+      mfmas(xf, wf);
+      // keep that order: the scheduler would otherwise sink each W read next to its 8 MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // 12 LDS reads
+      __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);  // then the 32 MFMAs
+    }
   }
 
   // Epilogue through LDS: a lane holds 4 consecutive columns of one row per (i, j), so direct stores would
