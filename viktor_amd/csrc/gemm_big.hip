@@ -546,8 +546,10 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
         if (odst != nullptr) *reinterpret_cast<u32x4 *>(odst + row * qa.kv_ld + hk * 64 + 8 * c) = v;
         continue;
       }
+      // non-temporal: the product's rows are read back by a later kernel, not by this one, and stores that
+      // allocate in L2 would push out the A blocks the XCD's next column tiles read
       if (row < M && col < N)
-        *reinterpret_cast<u32x4 *>(static_cast<char *>(y) + (row * N + col) * ESZ) = v;
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(static_cast<char *>(y) + (row * N + col) * ESZ));
     }
   }
 }
