@@ -4,7 +4,8 @@
 //   * 256 x 128 output tile per workgroup of 4 wavefronts, each wavefront 128 x 64 (32 fp32 MFMA tiles, 128
 //     accumulator registers), so a wavefront fits in 256 registers and two workgroups share a CU: one
 //     workgroup's barriers, LDS phases and epilogue overlap the other's MFMAs (with 256 x 256 tiles of
-//     128 x 128 per wavefront, one wavefront per SIMD left all of those exposed).
+//     128 x 128 per wavefront, one wavefront per SIMD left all of those exposed). Plain products use 256 x 256
+//     tiles of 8 such wavefronts instead (one workgroup per CU, a third fewer global->LDS bytes per flop).
 //   * Operands reach LDS with gfx950's direct global->LDS loads (global_load_lds_dwordx4: lane l of an
 //     instruction lands at LDS base + 16 l), so the prefetch costs no registers; a 3-stage ring of 32-wide K
 //     slices (72 KB) keeps two slices in flight while one feeds the MFMAs. LDS rows are 64 B without padding;
@@ -27,18 +28,35 @@
 namespace vk {
 
 constexpr int GB_BM = 256;   // rows of x per workgroup
-constexpr int GB_BW = 128;   // rows of w per workgroup
 constexpr int GB_BK = 32;    // K per stage
 constexpr int GB_GM = 8;     // row blocks per group of the tile order
 constexpr int GB_STAGES = 3;
 constexpr int GB_ROWB = GB_BK * 2;                   // bytes per LDS row
 constexpr int GB_XTILEB = GB_BM * GB_ROWB;           // 16 KB
-constexpr int GB_WTILEB = GB_BW * GB_ROWB;           // 8 KB
-constexpr int GB_STAGEB = GB_XTILEB + GB_WTILEB;     // 24 KB
-constexpr size_t GB_SMEM = static_cast<size_t>(GB_STAGES) * GB_STAGEB;  // 72 KB: two workgroups per CU
-constexpr int GB_LOADS = 6;                          // direct loads per thread per stage (4 x + 2 w)
+
+// GW wavefronts along the weight rows, each 64 of them; 2 GW wavefronts per workgroup, every one a 128 x 64 block.
+// GW = 2: 256 x 128 tiles, 4 wavefronts, 72 KB of ring (two workgroups per CU); GW = 4: 256 x 256 tiles, 8
+// wavefronts, 96 KB (one workgroup per CU): a third fewer global->LDS bytes per flop.
+template <int GW>
+struct GbShape {
+  static constexpr int WAVES = 2 * GW;
+  static constexpr int BW = 64 * GW;                                   // rows of w per workgroup
+  static constexpr int WTILEB = BW * GB_ROWB;                          // 8 / 16 KB
+  static constexpr int STAGEB = GB_XTILEB + WTILEB;                    // 24 / 32 KB
+  static constexpr size_t SMEM = static_cast<size_t>(GB_STAGES) * STAGEB;  // 72 / 96 KB
+  static constexpr int XLOADS = 16 / WAVES;                            // x instructions per wave per stage
+  static constexpr int LOADS = XLOADS + 2;                             // + 2 w instructions
+  static constexpr int WG_PER_CU = GW == 2 ? 2 : 1;
+};
 
 typedef __attribute__((address_space(3))) void lds_void;
+
+// One 16-byte direct global->LDS load per lane (lane l lands at dst + 16 l). A plain device function: written in
+// a kernel template with arguments that depend on its parameters, the builtin makes the host pass drop the
+// kernel's launch stub.
+__device__ __forceinline__ void gb_load_lds(const bf16_t *src, char *dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void *)dst, 16, 0, 0);
+}
 
 // s_waitcnt immediate that waits for vmcnt <= n and leaves expcnt / lgkmcnt unconstrained (gfx9 encoding:
 // vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt in 6:4, lgkmcnt in 11:8)
@@ -86,10 +104,13 @@ struct GbQkv {
   float *ss_out;      // [M, N / 64]
 };
 
-template <int EPI>
-__global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restrict__ x, const bf16_t *__restrict__ w,
-                                                          void *__restrict__ y, int64_t M, int N, int K, int tiles_n,
-                                                          int tiles_total, const GbQkv qa) {
+template <int EPI, int GW>
+__global__ __launch_bounds__(128 * GW, 4 / GW) void gemm_big_kernel(
+    const bf16_t *__restrict__ x, const bf16_t *__restrict__ w, void *__restrict__ y, int64_t M, int N, int K,
+    int tiles_n, int tiles_total, const GbQkv qa) {
+  using SH = GbShape<GW>;
+  constexpr int GB_STAGEB = SH::STAGEB, GB_LOADS = SH::LOADS, NWAVES = SH::WAVES;
+  constexpr size_t GB_SMEM = SH::SMEM;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr bool SWIGLU = EPI == GB_SWIGLU, OUT_F32 = EPI == GB_F32, RESID = EPI == GB_RESID;
   constexpr bool RESID32 = EPI == GB_RESID_F32;
@@ -97,8 +118,8 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
   constexpr bool TAB_F32 = EPI == GB_QKV || EPI == GB_QKV_W32, W32 = EPI == GB_QKV_W32;
   // wid through readfirstlane: wave-uniform for the compiler, so branches on the wavefront's quadrant or head are scalar
   const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wid >> 1, wn = wid & 1;
-  constexpr int OUT_COLS = SWIGLU ? 64 : 128;
+  const int wm = wid / GW, wn = wid % GW;
+  constexpr int OUT_COLS = SWIGLU ? 32 * GW : 64 * GW;
 
   // XCD-aware tile order: physical workgroup p runs on XCD p % 8; XCD x owns the contiguous logical
   // range [x q + min(x, r), ...) of q + (x < r) tiles (q = total / 8, r = total % 8) -- a bijection
@@ -117,12 +138,12 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
   const int n0 = nt * OUT_COLS;
 
   // direct-load sources: instruction q of an operand tile covers its rows 16 q .. 16 q + 15 (x: q < 16,
-  // w: q < 8); wave w issues q = w + 4 i. Lane l -> row 16 q + l / 4, LDS slot l % 4, K chunk slot ^ swizzle.
-  const bf16_t *xsrc[4];
+  // w: q < 4 GW); wave w issues q = w + NWAVES i. Lane l -> row 16 q + l / 4, LDS slot l % 4, K chunk slot ^ swizzle.
+  const bf16_t *xsrc[SH::XLOADS];
   const bf16_t *wsrc[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 16 * (wid + 4 * i) + (lane >> 2);
+  for (int i = 0; i < SH::XLOADS; ++i) {
+    const int r = 16 * (wid + NWAVES * i) + (lane >> 2);
     const int c = (lane & 3) ^ ((r >> 1) & 3);
     int64_t gr = m0 + r;
     gr = gr < M ? gr : M - 1;
@@ -130,13 +151,13 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int r = 16 * (wid + 4 * i) + (lane >> 2);
+    const int r = 16 * (wid + NWAVES * i) + (lane >> 2);
     const int c = (lane & 3) ^ ((r >> 1) & 3);
     int wr;
-    if (SWIGLU) {  // tile rows 0..63: gate rows n0.., rows 64..127: the matching up rows N + n0..
-      int colr = n0 + (r & 63);
+    if (SWIGLU) {  // tile rows 0..32 GW - 1: gate rows n0.., the next 32 GW: the matching up rows N + n0..
+      int colr = n0 + (r & (32 * GW - 1));
       colr = colr < N ? colr : N - 1;
-      wr = colr + (r >= 64 ? N : 0);
+      wr = colr + (r >= 32 * GW ? N : 0);
     } else {
       wr = n0 + r;
       wr = wr < N ? wr : N - 1;
@@ -146,11 +167,9 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
   auto issue = [&](int stage, int k0) {
     char *base = smem + (stage % GB_STAGES) * GB_STAGEB;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds(xsrc[i] + k0, (lds_void *)(base + (wid + 4 * i) * 1024), 16, 0, 0);
+    for (int i = 0; i < SH::XLOADS; ++i) gb_load_lds(xsrc[i] + k0, base + (wid + NWAVES * i) * 1024);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      __builtin_amdgcn_global_load_lds(wsrc[i] + k0, (lds_void *)(base + GB_XTILEB + (wid + 4 * i) * 1024), 16, 0, 0);
+    for (int i = 0; i < 2; ++i) gb_load_lds(wsrc[i] + k0, base + GB_XTILEB + (wid + NWAVES * i) * 1024);
   };
 
   f32x4 acc[4][8];
@@ -169,7 +188,7 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int R = SWIGLU ? ((i < 2 ? 0 : 64) + wn * 32 + 16 * (i & 1) + fr) : (wn * 64 + 16 * i + fr);
+    const int R = SWIGLU ? ((i < 2 ? 0 : 32 * GW) + wn * 32 + 16 * (i & 1) + fr) : (wn * 64 + 16 * i + fr);
     woff[i] = GB_XTILEB + R * GB_ROWB + 16 * (fg ^ ((R >> 1) & 3));
   }
 
@@ -366,10 +385,12 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
   constexpr int QCOLS = SWIGLU ? 32 : 64;             // output columns of a wavefront
   constexpr int RB = QCOLS * ESZ;                     // bytes of one quadrant row
   constexpr int PITCH = RB + 16;
-  constexpr int PASS_ROWS = ESZ == 4 ? 64 : 128;      // rows staged per pass (<= GB_SMEM / 4 bytes)
+  // rows staged per pass: what fits this wavefront's share of the ring (a power of two, 32..128)
+  constexpr int STG_BYTES = static_cast<int>(GB_SMEM / NWAVES);
+  constexpr int PASS_ROWS = 128 * PITCH <= STG_BYTES ? 128 : (64 * PITCH <= STG_BYTES ? 64 : 32);
   constexpr int CPR = RB / 16;                        // 16-byte chunks per row
-  static_assert(PASS_ROWS * PITCH <= static_cast<int>(GB_SMEM / 4), "epilogue staging exceeds a quarter of LDS");
-  char *stg = smem + wid * (GB_SMEM / 4);
+  static_assert(PASS_ROWS * PITCH <= STG_BYTES, "epilogue staging exceeds the wavefront's share of LDS");
+  char *stg = smem + wid * STG_BYTES;
   const int64_t qrow0 = m0 + wm * 128;
   const int qcol0 = n0 + wn * QCOLS;
 #pragma unroll
@@ -554,18 +575,31 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(const bf16_t *__restri
   }
 }
 
-template <int EPI>
-static int launch_big(const bf16_t *x, const bf16_t *w, void *y, int64_t M, int N, int K, const GbQkv &qa,
-                      hipStream_t s) {
-  VK_RAISE_LDS_ONCE(gemm_big_kernel<EPI>, GB_SMEM, "linear");
-  constexpr int OUT_COLS = EPI == GB_SWIGLU ? 64 : 128;
+template <int EPI, int GW>
+static int launch_big_gw(const bf16_t *x, const bf16_t *w, void *y, int64_t M, int N, int K, const GbQkv &qa,
+                         hipStream_t s) {
+  using SH = GbShape<GW>;
+  VK_RAISE_LDS_ONCE((gemm_big_kernel<EPI, GW>), SH::SMEM, "linear");
+  constexpr int OUT_COLS = EPI == GB_SWIGLU ? 32 * GW : 64 * GW;
   const int tiles_n = (N + OUT_COLS - 1) / OUT_COLS;
   const int64_t tiles_m = (M + GB_BM - 1) / GB_BM;
   const int64_t total = tiles_m * tiles_n;
   if (total >= (int64_t(1) << 31)) return fail(VK_ERR_ARG, "linear: too many tiles");
-  gemm_big_kernel<EPI><<<static_cast<unsigned>(total), 256, GB_SMEM, s>>>(x, w, y, M, N, K, tiles_n,
-                                                                           static_cast<int>(total), qa);
+  gemm_big_kernel<EPI, GW><<<static_cast<unsigned>(total), 128 * GW, SH::SMEM, s>>>(x, w, y, M, N, K, tiles_n,
+                                                                                    static_cast<int>(total), qa);
   return VK_OK;
+}
+
+// 256 x 256 tiles where they measured faster (same bits either way, M = 131136 and 4096): bf16 outputs at every K
+// (K 512 / 1536 / 2048: 8 / 4 / 10% faster) and fp32 outputs from K = 1024 (3 / 10% at 1536 / 2048, 1.5% slower at
+// 512). The SwiGLU, residual and Wqkv epilogues run 2-8% slower on them: with one workgroup per CU their epilogue
+// no longer overlaps another workgroup's K loop.
+template <int EPI>
+static int launch_big(const bf16_t *x, const bf16_t *w, void *y, int64_t M, int N, int K, const GbQkv &qa,
+                      hipStream_t s) {
+  const bool wide = EPI == GB_BF16 || (EPI == GB_F32 && K >= 1024);
+  if (wide) return launch_big_gw<EPI, 4>(x, w, y, M, N, K, qa, s);
+  return launch_big_gw<EPI, 2>(x, w, y, M, N, K, qa, s);
 }
 
 // Entry used by vk_linear for large M and by vk_gemm_rows (K % 64 == 0: an even number of K slices; N % 8 == 0:
