@@ -283,6 +283,9 @@ def test_grouped_rejects_unshared_prefix():
     bad[79, 511] += 1
     with pytest.raises(ValueError, match="share"):
         eng.generate(bad, [20, 20, 20, 20])
+    # the compare runs beside the prefill and raises at its end; the next prefill starts from a clean state
+    ok = eng.generate(same, [20, 20, 20, 20]).clone()
+    assert torch.equal(ok, eng.generate(same, [20, 20, 20, 20]))
 
 
 def test_sampled_stream_parity_k4_temperature():
