@@ -505,6 +505,9 @@ __global__ __launch_bounds__(128 * GW, 4 / GW) void gemm_big_kernel(
           *reinterpret_cast<u32x2 *>(rowp + (16 * i + 4 * fg) * 2) =
               u32x2{pack_bf(v[i][0], v[i][1]), pack_bf(v[i][2], v[i][3])};
       } else if (SWIGLU) {
+        // silu(g) = g / (1 + e^-g) as g times the hardware reciprocal (1 ulp) instead of the IEEE division: the
+        // epilogue's VALU work is on this product's critical path (the product ~5% faster at the prefill shape);
+        // 0.007% of the outputs then differ from the division's by one bf16 ulp
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           float o[4];
@@ -512,7 +515,7 @@ __global__ __launch_bounds__(128 * GW, 4 / GW) void gemm_big_kernel(
           for (int e = 0; e < 4; ++e) {
             const float gt = round_bf(acc[i][j][e]);
             const float up = round_bf(acc[i + 2][j][e]);
-            o[e] = round_bf(gt / (1.0f + __expf(-gt))) * up;
+            o[e] = round_bf(gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt))) * up;
           }
           *reinterpret_cast<u32x2 *>(rowp + (16 * i + 4 * fg) * 2) = u32x2{pack_bf(o[0], o[1]), pack_bf(o[2], o[3])};
         }
