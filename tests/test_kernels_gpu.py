@@ -127,6 +127,21 @@ def test_linear(M, N, K):
     assert torch.allclose(y32.cpu().double(), ref, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("M,N,K", [(4099, 1536, 512), (8192, 520, 512), (4608, 512, 1536), (5000, 3072, 1024)])
+def test_linear_large_m_tile_shapes_same_bits(M, N, K):
+    """Large M: bf16 outputs run 256 x 256 tiles, fp32 outputs at K < 1024 the 256 x 128 tiles; both accumulate
+    every output in the same K order, so the bf16 result is the fp32 result rounded, bit for bit (partial row
+    and column tiles included)."""
+    g = gen(M + 3 * N + K)
+    x = to_dev(R.bf(torch.randn(M, K, generator=g)), BF)
+    w = to_dev(R.bf(torch.randn(N, K, generator=g) / math.sqrt(K)), BF)
+    y = ops.linear(x, w)
+    y32 = ops.linear(x, w, out_dtype=torch.float32)
+    assert torch.equal(y, y32.to(BF))
+    ref = x.double() @ w.double().t()
+    assert torch.allclose(y32.double(), ref, rtol=1e-5, atol=1e-5)
+
+
 @pytest.mark.parametrize("M", [1, 100, 512, 4500])
 def test_linear_swiglu(M):
     g = gen(M)
