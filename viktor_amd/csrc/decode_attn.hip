@@ -398,8 +398,11 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   // The part's tiles: its static share of the prefix tiles (sized by pre_max, so they are known before any
   // length is read; tiles past the group's actual prefix length are fully masked), then its share of the
   // own-row tiles of all G members taken as one sequence (member 0's tiles, then member 1's, ...). Both
-  // shares are equal cuts, so parts are balanced for any part count.
-  const int tp_all = static_cast<int>((pre_max + GU_TILE - 1) / GU_TILE);
+  // shares are equal cuts, so parts are balanced for any part count. The tiles cover the prefix rows but its
+  // last (a window's BOS row, 2049 = 64 x 32 + 1 at the rollout's shape), which the last wavefront of the last
+  // part adds by VALU after its tiles: a 32-row tile for that one row would make the workgroup's tile count
+  // 1 or 5 (mod 8) at every step, so one to five wavefronts would run one more tile than the rest.
+  const int tp_all = static_cast<int>((pre_max - 1 + GU_TILE - 1) / GU_TILE);
   const int pt0 = tp_all * part / nparts, npre = tp_all * (part + 1) / nparts - pt0;
   const bf16_t *kpre = kp + pp * stride_pb + kvh * DA_D, *vpre = vp + pp * stride_pb + kvh * DA_D;
 
@@ -506,7 +509,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
     if (t < npre) {
       r.seg = 0;
       r.mc = m;
-      r.len = __builtin_amdgcn_readlane(len, G);
+      r.len = __builtin_amdgcn_readlane(len, G) - 1;  // (the last prefix row is added apart)
       r.k = kpre;
       r.v = vpre;
       r.stride = stride_ps;
@@ -535,7 +538,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   const int t0 = wid, t_end = T;
   if (t0 < t_end) {
     if (spec) {
-      cur.len = __builtin_amdgcn_readlane(len, G);
+      cur.len = __builtin_amdgcn_readlane(len, G) - 1;
     } else {
       cur = locate(t0, 0);
       gu_issue_tile(wring, cur.k, cur.stride, cur.row0, cur.clamp, lane);
@@ -653,6 +656,51 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
       stage ^= 1;
     }
     __builtin_amdgcn_s_waitcnt(gu_vmcnt(0));  // the ring's last loads, before its LDS is reused below
+  }
+  // The prefix's last row (row pre_len - 1) in the last wavefront of the last part, with the tile loop's rounding
+  // points: the score over the 64 d (this lane's 16 q values, the q fragments' layout, then the column's 4 lanes),
+  // the running-max rescale, the fp32 exponential into the row sum and its bf16 rounding into the output.
+  if (wid == GU_WAVES - 1 && part == nparts - 1) {
+    const int brow = __builtin_amdgcn_readlane(len, G) - 1;  // 0 .. pre_max - 1
+    const bf16_t *kb = kpre + static_cast<int64_t>(brow) * stride_ps;
+    const bf16_t *vb = vpre + static_cast<int64_t>(brow) * stride_ps;
+    const u32x4 kr[2] = {*reinterpret_cast<const u32x4 *>(kb + 8 * g),
+                         *reinterpret_cast<const u32x4 *>(kb + 32 + 8 * g)};
+    u32x2 vr[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) vr[dt] = *reinterpret_cast<const u32x2 *>(vb + 16 * dt + 4 * g);
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      float sc = 0.f;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const u32x4 qq = __builtin_bit_cast(u32x4, bq[cb][c]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc += lo_bf(qq[e]) * lo_bf(kr[c][e]) + hi_bf(qq[e]) * hi_bf(kr[c][e]);
+      }
+      sc += __shfl_xor(sc, 16, 64);
+      sc += __shfl_xor(sc, 32, 64);
+      const float sv = sc * scale_log2;
+      const float m_new = fmaxf(m_run[cb], sv);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float e = __builtin_amdgcn_exp2f(sv - m_use);
+      if (__builtin_amdgcn_ballot_w64(m_new != m_run[cb])) {
+        const float alpha = __builtin_amdgcn_exp2f(m_run[cb] - m_use);
+        l_run[cb] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) acc[cb][dt] *= alpha;
+      }
+      m_run[cb] = m_new;
+      l_run[cb] += g == 0 ? e : 0.f;  // (the row sum is reduced over the column's 4 lanes below)
+      const float pb = round_bf(e);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        acc[cb][dt][0] = fmaf(pb, lo_bf(vr[dt][0]), acc[cb][dt][0]);
+        acc[cb][dt][1] = fmaf(pb, hi_bf(vr[dt][0]), acc[cb][dt][1]);
+        acc[cb][dt][2] = fmaf(pb, lo_bf(vr[dt][1]), acc[cb][dt][2]);
+        acc[cb][dt][3] = fmaf(pb, hi_bf(vr[dt][1]), acc[cb][dt][3]);
+      }
+    }
   }
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
