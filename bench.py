@@ -676,6 +676,7 @@ def products_mode(reps=50, stamps=False):
         from viktor_amd.build import STAMPS_LIB
         L.load(STAMPS_LIB)  # before anything else loads the product library
     from viktor_amd import hip_ops as ops
+    from viktor_amd import DecodeEngine
     from viktor_amd.decoder import KVCache
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -684,8 +685,8 @@ def products_mode(reps=50, stamps=False):
     B, G = PREFIXES * GROUP, GROUP
     own = (NEW - 2) // 2 + 1  # own rows attended at the rollout's mean step, the new one included
     gen = torch.Generator(device=dev).manual_seed(0)
-    cache = KVCache(cfg, B, NEW, torch.bfloat16, dev)
-    pc = KVCache(cfg, B // G, P + 1, torch.bfloat16, dev)
+    cache = KVCache(cfg, B, NEW, torch.bfloat16, dev, pad_rows=DecodeEngine.OWN_PAD_ROWS)
+    pc = KVCache(cfg, B // G, P + 1, torch.bfloat16, dev, pad_rows=DecodeEngine.PREFIX_PAD_ROWS)
     for t in (cache.k, cache.v, pc.k, pc.v):
         t.normal_(generator=gen)
     plen32 = torch.full((B // G,), P + 1, dtype=torch.int32, device=dev)

@@ -153,6 +153,22 @@ def test_attention_plan_orders_longest_first():
         hip_ops.AttentionPlan([5], [4], [0], "cpu", causal=True)
 
 
+def test_kv_cache_pad_rows_layout():
+    """KVCache(pad_rows=p): k / v are [L, B, max_len, Hkv, D] views whose sequence stride is (max_len + p) rows
+    (what the kernels take as the cache's sequence stride); the pad rows are never part of the view."""
+    from viktor_amd.decoder import DecoderConfig, KVCache
+    cfg = DecoderConfig(vocab_size=7, n_layers=2)
+    c = KVCache(cfg, 3, 10, torch.bfloat16, "cpu", pad_rows=5)
+    row = cfg.n_kv_heads * cfg.head_dim
+    assert c.k.shape == c.v.shape == (2, 3, 10, cfg.n_kv_heads, cfg.head_dim) and c.max_len == 10
+    assert c.k.stride() == c.v.stride() == (3 * 15 * row, 15 * row, row, cfg.head_dim, 1)
+    c.k.fill_(1)
+    base = c.k.as_strided((2 * 3 * 15 * row,), (1,))  # the padded storage behind the view
+    assert float(base.sum()) == 2 * 3 * 10 * row
+    assert float(base.view(2, 3, 15, row)[:, :, 10:].abs().sum()) == 0
+    assert KVCache(cfg, 3, 10, torch.bfloat16, "cpu").k.is_contiguous()
+
+
 def test_batch_weights_map_bases_to_tokens():
     """Basecaller.batch with per-base weights (the GSPO update's SFT term): a k-mer token weighs its lowest
     base weight, a partial tail token its lowest real base, EOS 1, padding 0 (viktor/model.py:133-145)."""

@@ -267,6 +267,36 @@ def test_grouped_matches_ungrouped_engine():
     assert agree > 0.9
 
 
+def test_grouped_cache_padding_same_bits():
+    """The grouped layout's padded cache strides (prefix and own-token rows) change no bit: tokens and logp of a
+    sampled grouped rollout (EOS banned, so every step is a live choice) equal those of the same engine built
+    without padding."""
+    m = make_model(1, n_layers=2, seed=5, norm_jitter=0.1, bias_jitter=0.1)
+    gm = gpu_copy(m)
+    lens, steps, grp = [70, 33, 130], 40, 4
+    fr = synth_frames(1, sum(lens), 512, seed=6)[0]
+    fr = torch.cat([w for w in fr.split(lens) for _ in range(grp)]).to(DEV)
+    lens = [n for n in lens for _ in range(grp)]
+    u = synth_uniforms(len(lens), steps, seed=7).to(DEV)
+    outs = []
+    for pads in ((0, 0), (DecodeEngine.PREFIX_PAD_ROWS, DecodeEngine.OWN_PAD_ROWS)):
+        saved = DecodeEngine.PREFIX_PAD_ROWS, DecodeEngine.OWN_PAD_ROWS
+        DecodeEngine.PREFIX_PAD_ROWS, DecodeEngine.OWN_PAD_ROWS = pads
+        try:
+            eng = DecodeEngine(gm, len(lens), steps, max(lens), temperature=1.0, group_size=grp, logprobs=True,
+                               max_homopolymer=None, prefill_batch=2)
+        finally:
+            DecodeEngine.PREFIX_PAD_ROWS, DecodeEngine.OWN_PAD_ROWS = saved
+        assert eng.cache.k.stride(1) == (steps + pads[1]) * 128
+        assert eng.prefix_cache.k.stride(1) == (max(lens) + 1 + pads[0]) * 128
+        eng.bias.copy_(no_eos_bias(m.tokenizer.vocab_size))
+        eng.set_uniforms(u)
+        outs.append((eng.generate(fr, lens, steps=steps).clone(), eng.logp.clone()))
+        del eng
+    assert bool((outs[0][0] > R.EOS).all())
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
 def test_grouped_rejects_unshared_prefix():
     m = make_model(1, n_layers=1, seed=0)
     gm = gpu_copy(m)

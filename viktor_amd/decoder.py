@@ -43,12 +43,15 @@ def rope_tables(dim: int, max_len: int, theta: float):
 
 class KVCache:
     """Static cache, layout [layer, batch, position, kv_head, head_dim] (reference: viktor/decoder.py:43-51).
-    In HBM each (sequence, position) row of one layer is HKV * head_dim contiguous bf16 values (256 B)."""
+    In HBM each (sequence, position) row of one layer is HKV * head_dim contiguous bf16 values (256 B).
+    pad_rows > 0 leaves that many unused rows after each sequence's max_len rows (k / v are views of the
+    padded storage): it moves the sequences' start addresses off a power-of-two stride, where concurrent
+    streams over many sequences would share HBM channels."""
 
-    def __init__(self, cfg: DecoderConfig, batch: int, max_len: int, dtype, device):
-        shape = (cfg.n_layers, batch, max_len, cfg.n_kv_heads, cfg.head_dim)
-        self.k = torch.zeros(shape, dtype=dtype, device=device)
-        self.v = torch.zeros(shape, dtype=dtype, device=device)
+    def __init__(self, cfg: DecoderConfig, batch: int, max_len: int, dtype, device, pad_rows: int = 0):
+        shape = (cfg.n_layers, batch, max_len + int(pad_rows), cfg.n_kv_heads, cfg.head_dim)
+        self.k = torch.zeros(shape, dtype=dtype, device=device)[:, :, :max_len]
+        self.v = torch.zeros(shape, dtype=dtype, device=device)[:, :, :max_len]
         self.max_len = max_len
         self.positions = torch.arange(max_len, device=device)
 

@@ -32,6 +32,12 @@ from .tokenizer import BOS, EOS, PAD
 
 
 class DecodeEngine:
+    # unused rows after each sequence's rows (KVCache pad_rows) in the grouped layout's prefix and own-token
+    # caches: at the rollout's shape the per-sequence strides become 2144 x 256 B (536 KiB) and 1056 x 256 B
+    # (264 KiB) instead of 512 KiB + 256 B and 256 KiB
+    PREFIX_PAD_ROWS = 95
+    OWN_PAD_ROWS = 32
+
     def __init__(self, model, batch_size: int, max_new_tokens: int, max_frames: int, backend: str = "auto",
                  cuda_graph: bool = True, prefill_batch: int = 128, check_every: int = 32,
                  attention_backend: str = "auto", temperature: float = 0.0, max_homopolymer=64, group_size: int = 1,
@@ -71,8 +77,10 @@ class DecodeEngine:
             self.cache = KVCache(self.dec.cfg, batch_size, max_len, self.dtype, dev)
             self.prefix_cache = None
         else:
-            self.prefix_cache = KVCache(self.dec.cfg, batch_size // self.G, max_frames + 1, self.dtype, dev)
-            self.cache = KVCache(self.dec.cfg, batch_size, max(max_new_tokens, 2), self.dtype, dev)
+            self.prefix_cache = KVCache(self.dec.cfg, batch_size // self.G, max_frames + 1, self.dtype, dev,
+                                        pad_rows=self.PREFIX_PAD_ROWS)
+            self.cache = KVCache(self.dec.cfg, batch_size, max(max_new_tokens, 2), self.dtype, dev,
+                                 pad_rows=self.OWN_PAD_ROWS)
             self.prefix_len32 = torch.ones(batch_size // self.G, dtype=torch.int32, device=dev)
             self.cache_base = torch.zeros(batch_size, dtype=torch.long, device=dev)  # own-token row = pos - base
             self.grouped_workspace = ops.decode_attention_grouped_workspace(batch_size, self.G, max_frames + 1,
