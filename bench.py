@@ -613,7 +613,8 @@ def kernels_mode(group, reps=5):
     """Only the dominant kernel at the rollout's mean shape plus a plain 256 MiB device copy of known size,
     for hardware-counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): the copy's counter readings give
     the scale factor from counter units to bytes. group 1: 512 sequences x 2561 attended positions of a
-    3073-position cache layer; group G: 512 / G shared 2049-position prefixes + 512 own 512-position rows."""
+    3073-position cache layer; group G: 512 / G shared 2049-position prefixes + 512 own 512-position rows, in
+    the engine's padded cache layout."""
     from viktor_amd import hip_ops as ops
     dev = torch.device("cuda", 0)
     B, S, L = PREFIXES * GROUP, P + 1 + NEW, P + 2 + (NEW - 2) // 2
@@ -626,11 +627,13 @@ def kernels_mode(group, reps=5):
         ws = ops.decode_attention_workspace(B, 8, S, dev)
         call = lambda: ops.decode_attention(q, kc, vc, lens, workspace=ws)
         alg_rows = B * L
-    else:
-        kp = torch.randn(B // group, P + 1, 2, 64, device=dev, generator=g).to(torch.bfloat16)
-        vp = torch.randn(B // group, P + 1, 2, 64, device=dev, generator=g).to(torch.bfloat16)
-        ks = torch.randn(B, NEW, 2, 64, device=dev, generator=g).to(torch.bfloat16)
-        vs = torch.randn(B, NEW, 2, 64, device=dev, generator=g).to(torch.bfloat16)
+    else:  # the engine's padded sequence strides
+        from viktor_amd import DecodeEngine
+        pp, op = DecodeEngine.PREFIX_PAD_ROWS, DecodeEngine.OWN_PAD_ROWS
+        kp = torch.randn(B // group, P + 1 + pp, 2, 64, device=dev, generator=g).to(torch.bfloat16)[:, :P + 1]
+        vp = torch.randn(B // group, P + 1 + pp, 2, 64, device=dev, generator=g).to(torch.bfloat16)[:, :P + 1]
+        ks = torch.randn(B, NEW + op, 2, 64, device=dev, generator=g).to(torch.bfloat16)[:, :NEW]
+        vs = torch.randn(B, NEW + op, 2, 64, device=dev, generator=g).to(torch.bfloat16)[:, :NEW]
         plen = torch.full((B // group,), P + 1, dtype=torch.int32, device=dev)
         slen = torch.full((B,), L - P - 1, dtype=torch.int32, device=dev)
         ws = ops.decode_attention_grouped_workspace(B, group, P + 1, NEW, dev)
