@@ -381,7 +381,8 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   constexpr int NCB = (NC + 15) / 16;  // 16-column MFMA blocks
   constexpr int LDS_V = GU_WAVES * GU_WAVEB;
   constexpr int LDS_M = (GU_WAVES * NC * 64 + 2 * GU_WAVES * NC) * 4;
-  __shared__ __attribute__((aligned(16))) char smem[LDS_V > LDS_M ? LDS_V : LDS_M];
+  constexpr int LDS_BOS = LDS_V > LDS_M ? LDS_V : LDS_M;  // the prefix's last K / V row (256 B), past the rest
+  __shared__ __attribute__((aligned(16))) char smem[LDS_BOS + 256];
 
   // wave-uniform values go through readfirstlane / readlane so the tile loop and segment search stay scalar
   const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -491,6 +492,16 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   const int own_all = __builtin_amdgcn_readlane(incl, G - 1);
   const int ou0 = static_cast<int>(static_cast<int64_t>(own_all) * part / nparts);
   const int T = npre + static_cast<int>(static_cast<int64_t>(own_all) * (part + 1) / nparts) - ou0;  // tiles
+  // The wavefront that adds the prefix's last row after its tiles fetches that row now, by one direct load into
+  // LDS (lanes 0-31: its K half of the row, lanes 32-63: its V half, 4 bytes each), so the row is there when the
+  // tiles are done. A load issued after the first tiles' loads only makes the tile loop's counted waits
+  // stricter (they count the loads issued after the tile they need).
+  const bool bos_wave = wid == GU_WAVES - 1 && part == nparts - 1;
+  if (bos_wave) {
+    const int brow = __builtin_amdgcn_readlane(len, G) - 1;  // 0 .. pre_max - 1
+    const bf16_t *src = (lane < 32 ? kpre : vpre) + static_cast<int64_t>(brow) * stride_ps + 2 * (lane & 31);
+    __builtin_amdgcn_global_load_lds(src, (gu_lds_void_t *)(smem + LDS_BOS), 4, 0, 0);
+  }
 
   f32x4 acc[NCB][4];
   float m_run[NCB], l_run[NCB];
@@ -660,15 +671,14 @@ __global__ __launch_bounds__(GU_WAVES * 64) void grouped_attn_kernel(
   // The prefix's last row (row pre_len - 1) in the last wavefront of the last part, with the tile loop's rounding
   // points: the score over the 64 d (this lane's 16 q values, the q fragments' layout, then the column's 4 lanes),
   // the running-max rescale, the fp32 exponential into the row sum and its bf16 rounding into the output.
-  if (wid == GU_WAVES - 1 && part == nparts - 1) {
-    const int brow = __builtin_amdgcn_readlane(len, G) - 1;  // 0 .. pre_max - 1
-    const bf16_t *kb = kpre + static_cast<int64_t>(brow) * stride_ps;
-    const bf16_t *vb = vpre + static_cast<int64_t>(brow) * stride_ps;
-    const u32x4 kr[2] = {*reinterpret_cast<const u32x4 *>(kb + 8 * g),
-                         *reinterpret_cast<const u32x4 *>(kb + 32 + 8 * g)};
+  if (bos_wave) {
+    __builtin_amdgcn_s_waitcnt(gu_vmcnt(0));  // the row's load (a wavefront without tiles has not waited yet)
+    const char *kb = smem + LDS_BOS, *vb = kb + 128;
+    const u32x4 kr[2] = {*reinterpret_cast<const u32x4 *>(kb + 16 * g),
+                         *reinterpret_cast<const u32x4 *>(kb + 64 + 16 * g)};
     u32x2 vr[4];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) vr[dt] = *reinterpret_cast<const u32x2 *>(vb + 16 * dt + 4 * g);
+    for (int dt = 0; dt < 4; ++dt) vr[dt] = *reinterpret_cast<const u32x2 *>(vb + 32 * dt + 8 * g);
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
       float sc = 0.f;
