@@ -48,7 +48,7 @@ Extra objects on the JSON line:
                 (127, 128)) with seeded random weights; ms, chunks/s and the MFMA fraction of its algorithmic
                 flops (convolutions, 4 products per layer, window attention over the keys each frame sees).
 Usage: python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--no-cpu] [--no-configs]
-       python bench.py --mode encoder|prefill [--steps N]   (that object alone, N timed repetitions)
+       python bench.py --mode encoder|prefill|scoring [--steps N]   (that object alone, N timed repetitions)
        python bench.py --mode configs                       (the other configurations alone)
        python bench.py --mode kernels [--group-size G]      (the decode-attention traffic probe)
        python bench.py --mode products [--steps N] [--phase-stamps]   (the decode step's layer loop, captured)
@@ -776,10 +776,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the other configurations' measurements")
     ap.add_argument("--prefill-batch", type=int, default=128)
-    ap.add_argument("--mode", choices=["rollout", "kernels", "products", "encoder", "prefill", "configs", "update"],
+    ap.add_argument("--mode", choices=["rollout", "kernels", "products", "encoder", "prefill", "configs", "update",
+                                       "scoring"],
                     default="rollout",
                     help="kernels: decode-attention traffic probe; products: the decode step's layer loop captured "
-                         "(kernel traces, counters, --phase-stamps); encoder / prefill / configs / update: that object alone")
+                         "(kernel traces, counters, --phase-stamps); encoder / prefill / configs / update / scoring: "
+                         "that object alone")
     ap.add_argument("--phase-stamps", action="store_true",
                     help="products mode: load the phase-timestamp profiling build and summarise its stamps")
     ap.add_argument("--group-size", type=int, default=GROUP, help="sequences sharing one prefix KV copy (1: none)")
@@ -804,6 +806,11 @@ def main():
         fr = frames(PREFIXES, P, 512, seed=0).to(dev).repeat_interleave(GROUP, 0).reshape(-1, 512)
         u = uniforms(PREFIXES * GROUP, NEW, seed=1).to(dev)
         print(json.dumps({"configs": other_configs(dev, gm, fr, u)}), flush=True)
+        return
+    if args.mode == "scoring":
+        dev = torch.device("cuda", 0)
+        torch.cuda.set_device(dev)
+        print(json.dumps({"scoring": scoring_config(dev, reps=max(args.steps, 1))}), flush=True)
         return
     if args.mode == "update":
         print(json.dumps({"gspo_update": update_timing(steps=max(args.steps, 1), warmup=args.warmup)}), flush=True)
