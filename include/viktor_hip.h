@@ -111,9 +111,11 @@ int vk_group_rows_equal(const void *x, int64_t groups, int32_t G, int64_t member
  *   x_dtype f32: x[M, N] = alpha x + bf16(a w^T + bias) in fp32, the residual add x + sublayer(x) of an fp32 stream
  *     under torch.autocast bf16 (viktor/decoder.py:118-120 as scripts/gspo.py:345-347 runs it).
  * ss_out[M, N / 64] = the fp32 sum of squares of each row's new values per 64-column block.
+ * x_in (NULL: x itself): where the old residual is read, so x may be a fresh buffer and x_in the previous layer's
+ * stream, kept for the backward (the autograd graph of the reference keeps every layer's input alive).
  */
 int vk_linear_residual_big(const void *a, const void *w, void *x, int32_t x_dtype, int64_t M, int32_t N, int32_t K,
-                           const float *bias, float alpha, float *ss_out, void *stream);
+                           const float *bias, float alpha, float *ss_out, const void *x_in, void *stream);
 
 /*
  * RMSNorm from handed-over sums of squares: h = bf16(x * rsqrt(sum_b ss[row, b] / d + eps) * w) (x and w bf16 or

@@ -62,11 +62,11 @@ def test_argument_errors_return_status_without_device_work():
     rc = lib.vk_select_update(p, None, None, 1e-6, None, 0, 0, p, p, p, 0, 1.0, p, 16, 16, 1, p, None, p, None,
                               None, None, p, 16, 16, None, None, None, None, 0, 8, 7, 2, 0, None)
     assert rc == 1 and b"Gumbel" in lib.vk_last_error()
-    rc = lib.vk_linear_residual_big(p, p, p, 0, 4, 96, 64, None, 1.0, p, None)  # N % 128 != 0
+    rc = lib.vk_linear_residual_big(p, p, p, 0, 4, 96, 64, None, 1.0, p, None, None)  # N % 128 != 0
     assert rc == 1 and b"N" in lib.vk_last_error()
-    rc = lib.vk_linear_residual_big(p, p, p, 0, 4, 128, 64, None, 1.0, None, None)  # no sums-of-squares output
+    rc = lib.vk_linear_residual_big(p, p, p, 0, 4, 128, 64, None, 1.0, None, None, None)  # no sums-of-squares output
     assert rc == 1 and b"null" in lib.vk_last_error()
-    rc = lib.vk_linear_residual_big(p, p, p, 7, 4, 128, 64, None, 1.0, p, None)  # residual dtype
+    rc = lib.vk_linear_residual_big(p, p, p, 7, 4, 128, 64, None, 1.0, p, None, None)  # residual dtype
     assert rc == 1 and b"dtype" in lib.vk_last_error()
     rc = lib.vk_rmsnorm_apply_ss(p, 0, p, 8, p, 0, p, 4, 12, 1e-6, None)  # d % 8 != 0
     assert rc == 1 and b"d=12" in lib.vk_last_error()

@@ -698,8 +698,9 @@ def test_linear_qkv_rope(M, tables):
 
 @pytest.mark.parametrize("M,N,K,alpha,bias", [(4500, 512, 512, 1.0, False), (700, 512, 2048, 2.4494897, True)])
 def test_linear_residual_big_and_rmsnorm_apply(M, N, K, alpha, bias):
-    """x = bf16(bf16(a w^T + b) + bf16(alpha x)) in place with per-64-column sums of squares, then the RMSNorm from
-    those sums, against the formulas (and, for alpha 1 without bias, against add_rmsnorm of the unfused product)."""
+    """x = bf16(bf16(a w^T + b) + bf16(alpha x)) in place with per-64-column sums of squares (out of place: the same
+    bits, x untouched), then the RMSNorm from those sums, against the formulas (and, for alpha 1 without bias,
+    against add_rmsnorm of the unfused product)."""
     g = gen(M + K)
     a = R.bf(torch.randn(M, K, generator=g))
     w = R.bf(torch.randn(N, K, generator=g) / math.sqrt(K))
@@ -707,7 +708,12 @@ def test_linear_residual_big_and_rmsnorm_apply(M, N, K, alpha, bias):
     b = R.bf(0.1 * torch.randn(N, generator=g)) if bias else None
     nw = R.bf(torch.rand(N, generator=g) + 0.5)
     xd = to_dev(x, BF)
+    # out of place first (the old stream read from x, the new one written to out, x untouched): the same bits
+    x_keep, out = to_dev(x, BF), torch.empty(M, N, dtype=BF, device=DEV)
+    ss_o = ops.linear_residual_big(to_dev(a, BF), to_dev(w, BF), x_keep, bias=None if b is None else to_dev(b),
+                                   alpha=alpha, out=out)
     ss = ops.linear_residual_big(to_dev(a, BF), to_dev(w, BF), xd, bias=None if b is None else to_dev(b), alpha=alpha)
+    assert torch.equal(out, xd) and torch.equal(ss_o, ss) and torch.equal(x_keep.cpu(), x)
     acc = (a.double() @ w.double().t()).float() + (0 if b is None else b)
     want = R.bf(R.bf(acc) + R.bf(alpha * x))
     ok, err = bf_close(xd, want, ulps=1, atol=2e-2)  # an accumulation-order flip of bf16(acc) moves the sum one ulp
@@ -762,7 +768,11 @@ def test_linear_residual_big_fp32_stream(M, K, alpha, bias):
     b = R.bf(0.1 * torch.randn(N, generator=g)) if bias else None
     nw = torch.rand(N, generator=g) + 0.5  # fp32 master weights
     xd = to_dev(x)
+    x_keep, out = to_dev(x), torch.empty(M, N, dtype=torch.float32, device=DEV)
+    ss_o = ops.linear_residual_big(to_dev(a, BF), to_dev(w, BF), x_keep, bias=None if b is None else to_dev(b),
+                                   alpha=alpha, out=out)
     ss = ops.linear_residual_big(to_dev(a, BF), to_dev(w, BF), xd, bias=None if b is None else to_dev(b), alpha=alpha)
+    assert torch.equal(out, xd) and torch.equal(ss_o, ss) and torch.equal(x_keep.cpu(), x)  # out of place: same bits
     # the same kernel's fp32 accumulator (its fp32-output epilogue): the residual is then exact --
     # alpha x + bf16(acc + b) with one fp32 rounding (alpha is a power of two here, so alpha x is exact)
     from viktor_amd._lib import call, ptr, stream_handle

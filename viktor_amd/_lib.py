@@ -74,7 +74,7 @@ SIGNATURES = {
     "vk_deepnorm_rmsnorm": [_P, _P, _P, _F, _P, _F, _I64, _I32, _P],
     "vk_gemm_rows": [_P, _P, _P, _I64, _I32, _I32, _I32, _P],
     "vk_group_rows_equal": [_P, _I64, _I32, _I64, _P, _P],
-    "vk_linear_residual_big": [_P, _P, _P, _I32, _I64, _I32, _I32, _P, _F, _P, _P],
+    "vk_linear_residual_big": [_P, _P, _P, _I32, _I64, _I32, _I32, _P, _F, _P, _P, _P],
     "vk_rmsnorm_apply_ss": [_P, _I32, _P, _I32, _P, _I32, _P, _I64, _I32, _F, _P],
     "vk_rmsnorm_f32": [_P, _P, _P, _I64, _I32, _F, _P],
     "vk_timestamp": [_P, _I64, _P],

@@ -81,6 +81,8 @@ constexpr int vmcnt_imm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((
 // GB_RESID_F32: y is an fp32 residual stream updated in place, y = alpha y + bf16(acc + bias): the autocast residual
 // add x + sublayer(x) of an fp32 stream and a bf16 product (viktor/decoder.py:118-120 under torch.autocast bf16);
 // ss_out as GB_RESID, over the new fp32 values.
+// Both residual forms read the old residual from resid_in instead when it is given (out of place: y is then only
+// written, and resid_in keeps the previous layer's stream, as a backward pass needs it).
 enum GbEpi { GB_BF16 = 0, GB_F32 = 1, GB_SWIGLU = 2, GB_QKV = 3, GB_RESID = 4, GB_QKV_BF16 = 5, GB_RESID_F32 = 6,
              GB_QKV_W32 = 7 };
 
@@ -101,7 +103,8 @@ struct GbQkv {
   // GB_RESID
   const float *bias;  // [N] or NULL
   float alpha;
-  float *ss_out;      // [M, N / 64]
+  float *ss_out;         // [M, N / 64]
+  const void *resid_in;  // the old residual rows [M, N] (NULL: the output itself, updated in place)
 };
 
 template <int EPI, int GW>
@@ -313,7 +316,7 @@ __global__ __launch_bounds__(128 * GW, 4 / GW) void gemm_big_kernel(
   auto r32_load = [&](int j, f32x4 (&dst)[4]) {
     int64_t rrow = m0 + wm * 128 + 16 * j + fr_e;
     rrow = rrow < M ? rrow : M - 1;
-    const float *yrow = static_cast<const float *>(y) + rrow * N + n0 + wn * 64;
+    const float *yrow = static_cast<const float *>(qa.resid_in ? qa.resid_in : y) + rrow * N + n0 + wn * 64;
 #pragma unroll
     for (int i = 0; i < 4; ++i) dst[i] = *reinterpret_cast<const f32x4 *>(yrow + 16 * i + 4 * fg_e);
   };
@@ -335,7 +338,7 @@ __global__ __launch_bounds__(128 * GW, 4 / GW) void gemm_big_kernel(
     for (int j = 0; j < 8; ++j) {
       int64_t rrow = m0 + wm * 128 + 16 * j + fr_e;
       rrow = rrow < M ? rrow : M - 1;
-      const bf16_t *yrow = static_cast<const bf16_t *>(y) + rrow * N + n0 + wn * 64;
+      const bf16_t *yrow = static_cast<const bf16_t *>(qa.resid_in ? qa.resid_in : y) + rrow * N + n0 + wn * 64;
 #pragma unroll
       for (int i = 0; i < 4; ++i) res_old[j][i] = *reinterpret_cast<const u32x2 *>(yrow + 16 * i + 4 * fg_e);
     }
@@ -683,8 +686,10 @@ extern "C" int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32
 }
 
 extern "C" int vk_linear_residual_big(const void *a, const void *w, void *x, int32_t x_dtype, int64_t M, int32_t N,
-                                      int32_t K, const float *bias, float alpha, float *ss_out, void *stream) {
+                                      int32_t K, const float *bias, float alpha, float *ss_out, const void *x_in,
+                                      void *stream) {
   VK_CHECK_ARG(a && w && x && ss_out, "linear_residual_big: null pointer");
+  VK_CHECK_ARG(x_in == nullptr || vk_aligned16(x_in), "linear_residual_big: x_in must be 16-byte aligned");
   VK_CHECK_ARG(x_dtype == VK_DTYPE_BF16 || x_dtype == VK_DTYPE_F32, "linear_residual_big: bad residual dtype");
   VK_CHECK_ARG(M >= 0 && N > 0 && N % 128 == 0 && K > 0 && K % 64 == 0,
                "linear_residual_big: need N %% 128 == 0 and K %% 64 == 0 (N=%d K=%d)", N, K);
@@ -696,6 +701,7 @@ extern "C" int vk_linear_residual_big(const void *a, const void *w, void *x, int
   qa.bias = bias;
   qa.alpha = alpha;
   qa.ss_out = ss_out;
+  qa.resid_in = x_in;
   const auto ab = static_cast<const bf16_t *>(a), wb = static_cast<const bf16_t *>(w);
   const int rc = x_dtype == VK_DTYPE_F32 ? launch_big<GB_RESID_F32>(ab, wb, x, M, N, K, qa, VK_STREAM(stream))
                                          : launch_big<GB_RESID>(ab, wb, x, M, N, K, qa, VK_STREAM(stream));

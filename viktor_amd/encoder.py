@@ -330,11 +330,11 @@ class DoradoEncoder:
             # out_proj: bias + DeepNorm residual in the product's epilogue (x in place, row sums of squares out),
             # then the RMSNorm in place; the same for fc2 without bias
             call("vk_linear_residual_big", ptr(o), ptr(Lw["wo"]), ptr(x), BF, M, C, C, ptr(Lw["bo"]), Lw["alpha"],
-                 ptr(ss), st)
+                 ptr(ss), ptr(None), st)
             call("vk_rmsnorm_apply_ss", ptr(x), BF, ptr(ss), C // 64, ptr(Lw["n1"]), BF, ptr(x), M, C, 1e-5, st)
             call("vk_gemm_rows", ptr(x), ptr(Lw["w1"]), ptr(g), M, Fd, C, 2, st)
             call("vk_linear_residual_big", ptr(g), ptr(Lw["w2"]), ptr(x), BF, M, C, Fd, ptr(None), Lw["alpha"],
-                 ptr(ss), st)
+                 ptr(ss), ptr(None), st)
             call("vk_rmsnorm_apply_ss", ptr(x), BF, ptr(ss), C // 64, ptr(Lw["n2"]), BF, ptr(x), M, C, 1e-5, st)
 
     def flops_per_chunk(self, samples: int) -> float:

@@ -149,22 +149,26 @@ def linear_qkv_rope(x, w, q_norm_w, k_norm_w, cos, sin, pos, seq, k_cache, v_cac
     return (q, k, v) if return_kv else q
 
 
-def linear_residual_big(a, w, x, bias=None, alpha=1.0):
+def linear_residual_big(a, w, x, bias=None, alpha=1.0, out=None):
     """Large-M residual product, in place. bf16 x: x = bf16(bf16(a @ w^T + bias) + bf16(alpha x)) (alpha 1, no
     bias: add_rmsnorm's x += delta, viktor/triton_ops.py:17-31; with the out_proj bias and the DeepNorm alpha:
     viktor/encoder.py:106-108). fp32 x: x = alpha x + bf16(a @ w^T + bias), the residual add of an fp32 stream and
     a bf16 product under torch.autocast (viktor/decoder.py:118-120). Returns the row sums of squares of the new x
-    per 64-column block [M, N / 64] fp32, for rmsnorm_apply."""
+    per 64-column block [M, N / 64] fp32, for rmsnorm_apply. out: the new stream goes there (same shape and dtype
+    as x) and x is left as it was."""
     require_device(a, "linear_residual_big")
     M, K = a.shape
     N = w.shape[0]
     _require(a.dtype == w.dtype == BF16 and x.dtype in (BF16, torch.float32) and w.shape[1] == K and x.shape == (M, N)
              and _contig(a, w, x, bias), "linear_residual_big: shapes")
     _require(bias is None or (bias.dtype == torch.float32 and bias.shape == (N,)), "linear_residual_big: bias fp32 [N]")
+    _require(out is None or (out.shape == x.shape and out.dtype == x.dtype and out.is_contiguous()
+                             and out.data_ptr() != x.data_ptr()), "linear_residual_big: out buffer")
     ss = torch.empty(M, N // 64, dtype=torch.float32, device=a.device)
     xdt = VK_DTYPE_F32 if x.dtype == torch.float32 else VK_DTYPE_BF16
-    call("vk_linear_residual_big", ptr(a), ptr(w), ptr(x), xdt, M, N, K, ptr(bias), float(alpha), ptr(ss),
-         stream_handle())
+    dst, src = (x, None) if out is None else (out, x)
+    call("vk_linear_residual_big", ptr(a), ptr(w), ptr(dst), xdt, M, N, K, ptr(bias), float(alpha), ptr(ss),
+         ptr(src), stream_handle())
     return ss
 
 

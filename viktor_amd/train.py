@@ -44,10 +44,12 @@ def decoder_params(dec) -> List[torch.Tensor]:
 
 
 def _residual_norm(x, a, w, norm_w, eps):
-    """x += bf16(a @ w^T) in place on the fp32 residual stream x, then bf16(RMSNorm(x) * norm_w) with fp32
-    norm_w: `x = x + sublayer(...)` and the next nn.RMSNorm under autocast (viktor/decoder.py:118-120). The
-    residual add rides in the product's epilogue, which hands the row sums of squares to the norm."""
-    return ops.rmsnorm_apply(x, ops.linear_residual_big(a, w, x), norm_w, eps)
+    """x + bf16(a @ w^T) on the fp32 residual stream x, into a new buffer (x is kept for the backward), then
+    bf16(RMSNorm of it * norm_w) with fp32 norm_w: `x = x + sublayer(...)` and the next nn.RMSNorm under
+    autocast (viktor/decoder.py:118-120). The residual add rides in the product's epilogue, which hands the row
+    sums of squares to the norm. Returns (new stream, normed bf16 rows)."""
+    y = torch.empty_like(x)
+    return y, ops.rmsnorm_apply(y, ops.linear_residual_big(a, w, x, out=y), norm_w, eps)
 
 
 class _TokenEmbed(torch.autograd.Function):
@@ -174,23 +176,22 @@ class _DecoderStack(torch.autograd.Function):
         w = [p.detach().float().contiguous() if j in norm_slot else p.detach().to(BF16).contiguous()
              for j, p in enumerate(params)]
         plan, rpos, cos, sin = meta["plan"], meta["rpos"], meta["cos"], meta["sin"]
-        x = x.detach().float().contiguous().clone()
+        x = x.detach().float().contiguous()  # read only: every layer writes its stream into a new buffer
         h = ops.rmsnorm_f32(x, w[0], eps)
         saved = []
         for i in range(L):
             wa, wqkv, wqn, wkn, wo, wm, wgu, wd = w[8 * i:8 * i + 8]
-            x_in = x.clone()
+            x_in = x
             qkv = ops.linear(h, wqkv)
             q, k, v = ops.qkv_rope_cache(qkv, wqn, wkn, cos, sin, rpos, None, None, None, eps, H, HKV, D,
                                          return_kv=True)
             lse = torch.empty(N, H, dtype=torch.float32, device=x.device)
             o = ops.varlen_attention(q, k, v, plan.attn, lse=lse)
-            h2 = _residual_norm(x, o.view(N, H * D), wo, wm, eps)
-            x_mid = x.clone()
+            x_mid, h2 = _residual_norm(x_in, o.view(N, H * D), wo, wm, eps)
             gu = ops.linear(h2, wgu)
             g = ops.swiglu(gu)
             w_next = w[8 * (i + 1)] if i + 1 < L else w[8 * L]
-            h_next = _residual_norm(x, g, wd, w_next, eps)
+            x, h_next = _residual_norm(x_mid, g, wd, w_next, eps)
             saved.append((x_in, h, qkv, q, k, v, o, lse, x_mid, h2, gu, g))
             h = h_next
         ctx.meta, ctx.saved_acts, ctx.w, ctx.x_final = meta, saved, w, x
