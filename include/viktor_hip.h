@@ -395,12 +395,13 @@ int vk_rmsnorm_backward_blocks(int64_t n, int32_t *blocks);
  * RMSNorm backward (nn.RMSNorm of the decoder blocks, viktor/decoder.py:110-124), d = 512: given x [n, d] and
  * weight w [d] (both bf16, or both fp32: the autocast forward's residual stream and master weights) and dy [n, d]
  * (bf16 or fp32 per dy_dtype): dx = r w dy - x r^3 mean(w dy x)
- * (+ dres when not NULL: the residual stream's incoming gradient; dx may alias dres), fp32;
+ * (+ dres when not NULL: the residual stream's incoming gradient; dx may alias dres), fp32, and when dx_bf16 is
+ * not NULL also dx rounded to bf16 (nearest even) there: the operand the next products of the backward take;
  * dw_part [vk_rmsnorm_backward_blocks(n), d] fp32: per-workgroup sums of dy x r (reduce with vk_colsum).
  */
 int vk_rmsnorm_backward(const void *x, int32_t x_dtype, const void *w, int32_t w_dtype, const void *dy,
-                        int32_t dy_dtype, const float *dres, float *dx, float *dw_part, int64_t n, int32_t d, float eps,
-                        void *stream);
+                        int32_t dy_dtype, const float *dres, float *dx, void *dx_bf16, float *dw_part, int64_t n,
+                        int32_t d, float eps, void *stream);
 
 /* out[c] = sum_r part[r, c] (+ out[c] when accumulate), fixed order. */
 int vk_colsum(const float *part, float *out, int32_t rows, int32_t cols, int32_t accumulate, void *stream);

@@ -97,9 +97,11 @@ def test_rmsnorm_backward_fp32_stream():
         ww = w.clone().requires_grad_(True)
         (F.rms_norm(xx, (512,), ww, 1e-6) * dy_use).sum().backward()
         dy_dev = dy_use.to(DEV) if dy_use is dy else dy_use.to(BF).to(DEV)
-        dx, dw = ops.rmsnorm_backward(x.to(DEV), w.to(DEV), dy_dev, 1e-6, dres=dres.to(DEV).clone())
+        dxb = torch.empty(n, 512, dtype=BF, device=DEV)
+        dx, dw = ops.rmsnorm_backward(x.to(DEV), w.to(DEV), dy_dev, 1e-6, dres=dres.to(DEV).clone(), dx_bf16=dxb)
         assert torch.allclose(dx.cpu(), xx.grad + dres, rtol=1e-4, atol=1e-4)
         assert torch.allclose(dw.cpu(), ww.grad, rtol=1e-4, atol=1e-3)
+        assert torch.equal(dxb, dx.to(BF))  # the bf16 copy is the tensor cast of dx, bit for bit
 
 
 @pytest.mark.parametrize("wdtype", ["bf16", "f32"])

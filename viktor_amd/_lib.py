@@ -60,7 +60,7 @@ SIGNATURES = {
     "vk_embed_grad_workspace": [_I64, _I32, _I32, ctypes.POINTER(_I64)],
     "vk_embed_grad": [_P, _I32, _I64, _P, _I64, _I32, _I32, _P, _P, _I64, _P],
     "vk_rmsnorm_backward_blocks": [_I64, ctypes.POINTER(_I32)],
-    "vk_rmsnorm_backward": [_P, _I32, _P, _I32, _P, _I32, _P, _P, _P, _I64, _I32, _F, _P],
+    "vk_rmsnorm_backward": [_P, _I32, _P, _I32, _P, _I32, _P, _P, _P, _P, _I64, _I32, _F, _P],
     "vk_colsum": [_P, _P, _I32, _I32, _I32, _P],
     "vk_qknorm_rope_backward": [_P, _P, _P, _I32, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _F,
                                 _P],

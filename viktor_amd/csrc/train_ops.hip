@@ -38,8 +38,8 @@ __device__ __forceinline__ float ld<bf16_t>(const bf16_t *p, int64_t i) { return
 template <typename XT, typename WT, typename DT>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const XT *__restrict__ x, const WT *__restrict__ w,
                                                          const DT *__restrict__ dy, const float *__restrict__ dres,
-                                                         float *__restrict__ dx, float *__restrict__ dw_part,
-                                                         int64_t n, float eps) {
+                                                         float *__restrict__ dx, bf16_t *__restrict__ dx_bf,
+                                                         float *__restrict__ dw_part, int64_t n, float eps) {
   __shared__ float red[4][TR_D];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   float wv[8], dwa[8];
@@ -87,6 +87,9 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const XT *__restrict__
     float *dst = dx + row * TR_D + 8 * lane;
     *reinterpret_cast<f32x4 *>(dst) = f32x4{o[0], o[1], o[2], o[3]};
     *reinterpret_cast<f32x4 *>(dst + 4) = f32x4{o[4], o[5], o[6], o[7]};
+    if (dx_bf)  // the bf16 copy the next products take (round to nearest even, as a tensor cast)
+      *reinterpret_cast<u32x4 *>(dx_bf + row * TR_D + 8 * lane) =
+          u32x4{pack_bf(o[0], o[1]), pack_bf(o[2], o[3]), pack_bf(o[4], o[5]), pack_bf(o[6], o[7])};
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) red[wid][8 * lane + j] = dwa[j];
@@ -262,16 +265,17 @@ extern "C" int vk_rmsnorm_backward_blocks(int64_t n, int32_t *blocks) {
 }
 
 extern "C" int vk_rmsnorm_backward(const void *x, int32_t x_dtype, const void *w, int32_t w_dtype, const void *dy,
-                                   int32_t dy_dtype, const float *dres, float *dx, float *dw_part, int64_t n, int32_t d,
-                                   float eps, void *stream) {
+                                   int32_t dy_dtype, const float *dres, float *dx, void *dx_bf16, float *dw_part,
+                                   int64_t n, int32_t d, float eps, void *stream) {
   VK_CHECK_ARG(x && w && dy && dx && dw_part, "rmsnorm_backward: null pointer");
   if (d != TR_D) return fail(VK_ERR_UNSUPPORTED, "rmsnorm_backward: built for d = %d (got %d)", TR_D, d);
   VK_CHECK_ARG(n >= 0 && (dy_dtype == VK_DTYPE_BF16 || dy_dtype == VK_DTYPE_F32), "rmsnorm_backward: bad arguments");
   VK_CHECK_ARG((x_dtype == VK_DTYPE_BF16 || x_dtype == VK_DTYPE_F32) && (w_dtype == VK_DTYPE_BF16 || w_dtype == VK_DTYPE_F32),
                "rmsnorm_backward: bad dtypes");
   VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w) && vk_aligned16(dx) && vk_aligned16(dy) &&
-                   (!dres || vk_aligned16(dres)),
+                   (!dres || vk_aligned16(dres)) && (!dx_bf16 || vk_aligned16(dx_bf16)),
                "rmsnorm_backward: alignment");
+  bf16_t *const dxb = static_cast<bf16_t *>(dx_bf16);
   if (n == 0) return VK_OK;
   const unsigned grid = row_grid(n);
   hipStream_t s = VK_STREAM(stream);
@@ -280,16 +284,16 @@ extern "C" int vk_rmsnorm_backward(const void *x, int32_t x_dtype, const void *w
     const auto xb = static_cast<const bf16_t *>(x);
     const auto wb = static_cast<const bf16_t *>(w);
     if (dy_dtype == VK_DTYPE_F32)
-      rmsnorm_bwd_kernel<bf16_t, bf16_t, float><<<grid, 256, 0, s>>>(xb, wb, static_cast<const float *>(dy), dres, dx, dw_part, n, eps);
+      rmsnorm_bwd_kernel<bf16_t, bf16_t, float><<<grid, 256, 0, s>>>(xb, wb, static_cast<const float *>(dy), dres, dx, dxb, dw_part, n, eps);
     else
-      rmsnorm_bwd_kernel<bf16_t, bf16_t, bf16_t><<<grid, 256, 0, s>>>(xb, wb, static_cast<const bf16_t *>(dy), dres, dx, dw_part, n, eps);
+      rmsnorm_bwd_kernel<bf16_t, bf16_t, bf16_t><<<grid, 256, 0, s>>>(xb, wb, static_cast<const bf16_t *>(dy), dres, dx, dxb, dw_part, n, eps);
   } else if (x_dtype == VK_DTYPE_F32 && w_dtype == VK_DTYPE_F32) {
     const auto xf = static_cast<const float *>(x);
     const auto wf = static_cast<const float *>(w);
     if (dy_dtype == VK_DTYPE_F32)
-      rmsnorm_bwd_kernel<float, float, float><<<grid, 256, 0, s>>>(xf, wf, static_cast<const float *>(dy), dres, dx, dw_part, n, eps);
+      rmsnorm_bwd_kernel<float, float, float><<<grid, 256, 0, s>>>(xf, wf, static_cast<const float *>(dy), dres, dx, dxb, dw_part, n, eps);
     else
-      rmsnorm_bwd_kernel<float, float, bf16_t><<<grid, 256, 0, s>>>(xf, wf, static_cast<const bf16_t *>(dy), dres, dx, dw_part, n, eps);
+      rmsnorm_bwd_kernel<float, float, bf16_t><<<grid, 256, 0, s>>>(xf, wf, static_cast<const bf16_t *>(dy), dres, dx, dxb, dw_part, n, eps);
   } else {
     return fail(VK_ERR_UNSUPPORTED, "rmsnorm_backward: x and w are both bf16 or both fp32");
   }

@@ -689,9 +689,10 @@ def colsum(part, out=None, accumulate=False):
     return out
 
 
-def rmsnorm_backward(x, w, dy, eps, dres=None, dx=None):
+def rmsnorm_backward(x, w, dy, eps, dres=None, dx=None, dx_bf16=None):
     """Backward of h = rmsnorm(x) * w (x [n, 512] and w [512] both bf16 or both fp32, dy [n, 512] bf16 or fp32):
     returns (dx fp32 [n, 512] = the norm's input gradient + dres, dw fp32 [512]). dx may be dres (in place).
+    dx_bf16 (a bf16 [n, 512] buffer): also receives dx.to(bfloat16), written by the same kernel.
     Reference: nn.RMSNorm of the decoder blocks, viktor/decoder.py:110-124."""
     require_device(x, "rmsnorm_backward")
     n, d = x.shape
@@ -699,13 +700,15 @@ def rmsnorm_backward(x, w, dy, eps, dres=None, dx=None):
              and dy.dtype in (BF16, torch.float32), "rmsnorm_backward: dtypes")
     _require(_contig(x, w, dy, dres) and (dres is None or (dres.dtype == torch.float32 and dres.shape == x.shape)),
              "rmsnorm_backward: layouts")
+    _require(dx_bf16 is None or (dx_bf16.dtype == BF16 and dx_bf16.shape == x.shape and dx_bf16.is_contiguous()),
+             "rmsnorm_backward: dx_bf16 bf16 [n, d]")
     if dx is None:
         dx = dres if dres is not None else torch.empty(n, d, dtype=torch.float32, device=x.device)
     part = torch.empty(_norm_blocks(n), d, dtype=torch.float32, device=x.device)
     xdt = VK_DTYPE_F32 if x.dtype == torch.float32 else VK_DTYPE_BF16
     call("vk_rmsnorm_backward", ptr(x), xdt, ptr(w), xdt, ptr(dy),
-         VK_DTYPE_F32 if dy.dtype == torch.float32 else VK_DTYPE_BF16, ptr(dres), ptr(dx), ptr(part), n, d, float(eps),
-         stream_handle())
+         VK_DTYPE_F32 if dy.dtype == torch.float32 else VK_DTYPE_BF16, ptr(dres), ptr(dx), ptr(dx_bf16), ptr(part), n,
+         d, float(eps), stream_handle())
     return dx, colsum(part)
 
 

@@ -209,27 +209,30 @@ class _DecoderStack(torch.autograd.Function):
         grads = [None] * len(w)
         dh = torch.zeros(N, d, dtype=torch.float32, device=x_final.device)
         dh[meta["tok_rows"]] = dh_tok.float()
-        dx, grads[8 * L] = ops.rmsnorm_backward(x_final, w[8 * L], dh, eps)  # dx: d loss / d x_L (fp32)
+        # each norm backward also writes its fp32 input gradient rounded to bf16 (the next products' operand)
+        dxb = torch.empty(N, d, dtype=BF16, device=x_final.device)
+        dx, grads[8 * L] = ops.rmsnorm_backward(x_final, w[8 * L], dh, eps, dx_bf16=dxb)  # dx: d loss / d x_L (fp32)
         for i in reversed(range(L)):
             x_in, h, qkv, q, k, v, o, lse, x_mid, h2, gu, g = saved[i]
             wa, wqkv, wqn, wkn, wo, wm, wgu, wd = w[8 * i:8 * i + 8]
             # x_{i+1} = x_mid + g Wd^T
-            dm = dx.to(BF16)
+            dm = dxb
             gd = ops.wgrad(dm, g)
             dg = ops.linear(dm, wd.t().contiguous())
             dgu = ops.swiglu_backward(gu, dg)
             ggu = ops.wgrad(dgu, h2)
             dh2 = ops.linear(dgu, wgu.t().contiguous())
-            dx, gm = ops.rmsnorm_backward(x_mid, wm, dh2, eps, dres=dx)  # d / d x_mid
+            da = torch.empty(N, d, dtype=BF16, device=dx.device)
+            dx, gm = ops.rmsnorm_backward(x_mid, wm, dh2, eps, dres=dx, dx_bf16=da)  # d / d x_mid
             # x_mid = x_in + o Wo^T
-            da = dx.to(BF16)
             go = ops.wgrad(da, o.view(N, H * D))
             do = ops.linear(da, wo.t().contiguous()).view(N, H, D)
             dq, dk, dv = ops.attention_backward(q, k, v, o, do, lse, plan.attn, plan.keys)
             dqkv, gqn, gkn = ops.qknorm_rope_backward(qkv, wqn, wkn, cos, sin, rpos, dq, dk, dv, eps, H, HKV, D)
             gqkv = ops.wgrad(dqkv, h)
             dhh = ops.linear(dqkv, wqkv.t().contiguous())
-            dx, ga = ops.rmsnorm_backward(x_in, wa, dhh, eps, dres=dx)  # d / d x_in
+            dxb = torch.empty(N, d, dtype=BF16, device=dx.device) if i > 0 else None
+            dx, ga = ops.rmsnorm_backward(x_in, wa, dhh, eps, dres=dx, dx_bf16=dxb)  # d / d x_in
             grads[8 * i:8 * i + 8] = [ga, gqkv, gqn, gkn, go, gm, ggu, gd]
         ctx.saved_acts = None
         return (dx, None, *[gr.float() for gr in grads])
