@@ -146,13 +146,15 @@ int vk_rmsnorm_f32(const float *x, const float *w, void *h, int64_t n, int32_t d
  * the Wqkv product + apply_rope of the encoder (viktor/encoder.py:71-75). norm_w_dtype f32 (with f32 tables):
  * fp32 norm weights, the autocast forward's Attention.project (viktor/decoder.py:63-67): nn.RMSNorm of a bf16 head
  * with fp32 weights returns bf16(x / rms * w), then apply_rope in fp32 rounds back to bf16.
+ * qkv_out (NULL: none): also the product itself, rounded to bf16, as rows [M, (H + 2 HKV) 64] (the unrotated
+ * projection output the QK-norm + RoPE backward takes).
  */
 int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32_t K, const void *q_norm_w, const void *k_norm_w,
                        int32_t norm_w_dtype, float eps, const void *cos_t, const void *sin_t, int32_t table_dtype, int64_t table_rows,
                        const int32_t *pos, const int32_t *rope_pos, const int32_t *seq, void *q, int64_t q_ld,
                        void *k_cache, void *v_cache, int64_t stride_cb, int64_t stride_cs, int64_t cache_rows,
-                       int64_t cache_len, void *k_out, void *v_out, int64_t kv_ld, int32_t n_heads, int32_t n_kv_heads,
-                       int32_t head_dim, void *stream);
+                       int64_t cache_len, void *k_out, void *v_out, int64_t kv_ld, void *qkv_out, int32_t n_heads,
+                       int32_t n_kv_heads, int32_t head_dim, void *stream);
 
 /*
  * Single-query GQA attention against one layer of the KV cache:

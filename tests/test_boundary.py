@@ -76,7 +76,7 @@ def test_argument_errors_return_status_without_device_work():
     assert rc == 1 and b"d=4096" in lib.vk_last_error()
     # fp32 QK-norm weights with bf16 rotary tables
     rc = lib.vk_linear_qkv_rope(p, p, 4, 512, p, p, 1, 1e-6, p, p, 0, 16, p, None, None, p, 512, None, None, 0, 0, 0,
-                                0, p, p, 128, 8, 2, 64, None)
+                                0, p, p, 128, None, 8, 2, 64, None)
     assert rc == 1 and b"fp32 rotary tables" in lib.vk_last_error()
     rc = lib.vk_rmsnorm_backward(p, 1, p, 0, p, 0, None, p, None, p, 4, 512, 1e-6, None)  # fp32 x with bf16 weights
     assert rc == 3

@@ -656,7 +656,8 @@ def test_norm_qkv_rope_cache(M, embed):
 @pytest.mark.parametrize("M,tables", [(300, "bf16"), (4500, "f32")])
 def test_linear_qkv_rope(M, tables):
     """The Wqkv product with QK-norm + RoPE + cache write in its epilogue against the oracle's composition of the
-    fused path's rounding points, and against the unfused pair (linear, then qkv_rope_cache)."""
+    fused path's rounding points, and against the unfused pair (linear, then qkv_rope_cache); the kept unrotated
+    product (qkv_out) against linear."""
     g = gen(M + 5)
     H, HKV, D, K, S, Bc = 8, 2, 64, 512, 300, M
     x = R.bf(torch.randn(M, K, generator=g) * 2)
@@ -673,8 +674,9 @@ def test_linear_qkv_rope(M, tables):
     kc = torch.zeros(Bc, S, HKV, D, dtype=BF, device=DEV)
     vc = torch.zeros_like(kc)
     dev = [to_dev(t, BF) for t in (x, wq, qw, kw)] + [to_dev(cos, tdt), to_dev(sin, tdt)]
+    raw = torch.empty(M, (H + 2 * HKV) * D, dtype=BF, device=DEV)
     q, k, v = ops.linear_qkv_rope(dev[0], dev[1], dev[2], dev[3], dev[4], dev[5], to_dev(pos), to_dev(seq), kc, vc,
-                                  1e-6, H, HKV, D, return_kv=True, rope_pos=to_dev(rpos))
+                                  1e-6, H, HKV, D, return_kv=True, rope_pos=to_dev(rpos), qkv_out=raw)
     qkv = R.linear_fused(x, wq).view(M, H + 2 * HKV, D)
     rp = rpos.long()
     qr = R.qk_norm_rope_fused(qkv[:, :H], qw, cos[rp], sin[rp], 1e-6)
@@ -688,6 +690,7 @@ def test_linear_qkv_rope(M, tables):
     assert torch.equal(kc.cpu()[seq.long(), pos.long()], k.cpu()) and torch.equal(vc.cpu()[seq.long(), pos.long()], v.cpu())
     # the unfused pair on the same device: the same values up to the norm's summation order
     qkv_d = ops.linear(dev[0], dev[1])
+    assert torch.equal(raw, qkv_d)  # the kept unrotated projection is the plain product, bit for bit
     q2, k2, v2 = ops.qkv_rope_cache(qkv_d, dev[2], dev[3], dev[4], dev[5], to_dev(pos), None, None, None, 1e-6, H, HKV,
                                     D, return_kv=True, rope_pos=to_dev(rpos))
     assert torch.equal(v2, v)

@@ -80,7 +80,7 @@ SIGNATURES = {
     "vk_timestamp": [_P, _I64, _P],
     "vk_timestamp_rate_khz": [ctypes.POINTER(_I64)],
     "vk_linear_qkv_rope": [_P, _P, _I64, _I32, _P, _P, _I32, _F, _P, _P, _I32, _I64, _P, _P, _P, _P, _I64, _P, _P, _I64, _I64,
-                           _I64, _I64, _P, _P, _I64, _I32, _I32, _I32, _P],
+                           _I64, _I64, _P, _P, _I64, _P, _I32, _I32, _I32, _P],
 }
 
 _lock = threading.Lock()

@@ -99,6 +99,7 @@ struct GbQkv {
   int64_t stride_cb, stride_cs, cache_rows, cache_len;
   bf16_t *ko, *vo;  // k / v head h of row t at ko + t kv_ld + 64 h (NULL: none)
   int64_t kv_ld;
+  bf16_t *raw;      // the product itself, rounded to bf16, rows [M, N] before the QK-norm and rotation (NULL: none)
   int H, HKV;
   // GB_RESID
   const float *bias;  // [N] or NULL
@@ -453,6 +454,14 @@ __global__ __launch_bounds__(128 * GW, 4 / GW) void gemm_big_kernel(
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[i][e] = round_bf(acc[i][j][e]);
+        if (qa.raw != nullptr && qcol0 < N) {  // the unrotated projection, as the plain product stores it
+          const int64_t rrow = qrow0 + 16 * j + fr;
+          if (rrow < M)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              *reinterpret_cast<u32x2 *>(qa.raw + rrow * N + qcol0 + 16 * i + 4 * fg) =
+                  u32x2{pack_bf(v[i][0], v[i][1]), pack_bf(v[i][2], v[i][3])};
+        }
         if (hd < qa.H + qa.HKV) {  // q or k head: QK-norm, then the rotation
           // the next group's table entries go out before this group's arithmetic
           if (j + 1 < 8) qk_tables(j + 1, qk_c[(j + 1) & 1], qk_s[(j + 1) & 1]);
@@ -627,8 +636,8 @@ extern "C" int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32
                                   int32_t table_dtype, int64_t table_rows, const int32_t *pos, const int32_t *rope_pos,
                                   const int32_t *seq, void *q, int64_t q_ld, void *k_cache, void *v_cache,
                                   int64_t stride_cb, int64_t stride_cs, int64_t cache_rows, int64_t cache_len,
-                                  void *k_out, void *v_out, int64_t kv_ld, int32_t n_heads, int32_t n_kv_heads,
-                                  int32_t head_dim, void *stream) {
+                                  void *k_out, void *v_out, int64_t kv_ld, void *qkv_out, int32_t n_heads,
+                                  int32_t n_kv_heads, int32_t head_dim, void *stream) {
   VK_CHECK_ARG(x && w && cos_t && sin_t && q, "linear_qkv_rope: null pointer");
   VK_CHECK_ARG(head_dim == 64, "linear_qkv_rope: built for head_dim 64 (got %d)", head_dim);
   VK_CHECK_ARG(n_heads > 0 && n_kv_heads > 0, "linear_qkv_rope: bad head counts");
@@ -649,6 +658,7 @@ extern "C" int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32
   VK_CHECK_ARG(q_ld % 8 == 0 && kv_ld % 8 == 0 && stride_cb % 8 == 0 && stride_cs % 8 == 0,
                "linear_qkv_rope: row strides must be multiples of 8 elements");
   VK_CHECK_ARG(vk_aligned16(cos_t) && vk_aligned16(sin_t), "linear_qkv_rope: rotary tables must be 16-byte aligned");
+  VK_CHECK_ARG(qkv_out == nullptr || vk_aligned16(qkv_out), "linear_qkv_rope: qkv_out must be 16-byte aligned");
   VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w) && vk_aligned16(q) && (k_cache == nullptr || (vk_aligned16(k_cache) &&
                vk_aligned16(v_cache))) && (k_out == nullptr || (vk_aligned16(k_out) && vk_aligned16(v_out))),
                "linear_qkv_rope: pointers must be 16-byte aligned");
@@ -675,8 +685,10 @@ extern "C" int vk_linear_qkv_rope(const void *x, const void *w, int64_t M, int32
   qa.ko = static_cast<bf16_t *>(k_out);
   qa.vo = static_cast<bf16_t *>(v_out);
   qa.kv_ld = kv_ld;
+  qa.raw = static_cast<bf16_t *>(qkv_out);
   qa.H = n_heads;
   qa.HKV = n_kv_heads;
+  qa.resid_in = nullptr;
   const auto xb = static_cast<const bf16_t *>(x), wb = static_cast<const bf16_t *>(w);
   const int rc = norm_w_dtype == VK_DTYPE_F32 ? launch_big<GB_QKV_W32>(xb, wb, nullptr, M, N, K, qa, VK_STREAM(stream))
                  : qa.table_f32               ? launch_big<GB_QKV>(xb, wb, nullptr, M, N, K, qa, VK_STREAM(stream))

@@ -323,8 +323,8 @@ class DoradoEncoder:
             # Wqkv with the rotary embedding in its epilogue: q, k (rotated) and v back into the packed rows
             call("vk_linear_qkv_rope", ptr(x), ptr(Lw["wqkv"]), M, C, ptr(None), ptr(None), BF, 0.0, ptr(self.cos),
                  ptr(self.sin), _lib.VK_DTYPE_F32, self.cos.shape[0], ptr(plan.rope_pos), ptr(None), ptr(None),
-                 ptr(qkv), 3 * C, ptr(None), ptr(None), 0, 0, 0, 0, ptr(qkv[:, C:]), ptr(qkv[:, 2 * C:]), 3 * C, H, H,
-                 hd, st)
+                 ptr(qkv), 3 * C, ptr(None), ptr(None), 0, 0, 0, 0, ptr(qkv[:, C:]), ptr(qkv[:, 2 * C:]), 3 * C,
+                 ptr(None), H, H, hd, st)
             call("vk_window_attention", ptr(qkv), 3 * C, ptr(plan.cu), ptr(plan.plan), plan.n_blocks, n,
                  plan.max_frames, H, hd, ptr(None), ptr(None), 0, self.window[0], self.window[1], ptr(o), C, st)
             # out_proj: bias + DeepNorm residual in the product's epilogue (x in place, row sums of squares out),

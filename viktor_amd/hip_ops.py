@@ -99,13 +99,15 @@ def qkv_rope_cache(qkv, q_norm_w, k_norm_w, cos, sin, pos, seq, k_cache, v_cache
 
 
 def linear_qkv_rope(x, w, q_norm_w, k_norm_w, cos, sin, pos, seq, k_cache, v_cache, eps, n_heads, n_kv_heads,
-                    head_dim, return_kv=False, rope_pos=None, q_out=None, kv_out=None):
+                    head_dim, return_kv=False, rope_pos=None, q_out=None, kv_out=None, qkv_out=None):
     """The Wqkv product with qkv_rope_cache fused into its epilogue: x [n, K] @ w [(H + 2 Hkv) D, K]^T, then
     per-head QK-norm (q_norm_w / k_norm_w; both None: none) and RoPE at pos (or rope_pos) on the q and k heads,
     q to [n, H, D], k / v to the cache rows (seq, pos) and / or packed [n, Hkv, D] (return_kv). The rounding
     points of linear + qkv_rope_cache (viktor/triton_ops.py:43-108, 138-146). q_out / kv_out: caller's buffers
     (q_out [n, >= H D] rows; kv_out = (k, v) [n, >= Hkv D] rows, any row stride). fp32 norm weights (with fp32
-    tables): the autocast forward's QK-norm with fp32 master weights (viktor/decoder.py:63-67 under autocast)."""
+    tables): the autocast forward's QK-norm with fp32 master weights (viktor/decoder.py:63-67 under autocast).
+    qkv_out: a bf16 [n, (H + 2 Hkv) D] buffer that also receives the unrotated product (as linear(x, w) returns
+    it), for the QK-norm + RoPE backward."""
     require_device(x, "linear_qkv_rope")
     n, K = x.shape
     H, HKV, D = n_heads, n_kv_heads, head_dim
@@ -135,6 +137,8 @@ def linear_qkv_rope(x, w, q_norm_w, k_norm_w, cos, sin, pos, seq, k_cache, v_cac
     else:
         _require(return_kv, "linear_qkv_rope: nowhere to write k/v")
         sb = ss = rows = clen = 0
+    _require(qkv_out is None or (qkv_out.dtype == BF16 and qkv_out.shape == (n, (H + 2 * HKV) * D)
+                                 and qkv_out.is_contiguous()), "linear_qkv_rope: qkv_out bf16 [n, (H + 2 Hkv) D]")
     tdt = VK_DTYPE_F32 if cos.dtype == torch.float32 else VK_DTYPE_BF16
     _require((q_norm_w is None) == (k_norm_w is None), "linear_qkv_rope: q and k norm weights go together")
     wdt = VK_DTYPE_BF16
@@ -145,7 +149,7 @@ def linear_qkv_rope(x, w, q_norm_w, k_norm_w, cos, sin, pos, seq, k_cache, v_cac
         _require(wdt == VK_DTYPE_BF16 or tdt == VK_DTYPE_F32, "linear_qkv_rope: fp32 norm weights need fp32 tables")
     call("vk_linear_qkv_rope", ptr(x), ptr(w), n, K, ptr(q_norm_w), ptr(k_norm_w), wdt, float(eps), ptr(cos), ptr(sin), tdt,
          cos.shape[0], ptr(pos), ptr(rope_pos), ptr(seq), ptr(q), q.stride(0), ptr(k_cache), ptr(v_cache), sb, ss,
-         rows, clen, ptr(k), ptr(v), 0 if k is None else k.stride(0), H, HKV, D, stream_handle())
+         rows, clen, ptr(k), ptr(v), 0 if k is None else k.stride(0), ptr(qkv_out), H, HKV, D, stream_handle())
     return (q, k, v) if return_kv else q
 
 

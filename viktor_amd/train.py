@@ -182,9 +182,11 @@ class _DecoderStack(torch.autograd.Function):
         for i in range(L):
             wa, wqkv, wqn, wkn, wo, wm, wgu, wd = w[8 * i:8 * i + 8]
             x_in = x
-            qkv = ops.linear(h, wqkv)
-            q, k, v = ops.qkv_rope_cache(qkv, wqn, wkn, cos, sin, rpos, None, None, None, eps, H, HKV, D,
-                                         return_kv=True)
+            # the product, then QK-norm + RoPE in its epilogue (the scoring forward's kernel), keeping the unrotated
+            # projection for the backward
+            qkv = torch.empty(N, wqkv.shape[0], dtype=BF16, device=x.device)
+            q, k, v = ops.linear_qkv_rope(h, wqkv, wqn, wkn, cos, sin, rpos, None, None, None, eps, H, HKV, D,
+                                          return_kv=True, qkv_out=qkv)
             lse = torch.empty(N, H, dtype=torch.float32, device=x.device)
             o = ops.varlen_attention(q, k, v, plan.attn, lse=lse)
             x_mid, h2 = _residual_norm(x_in, o.view(N, H * D), wo, wm, eps)
