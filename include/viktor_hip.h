@@ -80,13 +80,14 @@ int vk_qkv_rope_cache(const void *qkv, const void *q_norm_w, const void *k_norm_
  * y[M, N] = x[M, K] @ w[N, K]^T on bf16 MFMA with fp32 accumulation; y is bf16 (out_dtype
  * VK_DTYPE_BF16) or fp32 (VK_DTYPE_F32).
  * swiglu != 0: w is gate_up [2N, K] and y[M, N] = bf16(bf16(silu(bf16(x w_gate^T))) * bf16(x w_up^T)),
- * the rounding points of the unfused linear + SwiGLU path.
+ * the rounding points of the unfused linear + SwiGLU path; gu_out (NULL: none, swiglu only) then also receives
+ * the gate | up product rows [M, 2N] in bf16, as the plain product stores them (the SwiGLU backward's operand).
  * Requires K % 32 == 0 and 16-byte aligned x, w.
  * Replaces linear (viktor/triton_ops.py:111-146), swiglu (212-229) and the F.linear / nn.Linear
  * projections of viktor/fast_decoder.py:39,56-57 and viktor/decoder.py:58-59,114-115,163-164.
  */
 int vk_linear(const void *x, const void *w, void *y, int64_t M, int32_t N, int32_t K, int32_t swiglu,
-              int32_t out_dtype, void *stream);
+              int32_t out_dtype, void *gu_out, void *stream);
 
 /*
  * out[n, F] = bf16(bf16(silu(gate)) * up) for gu[n, 2F] = [gate | up] (bf16).

@@ -43,11 +43,11 @@ def test_library_loads_and_reports_version():
 def test_argument_errors_return_status_without_device_work():
     """Invalid arguments are rejected on the host before any launch (null pointers / bad sizes)."""
     lib = _lib.load()
-    rc = lib.vk_linear(None, None, None, 4, 8, 32, 0, 0, None)
+    rc = lib.vk_linear(None, None, None, 4, 8, 32, 0, 0, None, None)
     assert rc == 1 and b"null" in lib.vk_last_error()
     buf = ctypes.create_string_buffer(64)
     p = ctypes.cast(buf, ctypes.c_void_p)
-    rc = lib.vk_linear(p, p, p, 4, 8, 30, 0, 0, None)  # K % 32 != 0
+    rc = lib.vk_linear(p, p, p, 4, 8, 30, 0, 0, None, None)  # K % 32 != 0
     assert rc == 1 and b"K" in lib.vk_last_error()
     rc = lib.vk_decode_attention(p, p, p, p, None, 4, p, 4, 8, 2, 128, 128, 128, 16, None, 0, None)  # head_dim 128
     assert rc == 3

@@ -158,6 +158,10 @@ def test_linear_swiglu(M):
     # the standalone SwiGLU op on the unfused GEMM output agrees (8 columns per thread: F % 8 == 0)
     gu = ops.linear(to_dev(x, BF), to_dev(w, BF))
     assert bf_close(ops.swiglu(gu), ref, ulps=4, atol=1e-4)[0]
+    # gu_out: the same SwiGLU rows, and the gate | up rows of the plain product, bit for bit
+    keep = torch.empty(M, 2 * Fd, dtype=BF, device=DEV)
+    y2 = ops.linear(to_dev(x, BF), to_dev(w, BF), swiglu=True, gu_out=keep)
+    assert torch.equal(y2, y) and torch.equal(keep, gu)
 
 
 def test_swiglu_op_widths():

@@ -215,6 +215,26 @@ def test_decoder_param_grads_pos_scale():
     print(_param_grads_vs_oracle(1, [40, 65], 17, seed=41, pos_scale=2))
 
 
+@pytest.mark.parametrize("B,P,T", [(1, 200, 64), (4, 2048, 256)])
+def test_train_logits_equal_scoring_logits(B, P, T):
+    """The update's differentiable forward (train_logits) and the scoring forward (Basecaller.logits, the old
+    policy's log-probs) are one function in the reference (scripts/gspo.py:345-347, 471-477), so a first update
+    step with unchanged weights sees a sequence ratio of exactly 1. Here they run the same kernels at the same
+    rounding points: bit-equal logits, below the large-product row count (small-M products) and above it."""
+    from viktor_amd.synthetic import frames, make_model
+    m = make_model(1, n_layers=2, seed=11, norm_jitter=0.1, bias_jitter=0.1).to(DEV)
+    g = gen(12)
+    fr = frames(B, P, 512, seed=13).to(DEV)
+    pl = torch.full((B,), P, device=DEV)
+    pl[0] = P - 37  # a ragged window
+    tok = torch.randint(3, 7, (B, T), generator=g).to(DEV)
+    with torch.no_grad():
+        z_train = TR.train_logits(m, fr, tok, pl)
+        z_score = m.logits(fr, tok, pl)
+    assert z_train.shape == z_score.shape == (B, T, 7)
+    assert torch.equal(z_train, z_score)
+
+
 def test_hip_adamw_update_changes_params_in_place():
     """HipAdamW: parameters become views of one flat buffer, a step moves them and keeps the module's
     tensors (the inference copy syncs from them by copy_)."""

@@ -32,7 +32,7 @@ SIGNATURES = {
     "vk_embed_rmsnorm": [_P, _P, _I64, _P, _P, _P, _I64, _I32, _F, _P],
     "vk_qkv_rope_cache": [_P, _P, _P, _I32, _P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P,
                           _I64, _F, _I32, _I32, _I32, _P],
-    "vk_linear": [_P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P],
+    "vk_linear": [_P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P],
     "vk_swiglu": [_P, _P, _I64, _I32, _P],
     "vk_decode_attention": [_P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _I32, _I32, _I64, _I64, _I64, _P, _I64, _P],
     "vk_decode_attention_workspace": [_I64, _I32, _I64, ctypes.POINTER(_I64)],

@@ -191,14 +191,17 @@ static void dispatch_gemm(const bf16_t *x, const bf16_t *w, void *y, int64_t M, 
 
 int gemm_big(const bf16_t *x, const bf16_t *w, void *y, int64_t M, int N, int K, bool swiglu, bool out_f32,
              hipStream_t s);
+int gemm_big_swiglu_keep(const bf16_t *x, const bf16_t *w, void *y, bf16_t *gu, int64_t M, int N, int K,
+                         hipStream_t s);
 
 }  // namespace vk
 
 using namespace vk;
 
 extern "C" int vk_linear(const void *x, const void *w, void *y, int64_t M, int32_t N, int32_t K, int32_t swiglu,
-                         int32_t out_dtype, void *stream) {
+                         int32_t out_dtype, void *gu_out, void *stream) {
   VK_CHECK_ARG(x && w && y, "linear: null pointer");
+  VK_CHECK_ARG(gu_out == nullptr || swiglu, "linear: gu_out goes with the SwiGLU epilogue");
   VK_CHECK_ARG(M >= 0 && N > 0 && K > 0 && K % 32 == 0, "linear: need K %% 32 == 0 (M=%lld N=%d K=%d)",
                static_cast<long long>(M), N, K);
   VK_CHECK_ARG(vk_aligned16(x) && vk_aligned16(w), "linear: x and w must be 16-byte aligned");
@@ -210,10 +213,18 @@ extern "C" int vk_linear(const void *x, const void *w, void *y, int64_t M, int32
   const auto ws = static_cast<const bf16_t *>(w);
   // large M: the direct-to-LDS pipeline of gemm_big (SwiGLU included: 778 against 626 TFLOP/s for the 128 x 64
   // tile kernel below at M = 131072)
-  if (M >= 4096 && K % 64 == 0 && N % 8 == 0 && vk_aligned16(y)) {
-    const int rc = gemm_big(xs, ws, y, M, N, K, swiglu != 0, out_dtype == VK_DTYPE_F32, VK_STREAM(stream));
+  if (M >= 4096 && K % 64 == 0 && N % 8 == 0 && vk_aligned16(y) && (gu_out == nullptr || vk_aligned16(gu_out))) {
+    const int rc = gu_out != nullptr
+                       ? gemm_big_swiglu_keep(xs, ws, y, static_cast<bf16_t *>(gu_out), M, N, K, VK_STREAM(stream))
+                       : gemm_big(xs, ws, y, M, N, K, swiglu != 0, out_dtype == VK_DTYPE_F32, VK_STREAM(stream));
     if (rc != VK_OK) return rc;
     return launch_status("linear");
+  }
+  if (gu_out != nullptr) {  // smaller M: the gate | up rows from the plain product, then the SwiGLU product
+    if (K % 64 == 0)
+      dispatch_gemm<64>(xs, ws, gu_out, M, 2 * N, K, false, false, VK_STREAM(stream));
+    else
+      dispatch_gemm<32>(xs, ws, gu_out, M, 2 * N, K, false, false, VK_STREAM(stream));
   }
   if (K % 64 == 0)
     dispatch_gemm<64>(xs, ws, y, M, N, K, swiglu != 0, out_dtype == VK_DTYPE_F32, VK_STREAM(stream));

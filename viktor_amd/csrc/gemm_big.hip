@@ -520,16 +520,26 @@ __global__ __launch_bounds__(128 * GW, 4 / GW) void gemm_big_kernel(
         // silu(g) = g / (1 + e^-g) as g times the hardware reciprocal (1 ulp) instead of the IEEE division: the
         // epilogue's VALU work is on this product's critical path (the product ~5% faster at the prefill shape);
         // 0.007% of the outputs then differ from the division's by one bf16 ulp
+        // qa.raw: the gate | up product rows [M, 2 N] as the plain product stores them (the backward's operand)
+        const int64_t grow = qrow0 + 16 * j + fr;
+        const bool keep = qa.raw != nullptr && grow < M && qcol0 < N;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-          float o[4];
+          float o[4], gt4[4], up4[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float gt = round_bf(acc[i][j][e]);
             const float up = round_bf(acc[i + 2][j][e]);
+            gt4[e] = gt;
+            up4[e] = up;
             o[e] = round_bf(gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt))) * up;
           }
           *reinterpret_cast<u32x2 *>(rowp + (16 * i + 4 * fg) * 2) = u32x2{pack_bf(o[0], o[1]), pack_bf(o[2], o[3])};
+          if (keep) {
+            bf16_t *gr = qa.raw + grow * (2 * static_cast<int64_t>(N)) + qcol0 + 16 * i + 4 * fg;
+            *reinterpret_cast<u32x2 *>(gr) = u32x2{pack_bf(gt4[0], gt4[1]), pack_bf(gt4[2], gt4[3])};
+            *reinterpret_cast<u32x2 *>(gr + N) = u32x2{pack_bf(up4[0], up4[1]), pack_bf(up4[2], up4[3])};
+          }
         }
       } else {
 #pragma unroll
@@ -625,6 +635,14 @@ int gemm_big(const bf16_t *x, const bf16_t *w, void *y, int64_t M, int N, int K,
   if (swiglu) return launch_big<GB_SWIGLU>(x, w, y, M, N, K, none, s);
   if (out_f32) return launch_big<GB_F32>(x, w, y, M, N, K, none, s);
   return launch_big<GB_BF16>(x, w, y, M, N, K, none, s);
+}
+
+// The SwiGLU product that also stores its gate | up rows [M, 2 N] to gu (for vk_linear's gu_out).
+int gemm_big_swiglu_keep(const bf16_t *x, const bf16_t *w, void *y, bf16_t *gu, int64_t M, int N, int K,
+                         hipStream_t s) {
+  GbQkv keep{};
+  keep.raw = gu;
+  return launch_big<GB_SWIGLU>(x, w, y, M, N, K, keep, s);
 }
 
 }  // namespace vk

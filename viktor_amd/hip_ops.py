@@ -204,9 +204,10 @@ def rmsnorm_f32(x, w, eps, out=None):
     return h
 
 
-def linear(x, w, swiglu=False, out_dtype=None, out=None):
+def linear(x, w, swiglu=False, out_dtype=None, out=None, gu_out=None):
     """x [M, K] @ w[N, K]^T on bf16 MFMA. swiglu: w is gate_up [2F, K] and the result silu(gate) * up
-    [M, F]. out_dtype: torch.float32 for unrounded logits. Reference: viktor/triton_ops.py:138-146
+    [M, F]; gu_out (swiglu only: a bf16 [M, 2F] buffer) also receives the gate | up product itself.
+    out_dtype: torch.float32 for unrounded logits. Reference: viktor/triton_ops.py:138-146
     (also serves the F.linear calls of the prefill path)."""
     require_device(x, "linear")
     _require(x.dim() == 2 and w.dim() == 2 and x.shape[1] == w.shape[1], "linear: shapes")
@@ -221,8 +222,10 @@ def linear(x, w, swiglu=False, out_dtype=None, out=None):
         out = torch.empty(M, N, dtype=odt, device=x.device)
     else:
         _require(out.shape == (M, N) and out.dtype == odt and out.is_contiguous(), "linear: out buffer")
+    _require(gu_out is None or (swiglu and gu_out.dtype == BF16 and gu_out.shape == (M, 2 * N)
+                                and gu_out.is_contiguous()), "linear: gu_out bf16 [M, 2F] with swiglu")
     call("vk_linear", ptr(x), ptr(w), ptr(out), M, N, K, int(bool(swiglu)),
-         VK_DTYPE_F32 if odt == torch.float32 else VK_DTYPE_BF16, stream_handle())
+         VK_DTYPE_F32 if odt == torch.float32 else VK_DTYPE_BF16, ptr(gu_out), stream_handle())
     return out
 
 

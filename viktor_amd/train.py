@@ -190,8 +190,9 @@ class _DecoderStack(torch.autograd.Function):
             lse = torch.empty(N, H, dtype=torch.float32, device=x.device)
             o = ops.varlen_attention(q, k, v, plan.attn, lse=lse)
             x_mid, h2 = _residual_norm(x_in, o.view(N, H * D), wo, wm, eps)
-            gu = ops.linear(h2, wgu)
-            g = ops.swiglu(gu)
+            # SwiGLU in the product's epilogue (the scoring forward's kernel), keeping gate | up for the backward
+            gu = torch.empty(N, wgu.shape[0], dtype=BF16, device=x.device)
+            g = ops.linear(h2, wgu, swiglu=True, gu_out=gu)
             w_next = w[8 * (i + 1)] if i + 1 < L else w[8 * L]
             x, h_next = _residual_norm(x_mid, g, wd, w_next, eps)
             saved.append((x_in, h, qkv, q, k, v, o, lse, x_mid, h2, gu, g))
