@@ -164,7 +164,10 @@ _NORMS = ("attn_norm.weight", "attn.q_norm.weight", "attn.k_norm.weight", "mlp_n
 class _DecoderStack(torch.autograd.Function):
     """x [N, d] fp32 packed rows -> final-normed hidden of the token rows [n_tok, d] bf16, with the rounding
     points of FastDecoder.teacher_forced (torch.autocast bf16 over fp32 master weights): products on bf16 weights,
-    the RMSNorms (QK-norm included) on the fp32 weights, an fp32 residual stream."""
+    the RMSNorms (QK-norm included) on the fp32 weights, an fp32 residual stream. The forward runs the same
+    kernels as teacher_forced (so its rows equal the scoring forward's bit for bit) and keeps what the backward
+    needs: each layer's input and middle stream (written out of place), the unrotated Wqkv product and the
+    gate | up rows."""
 
     @staticmethod
     def forward(ctx, x, meta, *params):
