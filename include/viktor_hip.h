@@ -415,7 +415,7 @@ int vk_colsum(const float *part, float *out, int32_t rows, int32_t cols, int32_t
  * attention's input gradients), RoPE rows rope_pos [n] of cos/sin [table_rows, 32]. Writes dqkv [n, (H + 2 HKV) 64]
  * bf16 (q / k heads through the rotation and the 64-wide norm, v heads copied) and dw_part
  * [vk_rmsnorm_backward_blocks(n), 128] fp32 (q-norm weight partials 0..63, k-norm 64..127). D = 64. Norm weights
- * bf16 or fp32 per norm_w_dtype.
+ * bf16 or fp32 per norm_w_dtype. Every pointer 16-byte aligned.
  */
 int vk_qknorm_rope_backward(const void *qkv, const void *q_norm_w, const void *k_norm_w, int32_t norm_w_dtype,
                             const void *cos_t, const void *sin_t, int32_t table_dtype, int64_t table_rows, const int32_t *rope_pos,

@@ -104,16 +104,21 @@ def test_rmsnorm_backward_fp32_stream():
         assert torch.equal(dxb, dx.to(BF))  # the bf16 copy is the tensor cast of dx, bit for bit
 
 
-@pytest.mark.parametrize("wdtype", ["bf16", "f32"])
-def test_qknorm_rope_backward(wdtype):
+@pytest.mark.parametrize("wdtype,tdtype,n,H,HKV", [
+    ("bf16", "f32", 50, 8, 2), ("f32", "f32", 50, 8, 2), ("f32", "bf16", 3001, 8, 2), ("bf16", "bf16", 1, 8, 2),
+    ("f32", "f32", 77, 4, 1)])
+def test_qknorm_rope_backward(wdtype, tdtype, n, H, HKV):
+    """The norm + rotation backward vs fp32 autograd: both weight and table types, one row, a row count whose
+    (row, head) items take several sweeps of the grid and end inside a sweep (3001 x 12), and run-time head counts."""
     g = gen(6)
-    n, H, HKV = 50, 8, 2
     qkv = (torch.randn(n, (H + 2 * HKV) * 64, generator=g) * 2).to(BF)
     wq = (torch.rand(64, generator=g) + 0.5)
     wk = (torch.rand(64, generator=g) + 0.5)
     if wdtype == "bf16":
         wq, wk = wq.to(BF), wk.to(BF)
     cos, sin = R.rope_tables(64, 4096, 1e6)
+    if tdtype == "bf16":
+        cos, sin = cos.to(BF), sin.to(BF)
     rpos = torch.randint(0, 4096, (n,), generator=g).int()
     dq = torch.randn(n, H, 64, generator=g)
     dk = torch.randn(n, HKV, 64, generator=g)
@@ -122,7 +127,7 @@ def test_qknorm_rope_backward(wdtype):
     q = x[:, :H].clone().requires_grad_(True)
     k = x[:, H:H + HKV].clone().requires_grad_(True)
     wqq, wkk = wq.float().requires_grad_(True), wk.float().requires_grad_(True)
-    c, s = cos[rpos.long()], sin[rpos.long()]
+    c, s = cos[rpos.long()].float(), sin[rpos.long()].float()
     loss = (R.apply_rope(F.rms_norm(q, (64,), wqq, 1e-6), c, s) * dq).sum() + \
            (R.apply_rope(F.rms_norm(k, (64,), wkk, 1e-6), c, s) * dk).sum()
     loss.backward()

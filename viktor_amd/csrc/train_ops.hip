@@ -119,12 +119,17 @@ __global__ __launch_bounds__(256) void colsum_kernel(const float *__restrict__ p
   }
 }
 
-// One wavefront per row, lane = dim of a 64-wide head: q heads 0..H-1 and k heads (norm + RoPE backward from
-// dq / dk [n, H|HKV, 64] fp32), v heads (dv passed through). qkv [n, (H + 2 HKV) 64] bf16 is the forward's
-// projection output, cos/sin [S, 32] fp32 (or bf16) at row position rpos. dw_part [gridDim.x, 128]: q-norm
-// weight gradient partials (0..63) and k-norm (64..127).
-// HT / HKVT > 0: the head counts as compile-time constants (the decoder's 8 / 2), so the head loops unroll and
-// every head's loads and reductions of a row are in flight together; 0: the run-time H / HKV.
+// The (row, head) items of qkv [n, (H + 2 HKV) 64] bf16 (the forward's projection output), flattened as
+// row (H + 2 HKV) + head: q heads 0..H-1 and k heads get the norm + RoPE backward from dq / dk [n, H|HKV, 64] fp32,
+// v heads pass dv through (rounded to bf16). cos/sin [S, 32] fp32 (or bf16) at row position rpos.
+// Eight lanes per item: lane j of a group owns dims 8 j .. 8 j + 7 (16-byte loads and stores; it loads its
+// rotation partners, dims d ^ 32, itself), so a wavefront takes 8 items at a time and a head's two sums over 64
+// dims are 8 lane partials and three lane swaps inside the group. Every lane runs the same code for every kind
+// of head (no divergent branches around the swaps); the kind selects the gradient source and the result.
+// dw_part [gridDim.x, 128]: this workgroup's q-norm weight gradient (0..63) and k-norm (64..127), summed over
+// its items in a fixed order (a lane's items in sequence, the wavefront's 8 groups by lane swaps, the 4
+// wavefronts in order).
+// HT / HKVT > 0: the head counts as compile-time constants (the decoder's 8 / 2); 0: the run-time H / HKV.
 // WT: the norm weights' type (bf16, or the fp32 master weights of the autocast forward).
 template <typename TT, typename WT, int HT, int HKVT>
 __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(
@@ -133,41 +138,104 @@ __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(
     const float *__restrict__ dq, const float *__restrict__ dk, const float *__restrict__ dv,
     bf16_t *__restrict__ dqkv, float *__restrict__ dw_part, int64_t n, int H_rt, int HKV_rt, float eps) {
   const int H = HT > 0 ? HT : H_rt, HKV = HKVT > 0 ? HKVT : HKV_rt;
+  const int NH = H + 2 * HKV;
   __shared__ float red[4][128];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int half = lane >> 5, fi = lane & 31;  // rotation half, frequency index
-  const int NH = H + 2 * HKV;
-  const float wq = ld(qw, lane), wk = ld(kw, lane);
-  float dwq = 0.f, dwk = 0.f;
-  for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wid; row < n; row += static_cast<int64_t>(gridDim.x) * 4) {
-    int64_t p = rpos[row];
-    p = p < 0 ? 0 : (p >= table_rows ? table_rows - 1 : p);
-    const float c = ld(cos_t, p * 32 + fi), s = ld(sin_t, p * 32 + fi);
+  const int j = lane & 7, slot = lane >> 3;
+  const int d0 = 8 * j, dp = d0 ^ 32, fi = d0 & 31;  // own dims, partner dims, rotary frequency index
+  const float rsign = d0 < 32 ? 1.f : -1.f;          // dy1 = c do1 + s do2, dy2 = c do2 - s do1
+  using TV = typename std::remove_cv<TT>::type;
+  using WV = typename std::remove_cv<WT>::type;
+  float wq[8], wk[8], dwq[8], dwk[8];
+  {
+    Raw8<WV> a, b;
+    a.load(qw + d0);
+    b.load(kw + d0);
 #pragma unroll
-    for (int h = 0; h < H + HKV; ++h) {
-      const bool isq = h < H;
-      const float go = isq ? dq[(row * H + h) * 64 + lane] : dk[(row * HKV + (h - H)) * 64 + lane];
-      const float gp = __shfl_xor(go, 32, 64);  // the other half's gradient
-      // out1 = y1 c - y2 s, out2 = y1 s + y2 c  =>  dy1 = c do1 + s do2, dy2 = -s do1 + c do2
-      const float gy = half == 0 ? c * go + s * gp : c * go - s * gp;
-      const float xv = bf2f(qkv[row * NH * 64 + h * 64 + lane]);
-      const float wv = isq ? wq : wk;
-      const float ss = wave_sum(xv * xv);
-      const float dot = wave_sum(gy * wv * xv);
-      const float r = rsqrtf(ss * (1.0f / 64) + eps);
-      const float dx = r * gy * wv - xv * (r * r * r * dot * (1.0f / 64));
-      dqkv[row * NH * 64 + h * 64 + lane] = f2bf(dx);
-      if (isq)
-        dwq += gy * xv * r;
-      else
-        dwk += gy * xv * r;
+    for (int e = 0; e < 8; ++e) {
+      wq[e] = a.get(e);
+      wk[e] = b.get(e);
+      dwq[e] = dwk[e] = 0.f;
+    }
+  }
+  const int64_t total = n * NH;
+  // a wavefront's items of one pass: 8 at t0 + u step (u < QB_U), loaded together before any is computed, so a
+  // pass keeps QB_U items' loads (and their dependent rotary-table loads) in flight per lane
+  constexpr int QB_U = 4;
+  const int64_t step = static_cast<int64_t>(gridDim.x) * 32;  // items per sweep of the grid (4 waves x 8)
+  for (int64_t t0 = (static_cast<int64_t>(blockIdx.x) * 4 + wid) * 8; t0 < total; t0 += QB_U * step) {
+    bool live[QB_U], isq[QB_U], isk[QB_U];
+    int64_t obase[QB_U];
+    Raw8<float> go[QB_U], gp[QB_U];
+    Raw8<bf16_t> xr[QB_U];
+    int64_t p[QB_U];
+#pragma unroll
+    for (int u = 0; u < QB_U; ++u) {
+      live[u] = t0 + u * step + slot < total;
+      const int64_t t = live[u] ? t0 + u * step + slot : total - 1;
+      const int64_t row = t / NH;
+      const int h = static_cast<int>(t - row * NH);
+      isq[u] = h < H;
+      isk[u] = !isq[u] && h < H + HKV;
+      const float *g = isq[u] ? dq + (row * H + h) * 64
+                              : (isk[u] ? dk + (row * HKV + (h - H)) * 64 : dv + (row * HKV + (h - H - HKV)) * 64);
+      go[u].load(g + d0);
+      gp[u].load(g + dp);
+      obase[u] = row * NH * 64 + h * 64 + d0;
+      xr[u].load(qkv + obase[u]);
+      p[u] = rpos[row];
+    }
+    Raw8<TV> cr[QB_U], sr[QB_U];
+#pragma unroll
+    for (int u = 0; u < QB_U; ++u) {
+      const int64_t pc = p[u] < 0 ? 0 : (p[u] >= table_rows ? table_rows - 1 : p[u]);
+      cr[u].load(cos_t + pc * 32 + fi);
+      sr[u].load(sin_t + pc * 32 + fi);
     }
 #pragma unroll
-    for (int h = 0; h < HKV; ++h)
-      dqkv[row * NH * 64 + (H + HKV + h) * 64 + lane] = f2bf(dv[(row * HKV + h) * 64 + lane]);
+    for (int u = 0; u < QB_U; ++u) {
+      float gy[8], xv[8], ss = 0.f, dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        gy[e] = cr[u].get(e) * go[u].get(e) + rsign * (sr[u].get(e) * gp[u].get(e));
+        xv[e] = xr[u].get(e);
+        ss += xv[e] * xv[e];
+        dot += gy[e] * (isq[u] ? wq[e] : wk[e]) * xv[e];
+      }
+      ss = group_sum<8>(ss);
+      dot = group_sum<8>(dot);
+      const float r = rsqrtf(ss * (1.0f / 64) + eps);
+      const float c3 = r * r * r * dot * (1.0f / 64);
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float dx = r * gy[e] * (isq[u] ? wq[e] : wk[e]) - xv[e] * c3;
+        o[e] = (isq[u] || isk[u]) ? dx : go[u].get(e);
+        const float gw = live[u] ? gy[e] * xv[e] * r : 0.f;
+        dwq[e] += isq[u] ? gw : 0.f;
+        dwk[e] += isk[u] ? gw : 0.f;
+      }
+      if (live[u])
+        *reinterpret_cast<u32x4 *>(dqkv + obase[u]) =
+            u32x4{pack_bf(o[0], o[1]), pack_bf(o[2], o[3]), pack_bf(o[4], o[5]), pack_bf(o[6], o[7])};
+    }
   }
-  red[wid][lane] = dwq;
-  red[wid][64 + lane] = dwk;
+  // the 8 groups of the wavefront (lanes j, j + 8, ..., j + 56 own the same dims), then the 4 wavefronts
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) {
+      dwq[e] += __shfl_xor(dwq[e], off, 64);
+      dwk[e] += __shfl_xor(dwk[e], off, 64);
+    }
+  }
+  if (slot == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      red[wid][d0 + e] = dwq[e];
+      red[wid][64 + d0 + e] = dwk[e];
+    }
+  }
   __syncthreads();
   if (threadIdx.x < 128)
     dw_part[static_cast<int64_t>(blockIdx.x) * 128 + threadIdx.x] =
@@ -320,6 +388,9 @@ extern "C" int vk_qknorm_rope_backward(const void *qkv, const void *q_norm_w, co
                    (table_dtype == VK_DTYPE_F32 || table_dtype == VK_DTYPE_BF16) &&
                    (norm_w_dtype == VK_DTYPE_F32 || norm_w_dtype == VK_DTYPE_BF16),
                "qknorm_rope_backward: bad arguments");
+  VK_CHECK_ARG(vk_aligned16(qkv) && vk_aligned16(q_norm_w) && vk_aligned16(k_norm_w) && vk_aligned16(cos_t) &&
+                   vk_aligned16(sin_t) && vk_aligned16(dq) && vk_aligned16(dk) && vk_aligned16(dv) && vk_aligned16(dqkv),
+               "qknorm_rope_backward: pointers must be 16-byte aligned");
   if (n == 0) return VK_OK;
   const unsigned grid = row_grid(n);
   hipStream_t s = VK_STREAM(stream);
