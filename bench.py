@@ -231,19 +231,24 @@ def scoring_config(dev, reps=2):
     """GSPO scoring: 512 sequences x (2048-frame prefix + 700..1024 response tokens), the teacher-forced forward
     of token_logprobs (scripts/gspo.py:340-353), then the sequence-ratio loss and its gradient w.r.t. the
     logits (scripts/gspo.py:459-477), with the fp32 master model and the autocast rounding points the reference
-    scores with (an fp32 residual stream).
-    Algorithmic flops per sequence of n = 2048 + L rows: the projector per frame, 2 x weights per row less the
-    last layer's products for the prefix rows (only the L token rows need logits), causal attention
-    1024 n (n + 1) per layer, the LM head per token."""
+    scores with (an fp32 residual stream). The sequences are a rollout's: 64 windows x 8 samples, each window's
+    frames repeated for its samples (scripts/gspo.py:444). Timed twice: with group_size 8 (each window's prefix
+    run once, the token rows attending to it; log-probs equal to the unshared forward's) and unshared, every
+    window in full as the reference computes it.
+    Algorithmic flops, unshared, per sequence of n = 2048 + L rows: the projector per frame, 2 x weights per row
+    less the last layer's products for the prefix rows (only the L token rows need logits), causal attention
+    1024 n (n + 1) per layer, the LM head per token. Shared: the projector and the prefix rows' products once per
+    window, the prefix rows' causal attention in 7 layers (1024 P (P + 1) each), and per sample its L token rows'
+    products, their attention to P + t + 1 keys (2048 (L P + L (L + 1) / 2) per layer) and the LM head."""
     from viktor_amd import gspo as G
     from viktor_amd.synthetic import scoring_inputs
     gm = _master_model(1, dev)
     B = PREFIXES * GROUP
     seqs, ended = scoring_inputs(B, 700, 1024, k=1, seed=5)
     g = torch.Generator(device=dev).manual_seed(6)
-    fr = torch.randn(B, P, 512, generator=g, device=dev).to(torch.bfloat16)
+    fr = torch.randn(PREFIXES, P, 512, generator=g, device=dev).to(torch.bfloat16).repeat_interleave(GROUP, 0)
     plens = torch.full((B,), P, device=dev)
-    lp, mask = G.token_logprobs(gm, fr, plens, seqs, ended)  # the old policy's log-probs
+    lp, mask = G.token_logprobs(gm, fr, plens, seqs, ended, group_size=GROUP)  # the old policy's log-probs
     old = (lp + 0.05 * torch.randn(lp.shape, generator=g, device=dev)).contiguous()
     nb = torch.tensor([max(len(q), 1) for q in seqs], dtype=torch.float32, device=dev)
     adv = torch.randn(B, generator=g, device=dev)
@@ -251,20 +256,27 @@ def scoring_config(dev, reps=2):
     tin, tgt = tin.to(dev), tgt.clamp(min=0).to(dev).contiguous()
     mask = mask.to(dev)
 
-    def run():  # teacher-forced logits, then log-probs + ratio + clipped loss + dL/dlogits in one kernel
-        logits = gm.logits(fr, tin, plens)
+    def run(group):  # teacher-forced logits, then log-probs + ratio + clipped loss + dL/dlogits in one kernel
+        logits = gm.logits(fr, tin, plens, group_size=group)
         G.ops.gspo_score(logits.contiguous(), tgt, mask, old, nb, adv, 3e-4, 4e-4, grad=True)
 
-    ms = _timed(run, reps)
+    ms = _timed(lambda: run(GROUP), reps)
+    ms_full = _timed(lambda: run(1), reps)
     L = [len(q) + 1 for q in seqs]
-    flops = 0
+    flops = flops_full = 0
     for n_tok in L:
         n = P + n_tok
-        flops += 2 * 2 * 512 * 512 * P + 2 * 3014656 * 8 * n - P * 5242880 + 8 * 1024 * n * (n + 1) + 2 * 512 * 7 * n_tok
-    out = {"sequences": B, "response_tokens": "U[700, 1024]", "ms": round(ms, 2),
-           "tokens_per_s": round(sum(L) / (ms / 1e3), 1), "alg_tflop": round(flops / 1e12, 2),
-           "achieved_tflops": round(flops / (ms / 1e3) / 1e12, 1),
-           "mfma_frac": round(flops / (ms / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        flops_full += 2 * 2 * 512 * 512 * P + 2 * 3014656 * 8 * n - P * 5242880 + 8 * 1024 * n * (n + 1) + 2 * 512 * 7 * n_tok
+        flops += 2 * 3014656 * 8 * n_tok + 8 * 2048 * (n_tok * P + n_tok * (n_tok + 1) // 2) + 2 * 512 * 7 * n_tok
+    flops += PREFIXES * (2 * 2 * 512 * 512 * P + 2 * 3014656 * 8 * P - P * 5242880 + 7 * 1024 * P * (P + 1))
+    tf = flops / (ms / 1e3) / 1e12
+    out = {"sequences": B, "windows": PREFIXES, "group_size": GROUP, "response_tokens": "U[700, 1024]",
+           "ms": round(ms, 2), "tokens_per_s": round(sum(L) / (ms / 1e3), 1), "alg_tflop": round(flops / 1e12, 2),
+           "achieved_tflops": round(tf, 1), "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+           "unshared": {"ms": round(ms_full, 2), "tokens_per_s": round(sum(L) / (ms_full / 1e3), 1),
+                        "alg_tflop": round(flops_full / 1e12, 2),
+                        "mfma_frac": round(flops_full / (ms_full / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                        "note": "every window in full, as the reference scores them"},
            "includes": "projector + teacher-forced 8-layer forward (fp32 master weights, autocast rounding points, "
                        "padded to a multiple of 128 tokens as the reference pads) + LM head + log-probs, ratio, "
                        "clipped loss and dL/dlogits [512, T, 7]"}

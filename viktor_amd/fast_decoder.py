@@ -101,6 +101,52 @@ class PrefillPlan:
         return full, last
 
 
+class SharedPrefixPlan:
+    """Host-side layout of a teacher-forced forward over groups of G sequences that share their prefix rows
+    (a GSPO rollout's repeated windows, scripts/gspo.py:444): group g's pre_lens[g] prefix rows are packed once
+    (back to back, as a PrefillPlan), and every member b = g G + m has T token rows (packed at b T). The token rows
+    attend to their group's prefix keys and their own keys, both kept in a key buffer [B, S, Hkv, D] with
+    S = max(pre_lens) + T: member b's prefix keys at rows 0 .. pre_lens[g] - 1 and its token keys right after,
+    as the window [prefix | tokens] lays them out."""
+
+    def __init__(self, pre_lens, group_size, T, hkv_d, device):
+        pre_lens = [int(p) for p in pre_lens]
+        G, T = int(group_size), int(T)
+        _require(G >= 1 and T > 0 and len(pre_lens) > 0 and all(p > 0 for p in pre_lens), "SharedPrefixPlan: sizes")
+        self.pre_lens, self.G, self.T = pre_lens, G, T
+        self.n_groups = len(pre_lens)
+        self.B = self.n_groups * G
+        self.S = max(pre_lens) + T
+        self.pre = PrefillPlan(pre_lens, device)
+        self.pre_full, _ = self.pre.packed_plans(hkv_d)
+        member_pre = np.repeat(np.asarray(pre_lens, dtype=np.int64), G)
+        self.tok = ops.AttentionPlan([T] * self.B, (member_pre + T).tolist(),
+                                     [b * self.S * hkv_d for b in range(self.B)], device, causal=True)
+        t = np.arange(T, dtype=np.int64)
+        # token rows: key buffer row (member, pre_len + t), which is also the row's position in its window
+        self.pos_tok = torch.from_numpy((member_pre[:, None] + t[None, :]).reshape(-1).astype(np.int32)).to(device)
+        self.seq_tok = torch.from_numpy(np.repeat(np.arange(self.B, dtype=np.int32), T)).to(device)
+        self.pos_pre = torch.from_numpy(np.concatenate([np.arange(p, dtype=np.int32) for p in pre_lens])).to(device)
+        self.equal = len(set(pre_lens)) == 1
+        self.bc_dst = self.bc_src = None
+        if not self.equal:  # member b's buffer row j <- its group's packed prefix row j
+            cu = self.pre.cu
+            dst = np.concatenate([b * self.S + np.arange(member_pre[b]) for b in range(self.B)])
+            src = np.concatenate([cu[b // G] + np.arange(member_pre[b]) for b in range(self.B)])
+            self.bc_dst = torch.from_numpy(dst).to(device)
+            self.bc_src = torch.from_numpy(src).to(device)
+
+    def broadcast(self, kv_pre, buf):
+        """buf [B, S, Hkv, D]: rows 0 .. pre_lens[g] - 1 of every member of group g <- the group's packed prefix
+        rows of kv_pre [n_pre, Hkv, D] (a device copy)."""
+        if self.equal:
+            P = self.pre_lens[0]
+            buf.view(self.n_groups, self.G, self.S, -1)[:, :, :P].copy_(
+                kv_pre.view(self.n_groups, 1, P, -1).expand(-1, self.G, -1, -1))
+        else:
+            buf.view(self.B * self.S, -1)[self.bc_dst] = kv_pre.view(kv_pre.shape[0], -1)[self.bc_src]
+
+
 class FastDecoder:
     """Packed-token forward of a Decoder on the HIP kernels (reference: viktor/fast_decoder.py:17-90)."""
 
@@ -187,13 +233,64 @@ class FastDecoder:
                 x = x[plan.last_idx]
                 q = q[plan.last_idx]
             o = ops.varlen_attention(q, k, v, lastp if last else full, stride_tok=k.stride(0))
-            ss = ops.linear_residual_big(o.reshape(x.shape[0], -1), W(a.o_proj.weight), x)
-            h = ops.rmsnorm_apply(x, ss, F(blk.mlp_norm.weight), eps)
-            g = ops.linear(h, W(blk.gate_up.weight), swiglu=True)
             w_next = layers[i + 1].attn_norm.weight if i + 1 < n_layers else self.dec.norm.weight
-            ss = ops.linear_residual_big(g, W(blk.down.weight), x)
-            h = ops.rmsnorm_apply(x, ss, F(w_next), eps)
+            h = self._tf_block(x, o, blk, w_next)
         return h
+
+    def _tf_block(self, x, o, blk, w_next):
+        """The rest of a teacher-forced layer after its attention output o: x += o Wo^T (fp32 stream, bf16
+        product), the MLP norm, gate_up with SwiGLU, x += down, and the next norm (w_next), which it returns."""
+        W, F, eps = self.w, self.w32, self.cfg.norm_eps
+        ss = ops.linear_residual_big(o.reshape(x.shape[0], -1), W(blk.attn.o_proj.weight), x)
+        h = ops.rmsnorm_apply(x, ss, F(blk.mlp_norm.weight), eps)
+        g = ops.linear(h, W(blk.gate_up.weight), swiglu=True)
+        ss = ops.linear_residual_big(g, W(blk.down.weight), x)
+        return ops.rmsnorm_apply(x, ss, F(w_next), eps)
+
+    def teacher_forced_shared(self, x_pre, x_tok, plan, rope_pre=None, rope_tok=None):
+        """teacher_forced over groups of sequences that share their prefix (plan: a SharedPrefixPlan): x_pre
+        [n_pre, d] fp32 holds each group's prefix rows once, x_tok [B T, d] fp32 every member's token rows. The
+        prefix rows run the layers once per group (the last layer only to its K / V), and each layer's prefix
+        K / V goes to every member's rows of the key buffer, beside the member's own token K / V; the token rows
+        attend to that buffer. Every step of a row is that of teacher_forced over the unshared windows
+        [prefix | tokens]: the products and norms are row by row, and a token row's attention meets the same keys
+        in the same order. So the token rows' hidden states are the unshared forward's, bit for bit wherever both
+        forwards run a product on the same kernel (each product with at least 4096 rows in both). Returns the
+        final-normed hidden of the token rows [B T, d] bf16. rope_pre / rope_tok [n_pre] / [B T] int32: the
+        rotary rows when they are not the positions (prefix row j at j, token t of a member at pre_len + t)."""
+        require_device(x_tok, "FastDecoder.teacher_forced_shared")
+        cfg, layers, W, F = self.cfg, self.dec.layers, self.w, self.w32
+        d = cfg.d_model
+        _require(x_pre.dtype == torch.float32 and x_pre.is_contiguous() and x_pre.shape == (plan.pre.total, d),
+                 "teacher_forced_shared: x_pre fp32 [prefix rows, d]")
+        _require(x_tok.dtype == torch.float32 and x_tok.is_contiguous() and x_tok.shape == (plan.B * plan.T, d),
+                 "teacher_forced_shared: x_tok fp32 [B T, d]")
+        eps = cfg.norm_eps
+        H, HKV, D = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+        cos, sin = (F(t) for t in self._tables())
+        kbuf = torch.empty(plan.B, plan.S, HKV, D, dtype=BF16, device=x_tok.device)
+        vbuf = torch.empty_like(kbuf)
+        n_layers = len(layers)
+        w0 = F(layers[0].attn_norm.weight)
+        hp = ops.rmsnorm_f32(x_pre, w0, eps)
+        ht = ops.rmsnorm_f32(x_tok, w0, eps)
+        for i, blk in enumerate(layers):
+            a = blk.attn
+            wqkv, qn, kn = W(a.qkv_proj.weight), F(a.q_norm.weight), F(a.k_norm.weight)
+            qp, kp, vp = ops.linear_qkv_rope(hp, wqkv, qn, kn, cos, sin, plan.pos_pre, None, None, None, eps, H, HKV,
+                                             D, return_kv=True, rope_pos=rope_pre)
+            plan.broadcast(kp, kbuf)
+            plan.broadcast(vp, vbuf)
+            # the token rows' K / V go straight to their members' buffer rows
+            qt = ops.linear_qkv_rope(ht, wqkv, qn, kn, cos, sin, plan.pos_tok, plan.seq_tok, kbuf, vbuf, eps, H, HKV,
+                                     D, rope_pos=rope_tok)
+            w_next = layers[i + 1].attn_norm.weight if i + 1 < n_layers else self.dec.norm.weight
+            if i + 1 < n_layers:  # the prefix rows feed the next layer's prefix keys
+                op = ops.varlen_attention(qp, kp, vp, plan.pre_full, stride_tok=kp.stride(0))
+                hp = self._tf_block(x_pre, op, blk, w_next)
+            ot = ops.varlen_attention(qt, kbuf, vbuf, plan.tok, stride_tok=kbuf.stride(1))
+            ht = self._tf_block(x_tok, ot, blk, w_next)
+        return ht
 
     def _layers(self, x, pos, seq, cache, attend, return_kv, last_idx=None, rope_pos=None, h=None):
         """x [n, d] residual stream (updated in place); h: its first attention norm when already computed.

@@ -74,13 +74,15 @@ def sampled_mask(targets, seqs, ended, k):
     return mask
 
 
-def token_logprobs(model, frames, plens, seqs, ended):
+def token_logprobs(model, frames, plens, seqs, ended, group_size=1):
     """Teacher-forced log pi of each call's tokens [B, T] (fp32) and the mask of its sampled tokens.
-    Reference: scripts/gspo.py:340-353 (T padded to a multiple of 128)."""
+    Reference: scripts/gspo.py:340-353 (T padded to a multiple of 128). group_size = G > 1: the rollout's G
+    samples of each window sit in consecutive rows and share its frames (scripts/gspo.py:444), so each window's
+    prefix runs once (Basecaller.logits); the log-probs are those of the unshared forward."""
     tokens_in, targets, _ = model.batch(seqs, pad_to=128)
     dev = frames.device
     tokens_in, targets = tokens_in.to(dev), targets.to(dev)
-    logits = model.logits(frames, tokens_in, plens)
+    logits = model.logits(frames, tokens_in, plens, group_size=group_size)
     lp = ops.gspo_score(logits.contiguous(), targets.clamp(min=0).contiguous())["lp"]
     mask = sampled_mask(targets, seqs, ended, model.tokenizer.k)
     return lp, mask

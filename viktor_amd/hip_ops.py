@@ -229,6 +229,24 @@ def linear(x, w, swiglu=False, out_dtype=None, out=None, gu_out=None):
     return out
 
 
+def group_rows_equal(x, group_size):
+    """True when every member x[b] of the groups of group_size consecutive members equals its group's first
+    member bit for bit (x contiguous [B, ...], B a multiple of group_size, x[b] a multiple of 16 bytes). One
+    pass over x on the device, then one flag read back. No reference counterpart: the reference runs every
+    repeated window (scripts/gspo.py:444)."""
+    require_device(x, "group_rows_equal")
+    G = int(group_size)
+    B = x.shape[0]
+    _require(G >= 1 and B % G == 0 and x.is_contiguous(), "group_rows_equal: contiguous [B, ...], B % G == 0")
+    member_bytes = x[0].numel() * x.element_size() if B else 0
+    _require(member_bytes % 16 == 0 and x.data_ptr() % 16 == 0, "group_rows_equal: 16-byte members")
+    if B == 0 or G == 1:
+        return True
+    flag = torch.zeros(1, dtype=torch.int32, device=x.device)
+    call("vk_group_rows_equal", ptr(x), B // G, G, member_bytes, ptr(flag), stream_handle())
+    return int(flag.item()) == 0
+
+
 def swiglu(gu):
     """gu [n, 2F] (gate | up) -> silu(gate) * up [n, F]. Reference: viktor/triton_ops.py:223-229."""
     require_device(gu, "swiglu")

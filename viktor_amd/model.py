@@ -19,7 +19,8 @@ import torch.nn.functional as F
 
 from ._lib import require_device
 from .decoder import Decoder, DecoderConfig
-from .fast_decoder import PrefillPlan
+from . import hip_ops as ops
+from .fast_decoder import PrefillPlan, SharedPrefixPlan
 from .tokenizer import PAD, KmerTokenizer, get_tokenizer
 
 BF16 = torch.bfloat16
@@ -89,24 +90,32 @@ class Basecaller(nn.Module):
         frames.index_copy_(0, torch.from_numpy(dst).to(out.device), out.index_select(0, torch.from_numpy(src).to(out.device)))
         return frames.view(B, P, -1), torch.from_numpy(plens).to(out.device)
 
-    def logits(self, frames, tokens_in, plens=None):
+    def logits(self, frames, tokens_in, plens=None, group_size=1):
         """Teacher forcing from encoder frames [B, P, d_enc]: bf16 logits [B, T, vocab] of every token
         position. plens [B]: real prefix frames per window (default P). Reference: viktor/model.py:55-60, with
         the rounding points it has where scripts/gspo.py:345-347 calls it, under torch.autocast bf16: the
         projector's bf16 output and the token embeddings gathered into an fp32 residual stream
         (viktor/model.py:81-84; fp32 embedding rows from fp32 weights), the decoder on that fp32 stream
-        (FastDecoder.teacher_forced) and the LM head as a bf16 product."""
-        return self.decoder.head(self.hidden(frames, tokens_in, plens)).view(frames.shape[0], tokens_in.shape[1], -1)
+        (FastDecoder.teacher_forced) and the LM head as a bf16 product.
+        group_size = G > 1: consecutive groups of G windows carry the same prefix (a GSPO rollout's repeated
+        windows, scripts/gspo.py:444; checked on the device, ValueError otherwise), which then runs once per group
+        (see hidden())."""
+        return self.decoder.head(self.hidden(frames, tokens_in, plens, group_size)).view(
+            frames.shape[0], tokens_in.shape[1], -1)
 
-    def hidden(self, frames, tokens_in, plens=None):
+    def hidden(self, frames, tokens_in, plens=None, group_size=1):
         """The final-normed hidden state of every token position [B T, d] bf16 (the LM head's operand) of the
-        teacher-forced forward that logits() runs."""
+        teacher-forced forward that logits() runs. group_size = G > 1: the projector and the decoder run each
+        group's prefix once (FastDecoder.teacher_forced_shared) and its members' token rows attend to that
+        prefix's keys; the token rows' results are those of the unshared forward (the same arithmetic per row)."""
         require_device(frames, "Basecaller.hidden")
         B, P = frames.shape[:2]
         T = tokens_in.shape[1]
         dev = frames.device
         plens_h = [P] * B if plens is None else [int(p) for p in plens.tolist()]
         assert all(0 < p <= P for p in plens_h), "plens outside 1..P"
+        if int(group_size) > 1:
+            return self._hidden_shared(frames, tokens_in, plens_h, int(group_size))
         prefix = self.project(frames)                                       # [B, P, d] bf16
         fast = self.decoder.fast()
         emb = fast.w32(self.decoder.embed.weight)[tokens_in.to(dev)]        # [B, T, d] fp32
@@ -136,6 +145,40 @@ class Basecaller(nn.Module):
             rpos = torch.cat([torch.cat([torch.arange(p, device=dev) * s, s * p + torch.arange(T, device=dev)])
                               for p in plens_h]).to(torch.int32)
         return fast.teacher_forced(x, pos, plan, rope_pos=rpos)            # [B * T, d] bf16
+
+    def _hidden_shared(self, frames, tokens_in, plens_h, G):
+        """hidden() over groups of G windows that share their prefix: each group's frames are projected and run
+        through the decoder once, as its members' common prefix."""
+        B, P = frames.shape[:2]
+        T = tokens_in.shape[1]
+        dev = frames.device
+        if B % G:
+            raise ValueError(f"group_size={G}: {B} windows are not whole groups")
+        pre_lens = plens_h[::G]
+        if any(plens_h[b] != pre_lens[b // G] for b in range(B)):
+            raise ValueError(f"group_size={G}: the windows of a group must have the same prefix length")
+        if all(p == P for p in plens_h) and frames.is_contiguous() and (frames[0].numel() * frames.element_size()) % 16 == 0:
+            same = ops.group_rows_equal(frames, G)
+        else:
+            same = all(torch.equal(frames[b:b + G, :p], frames[b:b + 1, :p].expand(G, -1, -1))
+                       for b, p in zip(range(0, B, G), pre_lens))
+        if not same:
+            raise ValueError(f"group_size={G}: the windows of a group must share their prefix frames")
+        d = self.cfg.d_model
+        prefix = self.project(frames[::G].contiguous())                    # [B / G, P, d] bf16, one per group
+        if all(p == P for p in pre_lens):
+            x_pre = prefix.reshape(-1, d).float()
+        else:
+            x_pre = torch.cat([prefix[g, :p] for g, p in enumerate(pre_lens)]).float()
+        fast = self.decoder.fast()
+        x_tok = fast.w32(self.decoder.embed.weight)[tokens_in.to(dev).reshape(-1)]  # [B T, d] fp32
+        plan = SharedPrefixPlan(pre_lens, G, T, self.cfg.n_kv_heads * self.cfg.head_dim, dev)
+        rope_pre = rope_tok = None
+        if self.pos_scale != 1:
+            s = self.pos_scale
+            rope_pre = torch.cat([torch.arange(p, device=dev) * s for p in pre_lens]).to(torch.int32)
+            rope_tok = torch.cat([s * plens_h[b] + torch.arange(T, device=dev) for b in range(B)]).to(torch.int32)
+        return fast.teacher_forced_shared(x_pre, x_tok, plan, rope_pre, rope_tok)  # [B * T, d] bf16
 
     def batch(self, seqs, weights=None, pad_to=1):
         """CPU teacher-forcing tensors: tokens_in, targets [B, T] and target weights [B, T], T padded up to a
