@@ -234,6 +234,20 @@ int vk_varlen_attention(const void *q, const void *k, const void *v, const int32
                         float *lse, void *stream);
 
 /*
+ * vk_varlen_attention with each sequence's first p_lens[i] keys taken from a second buffer: key j < p_lens[i] at
+ * k_prefix + p_off[i] + j * p_stride (+ hk * D), key j >= p_lens[i] at k + k_off[i] + (j - p_lens[i]) * stride_tok,
+ * same for v; k_lens[i] counts both. The sequences of a GSPO group score one window [prefix | own tokens] each
+ * and keep the shared prefix's keys once (scripts/gspo.py:340-353 over the repeated windows of
+ * scripts/gspo.py:444, where the reference recomputes the prefix per sample). No reference counterpart of its
+ * own: the key order is flash_attn_varlen_func's over the window (viktor/fast_decoder.py:68-73).
+ */
+int vk_varlen_attention_prefixed(const void *q, const void *k, const void *v, const int32_t *cu_q,
+                                 const int64_t *k_off, const int32_t *k_lens, const int32_t *plan, int32_t n_blocks,
+                                 int32_t n_seq, int64_t stride_tok, const void *k_prefix, const void *v_prefix,
+                                 const int64_t *p_off, const int32_t *p_lens, int64_t p_stride, void *out,
+                                 int32_t causal, int32_t H, int32_t HKV, int32_t D, float *lse, void *stream);
+
+/*
  * One decode step's token choice and bookkeeping for B sequences (DecodeEngine._select + state update):
  *   z = (logits[b] + bias) (fp32 logits, or bf16-rounded when h/w are given with round_bf16) ;
  *   greedy (temperature <= 0): nxt = first argmax of z;

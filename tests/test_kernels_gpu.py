@@ -407,6 +407,55 @@ def test_varlen_attention_reads_cache_rows():
     assert (out.float().cpu() - ref).abs().max() < 1e-2
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_varlen_attention_prefixed_equals_concatenated_keys(causal):
+    """Each sequence's first p_lens keys from a shared prefix buffer, the rest its own rows: the same bits (out and
+    log-sum-exp) as vk_varlen_attention over the concatenated keys -- prefix lengths off and on the 64-key tiles
+    (tiles straddling the two buffers), two sequences on one prefix, an empty own part, a sequence with no prefix."""
+    torch.manual_seed(31)
+    H, HKV, D = 8, 2, 64
+    pre = [(0, 100), (100, 128), (228, 77)]  # (first row, length) of three prefixes in one packed buffer
+    kp = torch.randn(305, HKV, D).to(BF)
+    vp = torch.randn(305, HKV, D).to(BF)
+    # sequences: (prefix index or None, own keys, queries)
+    seqs = [(0, 150, 150), (0, 40, 40), (1, 0, 0), (2, 300, 200), (None, 90, 90), (1, 64, 1)]
+    if not causal:
+        seqs[2] = (1, 0, 5)  # queries over the prefix keys alone
+    q_lens = [nq for _, _, nq in seqs]
+    own = [no for _, no, _ in seqs]
+    p_lens = [0 if p is None else pre[p][1] for p, _, _ in seqs]
+    p_off = [0 if p is None else pre[p][0] * HKV * D for p, _, _ in seqs]
+    k_lens = [a + b for a, b in zip(p_lens, own)]
+    ko = torch.randn(max(sum(own), 1), HKV, D).to(BF)
+    vo = torch.randn(max(sum(own), 1), HKV, D).to(BF)
+    k_off = list(np.concatenate([[0], np.cumsum(own)[:-1]]) * HKV * D)
+    q = torch.randn(sum(q_lens), H, D).to(BF)
+    dq, dkp, dvp, dko, dvo = (t.to(DEV) for t in (q, kp, vp, ko, vo))
+    plan = ops.AttentionPlan(q_lens, k_lens, k_off, DEV, causal=causal, p_lens=p_lens, p_off=p_off)
+    lse = torch.empty(sum(q_lens), H, dtype=torch.float32, device=DEV)
+    out = ops.varlen_attention(dq, dko, dvo, plan, stride_tok=HKV * D, lse=lse, prefix=(dkp, dvp))
+    # the same keys concatenated per sequence, one buffer
+    kc, vc, c_off, o = [], [], [], 0
+    oo = np.concatenate([[0], np.cumsum(own)])
+    for i, (p, no, _) in enumerate(seqs):
+        parts_k = ([kp[pre[p][0]:pre[p][0] + pre[p][1]]] if p is not None else []) + [ko[oo[i]:oo[i] + no]]
+        parts_v = ([vp[pre[p][0]:pre[p][0] + pre[p][1]]] if p is not None else []) + [vo[oo[i]:oo[i] + no]]
+        kc.append(torch.cat(parts_k))
+        vc.append(torch.cat(parts_v))
+        c_off.append(o * HKV * D)
+        o += k_lens[i]
+    kc, vc = torch.cat(kc).to(DEV), torch.cat(vc).to(DEV)
+    plan_c = ops.AttentionPlan(q_lens, k_lens, c_off, DEV, causal=causal)
+    lse_c = torch.empty_like(lse)
+    out_c = ops.varlen_attention(dq, kc, vc, plan_c, stride_tok=HKV * D, lse=lse_c)
+    assert torch.equal(out, out_c)
+    assert torch.equal(lse, lse_c)
+    ref = _varlen_ref(q, kc.cpu(), vc.cpu(), q_lens, k_lens, causal=causal)
+    assert (out.float().cpu() - ref).abs().max() < 1e-2
+    with pytest.raises(AssertionError, match="prefix tensors go with a prefixed plan"):
+        ops.varlen_attention(dq, kc, vc, plan_c, stride_tok=HKV * D, prefix=(dkp, dvp))
+
+
 def _select_ref(logits, prev, run, bias, tail, homo, homo_stop, T, u, gumbel=False):
     toks, runs, margins = [], [], []
     for b in range(logits.shape[0]):

@@ -38,6 +38,8 @@ SIGNATURES = {
     "vk_decode_attention_workspace": [_I64, _I32, _I64, ctypes.POINTER(_I64)],
     "vk_decode_attention_noalloc": [_P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _I32, _I32, _I64, _I64, _I64, _P],
     "vk_varlen_attention": [_P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I64, _P, _I32, _I32, _I32, _I32, _P, _P],
+    "vk_varlen_attention_prefixed": [_P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I64, _P, _P, _P, _P, _I64, _P, _I32,
+                                     _I32, _I32, _I32, _P, _P],
     "vk_select_update": [_P, _P, _P, _F, _P, _I32, _I32, _P, _P, _P, _I32, _F, _P, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P,
                          _P, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P],
     "vk_decode_attention_grouped": [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _I32,

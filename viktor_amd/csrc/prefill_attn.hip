@@ -18,6 +18,10 @@
 //     reads packed k/v rows or a KV-cache layer directly.
 //   * The host orders the query blocks longest-first (causal blocks near the end of a sequence do the
 //     most work) so the tail of the grid is short blocks.
+//   * PREFIXED: a sequence's first p_lens[i] keys come from a second buffer (kp / vp + p_off[i] + j * p_stride),
+//     the rest from k / v as above (key j at k_off[i] + (j - p_lens[i]) * stride_tok): the key order of one
+//     window [prefix | own rows] whose prefix rows are shared with other sequences (a GSPO group's samples).
+//     The choice is made per loaded row, so a tile may straddle the two.
 #include <math.h>
 
 #include "common.h"
@@ -31,11 +35,19 @@ constexpr int PA_KT = 64;     // keys per LDS tile
 constexpr int PA_PITCH = 72;  // 64 + 8 bf16
 constexpr float PA_SLACK = 8.0f;  // log2 units a row's score may pass its reference max before it moves
 
+struct PaPrefix {
+  const bf16_t *kp, *vp;       // prefix keys / values
+  const int64_t *p_off;        // per sequence: element offset of its prefix row 0
+  const int32_t *p_lens;       // per sequence: keys taken from the prefix buffer
+  int64_t p_stride;            // elements between prefix rows
+};
+
+template <bool PREFIXED>
 __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ k, const bf16_t *__restrict__ v,
     const int32_t *__restrict__ cu_q, const int64_t *__restrict__ k_off, const int32_t *__restrict__ k_lens,
     const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok, bf16_t *__restrict__ out, int causal,
-    float scale_log2, float *__restrict__ lse) {
+    float scale_log2, float *__restrict__ lse, const PaPrefix pre) {
   __shared__ __attribute__((aligned(16))) bf16_t Ks[2][PA_KT * PA_PITCH];
   __shared__ __attribute__((aligned(16))) bf16_t Vs[2][PA_KT * PA_PITCH];  // V rows, as K
 
@@ -54,7 +66,10 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
   const int q_end = cu_q[seq_c + 1];
   const int klen = k_lens[seq_c];
   const int64_t koff = k_off[seq_c];
+  const int plen = PREFIXED ? pre.p_lens[seq_c] : 0;
+  const int64_t poff = PREFIXED ? pre.p_off[seq_c] : 0;
   asm volatile("" ::"s"(q0), "s"(q_end), "s"(klen), "s"(koff));  // (kept ahead of the checks: the compiler would sink them)
+  if (PREFIXED) asm volatile("" ::"s"(plen), "s"(poff));
   if (seq < 0 || seq >= n_seq || qs < 0) return;
   const int q_len = q_end - static_cast<int>(q0);
   if (q_len <= 0 || klen <= 0 || qs >= q_len) return;
@@ -94,9 +109,18 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
   auto load_tile = [&](int t) {
     int key = t * PA_KT + lrow;
     key = key < klen ? key : klen - 1;
-    const int64_t off = koff + static_cast<int64_t>(key) * stride_tok + hk * PA_D + lchunk * 8;
-    rk = *reinterpret_cast<const u32x4 *>(k + off);
-    rv = *reinterpret_cast<const u32x4 *>(v + off);
+    const bf16_t *kb = k, *vb = v;
+    int64_t off;
+    if (PREFIXED && key < plen) {
+      kb = pre.kp;
+      vb = pre.vp;
+      off = poff + static_cast<int64_t>(key) * pre.p_stride;
+    } else {
+      off = koff + static_cast<int64_t>(key - plen) * stride_tok;
+    }
+    off += hk * PA_D + lchunk * 8;
+    rk = *reinterpret_cast<const u32x4 *>(kb + off);
+    rv = *reinterpret_cast<const u32x4 *>(vb + off);
   };
   auto store_tile = [&](int buf) {
     *reinterpret_cast<u32x4 *>(&Ks[buf][lrow * PA_PITCH + lchunk * 8]) = rk;
@@ -236,10 +260,10 @@ __global__ __launch_bounds__(PA_WAVES * 64) void varlen_attn_kernel(
 
 using namespace vk;
 
-extern "C" int vk_varlen_attention(const void *q, const void *k, const void *v, const int32_t *cu_q,
-                                   const int64_t *k_off, const int32_t *k_lens, const int32_t *plan, int32_t n_blocks,
-                                   int32_t n_seq, int64_t stride_tok, void *out, int32_t causal, int32_t H,
-                                   int32_t HKV, int32_t D, float *lse, void *stream) {
+static int varlen_launch(const void *q, const void *k, const void *v, const int32_t *cu_q, const int64_t *k_off,
+                         const int32_t *k_lens, const int32_t *plan, int32_t n_blocks, int32_t n_seq, int64_t stride_tok,
+                         void *out, int32_t causal, int32_t H, int32_t HKV, int32_t D, float *lse, const PaPrefix *pre,
+                         void *stream) {
   VK_CHECK_ARG(q && k && v && cu_q && k_off && k_lens && out, "varlen_attention: null pointer");
   if (H != PA_H || HKV != PA_HKV || D != PA_D)
     return fail(VK_ERR_UNSUPPORTED, "varlen_attention: built for H=8 HKV=2 D=64 (got %d/%d/%d)", H, HKV, D);
@@ -248,11 +272,41 @@ extern "C" int vk_varlen_attention(const void *q, const void *k, const void *v, 
   VK_CHECK_ARG(n_blocks == 0 || (plan != nullptr && n_seq > 0), "varlen_attention: missing plan or sequences");
   VK_CHECK_ARG(vk_aligned16(q) && vk_aligned16(k) && vk_aligned16(v) && vk_aligned16(out),
                "varlen_attention: pointers must be 16-byte aligned");
+  if (pre != nullptr) {
+    VK_CHECK_ARG(pre->kp && pre->vp && pre->p_off && pre->p_lens, "varlen_attention_prefixed: null pointer");
+    VK_CHECK_ARG(pre->p_stride >= PA_HKV * PA_D && pre->p_stride % 8 == 0, "varlen_attention_prefixed: bad prefix stride");
+    VK_CHECK_ARG(vk_aligned16(pre->kp) && vk_aligned16(pre->vp), "varlen_attention_prefixed: prefix pointers must be 16-byte aligned");
+  }
   if (n_blocks == 0) return VK_OK;
   const float scale_log2 = static_cast<float>(1.0 / sqrt(static_cast<double>(PA_D)) * 1.4426950408889634);
   const dim3 grid(static_cast<unsigned>(n_blocks), PA_HKV);
-  varlen_attn_kernel<<<grid, PA_WAVES * 64, 0, VK_STREAM(stream)>>>(
-      static_cast<const bf16_t *>(q), static_cast<const bf16_t *>(k), static_cast<const bf16_t *>(v), cu_q, k_off,
-      k_lens, plan, n_seq, stride_tok, static_cast<bf16_t *>(out), causal, scale_log2, lse);
+  const auto qb = static_cast<const bf16_t *>(q), kb = static_cast<const bf16_t *>(k), vb = static_cast<const bf16_t *>(v);
+  const auto ob = static_cast<bf16_t *>(out);
+  if (pre != nullptr)
+    varlen_attn_kernel<true><<<grid, PA_WAVES * 64, 0, VK_STREAM(stream)>>>(
+        qb, kb, vb, cu_q, k_off, k_lens, plan, n_seq, stride_tok, ob, causal, scale_log2, lse, *pre);
+  else
+    varlen_attn_kernel<false><<<grid, PA_WAVES * 64, 0, VK_STREAM(stream)>>>(
+        qb, kb, vb, cu_q, k_off, k_lens, plan, n_seq, stride_tok, ob, causal, scale_log2, lse, PaPrefix{});
   return launch_status("varlen_attention");
+}
+
+extern "C" int vk_varlen_attention(const void *q, const void *k, const void *v, const int32_t *cu_q,
+                                   const int64_t *k_off, const int32_t *k_lens, const int32_t *plan, int32_t n_blocks,
+                                   int32_t n_seq, int64_t stride_tok, void *out, int32_t causal, int32_t H,
+                                   int32_t HKV, int32_t D, float *lse, void *stream) {
+  return varlen_launch(q, k, v, cu_q, k_off, k_lens, plan, n_blocks, n_seq, stride_tok, out, causal, H, HKV, D, lse,
+                       nullptr, stream);
+}
+
+extern "C" int vk_varlen_attention_prefixed(const void *q, const void *k, const void *v, const int32_t *cu_q,
+                                            const int64_t *k_off, const int32_t *k_lens, const int32_t *plan,
+                                            int32_t n_blocks, int32_t n_seq, int64_t stride_tok, const void *k_prefix,
+                                            const void *v_prefix, const int64_t *p_off, const int32_t *p_lens,
+                                            int64_t p_stride, void *out, int32_t causal, int32_t H, int32_t HKV,
+                                            int32_t D, float *lse, void *stream) {
+  const PaPrefix pre{static_cast<const bf16_t *>(k_prefix), static_cast<const bf16_t *>(v_prefix), p_off, p_lens,
+                     p_stride};
+  return varlen_launch(q, k, v, cu_q, k_off, k_lens, plan, n_blocks, n_seq, stride_tok, out, causal, H, HKV, D, lse,
+                       &pre, stream);
 }

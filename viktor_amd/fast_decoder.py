@@ -104,10 +104,9 @@ class PrefillPlan:
 class SharedPrefixPlan:
     """Host-side layout of a teacher-forced forward over groups of G sequences that share their prefix rows
     (a GSPO rollout's repeated windows, scripts/gspo.py:444): group g's pre_lens[g] prefix rows are packed once
-    (back to back, as a PrefillPlan), and every member b = g G + m has T token rows (packed at b T). The token rows
-    attend to their group's prefix keys and their own keys, both kept in a key buffer [B, S, Hkv, D] with
-    S = max(pre_lens) + T: member b's prefix keys at rows 0 .. pre_lens[g] - 1 and its token keys right after,
-    as the window [prefix | tokens] lays them out."""
+    (back to back, as a PrefillPlan), and every member b = g G + m has T token rows (packed at b T). A token row
+    attends, in the key order of its window [prefix | tokens], to its group's packed prefix keys and then to its
+    member's own token keys (vk_varlen_attention_prefixed), so no prefix key is copied per member."""
 
     def __init__(self, pre_lens, group_size, T, hkv_d, device):
         pre_lens = [int(p) for p in pre_lens]
@@ -116,35 +115,17 @@ class SharedPrefixPlan:
         self.pre_lens, self.G, self.T = pre_lens, G, T
         self.n_groups = len(pre_lens)
         self.B = self.n_groups * G
-        self.S = max(pre_lens) + T
         self.pre = PrefillPlan(pre_lens, device)
         self.pre_full, _ = self.pre.packed_plans(hkv_d)
         member_pre = np.repeat(np.asarray(pre_lens, dtype=np.int64), G)
-        self.tok = ops.AttentionPlan([T] * self.B, (member_pre + T).tolist(),
-                                     [b * self.S * hkv_d for b in range(self.B)], device, causal=True)
+        cu = np.asarray(self.pre.cu[:-1], dtype=np.int64)
+        self.tok = ops.AttentionPlan([T] * self.B, (member_pre + T).tolist(), [b * T * hkv_d for b in range(self.B)],
+                                     device, causal=True, p_lens=member_pre.tolist(),
+                                     p_off=(np.repeat(cu, G) * hkv_d).tolist())
         t = np.arange(T, dtype=np.int64)
-        # token rows: key buffer row (member, pre_len + t), which is also the row's position in its window
+        # a token row's position in its window (pre_len + t) and the prefix rows' (0 .. pre_len - 1)
         self.pos_tok = torch.from_numpy((member_pre[:, None] + t[None, :]).reshape(-1).astype(np.int32)).to(device)
-        self.seq_tok = torch.from_numpy(np.repeat(np.arange(self.B, dtype=np.int32), T)).to(device)
         self.pos_pre = torch.from_numpy(np.concatenate([np.arange(p, dtype=np.int32) for p in pre_lens])).to(device)
-        self.equal = len(set(pre_lens)) == 1
-        self.bc_dst = self.bc_src = None
-        if not self.equal:  # member b's buffer row j <- its group's packed prefix row j
-            cu = self.pre.cu
-            dst = np.concatenate([b * self.S + np.arange(member_pre[b]) for b in range(self.B)])
-            src = np.concatenate([cu[b // G] + np.arange(member_pre[b]) for b in range(self.B)])
-            self.bc_dst = torch.from_numpy(dst).to(device)
-            self.bc_src = torch.from_numpy(src).to(device)
-
-    def broadcast(self, kv_pre, buf):
-        """buf [B, S, Hkv, D]: rows 0 .. pre_lens[g] - 1 of every member of group g <- the group's packed prefix
-        rows of kv_pre [n_pre, Hkv, D] (a device copy)."""
-        if self.equal:
-            P = self.pre_lens[0]
-            buf.view(self.n_groups, self.G, self.S, -1)[:, :, :P].copy_(
-                kv_pre.view(self.n_groups, 1, P, -1).expand(-1, self.G, -1, -1))
-        else:
-            buf.view(self.B * self.S, -1)[self.bc_dst] = kv_pre.view(kv_pre.shape[0], -1)[self.bc_src]
 
 
 class FastDecoder:
@@ -250,9 +231,8 @@ class FastDecoder:
     def teacher_forced_shared(self, x_pre, x_tok, plan, rope_pre=None, rope_tok=None):
         """teacher_forced over groups of sequences that share their prefix (plan: a SharedPrefixPlan): x_pre
         [n_pre, d] fp32 holds each group's prefix rows once, x_tok [B T, d] fp32 every member's token rows. The
-        prefix rows run the layers once per group (the last layer only to its K / V), and each layer's prefix
-        K / V goes to every member's rows of the key buffer, beside the member's own token K / V; the token rows
-        attend to that buffer. Every step of a row is that of teacher_forced over the unshared windows
+        prefix rows run the layers once per group (the last layer only to its K / V), and the token rows attend to
+        their group's prefix keys, then to their member's own (vk_varlen_attention_prefixed). Every step of a row is that of teacher_forced over the unshared windows
         [prefix | tokens]: the products and norms are row by row, and a token row's attention meets the same keys
         in the same order. So the token rows' hidden states are the unshared forward's, bit for bit wherever both
         forwards run a product on the same kernel (each product with at least 4096 rows in both). Returns the
@@ -268,8 +248,6 @@ class FastDecoder:
         eps = cfg.norm_eps
         H, HKV, D = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
         cos, sin = (F(t) for t in self._tables())
-        kbuf = torch.empty(plan.B, plan.S, HKV, D, dtype=BF16, device=x_tok.device)
-        vbuf = torch.empty_like(kbuf)
         n_layers = len(layers)
         w0 = F(layers[0].attn_norm.weight)
         hp = ops.rmsnorm_f32(x_pre, w0, eps)
@@ -279,16 +257,13 @@ class FastDecoder:
             wqkv, qn, kn = W(a.qkv_proj.weight), F(a.q_norm.weight), F(a.k_norm.weight)
             qp, kp, vp = ops.linear_qkv_rope(hp, wqkv, qn, kn, cos, sin, plan.pos_pre, None, None, None, eps, H, HKV,
                                              D, return_kv=True, rope_pos=rope_pre)
-            plan.broadcast(kp, kbuf)
-            plan.broadcast(vp, vbuf)
-            # the token rows' K / V go straight to their members' buffer rows
-            qt = ops.linear_qkv_rope(ht, wqkv, qn, kn, cos, sin, plan.pos_tok, plan.seq_tok, kbuf, vbuf, eps, H, HKV,
-                                     D, rope_pos=rope_tok)
+            qt, kt, vt = ops.linear_qkv_rope(ht, wqkv, qn, kn, cos, sin, plan.pos_tok, None, None, None, eps, H, HKV,
+                                             D, return_kv=True, rope_pos=rope_tok)
             w_next = layers[i + 1].attn_norm.weight if i + 1 < n_layers else self.dec.norm.weight
             if i + 1 < n_layers:  # the prefix rows feed the next layer's prefix keys
                 op = ops.varlen_attention(qp, kp, vp, plan.pre_full, stride_tok=kp.stride(0))
                 hp = self._tf_block(x_pre, op, blk, w_next)
-            ot = ops.varlen_attention(qt, kbuf, vbuf, plan.tok, stride_tok=kbuf.stride(1))
+            ot = ops.varlen_attention(qt, kt, vt, plan.tok, stride_tok=kt.stride(0), prefix=(kp, vp))
             ht = self._tf_block(x_tok, ot, blk, w_next)
         return ht
 

@@ -352,7 +352,9 @@ class AttentionPlan:
 
     BLOCK = 64
 
-    def __init__(self, q_lens, k_lens, k_off, device, causal=True):
+    def __init__(self, q_lens, k_lens, k_off, device, causal=True, p_lens=None, p_off=None):
+        """p_lens / p_off (prefixed key ranges, vk_varlen_attention_prefixed): sequence i's first p_lens[i] of its
+        k_lens[i] keys are rows of a prefix buffer from element p_off[i]; the rest are its k_off rows."""
         import numpy as np
         q = np.asarray([int(a) for a in q_lens], dtype=np.int64)
         k = np.asarray([int(a) for a in k_lens], dtype=np.int64)
@@ -376,13 +378,22 @@ class AttentionPlan:
         self.cu_q = torch.from_numpy(cu.astype(np.int32)).to(device)
         self.k_lens = torch.from_numpy((k if len(k) else np.zeros(1, np.int64)).astype(np.int32)).to(device)
         self.k_off = torch.tensor([int(o) for o in k_off] or [0], dtype=torch.int64).to(device)
+        self.p_lens = self.p_off = None
+        if p_lens is not None:
+            pl = np.asarray([int(a) for a in p_lens], dtype=np.int64)
+            _require(len(pl) == len(q) == len(p_off) and bool(((pl >= 0) & (pl <= k)).all()),
+                     "AttentionPlan: prefix lengths within the key counts")
+            self.p_lens = torch.from_numpy((pl if len(pl) else np.zeros(1, np.int64)).astype(np.int32)).to(device)
+            self.p_off = torch.tensor([int(o) for o in p_off] or [0], dtype=torch.int64).to(device)
 
 
-def varlen_attention(q, k, v, plan: AttentionPlan, stride_tok=None, out=None, lse=None):
+def varlen_attention(q, k, v, plan: AttentionPlan, stride_tok=None, out=None, lse=None, prefix=None):
     """Packed-query GQA attention following `plan`. q [total_q, H, D] bf16; k/v: base tensors (packed
     [n, Hkv, D] rows or one cache layer [B, S, Hkv, D]) addressed by plan.k_off + key * stride_tok
     elements. Returns [total_q, H, D] bf16. lse [total_q, H] fp32 (optional, written): each row's
     log-sum-exp of its scaled scores in log2 units, for attention_backward.
+    prefix = (k_prefix, v_prefix) with a plan built with p_lens / p_off: each sequence's first p_lens keys are rows
+    of those tensors (p_off + key * their row stride), the rest rows of k / v (vk_varlen_attention_prefixed).
     Reference: flash_attn_varlen_func at viktor/fast_decoder.py:68-73."""
     require_device(q, "varlen_attention")
     total, H, D = q.shape
@@ -396,9 +407,18 @@ def varlen_attention(q, k, v, plan: AttentionPlan, stride_tok=None, out=None, ls
         out = torch.empty_like(q)
     _require(lse is None or (lse.dtype == torch.float32 and lse.shape == (total, H) and lse.is_contiguous()),
              "varlen_attention: lse [total_q, H] fp32")
-    call("vk_varlen_attention", ptr(q), ptr(k), ptr(v), ptr(plan.cu_q), ptr(plan.k_off), ptr(plan.k_lens),
-         ptr(plan.plan), plan.n_blocks, plan.n_seq, stride_tok, ptr(out), int(plan.causal), H, HK, D, ptr(lse),
-         stream_handle())
+    _require((prefix is None) == (plan.p_lens is None), "varlen_attention: prefix tensors go with a prefixed plan")
+    if prefix is None:
+        call("vk_varlen_attention", ptr(q), ptr(k), ptr(v), ptr(plan.cu_q), ptr(plan.k_off), ptr(plan.k_lens),
+             ptr(plan.plan), plan.n_blocks, plan.n_seq, stride_tok, ptr(out), int(plan.causal), H, HK, D, ptr(lse),
+             stream_handle())
+        return out
+    kp, vp = prefix
+    _require(kp.dtype == vp.dtype == BF16 and kp.shape[-2:] == (HK, D) and kp.stride(-1) == 1 and kp.stride(-2) == D
+             and kp.stride() == vp.stride(), "varlen_attention: prefix layouts")
+    call("vk_varlen_attention_prefixed", ptr(q), ptr(k), ptr(v), ptr(plan.cu_q), ptr(plan.k_off), ptr(plan.k_lens),
+         ptr(plan.plan), plan.n_blocks, plan.n_seq, stride_tok, ptr(kp), ptr(vp), ptr(plan.p_off), ptr(plan.p_lens),
+         kp.stride(-3), ptr(out), int(plan.causal), H, HK, D, ptr(lse), stream_handle())
     return out
 
 
