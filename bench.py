@@ -37,12 +37,13 @@ Extra objects on the JSON line:
                 call); ms per rollout (device token decode + label packing + the DP kernel) and DP cells per
                 second (label x call bases). (The random-weight model of the rollout ends its calls after a
                 few bases, so its own output would time an almost empty DP.)
-  gspo_update   one micro-batch of the GSPO update (scripts/gspo.py:471-493 with --micro 32): 32 windows of
-                2048 frames + 768 tokens (the 1024-token rollout's calls padded to a multiple of 128),
-                teacher-forced forward + backward of the sequence-ratio loss into the fp32 projector and
-                decoder weights + clip + AdamW step; ms per micro-batch and the MFMA fraction of its
-                algorithmic flops (GEMMs 3 x 2 x weights per row, causal attention 3.5 x 1024 n (n + 1) per
-                layer and window: forward + the standard 2.5 x backward) against 2.5 PFLOP/s bf16.
+  gspo_update   one micro-batch of the GSPO update (scripts/gspo.py:471-493 with --micro 32): 32 calls = 4
+                windows x 8 calls of 2048 frames + 768 tokens (the 1024-token rollout's calls padded to a
+                multiple of 128), teacher-forced forward + backward of the sequence-ratio loss into the fp32
+                projector and decoder weights + clip + AdamW step, with each window's prefix run once for its
+                calls (and timed again unshared, every call's full window); ms per micro-batch and the MFMA
+                fraction of its algorithmic flops (GEMMs 3 x 2 x weights per row, causal attention 3.5 x the
+                forward's per layer: forward + the standard 2.5 x backward) against 2.5 PFLOP/s bf16.
   encoder       the frames producer for one rollout's windows: 128 chunks of 12288 samples (64 windows x 2048
                 frames) through the SUP-shaped encoder (5 convolutions, 18 DeepNorm layers, d_model 512, window
                 (127, 128)) with seeded random weights; ms, chunks/s and the MFMA fraction of its algorithmic
@@ -572,16 +573,21 @@ def prefill_timing(reps=3, prefill_batch=128, group_size=GROUP):
 
 
 def update_timing(steps=3, warmup=2):
-    """One GSPO update micro-batch on the HIP training path (see the module docstring): times and flops."""
+    """One GSPO update micro-batch on the HIP training path (see the module docstring): times and flops. The
+    micro-batch is whole groups, as the reference's update loop takes them (scripts/gspo.py:453, 466-468): 4
+    windows x 8 calls, each window's frames repeated for its calls. Timed with group_size 8 (each window's prefix
+    rows once, the backward summing its calls' gradients into them) and unshared (every call's full window, as
+    the reference computes it)."""
     from viktor_amd import train as TR
     from viktor_amd.gspo import sequence_ratio_loss
     from viktor_amd.synthetic import frames, make_model
     dev = torch.device("cuda", 0)
     B, T = UPDATE_MICRO, UPDATE_T
+    ng = B // GROUP
     m = make_model(1, n_layers=8, seed=7).to(dev)
     opt = TR.HipAdamW(list(m.parameters()), lr=1e-6, betas=(0.9, 0.95), weight_decay=0.0, max_grad_norm=1.0)
     g = torch.Generator().manual_seed(8)
-    fr = frames(B, P, 512, seed=9).to(dev)
+    fr = frames(ng, P, 512, seed=9).to(dev).repeat_interleave(GROUP, 0).contiguous()
     pl = torch.full((B,), P, device=dev)
     tok = torch.randint(3, 7, (B, T), generator=g).to(dev)
     tgt = torch.randint(3, 7, (B, T), generator=g).to(dev)
@@ -589,36 +595,52 @@ def update_timing(steps=3, warmup=2):
     nb = torch.full((B,), float(T), device=dev)
     adv = torch.randn(B, generator=g).to(dev)
     with torch.no_grad():
-        z0 = TR.train_logits(m, fr, tok, pl)
+        z0 = TR.train_logits(m, fr, tok, pl, group_size=GROUP)
         old = torch.log_softmax(z0.float(), -1).gather(-1, tgt[..., None])[..., 0]
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-    acc = [0.0, 0.0, 0.0]
-    for it in range(warmup + steps):
-        opt.zero_grad()
-        ev[0].record()
-        z = TR.train_logits(m, fr, tok, pl)
-        loss = sequence_ratio_loss(z, tgt, mask, old, nb, adv, 4e-4, 4e-4, 1.0 / B)[0]
-        ev[1].record()
-        loss.backward()
-        ev[2].record()
-        opt.step()
-        ev[3].record()
-        torch.cuda.synchronize()
-        if it >= warmup:
-            for i in range(3):
-                acc[i] += ev[i].elapsed_time(ev[i + 1]) / steps
-    n = P + T
-    rows = B * n
+
+    def run(group):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        acc = [0.0, 0.0, 0.0]
+        for it in range(warmup + steps):
+            opt.zero_grad()
+            ev[0].record()
+            z = TR.train_logits(m, fr, tok, pl, group_size=group)
+            loss = sequence_ratio_loss(z, tgt, mask, old, nb, adv, 4e-4, 4e-4, 1.0 / B)[0]
+            ev[1].record()
+            loss.backward()
+            ev[2].record()
+            opt.step()
+            ev[3].record()
+            torch.cuda.synchronize()
+            if it >= warmup:
+                for i in range(3):
+                    acc[i] += ev[i].elapsed_time(ev[i + 1]) / steps
+        return acc
+
+    acc = run(GROUP)
+    acc_full = run(1)
     weights = 8 * 3014656  # decoder matmul weights
-    gemm = 3 * 2 * weights * rows + 3 * 2 * 2 * 512 * 512 * B * P + 3 * 2 * 512 * 7 * B * T
-    attn = 3.5 * 1024 * n * (n + 1) * 8 * B
-    ms = sum(acc)
+    n = P + T
+    rows_full = B * n
+    gemm_full = 3 * 2 * weights * rows_full + 3 * 2 * 2 * 512 * 512 * B * P + 3 * 2 * 512 * 7 * B * T
+    attn_full = 3.5 * 1024 * n * (n + 1) * 8 * B
+    rows = ng * P + B * T
+    gemm = 3 * 2 * weights * rows + 3 * 2 * 2 * 512 * 512 * ng * P + 3 * 2 * 512 * 7 * B * T
+    attn = 3.5 * 8 * (1024 * P * (P + 1) * ng + (1024 * T * (T + 1) + 2048 * T * P) * B)
+    ms, ms_full = sum(acc), sum(acc_full)
     tflops = (gemm + attn) / (ms / 1e3) / 1e12
-    return {"microbatch": f"{B} windows x ({P} frames + {T} tokens), 8 layers, fwd + bwd + clip + AdamW",
+    return {"microbatch": f"{B} calls = {ng} windows x {GROUP} ({P} frames + {T} tokens), 8 layers, "
+                          "fwd + bwd + clip + AdamW", "group_size": GROUP,
             "ms_per_microbatch": round(ms, 2), "forward_ms": round(acc[0], 2), "backward_ms": round(acc[1], 2),
-            "optimizer_ms": round(acc[2], 3), "rows_per_s": round(rows / (ms / 1e3), 1),
+            "optimizer_ms": round(acc[2], 3), "calls_per_s": round(B / (ms / 1e3), 1),
             "alg_tflop": round((gemm + attn) / 1e12, 2), "achieved_tflops": round(tflops, 1),
-            "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+            "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "unshared": {"ms_per_microbatch": round(ms_full, 2), "forward_ms": round(acc_full[0], 2),
+                         "backward_ms": round(acc_full[1], 2), "rows_per_s": round(rows_full / (ms_full / 1e3), 1),
+                         "alg_tflop": round((gemm_full + attn_full) / 1e12, 2),
+                         "mfma_frac": round((gemm_full + attn_full) / (ms_full / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                                            4),
+                         "note": "every call's full window, as the reference computes it"}}
 
 
 def kernels_mode(group, reps=5):

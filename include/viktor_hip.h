@@ -359,6 +359,26 @@ int vk_attention_backward(const void *q, const void *k, const void *v, const voi
                           float *dq, float *dk, float *dv, int32_t H, int32_t HKV, int32_t D, void *stream);
 
 /*
+ * vk_attention_backward for the shared-prefix layout of a GSPO group's samples (the prefix rows kept once, each
+ * sample's token rows after them in the key order of its window). dQ: sequence i's queries first see p_lens[i]
+ * prefix keys, rows of k / v from element p_off[i] (row stride stride_tok), then its own rows (query r at key
+ * position p_lens[i] + r). dK / dV: k_plan holds n_kblocks entries (sequence, first key of a 128-key block, xr0,
+ * xl, slot): xl < 0 takes the sequence's own query rows (causal), xl >= 0 the xl query rows from packed row xr0
+ * (of q / out / dout / lse), each of which sees every key of the block; slot < 0 writes dk / dv, slot >= 0 the
+ * partial rows [slot][row] of part_k / part_v ([n_slots, n_part, HKV, D] fp32, a caller's workspace; those
+ * sequences' rows < n_part), which are then summed in slot order into dk / dv rows 0 .. n_part - 1. So dK / dV
+ * of the prefix rows sum the gradients of the prefix's own queries and of every sample's token queries, in a
+ * fixed order. No reference counterpart of its own: the reference differentiates every sample's full window
+ * (scripts/gspo.py:477); these are the same sums, regrouped.
+ */
+int vk_attention_backward_prefixed(const void *q, const void *k, const void *v, const void *out, const void *dout,
+                                   const float *lse, const int32_t *cu, int32_t n_seq, const int32_t *q_plan,
+                                   int32_t n_qblocks, const int32_t *k_plan, int32_t n_kblocks, int64_t n_rows,
+                                   int64_t stride_tok, const int32_t *p_lens, const int64_t *p_off, float *part_k,
+                                   float *part_v, int64_t n_part, int32_t n_slots, float *dd, float *dq, float *dk,
+                                   float *dv, int32_t H, int32_t HKV, int32_t D, void *stream);
+
+/*
  * Weight gradient of a linear layer over packed rows: out[Ka, Kb] = a^T b = sum_r a[r, ka] b[r, kb] for a [N, Ka]
  * (the layer's output gradient) and b [N, Kb] (its input), bf16 row-major with row strides lda / ldb (elements,
  * multiples of 8); fp32 accumulation, the N rows split into slices whose fp32 partials are summed in slice order

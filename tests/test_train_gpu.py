@@ -65,6 +65,68 @@ def test_attention_backward(lens):
         off += n
 
 
+@pytest.mark.parametrize("pre_lens,G,T", [((300, 129), 3, 100), ((64,), 2, 1), ((1000, 517), 4, 256)])
+def test_attention_backward_shared_prefix(pre_lens, G, T):
+    """The shared-prefix layout (TrainPlan.shared: each group's prefix rows once, then every member's T token rows
+    seeing that prefix) against the same attention over each member's full window [prefix | tokens]: outputs and
+    log-sum-exp bit for bit, dQ of the token rows and dK / dV of the token keys to fp32 rounding, and the prefix
+    rows' dQ / dK / dV against the unshared sums over the members (dQ: the prefix rows are the same in every
+    window; dK / dV: the members' contributions added)."""
+    g = gen(sum(pre_lens) + G + T)
+    ng = len(pre_lens)
+    n_pre, B = sum(pre_lens), ng * G
+    N = n_pre + B * T
+    q = torch.randn(N, 8, 64, generator=g).to(BF)
+    k = torch.randn(N, 2, 64, generator=g).to(BF)
+    v = torch.randn(N, 2, 64, generator=g).to(BF)
+    do = torch.randn(N, 8, 64, generator=g).to(BF)
+    plan = TR.TrainPlan.shared(list(pre_lens), G, T, DEV)
+    lse = torch.empty(N, 8, device=DEV)
+    qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+    o = ops.varlen_attention(qd, kd, vd, plan.attn, lse=lse, prefix=(kd, vd))
+    dq, dk, dv = (t.cpu() for t in ops.attention_backward(qd, kd, vd, o, dod, lse, plan.attn, plan.keys))
+    # the unshared layout: member b's window = [its group's prefix rows | its token rows]; the prefix rows' dO goes
+    # to the first window of each group only (the others' copies get zero), so the windows' sums are the shared ones
+    cu_pre = [0]
+    for p in pre_lens:
+        cu_pre.append(cu_pre[-1] + p)
+    rows, share = [], []
+    for b in range(B):
+        gi = b // G
+        rows.append(torch.arange(cu_pre[gi], cu_pre[gi + 1]))
+        rows.append(n_pre + b * T + torch.arange(T))
+        share.append(torch.full((pre_lens[gi],), 1.0 if b % G == 0 else 0.0))
+        share.append(torch.ones(T))
+    idx, share = torch.cat(rows), torch.cat(share)
+    do_u = (do[idx].float() * share[:, None, None]).to(BF)
+    lens_u = [pre_lens[b // G] + T for b in range(B)]
+    plan_u = TR.TrainPlan(lens_u, DEV)
+    lse_u = torch.empty(idx.numel(), 8, device=DEV)
+    qu, ku, vu = (t[idx].contiguous().to(DEV) for t in (q, k, v))
+    o_u = ops.varlen_attention(qu, ku, vu, plan_u.attn, lse=lse_u)
+    dq_u, dk_u, dv_u = (t.cpu() for t in ops.attention_backward(qu, ku, vu, o_u, do_u.to(DEV), lse_u, plan_u.attn,
+                                                                plan_u.keys))
+    # forward: every row of the shared layout equals its rows in the windows, bit for bit
+    o_c, lse_c = o.cpu(), lse.cpu()
+    tok_u = torch.cat([torch.arange(sum(lens_u[:b]) + pre_lens[b // G], sum(lens_u[:b + 1])) for b in range(B)])
+    pre_u = torch.cat([torch.arange(sum(lens_u[:b]), sum(lens_u[:b]) + pre_lens[b // G]) for b in range(0, B, G)])
+    assert torch.equal(o_c[n_pre:], o_u.cpu()[tok_u]) and torch.equal(lse_c[n_pre:], lse_u.cpu()[tok_u])
+    assert torch.equal(o_c[:n_pre], o_u.cpu()[pre_u]) and torch.equal(lse_c[:n_pre], lse_u.cpu()[pre_u])
+    # backward: token rows' dQ and the token keys' dK / dV (same sums; dS rounding identical)
+    scale = max(float(dq_u.abs().max()), float(dk_u.abs().max()), float(dv_u.abs().max()))
+    for got, ref in ((dq[n_pre:], dq_u[tok_u]), (dk[n_pre:], dk_u[tok_u]), (dv[n_pre:], dv_u[tok_u])):
+        assert (got - ref).abs().max() <= 1e-5 * scale, float((got - ref).abs().max())
+    # prefix rows: dQ from the first window (the only one with their dO); dK / dV summed over the G windows
+    assert (dq[:n_pre] - dq_u[pre_u]).abs().max() <= 1e-5 * scale
+    for got, ref in ((dk, dk_u), (dv, dv_u)):
+        want = torch.zeros(n_pre, 2, 64)
+        for b in range(B):
+            gi = b // G
+            start = sum(lens_u[:b])
+            want[cu_pre[gi]:cu_pre[gi + 1]] += ref[start:start + pre_lens[gi]]
+        assert (got[:n_pre] - want).abs().max() <= 2e-5 * scale, float((got[:n_pre] - want).abs().max())
+
+
 def test_rmsnorm_backward():
     g = gen(5)
     n = 77
@@ -238,6 +300,41 @@ def test_train_logits_equal_scoring_logits(B, P, T):
         z_score = m.logits(fr, tok, pl)
     assert z_train.shape == z_score.shape == (B, T, 7)
     assert torch.equal(z_train, z_score)
+
+
+@pytest.mark.parametrize("pre_lens,pos_scale", [((1024, 1024), 1), ((1024, 900), 2)])
+def test_train_logits_shared_prefix(pre_lens, pos_scale):
+    """train_logits over groups of G windows that share their frames (a GSPO micro-batch of whole groups): the
+    logits equal the unshared forward's bit for bit (every product over at least 4096 rows in both forwards), and
+    every parameter's gradient is the unshared one's up to the order of the fp32 sums over the members (relative
+    L2 < 1e-2, cosine > 0.9999 per tensor)."""
+    from viktor_amd.synthetic import make_model
+    G, T, P = 4, 256, 1024
+    ng = len(pre_lens)
+    B = ng * G
+    m = make_model(1, n_layers=2, seed=61, norm_jitter=0.1, bias_jitter=0.1).to(DEV)
+    m.pos_scale = pos_scale
+    g = torch.Generator(device=DEV).manual_seed(62)
+    fr = torch.randn(ng, P, 512, generator=g, device=DEV).repeat_interleave(G, 0).contiguous()
+    pl = torch.tensor(pre_lens, device=DEV).repeat_interleave(G)
+    tok = torch.randint(3, 7, (B, T), generator=torch.Generator().manual_seed(63)).to(DEV)
+    w = torch.randn(B, T, 7, generator=g, device=DEV)
+    params = [p for p in m.parameters()]
+
+    def grads(group):
+        for p in params:
+            p.grad = None
+        z = TR.train_logits(m, fr, tok, pl, group_size=group)
+        (z.float() * w).sum().backward()
+        return z.detach(), [p.grad.detach().clone() for p in params]
+
+    z1, g1 = grads(1)
+    zg, gg = grads(G)
+    assert torch.equal(zg, z1)
+    for (name, _), a, b in zip(m.named_parameters(), gg, g1):
+        rel = float((a - b).norm() / b.norm().clamp_min(1e-30))
+        cos = float(F.cosine_similarity(a.flatten().double(), b.flatten().double(), dim=0))
+        assert rel < 1e-2 and cos > 0.9999, (name, rel, cos)
 
 
 def test_hip_adamw_update_changes_params_in_place():

@@ -54,6 +54,8 @@ SIGNATURES = {
     "vk_group_advantage": [_P, _I64, _I32, _I32, _F, _P, _P, _P],
     "vk_attention_backward": [_P, _P, _P, _P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _I64, _I64, _P, _P, _P, _P, _I32,
                               _I32, _I32, _P],
+    "vk_attention_backward_prefixed": [_P, _P, _P, _P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _I64, _I64, _P, _P, _P,
+                                       _P, _I64, _I32, _P, _P, _P, _P, _I32, _I32, _I32, _P],
     "vk_wgrad": [_P, _I64, _P, _I64, _I64, _I32, _I32, _P, _I32, _P, _I64, _P],
     "vk_wgrad_workspace": [_I64, _I32, _I32, ctypes.POINTER(_I64)],
     "vk_bias_act": [_P, _P, _P, _P, _I64, _I32, _I32, _P],

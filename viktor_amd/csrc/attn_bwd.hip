@@ -75,12 +75,28 @@ __global__ __launch_bounds__(256) void attn_bwd_dot_kernel(const bf16_t *__restr
   dd[i] = s;
 }
 
+// Shared-prefix layout (the GSPO group's samples scored as one window each, their common prefix rows kept once):
+// in dQ, sequence i's queries see first p_lens[i] prefix keys, rows of k / v from element p_off[i] (row stride
+// stride_tok), then its own rows, query r at key position p_lens[i] + r. In dK / dV a work item is
+// (sequence, first key, xr0, xl, slot): xl < 0 takes the sequence's own query rows (causal), xl >= 0 the xl rows
+// from packed row xr0 (of q / dO / lse / D), each of which sees every key of the block (the samples' token rows
+// against their prefix keys); slot < 0 writes dk / dv, slot >= 0 the partial rows part[slot][r0 + key], which
+// attn_bwd_part_reduce_kernel sums over the slots in order into dk / dv (rows < n_part). Not PREFIXED: plain
+// causal self-attention with (sequence, first key) items.
+struct AbPrefix {
+  const int32_t *p_lens;
+  const int64_t *p_off;
+  float *part_k, *part_v;  // [slots, n_part, HKV, D]
+  int64_t n_part;
+};
+
 // ---- dQ: workgroup = 64 query rows of one sequence x one KV head -----------------------------------------
+template <bool PREFIXED>
 __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ k, const bf16_t *__restrict__ v,
     const bf16_t *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ dd,
     const int32_t *__restrict__ cu, const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok,
-    float *__restrict__ dq, float scale_log2, float scale) {
+    float *__restrict__ dq, float scale_log2, float scale, const AbPrefix pre) {
   // K and V rows: the A operands of S^T and dP^T, and (through transpose reads of K) of dQ^T = K^T dS^T
   __shared__ __attribute__((aligned(16))) bf16_t Ks[2][64 * AB_PITCH];
   __shared__ __attribute__((aligned(16))) bf16_t Vs[2][64 * AB_PITCH];
@@ -93,7 +109,10 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
   const int len = cu[seq + 1] - static_cast<int>(r0);
   if (len <= 0 || qs >= len) return;
   const int nq = min(64, len - qs);
-  const int kend = qs + nq;  // causal: the block's last row sees keys < kend
+  const int plen = PREFIXED ? pre.p_lens[seq] : 0;  // keys before the sequence's own rows
+  const int64_t poff = PREFIXED ? pre.p_off[seq] : 0;
+  const int klen = plen + len;
+  const int kend = plen + qs + nq;  // causal: the block's last row sees keys < kend
   const int ntiles = (kend + 63) / 64;
 
   const int r_first = qs + 32 * half;
@@ -104,7 +123,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
   for (int qb = 0; qb < 2; ++qb) {
     int r = r_first + 16 * qb + col;
     r = r < len ? r : len - 1;
-    qpos[qb] = r;
+    qpos[qb] = plen + r;
     const int64_t row = (r0 + r) * AB_H + hq;
 #pragma unroll
     for (int dc = 0; dc < 2; ++dc) {
@@ -114,7 +133,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
     lse2[qb] = lse[row];
     dr[qb] = dd[row];
   }
-  const int wave_kmax = min(r_first + 31, len - 1);
+  const int wave_kmax = plen + min(r_first + 31, len - 1);
 
   f32x4 acc[4][2];  // dQ^T tiles [d tile][query block]
 #pragma unroll
@@ -126,8 +145,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
   u32x4 rk, rv;
   auto load_tile = [&](int t) {
     int key = t * 64 + lrow;
-    key = key < len ? key : len - 1;
-    const int64_t off = (r0 + key) * stride_tok + hk * AB_D + lchunk * 8;
+    key = key < klen ? key : klen - 1;
+    const int64_t off = (PREFIXED && key < plen ? poff + static_cast<int64_t>(key) * stride_tok
+                                                : (r0 + key - plen) * stride_tok) + hk * AB_D + lchunk * 8;
     rk = *reinterpret_cast<const u32x4 *>(k + off);
     rv = *reinterpret_cast<const u32x4 *>(v + off);
   };
@@ -170,11 +190,11 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
       // dS^T in the accumulator layout (key 16 kb + 4 g + i, query col), as the B operand of K^T dS^T;
       // exponents are <= 0 (the row's log-sum-exp bounds every score), so the bare v_exp_f32 serves. Only a
       // half that reaches a row's diagonal is masked (a wave-uniform branch; a masked score's exponent is -inf)
-      const bool need_mask = kbase + 31 > r_first;
+      const bool need_mask = kbase + 31 > plen + r_first;
       bf16x8 dsf[2];
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
-        const int hi_k = min(qpos[qb], len - 1);
+        const int hi_k = min(qpos[qb], klen - 1);
         float x[8];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -217,11 +237,12 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_kernel(
 }
 
 // ---- dK / dV: workgroup = AB_KB keys of one sequence x one KV head ----------------------------------------
+template <bool PREFIXED>
 __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ k, const bf16_t *__restrict__ v,
     const bf16_t *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ dd,
     const int32_t *__restrict__ cu, const int32_t *__restrict__ plan, int n_seq, int64_t stride_tok,
-    float *__restrict__ dk, float *__restrict__ dv, float scale_log2, float scale) {
+    float *__restrict__ dk, float *__restrict__ dv, float scale_log2, float scale, const AbPrefix pre) {
   // row-major Q / dO tiles [head][row]: the A operands of S and dP, and (through transpose reads) of dK^T and dV^T
   __shared__ __attribute__((aligned(16))) bf16_t Qs[4 * 32 * AB_PITCH];
   __shared__ __attribute__((aligned(16))) bf16_t Os[4 * 32 * AB_PITCH];  // dO
@@ -229,11 +250,18 @@ __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
   const int col = lane & 15, g = lane >> 4;
   const int hk = blockIdx.y;
-  const int seq = plan[2 * blockIdx.x], ks = plan[2 * blockIdx.x + 1];
+  constexpr int PS = PREFIXED ? 5 : 2;  // plan entry size
+  const int seq = plan[PS * blockIdx.x], ks = plan[PS * blockIdx.x + 1];
+  const int xl = PREFIXED ? plan[PS * blockIdx.x + 3] : -1;
+  const int64_t xr0 = PREFIXED ? plan[PS * blockIdx.x + 2] : 0;
+  const int slot = PREFIXED ? plan[PS * blockIdx.x + 4] : -1;
   if (seq < 0 || seq >= n_seq || ks < 0) return;
   const int64_t r0 = cu[seq];
   const int len = cu[seq + 1] - static_cast<int>(r0);
   if (len <= 0 || ks >= len) return;
+  // query tiles: the sequence's own rows from the block's first key (causal), or the xl extra rows
+  const bool xt = xl >= 0;  // extra rows: every row sees every key of the block
+  const int ntl = xt ? (xl + 31) / 32 : (len - ks + 31) / 32;
 
   // this wave's 32 keys, two blocks of 16 (lane col -> key of each), K^T / V^T fragments of the B operand
   int keyb[2];
@@ -263,25 +291,37 @@ __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
   constexpr int NT = AB_KW * 64, NC = 1024 / NT;
   u32x4 qv[NC], ov[NC];
   float lv = 0.f;
-  auto load_tile = [&](int rs) {
+  // query tile it: rows rs .. rs + 31 of the sequence (rs = ks + 32 it) or of the extra rows (rs = 32 it)
+  auto tile_rows = [&](int it, int &rs, int &n, int64_t &base) {
+    rs = xt ? 32 * it : ks + 32 * it;
+    n = xt ? xl : len;
+    base = xt ? xr0 : r0;
+  };
+  auto load_tile = [&](int it) {
+    int rs, n;
+    int64_t base;
+    tile_rows(it, rs, n, base);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int chunk = tid + NT * c;
       const int hh = chunk >> 8, rr = (chunk >> 3) & 31, dc8 = chunk & 7;
       int r = rs + rr;
-      r = r < len ? r : len - 1;
-      const int64_t off = ((r0 + r) * AB_H + hk * 4 + hh) * AB_D + 8 * dc8;
+      r = r < n ? r : n - 1;
+      const int64_t off = ((base + r) * AB_H + hk * 4 + hh) * AB_D + 8 * dc8;
       qv[c] = *reinterpret_cast<const u32x4 *>(q + off);
       ov[c] = *reinterpret_cast<const u32x4 *>(dout + off);
     }
     const int hh = (tid & 127) >> 5, rr = tid & 31;
     int r = rs + rr;
-    r = r < len ? r : len - 1;
-    const int64_t row = (r0 + r) * AB_H + hk * 4 + hh;
+    r = r < n ? r : n - 1;
+    const int64_t row = (base + r) * AB_H + hk * 4 + hh;
     lv = tid < 128 ? lse[row] : dd[row];  // (threads >= 256 load a D value they do not store)
   };
-  load_tile(ks);
-  for (int rs = ks; rs < len; rs += 32) {
+  if (ntl > 0) load_tile(0);
+  for (int it = 0; it < ntl; ++it) {
+    int rs, n;
+    int64_t base;
+    tile_rows(it, rs, n, base);
     __syncthreads();  // the previous tile's readers are done
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -295,8 +335,8 @@ __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
     else if (tid < 256)
       Ds[tid - 128] = lv;
     __syncthreads();
-    if (rs + 32 < len) load_tile(rs + 32);
-    if (rs + 31 < wave_kmin) continue;  // wave-uniform: every row of the tile lies above this wave's keys
+    if (it + 1 < ntl) load_tile(it + 1);
+    if (!xt && rs + 31 < wave_kmin) continue;  // wave-uniform: every row of the tile lies above this wave's keys
 
 #pragma unroll
     for (int hh = 0; hh < 4; ++hh) {
@@ -322,7 +362,7 @@ __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
       // row order {4g..4g+3, 16+4g..16+4g+3}; exponents are <= 0 (bare v_exp_f32). A tile wholly below the
       // diagonal and inside the sequence needs no mask (a wave-uniform branch); else a masked entry's exponent
       // is -inf (exp2 -> 0)
-      const bool full = wave_kmin + 31 <= rs && rs + 31 < len;
+      const bool full = xt ? rs + 31 < n && wave_kmin + 31 < len : wave_kmin + 31 <= rs && rs + 31 < len;
       bf16x8 pf[2], dsf[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
@@ -338,7 +378,7 @@ __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const int r = rs + 16 * rb + 4 * g + i;
-              const bool ok = (r < len) & (key <= r) & (key < len);
+              const bool ok = (r < n) & (xt | (key <= r)) & (key < len);
               x[rb * 4 + i] = ok ? x[rb * 4 + i] : -INFINITY;
             }
         }
@@ -373,8 +413,9 @@ __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     if (keyb[kb] < len) {
-      float *dkp = dk + ((r0 + keyb[kb]) * AB_HKV + hk) * AB_D + 4 * g;
-      float *dvp = dv + ((r0 + keyb[kb]) * AB_HKV + hk) * AB_D + 4 * g;
+      const int64_t orow = slot < 0 ? r0 + keyb[kb] : slot * pre.n_part + r0 + keyb[kb];
+      float *dkp = (slot < 0 ? dk : pre.part_k) + (orow * AB_HKV + hk) * AB_D + 4 * g;
+      float *dvp = (slot < 0 ? dv : pre.part_v) + (orow * AB_HKV + hk) * AB_D + 4 * g;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         *reinterpret_cast<f32x4 *>(dkp + 16 * dt) = acck[kb][dt] * scale;
@@ -384,15 +425,32 @@ __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
   }
 }
 
+// dk / dv rows 0 .. n_part - 1 = the sum over slots 0 .. S - 1 of part[slot] (in slot order), 4 values per thread
+__global__ __launch_bounds__(256) void attn_bwd_part_reduce_kernel(const float *__restrict__ part_k,
+                                                                  const float *__restrict__ part_v,
+                                                                  float *__restrict__ dk, float *__restrict__ dv,
+                                                                  int64_t n4, int S) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const f32x4 *pk = reinterpret_cast<const f32x4 *>(part_k), *pv = reinterpret_cast<const f32x4 *>(part_v);
+  f32x4 a = pk[i], b = pv[i];
+  for (int s = 1; s < S; ++s) {
+    a += pk[s * n4 + i];
+    b += pv[s * n4 + i];
+  }
+  reinterpret_cast<f32x4 *>(dk)[i] = a;
+  reinterpret_cast<f32x4 *>(dv)[i] = b;
+}
+
 }  // namespace vk
 
 using namespace vk;
 
-extern "C" int vk_attention_backward(const void *q, const void *k, const void *v, const void *out, const void *dout,
-                                     const float *lse, const int32_t *cu, int32_t n_seq, const int32_t *q_plan,
-                                     int32_t n_qblocks, const int32_t *k_plan, int32_t n_kblocks, int64_t n_rows,
-                                     int64_t stride_tok, float *dd, float *dq, float *dk, float *dv, int32_t H,
-                                     int32_t HKV, int32_t D, void *stream) {
+static int attn_bwd_launch(const void *q, const void *k, const void *v, const void *out, const void *dout,
+                           const float *lse, const int32_t *cu, int32_t n_seq, const int32_t *q_plan,
+                           int32_t n_qblocks, const int32_t *k_plan, int32_t n_kblocks, int64_t n_rows,
+                           int64_t stride_tok, const AbPrefix *pre, int32_t n_slots, float *dd, float *dq,
+                           float *dk, float *dv, int32_t H, int32_t HKV, int32_t D, void *stream) {
   VK_CHECK_ARG(q && k && v && out && dout && lse && cu && dd && dq && dk && dv, "attention_backward: null pointer");
   if (H != AB_H || HKV != AB_HKV || D != AB_D)
     return fail(VK_ERR_UNSUPPORTED, "attention_backward: built for H=8 HKV=2 D=64 (got %d/%d/%d)", H, HKV, D);
@@ -403,6 +461,10 @@ extern "C" int vk_attention_backward(const void *q, const void *k, const void *v
   VK_CHECK_ARG(vk_aligned16(q) && vk_aligned16(k) && vk_aligned16(v) && vk_aligned16(out) && vk_aligned16(dout) &&
                    vk_aligned16(dq) && vk_aligned16(dk) && vk_aligned16(dv),
                "attention_backward: pointers must be 16-byte aligned");
+  VK_CHECK_ARG(pre == nullptr || (pre->p_lens && pre->p_off && pre->n_part >= 0 &&
+                                  (pre->n_part == 0 || (pre->part_k && pre->part_v && vk_aligned16(pre->part_k) &&
+                                                        vk_aligned16(pre->part_v)))),
+               "attention_backward_prefixed: prefix arrays or partial buffers");
   if (n_rows == 0) return VK_OK;
   hipStream_t s = VK_STREAM(stream);
   const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(AB_D)));
@@ -412,20 +474,60 @@ extern "C" int vk_attention_backward(const void *q, const void *k, const void *v
   const auto vb = static_cast<const bf16_t *>(v);
   const auto ob = static_cast<const bf16_t *>(out);
   const auto dob = static_cast<const bf16_t *>(dout);
+  const AbPrefix none{nullptr, nullptr, nullptr, nullptr, 0};
   const int64_t nd = n_rows * AB_H;
   attn_bwd_dot_kernel<<<static_cast<unsigned>((nd + 255) / 256), 256, 0, s>>>(dob, ob, dd, n_rows);
   int rc = launch_status("attention_backward dot");
   if (rc != VK_OK) return rc;
   if (n_qblocks > 0) {
-    attn_bwd_dq_kernel<<<dim3(static_cast<unsigned>(n_qblocks), AB_HKV), 512, 0, s>>>(
-        qb, kb, vb, dob, lse, dd, cu, q_plan, n_seq, stride_tok, dq, scale_log2, scale);
+    const dim3 grid(static_cast<unsigned>(n_qblocks), AB_HKV);
+    if (pre != nullptr)
+      attn_bwd_dq_kernel<true><<<grid, 512, 0, s>>>(qb, kb, vb, dob, lse, dd, cu, q_plan, n_seq, stride_tok, dq,
+                                                   scale_log2, scale, *pre);
+    else
+      attn_bwd_dq_kernel<false><<<grid, 512, 0, s>>>(qb, kb, vb, dob, lse, dd, cu, q_plan, n_seq, stride_tok, dq,
+                                                    scale_log2, scale, none);
     rc = launch_status("attention_backward dq");
     if (rc != VK_OK) return rc;
   }
   if (n_kblocks > 0) {
-    attn_bwd_dkdv_kernel<<<dim3(static_cast<unsigned>(n_kblocks), AB_HKV), AB_KW * 64, 0, s>>>(
-        qb, kb, vb, dob, lse, dd, cu, k_plan, n_seq, stride_tok, dk, dv, scale_log2, scale);
+    const dim3 grid(static_cast<unsigned>(n_kblocks), AB_HKV);
+    if (pre != nullptr)
+      attn_bwd_dkdv_kernel<true><<<grid, AB_KW * 64, 0, s>>>(qb, kb, vb, dob, lse, dd, cu, k_plan, n_seq, stride_tok,
+                                                            dk, dv, scale_log2, scale, *pre);
+    else
+      attn_bwd_dkdv_kernel<false><<<grid, AB_KW * 64, 0, s>>>(qb, kb, vb, dob, lse, dd, cu, k_plan, n_seq, stride_tok,
+                                                             dk, dv, scale_log2, scale, none);
     rc = launch_status("attention_backward dkdv");
+    if (rc != VK_OK) return rc;
+  }
+  if (pre != nullptr && pre->n_part > 0 && n_slots > 0) {
+    const int64_t n4 = pre->n_part * AB_HKV * AB_D / 4;
+    attn_bwd_part_reduce_kernel<<<static_cast<unsigned>((n4 + 255) / 256), 256, 0, s>>>(pre->part_k, pre->part_v, dk,
+                                                                                        dv, n4, n_slots);
+    rc = launch_status("attention_backward partial sums");
   }
   return rc;
+}
+
+extern "C" int vk_attention_backward(const void *q, const void *k, const void *v, const void *out, const void *dout,
+                                     const float *lse, const int32_t *cu, int32_t n_seq, const int32_t *q_plan,
+                                     int32_t n_qblocks, const int32_t *k_plan, int32_t n_kblocks, int64_t n_rows,
+                                     int64_t stride_tok, float *dd, float *dq, float *dk, float *dv, int32_t H,
+                                     int32_t HKV, int32_t D, void *stream) {
+  return attn_bwd_launch(q, k, v, out, dout, lse, cu, n_seq, q_plan, n_qblocks, k_plan, n_kblocks, n_rows, stride_tok,
+                         nullptr, 0, dd, dq, dk, dv, H, HKV, D, stream);
+}
+
+extern "C" int vk_attention_backward_prefixed(const void *q, const void *k, const void *v, const void *out,
+                                              const void *dout, const float *lse, const int32_t *cu, int32_t n_seq,
+                                              const int32_t *q_plan, int32_t n_qblocks, const int32_t *k_plan,
+                                              int32_t n_kblocks, int64_t n_rows, int64_t stride_tok,
+                                              const int32_t *p_lens, const int64_t *p_off, float *part_k,
+                                              float *part_v, int64_t n_part, int32_t n_slots, float *dd, float *dq,
+                                              float *dk, float *dv, int32_t H, int32_t HKV, int32_t D, void *stream) {
+  VK_CHECK_ARG(n_slots >= 0 && n_part <= n_rows, "attention_backward_prefixed: bad partial sizes");
+  const AbPrefix pre{p_lens, p_off, part_k, part_v, n_part};
+  return attn_bwd_launch(q, k, v, out, dout, lse, cu, n_seq, q_plan, n_qblocks, k_plan, n_kblocks, n_rows, stride_tok,
+                         &pre, n_slots, dd, dq, dk, dv, H, HKV, D, stream);
 }

@@ -16,6 +16,8 @@ status other than OK raises HipLibraryError.
 
 import ctypes
 
+import numpy as np
+
 import torch
 
 from . import _lib
@@ -604,12 +606,41 @@ class KeyBlockPlan:
 
     BLOCK = 128
 
-    def __init__(self, seq_lens, device):
+    def __init__(self, seq_lens, device, extra=None):
+        """extra (the shared-prefix layout of vk_attention_backward_prefixed): per sequence, a list of (first
+        packed row, rows) query segments that see every key of the sequence (their samples' token rows against a
+        shared prefix). Such a sequence's key blocks get a work item for its own rows (partial slot 0) and one
+        per segment (slot 1 + j), summed in slot order; those sequences must come first in the packing and carry
+        the same number of segments."""
         lens = [int(n) for n in seq_lens]
-        blocks = sorted(((n - ks, i, ks) for i, n in enumerate(lens) for ks in range(0, n, self.BLOCK)),
-                        key=lambda b: -b[0])
-        flat = [v for _, i, ks in blocks for v in (i, ks)] or [0, 0]
+        self.n_slots, self.n_part = 0, 0
+        if extra is None:
+            blocks = sorted(((n - ks, i, ks) for i, n in enumerate(lens) for ks in range(0, n, self.BLOCK)),
+                            key=lambda b: -b[0])
+            flat = [v for _, i, ks in blocks for v in (i, ks)] or [0, 0]
+        else:
+            _require(len(extra) == len(lens), "KeyBlockPlan: one segment list per sequence")
+            segs = [list(e or []) for e in extra]
+            with_x = [i for i, e in enumerate(segs) if e]
+            cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+            if with_x:
+                _require(with_x == list(range(len(with_x))) and len({len(segs[i]) for i in with_x}) == 1,
+                         "KeyBlockPlan: sequences with segments first, each with the same number")
+                self.n_slots = 1 + len(segs[0])
+                self.n_part = int(cu[len(with_x)])
+            items = []
+            for i, n in enumerate(lens):
+                for ks in range(0, n, self.BLOCK):
+                    if segs[i]:
+                        items.append((n - ks, i, ks, 0, -1, 0))
+                        items += [(int(xn), i, ks, int(x0), int(xn), 1 + j) for j, (x0, xn) in enumerate(segs[i])]
+                    else:
+                        items.append((n - ks, i, ks, 0, -1, -1))
+            items.sort(key=lambda b: -b[0])
+            flat = [v for it in items for v in it[1:]] or [0, 0, 0, -1, -1]
+            blocks = items
         self.n_blocks = len(blocks)
+        self.prefixed = extra is not None
         self.plan = torch.tensor(flat, dtype=torch.int32).to(device)
 
 
@@ -617,6 +648,9 @@ def attention_backward(q, k, v, out, dout, lse, q_plan: AttentionPlan, k_plan: K
     """Gradients of causal GQA self-attention over the packed sequences of q_plan (q_lens == k_lens, keys of
     sequence i at rows cu[i].. of k / v). q / out / dout [n, 8, 64] bf16, k / v [n, 2, 64] (row stride
     stride_tok), lse [n, 8] from varlen_attention(..., lse=). Returns dq [n, 8, 64], dk, dv [n, 2, 64] fp32.
+    Shared-prefix layout (q_plan with p_lens / p_off, k_plan with extra segments): sequence i's queries first see
+    p_lens[i] prefix keys (rows of k / v from element p_off[i]) and its key blocks also collect the gradients of
+    its extra query segments (vk_attention_backward_prefixed).
     Reference: the backward of flash_attn_func(causal=True) at viktor/decoder.py:82-87."""
     require_device(q, "attention_backward")
     n, H, D = q.shape
@@ -632,8 +666,21 @@ def attention_backward(q, k, v, out, dout, lse, q_plan: AttentionPlan, k_plan: K
     dq = torch.empty(n, H, D, dtype=torch.float32, device=q.device)
     dk = torch.empty(n, HK, D, dtype=torch.float32, device=q.device)
     dv = torch.empty_like(dk)
-    call("vk_attention_backward", ptr(q), ptr(k), ptr(v), ptr(out), ptr(dout), ptr(lse), ptr(q_plan.cu_q),
-         q_plan.n_seq, ptr(q_plan.plan), q_plan.n_blocks, ptr(k_plan.plan), k_plan.n_blocks, n, stride_tok, ptr(dd),
+    prefixed = q_plan.p_lens is not None or k_plan.prefixed
+    if not prefixed:
+        call("vk_attention_backward", ptr(q), ptr(k), ptr(v), ptr(out), ptr(dout), ptr(lse), ptr(q_plan.cu_q),
+             q_plan.n_seq, ptr(q_plan.plan), q_plan.n_blocks, ptr(k_plan.plan), k_plan.n_blocks, n, stride_tok,
+             ptr(dd), ptr(dq), ptr(dk), ptr(dv), H, HK, D, stream_handle())
+        return dq, dk, dv
+    _require(q_plan.p_lens is not None and k_plan.prefixed,
+             "attention_backward: a shared-prefix layout needs both plans' prefix fields")
+    part_k = part_v = None
+    if k_plan.n_slots:
+        part_k = torch.empty(k_plan.n_slots, k_plan.n_part, HK, D, dtype=torch.float32, device=q.device)
+        part_v = torch.empty_like(part_k)
+    call("vk_attention_backward_prefixed", ptr(q), ptr(k), ptr(v), ptr(out), ptr(dout), ptr(lse), ptr(q_plan.cu_q),
+         q_plan.n_seq, ptr(q_plan.plan), q_plan.n_blocks, ptr(k_plan.plan), k_plan.n_blocks, n, stride_tok,
+         ptr(q_plan.p_lens), ptr(q_plan.p_off), ptr(part_k), ptr(part_v), k_plan.n_part, k_plan.n_slots, ptr(dd),
          ptr(dq), ptr(dk), ptr(dv), H, HK, D, stream_handle())
     return dq, dk, dv
 

@@ -26,6 +26,25 @@ from .tokenizer import PAD, KmerTokenizer, get_tokenizer
 BF16 = torch.bfloat16
 
 
+def check_groups(frames, plens_h, G):
+    """The prefix lengths of the groups of G consecutive windows (ValueError unless B is whole groups and each
+    group's windows have one prefix length and the same real frames, bit for bit)."""
+    B, P = frames.shape[:2]
+    if B % G:
+        raise ValueError(f"group_size={G}: {B} windows are not whole groups")
+    pre_lens = plens_h[::G]
+    if any(plens_h[b] != pre_lens[b // G] for b in range(B)):
+        raise ValueError(f"group_size={G}: the windows of a group must have the same prefix length")
+    if all(p == P for p in plens_h) and frames.is_contiguous() and (frames[0].numel() * frames.element_size()) % 16 == 0:
+        same = ops.group_rows_equal(frames, G)
+    else:
+        same = all(torch.equal(frames[b:b + G, :p], frames[b:b + 1, :p].expand(G, -1, -1))
+                   for b, p in zip(range(0, B, G), pre_lens))
+    if not same:
+        raise ValueError(f"group_size={G}: the windows of a group must share their prefix frames")
+    return pre_lens
+
+
 class Basecaller(nn.Module):
     def __init__(self, encoder, tokenizer: KmerTokenizer, cfg: Optional[DecoderConfig] = None, d_enc: int = 512):
         super().__init__()
@@ -152,18 +171,7 @@ class Basecaller(nn.Module):
         B, P = frames.shape[:2]
         T = tokens_in.shape[1]
         dev = frames.device
-        if B % G:
-            raise ValueError(f"group_size={G}: {B} windows are not whole groups")
-        pre_lens = plens_h[::G]
-        if any(plens_h[b] != pre_lens[b // G] for b in range(B)):
-            raise ValueError(f"group_size={G}: the windows of a group must have the same prefix length")
-        if all(p == P for p in plens_h) and frames.is_contiguous() and (frames[0].numel() * frames.element_size()) % 16 == 0:
-            same = ops.group_rows_equal(frames, G)
-        else:
-            same = all(torch.equal(frames[b:b + G, :p], frames[b:b + 1, :p].expand(G, -1, -1))
-                       for b, p in zip(range(0, B, G), pre_lens))
-        if not same:
-            raise ValueError(f"group_size={G}: the windows of a group must share their prefix frames")
+        pre_lens = check_groups(frames, plens_h, G)
         d = self.cfg.d_model
         prefix = self.project(frames[::G].contiguous())                    # [B / G, P, d] bf16, one per group
         if all(p == P for p in pre_lens):

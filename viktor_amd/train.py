@@ -191,7 +191,7 @@ class _DecoderStack(torch.autograd.Function):
             q, k, v = ops.linear_qkv_rope(h, wqkv, wqn, wkn, cos, sin, rpos, None, None, None, eps, H, HKV, D,
                                           return_kv=True, qkv_out=qkv)
             lse = torch.empty(N, H, dtype=torch.float32, device=x.device)
-            o = ops.varlen_attention(q, k, v, plan.attn, lse=lse)
+            o = ops.varlen_attention(q, k, v, plan.attn, lse=lse, prefix=(k, v) if plan.prefixed else None)
             x_mid, h2 = _residual_norm(x_in, o.view(N, H * D), wo, wm, eps)
             # SwiGLU in the product's epilogue (the scoring forward's kernel), keeping gate | up for the backward
             gu = torch.empty(N, wgu.shape[0], dtype=BF16, device=x.device)
@@ -254,12 +254,43 @@ class TrainPlan:
             cu.append(cu[-1] + int(n))
         self.attn = ops.AttentionPlan(seq_lens, seq_lens, [c * kv_row for c in cu[:-1]], device, causal=True)
         self.keys = ops.KeyBlockPlan(seq_lens, device)
+        self.prefixed = False
+
+    @classmethod
+    def shared(cls, pre_lens, G, T, device, kv_row=128):
+        """The shared-prefix layout of groups of G windows with one prefix each: the n_groups prefixes packed
+        first (group g: pre_lens[g] rows), then every member's T token rows. A prefix is a causal sequence on its
+        own; a member's token rows see its group's prefix keys, then their own keys causally (in the key order
+        of the window [prefix | tokens]); each prefix key block also collects the gradients of every member's T
+        token rows, which see all of its keys (one work item per member, summed in member order)."""
+        pre_lens = [int(p) for p in pre_lens]
+        ng = len(pre_lens)
+        cu_pre = np.concatenate([[0], np.cumsum(pre_lens)]).astype(np.int64)
+        n_pre = int(cu_pre[-1])
+        member_pre = np.repeat(np.asarray(pre_lens, dtype=np.int64), G)
+        B = ng * G
+        lens = pre_lens + [T] * B
+        starts = np.concatenate([cu_pre[:-1], n_pre + T * np.arange(B, dtype=np.int64)])
+        self = cls.__new__(cls)
+        self.attn = ops.AttentionPlan(lens, pre_lens + (member_pre + T).tolist(), (starts * kv_row).tolist(), device,
+                                      causal=True, p_lens=[0] * ng + member_pre.tolist(),
+                                      p_off=[0] * ng + (np.repeat(cu_pre[:-1], G) * kv_row).tolist())
+        # group g's prefix key blocks: its own causal rows, then one segment per member (T token rows each)
+        extra = [[(n_pre + (g * G + m) * T, T) for m in range(G)] for g in range(ng)] + [None] * B
+        self.keys = ops.KeyBlockPlan(lens, device, extra=extra)
+        self.prefixed = True
+        return self
 
 
-def train_logits(model, frames, tokens_in, plens=None):
+def train_logits(model, frames, tokens_in, plens=None, group_size=1):
     """Differentiable Basecaller.logits: bf16 logits [B, T, V] of every token position, with gradients into the
     fp32 projector and decoder parameters (reference: viktor/model.py:55-60 under torch.autocast bf16, as
-    token_logprobs calls it at scripts/gspo.py:345-347). frames [B, P, d_enc]; plens [B] real prefix frames."""
+    token_logprobs calls it at scripts/gspo.py:345-347). frames [B, P, d_enc]; plens [B] real prefix frames.
+    group_size = G > 1: consecutive groups of G windows share their frames (a GSPO micro-batch of whole groups,
+    scripts/gspo.py:444, 459-466; checked, ValueError otherwise). Each group's prefix rows then run the
+    projector and the decoder once, its members' token rows attend to them, and the backward sums every
+    member's gradient into them: the same logits as the unshared forward, and the same gradients up to the
+    order of the fp32 sums over the members."""
     dec = model.decoder
     cfg = dec.cfg
     B, P = frames.shape[:2]
@@ -267,6 +298,8 @@ def train_logits(model, frames, tokens_in, plens=None):
     dev = frames.device
     plens_h = [P] * B if plens is None else [int(p) for p in plens.tolist()]
     assert all(0 < p <= P for p in plens_h), "plens outside 1..P"
+    if int(group_size) > 1:
+        return _train_logits_shared(model, frames, tokens_in, plens_h, int(group_size))
     proj = model.projector
     prefix = _Projector.apply(frames.reshape(B * P, -1).to(BF16).contiguous(), proj[0].weight, proj[0].bias,
                               proj[2].weight, proj[2].bias)                            # [B P, d] bf16
@@ -287,6 +320,44 @@ def train_logits(model, frames, tokens_in, plens=None):
     rpos = idx[2 * n_pre + n_tok:].to(torch.int32)
     x = _PackRows.apply(prefix, emb, pre_src_d, pre_dst_d, tok_rows, n_pre == B * P)
     plan = TrainPlan(seq_lens, dev)
+    cos, sin = dec.cos.float().contiguous(), dec.sin.float().contiguous()
+    meta = {"cfg": cfg, "plan": plan, "rpos": rpos, "cos": cos, "sin": sin, "tok_rows": tok_rows}
+    h = _DecoderStack.apply(x, meta, *decoder_params(dec))
+    return _LMHead.apply(h, dec.lm_head.weight).view(B, T, -1)
+
+
+def _train_logits_shared(model, frames, tokens_in, plens_h, G):
+    """train_logits over groups of G windows that share their prefix: packed rows [each group's prefix rows |
+    every member's token rows] (TrainPlan.shared)."""
+    from .model import check_groups
+    dec = model.decoder
+    cfg = dec.cfg
+    B, P = frames.shape[:2]
+    T = tokens_in.shape[1]
+    dev = frames.device
+    pre_lens = check_groups(frames, plens_h, G)
+    ng = len(pre_lens)
+    proj = model.projector
+    prefix = _Projector.apply(frames[::G].reshape(ng * P, -1).to(BF16).contiguous(), proj[0].weight, proj[0].bias,
+                              proj[2].weight, proj[2].bias)                            # [B / G P, d] bf16
+    emb = _TokenEmbed.apply(dec.embed.weight, tokens_in.to(dev).reshape(-1))          # [B T, d] fp32
+    s = model.pos_scale
+    pl = np.asarray(pre_lens, dtype=np.int64)
+    cu_pre = np.concatenate([[0], np.cumsum(pl)])
+    n_pre = int(cu_pre[-1])
+    pre_src = np.concatenate([g * P + np.arange(pl[g]) for g in range(ng)])
+    pre_dst = np.arange(n_pre, dtype=np.int64)
+    tok_rows_h = n_pre + np.arange(B * T, dtype=np.int64)
+    member_pre = np.repeat(pl, G)
+    rpos_h = np.concatenate([np.concatenate([np.arange(p) * s for p in pre_lens]),
+                             (s * member_pre[:, None] + np.arange(T)[None, :]).reshape(-1)])
+    idx = torch.from_numpy(np.concatenate([pre_src, pre_dst, tok_rows_h, rpos_h])).to(dev)
+    n_tok = B * T
+    pre_src_d, pre_dst_d = idx[:n_pre], idx[n_pre:2 * n_pre]
+    tok_rows = idx[2 * n_pre:2 * n_pre + n_tok]
+    rpos = idx[2 * n_pre + n_tok:].to(torch.int32)
+    x = _PackRows.apply(prefix, emb, pre_src_d, pre_dst_d, tok_rows, n_pre == ng * P)
+    plan = TrainPlan.shared(pre_lens, G, T, dev)
     cos, sin = dec.cos.float().contiguous(), dec.sin.float().contiguous()
     meta = {"cfg": cfg, "plan": plan, "rpos": rpos, "cos": cos, "sin": sin, "tok_rows": tok_rows}
     h = _DecoderStack.apply(x, meta, *decoder_params(dec))
@@ -348,13 +419,14 @@ class HipAdamW:
                   self.step_count, coef=coef)
 
 
-def token_logprobs_train(model, frames, plens, seqs, ended):
-    """Differentiable token_logprobs (scripts/gspo.py:340-353): (logits [B, T, V] bf16, targets, mask)."""
+def token_logprobs_train(model, frames, plens, seqs, ended, group_size=1):
+    """Differentiable token_logprobs (scripts/gspo.py:340-353): (logits [B, T, V] bf16, targets, mask).
+    group_size: as train_logits."""
     from .gspo import sampled_mask
     tokens_in, targets, _ = model.batch(seqs, pad_to=128)
     dev = frames.device
     tokens_in, targets = tokens_in.to(dev), targets.to(dev)
-    logits = train_logits(model, frames, tokens_in, plens)
+    logits = train_logits(model, frames, tokens_in, plens, group_size)
     mask = sampled_mask(targets, seqs, ended, model.tokenizer.k)
     return logits, targets, mask
 
@@ -406,11 +478,17 @@ def gspo_update(model, opt: HipAdamW, frames, plens, calls, ended, reward, G, up
         ix = torch.tensor([b for b, _ in mb], device=dev)
         return frames[ix], plens[ix], [calls[b * G + j] for b, j in mb], [ended[b * G + j] for b, j in mb]
 
+    def group_of(mb):
+        """G when the micro-batch is whole groups (each window's G calls in a row, as `seqs` lists them): its
+        windows' prefixes then run once (train_logits(group_size=G)); 1 otherwise."""
+        whole = len(mb) % G == 0 and all(mb[i][0] == mb[i - i % G][0] and mb[i][1] == i % G for i in range(len(mb)))
+        return G if G > 1 and whole else 1
+
     old = {}
     with torch.no_grad():  # pi_old through the same forward as the update's (scripts/gspo.py:455-462)
         for i in range(0, len(seqs), micro):
             mb = seqs[i:i + micro]
-            logits, targets, m = token_logprobs_train(model, *batch_of(mb))
+            logits, targets, m = token_logprobs_train(model, *batch_of(mb), group_size=group_of(mb))
             lp = ops.gspo_score(logits.contiguous(), targets.clamp(min=0).contiguous())["lp"]
             for k, bj in enumerate(mb):
                 old[bj] = lp[k][m[k]].clone()
@@ -421,7 +499,7 @@ def gspo_update(model, opt: HipAdamW, frames, plens, calls, ended, reward, G, up
         opt.zero_grad()
         for i in range(0, len(mine), micro):
             mb = mine[i:i + micro]
-            logits, targets, mask = token_logprobs_train(model, *batch_of(mb))
+            logits, targets, mask = token_logprobs_train(model, *batch_of(mb), group_size=group_of(mb))
             old_lp = torch.stack([_old_row(old[bj], mask[k]) for k, bj in enumerate(mb)])
             nb = torch.tensor([float(n_bases[bj]) for bj in mb], device=dev)
             a = torch.tensor([adv[b, j] for b, j in mb], device=dev, dtype=torch.float32)
