@@ -363,10 +363,11 @@ int vk_attention_backward(const void *q, const void *k, const void *v, const voi
  * sample's token rows after them in the key order of its window). dQ: sequence i's queries first see p_lens[i]
  * prefix keys, rows of k / v from element p_off[i] (row stride stride_tok), then its own rows (query r at key
  * position p_lens[i] + r). dK / dV: k_plan holds n_kblocks entries (sequence, first key of a 128-key block, xr0,
- * xl, slot): xl < 0 takes the sequence's own query rows (causal), xl >= 0 the xl query rows from packed row xr0
- * (of q / out / dout / lse), each of which sees every key of the block; slot < 0 writes dk / dv, slot >= 0 the
- * partial rows [slot][row] of part_k / part_v ([n_slots, n_part, HKV, D] fp32, a caller's workspace; those
- * sequences' rows < n_part), which are then summed in slot order into dk / dv rows 0 .. n_part - 1. So dK / dV
+ * xl, slot): xl < 0 takes -xl of the sequence's own query rows from its row xr0 (causal), xl >= 0 the xl query
+ * rows from packed row xr0 (of q / out / dout / lse), each of which sees every key of the block; slot < 0 writes
+ * dk / dv, slot >= 0 the partial rows [slot][row] of part_k / part_v ([n_slots, n_part, HKV, D] fp32, a caller's
+ * workspace whose slots no entry writes for a row hold zeros; those sequences' rows < n_part), which are then
+ * summed in slot order into dk / dv rows 0 .. n_part - 1. So dK / dV
  * of the prefix rows sum the gradients of the prefix's own queries and of every sample's token queries, in a
  * fixed order. No reference counterpart of its own: the reference differentiates every sample's full window
  * (scripts/gspo.py:477); these are the same sums, regrouped.

@@ -78,11 +78,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dot_kernel(const bf16_t *__restr
 // Shared-prefix layout (the GSPO group's samples scored as one window each, their common prefix rows kept once):
 // in dQ, sequence i's queries see first p_lens[i] prefix keys, rows of k / v from element p_off[i] (row stride
 // stride_tok), then its own rows, query r at key position p_lens[i] + r. In dK / dV a work item is
-// (sequence, first key, xr0, xl, slot): xl < 0 takes the sequence's own query rows (causal), xl >= 0 the xl rows
-// from packed row xr0 (of q / dO / lse / D), each of which sees every key of the block (the samples' token rows
-// against their prefix keys); slot < 0 writes dk / dv, slot >= 0 the partial rows part[slot][r0 + key], which
-// attn_bwd_part_reduce_kernel sums over the slots in order into dk / dv (rows < n_part). Not PREFIXED: plain
-// causal self-attention with (sequence, first key) items.
+// (sequence, first key, xr0, xl, slot): xl < 0 takes -xl of the sequence's own query rows from its row xr0
+// (causal), xl >= 0 the xl rows from packed row xr0 (of q / dO / lse / D), each of which sees every key of the
+// block (the samples' token rows against their prefix keys); slot < 0 writes dk / dv, slot >= 0 the partial rows
+// part[slot][r0 + key], which attn_bwd_part_reduce_kernel sums over the slots in order into dk / dv (rows <
+// n_part; a slot no item of a row writes must hold zeros). Not PREFIXED: plain causal self-attention with
+// (sequence, first key) items.
 struct AbPrefix {
   const int32_t *p_lens;
   const int64_t *p_off;
@@ -261,7 +262,10 @@ __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
   if (len <= 0 || ks >= len) return;
   // query tiles: the sequence's own rows from the block's first key (causal), or the xl extra rows
   const bool xt = xl >= 0;  // extra rows: every row sees every key of the block
-  const int ntl = xt ? (xl + 31) / 32 : (len - ks + 31) / 32;
+  // own rows (causal): rows r_beg .. r_lim - 1 of the sequence; extra rows: 0 .. xl - 1 from packed row xr0
+  const int r_beg = xt ? 0 : (PREFIXED ? static_cast<int>(xr0) : ks);
+  const int r_lim = xt ? xl : (PREFIXED ? min(len, r_beg - xl) : len);
+  const int ntl = r_lim > r_beg ? (r_lim - r_beg + 31) / 32 : 0;
 
   // this wave's 32 keys, two blocks of 16 (lane col -> key of each), K^T / V^T fragments of the B operand
   int keyb[2];
@@ -293,8 +297,8 @@ __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
   float lv = 0.f;
   // query tile it: rows rs .. rs + 31 of the sequence (rs = ks + 32 it) or of the extra rows (rs = 32 it)
   auto tile_rows = [&](int it, int &rs, int &n, int64_t &base) {
-    rs = xt ? 32 * it : ks + 32 * it;
-    n = xt ? xl : len;
+    rs = r_beg + 32 * it;
+    n = r_lim;
     base = xt ? xr0 : r0;
   };
   auto load_tile = [&](int it) {
@@ -362,7 +366,7 @@ __global__ __launch_bounds__(AB_KW * 64, 2) void attn_bwd_dkdv_kernel(
       // row order {4g..4g+3, 16+4g..16+4g+3}; exponents are <= 0 (bare v_exp_f32). A tile wholly below the
       // diagonal and inside the sequence needs no mask (a wave-uniform branch); else a masked entry's exponent
       // is -inf (exp2 -> 0)
-      const bool full = xt ? rs + 31 < n && wave_kmin + 31 < len : wave_kmin + 31 <= rs && rs + 31 < len;
+      const bool full = xt ? rs + 31 < n && wave_kmin + 31 < len : wave_kmin + 31 <= rs && rs + 31 < n;
       bf16x8 pf[2], dsf[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {

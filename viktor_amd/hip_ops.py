@@ -606,14 +606,16 @@ class KeyBlockPlan:
 
     BLOCK = 128
 
-    def __init__(self, seq_lens, device, extra=None):
+    def __init__(self, seq_lens, device, extra=None, chunk=None):
         """extra (the shared-prefix layout of vk_attention_backward_prefixed): per sequence, a list of (first
         packed row, rows) query segments that see every key of the sequence (their samples' token rows against a
-        shared prefix). Such a sequence's key blocks get a work item for its own rows (partial slot 0) and one
-        per segment (slot 1 + j), summed in slot order; those sequences must come first in the packing and carry
-        the same number of segments."""
+        shared prefix). Such a sequence's key blocks get work items for its own rows, in chunks of at most `chunk`
+        rows (default: the longest segment), in partial slots 0, 1, .., and one item per segment in the slots
+        after the largest own-chunk count; the slots are summed in order. Those sequences come first in the
+        packing and carry the same number of segments."""
         lens = [int(n) for n in seq_lens]
         self.n_slots, self.n_part = 0, 0
+        self.part = None
         if extra is None:
             blocks = sorted(((n - ks, i, ks) for i, n in enumerate(lens) for ks in range(0, n, self.BLOCK)),
                             key=lambda b: -b[0])
@@ -623,25 +625,38 @@ class KeyBlockPlan:
             segs = [list(e or []) for e in extra]
             with_x = [i for i, e in enumerate(segs) if e]
             cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+            n_own = 0
             if with_x:
                 _require(with_x == list(range(len(with_x))) and len({len(segs[i]) for i in with_x}) == 1,
                          "KeyBlockPlan: sequences with segments first, each with the same number")
-                self.n_slots = 1 + len(segs[0])
+                C = int(chunk) if chunk else max(int(xn) for i in with_x for _, xn in segs[i])
+                C = max(C, 32)
+                n_own = max(-(-lens[i] // C) for i in with_x)
+                self.n_slots = n_own + len(segs[0])
                 self.n_part = int(cu[len(with_x)])
             items = []
             for i, n in enumerate(lens):
                 for ks in range(0, n, self.BLOCK):
                     if segs[i]:
-                        items.append((n - ks, i, ks, 0, -1, 0))
-                        items += [(int(xn), i, ks, int(x0), int(xn), 1 + j) for j, (x0, xn) in enumerate(segs[i])]
+                        for c, r in enumerate(range(ks, n, C)):
+                            items.append((min(C, n - r), i, ks, r, -min(C, n - r), c))
+                        items += [(int(xn), i, ks, int(x0), int(xn), n_own + j) for j, (x0, xn) in enumerate(segs[i])]
                     else:
-                        items.append((n - ks, i, ks, 0, -1, -1))
+                        items.append((n - ks, i, ks, ks, -(n - ks), -1))
             items.sort(key=lambda b: -b[0])
             flat = [v for it in items for v in it[1:]] or [0, 0, 0, -1, -1]
             blocks = items
         self.n_blocks = len(blocks)
         self.prefixed = extra is not None
         self.plan = torch.tensor(flat, dtype=torch.int32).to(device)
+
+    def partials(self, hkv, d, device):
+        """The plan's partial-slot workspace (k, v) [n_slots, n_part, hkv, d] fp32, zeroed once: every call with
+        this plan writes the same (slot, row) entries, so the ones no item writes stay zero."""
+        if self.part is None:
+            k = torch.zeros(self.n_slots, self.n_part, hkv, d, dtype=torch.float32, device=device)
+            self.part = (k, torch.zeros_like(k))
+        return self.part
 
 
 def attention_backward(q, k, v, out, dout, lse, q_plan: AttentionPlan, k_plan: KeyBlockPlan, stride_tok=None):
@@ -676,8 +691,7 @@ def attention_backward(q, k, v, out, dout, lse, q_plan: AttentionPlan, k_plan: K
              "attention_backward: a shared-prefix layout needs both plans' prefix fields")
     part_k = part_v = None
     if k_plan.n_slots:
-        part_k = torch.empty(k_plan.n_slots, k_plan.n_part, HK, D, dtype=torch.float32, device=q.device)
-        part_v = torch.empty_like(part_k)
+        part_k, part_v = k_plan.partials(HK, D, q.device)
     call("vk_attention_backward_prefixed", ptr(q), ptr(k), ptr(v), ptr(out), ptr(dout), ptr(lse), ptr(q_plan.cu_q),
          q_plan.n_seq, ptr(q_plan.plan), q_plan.n_blocks, ptr(k_plan.plan), k_plan.n_blocks, n, stride_tok,
          ptr(q_plan.p_lens), ptr(q_plan.p_off), ptr(part_k), ptr(part_v), k_plan.n_part, k_plan.n_slots, ptr(dd),
