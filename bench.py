@@ -49,7 +49,8 @@ Extra objects on the JSON line:
                 (127, 128)) with seeded random weights; ms, chunks/s and the MFMA fraction of its algorithmic
                 flops (convolutions, 4 products per layer, window attention over the keys each frame sees).
 Usage: python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--no-cpu] [--no-configs]
-       python bench.py --mode encoder|prefill|scoring [--steps N]   (that object alone, N timed repetitions)
+       python bench.py --mode encoder|prefill|scoring|update [--steps N]   (that object alone, N timed repetitions;
+                                                    scoring / update: [--forms shared|unshared|shared,unshared])
        python bench.py --mode configs                       (the other configurations alone)
        python bench.py --mode kernels [--group-size G]      (the decode-attention traffic probe)
        python bench.py --mode products [--steps N] [--phase-stamps]   (the decode step's layer loop, captured)
@@ -228,7 +229,7 @@ def varlen_kmer_config(dev, steps=340):
     return out
 
 
-def scoring_config(dev, reps=2):
+def scoring_config(dev, reps=2, forms=("shared", "unshared")):
     """GSPO scoring: 512 sequences x (2048-frame prefix + 700..1024 response tokens), the teacher-forced forward
     of token_logprobs (scripts/gspo.py:340-353), then the sequence-ratio loss and its gradient w.r.t. the
     logits (scripts/gspo.py:459-477), with the fp32 master model and the autocast rounding points the reference
@@ -249,7 +250,8 @@ def scoring_config(dev, reps=2):
     g = torch.Generator(device=dev).manual_seed(6)
     fr = torch.randn(PREFIXES, P, 512, generator=g, device=dev).to(torch.bfloat16).repeat_interleave(GROUP, 0)
     plens = torch.full((B,), P, device=dev)
-    lp, mask = G.token_logprobs(gm, fr, plens, seqs, ended, group_size=GROUP)  # the old policy's log-probs
+    # the old policy's log-probs (in the first form timed)
+    lp, mask = G.token_logprobs(gm, fr, plens, seqs, ended, group_size=GROUP if "shared" in forms else 1)
     old = (lp + 0.05 * torch.randn(lp.shape, generator=g, device=dev)).contiguous()
     nb = torch.tensor([max(len(q), 1) for q in seqs], dtype=torch.float32, device=dev)
     adv = torch.randn(B, generator=g, device=dev)
@@ -261,8 +263,8 @@ def scoring_config(dev, reps=2):
         logits = gm.logits(fr, tin, plens, group_size=group)
         G.ops.gspo_score(logits.contiguous(), tgt, mask, old, nb, adv, 3e-4, 4e-4, grad=True)
 
-    ms = _timed(lambda: run(GROUP), reps)
-    ms_full = _timed(lambda: run(1), reps)
+    ms = _timed(lambda: run(GROUP), reps) if "shared" in forms else None
+    ms_full = _timed(lambda: run(1), reps) if "unshared" in forms else None
     L = [len(q) + 1 for q in seqs]
     flops = flops_full = 0
     for n_tok in L:
@@ -270,17 +272,20 @@ def scoring_config(dev, reps=2):
         flops_full += 2 * 2 * 512 * 512 * P + 2 * 3014656 * 8 * n - P * 5242880 + 8 * 1024 * n * (n + 1) + 2 * 512 * 7 * n_tok
         flops += 2 * 3014656 * 8 * n_tok + 8 * 2048 * (n_tok * P + n_tok * (n_tok + 1) // 2) + 2 * 512 * 7 * n_tok
     flops += PREFIXES * (2 * 2 * 512 * 512 * P + 2 * 3014656 * 8 * P - P * 5242880 + 7 * 1024 * P * (P + 1))
-    tf = flops / (ms / 1e3) / 1e12
-    out = {"sequences": B, "windows": PREFIXES, "group_size": GROUP, "response_tokens": "U[700, 1024]",
-           "ms": round(ms, 2), "tokens_per_s": round(sum(L) / (ms / 1e3), 1), "alg_tflop": round(flops / 1e12, 2),
-           "achieved_tflops": round(tf, 1), "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-           "unshared": {"ms": round(ms_full, 2), "tokens_per_s": round(sum(L) / (ms_full / 1e3), 1),
-                        "alg_tflop": round(flops_full / 1e12, 2),
-                        "mfma_frac": round(flops_full / (ms_full / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-                        "note": "every window in full, as the reference scores them"},
-           "includes": "projector + teacher-forced 8-layer forward (fp32 master weights, autocast rounding points, "
+    out = {"sequences": B, "windows": PREFIXES, "group_size": GROUP, "response_tokens": "U[700, 1024]"}
+    if ms is not None:
+        tf = flops / (ms / 1e3) / 1e12
+        out.update({"ms": round(ms, 2), "tokens_per_s": round(sum(L) / (ms / 1e3), 1),
+                    "alg_tflop": round(flops / 1e12, 2), "achieved_tflops": round(tf, 1),
+                    "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)})
+    if ms_full is not None:
+        out["unshared"] = {"ms": round(ms_full, 2), "tokens_per_s": round(sum(L) / (ms_full / 1e3), 1),
+                           "alg_tflop": round(flops_full / 1e12, 2),
+                           "mfma_frac": round(flops_full / (ms_full / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                           "note": "every window in full, as the reference scores them"}
+    out.update({"includes": "projector + teacher-forced 8-layer forward (fp32 master weights, autocast rounding points, "
                        "padded to a multiple of 128 tokens as the reference pads) + LM head + log-probs, ratio, "
-                       "clipped loss and dL/dlogits [512, T, 7]"}
+                       "clipped loss and dL/dlogits [512, T, 7]"})
     del fr
     torch.cuda.empty_cache()
     return out
@@ -572,7 +577,7 @@ def prefill_timing(reps=3, prefill_batch=128, group_size=GROUP):
             "achieved_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
 
 
-def update_timing(steps=3, warmup=2):
+def update_timing(steps=3, warmup=2, forms=("shared", "unshared")):
     """One GSPO update micro-batch on the HIP training path (see the module docstring): times and flops. The
     micro-batch is whole groups, as the reference's update loop takes them (scripts/gspo.py:453, 466-468): 4
     windows x 8 calls, each window's frames repeated for its calls. Timed with group_size 8 (each window's prefix
@@ -595,7 +600,7 @@ def update_timing(steps=3, warmup=2):
     nb = torch.full((B,), float(T), device=dev)
     adv = torch.randn(B, generator=g).to(dev)
     with torch.no_grad():
-        z0 = TR.train_logits(m, fr, tok, pl, group_size=GROUP)
+        z0 = TR.train_logits(m, fr, tok, pl, group_size=GROUP if "shared" in forms else 1)
         old = torch.log_softmax(z0.float(), -1).gather(-1, tgt[..., None])[..., 0]
 
     def run(group):
@@ -617,8 +622,8 @@ def update_timing(steps=3, warmup=2):
                     acc[i] += ev[i].elapsed_time(ev[i + 1]) / steps
         return acc
 
-    acc = run(GROUP)
-    acc_full = run(1)
+    acc = run(GROUP) if "shared" in forms else None
+    acc_full = run(1) if "unshared" in forms else None
     weights = 8 * 3014656  # decoder matmul weights
     n = P + T
     rows_full = B * n
@@ -627,20 +632,25 @@ def update_timing(steps=3, warmup=2):
     rows = ng * P + B * T
     gemm = 3 * 2 * weights * rows + 3 * 2 * 2 * 512 * 512 * ng * P + 3 * 2 * 512 * 7 * B * T
     attn = 3.5 * 8 * (1024 * P * (P + 1) * ng + (1024 * T * (T + 1) + 2048 * T * P) * B)
-    ms, ms_full = sum(acc), sum(acc_full)
-    tflops = (gemm + attn) / (ms / 1e3) / 1e12
-    return {"microbatch": f"{B} calls = {ng} windows x {GROUP} ({P} frames + {T} tokens), 8 layers, "
-                          "fwd + bwd + clip + AdamW", "group_size": GROUP,
-            "ms_per_microbatch": round(ms, 2), "forward_ms": round(acc[0], 2), "backward_ms": round(acc[1], 2),
-            "optimizer_ms": round(acc[2], 3), "calls_per_s": round(B / (ms / 1e3), 1),
-            "alg_tflop": round((gemm + attn) / 1e12, 2), "achieved_tflops": round(tflops, 1),
-            "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-            "unshared": {"ms_per_microbatch": round(ms_full, 2), "forward_ms": round(acc_full[0], 2),
-                         "backward_ms": round(acc_full[1], 2), "rows_per_s": round(rows_full / (ms_full / 1e3), 1),
-                         "alg_tflop": round((gemm_full + attn_full) / 1e12, 2),
-                         "mfma_frac": round((gemm_full + attn_full) / (ms_full / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-                                            4),
-                         "note": "every call's full window, as the reference computes it"}}
+    out = {"microbatch": f"{B} calls = {ng} windows x {GROUP} ({P} frames + {T} tokens), 8 layers, "
+                         "fwd + bwd + clip + AdamW", "group_size": GROUP}
+    if acc is not None:
+        ms = sum(acc)
+        tflops = (gemm + attn) / (ms / 1e3) / 1e12
+        out.update({"ms_per_microbatch": round(ms, 2), "forward_ms": round(acc[0], 2),
+                    "backward_ms": round(acc[1], 2), "optimizer_ms": round(acc[2], 3),
+                    "calls_per_s": round(B / (ms / 1e3), 1), "alg_tflop": round((gemm + attn) / 1e12, 2),
+                    "achieved_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)})
+    if acc_full is not None:
+        ms_full = sum(acc_full)
+        out["unshared"] = {"ms_per_microbatch": round(ms_full, 2), "forward_ms": round(acc_full[0], 2),
+                           "backward_ms": round(acc_full[1], 2),
+                           "rows_per_s": round(rows_full / (ms_full / 1e3), 1),
+                           "alg_tflop": round((gemm_full + attn_full) / 1e12, 2),
+                           "mfma_frac": round((gemm_full + attn_full) / (ms_full / 1e3) / 1e12 /
+                                              MFMA_BF16_PEAK_TFLOPS, 4),
+                           "note": "every call's full window, as the reference computes it"}
+    return out
 
 
 def kernels_mode(group, reps=5):
@@ -819,6 +829,9 @@ def main():
     ap.add_argument("--phase-stamps", action="store_true",
                     help="products mode: load the phase-timestamp profiling build and summarise its stamps")
     ap.add_argument("--group-size", type=int, default=GROUP, help="sequences sharing one prefix KV copy (1: none)")
+    ap.add_argument("--forms", default="shared,unshared",
+                    help="--mode scoring / update: which forms to time (shared: each window's prefix once for its "
+                         "calls; unshared: every call's full window)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the rollout path has no multi-GPU mode here (one process per GPU, "
@@ -844,10 +857,12 @@ def main():
     if args.mode == "scoring":
         dev = torch.device("cuda", 0)
         torch.cuda.set_device(dev)
-        print(json.dumps({"scoring": scoring_config(dev, reps=max(args.steps, 1))}), flush=True)
+        print(json.dumps({"scoring": scoring_config(dev, reps=max(args.steps, 1), forms=args.forms.split(","))}),
+              flush=True)
         return
     if args.mode == "update":
-        print(json.dumps({"gspo_update": update_timing(steps=max(args.steps, 1), warmup=args.warmup)}), flush=True)
+        print(json.dumps({"gspo_update": update_timing(steps=max(args.steps, 1), warmup=args.warmup,
+                                                       forms=args.forms.split(","))}), flush=True)
         return
     if args.mode == "prefill":
         print(json.dumps({"prefill": prefill_timing(reps=max(args.steps, 1), prefill_batch=args.prefill_batch,
