@@ -10,6 +10,8 @@ last layer of a prefill can keep only some rows of each sequence (the BOS row fo
 response rows for teacher-forced scoring), which then attend to their whole sequence.
 """
 
+from collections import OrderedDict
+
 import numpy as np
 import torch
 
@@ -93,12 +95,15 @@ class PrefillPlan:
                     self.bos_lengths = torch.tensor(seq_lens, dtype=torch.int32).to(device)
 
     def packed_plans(self, hkv_d):
-        """Attention plans over packed k/v rows [total, HKV, D] (no cache)."""
-        k_off = [c * hkv_d for c in self.cu[:-1]]
-        full = ops.AttentionPlan(self.seq_lens, self.seq_lens, k_off, self.device, causal=True)
-        last = None if self.keep is None else ops.AttentionPlan(self.keep, self.seq_lens, k_off, self.device,
-                                                                causal=self.last_causal)
-        return full, last
+        """Attention plans over packed k/v rows [total, HKV, D] (no cache); built once per hkv_d."""
+        memo = self.__dict__.setdefault("_packed", {})
+        if hkv_d not in memo:
+            k_off = [c * hkv_d for c in self.cu[:-1]]
+            full = ops.AttentionPlan(self.seq_lens, self.seq_lens, k_off, self.device, causal=True)
+            last = None if self.keep is None else ops.AttentionPlan(self.keep, self.seq_lens, k_off, self.device,
+                                                                    causal=self.last_causal)
+            memo[hkv_d] = (full, last)
+        return memo[hkv_d]
 
 
 class SharedPrefixPlan:
@@ -143,6 +148,7 @@ class FastDecoder:
         self.attention_backend = "hip"
         self._wcache = {}
         self._plans = {}
+        self._layouts = OrderedDict()
         self.decode_workspace = None
         # optional attn_marks(layer, k): called right before (k = 0) and after (k = 1) each decode step's attention
         # launch, on the launching stream -- the benchmark records timing events there, inside the captured step
@@ -178,6 +184,20 @@ class FastDecoder:
 
     def _tables(self):
         return self.dec.cos, self.dec.sin
+
+    def layout(self, key, build, cap=4):
+        """The host-built layout of a packed batch (plans and their small index tensors on the device) for key,
+        built by build() on a miss; the cap most recent are kept. A batch of a layout seen before then starts
+        without host work or host-to-device copies (each copy from pageable memory waits for the stream)."""
+        hit = self._layouts.get(key)
+        if hit is None:
+            hit = build()
+            self._layouts[key] = hit
+            while len(self._layouts) > cap:
+                self._layouts.popitem(last=False)
+        else:
+            self._layouts.move_to_end(key)
+        return hit
 
     def teacher_forced(self, x, pos, plan, rope_pos=None):
         """The teacher-forced causal forward of packed windows with the rounding points of the reference's

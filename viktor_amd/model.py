@@ -138,31 +138,37 @@ class Basecaller(nn.Module):
         prefix = self.project(frames)                                       # [B, P, d] bf16
         fast = self.decoder.fast()
         emb = fast.w32(self.decoder.embed.weight)[tokens_in.to(dev)]        # [B, T, d] fp32
-        seq_lens = [p + T for p in plens_h]
-        plan = PrefillPlan(seq_lens, dev, keep=[T] * B)
+        s = self.pos_scale
+
+        def build():  # the packing plan, the window layout's row indices and each row's (rotary) position
+            seq_lens = [p + T for p in plens_h]
+            plan = PrefillPlan(seq_lens, dev, keep=[T] * B)
+            pl = np.asarray(plens_h, dtype=np.int64)
+            cu = np.asarray(plan.cu[:-1], dtype=np.int64)
+            pre_dst = np.concatenate([cu[b] + np.arange(pl[b]) for b in range(B)])
+            pre_src = np.concatenate([b * P + np.arange(pl[b]) for b in range(B)])
+            tok_dst = (cu + pl)[:, None] + np.arange(T)[None, :]
+            pos = np.concatenate([np.arange(n) for n in seq_lens])
+            parts = [pre_dst, pre_src, tok_dst.reshape(-1), pos]
+            if s != 1:
+                parts.append(np.concatenate([np.concatenate([np.arange(p) * s, s * p + np.arange(T)])
+                                             for p in plens_h]))
+            idx = torch.from_numpy(np.concatenate(parts)).to(dev)  # one host-to-device copy
+            o = np.cumsum([0] + [len(a) for a in parts])
+            sl = [idx[o[i]:o[i + 1]] for i in range(len(parts))]
+            rpos = sl[4].to(torch.int32) if s != 1 else None
+            return plan, sl[0], sl[1], sl[2], sl[3].to(torch.int32), rpos
+
+        plan, pre_dst, pre_src, tok_dst, pos, rpos = fast.layout(("tf", tuple(plens_h), P, T, s), build)
         # packed rows: window b = [prefix[b, :plens[b]] | emb[b]]
-        pl = torch.tensor(plens_h, device=dev)
-        cu = torch.tensor(plan.cu[:-1], device=dev)
         x = torch.empty(plan.total, prefix.shape[-1], dtype=torch.float32, device=dev)
         if all(p == P for p in plens_h):  # full windows: two strided copies
             xv = x.view(B, P + T, -1)
             xv[:, :P] = prefix
             xv[:, P:] = emb
         else:
-            frame_rows = torch.repeat_interleave(torch.arange(B, device=dev), pl)
-            frame_pos = torch.arange(int(pl.sum()), device=dev) - torch.repeat_interleave(
-                torch.cumsum(pl, 0) - pl, pl)
-            x[cu[frame_rows] + frame_pos] = prefix[frame_rows, frame_pos].float()
-            tok_dst = (cu + pl)[:, None] + torch.arange(T, device=dev)[None, :]
-            x[tok_dst.reshape(-1)] = emb.reshape(B * T, -1)
-        # each row's position inside its window
-        pos = (torch.arange(plan.total, device=dev) - torch.repeat_interleave(
-            cu, torch.tensor(seq_lens, device=dev))).to(torch.int32)
-        rpos = None
-        if self.pos_scale != 1:
-            s = self.pos_scale
-            rpos = torch.cat([torch.cat([torch.arange(p, device=dev) * s, s * p + torch.arange(T, device=dev)])
-                              for p in plens_h]).to(torch.int32)
+            x[pre_dst] = prefix.reshape(B * P, -1)[pre_src].float()
+            x[tok_dst] = emb.reshape(B * T, -1)
         return fast.teacher_forced(x, pos, plan, rope_pos=rpos)            # [B * T, d] bf16
 
     def _hidden_shared(self, frames, tokens_in, plens_h, G):
@@ -180,12 +186,18 @@ class Basecaller(nn.Module):
             x_pre = torch.cat([prefix[g, :p] for g, p in enumerate(pre_lens)]).float()
         fast = self.decoder.fast()
         x_tok = fast.w32(self.decoder.embed.weight)[tokens_in.to(dev).reshape(-1)]  # [B T, d] fp32
-        plan = SharedPrefixPlan(pre_lens, G, T, self.cfg.n_kv_heads * self.cfg.head_dim, dev)
-        rope_pre = rope_tok = None
-        if self.pos_scale != 1:
-            s = self.pos_scale
-            rope_pre = torch.cat([torch.arange(p, device=dev) * s for p in pre_lens]).to(torch.int32)
-            rope_tok = torch.cat([s * plens_h[b] + torch.arange(T, device=dev) for b in range(B)]).to(torch.int32)
+        s = self.pos_scale
+
+        def build():
+            plan = SharedPrefixPlan(pre_lens, G, T, self.cfg.n_kv_heads * self.cfg.head_dim, dev)
+            rope_pre = rope_tok = None
+            if s != 1:
+                rope_pre = torch.from_numpy(np.concatenate([np.arange(p) * s for p in pre_lens]).astype(np.int32)).to(dev)
+                rope_tok = torch.from_numpy((s * np.repeat(np.asarray(pre_lens), G)[:, None] +
+                                             np.arange(T)[None, :]).reshape(-1).astype(np.int32)).to(dev)
+            return plan, rope_pre, rope_tok
+
+        plan, rope_pre, rope_tok = fast.layout(("shared", tuple(pre_lens), G, T, s), build)
         return fast.teacher_forced_shared(x_pre, x_tok, plan, rope_pre, rope_tok)  # [B * T, d] bf16
 
     def batch(self, seqs, weights=None, pad_to=1):

@@ -305,21 +305,24 @@ def train_logits(model, frames, tokens_in, plens=None, group_size=1):
                               proj[2].weight, proj[2].bias)                            # [B P, d] bf16
     emb = _TokenEmbed.apply(dec.embed.weight, tokens_in.to(dev).reshape(-1))          # [B T, d] fp32
     # packed layout, window b: its plens[b] real prefix rows, then its T token rows; row indices on the host
-    seq_lens = [p + T for p in plens_h]
     s = model.pos_scale
-    pl = np.asarray(plens_h, dtype=np.int64)
-    off = np.concatenate([[0], np.cumsum(pl + T)])
-    pre_dst = np.concatenate([np.arange(off[b], off[b] + pl[b]) for b in range(B)])
-    pre_src = np.concatenate([b * P + np.arange(pl[b]) for b in range(B)])
-    tok_rows_h = np.concatenate([np.arange(off[b] + pl[b], off[b + 1]) for b in range(B)])
-    rpos_h = np.concatenate([np.concatenate([np.arange(p) * s, s * p + np.arange(T)]) for p in plens_h])
-    idx = torch.from_numpy(np.concatenate([pre_src, pre_dst, tok_rows_h, rpos_h])).to(dev)
-    n_pre, n_tok = len(pre_src), len(tok_rows_h)
-    pre_src_d, pre_dst_d = idx[:n_pre], idx[n_pre:2 * n_pre]
-    tok_rows = idx[2 * n_pre:2 * n_pre + n_tok]
-    rpos = idx[2 * n_pre + n_tok:].to(torch.int32)
-    x = _PackRows.apply(prefix, emb, pre_src_d, pre_dst_d, tok_rows, n_pre == B * P)
-    plan = TrainPlan(seq_lens, dev)
+
+    def build():
+        seq_lens = [p + T for p in plens_h]
+        pl = np.asarray(plens_h, dtype=np.int64)
+        off = np.concatenate([[0], np.cumsum(pl + T)])
+        pre_dst = np.concatenate([np.arange(off[b], off[b] + pl[b]) for b in range(B)])
+        pre_src = np.concatenate([b * P + np.arange(pl[b]) for b in range(B)])
+        tok_rows_h = np.concatenate([np.arange(off[b] + pl[b], off[b + 1]) for b in range(B)])
+        rpos_h = np.concatenate([np.concatenate([np.arange(p) * s, s * p + np.arange(T)]) for p in plens_h])
+        idx = torch.from_numpy(np.concatenate([pre_src, pre_dst, tok_rows_h, rpos_h])).to(dev)
+        n_pre, n_tok = len(pre_src), len(tok_rows_h)
+        return (TrainPlan(seq_lens, dev), idx[:n_pre], idx[n_pre:2 * n_pre], idx[2 * n_pre:2 * n_pre + n_tok],
+                idx[2 * n_pre + n_tok:].to(torch.int32), n_pre == B * P)
+
+    plan, pre_src_d, pre_dst_d, tok_rows, rpos, all_prefix = dec.fast().layout(("train", tuple(plens_h), P, T, s),
+                                                                               build)
+    x = _PackRows.apply(prefix, emb, pre_src_d, pre_dst_d, tok_rows, all_prefix)
     cos, sin = dec.cos.float().contiguous(), dec.sin.float().contiguous()
     meta = {"cfg": cfg, "plan": plan, "rpos": rpos, "cos": cos, "sin": sin, "tok_rows": tok_rows}
     h = _DecoderStack.apply(x, meta, *decoder_params(dec))
@@ -342,22 +345,25 @@ def _train_logits_shared(model, frames, tokens_in, plens_h, G):
                               proj[2].weight, proj[2].bias)                            # [B / G P, d] bf16
     emb = _TokenEmbed.apply(dec.embed.weight, tokens_in.to(dev).reshape(-1))          # [B T, d] fp32
     s = model.pos_scale
-    pl = np.asarray(pre_lens, dtype=np.int64)
-    cu_pre = np.concatenate([[0], np.cumsum(pl)])
-    n_pre = int(cu_pre[-1])
-    pre_src = np.concatenate([g * P + np.arange(pl[g]) for g in range(ng)])
-    pre_dst = np.arange(n_pre, dtype=np.int64)
-    tok_rows_h = n_pre + np.arange(B * T, dtype=np.int64)
-    member_pre = np.repeat(pl, G)
-    rpos_h = np.concatenate([np.concatenate([np.arange(p) * s for p in pre_lens]),
-                             (s * member_pre[:, None] + np.arange(T)[None, :]).reshape(-1)])
-    idx = torch.from_numpy(np.concatenate([pre_src, pre_dst, tok_rows_h, rpos_h])).to(dev)
-    n_tok = B * T
-    pre_src_d, pre_dst_d = idx[:n_pre], idx[n_pre:2 * n_pre]
-    tok_rows = idx[2 * n_pre:2 * n_pre + n_tok]
-    rpos = idx[2 * n_pre + n_tok:].to(torch.int32)
-    x = _PackRows.apply(prefix, emb, pre_src_d, pre_dst_d, tok_rows, n_pre == ng * P)
-    plan = TrainPlan.shared(pre_lens, G, T, dev)
+
+    def build():
+        pl = np.asarray(pre_lens, dtype=np.int64)
+        cu_pre = np.concatenate([[0], np.cumsum(pl)])
+        n_pre = int(cu_pre[-1])
+        pre_src = np.concatenate([g * P + np.arange(pl[g]) for g in range(ng)])
+        pre_dst = np.arange(n_pre, dtype=np.int64)
+        tok_rows_h = n_pre + np.arange(B * T, dtype=np.int64)
+        member_pre = np.repeat(pl, G)
+        rpos_h = np.concatenate([np.concatenate([np.arange(p) * s for p in pre_lens]),
+                                 (s * member_pre[:, None] + np.arange(T)[None, :]).reshape(-1)])
+        idx = torch.from_numpy(np.concatenate([pre_src, pre_dst, tok_rows_h, rpos_h])).to(dev)
+        n_tok = B * T
+        return (TrainPlan.shared(pre_lens, G, T, dev), idx[:n_pre], idx[n_pre:2 * n_pre],
+                idx[2 * n_pre:2 * n_pre + n_tok], idx[2 * n_pre + n_tok:].to(torch.int32), n_pre == ng * P)
+
+    plan, pre_src_d, pre_dst_d, tok_rows, rpos, all_prefix = dec.fast().layout(
+        ("train_shared", tuple(pre_lens), G, P, T, s), build)
+    x = _PackRows.apply(prefix, emb, pre_src_d, pre_dst_d, tok_rows, all_prefix)
     cos, sin = dec.cos.float().contiguous(), dec.sin.float().contiguous()
     meta = {"cfg": cfg, "plan": plan, "rpos": rpos, "cos": cos, "sin": sin, "tok_rows": tok_rows}
     h = _DecoderStack.apply(x, meta, *decoder_params(dec))
